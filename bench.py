@@ -1,0 +1,222 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized MoE FFN layer (one GPU).
+
+A step is one MoE FFN layer call (hip_moe_ffn_dev) over one batch of
+synthetic tokens whose activations are already resident in HBM.  The default
+workload is the OLMoE-1B-7B-shaped decode layer: d_model 2048, 64 experts,
+top-8 softmax routing without renormalisation, SwiGLU d_ff 1024, Q8_0 expert
+weights drawn N(0, 0.02), fp32 router, one token per call.
+
+The selected experts of one call (~53.5 MB) fit in MI355X's 256 MB
+Infinity Cache, so the timed loop rotates over `--layers` copies of the layer
+(distinct device allocations, like the 16 layers of the full model) and over
+distinct tokens: consecutive calls touch different memory and the figure is
+an HBM figure.  Calls are replayed from HIP graphs of one call per layer copy.
+
+Prints one JSON line on stdout (progress goes to stderr).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "llm.c_amd"))
+import hipmoe  # noqa: E402
+
+METRIC = "MoE-layer tokens/s & % of HBM roofline; OLMoE-shaped decode tok/s"
+HBM_PEAK_GBS = 8000.0
+SEED = 1337
+
+WORKLOADS = {
+    "olmoe_q8_decode": dict(wtype=hipmoe.Q8_0, E=2048, EI=1024, NE=64, K=8, renorm=0, T=1,
+                            bias_std=None),
+    "olmoe_q4_prefill512_skew": dict(wtype=hipmoe.Q4_0, E=2048, EI=1024, NE=64, K=8, renorm=0,
+                                     T=512, bias_std=1.0),
+    "mixtral_q4_decode": dict(wtype=hipmoe.Q4_0, E=4096, EI=14336, NE=8, K=2, renorm=1, T=1,
+                              bias_std=None),
+    "mixtral_q4_T16": dict(wtype=hipmoe.Q4_0, E=4096, EI=14336, NE=8, K=2, renorm=1, T=16,
+                           bias_std=None),
+    "mixtral_q4_T64": dict(wtype=hipmoe.Q4_0, E=4096, EI=14336, NE=8, K=2, renorm=1, T=64,
+                           bias_std=None),
+}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def expert_bytes(w):
+    return 2 * w["EI"] * hipmoe.row_bytes(w["wtype"], w["E"]) + \
+        w["E"] * hipmoe.row_bytes(w["wtype"], w["EI"])
+
+
+def cpu_baseline(lw, w, xs, seconds):
+    """The oracle (a C restatement of the reference's AVX2 CPU path) on this
+    host, one thread: the reference runs the OLMoE router (T < 64) and the
+    expert FFN (2*2048*1024 flops < 16 Mi, thread_pool.c:25,178-185) on one
+    thread.  Bounded by `seconds`."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle
+    T = w["T"]
+    sample_T = min(T, 8)
+    done_tokens = 0
+    t0 = time.perf_counter()
+    i = 0
+    while True:
+        x = xs[i % len(xs)][:sample_T]
+        oracle.moe_ffn(x, lw, w["K"], bool(w["renorm"]), lw["bias"], nthreads=1)
+        done_tokens += sample_T
+        i += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return dict(value=done_tokens / el, unit="tokens/s", cores=1, kind="port",
+                sample=f"{done_tokens} tokens in {i} layer calls of {sample_T} token(s), "
+                       f"{el:.1f} s, 1 thread, oracle/moe_oracle.c built -O3 -mavx2 -mfma")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=4096)
+    ap.add_argument("--warmup", type=int, default=64)
+    ap.add_argument("--workload", default="olmoe_q8_decode", choices=sorted(WORKLOADS))
+    ap.add_argument("--layers", type=int, default=16, help="layer copies rotated over")
+    ap.add_argument("--tokens", type=int, default=64, help="distinct token batches")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="launch without HIP graphs")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the MoE path here runs on a single MI355X "
+              "(multi-GPU sharding is a design note, not a measured path); use --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    w = WORKLOADS[args.workload]
+    H = hipmoe.hip()
+    if H.device_count() < 1:
+        sys.exit("no HIP device")
+    E, T, K = w["E"], w["T"], w["K"]
+
+    t0 = time.perf_counter()
+    lw = hipmoe.synth_layer(SEED, 0, w["wtype"], E, w["EI"], w["NE"], 0.02, w["bias_std"])
+    log(f"generated layer in {time.perf_counter() - t0:.1f} s")
+    nl = max(1, args.layers)
+    layers = [hipmoe.MoeLayer.from_synth(lw, K, bool(w["renorm"])) for _ in range(nl)]
+    log(f"uploaded {nl} layer copies ({nl * layers[0].weight_bytes() / 1e9:.2f} GB)")
+
+    ntok = max(1, args.tokens)
+    xs = [hipmoe.synth_input(SEED, 1000 + i, T, E) for i in range(ntok)]
+    d_x = H.upload(np.stack(xs))
+    d_bias = H.upload(lw["bias"]) if lw["bias"] is not None else None
+    d_out = H.malloc(T * E * 4)
+    s = H.stream()
+    xbytes = T * E * 4
+
+    def call(i):
+        layers[i % nl].ffn_dev(d_x + (i % ntok) * xbytes, d_out, T, d_bias, None, None, s)
+
+    # algorithmic bytes: the unique experts each call touches, the router, x and out
+    uniq = []
+    for i in range(ntok):
+        _, _, ids, _ = layers[0].route(xs[i], lw["bias"])
+        uniq.append(len(np.unique(ids)))
+    router_bytes = w["NE"] * E * 4
+    bytes_per_call = float(np.mean(uniq)) * expert_bytes(w) + router_bytes + 2 * xbytes
+
+    for i in range(nl):  # every copy allocates its scratch before any capture
+        call(i)
+    for i in range(args.warmup):
+        call(i)
+    H.stream_sync(s)
+    log(f"warmup {args.warmup} calls done")
+
+    graphs = []
+    if not args.eager:
+        G = nl
+        ngraphs = max(1, min(4, ntok // G)) if ntok >= G else 1
+        for g in range(ngraphs):
+            H.begin_capture(s)
+            for i in range(G):
+                layers[i].ffn_dev(d_x + ((g * G + i) % ntok) * xbytes, d_out, T, d_bias,
+                                  None, None, s)
+            graphs.append(H.end_capture(s))
+        for ge in graphs:  # warm the graphs
+            H.graph_launch(ge, s)
+        H.stream_sync(s)
+        log(f"captured {len(graphs)} graphs of {G} calls")
+
+    steps = args.steps
+    e0, e1 = H.event(), H.event()
+    H.sync()
+    H.record(e0, s)
+    if graphs:
+        G = nl
+        full, rem = divmod(steps, G)
+        for r in range(full):
+            H.graph_launch(graphs[r % len(graphs)], s)
+        for i in range(rem):
+            call(i)
+    else:
+        for i in range(steps):
+            call(i)
+    H.record(e1, s)
+    ms = H.elapsed_ms(e0, e1)
+    H.sync()
+    ms_per_step = ms / steps
+    tokens_per_s = steps * T / (ms / 1e3)
+    achieved_gbs = bytes_per_call / (ms_per_step / 1e3) / 1e9
+    log(f"{steps} steps in {ms:.2f} ms: {ms_per_step * 1e3:.2f} us/step, "
+        f"{tokens_per_s:.1f} tokens/s, {achieved_gbs:.1f} GB/s algorithmic")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log(f"cpu baseline ({args.cpu_seconds:.0f} s)")
+        cpu = cpu_baseline(lw, w, xs, args.cpu_seconds)
+        log(f"cpu baseline: {cpu['value']:.2f} tokens/s")
+
+    line = {
+        "metric": METRIC,
+        "value": round(tokens_per_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": args.workload,
+            "d_model": E, "experts": w["NE"], "topk": K, "d_ff": w["EI"],
+            "weights": "Q8_0" if w["wtype"] == hipmoe.Q8_0 else "Q4_0",
+            "tokens_per_call": T, "renorm": bool(w["renorm"]),
+            "router_bias_std": w["bias_std"], "layer_copies": nl, "distinct_inputs": ntok,
+            "graphs": bool(graphs),
+            "mean_unique_experts": round(float(np.mean(uniq)), 3),
+            "algorithmic_bytes_per_call": int(bytes_per_call),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "whole layer call (router, softmax/top-k, gate/up, down, combine)",
+            "achieved": round(achieved_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

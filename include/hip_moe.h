@@ -1,0 +1,134 @@
+/*
+ * hip_moe.h - C ABI of the MI355X (gfx950) quantized mixture-of-experts FFN.
+ *
+ * Drop-in for the body of the reference's moe_ffn:
+ *   models/olmoe/olmoe.c:343-407   (OLMoE: softmax top-k, no renormalisation)
+ *   models/llama/llama.c:393-457   (Mixtral: top-k weights renormalised)
+ * and everything below it on that call (router GEMV/GEMM matmul.c:270-324,
+ * softmax_1d nn.c:221-262, top_k nn.c:276-308, fused_ffn_silu nn.c:496-539,
+ * the Q8_0/Q4_0 dots quant.c:103-155, the combine tensor.c:334-353,435-456).
+ *
+ * Plain C: pointers, sizes and ints only.  Conventions follow the
+ * reference's fused_ffn_silu (nn.h:33-39): an int return of 1 means "done",
+ * 0 means "not applicable" (unsupported type or shape, no device, HIP error),
+ * in which case the caller runs its own CPU body.  Errors are also printed to
+ * stderr and kept for hip_moe_last_error().  Nothing here calls exit().
+ *
+ * Expert ids and routing weights are bit-identical to the reference's AVX2
+ * build; layer outputs agree with it to ~1e-6 relative L2 (fp32 throughout).
+ *
+ * Threading: a layer object owns one HIP stream and device scratch; calls on
+ * the same layer object must not overlap (the reference is single-threaded
+ * per model too, thread_pool.c:45).
+ */
+#ifndef HIP_MOE_H
+#define HIP_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Weight block types: the reference's enum tensor_dtype values (tensor.h:10-17).
+ * Q8_0 = 34-byte blocks {f16 d; int8 qs[32]}, Q4_0 = 18-byte blocks
+ * {f16 d; uint8 qs[16]} (quant.h:14-26), rows of cols/32 blocks, row-major. */
+#define HIP_MOE_Q8_0 1
+#define HIP_MOE_Q4_0 2
+
+typedef struct hip_moe_layer hip_moe_layer;
+
+/*
+ * Upload one MoE layer's weights to device memory, once, in their native GGUF
+ * block layout.  Replaces the residency of
+ *   olmoe_load  (olmoe.c:179-182: ffn_gate_inp + stacked *_exps tensors) and
+ *   llama_load  (llama.c:157-166: ffn_gate_inp + per-expert tensors).
+ *
+ * gate_inp : router weights, fp32 [NE][E] (tensor gate_inp->data).
+ * gate_e, up_e : NE base pointers, each to EI rows of E columns (blocks).
+ * down_e   : NE base pointers, each to E rows of EI columns (blocks).
+ *            For OLMoE's stacked tensors pass base + e * expert_bytes, exactly
+ *            the view tensor_at_q (olmoe.c:20-60) forms; for Mixtral pass
+ *            hl->gate_exp[e]->qdata etc.
+ * wtype    : HIP_MOE_Q8_0 or HIP_MOE_Q4_0 (all three matrices the same type).
+ * topk     : experts per token (1 <= topk <= NE <= 256).
+ * renorm   : 0 = OLMoE (weights are the softmax probabilities),
+ *            1 = Mixtral (weights divided by their sequential sum, llama.c:422-427).
+ * E and EI must be multiples of 256.
+ *
+ * Host buffers are only read; the caller keeps ownership (GGUF mmap views).
+ * Returns NULL if not applicable (no device, unsupported type/shape, OOM).
+ */
+hip_moe_layer *hip_moe_upload(const float *gate_inp,
+                              const void *const *gate_e,
+                              const void *const *up_e,
+                              const void *const *down_e,
+                              int wtype, size_t E, size_t EI, size_t NE,
+                              size_t topk, int renorm);
+
+/*
+ * out[T][E] = moe_ffn(x[T][E]), synchronous, host fp32 buffers (the contract
+ * of moe_ffn(model, input, output, l): output is overwritten, olmoe.c:357).
+ *
+ * router_bias : optional fp32 [NE] added to every token's router logits
+ *               first, as the reference's add argument of
+ *               tensor_mma_transposed_2x2 does (matmul.c:13-33): logit =
+ *               bias + dot.  NULL = no bias (what moe_ffn passes).
+ * ids_out     : optional [T][topk] expert ids, ascending weight (top_k order).
+ * w_out       : optional [T][topk] routing weights (after renorm if enabled).
+ * Returns 1 on success, 0 if not applicable.
+ */
+int hip_moe_ffn(hip_moe_layer *L, const float *x, float *out, size_t T,
+                const float *router_bias, uint32_t *ids_out, float *w_out);
+
+/*
+ * Same as hip_moe_ffn with every pointer in device memory, enqueued on
+ * `stream` (a hipStream_t; NULL = the layer's own stream) without waiting.
+ * This is the form a device-resident forward pass (and a HIP graph) uses.
+ */
+int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
+                    const float *d_router_bias, uint32_t *d_ids_out,
+                    float *d_w_out, void *stream);
+
+/*
+ * Routing stage alone, device pointers, enqueued on `stream`:
+ * router logits (matmul.c:270-324), softmax_1d (nn.c:221-262), top_k
+ * (nn.c:276-308) and the Mixtral renormalisation (llama.c:422-427).
+ * d_logits [T][NE] receives the raw logits and d_probs [T][NE] the softmax
+ * probabilities (either may be NULL); d_ids/d_w [T][topk] are required.
+ */
+int hip_moe_route_dev(hip_moe_layer *L, const float *d_x, size_t T,
+                      const float *d_router_bias, float *d_logits,
+                      float *d_probs, uint32_t *d_ids, float *d_w,
+                      void *stream);
+
+/*
+ * One expert for one token, device pointers: out[E] = down_e .
+ * (silu(gate_e . x) * (up_e . x)).  The per-expert body of moe_ffn, i.e.
+ * fused_ffn_silu (nn.c:496-539) on the views tensor_at_q forms.
+ */
+int hip_moe_expert_ffn_dev(hip_moe_layer *L, size_t expert, const float *d_x,
+                           float *d_out, void *stream);
+
+/* Release the device copies and scratch of a layer (NULL is a no-op). */
+void hip_moe_free(hip_moe_layer *L);
+
+/* Device bytes held by the layer's weights (router + experts). */
+size_t hip_moe_weight_bytes(const hip_moe_layer *L);
+
+/* The last error message of this library ("" if none). */
+const char *hip_moe_last_error(void);
+
+/*
+ * expf as the device evaluates it inside softmax and SwiGLU, over n floats
+ * in device memory.  It has no counterpart in the reference; it exists so the
+ * device function can be compared with the host's glibc expf (which the
+ * reference calls, vector_avx2.h:50-63) over every input.
+ */
+int hip_moe_expf_dev(const float *d_in, float *d_out, size_t n, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,384 @@
+/*
+ * hip_moe.c - thin C host layer of the MI355X MoE FFN (see include/hip_moe.h).
+ *
+ * Owns device residency of one layer's weights (uploaded once, GGUF block
+ * layout unchanged), per-layer scratch, and the launch sequence
+ *   router -> softmax/top-k -> gate/up + SwiGLU -> down -> combine
+ * that replaces the per-token loop of moe_ffn (olmoe.c:359-406,
+ * llama.c:409-456).  Errors follow the reference's "return 0, caller falls
+ * back" convention of fused_ffn_silu (nn.c:496-539): nothing here aborts.
+ */
+#include "hip_moe.h"
+#include "moe_internal.h"
+
+#include <hip/hip_runtime_api.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+struct hip_moe_layer {
+	int wtype;
+	size_t E, EI, NE, topk;
+	int renorm;
+	int device;
+
+	size_t rb_in;       /* bytes of one row with E columns */
+	size_t rb_mid;      /* bytes of one row with EI columns */
+	size_t gu_stride;   /* bytes of one expert's gate (or up) matrix */
+	size_t down_stride; /* bytes of one expert's down matrix */
+	int kchunks;        /* K-chunks of a down row */
+
+	float *d_router;
+	uint8_t *d_weights; /* [gate NE][up NE][down NE] */
+	uint8_t *d_gate, *d_up, *d_down;
+	size_t weight_bytes;
+
+	hipStream_t stream;
+
+	/* scratch for up to cap_T tokens */
+	size_t cap_T;
+	float *d_logits;
+	uint32_t *d_ids;
+	float *d_w;
+	float *d_h;
+	float *d_ypart;
+
+	/* staging for the host-pointer entry point */
+	size_t cap_io;
+	float *d_x, *d_out, *d_bias;
+	uint32_t *d_ids_io;
+	float *d_w_io;
+};
+
+static __thread char g_err[512];
+
+static void set_err(const char *fmt, ...)
+{
+	va_list ap;
+	va_start(ap, fmt);
+	vsnprintf(g_err, sizeof(g_err), fmt, ap);
+	va_end(ap);
+	fprintf(stderr, "hip_moe: %s\n", g_err);
+}
+
+const char *hip_moe_last_error(void)
+{
+	return g_err;
+}
+
+#define HIPCHK(call, what)                                                        \
+	do {                                                                      \
+		hipError_t e_ = (call);                                           \
+		if (e_ != hipSuccess) {                                           \
+			set_err("%s: %s", what, hipGetErrorString(e_));            \
+			goto fail;                                                \
+		}                                                                 \
+	} while (0)
+
+#define LCHK(rc, what)                                                            \
+	do {                                                                      \
+		int r_ = (rc);                                                    \
+		if (r_ != 0) {                                                    \
+			set_err("%s: %s", what, hipGetErrorString((hipError_t)r_)); \
+			return 0;                                                 \
+		}                                                                 \
+	} while (0)
+
+static size_t row_bytes(int wtype, size_t n)
+{
+	return (n / MOE_QK) * (wtype == HIP_MOE_Q8_0 ? 34 : 18);
+}
+
+static int is_pow2(size_t v)
+{
+	return v && !(v & (v - 1));
+}
+
+void hip_moe_free(hip_moe_layer *L)
+{
+	if (!L)
+		return;
+	hipFree(L->d_router);
+	hipFree(L->d_weights);
+	hipFree(L->d_logits);
+	hipFree(L->d_ids);
+	hipFree(L->d_w);
+	hipFree(L->d_h);
+	hipFree(L->d_ypart);
+	hipFree(L->d_x);
+	hipFree(L->d_out);
+	hipFree(L->d_bias);
+	hipFree(L->d_ids_io);
+	hipFree(L->d_w_io);
+	if (L->stream)
+		hipStreamDestroy(L->stream);
+	free(L);
+}
+
+hip_moe_layer *hip_moe_upload(const float *gate_inp, const void *const *gate_e,
+			      const void *const *up_e, const void *const *down_e,
+			      int wtype, size_t E, size_t EI, size_t NE, size_t topk,
+			      int renorm)
+{
+	hip_moe_layer *L = NULL;
+	int ndev = 0;
+
+	if (wtype != HIP_MOE_Q8_0 && wtype != HIP_MOE_Q4_0) {
+		set_err("upload: unsupported weight type %d (Q8_0=1, Q4_0=2)", wtype);
+		return NULL;
+	}
+	if (!gate_inp || !gate_e || !up_e || !down_e) {
+		set_err("upload: NULL weight pointer");
+		return NULL;
+	}
+	if (E == 0 || EI == 0 || E % 256 || EI % 256) {
+		set_err("upload: E=%zu and EI=%zu must be non-zero multiples of 256", E, EI);
+		return NULL;
+	}
+	/* gate/up rows are covered by one wave without K-split: E/64 lanes */
+	if (!is_pow2(E / MOE_SEG_COLS) || E / MOE_SEG_COLS > 64) {
+		set_err("upload: E=%zu not supported (needs E/64 a power of two <= 64)", E);
+		return NULL;
+	}
+	if (NE == 0 || NE > MOE_MAX_NE || topk == 0 || topk > NE || topk > MOE_MAX_TOPK) {
+		set_err("upload: NE=%zu topk=%zu out of range (1<=topk<=NE<=%d, topk<=%d)",
+			NE, topk, MOE_MAX_NE, MOE_MAX_TOPK);
+		return NULL;
+	}
+	if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1) {
+		set_err("upload: no HIP device");
+		return NULL;
+	}
+
+	L = calloc(1, sizeof(*L));
+	if (!L) {
+		set_err("upload: out of host memory");
+		return NULL;
+	}
+	L->wtype = wtype;
+	L->E = E;
+	L->EI = EI;
+	L->NE = NE;
+	L->topk = topk;
+	L->renorm = renorm ? 1 : 0;
+	L->rb_in = row_bytes(wtype, E);
+	L->rb_mid = row_bytes(wtype, EI);
+	L->gu_stride = EI * L->rb_in;
+	L->down_stride = E * L->rb_mid;
+	L->kchunks = moe_kchunks(EI);
+	L->weight_bytes = NE * E * sizeof(float) + NE * (2 * L->gu_stride + L->down_stride);
+
+	HIPCHK(hipGetDevice(&L->device), "hipGetDevice");
+	HIPCHK(hipStreamCreateWithFlags(&L->stream, hipStreamNonBlocking), "hipStreamCreate");
+	HIPCHK(hipMalloc((void **)&L->d_router, NE * E * sizeof(float)), "hipMalloc(router)");
+	HIPCHK(hipMalloc((void **)&L->d_weights, NE * (2 * L->gu_stride + L->down_stride)),
+	       "hipMalloc(experts)");
+	L->d_gate = L->d_weights;
+	L->d_up = L->d_gate + NE * L->gu_stride;
+	L->d_down = L->d_up + NE * L->gu_stride;
+
+	HIPCHK(hipMemcpy(L->d_router, gate_inp, NE * E * sizeof(float), hipMemcpyHostToDevice),
+	       "upload router");
+	for (size_t e = 0; e < NE; e++) {
+		if (!gate_e[e] || !up_e[e] || !down_e[e]) {
+			set_err("upload: NULL pointer for expert %zu", e);
+			goto fail;
+		}
+		HIPCHK(hipMemcpy(L->d_gate + e * L->gu_stride, gate_e[e], L->gu_stride,
+				 hipMemcpyHostToDevice), "upload gate");
+		HIPCHK(hipMemcpy(L->d_up + e * L->gu_stride, up_e[e], L->gu_stride,
+				 hipMemcpyHostToDevice), "upload up");
+		HIPCHK(hipMemcpy(L->d_down + e * L->down_stride, down_e[e], L->down_stride,
+				 hipMemcpyHostToDevice), "upload down");
+	}
+	return L;
+fail:
+	hip_moe_free(L);
+	return NULL;
+}
+
+size_t hip_moe_weight_bytes(const hip_moe_layer *L)
+{
+	return L ? L->weight_bytes : 0;
+}
+
+static int ensure_scratch(hip_moe_layer *L, size_t T)
+{
+	if (T <= L->cap_T)
+		return 1;
+	size_t P = T * L->topk;
+	hipFree(L->d_logits);
+	hipFree(L->d_ids);
+	hipFree(L->d_w);
+	hipFree(L->d_h);
+	hipFree(L->d_ypart);
+	L->d_logits = NULL;
+	L->d_ids = NULL;
+	L->d_w = NULL;
+	L->d_h = NULL;
+	L->d_ypart = NULL;
+	L->cap_T = 0;
+	HIPCHK(hipMalloc((void **)&L->d_logits, T * L->NE * sizeof(float)), "hipMalloc(logits)");
+	HIPCHK(hipMalloc((void **)&L->d_ids, P * sizeof(uint32_t)), "hipMalloc(ids)");
+	HIPCHK(hipMalloc((void **)&L->d_w, P * sizeof(float)), "hipMalloc(w)");
+	HIPCHK(hipMalloc((void **)&L->d_h, P * L->EI * sizeof(float)), "hipMalloc(h)");
+	HIPCHK(hipMalloc((void **)&L->d_ypart, P * L->kchunks * L->E * sizeof(float)),
+	       "hipMalloc(ypart)");
+	L->cap_T = T;
+	return 1;
+fail:
+	return 0;
+}
+
+static hipStream_t pick_stream(hip_moe_layer *L, void *stream)
+{
+	return stream ? (hipStream_t)stream : L->stream;
+}
+
+static int check_T(size_t T)
+{
+	if (T == 0 || T > 65535) {
+		set_err("token count %zu out of range 1..65535", T);
+		return 0;
+	}
+	return 1;
+}
+
+static int route(hip_moe_layer *L, const float *d_x, size_t T, const float *d_bias,
+		 float *d_logits, float *d_probs, uint32_t *d_ids, float *d_w,
+		 hipStream_t s)
+{
+	LCHK(moe_launch_router(d_x, L->d_router, d_bias, d_logits, (int)T, (int)L->E,
+			       (int)L->NE, s), "router");
+	LCHK(moe_launch_softmax_topk(d_logits, d_probs, d_ids, d_w, (int)T, (int)L->NE,
+				     (int)L->topk, L->renorm, s), "softmax/top-k");
+	return 1;
+}
+
+int hip_moe_route_dev(hip_moe_layer *L, const float *d_x, size_t T,
+		      const float *d_router_bias, float *d_logits, float *d_probs,
+		      uint32_t *d_ids, float *d_w, void *stream)
+{
+	if (!L || !d_x || !d_ids || !d_w) {
+		set_err("route: NULL argument");
+		return 0;
+	}
+	if (!check_T(T) || !ensure_scratch(L, T))
+		return 0;
+	return route(L, d_x, T, d_router_bias, d_logits ? d_logits : L->d_logits, d_probs,
+		     d_ids, d_w, pick_stream(L, stream));
+}
+
+int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
+		    const float *d_router_bias, uint32_t *d_ids_out, float *d_w_out,
+		    void *stream)
+{
+	if (!L || !d_x || !d_out) {
+		set_err("ffn: NULL argument");
+		return 0;
+	}
+	if (!check_T(T) || !ensure_scratch(L, T))
+		return 0;
+	hipStream_t s = pick_stream(L, stream);
+	uint32_t *ids = d_ids_out ? d_ids_out : L->d_ids;
+	float *w = d_w_out ? d_w_out : L->d_w;
+	int P = (int)(T * L->topk);
+
+	if (!route(L, d_x, T, d_router_bias, L->d_logits, NULL, ids, w, s))
+		return 0;
+	LCHK(moe_launch_gateup(L->wtype, L->d_gate, L->d_up, L->gu_stride, ids, -1, d_x,
+			       L->d_h, P, (int)L->topk, (int)L->E, (int)L->EI, s),
+	     "gate/up");
+	LCHK(moe_launch_down(L->wtype, L->d_down, L->down_stride, ids, -1, L->d_h,
+			     L->d_ypart, P, (int)L->topk, (int)L->E, (int)L->EI, s),
+	     "down");
+	LCHK(moe_launch_combine(L->d_ypart, w, d_out, (int)T, (int)L->topk, (int)L->E,
+				L->kchunks, s), "combine");
+	return 1;
+}
+
+int hip_moe_expert_ffn_dev(hip_moe_layer *L, size_t expert, const float *d_x,
+			   float *d_out, void *stream)
+{
+	if (!L || !d_x || !d_out) {
+		set_err("expert_ffn: NULL argument");
+		return 0;
+	}
+	if (expert >= L->NE) {
+		set_err("expert_ffn: expert %zu >= NE %zu", expert, L->NE);
+		return 0;
+	}
+	if (!ensure_scratch(L, 1))
+		return 0;
+	hipStream_t s = pick_stream(L, stream);
+	LCHK(moe_launch_gateup(L->wtype, L->d_gate, L->d_up, L->gu_stride, NULL, (int)expert,
+			       d_x, L->d_h, 1, 1, (int)L->E, (int)L->EI, s), "gate/up");
+	LCHK(moe_launch_down(L->wtype, L->d_down, L->down_stride, NULL, (int)expert, L->d_h,
+			     L->d_ypart, 1, 1, (int)L->E, (int)L->EI, s), "down");
+	LCHK(moe_launch_combine(L->d_ypart, NULL, d_out, 1, 1, (int)L->E, L->kchunks, s),
+	     "combine");
+	return 1;
+}
+
+static int ensure_io(hip_moe_layer *L, size_t T)
+{
+	if (T <= L->cap_io)
+		return 1;
+	hipFree(L->d_x);
+	hipFree(L->d_out);
+	hipFree(L->d_bias);
+	hipFree(L->d_ids_io);
+	hipFree(L->d_w_io);
+	L->d_x = L->d_out = L->d_bias = L->d_w_io = NULL;
+	L->d_ids_io = NULL;
+	L->cap_io = 0;
+	HIPCHK(hipMalloc((void **)&L->d_x, T * L->E * sizeof(float)), "hipMalloc(x)");
+	HIPCHK(hipMalloc((void **)&L->d_out, T * L->E * sizeof(float)), "hipMalloc(out)");
+	HIPCHK(hipMalloc((void **)&L->d_bias, L->NE * sizeof(float)), "hipMalloc(bias)");
+	HIPCHK(hipMalloc((void **)&L->d_ids_io, T * L->topk * sizeof(uint32_t)),
+	       "hipMalloc(ids)");
+	HIPCHK(hipMalloc((void **)&L->d_w_io, T * L->topk * sizeof(float)), "hipMalloc(w)");
+	L->cap_io = T;
+	return 1;
+fail:
+	return 0;
+}
+
+int hip_moe_ffn(hip_moe_layer *L, const float *x, float *out, size_t T,
+		const float *router_bias, uint32_t *ids_out, float *w_out)
+{
+	if (!L || !x || !out) {
+		set_err("ffn: NULL argument");
+		return 0;
+	}
+	if (!check_T(T) || !ensure_io(L, T))
+		return 0;
+	hipStream_t s = L->stream;
+	HIPCHK(hipMemcpyAsync(L->d_x, x, T * L->E * sizeof(float), hipMemcpyHostToDevice, s),
+	       "copy x");
+	if (router_bias)
+		HIPCHK(hipMemcpyAsync(L->d_bias, router_bias, L->NE * sizeof(float),
+				      hipMemcpyHostToDevice, s), "copy bias");
+	if (!hip_moe_ffn_dev(L, L->d_x, L->d_out, T, router_bias ? L->d_bias : NULL,
+			     L->d_ids_io, L->d_w_io, s))
+		return 0;
+	HIPCHK(hipMemcpyAsync(out, L->d_out, T * L->E * sizeof(float), hipMemcpyDeviceToHost, s),
+	       "copy out");
+	if (ids_out)
+		HIPCHK(hipMemcpyAsync(ids_out, L->d_ids_io, T * L->topk * sizeof(uint32_t),
+				      hipMemcpyDeviceToHost, s), "copy ids");
+	if (w_out)
+		HIPCHK(hipMemcpyAsync(w_out, L->d_w_io, T * L->topk * sizeof(float),
+				      hipMemcpyDeviceToHost, s), "copy w");
+	HIPCHK(hipStreamSynchronize(s), "synchronize");
+	return 1;
+fail:
+	return 0;
+}
+
+int hip_moe_expf_dev(const float *d_in, float *d_out, size_t n, void *stream)
+{
+	LCHK(moe_launch_expf(d_in, d_out, n, stream), "expf");
+	return 1;
+}

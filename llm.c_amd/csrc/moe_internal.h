@@ -1,0 +1,56 @@
+/*
+ * Internal interface between the C host layer (hip_moe.c) and the HIP
+ * kernels (moe_kernels.hip).  Every launcher returns a hipError_t value
+ * (0 = success) and enqueues on the given stream without waiting.
+ */
+#ifndef MOE_INTERNAL_H
+#define MOE_INTERNAL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Geometry shared by host and kernels. */
+#define MOE_QK 32           /* elements per block */
+#define MOE_SEG_COLS 64     /* columns one lane holds: a pair of blocks */
+#define MOE_MAX_NE 256
+#define MOE_MAX_TOPK 64
+
+/* lanes per row for a K-long dot: the largest power of two <= 64 that
+ * divides K / 64, and the number of K-chunks the row is split into. */
+int moe_lanes_per_row(size_t K);
+int moe_kchunks(size_t K);
+
+int moe_launch_router(const float *x, const float *wr, const float *bias,
+                      float *logits, int T, int E, int NE, void *stream);
+
+int moe_launch_softmax_topk(const float *logits, float *probs, uint32_t *ids,
+                            float *w, int T, int NE, int K, int renorm,
+                            void *stream);
+
+/* h[p][EI] = silu(gate_e . x_t) * (up_e . x_t), p = t*K + s, e = ids[p]
+ * (or fixed_e >= 0 for every p). */
+int moe_launch_gateup(int wtype, const uint8_t *gate, const uint8_t *up,
+                      size_t expert_stride, const uint32_t *ids, int fixed_e,
+                      const float *x, float *h, int P, int K, int E, int EI,
+                      void *stream);
+
+/* ypart[p][kc][E] = partial dots of down_e rows with h[p] over K-chunk kc. */
+int moe_launch_down(int wtype, const uint8_t *down, size_t expert_stride,
+                    const uint32_t *ids, int fixed_e, const float *h,
+                    float *ypart, int P, int K, int E, int EI, void *stream);
+
+/* out[t][E] = sum over slots s, in order, of y[t*K+s] / (1/w[t*K+s]);
+ * y = sum of the kchunks partials in order.  w == NULL means weight 1. */
+int moe_launch_combine(const float *ypart, const float *w, float *out, int T,
+                       int K, int E, int kchunks, void *stream);
+
+int moe_launch_expf(const float *in, float *out, size_t n, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

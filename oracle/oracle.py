@@ -1,0 +1,139 @@
+"""ctypes binding of the CPU oracle (liboracle.so, moe_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker.  The product never imports it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+Q8_0, Q4_0 = 1, 2
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built; run `make -C oracle`")
+        L = C.CDLL(LIB_PATH)
+        vp, sz, i32 = C.c_void_p, C.c_size_t, C.c_int
+        L.orc_router.argtypes = [vp, vp, vp, sz, sz, sz, vp]
+        L.orc_router.restype = None
+        L.orc_softmax_1d.argtypes = [vp, sz]
+        L.orc_softmax_1d.restype = None
+        L.orc_top_k.argtypes = [vp, sz, vp, vp, sz]
+        L.orc_top_k.restype = None
+        L.orc_dot_quant.argtypes = [vp, vp, i32, sz]
+        L.orc_dot_quant.restype = C.c_float
+        L.orc_dequant_row.argtypes = [vp, i32, vp, sz]
+        L.orc_dequant_row.restype = None
+        L.orc_fused_ffn.argtypes = [vp, vp, vp, vp, i32, sz, sz, vp, vp]
+        L.orc_fused_ffn.restype = None
+        L.orc_moe_ffn.argtypes = [vp, vp, sz, vp, vp, vp, vp, vp, i32, sz, sz, sz, sz, i32,
+                                  vp, vp, vp, vp, i32]
+        L.orc_moe_ffn.restype = None
+        L.orc_expf_array.argtypes = [vp, vp, sz]
+        L.orc_expf_array.restype = None
+        L.orc_expf_bits.argtypes = [C.c_uint32, sz, vp, i32]
+        L.orc_expf_bits.restype = None
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def _ptrs(stacked):
+    arr = (C.c_void_p * stacked.shape[0])()
+    for e in range(stacked.shape[0]):
+        arr[e] = stacked[e].ctypes.data
+    return arr
+
+
+def threads() -> int:
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def router(x, wr, bias=None):
+    x = np.ascontiguousarray(x, np.float32)
+    wr = np.ascontiguousarray(wr, np.float32)
+    T, E = x.shape
+    NE = wr.shape[0]
+    out = np.empty((T, NE), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().orc_router(_p(x), _p(wr), _p(b), T, E, NE, _p(out))
+    return out
+
+
+def softmax(row):
+    r = np.array(row, np.float32, copy=True)
+    lib().orc_softmax_1d(_p(r), r.size)
+    return r
+
+
+def top_k(row, k):
+    r = np.ascontiguousarray(row, np.float32)
+    ids = np.empty(k, np.uint32)
+    w = np.empty(k, np.float32)
+    lib().orc_top_k(_p(r), r.size, _p(ids), _p(w), k)
+    return ids, w
+
+
+def dot(x, qrow, wtype):
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.ascontiguousarray(qrow, np.uint8)
+    return np.float32(lib().orc_dot_quant(_p(x), _p(q), wtype, x.size))
+
+
+def dequant(qrow, wtype, n):
+    q = np.ascontiguousarray(qrow, np.uint8)
+    out = np.empty(n, np.float32)
+    lib().orc_dequant_row(_p(q), wtype, _p(out), n)
+    return out
+
+
+def fused_ffn(x, gate, up, down, wtype, E, EI):
+    x = np.ascontiguousarray(x, np.float32)
+    h = np.empty(EI, np.float32)
+    out = np.empty(E, np.float32)
+    lib().orc_fused_ffn(_p(x), _p(gate), _p(up), _p(down), wtype, E, EI, _p(h), _p(out))
+    return out
+
+
+def moe_ffn(x, layer: dict, topk: int, renorm: bool, bias=None, nthreads=None):
+    """Whole layer: returns (out, ids, w, logits, probs)."""
+    x = np.ascontiguousarray(x, np.float32)
+    T, E = x.shape
+    NE, EI = layer["NE"], layer["EI"]
+    out = np.empty((T, E), np.float32)
+    ids = np.empty((T, topk), np.uint32)
+    w = np.empty((T, topk), np.float32)
+    lg = np.empty((T, NE), np.float32)
+    pr = np.empty((T, NE), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().orc_moe_ffn(_p(x), _p(out), T, _p(layer["router"]), _p(b), _ptrs(layer["gate"]),
+                      _ptrs(layer["up"]), _ptrs(layer["down"]), layer["wtype"], E, EI, NE,
+                      topk, int(renorm), _p(ids), _p(w), _p(lg), _p(pr),
+                      nthreads or threads())
+    return out, ids, w, lg, pr
+
+
+def expf(x):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    lib().orc_expf_array(_p(x), _p(out), x.size)
+    return out
+
+
+def expf_bits(bits0: int, n: int, nthreads=None):
+    out = np.empty(n, np.float32)
+    lib().orc_expf_bits(bits0, n, _p(out), nthreads or threads())
+    return out

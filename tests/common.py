@@ -1,0 +1,98 @@
+"""Shared helpers for the tests: configurations, golden fixtures, metrics."""
+from __future__ import annotations
+
+import ctypes as C
+import functools
+import hashlib
+import os
+
+import numpy as np
+
+import hipmoe
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+GOLDEN = os.path.join(HERE, "golden")
+REPO = os.path.abspath(os.path.join(HERE, ".."))
+SEED = 1337
+
+# name: (wtype, E, EI, NE, topk, renorm, bias_std)
+CONFIGS = {
+    "olmoe_q8": (hipmoe.Q8_0, 2048, 1024, 64, 8, 0, None),
+    "olmoe_q4_skew": (hipmoe.Q4_0, 2048, 1024, 64, 8, 0, 1.0),
+    "mixtral_q4": (hipmoe.Q4_0, 4096, 14336, 8, 2, 1, None),
+}
+
+# Output tolerance of the layer (relative L2 against the reference CPU path).
+REL_L2_TOL = 1e-3
+
+
+def sha(a) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def golden(name: str):
+    return np.load(os.path.join(GOLDEN, name), allow_pickle=False)
+
+
+def rel_l2(a, b) -> float:
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def bits(a) -> np.ndarray:
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@functools.lru_cache(maxsize=2)
+def layer(cfg: str, layer_index: int = 0) -> dict:
+    wt, E, EI, NE, K, renorm, bias_std = CONFIGS[cfg]
+    return hipmoe.synth_layer(SEED, layer_index, wt, E, EI, NE, 0.02, bias_std)
+
+
+def router_inputs(cfg: str, T: int, call: int):
+    wt, E, EI, NE, K, renorm, bias_std = CONFIGS[cfg]
+    L = hipmoe.lib()
+    wr = hipmoe.synth_normal(SEED, L.moe_stream_router(0), NE * E, 0.0, 0.02).reshape(NE, E)
+    bias = None
+    if bias_std is not None:
+        bias = hipmoe.synth_normal(SEED, L.moe_stream_bias(0), NE, 0.0, bias_std)
+    x = hipmoe.synth_normal(SEED, L.moe_stream_input(call), T * E).reshape(T, E)
+    return wr, bias, x
+
+
+_host_expf = None
+
+
+def host_expf_lib():
+    global _host_expf
+    if _host_expf is None:
+        path = os.path.join(HERE, "native", "libhost_expf.so")
+        L = C.CDLL(path)
+        L.host_expf_mismatches.restype = C.c_uint64
+        L.host_expf_mismatches.argtypes = [C.c_uint32, C.c_uint64, C.c_uint64, C.c_int,
+                                           C.POINTER(C.c_uint32)]
+        L.host_moe_expf.restype = None
+        L.host_moe_expf.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64]
+        _host_expf = L
+    return _host_expf
+
+
+def top_k_closed_form(p: np.ndarray, k: int):
+    """The closed form the device evaluates for top_k (nn.c:276-308):
+    rank_i = #{j: p_j > p_i or (p_j == p_i and j < i)}, r0 = rank_0; i != 0
+    goes to slot k-1-rank_i iff rank_i < min(r0, k); slots 0..k-1-r0 hold
+    element 0 when r0 < k."""
+    n = p.size
+    idx = np.arange(n)
+    gt = (p[None, :] > p[:, None]) | ((p[None, :] == p[:, None]) & (idx[None, :] < idx[:, None]))
+    rank = gt.sum(axis=1)
+    r0 = int(rank[0])
+    ids = np.zeros(k, np.uint32)
+    w = np.full(k, p[0], np.float32)
+    lim = min(r0, k)
+    for i in range(1, n):
+        if rank[i] < lim:
+            ids[k - 1 - rank[i]] = i
+            w[k - 1 - rank[i]] = p[i]
+    return ids, w

@@ -1,0 +1,183 @@
+"""Write golden vectors for the MoE FFN path from the compiled reference.
+
+Run in a container that holds the reference tree (after
+`oracle/ref/build_ref.sh`), as a standalone process:
+
+    python tests/golden/make_golden.py
+
+The reference library (oracle/_ref/libref_moe.so) is built from the
+reference's own C sources with AVX2 flags; its thread pool starts with the
+library and spins until the process exits, which is why this is a separate
+script.  Inputs come from the package's seeded generator (llm.c_amd/host/
+synth.c); each fixture stores the seed plus SHA-256 digests of the generated
+input bytes, so a test regenerates the inputs and first proves they are the
+same bytes.  Outputs are the reference's own results:
+
+  quant.npz          quantize_row_q8_0 (quant.c:62-78) and the Q4_0 quantizer
+                     of test/quant.c:45-79 on seeded and edge-case blocks
+  dot.npz            dot_f32_quant (quant.c:577-614) on seeded rows
+  route_<cfg>.npz    router logits, softmax probabilities, top-k ids/weights
+                     (matmul.c:451-462, nn.c:221-308, llama.c:422-427)
+  ffn_<wt>.npz       fused_ffn_silu for one expert (nn.c:496-539)
+  moe_<cfg>.npz      full moe_ffn layer outputs (olmoe.c:343-407,
+                     llama.c:393-457; with a router bias through the add
+                     argument of tensor_mma_transposed_2x2)
+"""
+from __future__ import annotations
+
+import ctypes as C
+import hashlib
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.abspath(os.path.join(HERE, "..", ".."))
+sys.path.insert(0, os.path.join(REPO, "llm.c_amd"))
+import hipmoe  # noqa: E402
+
+SEED = 1337
+REF_LIB = os.path.join(REPO, "oracle", "_ref", "libref_moe.so")
+
+CONFIGS = {
+    # name: (wtype, E, EI, NE, topk, renorm, bias_std)
+    "olmoe_q8": (hipmoe.Q8_0, 2048, 1024, 64, 8, 0, None),
+    "olmoe_q4_skew": (hipmoe.Q4_0, 2048, 1024, 64, 8, 0, 1.0),
+    "mixtral_q4": (hipmoe.Q4_0, 4096, 14336, 8, 2, 1, None),
+}
+
+
+def sha(a: np.ndarray) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def ref():
+    L = C.CDLL(REF_LIB)
+    vp, sz, i32 = C.c_void_p, C.c_size_t, C.c_int
+    L.ref_route.argtypes = [vp, sz, sz, sz, vp, vp, sz, i32, vp, vp, vp, vp]
+    L.ref_moe_ffn_composed.argtypes = [vp, vp, sz, vp, vp, vp, vp, vp, i32, sz, sz, sz, sz,
+                                       i32]
+    L.ref_olmoe_moe_ffn.argtypes = [vp, vp, sz, vp, vp, vp, vp, i32, sz, sz, sz, sz]
+    L.ref_llama_moe_ffn.argtypes = [vp, vp, sz, vp, vp, vp, vp, i32, sz, sz, sz, sz]
+    L.ref_fused_ffn.argtypes = [vp, vp, vp, vp, i32, sz, sz, vp]
+    L.ref_dot.argtypes = [vp, vp, i32, sz]
+    L.ref_dot.restype = C.c_float
+    L.ref_quantize_q8_0.argtypes = [vp, vp, sz]
+    L.ref_quantize_q4_0.argtypes = [vp, vp, sz]
+    return L
+
+
+def p(a):
+    return None if a is None else a.ctypes.data
+
+
+def quant_blocks() -> np.ndarray:
+    """Seeded blocks plus edge cases, 32 floats each."""
+    rng_blocks = [hipmoe.synth_normal(SEED, 0x5151_0000 + i, 32, 0.0, s)
+                  for i, s in enumerate([0.02] * 24 + [1.0] * 24 + [1e-3, 50.0, 3e4, 1e-6])]
+    edge = []
+    edge.append(np.zeros(32, np.float32))                      # amax = 0
+    b = np.zeros(32, np.float32); b[5] = -1.0; edge.append(b)  # single negative
+    edge.append(np.linspace(-1, 1, 32, dtype=np.float32))      # ramp
+    b = np.full(32, 0.5, np.float32); b[0] = 127.0; edge.append(b)  # x*id ties
+    b = (np.arange(32, dtype=np.float32) - 16) * 0.25; edge.append(b)
+    edge.append(np.full(32, 7e4, np.float32))                   # scale overflows fp16
+    edge.append(np.full(32, -3e-8, np.float32))                 # subnormal fp16 scale
+    b = np.arange(32, dtype=np.float32) / 7.0; edge.append(b)  # Q4 half-way ties
+    return np.stack(rng_blocks + edge).astype(np.float32)
+
+
+def main():
+    if not os.path.exists(REF_LIB):
+        sys.exit(f"{REF_LIB} missing: run oracle/ref/build_ref.sh first")
+    R = ref()
+
+    # ---- quantizers -----------------------------------------------------
+    blocks = quant_blocks()
+    flat = np.ascontiguousarray(blocks.reshape(-1))
+    q8 = np.empty(blocks.shape[0] * 34, np.uint8)
+    q4 = np.empty(blocks.shape[0] * 18, np.uint8)
+    R.ref_quantize_q8_0(p(flat), p(q8), flat.size)
+    R.ref_quantize_q4_0(p(flat), p(q4), flat.size)
+    np.savez(os.path.join(HERE, "quant.npz"), x=blocks, q8_0=q8, q4_0=q4)
+
+    # ---- dots -------------------------------------------------------------
+    dots = {}
+    for wt, name in ((hipmoe.Q8_0, "q8_0"), (hipmoe.Q4_0, "q4_0")):
+        for n in (256, 1024, 2048, 4096, 14336):
+            rows = 4
+            qm = hipmoe.synth_quant_matrix(SEED, 0x7000 + n + wt, 0.02, wt, rows, n)
+            x = hipmoe.synth_normal(SEED, 0x7100 + n + wt, rows * n).reshape(rows, n)
+            rb = hipmoe.row_bytes(wt, n)
+            out = np.array([R.ref_dot(p(np.ascontiguousarray(x[r])),
+                                      p(np.ascontiguousarray(qm[r * rb:(r + 1) * rb])), wt, n)
+                            for r in range(rows)], np.float32)
+            dots[f"{name}_{n}_sha_w"] = sha(qm)
+            dots[f"{name}_{n}_sha_x"] = sha(x)
+            dots[f"{name}_{n}_dot"] = out
+    np.savez(os.path.join(HERE, "dot.npz"), seed=SEED, **dots)
+
+    # ---- routing ----------------------------------------------------------
+    for cfg, (wt, E, EI, NE, K, renorm, bias_std) in CONFIGS.items():
+        T = 2048
+        wr = hipmoe.synth_normal(SEED, hipmoe.lib().moe_stream_router(0), NE * E, 0.0,
+                                 0.02).reshape(NE, E)
+        bias = None
+        if bias_std is not None:
+            bias = hipmoe.synth_normal(SEED, hipmoe.lib().moe_stream_bias(0), NE, 0.0, bias_std)
+        x = hipmoe.synth_normal(SEED, hipmoe.lib().moe_stream_input(777), T * E).reshape(T, E)
+        lg = np.empty((T, NE), np.float32)
+        pr = np.empty((T, NE), np.float32)
+        ids = np.empty((T, K), np.uint32)
+        w = np.empty((T, K), np.float32)
+        R.ref_route(p(x), T, E, NE, p(wr), p(bias), K, renorm, p(lg), p(pr), p(ids), p(w))
+        keep = 256
+        np.savez(os.path.join(HERE, f"route_{cfg}.npz"), seed=SEED, input_call=777, T=T,
+                 sha_x=sha(x), sha_router=sha(wr), sha_bias=sha(bias) if bias is not None else "",
+                 logits=lg[:keep], probs=pr[:keep], ids=ids, w=w)
+        dup = int(np.sum(ids[:, 0] == 0) if K > 1 else 0)
+        print(f"route {cfg}: {T} tokens, tokens with expert 0 in slot 0: {dup}")
+
+    # ---- one expert, one token ---------------------------------------------
+    for wt, name in ((hipmoe.Q8_0, "q8_0"), (hipmoe.Q4_0, "q4_0")):
+        E, EI = 2048, 1024
+        g = hipmoe.synth_quant_matrix(SEED, 0x9001, 0.02, wt, EI, E)
+        u = hipmoe.synth_quant_matrix(SEED, 0x9002, 0.02, wt, EI, E)
+        d = hipmoe.synth_quant_matrix(SEED, 0x9003, 0.02, wt, E, EI)
+        x = hipmoe.synth_normal(SEED, 0x9004, E)
+        out = np.empty(E, np.float32)
+        R.ref_fused_ffn(p(x), p(g), p(u), p(d), wt, E, EI, p(out))
+        np.savez(os.path.join(HERE, f"ffn_{name}.npz"), seed=SEED, sha_gate=sha(g),
+                 sha_up=sha(u), sha_down=sha(d), sha_x=sha(x), out=out)
+
+    # ---- whole layers -----------------------------------------------------------
+    for cfg, (wt, E, EI, NE, K, renorm, bias_std) in CONFIGS.items():
+        T = 4 if NE == 64 else 2
+        layer = hipmoe.synth_layer(SEED, 0, wt, E, EI, NE, 0.02, bias_std)
+        x = hipmoe.synth_input(SEED, 0, T, E)
+        gp, up_, dp = (hipmoe.expert_ptrs(layer[k]) for k in ("gate", "up", "down"))
+        out_c = np.empty((T, E), np.float32)
+        R.ref_moe_ffn_composed(p(x), p(out_c), T, p(layer["router"]), p(layer["bias"]), gp,
+                               up_, dp, wt, E, EI, NE, K, renorm)
+        if layer["bias"] is None:
+            out_s = np.empty((T, E), np.float32)
+            if renorm:
+                R.ref_llama_moe_ffn(p(x), p(out_s), T, p(layer["router"]), gp, up_, dp, wt, E,
+                                    EI, NE, K)
+            else:
+                R.ref_olmoe_moe_ffn(p(x), p(out_s), T, p(layer["router"]), p(layer["gate"]),
+                                    p(layer["up"]), p(layer["down"]), wt, E, EI, NE, K)
+            assert np.array_equal(out_s.view(np.uint32), out_c.view(np.uint32)), \
+                f"{cfg}: composed loop differs from the reference's static moe_ffn"
+            print(f"moe {cfg}: composed loop == static moe_ffn (bitwise)")
+        np.savez(os.path.join(HERE, f"moe_{cfg}.npz"), seed=SEED, T=T,
+                 sha_router=sha(layer["router"]), sha_gate=sha(layer["gate"]),
+                 sha_up=sha(layer["up"]), sha_down=sha(layer["down"]), sha_x=sha(x),
+                 sha_bias=sha(layer["bias"]) if layer["bias"] is not None else "", out=out_c)
+        print(f"moe {cfg}: T={T} |out|={np.linalg.norm(out_c):.4f}")
+        del layer
+
+
+if __name__ == "__main__":
+    main()

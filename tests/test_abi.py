@@ -1,0 +1,94 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry
+point its headers declare, and refuses what it cannot do with the
+reference's "return 0 / NULL, caller falls back" convention (nn.h:33-39)."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+import hipmoe
+from common import REPO
+
+
+def declared_functions(header: str):
+    text = open(os.path.join(REPO, "include", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"\b([a-z_][a-z0-9_]*)\s*\(", text)
+    return sorted({n for n in names if n.startswith(("hip_moe_", "moe_"))})
+
+
+@pytest.mark.parametrize("header", ["hip_moe.h", "moe_synth.h"])
+def test_library_exports_every_declared_symbol(header):
+    L = hipmoe.lib()
+    names = declared_functions(header)
+    assert len(names) >= 5
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def _tiny_layer(wtype=hipmoe.Q8_0, E=256, EI=256, NE=4):
+    rb_in, rb_mid = hipmoe.row_bytes(wtype, E), hipmoe.row_bytes(wtype, EI)
+    router = np.zeros((NE, E), np.float32)
+    gate = np.zeros((NE, EI * rb_in), np.uint8)
+    down = np.zeros((NE, E * rb_mid), np.uint8)
+    return router, gate, gate.copy(), down
+
+
+def _upload(router, gate, up, down, wtype, E, EI, NE, topk, renorm=0):
+    L = hipmoe.lib()
+    return L.hip_moe_upload(router.ctypes.data, hipmoe.expert_ptrs(gate),
+                            hipmoe.expert_ptrs(up), hipmoe.expert_ptrs(down), wtype, E, EI,
+                            NE, topk, renorm)
+
+
+@pytest.mark.parametrize("wtype,E,EI,NE,topk,msg", [
+    (3, 256, 256, 4, 2, "unsupported weight type"),
+    (0, 256, 256, 4, 2, "unsupported weight type"),
+    (1, 250, 256, 4, 2, "multiples of 256"),
+    (1, 256, 300, 4, 2, "multiples of 256"),
+    (1, 768, 256, 4, 2, "not supported"),
+    (1, 256, 256, 4, 5, "out of range"),
+    (1, 256, 256, 300, 2, "out of range"),
+])
+def test_upload_rejects_unsupported(wtype, E, EI, NE, topk, msg):
+    router, gate, up, down = _tiny_layer(1 if wtype not in (1, 2) else wtype, 256, 256, 4)
+    h = _upload(router, gate, up, down, wtype, E, EI, NE, topk)
+    assert not h
+    assert msg in hipmoe.last_error()
+
+
+def test_calls_on_null_layer_return_zero():
+    L = hipmoe.lib()
+    x = np.zeros(256, np.float32)
+    assert L.hip_moe_ffn(None, x.ctypes.data, x.ctypes.data, 1, None, None, None) == 0
+    assert L.hip_moe_ffn_dev(None, 1, 1, 1, None, None, None, None) == 0
+    assert L.hip_moe_route_dev(None, 1, 1, None, None, None, 1, 1, None) == 0
+    assert L.hip_moe_expert_ffn_dev(None, 0, 1, 1, None) == 0
+    L.hip_moe_free(None)
+    assert L.hip_moe_weight_bytes(None) == 0
+
+
+def test_upload_without_device_returns_null():
+    if hipmoe.hip().device_count() > 0:
+        pytest.skip("a GPU is visible")
+    router, gate, up, down = _tiny_layer()
+    assert not _upload(router, gate, up, down, 1, 256, 256, 4, 2)
+    assert "no HIP device" in hipmoe.last_error()
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(hipmoe, "_lib", None)
+    monkeypatch.setattr(hipmoe, "LIB_PATH", str(tmp_path / "nope.so"))
+    with pytest.raises(hipmoe.HipMoeError):
+        hipmoe.lib()
+
+
+def test_oracle_library_is_separate_from_product():
+    """The product library links nothing from oracle/."""
+    import subprocess
+    out = subprocess.run(["ldd", hipmoe.LIB_PATH], capture_output=True, text=True).stdout
+    assert "oracle" not in out
+    syms = subprocess.run(["nm", "-D", hipmoe.LIB_PATH], capture_output=True, text=True).stdout
+    assert "orc_" not in syms and "ref_" not in syms

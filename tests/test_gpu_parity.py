@@ -1,0 +1,277 @@
+"""GPU parity: the HIP path (through the C ABI) against the oracle and the
+reference's golden vectors.
+
+Bars:
+  * expert ids, routing weights, router logits, softmax probabilities:
+    bit-exact (the reference's AVX2 build, tests/golden/);
+  * layer outputs: relative L2 <= 1e-3 against the reference CPU path
+    (REL_L2_TOL); the fp32 kernels land near 1e-6, so the tests also assert
+    a tighter 2e-5 to catch regressions early;
+  * the device expf: bit-exact with the host's glibc expf on every float in
+    [-104, 0] and on a stride over all floats.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import hipmoe
+import oracle
+from common import (CONFIGS, REL_L2_TOL, SEED, bits, golden, layer, rel_l2,
+                    router_inputs, sha)
+
+pytestmark = pytest.mark.gpu
+TIGHT = 2e-5
+
+
+def say(msg):
+    print(f"[gpu-test] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def need_gpu():
+    n = hipmoe.hip().device_count()
+    assert n >= 1, "no HIP device visible: GPU tests need an MI355X"
+
+
+_layers = {}
+
+
+def gpu_layer(cfg):
+    if cfg not in _layers:
+        _layers.clear()
+        wt, E, EI, NE, K, renorm, bias_std = CONFIGS[cfg]
+        say(f"upload {cfg}")
+        _layers[cfg] = hipmoe.MoeLayer.from_synth(layer(cfg), K, bool(renorm))
+    return _layers[cfg]
+
+
+# --------------------------------------------------------------------------
+# expf
+# --------------------------------------------------------------------------
+
+def _expf_chunk(b0, n, step=1):
+    u = (np.arange(n, dtype=np.uint64) * step + b0).astype(np.uint32)
+    x = u.view(np.float32)
+    g = hipmoe.expf_dev(x)
+    if step == 1:
+        ref = oracle.expf_bits(b0, n)
+    else:
+        ref = oracle.expf(x)
+    same = (bits(g) == bits(ref)) | (np.isnan(g) & np.isnan(ref))
+    return int((~same).sum()), (int(u[~same][0]) if (~same).any() else None)
+
+
+def test_gpu_expf_softmax_range_exhaustive():
+    say("expf exhaustive over [-104, 0]")
+    lo = 0x80000000
+    hi = int(np.array([-104.0], np.float32).view(np.uint32)[0])
+    chunk = 1 << 25
+    b = lo
+    while b <= hi:
+        n = min(chunk, hi - b + 1)
+        bad, first = _expf_chunk(b, n)
+        assert bad == 0, f"{bad} mismatches from {first:#x}"
+        b += n
+    bad, _ = _expf_chunk(0, 1)
+    assert bad == 0
+
+
+def test_gpu_expf_all_floats_strided():
+    say("expf strided over all floats")
+    bad, first = _expf_chunk(0, (1 << 32) // 61 + 1, 61)
+    assert bad == 0, f"{bad} mismatches from {first:#x}"
+
+
+# --------------------------------------------------------------------------
+# routing
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("cfg", list(CONFIGS))
+def test_gpu_routing_bits_vs_reference(cfg):
+    say(f"routing {cfg}")
+    wt, E, EI, NE, K, renorm, bias_std = CONFIGS[cfg]
+    g = golden(f"route_{cfg}.npz")
+    T = int(g["T"])
+    wr, bias, x = router_inputs(cfg, T, int(g["input_call"]))
+    assert sha(wr) == str(g["sha_router"]) and sha(x) == str(g["sha_x"])
+    lay = gpu_layer(cfg)
+    assert np.array_equal(bits(lay.router), bits(wr))
+    lg, pr, ids, w = lay.route(x, bias)
+    keep = g["logits"].shape[0]
+    assert np.array_equal(bits(lg[:keep]), bits(g["logits"]))
+    assert np.array_equal(bits(pr[:keep]), bits(g["probs"]))
+    assert np.array_equal(ids, g["ids"])
+    assert np.array_equal(bits(w), bits(g["w"]))
+
+
+def _oracle_route(x, wr, bias, K, renorm):
+    lg = oracle.router(x, wr, bias)
+    ids = np.empty((x.shape[0], K), np.uint32)
+    w = np.empty((x.shape[0], K), np.float32)
+    for t in range(x.shape[0]):
+        i, ww = oracle.top_k(oracle.softmax(lg[t]), K)
+        if renorm:
+            s = np.float32(0)
+            for v in ww:
+                s = np.float32(s + v)
+            ww = (ww / s).astype(np.float32)
+        ids[t], w[t] = i, ww
+    return ids, w
+
+
+@pytest.mark.parametrize("case", ["equal_logits", "expert0_dominant", "expert0_second",
+                                  "huge_spread"])
+def test_gpu_routing_edge_cases(case):
+    say(f"routing edge case {case}")
+    lay = gpu_layer("olmoe_q8")
+    wt, E, EI, NE, K, renorm, bias_std = CONFIGS["olmoe_q8"]
+    x = hipmoe.synth_input(SEED, 9, 16, E)
+    bias = np.zeros(NE, np.float32)
+    if case == "equal_logits":
+        x = np.zeros_like(x)
+    elif case == "expert0_dominant":
+        bias[0] = 50.0
+    elif case == "expert0_second":
+        bias[0] = 30.0
+        bias[17] = 31.0
+    elif case == "huge_spread":
+        bias[:] = np.linspace(-200, 0, NE, dtype=np.float32)
+    lg, pr, ids, w = lay.route(x, bias)
+    oids, ow = _oracle_route(x, lay.router, bias, K, False)
+    assert np.array_equal(ids, oids)
+    assert np.array_equal(bits(w), bits(ow))
+    if case == "equal_logits":
+        assert (ids == 0).all()
+
+
+# --------------------------------------------------------------------------
+# one expert, one token (fused_ffn_silu)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("wtype,name", [(hipmoe.Q8_0, "q8_0"), (hipmoe.Q4_0, "q4_0")])
+def test_gpu_expert_ffn_vs_reference(wtype, name):
+    say(f"expert ffn {name}")
+    g = golden(f"ffn_{name}.npz")
+    E, EI = 2048, 1024
+    gm = hipmoe.synth_quant_matrix(SEED, 0x9001, 0.02, wtype, EI, E)
+    um = hipmoe.synth_quant_matrix(SEED, 0x9002, 0.02, wtype, EI, E)
+    dm = hipmoe.synth_quant_matrix(SEED, 0x9003, 0.02, wtype, E, EI)
+    x = hipmoe.synth_normal(SEED, 0x9004, E)
+    assert sha(gm) == str(g["sha_gate"]) and sha(dm) == str(g["sha_down"])
+    lay = hipmoe.MoeLayer(np.zeros((1, E), np.float32), gm.reshape(1, -1), um.reshape(1, -1),
+                          dm.reshape(1, -1), wtype, E, EI, 1, 1, False)
+    out = lay.expert_ffn(0, x)
+    lay.free()
+    err = rel_l2(out, g["out"])
+    say(f"expert ffn {name}: rel L2 {err:.3e}")
+    assert err <= REL_L2_TOL and err <= TIGHT
+
+
+# --------------------------------------------------------------------------
+# whole layers
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("cfg", list(CONFIGS))
+def test_gpu_moe_layer_vs_reference_golden(cfg):
+    say(f"moe layer golden {cfg}")
+    wt, E, EI, NE, K, renorm, bias_std = CONFIGS[cfg]
+    g = golden(f"moe_{cfg}.npz")
+    T = int(g["T"])
+    lay = gpu_layer(cfg)
+    x = hipmoe.synth_input(SEED, 0, T, E)
+    assert sha(x) == str(g["sha_x"])
+    out, ids, w = lay.ffn(x, layer(cfg)["bias"])
+    err = rel_l2(out, g["out"])
+    say(f"moe layer golden {cfg}: rel L2 {err:.3e}")
+    assert err <= REL_L2_TOL and err <= TIGHT
+
+
+def _check_layer_vs_oracle(cfg, T, call, per_token=True):
+    wt, E, EI, NE, K, renorm, bias_std = CONFIGS[cfg]
+    lay = gpu_layer(cfg)
+    lw = layer(cfg)
+    x = hipmoe.synth_input(SEED, call, T, E)
+    out, ids, w = lay.ffn(x, lw["bias"])
+    oout, oids, ow, _, _ = oracle.moe_ffn(x, lw, K, bool(renorm), lw["bias"])
+    assert np.array_equal(ids, oids)
+    assert np.array_equal(bits(w), bits(ow))
+    err = rel_l2(out, oout)
+    worst = max(rel_l2(out[t], oout[t]) for t in range(T)) if per_token else err
+    say(f"{cfg} T={T}: rel L2 {err:.3e}, worst token {worst:.3e}")
+    assert err <= REL_L2_TOL and worst <= REL_L2_TOL
+    assert err <= TIGHT
+    return out
+
+
+def test_gpu_olmoe_q8_decode_tokens():
+    say("olmoe_q8 decode T=1 x 24 calls")
+    for call in range(24):
+        _check_layer_vs_oracle("olmoe_q8", 1, 100 + call)
+
+
+def test_gpu_olmoe_q8_batch():
+    say("olmoe_q8 T=64")
+    _check_layer_vs_oracle("olmoe_q8", 64, 200)
+
+
+def test_gpu_olmoe_q4_skew_prefill_512():
+    say("olmoe_q4_skew prefill T=512")
+    _check_layer_vs_oracle("olmoe_q4_skew", 512, 300)
+
+
+def test_gpu_mixtral_q4_decode_and_64():
+    say("mixtral_q4 T=1")
+    _check_layer_vs_oracle("mixtral_q4", 1, 400)
+    say("mixtral_q4 T=64")
+    _check_layer_vs_oracle("mixtral_q4", 64, 401)
+
+
+# --------------------------------------------------------------------------
+# size-independent properties
+# --------------------------------------------------------------------------
+
+def test_gpu_deterministic_and_token_permutation():
+    say("determinism + token permutation (olmoe_q8, T=96)")
+    lay = gpu_layer("olmoe_q8")
+    x = hipmoe.synth_input(SEED, 500, 96, 2048)
+    a, ia, wa = lay.ffn(x)
+    b, ib, wb = lay.ffn(x)
+    assert np.array_equal(bits(a), bits(b)) and np.array_equal(ia, ib)
+    perm = np.random.default_rng(3).permutation(96)
+    c, ic, wc = lay.ffn(x[perm])
+    assert np.array_equal(ic, ia[perm]) and np.array_equal(bits(wc), bits(wa[perm]))
+    assert rel_l2(c, a[perm]) <= TIGHT
+
+
+def test_gpu_decode_equals_batched():
+    say("T=1 calls vs one T=16 call (olmoe_q8)")
+    lay = gpu_layer("olmoe_q8")
+    x = hipmoe.synth_input(SEED, 501, 16, 2048)
+    batched, ib, wb = lay.ffn(x)
+    for t in range(16):
+        o, i, w = lay.ffn(x[t:t + 1])
+        assert np.array_equal(i[0], ib[t]) and np.array_equal(bits(w[0]), bits(wb[t]))
+        assert rel_l2(o[0], batched[t]) <= TIGHT
+
+
+def test_gpu_dev_entry_matches_host_entry():
+    say("hip_moe_ffn_dev vs hip_moe_ffn (olmoe_q8, T=8)")
+    H = hipmoe.hip()
+    lay = gpu_layer("olmoe_q8")
+    x = hipmoe.synth_input(SEED, 502, 8, 2048)
+    ref, ids, w = lay.ffn(x)
+    d_x = H.upload(x)
+    d_o = H.malloc(x.nbytes)
+    d_i = H.malloc(8 * 8 * 4)
+    d_w = H.malloc(8 * 8 * 4)
+    try:
+        lay.ffn_dev(d_x, d_o, 8, None, d_i, d_w)
+        H.sync()
+        out = H.download(d_o, x.shape, np.float32)
+        assert np.array_equal(bits(out), bits(ref))
+        assert np.array_equal(H.download(d_i, (8, 8), np.uint32), ids)
+    finally:
+        for p in (d_x, d_o, d_i, d_w):
+            H.free(p)
