@@ -35,6 +35,7 @@ struct hip_moe_layer {
 	size_t weight_bytes;
 
 	hipStream_t stream;
+	int fused_grid;     /* workgroups of the persistent kernel, 0 = none */
 
 	/* scratch for up to cap_T tokens */
 	size_t cap_T;
@@ -43,6 +44,8 @@ struct hip_moe_layer {
 	float *d_w;
 	float *d_h;
 	float *d_ypart;
+	uint32_t *d_sync;   /* counters of the persistent kernel, zero between launches */
+	size_t sync_words;
 
 	/* staging for the host-pointer entry point */
 	size_t cap_io;
@@ -106,6 +109,7 @@ void hip_moe_free(hip_moe_layer *L)
 	hipFree(L->d_w);
 	hipFree(L->d_h);
 	hipFree(L->d_ypart);
+	hipFree(L->d_sync);
 	hipFree(L->d_x);
 	hipFree(L->d_out);
 	hipFree(L->d_bias);
@@ -168,6 +172,7 @@ hip_moe_layer *hip_moe_upload(const float *gate_inp, const void *const *gate_e,
 	L->down_stride = E * L->rb_mid;
 	L->kchunks = moe_kchunks(EI);
 	L->weight_bytes = NE * E * sizeof(float) + NE * (2 * L->gu_stride + L->down_stride);
+	L->fused_grid = moe_fused_grid(wtype, E, EI);
 
 	HIPCHK(hipGetDevice(&L->device), "hipGetDevice");
 	HIPCHK(hipStreamCreateWithFlags(&L->stream, hipStreamNonBlocking), "hipStreamCreate");
@@ -213,11 +218,13 @@ static int ensure_scratch(hip_moe_layer *L, size_t T)
 	hipFree(L->d_w);
 	hipFree(L->d_h);
 	hipFree(L->d_ypart);
+	hipFree(L->d_sync);
 	L->d_logits = NULL;
 	L->d_ids = NULL;
 	L->d_w = NULL;
 	L->d_h = NULL;
 	L->d_ypart = NULL;
+	L->d_sync = NULL;
 	L->cap_T = 0;
 	HIPCHK(hipMalloc((void **)&L->d_logits, T * L->NE * sizeof(float)), "hipMalloc(logits)");
 	HIPCHK(hipMalloc((void **)&L->d_ids, P * sizeof(uint32_t)), "hipMalloc(ids)");
@@ -225,6 +232,10 @@ static int ensure_scratch(hip_moe_layer *L, size_t T)
 	HIPCHK(hipMalloc((void **)&L->d_h, P * L->EI * sizeof(float)), "hipMalloc(h)");
 	HIPCHK(hipMalloc((void **)&L->d_ypart, P * L->kchunks * L->E * sizeof(float)),
 	       "hipMalloc(ypart)");
+	L->sync_words = moe_fused_sync_words(T, L->topk, L->E);
+	HIPCHK(hipMalloc((void **)&L->d_sync, L->sync_words * sizeof(uint32_t)), "hipMalloc(sync)");
+	/* zeroed once here; each persistent launch leaves the counters at zero */
+	HIPCHK(hipMemset(L->d_sync, 0, L->sync_words * sizeof(uint32_t)), "hipMemset(sync)");
 	L->cap_T = T;
 	return 1;
 fail:
@@ -285,6 +296,14 @@ int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 	float *w = d_w_out ? d_w_out : L->d_w;
 	int P = (int)(T * L->topk);
 
+	if (L->fused_grid > 0 && moe_fused_supported(L->wtype, L->E, L->EI, T, L->topk)) {
+		LCHK(moe_launch_fused(L->wtype, d_x, L->d_router, d_router_bias, L->d_gate,
+				      L->d_up, L->d_down, L->gu_stride, L->down_stride,
+				      L->d_logits, ids, w, L->d_h, L->d_ypart, d_out, L->d_sync,
+				      (int)T, (int)L->E, (int)L->EI, (int)L->NE, (int)L->topk,
+				      L->renorm, L->fused_grid, s), "fused layer");
+		return 1;
+	}
 	if (!route(L, d_x, T, d_router_bias, L->d_logits, NULL, ids, w, s))
 		return 0;
 	LCHK(moe_launch_gateup(L->wtype, L->d_gate, L->d_up, L->gu_stride, ids, -1, d_x,
@@ -372,6 +391,16 @@ int hip_moe_ffn(hip_moe_layer *L, const float *x, float *out, size_t T,
 		HIPCHK(hipMemcpyAsync(w_out, L->d_w_io, T * L->topk * sizeof(float),
 				      hipMemcpyDeviceToHost, s), "copy w");
 	HIPCHK(hipStreamSynchronize(s), "synchronize");
+	if (L->d_sync) { /* a bounded wait inside the persistent kernel ran out */
+		uint32_t err = 0;
+		HIPCHK(hipMemcpy(&err, L->d_sync + MOE_SYNC_ERR_WORD, sizeof(err),
+				 hipMemcpyDeviceToHost), "read error word");
+		if (err) { /* counters may be left mid-flight: zero them all */
+			hipMemset(L->d_sync, 0, L->sync_words * sizeof(uint32_t));
+			set_err("persistent kernel: a dependency wait timed out");
+			return 0;
+		}
+	}
 	return 1;
 fail:
 	return 0;

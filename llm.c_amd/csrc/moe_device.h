@@ -1,0 +1,306 @@
+/*
+ * Device helpers shared by the MoE kernels (gfx950, wave64).
+ *
+ * Weights stay in GGUF block layout (Q8_0: 34-byte blocks, Q4_0: 18-byte
+ * blocks, quant.h:14-26).  A lane owns a "segment" of two consecutive blocks
+ * (64 columns: 68 bytes Q8_0 / 36 bytes Q4_0, always 4-byte aligned because
+ * rows hold an even number of blocks) and keeps the matching 64 activations in
+ * registers for all the rows it visits; C lanes cover one row (or one K-chunk
+ * of a row), 64/C rows are in flight per wave step, and a row's partial sums
+ * meet in an xor-shuffle tree.
+ *
+ * Compiled with -ffp-contract=off: every fused multiply-add is written.
+ */
+#ifndef MOE_DEVICE_H
+#define MOE_DEVICE_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "moe_expf.h"
+#include "moe_internal.h"
+
+typedef uint32_t u32;
+
+#define WAVE 64
+
+/* LDS ordering between lanes of one wave (no workgroup barrier). */
+#define WAVE_SYNC()                                              \
+	do {                                                     \
+		__builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront"); \
+		__builtin_amdgcn_wave_barrier();                 \
+		__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront"); \
+	} while (0)
+
+__device__ static inline float f16_bits_to_f32(u32 h)
+{
+	return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xffffu));
+}
+
+/* 16 bytes read from a 4-byte aligned address (one global_load_dwordx4). */
+struct __attribute__((packed, aligned(4))) dw4 {
+	u32 v[4];
+};
+
+template <int N>
+__device__ static inline void load_dwords(const uint8_t *p, u32 (&d)[N])
+{
+	const dw4 *q = (const dw4 *)p;
+#pragma unroll
+	for (int i = 0; i < N / 4; i++) {
+		dw4 t = q[i];
+		d[4 * i + 0] = t.v[0];
+		d[4 * i + 1] = t.v[1];
+		d[4 * i + 2] = t.v[2];
+		d[4 * i + 3] = t.v[3];
+	}
+#pragma unroll
+	for (int i = (N / 4) * 4; i < N; i++)
+		d[i] = ((const u32 *)p)[i];
+}
+
+/* Q8_0 segment: 17 dwords.  Block 0 = bytes 0..33 (scale in bytes 0-1,
+ * quants 2..33, i.e. misaligned by 2), block 1 = bytes 34..67 (scale 34-35,
+ * quants 36..67 = dwords 9..16). */
+__device__ static inline float seg_dot_q8_0(const u32 (&d)[17], const float (&x)[64])
+{
+	float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+	for (int k = 0; k < 8; k++) {
+		u32 q = __builtin_amdgcn_alignbit(d[k + 1], d[k], 16);
+#pragma unroll
+		for (int b = 0; b < 4; b++)
+			s0 = __builtin_fmaf((float)(int)(int8_t)(q >> (8 * b)), x[4 * k + b], s0);
+	}
+#pragma unroll
+	for (int k = 0; k < 8; k++) {
+		u32 q = d[9 + k];
+#pragma unroll
+		for (int b = 0; b < 4; b++)
+			s1 = __builtin_fmaf((float)(int)(int8_t)(q >> (8 * b)), x[32 + 4 * k + b], s1);
+	}
+	float d0 = f16_bits_to_f32(d[0]);
+	float d1 = f16_bits_to_f32(d[8] >> 16);
+	return __builtin_fmaf(d1, s1, d0 * s0);
+}
+
+/* Q4_0 segment: 9 dwords.  Block 0 = bytes 0..17 (scale 0-1, packed nibbles
+ * 2..17), block 1 = bytes 18..35 (scale 18-19, nibbles 20..35 = dwords 5..8).
+ * Byte j of a block holds element j (low nibble) and j+16 (high nibble),
+ * each biased by 8 (quant.c:126-155). */
+__device__ static inline float seg_dot_q4_0(const u32 (&d)[9], const float (&x)[64])
+{
+	float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+	for (int k = 0; k < 4; k++) {
+		u32 q = __builtin_amdgcn_alignbit(d[k + 1], d[k], 16);
+#pragma unroll
+		for (int b = 0; b < 4; b++) {
+			int lo = (int)((q >> (8 * b)) & 15u) - 8;
+			int hi = (int)((q >> (8 * b + 4)) & 15u) - 8;
+			s0 = __builtin_fmaf((float)lo, x[4 * k + b], s0);
+			s0 = __builtin_fmaf((float)hi, x[16 + 4 * k + b], s0);
+		}
+	}
+#pragma unroll
+	for (int k = 0; k < 4; k++) {
+		u32 q = d[5 + k];
+#pragma unroll
+		for (int b = 0; b < 4; b++) {
+			int lo = (int)((q >> (8 * b)) & 15u) - 8;
+			int hi = (int)((q >> (8 * b + 4)) & 15u) - 8;
+			s1 = __builtin_fmaf((float)lo, x[32 + 4 * k + b], s1);
+			s1 = __builtin_fmaf((float)hi, x[48 + 4 * k + b], s1);
+		}
+	}
+	float d0 = f16_bits_to_f32(d[0]);
+	float d1 = f16_bits_to_f32(d[4] >> 16);
+	return __builtin_fmaf(d1, s1, d0 * s0);
+}
+
+template <int WT> struct qseg;
+template <> struct qseg<1> {
+	static constexpr int BYTES = 68;
+	static constexpr int DW = 17;
+	__device__ static inline float dot(const uint8_t *p, const float (&x)[64])
+	{
+		u32 d[17];
+		load_dwords<17>(p, d);
+		return seg_dot_q8_0(d, x);
+	}
+};
+template <> struct qseg<2> {
+	static constexpr int BYTES = 36;
+	static constexpr int DW = 9;
+	__device__ static inline float dot(const uint8_t *p, const float (&x)[64])
+	{
+		u32 d[9];
+		load_dwords<9>(p, d);
+		return seg_dot_q4_0(d, x);
+	}
+};
+
+/* sum over the C consecutive lanes of a row group (C a power of two) */
+template <int C>
+__device__ static inline float group_sum(float v)
+{
+#pragma unroll
+	for (int off = C / 2; off >= 1; off >>= 1)
+		v += __shfl_xor(v, off, WAVE);
+	return v;
+}
+
+__device__ static inline void load_x64(const float *src, float (&x)[64])
+{
+	const float4 *s4 = (const float4 *)src;
+#pragma unroll
+	for (int i = 0; i < 16; i++) {
+		float4 v = s4[i];
+		x[4 * i + 0] = v.x;
+		x[4 * i + 1] = v.y;
+		x[4 * i + 2] = v.z;
+		x[4 * i + 3] = v.w;
+	}
+}
+
+/* Activations staged in LDS with 4 floats of padding after every 64-float
+ * segment, so the C lanes of a row group reading their segments with 16-byte
+ * LDS reads hit distinct banks. */
+#define SEG_STRIDE 68
+
+__device__ static inline void lds_x64(const float *s, int seg, float (&x)[64])
+{
+	const float4 *s4 = (const float4 *)(s + seg * SEG_STRIDE);
+#pragma unroll
+	for (int i = 0; i < 16; i++) {
+		float4 v = s4[i];
+		x[4 * i + 0] = v.x;
+		x[4 * i + 1] = v.y;
+		x[4 * i + 2] = v.z;
+		x[4 * i + 3] = v.w;
+	}
+}
+
+/* Copy n floats (n a multiple of 64) from global into the padded LDS
+ * layout, all threads of a block of nthreads cooperating. */
+__device__ static inline void stage_padded(float *s, const float *g, int n, int tid,
+					   int nthreads)
+{
+	const float4 *g4 = (const float4 *)g;
+	for (int i = tid; i < n / 4; i += nthreads) {
+		float4 v = g4[i];
+		*(float4 *)(s + (i >> 4) * SEG_STRIDE + (i & 15) * 4) = v;
+	}
+}
+
+/*
+ * softmax_1d + top_k (+ Mixtral renormalisation) for one token, one wave.
+ *
+ * softmax_1d (nn.c:221-262): e_i = expf(v_i - max); lane sums s_l over the
+ * 8-wide chunks in order, the reduction tree ((s0+s4)+(s2+s6))+((s1+s5)+
+ * (s3+s7)), then the scalar tail; p_i = e_i / sum (IEEE division).
+ *
+ * top_k (nn.c:276-308) seeds all k slots with element 0 and inserts later
+ * elements only when strictly greater than the current minimum.  Its result
+ * in closed form: rank_i = #{j : p_j > p_i or (p_j == p_i and j < i)};
+ * r0 = rank of element 0.  Element i != 0 lands in slot k-1-rank_i iff
+ * rank_i < min(r0, k); when r0 < k, slots 0..k-1-r0 hold copies of element 0.
+ * Slots ascend by weight, later indices below earlier ones among ties.
+ *
+ * renorm (llama.c:422-427): w_e /= (sequential sum of the k weights).
+ * sp holds NE floats and sid/sw K entries of this wave's LDS.
+ */
+__device__ static inline void wave_softmax_topk(const float *logits, float *probs, u32 *ids,
+						float *wout, int NE, int K, int renorm,
+						float *sp, u32 *sid, float *sw, int lane)
+{
+	float mx = -__builtin_inff();
+	for (int i = lane; i < NE; i += WAVE)
+		mx = fmaxf(mx, logits[i]);
+#pragma unroll
+	for (int off = 32; off >= 1; off >>= 1)
+		mx = fmaxf(mx, __shfl_xor(mx, off, WAVE));
+
+	for (int i = lane; i < NE; i += WAVE)
+		sp[i] = moe_expf(logits[i] - mx);
+	WAVE_SYNC();
+
+	const int nv = NE - NE % 8;
+	float s = 0.0f;
+	if (lane < 8)
+		for (int c = 0; c < nv; c += 8)
+			s = s + sp[c + lane];
+	s = s + __shfl_xor(s, 4, 8);
+	s = s + __shfl_xor(s, 2, 8);
+	s = s + __shfl_xor(s, 1, 8);
+	for (int i = nv; i < NE; i++)
+		s += sp[i];
+	const float sum = __shfl(s, 0, WAVE);
+
+	float pv[MOE_MAX_NE / WAVE];
+#pragma unroll
+	for (int r = 0; r < MOE_MAX_NE / WAVE; r++) {
+		int i = lane + r * WAVE;
+		pv[r] = 0.0f;
+		if (i < NE) {
+			pv[r] = sp[i] / sum;
+			if (probs)
+				probs[i] = pv[r];
+		}
+	}
+	WAVE_SYNC();
+#pragma unroll
+	for (int r = 0; r < MOE_MAX_NE / WAVE; r++) {
+		int i = lane + r * WAVE;
+		if (i < NE)
+			sp[i] = pv[r];
+	}
+	WAVE_SYNC();
+
+	int rank[MOE_MAX_NE / WAVE];
+#pragma unroll
+	for (int r = 0; r < MOE_MAX_NE / WAVE; r++) {
+		int i = lane + r * WAVE;
+		int rk = 0;
+		if (i < NE) {
+			float pi = pv[r];
+			for (int j = 0; j < NE; j++) {
+				float pj = sp[j];
+				rk += (pj > pi) || (pj == pi && j < i);
+			}
+		}
+		rank[r] = rk;
+	}
+	const int r0 = __shfl(rank[0], 0, WAVE);
+	const int lim = r0 < K ? r0 : K;
+#pragma unroll
+	for (int r = 0; r < MOE_MAX_NE / WAVE; r++) {
+		int i = lane + r * WAVE;
+		if (i > 0 && i < NE && rank[r] < lim) {
+			sid[K - 1 - rank[r]] = (u32)i;
+			sw[K - 1 - rank[r]] = pv[r];
+		}
+	}
+	if (r0 < K) {
+		float p0 = sp[0];
+		for (int slot = lane; slot < K - r0; slot += WAVE) {
+			sid[slot] = 0;
+			sw[slot] = p0;
+		}
+	}
+	WAVE_SYNC();
+	if (lane == 0 && renorm) {
+		float ws = 0.0f;
+		for (int e = 0; e < K; e++)
+			ws += sw[e];
+		for (int e = 0; e < K; e++)
+			sw[e] /= ws;
+	}
+	WAVE_SYNC();
+	for (int e = lane; e < K; e += WAVE) {
+		ids[e] = sid[e];
+		wout[e] = sw[e];
+	}
+}
+
+#endif

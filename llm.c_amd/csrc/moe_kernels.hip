@@ -18,150 +18,7 @@
  * tree.  The file is compiled with -ffp-contract=off: every fused
  * multiply-add is written as one.
  */
-#include <hip/hip_runtime.h>
-#include <stdint.h>
-
-#include "moe_expf.h"
-#include "moe_internal.h"
-
-typedef uint32_t u32;
-
-#define WAVE 64
-
-/* ------------------------------------------------------------------ */
-/* helpers                                                            */
-/* ------------------------------------------------------------------ */
-
-__device__ static inline float f16_bits_to_f32(u32 h)
-{
-	return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xffffu));
-}
-
-/* 16 bytes read from a 4-byte aligned address (one global_load_dwordx4). */
-struct __attribute__((packed, aligned(4))) dw4 {
-	u32 v[4];
-};
-
-template <int N>
-__device__ static inline void load_dwords(const uint8_t *p, u32 (&d)[N])
-{
-	const dw4 *q = (const dw4 *)p;
-#pragma unroll
-	for (int i = 0; i < N / 4; i++) {
-		dw4 t = q[i];
-		d[4 * i + 0] = t.v[0];
-		d[4 * i + 1] = t.v[1];
-		d[4 * i + 2] = t.v[2];
-		d[4 * i + 3] = t.v[3];
-	}
-#pragma unroll
-	for (int i = (N / 4) * 4; i < N; i++)
-		d[i] = ((const u32 *)p)[i];
-}
-
-/* Q8_0 segment: 17 dwords.  Block 0 = bytes 0..33 (scale in bytes 0-1,
- * quants 2..33, i.e. misaligned by 2), block 1 = bytes 34..67 (scale 34-35,
- * quants 36..67 = dwords 9..16). */
-__device__ static inline float seg_dot_q8_0(const u32 (&d)[17], const float (&x)[64])
-{
-	float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-	for (int k = 0; k < 8; k++) {
-		u32 q = __builtin_amdgcn_alignbit(d[k + 1], d[k], 16);
-#pragma unroll
-		for (int b = 0; b < 4; b++)
-			s0 = __builtin_fmaf((float)(int)(int8_t)(q >> (8 * b)), x[4 * k + b], s0);
-	}
-#pragma unroll
-	for (int k = 0; k < 8; k++) {
-		u32 q = d[9 + k];
-#pragma unroll
-		for (int b = 0; b < 4; b++)
-			s1 = __builtin_fmaf((float)(int)(int8_t)(q >> (8 * b)), x[32 + 4 * k + b], s1);
-	}
-	float d0 = f16_bits_to_f32(d[0]);
-	float d1 = f16_bits_to_f32(d[8] >> 16);
-	return __builtin_fmaf(d1, s1, d0 * s0);
-}
-
-/* Q4_0 segment: 9 dwords.  Block 0 = bytes 0..17 (scale 0-1, packed nibbles
- * 2..17), block 1 = bytes 18..35 (scale 18-19, nibbles 20..35 = dwords 5..8).
- * Byte j of a block holds element j (low nibble) and j+16 (high nibble),
- * each biased by 8 (quant.c:126-155). */
-__device__ static inline float seg_dot_q4_0(const u32 (&d)[9], const float (&x)[64])
-{
-	float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-	for (int k = 0; k < 4; k++) {
-		u32 q = __builtin_amdgcn_alignbit(d[k + 1], d[k], 16);
-#pragma unroll
-		for (int b = 0; b < 4; b++) {
-			int lo = (int)((q >> (8 * b)) & 15u) - 8;
-			int hi = (int)((q >> (8 * b + 4)) & 15u) - 8;
-			s0 = __builtin_fmaf((float)lo, x[4 * k + b], s0);
-			s0 = __builtin_fmaf((float)hi, x[16 + 4 * k + b], s0);
-		}
-	}
-#pragma unroll
-	for (int k = 0; k < 4; k++) {
-		u32 q = d[5 + k];
-#pragma unroll
-		for (int b = 0; b < 4; b++) {
-			int lo = (int)((q >> (8 * b)) & 15u) - 8;
-			int hi = (int)((q >> (8 * b + 4)) & 15u) - 8;
-			s1 = __builtin_fmaf((float)lo, x[32 + 4 * k + b], s1);
-			s1 = __builtin_fmaf((float)hi, x[48 + 4 * k + b], s1);
-		}
-	}
-	float d0 = f16_bits_to_f32(d[0]);
-	float d1 = f16_bits_to_f32(d[4] >> 16);
-	return __builtin_fmaf(d1, s1, d0 * s0);
-}
-
-template <int WT> struct qseg;
-template <> struct qseg<1> {
-	static constexpr int BYTES = 68;
-	static constexpr int DW = 17;
-	__device__ static inline float dot(const uint8_t *p, const float (&x)[64])
-	{
-		u32 d[17];
-		load_dwords<17>(p, d);
-		return seg_dot_q8_0(d, x);
-	}
-};
-template <> struct qseg<2> {
-	static constexpr int BYTES = 36;
-	static constexpr int DW = 9;
-	__device__ static inline float dot(const uint8_t *p, const float (&x)[64])
-	{
-		u32 d[9];
-		load_dwords<9>(p, d);
-		return seg_dot_q4_0(d, x);
-	}
-};
-
-/* sum over the C consecutive lanes of a row group (C a power of two) */
-template <int C>
-__device__ static inline float group_sum(float v)
-{
-#pragma unroll
-	for (int off = C / 2; off >= 1; off >>= 1)
-		v += __shfl_xor(v, off, WAVE);
-	return v;
-}
-
-__device__ static inline void load_x64(const float *src, float (&x)[64])
-{
-	const float4 *s4 = (const float4 *)src;
-#pragma unroll
-	for (int i = 0; i < 16; i++) {
-		float4 v = s4[i];
-		x[4 * i + 0] = v.x;
-		x[4 * i + 1] = v.y;
-		x[4 * i + 2] = v.z;
-		x[4 * i + 3] = v.w;
-	}
-}
+#include "moe_device.h"
 
 /* ------------------------------------------------------------------ */
 /* router: logits[t][j] = (bias[j] or 0) + dot(x[t], wr[j])            */
@@ -193,20 +50,9 @@ __global__ __launch_bounds__(64) void k_router(const float *__restrict__ x,
 }
 
 /* ------------------------------------------------------------------ */
-/* softmax + top-k, one wave per token                                 */
+/* softmax + top-k, one wave per token (wave_softmax_topk)             */
 /* ------------------------------------------------------------------ */
 
-/*
- * softmax_1d (nn.c:221-262): e_i = expf(v_i - max); lane sums s_l over the
- * 8-wide chunks in order, the reduction tree, then the scalar tail; p = e/sum.
- *
- * top_k (nn.c:276-308) seeds all k slots with element 0 and inserts later
- * elements only when strictly greater than the current minimum.  Its result
- * in closed form: rank_i = #{j : p_j > p_i or (p_j == p_i and j < i)};
- * r0 = rank of element 0.  Element i != 0 lands in slot k-1-rank_i iff
- * rank_i < min(r0, k); when r0 < k, slots 0..k-1-r0 hold copies of element 0.
- * Slots ascend by weight, later indices below earlier ones among ties.
- */
 __global__ __launch_bounds__(64) void k_softmax_topk(const float *__restrict__ logits,
 						     float *__restrict__ probs,
 						     u32 *__restrict__ ids,
@@ -216,92 +62,10 @@ __global__ __launch_bounds__(64) void k_softmax_topk(const float *__restrict__ l
 	__shared__ float sp[MOE_MAX_NE];
 	__shared__ u32 sid[MOE_MAX_TOPK];
 	__shared__ float sw[MOE_MAX_TOPK];
-	__shared__ int srank0;
-	__shared__ float ssum;
-
-	const int t = blockIdx.x, lane = threadIdx.x;
-	const float *row = logits + (size_t)t * NE;
-
-	float mx = -__builtin_inff();
-	for (int i = lane; i < NE; i += WAVE)
-		mx = fmaxf(mx, row[i]);
-#pragma unroll
-	for (int off = 32; off >= 1; off >>= 1)
-		mx = fmaxf(mx, __shfl_xor(mx, off, WAVE));
-
-	for (int i = lane; i < NE; i += WAVE)
-		sp[i] = moe_expf(row[i] - mx);
-	__syncthreads();
-
-	const int nv = NE - NE % 8;
-	float s = 0.0f;
-	if (lane < 8)
-		for (int c = 0; c < nv; c += 8)
-			s = s + sp[c + lane];
-	s = s + __shfl_xor(s, 4, 8);
-	s = s + __shfl_xor(s, 2, 8);
-	s = s + __shfl_xor(s, 1, 8);
-	if (lane == 0) {
-		for (int i = nv; i < NE; i++)
-			s += sp[i];
-		ssum = s;
-	}
-	__syncthreads();
-	const float sum = ssum;
-	for (int i = lane; i < NE; i += WAVE) {
-		float p = sp[i] / sum;
-		sp[i] = p;
-		if (probs)
-			probs[(size_t)t * NE + i] = p;
-	}
-	__syncthreads();
-
-	int myrank[MOE_MAX_NE / WAVE];
-#pragma unroll
-	for (int r = 0; r < MOE_MAX_NE / WAVE; r++) {
-		int i = lane + r * WAVE;
-		int rank = 0;
-		if (i < NE) {
-			float pi = sp[i];
-			for (int j = 0; j < NE; j++) {
-				float pj = sp[j];
-				rank += (pj > pi) || (pj == pi && j < i);
-			}
-			if (i == 0)
-				srank0 = rank;
-		}
-		myrank[r] = rank;
-	}
-	__syncthreads();
-	const int r0 = srank0;
-	const int lim = r0 < K ? r0 : K;
-#pragma unroll
-	for (int r = 0; r < MOE_MAX_NE / WAVE; r++) {
-		int i = lane + r * WAVE;
-		if (i > 0 && i < NE && myrank[r] < lim) {
-			sid[K - 1 - myrank[r]] = (u32)i;
-			sw[K - 1 - myrank[r]] = sp[i];
-		}
-	}
-	if (r0 < K)
-		for (int slot = lane; slot < K - r0; slot += WAVE) {
-			sid[slot] = 0;
-			sw[slot] = sp[0];
-		}
-	__syncthreads();
-	if (lane == 0) {
-		if (renorm) {
-			float ws = 0.0f;
-			for (int e = 0; e < K; e++)
-				ws += sw[e];
-			for (int e = 0; e < K; e++)
-				sw[e] /= ws;
-		}
-		for (int e = 0; e < K; e++) {
-			ids[(size_t)t * K + e] = sid[e];
-			wout[(size_t)t * K + e] = sw[e];
-		}
-	}
+	const int t = blockIdx.x;
+	wave_softmax_topk(logits + (size_t)t * NE, probs ? probs + (size_t)t * NE : NULL,
+			  ids + (size_t)t * K, wout + (size_t)t * K, NE, K, renorm, sp, sid, sw,
+			  threadIdx.x);
 }
 
 /* ------------------------------------------------------------------ */

@@ -275,3 +275,59 @@ def test_gpu_dev_entry_matches_host_entry():
     finally:
         for p in (d_x, d_o, d_i, d_w):
             H.free(p)
+
+
+# --------------------------------------------------------------------------
+# the persistent decode kernel (T*K <= 64): boundary, reuse, graph replays
+# --------------------------------------------------------------------------
+
+def test_gpu_fused_boundary_T8():
+    say("olmoe_q8 T=8 (T*K = 64, largest persistent launch)")
+    _check_layer_vs_oracle("olmoe_q8", 8, 600)
+
+
+def test_gpu_fused_many_calls_reset_counters():
+    say("olmoe_q8: 64 consecutive T=1 calls, each checked")
+    lay = gpu_layer("olmoe_q8")
+    lw = layer("olmoe_q8")
+    xs = hipmoe.synth_input(SEED, 601, 64, 2048)
+    oout, oids, ow, _, _ = oracle.moe_ffn(xs, lw, 8, False, None)
+    for t in range(64):
+        out, ids, w = lay.ffn(xs[t:t + 1])
+        assert np.array_equal(ids[0], oids[t]) and np.array_equal(bits(w[0]), bits(ow[t]))
+        assert rel_l2(out[0], oout[t]) <= TIGHT
+
+
+def test_gpu_graph_replays_match_eager():
+    say("HIP graph of 4 decode calls, replayed 5 times")
+    H = hipmoe.hip()
+    lay = gpu_layer("olmoe_q8")
+    xs = hipmoe.synth_input(SEED, 602, 4, 2048)
+    eager = np.stack([lay.ffn(xs[i:i + 1])[0][0] for i in range(4)])
+    s = H.stream()
+    d_x = H.upload(xs)
+    d_o = H.malloc(4 * 2048 * 4)
+    try:
+        for i in range(4):  # eager warm-up on the capture stream
+            lay.ffn_dev(d_x + i * 8192, d_o + i * 8192, 1, None, None, None, s)
+        H.stream_sync(s)
+        H.begin_capture(s)
+        for i in range(4):
+            lay.ffn_dev(d_x + i * 8192, d_o + i * 8192, 1, None, None, None, s)
+        ge = H.end_capture(s)
+        for rep in range(5):
+            H.check(H.h.hipMemsetAsync(d_o, 0, 4 * 2048 * 4, s), "memset")
+            H.graph_launch(ge, s)
+            H.stream_sync(s)
+            got = H.download(d_o, (4, 2048), np.float32)
+            assert np.array_equal(bits(got), bits(eager)), f"replay {rep}"
+            lay.ffn(xs[:1])  # eager work between replays
+    finally:
+        H.free(d_x)
+        H.free(d_o)
+
+
+def test_gpu_mixtral_fused_T2_and_T32():
+    say("mixtral_q4 T=2 and T=32 (persistent path)")
+    _check_layer_vs_oracle("mixtral_q4", 2, 603)
+    _check_layer_vs_oracle("mixtral_q4", 32, 604)
