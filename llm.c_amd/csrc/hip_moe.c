@@ -44,7 +44,7 @@ struct hip_moe_layer {
 	float *d_w;
 	float *d_h;
 	float *d_ypart;
-	uint32_t *d_sync;   /* counters of the persistent kernel, zero between launches */
+	uint32_t *d_sync;   /* epoch and flags of the decode kernel */
 	size_t sync_words;
 
 	/* staging for the host-pointer entry point */
@@ -171,8 +171,10 @@ hip_moe_layer *hip_moe_upload(const float *gate_inp, const void *const *gate_e,
 	L->gu_stride = EI * L->rb_in;
 	L->down_stride = E * L->rb_mid;
 	L->kchunks = moe_kchunks(EI);
+	if (moe_fused_kchunks(wtype, EI) > L->kchunks) /* ypart holds either path's chunks */
+		L->kchunks = moe_fused_kchunks(wtype, EI);
 	L->weight_bytes = NE * E * sizeof(float) + NE * (2 * L->gu_stride + L->down_stride);
-	L->fused_grid = moe_fused_grid(wtype, E, EI);
+	L->fused_grid = moe_fused_grid(wtype, E, EI, NE);
 
 	HIPCHK(hipGetDevice(&L->device), "hipGetDevice");
 	HIPCHK(hipStreamCreateWithFlags(&L->stream, hipStreamNonBlocking), "hipStreamCreate");
@@ -232,9 +234,10 @@ static int ensure_scratch(hip_moe_layer *L, size_t T)
 	HIPCHK(hipMalloc((void **)&L->d_h, P * L->EI * sizeof(float)), "hipMalloc(h)");
 	HIPCHK(hipMalloc((void **)&L->d_ypart, P * L->kchunks * L->E * sizeof(float)),
 	       "hipMalloc(ypart)");
-	L->sync_words = moe_fused_sync_words(T, L->topk, L->E);
+	L->sync_words = moe_fused_sync_words(L->wtype, T, L->topk, L->E, L->EI, L->NE,
+					     L->fused_grid > 0 ? L->fused_grid : 1);
 	HIPCHK(hipMalloc((void **)&L->d_sync, L->sync_words * sizeof(uint32_t)), "hipMalloc(sync)");
-	/* zeroed once here; each persistent launch leaves the counters at zero */
+	/* zeroed once here; the decode kernel's flags carry an epoch */
 	HIPCHK(hipMemset(L->d_sync, 0, L->sync_words * sizeof(uint32_t)), "hipMemset(sync)");
 	L->cap_T = T;
 	return 1;
@@ -296,10 +299,10 @@ int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 	float *w = d_w_out ? d_w_out : L->d_w;
 	int P = (int)(T * L->topk);
 
-	if (L->fused_grid > 0 && moe_fused_supported(L->wtype, L->E, L->EI, T, L->topk)) {
+	if (L->fused_grid > 0 && moe_fused_supported(L->wtype, L->E, L->EI, L->NE, T, L->topk)) {
 		LCHK(moe_launch_fused(L->wtype, d_x, L->d_router, d_router_bias, L->d_gate,
 				      L->d_up, L->d_down, L->gu_stride, L->down_stride,
-				      L->d_logits, ids, w, L->d_h, L->d_ypart, d_out, L->d_sync,
+				      ids, w, L->d_h, L->d_ypart, d_out, L->d_sync,
 				      (int)T, (int)L->E, (int)L->EI, (int)L->NE, (int)L->topk,
 				      L->renorm, L->fused_grid, s), "fused layer");
 		return 1;
@@ -391,11 +394,11 @@ int hip_moe_ffn(hip_moe_layer *L, const float *x, float *out, size_t T,
 		HIPCHK(hipMemcpyAsync(w_out, L->d_w_io, T * L->topk * sizeof(float),
 				      hipMemcpyDeviceToHost, s), "copy w");
 	HIPCHK(hipStreamSynchronize(s), "synchronize");
-	if (L->d_sync) { /* a bounded wait inside the persistent kernel ran out */
+	if (L->d_sync) { /* a bounded wait inside the decode kernel ran out */
 		uint32_t err = 0;
 		HIPCHK(hipMemcpy(&err, L->d_sync + MOE_SYNC_ERR_WORD, sizeof(err),
 				 hipMemcpyDeviceToHost), "read error word");
-		if (err) { /* counters may be left mid-flight: zero them all */
+		if (err) { /* flags may be left mid-flight: restart the epoch at zero */
 			hipMemset(L->d_sync, 0, L->sync_words * sizeof(uint32_t));
 			set_err("persistent kernel: a dependency wait timed out");
 			return 0;

@@ -1,0 +1,750 @@
+/*
+ * Decode-sized MoE FFN layer (T*K <= 64) in one launch: k_moe_decode.
+ *
+ * Every workgroup (G of them, four per CU) runs:
+ *
+ *  1. routing.  Workgroup j < NE computes router logit j for every token
+ *     with the 8-lane FMA chains of dot_f32_f32 (matmul.c:91-105), fed from
+ *     LDS-transposed copies of router row j and the token, and writes it into
+ *     NREP replicas of the logit table, each entry tagged with this launch's
+ *     epoch.  Every workgroup then polls its own replica until all NE*T
+ *     entries carry the epoch and runs softmax + top-k (+ renorm) itself
+ *     (nn.c:221-308, llama.c:422-427): no second hop, no hot line.
+ *  2. expert items, statically assigned: item i runs on workgroup i % G, in
+ *     increasing i.  Items are gate/up tiles (16 rows of gate and up of the
+ *     expert in slot p: h[p][row] = silu(gate.x) * (up.x), nn.c:460-478), then
+ *     down tiles (32 rows of down over one K-chunk of h[p], nn.c:490-492).
+ *     A down tile issues its weight loads, then waits for the gate/up tiles
+ *     covering its K-chunk.  The workgroup holding the last down tile of a
+ *     (token, row block) waits for the others and combines the slots in
+ *     order: out += y / (1/w)  (olmoe.c:401-403).
+ *  3. exit.  Each workgroup raises its exit flag; workgroup 0 waits for all
+ *     of them and advances the epoch for the next launch.
+ *
+ * Synchronisation uses no read-modify-write: same-address device atomics
+ * serialise (~0.1 us each), so producers write epoch-tagged flags (one word
+ * per producing wave) and consumers poll them.  Dependencies point only to
+ * items with smaller indices, which every workgroup processes first, so with
+ * all G workgroups resident (G is the occupancy limit) every wait ends.
+ * Waits are bounded regardless; one that runs out sets an error word instead
+ * of hanging.
+ *
+ * Data produced by another workgroup in the same launch (logits, h, partial
+ * y) is written with device-coherent stores (agent-scope relaxed atomics:
+ * `sc1` on gfx950, written through the per-XCD L2) and read with
+ * device-coherent loads; a producer waits for its stores to complete
+ * (s_waitcnt) before raising its flag.  Agent-scope release/acquire fences
+ * are avoided: on gfx950 they write back / invalidate a whole XCD L2.
+ *
+ * Weights stay in GGUF block layout.  A lane owns one segment of a row:
+ * Q8_0 one 34-byte block (9 dwords loaded from the 4-byte aligned window
+ * that holds it, 32 columns), Q4_0 a pair of 18-byte blocks (9 dwords, 64
+ * columns), and keeps the matching activations in registers.
+ */
+#include "moe_device.h"
+
+#define NTHREADS 256
+#define GU_ROWS 8
+#define DN_ROWS 16
+#define NREP 64 /* == WAVE: one replica per lane of the writing wave */
+
+struct DecodeArgs {
+	const float *x;
+	const float *router;
+	const float *bias;
+	const uint8_t *gate, *up, *down;
+	size_t gu_stride, dn_stride;
+	u32 *ids_out;
+	float *w_out;
+	float *h;
+	float *ypart;
+	float *out;
+	u32 *sync;
+	int T, E, EI, NE, K, renorm, kch;
+	int n_gu, n_dn;
+	int off_exit, off_rep, off_hf, off_ready, off_yf;
+	int rep_stride; /* u64 entries between replicas (a multiple of 512: 4 KB) */
+};
+
+#define SPIN_LIMIT (1 << 20)
+
+/* device-coherent accesses (global_{load,store} ... sc1) */
+__device__ static inline void st_dev(float *p, float v)
+{
+	__hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ static inline void st_dev_u32(u32 *p, u32 v)
+{
+	__hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ static inline void st_dev_u64(uint64_t *p, uint64_t v)
+{
+	__hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ static inline float ld_dev(const float *p)
+{
+	return __hip_atomic_load((float *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ static inline u32 ld_dev_u32(const u32 *p)
+{
+	return __hip_atomic_load((u32 *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ static inline uint64_t ld_dev_u64(const uint64_t *p)
+{
+	return __hip_atomic_load((uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ static inline void backoff(int &step)
+{
+	switch (step) {
+	case 0: __builtin_amdgcn_s_sleep(1); break;
+	case 1: __builtin_amdgcn_s_sleep(2); break;
+	case 2: __builtin_amdgcn_s_sleep(4); break;
+	default: __builtin_amdgcn_s_sleep(8); break;
+	}
+	step += step < 3;
+}
+
+/*
+ * The whole workgroup waits until n flags starting at f all equal `epoch`.
+ * Each thread checks n / NTHREADS of them per round.
+ */
+__device__ static inline void wait_flags(const u32 *f, int n, u32 epoch, u32 *err)
+{
+	__shared__ int s_ok;
+	int step = 0;
+	for (int round = 0;; round++) {
+		bool ok = true;
+		for (int i = threadIdx.x; i < n; i += NTHREADS)
+			ok &= ld_dev_u32(&f[i]) == epoch;
+		if (threadIdx.x == 0)
+			s_ok = 1;
+		__syncthreads();
+		if (!ok)
+			s_ok = 0;
+		__syncthreads();
+		if (s_ok)
+			return;
+		if (round >= SPIN_LIMIT) {
+			if (threadIdx.x == 0)
+				st_dev_u32(err, 1u);
+			return;
+		}
+		backoff(step);
+		__syncthreads();
+	}
+}
+
+/* ---------------------------------------------------------------------- */
+/* segments                                                               */
+/* ---------------------------------------------------------------------- */
+
+template <int WT> struct segq;
+
+/* Q8_0: one block per lane.  Block s of a row starts at byte 34s; the 36-byte
+ * window starting at (34s & ~3) holds it: scale in bytes 0-1 of the window
+ * (even s) or 2-3 (odd s), quants right after. */
+template <> struct segq<1> {
+	static constexpr int DW = 9, COLS = 32;
+	__device__ static inline const uint8_t *win(const uint8_t *row, int s)
+	{
+		return row + ((34 * s) & ~3);
+	}
+	__device__ static inline float dot(const u32 (&d)[9], const float (&x)[32], int s)
+	{
+		const int sh = (s & 1) ? 32 : 16;
+		float acc = 0.0f;
+#pragma unroll
+		for (int k = 0; k < 8; k++) {
+			u32 q = (u32)((((uint64_t)d[k + 1] << 32) | d[k]) >> sh);
+#pragma unroll
+			for (int b = 0; b < 4; b++)
+				acc = __builtin_fmaf((float)(int)(int8_t)(q >> (8 * b)), x[4 * k + b], acc);
+		}
+		return f16_bits_to_f32(d[0] >> (sh - 16)) * acc;
+	}
+};
+
+/* Q4_0: a pair of blocks per lane, 36 bytes at 36s (quant.c:126-155). */
+template <> struct segq<2> {
+	static constexpr int DW = 9, COLS = 64;
+	__device__ static inline const uint8_t *win(const uint8_t *row, int s)
+	{
+		return row + 36 * s;
+	}
+	__device__ static inline float dot(const u32 (&d)[9], const float (&x)[64], int)
+	{
+		return seg_dot_q4_0(d, x);
+	}
+};
+
+template <int COLS>
+__device__ static inline void lds_seg(const float *s, int seg, float (&x)[COLS])
+{
+	const float4 *s4 = (const float4 *)(s + seg * (COLS + 4));
+#pragma unroll
+	for (int i = 0; i < COLS / 4; i++) {
+		float4 v = s4[i];
+		x[4 * i + 0] = v.x;
+		x[4 * i + 1] = v.y;
+		x[4 * i + 2] = v.z;
+		x[4 * i + 3] = v.w;
+	}
+}
+
+/* n floats from global into LDS, COLS-float segments padded by 4 floats */
+template <int COLS>
+__device__ static inline void stage_seg(float *s, const float *g, int n)
+{
+	const float4 *g4 = (const float4 *)g;
+	for (int i = threadIdx.x; i < n / 4; i += NTHREADS) {
+		int k = 4 * i;
+		*(float4 *)(s + (k / COLS) * (COLS + 4) + k % COLS) = g4[i];
+	}
+}
+
+/* the same for data another workgroup produced in this launch */
+template <int COLS>
+__device__ static inline void stage_seg_dev(float *s, const float *g, int n)
+{
+	for (int i = threadIdx.x; i < n / 2; i += NTHREADS) {
+		uint64_t v = ld_dev_u64((const uint64_t *)(g + 2 * i));
+		int k = 2 * i;
+		*(uint64_t *)(s + (k / COLS) * (COLS + 4) + k % COLS) = v;
+	}
+}
+
+/* ---------------------------------------------------------------------- */
+/* routing                                                                */
+/* ---------------------------------------------------------------------- */
+
+/* copy n floats, element k -> dst[(k & 7) * RS + (k >> 3)] */
+__device__ static inline void stage_transposed(float *dst, const float *src, int n, int RS)
+{
+	const float4 *s4 = (const float4 *)src;
+	for (int i = threadIdx.x; i < n / 4; i += NTHREADS) {
+		float4 v = s4[i];
+		int k = 4 * i;
+		dst[((k + 0) & 7) * RS + ((k + 0) >> 3)] = v.x;
+		dst[((k + 1) & 7) * RS + ((k + 1) >> 3)] = v.y;
+		dst[((k + 2) & 7) * RS + ((k + 2) >> 3)] = v.z;
+		dst[((k + 3) & 7) * RS + ((k + 3) >> 3)] = v.w;
+	}
+}
+
+/* acc = fma(x[k], w[k], acc) over k = 0, 8, 16, ... of one transposed row
+ * pair (E8 floats each); LDS reads double-buffered ahead of the chain */
+__device__ static inline float router_chain(const float *xrow, const float *wrow, int E8)
+{
+	const float4 *xr = (const float4 *)xrow, *wr = (const float4 *)wrow;
+	float4 xa[4], wa[4], xb[4], wb[4];
+	float acc = 0.0f;
+	const int nb = E8 / 16; /* batches of 4 float4 pairs; even */
+#pragma unroll
+	for (int u = 0; u < 4; u++) {
+		xa[u] = xr[u];
+		wa[u] = wr[u];
+	}
+	for (int b = 0; b < nb; b += 2) {
+#pragma unroll
+		for (int u = 0; u < 4; u++) {
+			xb[u] = xr[4 * (b + 1) + u];
+			wb[u] = wr[4 * (b + 1) + u];
+		}
+#pragma unroll
+		for (int u = 0; u < 4; u++) {
+			acc = __builtin_fmaf(xa[u].x, wa[u].x, acc);
+			acc = __builtin_fmaf(xa[u].y, wa[u].y, acc);
+			acc = __builtin_fmaf(xa[u].z, wa[u].z, acc);
+			acc = __builtin_fmaf(xa[u].w, wa[u].w, acc);
+		}
+		if (b + 2 < nb) {
+#pragma unroll
+			for (int u = 0; u < 4; u++) {
+				xa[u] = xr[4 * (b + 2) + u];
+				wa[u] = wr[4 * (b + 2) + u];
+			}
+		}
+#pragma unroll
+		for (int u = 0; u < 4; u++) {
+			acc = __builtin_fmaf(xb[u].x, wb[u].x, acc);
+			acc = __builtin_fmaf(xb[u].y, wb[u].y, acc);
+			acc = __builtin_fmaf(xb[u].z, wb[u].z, acc);
+			acc = __builtin_fmaf(xb[u].w, wb[u].w, acc);
+		}
+	}
+	return acc;
+}
+
+/* router row j for every token, published into every replica by wave 0;
+ * prev_epoch (the launch's epoch minus one, valid in thread 0) is consumed
+ * only after the chain, so its load is in flight meanwhile */
+__device__ static void router_row(const DecodeArgs &a, int j, u32 prev_epoch, float *lds)
+{
+	const int E = a.E, E8 = E / 8, RS = E8 + 4;
+	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+	float *sw = lds;          /* [8][RS] router row, transposed */
+	float *sx = lds + 8 * RS; /* [8][RS] token, transposed */
+	__shared__ float s_logit;
+	uint64_t *rep = (uint64_t *)(a.sync + a.off_rep);
+
+	stage_transposed(sw, a.router + (size_t)j * E, E, RS);
+	for (int t = 0; t < a.T; t++) {
+		stage_transposed(sx, a.x + (size_t)t * E, E, RS);
+		__syncthreads();
+		if (wave == 0) {
+			/* lane l < 8 replays AVX2 lane l: elements l, l+8, ... in order */
+			const int l = lane & 7;
+			float acc = router_chain(sx + l * RS, sw + l * RS, E8);
+			acc = acc + __shfl_xor(acc, 4, 8);
+			acc = acc + __shfl_xor(acc, 2, 8);
+			acc = acc + __shfl_xor(acc, 1, 8);
+			if (lane == 0)
+				s_logit = (a.bias ? a.bias[j] : 0.0f) + acc;
+		}
+		__syncthreads();
+		if (wave == 0) { /* NREP == WAVE: lane r writes replica r */
+			const u32 ep = __shfl(prev_epoch, 0, WAVE) + 1;
+			const uint64_t v = ((uint64_t)ep << 32) | __builtin_bit_cast(u32, s_logit);
+			st_dev_u64(&rep[(size_t)lane * a.rep_stride + (size_t)t * a.NE + j], v);
+		}
+		__syncthreads();
+	}
+}
+
+/* wait for this workgroup's replica, then softmax/top-k of every token into
+ * LDS: s_ids/s_w [T*K] */
+__device__ static void route_local(const DecodeArgs &a, u32 epoch, float *lds, u32 *s_ids,
+				   float *s_w, const uint64_t *s_tab)
+{
+	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+	const int n = a.T * a.NE;
+	const uint64_t *rep = (const uint64_t *)(a.sync + a.off_rep) +
+			      (size_t)(blockIdx.x % NREP) * a.rep_stride;
+	float *slg = lds; /* [T][NE] logits */
+	__shared__ int s_ok;
+	int step = 0;
+	/* one word first: the last router row, usually the last to land */
+	if (threadIdx.x == 0)
+		for (int i = 0; i < SPIN_LIMIT && (u32)(ld_dev_u64(&rep[n - 1]) >> 32) != epoch; i++)
+			backoff(step);
+	__syncthreads();
+	step = 0;
+	for (int round = 0;; round++) {
+		bool ok = true;
+		for (int i = threadIdx.x; i < n; i += NTHREADS) {
+			uint64_t v = ld_dev_u64(&rep[i]);
+			ok &= (u32)(v >> 32) == epoch;
+			slg[i] = __builtin_bit_cast(float, (u32)v);
+		}
+		if (threadIdx.x == 0)
+			s_ok = 1;
+		__syncthreads();
+		if (!ok)
+			s_ok = 0;
+		__syncthreads();
+		if (s_ok)
+			break;
+		if (round >= SPIN_LIMIT) {
+			if (threadIdx.x == 0)
+				st_dev_u32(a.sync + MOE_SYNC_ERR_WORD, 1u);
+			break;
+		}
+		backoff(step);
+		__syncthreads();
+	}
+	float *scr = lds + ((a.T * a.NE + 15) & ~15) + wave * (MOE_MAX_NE + 2 * MOE_MAX_TOPK);
+	for (int t = wave; t < a.T; t += NTHREADS / WAVE) /* NE <= 64: one expert per lane */
+		wave_softmax_topk64(lane < a.NE ? slg[t * a.NE + lane] : 0.0f, s_ids + t * a.K,
+				    s_w + t * a.K, a.NE, a.K, a.renorm, s_tab, scr,
+				    (u32 *)(scr + MOE_MAX_NE), scr + MOE_MAX_NE + MOE_MAX_TOPK, lane);
+	__syncthreads();
+}
+
+/* ---------------------------------------------------------------------- */
+/* expert items                                                           */
+/* ---------------------------------------------------------------------- */
+
+template <int WT, int CD> struct down_geo {
+	static constexpr int RPS = WAVE / CD, RW = DN_ROWS / 4, NS = RW / RPS;
+	static constexpr int CHUNK = CD * segq<WT>::COLS; /* columns of one K-chunk */
+};
+
+/* issue the weight loads of down item d (they do not depend on h) */
+template <int WT, int CD>
+__device__ static inline void down_load(const DecodeArgs &a, int d, const u32 *s_ids,
+					u32 (&dd)[down_geo<WT, CD>::NS][9])
+{
+	typedef segq<WT> S;
+	typedef down_geo<WT, CD> DG;
+	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+	const int nrb = a.E / DN_ROWS;
+	const int p = d / (a.kch * nrb), rem = d % (a.kch * nrb);
+	const int kc = rem / nrb, rbk = rem % nrb;
+	const int row0 = rbk * DN_ROWS + wave * DG::RW;
+	const int seg = lane % CD, sub = lane / CD;
+	const size_t rb = (size_t)(a.EI / MOE_QK) * (WT == 1 ? 34 : 18);
+	const uint8_t *D = S::win(a.down + (size_t)s_ids[p] * a.dn_stride, kc * CD + seg);
+#pragma unroll
+	for (int s2 = 0; s2 < DG::NS; s2++)
+		load_dwords<S::DW>(D + (size_t)(row0 + s2 * DG::RPS + sub) * rb, dd[s2]);
+}
+
+/*
+ * Gate/up tile g: h[p][rows] = silu(gate.x) * (up.x).  If pre_d >= 0 the
+ * weight loads of down item pre_d are issued right after this tile's own.
+ * The last tile of a K-chunk of h[p] (in item order) waits for the chunk's
+ * other tiles and raises the chunk's single ready word.
+ */
+template <int WT, int CG, int CD>
+__device__ static void gateup_item(const DecodeArgs &a, int g, const u32 *s_ids, float *sx,
+				   int &staged, u32 epoch, int pre_d,
+				   u32 (&dd)[down_geo<WT, CD>::NS][9], const uint64_t *s_tab)
+{
+	typedef segq<WT> S;
+	constexpr int RPS = WAVE / CG, RW = GU_ROWS / 4, NS = RW / RPS;
+	constexpr int TPC = down_geo<WT, CD>::CHUNK / GU_ROWS; /* tiles per K-chunk */
+	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+	const int tiles = a.EI / GU_ROWS;
+	const int p = g / tiles, tile = g % tiles;
+	const int row0 = tile * GU_ROWS + wave * RW;
+	const int t = p / a.K;
+	const int e = (int)s_ids[p];
+	const int seg = lane % CG, sub = lane / CG;
+	const size_t rb = (size_t)(a.E / MOE_QK) * (WT == 1 ? 34 : 18);
+	const uint8_t *G = S::win(a.gate + (size_t)e * a.gu_stride, seg);
+	const uint8_t *U = S::win(a.up + (size_t)e * a.gu_stride, seg);
+
+	u32 dg[NS][S::DW], du[NS][S::DW];
+#pragma unroll
+	for (int s2 = 0; s2 < NS; s2++) {
+		const size_t ro = (size_t)(row0 + s2 * RPS + sub) * rb;
+		load_dwords<S::DW>(G + ro, dg[s2]);
+		load_dwords<S::DW>(U + ro, du[s2]);
+	}
+	if (pre_d >= 0)
+		down_load<WT, CD>(a, pre_d, s_ids, dd);
+	if (staged != t) {
+		__syncthreads(); /* earlier readers of sx are done */
+		stage_seg<S::COLS>(sx, a.x + (size_t)t * a.E, a.E);
+		__syncthreads();
+		staged = t;
+	}
+	float xr[S::COLS];
+	lds_seg<S::COLS>(sx, seg, xr);
+#pragma unroll
+	for (int s2 = 0; s2 < NS; s2++) {
+		const int row = row0 + s2 * RPS + sub;
+		float gv = group_sum<CG>(S::dot(dg[s2], xr, seg));
+		float uv = group_sum<CG>(S::dot(du[s2], xr, seg));
+		if (seg == 0)
+			st_dev(&a.h[(size_t)p * a.EI + row],
+			       (gv / (1.0f + moe_expf_tab(-gv, s_tab))) * uv);
+	}
+	__builtin_amdgcn_s_waitcnt(0);
+	__syncthreads();
+	u32 *hf = a.sync + a.off_hf + (size_t)p * tiles;
+	if (threadIdx.x == 0)
+		st_dev_u32(&hf[tile], epoch);
+	if ((tile + 1) % TPC)
+		return;
+	const int kc = tile / TPC;
+	wait_flags(hf + kc * TPC, TPC - 1, epoch, a.sync + MOE_SYNC_ERR_WORD);
+	if (threadIdx.x == 0)
+		st_dev_u32(a.sync + a.off_ready + (size_t)p * a.kch + kc, epoch);
+}
+
+/* down item d with its weights already in dd: wait for its K-chunk of h[p],
+ * write partial y; the last contribution (in item order) of a (token, row
+ * block) waits for the others and combines the slots in order */
+template <int WT, int CD>
+__device__ static void down_item(const DecodeArgs &a, int d, const float *s_w, float *sh,
+				 u32 epoch, const u32 (&dd)[down_geo<WT, CD>::NS][9])
+{
+	typedef segq<WT> S;
+	typedef down_geo<WT, CD> DG;
+	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+	const int nrb = a.E / DN_ROWS;
+	const int p = d / (a.kch * nrb), rem = d % (a.kch * nrb);
+	const int kc = rem / nrb, rbk = rem % nrb;
+	const int t = p / a.K, slot = p % a.K;
+	const int row0 = rbk * DN_ROWS + wave * DG::RW;
+	const int seg = lane % CD, sub = lane / CD;
+
+	wait_flags(a.sync + a.off_ready + (size_t)p * a.kch + kc, 1, epoch,
+		   a.sync + MOE_SYNC_ERR_WORD);
+	stage_seg_dev<S::COLS>(sh, a.h + (size_t)p * a.EI + (size_t)kc * DG::CHUNK, DG::CHUNK);
+	__syncthreads();
+	float xr[S::COLS];
+	lds_seg<S::COLS>(sh, seg, xr);
+#pragma unroll
+	for (int s2 = 0; s2 < DG::NS; s2++) {
+		const int row = row0 + s2 * DG::RPS + sub;
+		float y = group_sum<CD>(S::dot(dd[s2], xr, kc * CD + seg));
+		if (seg == 0)
+			st_dev(&a.ypart[((size_t)p * a.kch + kc) * a.E + row], y);
+	}
+	__builtin_amdgcn_s_waitcnt(0);
+	__syncthreads();
+	const int ncontrib = a.K * a.kch;
+	u32 *yf = a.sync + a.off_yf + ((size_t)t * nrb + rbk) * ncontrib;
+	if (threadIdx.x == 0)
+		st_dev_u32(&yf[slot * a.kch + kc], epoch);
+	if (slot != a.K - 1 || kc != a.kch - 1)
+		return;
+	wait_flags(yf, ncontrib - 1, epoch, a.sync + MOE_SYNC_ERR_WORD);
+	if (threadIdx.x < DN_ROWS) {
+		const int row = rbk * DN_ROWS + threadIdx.x;
+		float acc = 0.0f;
+		for (int s = 0; s < a.K; s++) {
+			const size_t ps = (size_t)t * a.K + s;
+			float y = ld_dev(&a.ypart[ps * a.kch * a.E + row]);
+			for (int c = 1; c < a.kch; c++)
+				y += ld_dev(&a.ypart[(ps * a.kch + c) * a.E + row]);
+			acc = acc + y / (1.0f / s_w[ps]);
+		}
+		a.out[(size_t)t * a.E + row] = acc;
+	}
+}
+
+template <int WT, int CG, int CD>
+__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(4, 4)))
+void k_moe_decode(DecodeArgs a)
+{
+	extern __shared__ float lds[];
+	__shared__ u32 s_ids[MOE_FUSED_MAX_P];
+	__shared__ float s_w[MOE_FUSED_MAX_P];
+	__shared__ u32 s_epoch;
+	__shared__ uint64_t s_tab[32];
+	typedef segq<WT> S;
+
+	if (threadIdx.x < 32)
+		s_tab[threadIdx.x] = moe_exp2_tab[threadIdx.x];
+	u32 prev_epoch = 0;
+	if (threadIdx.x == 0)
+		prev_epoch = ld_dev_u32(a.sync); /* consumed late: the load overlaps routing */
+	if ((int)blockIdx.x < a.NE) {
+		router_row(a, blockIdx.x, prev_epoch, lds);
+		__syncthreads();
+	}
+	if (threadIdx.x == 0)
+		s_epoch = prev_epoch + 1;
+	__syncthreads();
+	const u32 epoch = s_epoch;
+	route_local(a, epoch, lds, s_ids, s_w, s_tab);
+	if (blockIdx.x == 0)
+		for (int i = threadIdx.x; i < a.T * a.K; i += NTHREADS) {
+			a.ids_out[i] = s_ids[i];
+			a.w_out[i] = s_w[i];
+		}
+
+	float *sx = lds;                                       /* x, padded segments */
+	float *sh = lds + (a.E / S::COLS) * (S::COLS + 4);     /* h chunk, padded */
+	int staged = -1;
+	const int total = a.n_gu + a.n_dn;
+	u32 dd[down_geo<WT, CD>::NS][9];
+	bool have_dd = false;
+	int item = blockIdx.x;
+	for (; item < a.n_gu; item += gridDim.x) {
+		const int nxt = item + (int)gridDim.x;
+		const int pre = (nxt >= a.n_gu && nxt < total) ? nxt - a.n_gu : -1;
+		gateup_item<WT, CG, CD>(a, item, s_ids, sx, staged, epoch, pre, dd, s_tab);
+		have_dd = pre >= 0;
+		__syncthreads();
+	}
+	for (; item < total; item += gridDim.x) {
+		if (!have_dd)
+			down_load<WT, CD>(a, item - a.n_gu, s_ids, dd);
+		have_dd = false;
+		down_item<WT, CD>(a, item - a.n_gu, s_w, sh, epoch, dd);
+		__syncthreads();
+	}
+
+	/* exit: workgroup 0 advances the epoch once every workgroup is out */
+	u32 *exitf = a.sync + a.off_exit;
+	if (blockIdx.x != 0) {
+		if (threadIdx.x == 0)
+			st_dev_u32(&exitf[blockIdx.x], epoch);
+		return;
+	}
+	wait_flags(exitf + 1, (int)gridDim.x - 1, epoch, a.sync + MOE_SYNC_ERR_WORD);
+	if (threadIdx.x == 0)
+		st_dev_u32(a.sync, epoch);
+}
+
+/* ---------------------------------------------------------------------- */
+
+template <int WT, int CG, int CD>
+static const void *decode_fn()
+{
+	return (const void *)k_moe_decode<WT, CG, CD>;
+}
+
+/* Q8_0: CG = E/32, CD from EI/32; Q4_0: CG = E/64, CD from EI/64 */
+static const void *pick_decode(int wtype, int CG, int CD)
+{
+#define F3(W_, G, D)                                  \
+	if (wtype == W_ && CG == G && CD == D)        \
+		return decode_fn<W_, G, D>();
+#define FD(W_, G) F3(W_, G, 16) F3(W_, G, 32) F3(W_, G, 64)
+	FD(1, 32) FD(1, 64) FD(2, 32) FD(2, 64)
+#undef FD
+#undef F3
+	return NULL;
+}
+
+static int seg_cols(int wtype)
+{
+	return wtype == 1 ? 32 : 64;
+}
+
+/* lanes per row: the largest power of two <= 64 dividing K / cols */
+static int lanes_for(size_t K, int cols)
+{
+	size_t nseg = K / (size_t)cols;
+	int c = 64;
+	while (c > 1 && nseg % (size_t)c)
+		c >>= 1;
+	return c;
+}
+
+struct Geo {
+	int CG, CD, kch;
+	const void *fn;
+};
+
+static Geo geometry(int wtype, size_t E, size_t EI)
+{
+	Geo g;
+	int cols = seg_cols(wtype);
+	g.CG = lanes_for(E, cols);
+	g.CD = lanes_for(EI, cols);
+	g.kch = (int)(EI / (size_t)cols / (size_t)g.CD);
+	g.fn = NULL;
+	if (E % (size_t)cols || EI % (size_t)cols || E / (size_t)cols != (size_t)g.CG)
+		return g; /* a gate/up row must fit one wave */
+	g.fn = pick_decode(wtype, g.CG, g.CD);
+	return g;
+}
+
+static size_t decode_lds_bytes(int wtype, size_t E, size_t EI, size_t T, size_t NE)
+{
+	int cols = seg_cols(wtype);
+	Geo g = geometry(wtype, E, EI);
+	size_t rt = (size_t)2 * 8 * (E / 8 + 4) * sizeof(float);
+	size_t tk = (((T * NE + 15) & ~(size_t)15) + 4 * (MOE_MAX_NE + 2 * MOE_MAX_TOPK)) *
+		    sizeof(float);
+	size_t ex = (E / cols + g.CD) * (cols + 4) * sizeof(float);
+	size_t m = rt > tk ? rt : tk;
+	return m > ex ? m : ex;
+}
+
+struct SyncLayout {
+	size_t off_exit, off_rep, off_hf, off_ready, off_yf, words, rep_stride;
+};
+
+static SyncLayout sync_layout(int wtype, size_t T, size_t K, size_t E, size_t EI, size_t NE,
+			      int grid)
+{
+	Geo g = geometry(wtype, E, EI);
+	SyncLayout s;
+	s.rep_stride = (T * NE + 511) & ~(size_t)511;
+	s.off_exit = 1024;
+	s.off_rep = s.off_exit + (((size_t)grid + 1023) & ~(size_t)1023);
+	s.off_hf = s.off_rep + (size_t)NREP * s.rep_stride * 2;
+	s.off_ready = s.off_hf + T * K * (EI / GU_ROWS);
+	s.off_yf = s.off_ready + T * K * (size_t)g.kch;
+	s.words = s.off_yf + T * (E / DN_ROWS) * K * (size_t)g.kch;
+	return s;
+}
+
+extern "C" int moe_fused_supported(int wtype, size_t E, size_t EI, size_t NE, size_t T,
+				   size_t K)
+{
+	if (NE > WAVE || T * K > MOE_FUSED_MAX_P || E % DN_ROWS || EI % GU_ROWS || E % 256 ||
+	    EI % 256)
+		return 0;
+	return geometry(wtype, E, EI).fn != NULL;
+}
+
+extern "C" int moe_fused_kchunks(int wtype, size_t EI)
+{
+	return geometry(wtype, 4096, EI).kch;
+}
+
+extern "C" size_t moe_fused_sync_words(int wtype, size_t T, size_t K, size_t E, size_t EI,
+				       size_t NE, int grid)
+{
+	return sync_layout(wtype, T, K, E, EI, NE, grid).words;
+}
+
+extern "C" int moe_fused_grid(int wtype, size_t E, size_t EI, size_t NE)
+{
+	Geo g = geometry(wtype, E, EI);
+	if (!g.fn)
+		return 0;
+	int dev = 0, ncu = 0, per = 0;
+	if (hipGetDevice(&dev) != hipSuccess ||
+	    hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+		return 0;
+	size_t lds = decode_lds_bytes(wtype, E, EI, MOE_FUSED_MAX_P, NE);
+	if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, g.fn, NTHREADS, lds) != hipSuccess ||
+	    per < 1)
+		return 0;
+	if (per > MOE_FUSED_WG_PER_CU)
+		per = MOE_FUSED_WG_PER_CU;
+	int grid = ncu * per;
+	return grid >= (int)NE ? grid : 0; /* router rows need one workgroup each */
+}
+
+extern "C" int moe_launch_fused(int wtype, const float *x, const float *router,
+				const float *bias, const uint8_t *gate, const uint8_t *up,
+				const uint8_t *down, size_t gu_stride, size_t dn_stride,
+				uint32_t *ids, float *w, float *h, float *ypart, float *out,
+				uint32_t *sync, int T, int E, int EI, int NE, int K, int renorm,
+				int grid, void *stream)
+{
+	Geo g = geometry(wtype, (size_t)E, (size_t)EI);
+	if (!g.fn || grid < NE)
+		return (int)hipErrorInvalidValue;
+	SyncLayout sl = sync_layout(wtype, (size_t)T, (size_t)K, (size_t)E, (size_t)EI,
+				    (size_t)NE, grid);
+	DecodeArgs a;
+	a.x = x;
+	a.router = router;
+	a.bias = bias;
+	a.gate = gate;
+	a.up = up;
+	a.down = down;
+	a.gu_stride = gu_stride;
+	a.dn_stride = dn_stride;
+	a.ids_out = ids;
+	a.w_out = w;
+	a.h = h;
+	a.ypart = ypart;
+	a.out = out;
+	a.sync = sync;
+	a.T = T;
+	a.E = E;
+	a.EI = EI;
+	a.NE = NE;
+	a.K = K;
+	a.renorm = renorm;
+	a.kch = g.kch;
+	a.n_gu = T * K * (EI / GU_ROWS);
+	a.n_dn = T * K * g.kch * (E / DN_ROWS);
+	a.off_exit = (int)sl.off_exit;
+	a.off_rep = (int)sl.off_rep;
+	a.off_hf = (int)sl.off_hf;
+	a.off_ready = (int)sl.off_ready;
+	a.off_yf = (int)sl.off_yf;
+	a.rep_stride = (int)sl.rep_stride;
+	void *args[] = {&a};
+	hipError_t rc = hipLaunchKernel(g.fn, dim3(grid), dim3(NTHREADS), args,
+					decode_lds_bytes(wtype, (size_t)E, (size_t)EI, (size_t)T,
+							 (size_t)NE),
+					(hipStream_t)stream);
+	if (rc != hipSuccess)
+		return (int)rc;
+	return (int)hipGetLastError();
+}

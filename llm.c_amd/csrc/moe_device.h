@@ -128,6 +128,10 @@ template <> struct qseg<1> {
 		load_dwords<17>(p, d);
 		return seg_dot_q8_0(d, x);
 	}
+	__device__ static inline float dot_regs(const u32 (&d)[17], const float (&x)[64])
+	{
+		return seg_dot_q8_0(d, x);
+	}
 };
 template <> struct qseg<2> {
 	static constexpr int BYTES = 36;
@@ -136,6 +140,10 @@ template <> struct qseg<2> {
 	{
 		u32 d[9];
 		load_dwords<9>(p, d);
+		return seg_dot_q4_0(d, x);
+	}
+	__device__ static inline float dot_regs(const u32 (&d)[9], const float (&x)[64])
+	{
 		return seg_dot_q4_0(d, x);
 	}
 };
@@ -226,10 +234,19 @@ __device__ static inline void wave_softmax_topk(const float *logits, float *prob
 	WAVE_SYNC();
 
 	const int nv = NE - NE % 8;
+	float ev[MOE_MAX_NE / WAVE];
+#pragma unroll
+	for (int r = 0; r < MOE_MAX_NE / WAVE; r++)
+		ev[r] = (lane + r * WAVE < NE) ? sp[lane + r * WAVE] : 0.0f;
+	/* lane l < 8: s_l = e_l + e_{8+l} + e_{16+l} + ... in order; element
+	 * 8c+l sits in ev[c/8] of lane 8(c%8)+l */
 	float s = 0.0f;
-	if (lane < 8)
-		for (int c = 0; c < nv; c += 8)
-			s = s + sp[c + lane];
+#pragma unroll
+	for (int c = 0; c < MOE_MAX_NE / 8; c++) {
+		float v = __shfl(ev[c >> 3], 8 * (c & 7) + (lane & 7), WAVE);
+		if (8 * c < nv)
+			s = s + v;
+	}
 	s = s + __shfl_xor(s, 4, 8);
 	s = s + __shfl_xor(s, 2, 8);
 	s = s + __shfl_xor(s, 1, 8);
@@ -243,9 +260,31 @@ __device__ static inline void wave_softmax_topk(const float *logits, float *prob
 		int i = lane + r * WAVE;
 		pv[r] = 0.0f;
 		if (i < NE) {
-			pv[r] = sp[i] / sum;
+			pv[r] = ev[r] / sum;
 			if (probs)
 				probs[i] = pv[r];
+		}
+	}
+
+	/* rank_i over broadcasts of every p_j (v_readlane, no memory round trip) */
+	int rank[MOE_MAX_NE / WAVE];
+#pragma unroll
+	for (int r = 0; r < MOE_MAX_NE / WAVE; r++)
+		rank[r] = 0;
+#pragma unroll
+	for (int r2 = 0; r2 < MOE_MAX_NE / WAVE; r2++) {
+		if (r2 * WAVE >= NE)
+			break;
+		const int pbits = __builtin_bit_cast(int, pv[r2]);
+		const int n2 = NE - r2 * WAVE < WAVE ? NE - r2 * WAVE : WAVE;
+		for (int j2 = 0; j2 < n2; j2++) {
+			const float pj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(pbits, j2));
+			const int j = r2 * WAVE + j2;
+#pragma unroll
+			for (int r = 0; r < MOE_MAX_NE / WAVE; r++) {
+				const int i = lane + r * WAVE;
+				rank[r] += (pj > pv[r]) || (pj == pv[r] && j < i);
+			}
 		}
 	}
 	WAVE_SYNC();
@@ -256,21 +295,6 @@ __device__ static inline void wave_softmax_topk(const float *logits, float *prob
 			sp[i] = pv[r];
 	}
 	WAVE_SYNC();
-
-	int rank[MOE_MAX_NE / WAVE];
-#pragma unroll
-	for (int r = 0; r < MOE_MAX_NE / WAVE; r++) {
-		int i = lane + r * WAVE;
-		int rk = 0;
-		if (i < NE) {
-			float pi = pv[r];
-			for (int j = 0; j < NE; j++) {
-				float pj = sp[j];
-				rk += (pj > pi) || (pj == pi && j < i);
-			}
-		}
-		rank[r] = rk;
-	}
 	const int r0 = __shfl(rank[0], 0, WAVE);
 	const int lim = r0 < K ? r0 : K;
 #pragma unroll
@@ -300,6 +324,85 @@ __device__ static inline void wave_softmax_topk(const float *logits, float *prob
 	for (int e = lane; e < K; e += WAVE) {
 		ids[e] = sid[e];
 		wout[e] = sw[e];
+	}
+}
+
+/*
+ * wave_softmax_topk for NE <= 64: element i lives in lane i.  Same arithmetic
+ * and order as wave_softmax_topk; the lane sums fetch their eight inputs with
+ * independent shuffles and the ranks come from broadcast LDS reads of integer
+ * keys.  tab is the exp table (an LDS copy), sp 128 floats of this wave's LDS
+ * (8-byte aligned), ids/w receive the k slots (LDS or global).
+ */
+__device__ static inline void wave_softmax_topk64(float logit, u32 *ids, float *wout, int NE,
+						  int K, int renorm, const uint64_t *tab,
+						  float *sp, u32 *sid, float *sw, int lane)
+{
+	const bool valid = lane < NE;
+	float mx = valid ? logit : -__builtin_inff();
+#pragma unroll
+	for (int off = 32; off >= 1; off >>= 1)
+		mx = fmaxf(mx, __shfl_xor(mx, off, WAVE));
+	const float e = valid ? moe_expf_tab(logit - mx, tab) : 0.0f;
+
+	const int nv = NE - NE % 8;
+	float g[8];
+#pragma unroll
+	for (int c = 0; c < 8; c++)
+		g[c] = __shfl(e, 8 * c + (lane & 7), WAVE);
+	float s = 0.0f;
+#pragma unroll
+	for (int c = 0; c < 8; c++)
+		if (8 * c < nv)
+			s = s + g[c];
+	s = s + __shfl_xor(s, 4, 8);
+	s = s + __shfl_xor(s, 2, 8);
+	s = s + __shfl_xor(s, 1, 8);
+	for (int i = nv; i < NE; i++)
+		s += __shfl(e, i, WAVE);
+	const float sum = __shfl(s, 0, WAVE);
+	const float p = e / sum;
+
+	/* p >= 0, so its bits order like the values: j beats i iff key_j > key_i,
+	 * key = (bits(p) + 1) << 6 | (63 - index), 0 for lanes past NE */
+	uint64_t *sk = (uint64_t *)sp;
+	const uint64_t key = valid ? ((uint64_t)(__builtin_bit_cast(u32, p) + 1u) << 6) |
+					     (uint64_t)(63 - lane)
+				   : 0;
+	sk[lane] = key;
+	WAVE_SYNC();
+	int rank = 0;
+	const ulonglong2 *sk2 = (const ulonglong2 *)sk;
+#pragma unroll
+	for (int q = 0; q < 32; q++) {
+		const ulonglong2 v = sk2[q];
+		rank += (int)((key - v.x) >> 63);
+		rank += (int)((key - v.y) >> 63);
+	}
+	const int r0 = __shfl(rank, 0, WAVE);
+	const int lim = r0 < K ? r0 : K;
+	if (lane > 0 && valid && rank < lim) {
+		sid[K - 1 - rank] = (u32)lane;
+		sw[K - 1 - rank] = p;
+	}
+	const float p0 = __shfl(p, 0, WAVE);
+	if (r0 < K)
+		for (int slot = lane; slot < K - r0; slot += WAVE) {
+			sid[slot] = 0;
+			sw[slot] = p0;
+		}
+	WAVE_SYNC();
+	if (lane == 0 && renorm) {
+		float ws = 0.0f;
+		for (int k = 0; k < K; k++)
+			ws += sw[k];
+		for (int k = 0; k < K; k++)
+			sw[k] /= ws;
+	}
+	WAVE_SYNC();
+	for (int k = lane; k < K; k += WAVE) {
+		ids[k] = sid[k];
+		wout[k] = sw[k];
 	}
 }
 

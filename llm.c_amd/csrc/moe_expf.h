@@ -67,7 +67,8 @@ MOE_EXPF_FN uint64_t moe_d2u(double d)
 	return u;
 }
 
-MOE_EXPF_FN float moe_expf(float x)
+/* the same with the 2^(i/32) table at tab (e.g. an LDS copy on the device) */
+MOE_EXPF_FN float moe_expf_tab(float x, const uint64_t *tab)
 {
 	const double inv_ln2_n = 0x1.71547652b82fep+0 * 32; /* 32/ln2 */
 	const double shift = 0x1.8p+52;
@@ -92,7 +93,7 @@ MOE_EXPF_FN float moe_expf(float x)
 	uint64_t ki = moe_d2u(kd);
 	kd -= shift;
 	double r = __builtin_fma(inv_ln2_n, xd, -kd);
-	uint64_t t = moe_exp2_tab[ki % 32];
+	uint64_t t = tab[ki % 32];
 	t += ki << 47;
 	double s = moe_u2d(t);
 	double z = __builtin_fma(c0, r, c1);
@@ -101,6 +102,11 @@ MOE_EXPF_FN float moe_expf(float x)
 	y = __builtin_fma(z, r2, y);
 	y = y * s;
 	return (float)y;
+}
+
+MOE_EXPF_FN float moe_expf(float x)
+{
+	return moe_expf_tab(x, moe_exp2_tab);
 }
 
 #endif

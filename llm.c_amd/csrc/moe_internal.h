@@ -20,7 +20,7 @@ extern "C" {
 #define MOE_MAX_TOPK 64
 #define MOE_FUSED_MAX_P 64  /* T*K handled by the persistent decode kernel */
 #define MOE_SYNC_ERR_WORD 256 /* error word in the persistent kernel's counters */
-#define MOE_FUSED_WG_PER_CU 2 /* workgroups per CU of the persistent expert kernel */
+#define MOE_FUSED_WG_PER_CU 4 /* workgroups per CU of the decode kernel */
 
 /* lanes per row for a K-long dot: the largest power of two <= 64 that
  * divides K / 64, and the number of K-chunks the row is split into. */
@@ -53,15 +53,17 @@ int moe_launch_combine(const float *ypart, const float *w, float *out, int T,
 
 int moe_launch_expf(const float *in, float *out, size_t n, void *stream);
 
-/* Persistent fused layer (moe_fused.hip) for T*K <= MOE_FUSED_MAX_P. */
-int moe_fused_supported(int wtype, size_t E, size_t EI, size_t T, size_t K);
-size_t moe_fused_sync_words(size_t T, size_t K, size_t E);
-int moe_fused_grid(int wtype, size_t E, size_t EI);
+/* One-launch decode layer (moe_decode.hip) for T*K <= MOE_FUSED_MAX_P. */
+int moe_fused_supported(int wtype, size_t E, size_t EI, size_t NE, size_t T, size_t K);
+int moe_fused_kchunks(int wtype, size_t EI);
+size_t moe_fused_sync_words(int wtype, size_t T, size_t K, size_t E, size_t EI, size_t NE,
+                            int grid);
+int moe_fused_grid(int wtype, size_t E, size_t EI, size_t NE);
 int moe_launch_fused(int wtype, const float *x, const float *router, const float *bias,
                      const uint8_t *gate, const uint8_t *up, const uint8_t *down,
-                     size_t gu_stride, size_t dn_stride, float *logits, uint32_t *ids,
-                     float *w, float *h, float *ypart, float *out, uint32_t *sync, int T,
-                     int E, int EI, int NE, int K, int renorm, int grid, void *stream);
+                     size_t gu_stride, size_t dn_stride, uint32_t *ids, float *w, float *h,
+                     float *ypart, float *out, uint32_t *sync, int T, int E, int EI, int NE,
+                     int K, int renorm, int grid, void *stream);
 
 #ifdef __cplusplus
 }
