@@ -79,6 +79,20 @@ def cpu_baseline(lw, w, xs, seconds):
                        f"{el:.1f} s, 1 thread, oracle/moe_oracle.c built -O3 -mavx2 -mfma")
 
 
+def traffic_bytes(kernel, workload):
+    """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, each divided by the
+    factor the same counter reads for a copy of known size), from the
+    committed counter summary of this kernel and workload, or None."""
+    path = os.path.join(REPO, "profiles", f"{kernel}.{workload}.pmc.md")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -90,6 +104,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch without HIP graphs")
+    ap.add_argument("--copy-calib-mb", type=int, default=0,
+                    help="before warmup, run a plain device copy of this many MiB four "
+                         "times (its byte counters calibrate the kernels' counters)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -129,6 +146,17 @@ def main():
         uniq.append(len(np.unique(ids)))
     router_bytes = w["NE"] * E * 4
     bytes_per_call = float(np.mean(uniq)) * expert_bytes(w) + router_bytes + 2 * xbytes
+
+    if args.copy_calib_mb > 0:
+        nb = args.copy_calib_mb << 20
+        c_src, c_dst = H.malloc(nb), H.malloc(nb)
+        for _ in range(4):
+            if hipmoe.lib().hip_moe_copy_dev(c_src, c_dst, nb, s) != 1:
+                sys.exit("hip_moe_copy_dev: " + hipmoe.last_error())
+        H.stream_sync(s)
+        H.free(c_src)
+        H.free(c_dst)
+        log(f"copy calibration: 4 x {nb} bytes")
 
     for i in range(nl):  # every copy allocates its scratch before any capture
         call(i)
@@ -175,6 +203,11 @@ def main():
     log(f"{steps} steps in {ms:.2f} ms: {ms_per_step * 1e3:.2f} us/step, "
         f"{tokens_per_s:.1f} tokens/s, {achieved_gbs:.1f} GB/s algorithmic")
 
+    # one launch of k_moe_decode per call when it applies (T*K <= 64, NE <= 64);
+    # otherwise the call is the router, top-k, gate/up, down and combine kernels
+    fused = T * K <= 64 and w["NE"] <= 64
+    kernel = "k_moe_decode" if fused else "whole layer call (5 kernels)"
+
     cpu = None
     if not args.no_cpu_baseline:
         log(f"cpu baseline ({args.cpu_seconds:.0f} s)")
@@ -206,12 +239,12 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "whole layer call (router, softmax/top-k, gate/up, down, combine)",
+            "kernel": kernel,
             "achieved": round(achieved_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic_bytes(kernel, args.workload),
         },
         "cpu_baseline": cpu,
     }

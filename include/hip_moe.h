@@ -128,6 +128,14 @@ const char *hip_moe_last_error(void);
  */
 int hip_moe_expf_dev(const float *d_in, float *d_out, size_t n, void *stream);
 
+/*
+ * A plain streaming copy of `bytes` (a multiple of 16) between device
+ * buffers, with 16-byte loads and stores.  It has no counterpart in the
+ * reference: profilers read its HBM byte counters (bytes read and written
+ * known exactly) to calibrate the counters of the MoE kernels.
+ */
+int hip_moe_copy_dev(const void *d_src, void *d_dst, size_t bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

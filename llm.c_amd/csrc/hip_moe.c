@@ -414,3 +414,13 @@ int hip_moe_expf_dev(const float *d_in, float *d_out, size_t n, void *stream)
 	LCHK(moe_launch_expf(d_in, d_out, n, stream), "expf");
 	return 1;
 }
+
+int hip_moe_copy_dev(const void *d_src, void *d_dst, size_t bytes, void *stream)
+{
+	if (bytes == 0 || bytes % 16) {
+		set_err("hip_moe_copy_dev: bytes must be a positive multiple of 16");
+		return 0;
+	}
+	LCHK(moe_launch_copy(d_src, d_dst, bytes, stream), "copy");
+	return 1;
+}

@@ -52,6 +52,7 @@ int moe_launch_combine(const float *ypart, const float *w, float *out, int T,
                        int K, int E, int kchunks, void *stream);
 
 int moe_launch_expf(const float *in, float *out, size_t n, void *stream);
+int moe_launch_copy(const void *src, void *dst, size_t bytes, void *stream);
 
 /* One-launch decode layer (moe_decode.hip) for T*K <= MOE_FUSED_MAX_P. */
 int moe_fused_supported(int wtype, size_t E, size_t EI, size_t NE, size_t T, size_t K);

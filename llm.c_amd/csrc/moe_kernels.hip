@@ -180,6 +180,15 @@ __global__ __launch_bounds__(256) void k_expf(const float *__restrict__ in,
 		out[i] = moe_expf(in[i]);
 }
 
+/* plain streaming copy of n 16-byte words (calibrates the HBM byte counters) */
+__global__ __launch_bounds__(256) void k_copy(const uint4 *__restrict__ src,
+					      uint4 *__restrict__ dst, size_t n)
+{
+	for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n;
+	     i += (size_t)gridDim.x * 256)
+		dst[i] = src[i];
+}
+
 /* ------------------------------------------------------------------ */
 /* launchers                                                           */
 /* ------------------------------------------------------------------ */
@@ -326,5 +335,16 @@ extern "C" int moe_launch_expf(const float *in, float *out, size_t n, void *stre
 		return 0;
 	dim3 grid((unsigned)((n + 255) / 256));
 	hipLaunchKernelGGL(k_expf, grid, dim3(256), 0, (hipStream_t)stream, in, out, n);
+	return (int)hipGetLastError();
+}
+
+extern "C" int moe_launch_copy(const void *src, void *dst, size_t bytes, void *stream)
+{
+	if (bytes == 0 || bytes % 16)
+		return (int)hipErrorInvalidValue;
+	size_t n = bytes / 16, blocks = (n + 255) / 256;
+	dim3 grid((unsigned)(blocks < 8192 ? blocks : 8192));
+	hipLaunchKernelGGL(k_copy, grid, dim3(256), 0, (hipStream_t)stream, (const uint4 *)src,
+			   (uint4 *)dst, n);
 	return (int)hipGetLastError();
 }

@@ -60,6 +60,8 @@ def lib():
     L.hip_moe_last_error.argtypes = []
     L.hip_moe_expf_dev.restype = i32
     L.hip_moe_expf_dev.argtypes = [vp, vp, sz, vp]
+    L.hip_moe_copy_dev.restype = i32
+    L.hip_moe_copy_dev.argtypes = [vp, vp, sz, vp]
     # synthetic inputs
     L.moe_row_bytes.restype = sz
     L.moe_row_bytes.argtypes = [i32, sz]
