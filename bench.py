@@ -203,10 +203,13 @@ def main():
     log(f"{steps} steps in {ms:.2f} ms: {ms_per_step * 1e3:.2f} us/step, "
         f"{tokens_per_s:.1f} tokens/s, {achieved_gbs:.1f} GB/s algorithmic")
 
-    # one launch of k_moe_decode per call when it applies (T*K <= 64, NE <= 64);
-    # otherwise the call is the router, top-k, gate/up, down and combine kernels
-    fused = T * K <= 64 and w["NE"] <= 64
-    kernel = "k_moe_decode" if fused else "whole layer call (5 kernels)"
+    # the path the library takes for this T: one launch of k_moe_decode, or
+    # router, top-k, sort and the grouped GEMMs, or router, top-k, GEMVs
+    path = layers[0].path_for(T)
+    kernel = {hipmoe.PATH_DECODE: "k_moe_decode",
+              hipmoe.PATH_GROUPED: "whole layer call (router, top-k, sort, k_pf_gateup, "
+                                   "k_pf_down, combine)",
+              hipmoe.PATH_GEMV: "whole layer call (router, top-k, gate/up, down, combine)"}[path]
 
     cpu = None
     if not args.no_cpu_baseline:

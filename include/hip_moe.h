@@ -111,6 +111,30 @@ int hip_moe_route_dev(hip_moe_layer *L, const float *d_x, size_t T,
 int hip_moe_expert_ffn_dev(hip_moe_layer *L, size_t expert, const float *d_x,
                            float *d_out, void *stream);
 
+/*
+ * Execution paths of hip_moe_ffn / hip_moe_ffn_dev.  None has a counterpart
+ * in the reference, which runs one per-token loop (olmoe.c:364-406):
+ *   DECODE   one persistent launch (T*K <= 64, NE <= 64), fp32 arithmetic
+ *   GEMV     router, top-k, per-pair dequant-GEMV kernels, combine; fp32
+ *   GROUPED  router, top-k, sort by expert, f16 MFMA grouped GEMMs, combine
+ * AUTO picks DECODE where it applies, else GROUPED when the (token, slot)
+ * pairs average at least 4 per expert, else GEMV.  Routing (ids and
+ * weights) is bit-identical on every path; outputs agree with the reference
+ * within 1e-3 relative L2 (fp32 paths: ~1e-6; GROUPED: ~5e-4 from f16
+ * operands).
+ */
+#define HIP_MOE_PATH_AUTO 0
+#define HIP_MOE_PATH_DECODE 1
+#define HIP_MOE_PATH_GEMV 2
+#define HIP_MOE_PATH_GROUPED 3
+
+/* Force a path for later calls (AUTO restores the default); 1 = ok.  A
+ * forced path that does not apply to a call makes that call return 0. */
+int hip_moe_set_path(hip_moe_layer *L, int path);
+
+/* The path a call with T tokens takes now, 0 if none applies. */
+int hip_moe_path_for(const hip_moe_layer *L, size_t T);
+
 /* Release the device copies and scratch of a layer (NULL is a no-op). */
 void hip_moe_free(hip_moe_layer *L);
 

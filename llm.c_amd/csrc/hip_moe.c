@@ -36,6 +36,7 @@ struct hip_moe_layer {
 
 	hipStream_t stream;
 	int fused_grid;     /* workgroups of the persistent kernel, 0 = none */
+	int path;           /* HIP_MOE_PATH_*, AUTO unless set */
 
 	/* scratch for up to cap_T tokens */
 	size_t cap_T;
@@ -46,6 +47,9 @@ struct hip_moe_layer {
 	float *d_ypart;
 	uint32_t *d_sync;   /* epoch and flags of the decode kernel */
 	size_t sync_words;
+	int *d_rows;        /* grouped path: sorted pair per row, -1 = padding */
+	int *d_tile_e;      /* grouped path: expert of each m-tile, -1 = unused */
+	void *d_h16;        /* grouped path: f16 h in sorted row order */
 
 	/* staging for the host-pointer entry point */
 	size_t cap_io;
@@ -110,6 +114,9 @@ void hip_moe_free(hip_moe_layer *L)
 	hipFree(L->d_h);
 	hipFree(L->d_ypart);
 	hipFree(L->d_sync);
+	hipFree(L->d_rows);
+	hipFree(L->d_tile_e);
+	hipFree(L->d_h16);
 	hipFree(L->d_x);
 	hipFree(L->d_out);
 	hipFree(L->d_bias);
@@ -221,6 +228,12 @@ static int ensure_scratch(hip_moe_layer *L, size_t T)
 	hipFree(L->d_h);
 	hipFree(L->d_ypart);
 	hipFree(L->d_sync);
+	hipFree(L->d_rows);
+	hipFree(L->d_tile_e);
+	hipFree(L->d_h16);
+	L->d_rows = NULL;
+	L->d_tile_e = NULL;
+	L->d_h16 = NULL;
 	L->d_logits = NULL;
 	L->d_ids = NULL;
 	L->d_w = NULL;
@@ -239,6 +252,14 @@ static int ensure_scratch(hip_moe_layer *L, size_t T)
 	HIPCHK(hipMalloc((void **)&L->d_sync, L->sync_words * sizeof(uint32_t)), "hipMalloc(sync)");
 	/* zeroed once here; the decode kernel's flags carry an epoch */
 	HIPCHK(hipMemset(L->d_sync, 0, L->sync_words * sizeof(uint32_t)), "hipMemset(sync)");
+	if (moe_prefill_supported(L->wtype, L->E, L->EI, L->NE)) {
+		size_t rows = (size_t)moe_prefill_max_tiles(P, L->NE) * moe_prefill_tile_rows();
+		HIPCHK(hipMalloc((void **)&L->d_rows, rows * sizeof(int)), "hipMalloc(rows)");
+		HIPCHK(hipMalloc((void **)&L->d_tile_e,
+				 (size_t)moe_prefill_max_tiles(P, L->NE) * sizeof(int)),
+		       "hipMalloc(tiles)");
+		HIPCHK(hipMalloc(&L->d_h16, rows * L->EI * 2), "hipMalloc(h16)");
+	}
 	L->cap_T = T;
 	return 1;
 fail:
@@ -284,6 +305,45 @@ int hip_moe_route_dev(hip_moe_layer *L, const float *d_x, size_t T,
 		     d_ids, d_w, pick_stream(L, stream));
 }
 
+/* the path a call of T tokens takes (HIP_MOE_PATH_*), 0 if none applies */
+static int choose_path(const hip_moe_layer *L, size_t T)
+{
+	int dec = L->fused_grid > 0 &&
+		  moe_fused_supported(L->wtype, L->E, L->EI, L->NE, T, L->topk);
+	int grp = moe_prefill_supported(L->wtype, L->E, L->EI, L->NE);
+	switch (L->path) {
+	case HIP_MOE_PATH_DECODE:
+		return dec ? HIP_MOE_PATH_DECODE : 0;
+	case HIP_MOE_PATH_GEMV:
+		return HIP_MOE_PATH_GEMV;
+	case HIP_MOE_PATH_GROUPED:
+		return grp ? HIP_MOE_PATH_GROUPED : 0;
+	default:
+		if (dec)
+			return HIP_MOE_PATH_DECODE;
+		if (grp && T * L->topk >= (size_t)MOE_GROUPED_MIN_PER_EXPERT * L->NE)
+			return HIP_MOE_PATH_GROUPED;
+		return HIP_MOE_PATH_GEMV;
+	}
+}
+
+int hip_moe_set_path(hip_moe_layer *L, int path)
+{
+	if (!L || path < HIP_MOE_PATH_AUTO || path > HIP_MOE_PATH_GROUPED) {
+		set_err("set_path: bad layer or path %d", path);
+		return 0;
+	}
+	L->path = path;
+	return 1;
+}
+
+int hip_moe_path_for(const hip_moe_layer *L, size_t T)
+{
+	if (!L || T == 0)
+		return 0;
+	return choose_path(L, T);
+}
+
 int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 		    const float *d_router_bias, uint32_t *d_ids_out, float *d_w_out,
 		    void *stream)
@@ -298,8 +358,13 @@ int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 	uint32_t *ids = d_ids_out ? d_ids_out : L->d_ids;
 	float *w = d_w_out ? d_w_out : L->d_w;
 	int P = (int)(T * L->topk);
+	int path = choose_path(L, T);
 
-	if (L->fused_grid > 0 && moe_fused_supported(L->wtype, L->E, L->EI, L->NE, T, L->topk)) {
+	if (!path) {
+		set_err("ffn: the requested path does not apply to this layer and T=%zu", T);
+		return 0;
+	}
+	if (path == HIP_MOE_PATH_DECODE) {
 		LCHK(moe_launch_fused(L->wtype, d_x, L->d_router, d_router_bias, L->d_gate,
 				      L->d_up, L->d_down, L->gu_stride, L->down_stride,
 				      ids, w, L->d_h, L->d_ypart, d_out, L->d_sync,
@@ -309,6 +374,15 @@ int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 	}
 	if (!route(L, d_x, T, d_router_bias, L->d_logits, NULL, ids, w, s))
 		return 0;
+	if (path == HIP_MOE_PATH_GROUPED) {
+		LCHK(moe_launch_prefill(L->wtype, d_x, L->d_gate, L->d_up, L->d_down,
+					L->gu_stride, L->down_stride, ids, L->d_rows,
+					L->d_tile_e, L->d_h16, L->d_ypart, (int)T, (int)L->topk,
+					(int)L->E, (int)L->EI, (int)L->NE, s), "grouped GEMMs");
+		LCHK(moe_launch_combine(L->d_ypart, w, d_out, (int)T, (int)L->topk, (int)L->E, 1,
+					s), "combine");
+		return 1;
+	}
 	LCHK(moe_launch_gateup(L->wtype, L->d_gate, L->d_up, L->gu_stride, ids, -1, d_x,
 			       L->d_h, P, (int)L->topk, (int)L->E, (int)L->EI, s),
 	     "gate/up");

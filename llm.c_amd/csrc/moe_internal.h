@@ -54,6 +54,18 @@ int moe_launch_combine(const float *ypart, const float *w, float *out, int T,
 int moe_launch_expf(const float *in, float *out, size_t n, void *stream);
 int moe_launch_copy(const void *src, void *dst, size_t bytes, void *stream);
 
+/* Grouped path (moe_prefill.hip): sort by expert + f16 MFMA GEMMs.  Taken by
+ * default when the pairs per expert average at least this many. */
+#define MOE_GROUPED_MIN_PER_EXPERT 4
+int moe_prefill_supported(int wtype, size_t E, size_t EI, size_t NE);
+int moe_prefill_max_tiles(size_t P, size_t NE);
+int moe_prefill_tile_rows(void);
+/* ypart[p][E] (no K-chunks) for every pair p; combine with kchunks = 1 */
+int moe_launch_prefill(int wtype, const float *x, const uint8_t *gate, const uint8_t *up,
+                       const uint8_t *down, size_t gu_stride, size_t dn_stride,
+                       const uint32_t *ids, int *rows, int *tile_e, void *h16, float *ypart,
+                       int T, int K, int E, int EI, int NE, void *stream);
+
 /* One-launch decode layer (moe_decode.hip) for T*K <= MOE_FUSED_MAX_P. */
 int moe_fused_supported(int wtype, size_t E, size_t EI, size_t NE, size_t T, size_t K);
 int moe_fused_kchunks(int wtype, size_t EI);

@@ -19,6 +19,8 @@ LIB_PATH = os.path.join(HERE, "libhip_moe.so")
 
 Q8_0 = 1
 Q4_0 = 2
+# execution paths (include/hip_moe.h)
+PATH_AUTO, PATH_DECODE, PATH_GEMV, PATH_GROUPED = 0, 1, 2, 3
 QK = 32
 
 _lib = None
@@ -61,6 +63,10 @@ def lib():
     L.hip_moe_expf_dev.restype = i32
     L.hip_moe_expf_dev.argtypes = [vp, vp, sz, vp]
     L.hip_moe_copy_dev.restype = i32
+    L.hip_moe_set_path.restype = i32
+    L.hip_moe_set_path.argtypes = [vp, i32]
+    L.hip_moe_path_for.restype = i32
+    L.hip_moe_path_for.argtypes = [vp, sz]
     L.hip_moe_copy_dev.argtypes = [vp, vp, sz, vp]
     # synthetic inputs
     L.moe_row_bytes.restype = sz
@@ -378,6 +384,14 @@ class MoeLayer:
 
     def weight_bytes(self) -> int:
         return lib().hip_moe_weight_bytes(self.h)
+
+    def set_path(self, path: int):
+        """Force PATH_DECODE / PATH_GEMV / PATH_GROUPED (PATH_AUTO restores)."""
+        if lib().hip_moe_set_path(self.h, path) != 1:
+            raise HipMoeError("hip_moe_set_path: " + last_error())
+
+    def path_for(self, T: int) -> int:
+        return lib().hip_moe_path_for(self.h, T)
 
     def free(self):
         if self.h:

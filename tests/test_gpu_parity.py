@@ -5,8 +5,9 @@ Bars:
   * expert ids, routing weights, router logits, softmax probabilities:
     bit-exact (the reference's AVX2 build, tests/golden/);
   * layer outputs: relative L2 <= 1e-3 against the reference CPU path
-    (REL_L2_TOL); the fp32 kernels land near 1e-6, so the tests also assert
-    a tighter 2e-5 to catch regressions early;
+    (REL_L2_TOL); the fp32 paths (decode, GEMV) land near 1e-6, so their
+    tests also assert a tighter 2e-5 to catch regressions early; the grouped
+    path (f16 MFMA operands) lands near 5e-4 and is held to 1e-3;
   * the device expf: bit-exact with the host's glibc expf on every float in
     [-104, 0] and on a stride over all floats.
 """
@@ -186,22 +187,44 @@ def test_gpu_moe_layer_vs_reference_golden(cfg):
     err = rel_l2(out, g["out"])
     say(f"moe layer golden {cfg}: rel L2 {err:.3e}")
     assert err <= REL_L2_TOL and err <= TIGHT
+    lay.set_path(hipmoe.PATH_GROUPED)
+    try:
+        gout, gids, gw = lay.ffn(x, layer(cfg)["bias"])
+    finally:
+        lay.set_path(hipmoe.PATH_AUTO)
+    gerr = rel_l2(gout, g["out"])
+    say(f"moe layer golden {cfg} [grouped]: rel L2 {gerr:.3e}")
+    assert np.array_equal(gids, ids) and np.array_equal(bits(gw), bits(w))
+    assert gerr <= REL_L2_TOL
 
 
-def _check_layer_vs_oracle(cfg, T, call, per_token=True):
+PATH_NAMES = {hipmoe.PATH_DECODE: "decode", hipmoe.PATH_GEMV: "gemv",
+              hipmoe.PATH_GROUPED: "grouped"}
+
+
+def _check_layer_vs_oracle(cfg, T, call, per_token=True, path=hipmoe.PATH_AUTO,
+                           expect_path=None):
     wt, E, EI, NE, K, renorm, bias_std = CONFIGS[cfg]
     lay = gpu_layer(cfg)
     lw = layer(cfg)
     x = hipmoe.synth_input(SEED, call, T, E)
-    out, ids, w = lay.ffn(x, lw["bias"])
+    lay.set_path(path)
+    try:
+        taken = lay.path_for(T)
+        if expect_path is not None:
+            assert taken == expect_path
+        out, ids, w = lay.ffn(x, lw["bias"])
+    finally:
+        lay.set_path(hipmoe.PATH_AUTO)
     oout, oids, ow, _, _ = oracle.moe_ffn(x, lw, K, bool(renorm), lw["bias"])
     assert np.array_equal(ids, oids)
     assert np.array_equal(bits(w), bits(ow))
     err = rel_l2(out, oout)
     worst = max(rel_l2(out[t], oout[t]) for t in range(T)) if per_token else err
-    say(f"{cfg} T={T}: rel L2 {err:.3e}, worst token {worst:.3e}")
+    say(f"{cfg} T={T} [{PATH_NAMES[taken]}]: rel L2 {err:.3e}, worst token {worst:.3e}")
     assert err <= REL_L2_TOL and worst <= REL_L2_TOL
-    assert err <= TIGHT
+    if taken != hipmoe.PATH_GROUPED:
+        assert err <= TIGHT
     return out
 
 
@@ -218,14 +241,85 @@ def test_gpu_olmoe_q8_batch():
 
 def test_gpu_olmoe_q4_skew_prefill_512():
     say("olmoe_q4_skew prefill T=512")
-    _check_layer_vs_oracle("olmoe_q4_skew", 512, 300)
+    _check_layer_vs_oracle("olmoe_q4_skew", 512, 300, expect_path=hipmoe.PATH_GROUPED)
 
 
 def test_gpu_mixtral_q4_decode_and_64():
     say("mixtral_q4 T=1")
     _check_layer_vs_oracle("mixtral_q4", 1, 400)
     say("mixtral_q4 T=64")
-    _check_layer_vs_oracle("mixtral_q4", 64, 401)
+    _check_layer_vs_oracle("mixtral_q4", 64, 401, expect_path=hipmoe.PATH_GROUPED)
+
+
+# --------------------------------------------------------------------------
+# the grouped path (sort by expert + f16 MFMA GEMMs)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("cfg,T", [("olmoe_q8", 1), ("olmoe_q8", 3), ("olmoe_q8", 130),
+                                   ("olmoe_q4_skew", 40), ("mixtral_q4", 5)])
+def test_gpu_grouped_forced_small_and_ragged(cfg, T):
+    """Heavy padding (1..few rows per expert tile), ragged tile tails,
+    duplicated expert-0 slots (top_k quirk) all go through the sort."""
+    say(f"grouped path forced: {cfg} T={T}")
+    _check_layer_vs_oracle(cfg, T, 700 + T, path=hipmoe.PATH_GROUPED,
+                           expect_path=hipmoe.PATH_GROUPED)
+
+
+def test_gpu_grouped_q8_prefill_512():
+    say("olmoe_q8 prefill T=512 (grouped, Q8_0)")
+    _check_layer_vs_oracle("olmoe_q8", 512, 710, expect_path=hipmoe.PATH_GROUPED)
+
+
+def test_gpu_grouped_full_tiles():
+    """Every token picks the same experts, so each expert's row count is an
+    exact multiple of the 64-row tile (no padding rows)."""
+    say("grouped path, identical tokens: full tiles")
+    cfg = "olmoe_q8"
+    wt, E, EI, NE, K, renorm, bias_std = CONFIGS[cfg]
+    lay = gpu_layer(cfg)
+    lw = layer(cfg)
+    x = np.repeat(hipmoe.synth_input(SEED, 720, 1, E), 128, axis=0)
+    lay.set_path(hipmoe.PATH_GROUPED)
+    try:
+        out, ids, w = lay.ffn(x)
+    finally:
+        lay.set_path(hipmoe.PATH_AUTO)
+    o1, i1, w1, _, _ = oracle.moe_ffn(x[:1], lw, K, False, None)
+    assert (ids == i1[0]).all() and (bits(w) == bits(w1[0])).all()
+    for t in (0, 63, 64, 127):
+        assert rel_l2(out[t], o1[0]) <= REL_L2_TOL
+    assert np.array_equal(bits(out), bits(np.repeat(out[:1], 128, axis=0)))
+
+
+def test_gpu_grouped_deterministic_and_permutation():
+    say("grouped path: determinism + token permutation (olmoe_q4_skew, T=256)")
+    lay = gpu_layer("olmoe_q4_skew")
+    lw = layer("olmoe_q4_skew")
+    x = hipmoe.synth_input(SEED, 730, 256, 2048)
+    assert lay.path_for(256) == hipmoe.PATH_GROUPED
+    a, ia, wa = lay.ffn(x, lw["bias"])
+    b, ib, wb = lay.ffn(x, lw["bias"])
+    assert np.array_equal(bits(a), bits(b))
+    perm = np.random.default_rng(5).permutation(256)
+    c, ic, wc = lay.ffn(x[perm], lw["bias"])
+    assert np.array_equal(ic, ia[perm])
+    # a row's MFMA sums do not depend on the rows sharing its tile
+    assert np.array_equal(bits(c), bits(a[perm]))
+
+
+def test_gpu_grouped_vs_gemv_paths():
+    say("grouped vs GEMV path (mixtral_q4, T=16)")
+    lay = gpu_layer("mixtral_q4")
+    x = hipmoe.synth_input(SEED, 740, 16, 4096)
+    lay.set_path(hipmoe.PATH_GEMV)
+    try:
+        g, ig, wg = lay.ffn(x)
+        lay.set_path(hipmoe.PATH_GROUPED)
+        m, im, wm = lay.ffn(x)
+    finally:
+        lay.set_path(hipmoe.PATH_AUTO)
+    assert np.array_equal(ig, im) and np.array_equal(bits(wg), bits(wm))
+    assert rel_l2(m, g) <= REL_L2_TOL
 
 
 # --------------------------------------------------------------------------
