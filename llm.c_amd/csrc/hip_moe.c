@@ -245,13 +245,19 @@ static int ensure_scratch(hip_moe_layer *L, size_t T)
 	HIPCHK(hipMalloc((void **)&L->d_ids, P * sizeof(uint32_t)), "hipMalloc(ids)");
 	HIPCHK(hipMalloc((void **)&L->d_w, P * sizeof(float)), "hipMalloc(w)");
 	HIPCHK(hipMalloc((void **)&L->d_h, P * L->EI * sizeof(float)), "hipMalloc(h)");
-	HIPCHK(hipMalloc((void **)&L->d_ypart, P * L->kchunks * L->E * sizeof(float)),
+	/* fp32 partials of the GEMV and grouped paths, or epoch-tagged 64-bit
+	 * partials of the decode kernel */
+	HIPCHK(hipMalloc((void **)&L->d_ypart, P * L->kchunks * L->E * sizeof(uint64_t)),
 	       "hipMalloc(ypart)");
 	L->sync_words = moe_fused_sync_words(L->wtype, T, L->topk, L->E, L->EI, L->NE,
 					     L->fused_grid > 0 ? L->fused_grid : 1);
 	HIPCHK(hipMalloc((void **)&L->d_sync, L->sync_words * sizeof(uint32_t)), "hipMalloc(sync)");
-	/* zeroed once here; the decode kernel's flags carry an epoch */
+	/* zeroed once here: the decode kernel's flags and its partials carry an
+	 * epoch that starts at 1, and reused device memory may hold tags of an
+	 * earlier layer */
 	HIPCHK(hipMemset(L->d_sync, 0, L->sync_words * sizeof(uint32_t)), "hipMemset(sync)");
+	HIPCHK(hipMemset(L->d_ypart, 0, P * L->kchunks * L->E * sizeof(uint64_t)),
+	       "hipMemset(ypart)");
 	if (moe_prefill_supported(L->wtype, L->E, L->EI, L->NE)) {
 		size_t rows = (size_t)moe_prefill_max_tiles(P, L->NE) * moe_prefill_tile_rows();
 		HIPCHK(hipMalloc((void **)&L->d_rows, rows * sizeof(int)), "hipMalloc(rows)");
@@ -474,6 +480,8 @@ int hip_moe_ffn(hip_moe_layer *L, const float *x, float *out, size_t T,
 				 hipMemcpyDeviceToHost), "read error word");
 		if (err) { /* flags may be left mid-flight: restart the epoch at zero */
 			hipMemset(L->d_sync, 0, L->sync_words * sizeof(uint32_t));
+			hipMemset(L->d_ypart, 0, L->cap_T * L->topk * L->kchunks * L->E *
+						 sizeof(uint64_t));
 			set_err("persistent kernel: a dependency wait timed out");
 			return 0;
 		}

@@ -7,19 +7,22 @@
  *     with the 8-lane FMA chains of dot_f32_f32 (matmul.c:91-105), fed from
  *     LDS-transposed copies of router row j and the token, and writes it into
  *     NREP replicas of the logit table, each entry tagged with this launch's
- *     epoch.  Every workgroup then polls its own replica until all NE*T
- *     entries carry the epoch and runs softmax + top-k (+ renorm) itself
- *     (nn.c:221-308, llama.c:422-427): no second hop, no hot line.
+ *     epoch.  Every workgroup then polls its own replica (lane j of a wave
+ *     polls expert j of a token; the loads that see the epoch deliver the
+ *     logits) and runs softmax + top-k (+ renorm) itself (nn.c:221-308,
+ *     llama.c:422-427): no second hop, no hot line.
  *  2. expert items, statically assigned: item i runs on workgroup i % G, in
- *     increasing i.  Items are gate/up tiles (16 rows of gate and up of the
- *     expert in slot p: h[p][row] = silu(gate.x) * (up.x), nn.c:460-478), then
- *     down tiles (32 rows of down over one K-chunk of h[p], nn.c:490-492).
- *     A down tile issues its weight loads, then waits for the gate/up tiles
- *     covering its K-chunk.  The workgroup holding the last down tile of a
- *     (token, row block) waits for the others and combines the slots in
- *     order: out += y / (1/w)  (olmoe.c:401-403).
- *  3. exit.  Each workgroup raises its exit flag; workgroup 0 waits for all
- *     of them and advances the epoch for the next launch.
+ *     increasing i.  Items are gate/up tiles (8 rows of gate and up of the
+ *     expert in slot p: h[p][row] = silu(gate.x) * (up.x), nn.c:460-478), each
+ *     ending with its tile flag, then down tiles (16 rows of down over one
+ *     K-chunk of h[p], nn.c:490-492).  A down tile issues its weight loads,
+ *     then waits for the flags of the gate/up tiles covering its K-chunk.
+ *     The workgroup holding the last down tile of a (token, row block) waits
+ *     for the others and combines the slots in order: out += y / (1/w)
+ *     (olmoe.c:401-403).
+ *  3. epoch.  Each workgroup raises a start flag once it has read the epoch
+ *     word; workgroup 0, when done with its items, checks them and advances
+ *     the epoch for the next launch (which starts after this one drains).
  *
  * Synchronisation uses no read-modify-write: same-address device atomics
  * serialise (~0.1 us each), so producers write epoch-tagged flags (one word
@@ -62,7 +65,7 @@ struct DecodeArgs {
 	u32 *sync;
 	int T, E, EI, NE, K, renorm, kch;
 	int n_gu, n_dn;
-	int off_exit, off_rep, off_hf, off_ready, off_yf;
+	int off_start, off_rep, off_hf;
 	int rep_stride; /* u64 entries between replicas (a multiple of 512: 4 KB) */
 };
 
@@ -233,45 +236,54 @@ __device__ static inline void stage_transposed(float *dst, const float *src, int
 }
 
 /* acc = fma(x[k], w[k], acc) over k = 0, 8, 16, ... of one transposed row
- * pair (E8 floats each); LDS reads double-buffered ahead of the chain */
+ * pair (E8 floats each).  The chain is 256 dependent FMAs for E = 2048, so
+ * its LDS operands are fetched two batches (of 16 FMAs) ahead. */
+struct chain_batch {
+	float4 x[4], w[4];
+	__device__ inline void load(const float4 *xr, const float4 *wr, int b)
+	{
+#pragma unroll
+		for (int u = 0; u < 4; u++) {
+			x[u] = xr[4 * b + u];
+			w[u] = wr[4 * b + u];
+		}
+	}
+	__device__ inline float run(float acc) const
+	{
+#pragma unroll
+		for (int u = 0; u < 4; u++) {
+			acc = __builtin_fmaf(x[u].x, w[u].x, acc);
+			acc = __builtin_fmaf(x[u].y, w[u].y, acc);
+			acc = __builtin_fmaf(x[u].z, w[u].z, acc);
+			acc = __builtin_fmaf(x[u].w, w[u].w, acc);
+		}
+		return acc;
+	}
+};
+
 __device__ static inline float router_chain(const float *xrow, const float *wrow, int E8)
 {
 	const float4 *xr = (const float4 *)xrow, *wr = (const float4 *)wrow;
-	float4 xa[4], wa[4], xb[4], wb[4];
+	const int nb = E8 / 16; /* batches of 16 FMAs */
+	chain_batch A, B, C;
 	float acc = 0.0f;
-	const int nb = E8 / 16; /* batches of 4 float4 pairs; even */
-#pragma unroll
-	for (int u = 0; u < 4; u++) {
-		xa[u] = xr[u];
-		wa[u] = wr[u];
-	}
-	for (int b = 0; b < nb; b += 2) {
-#pragma unroll
-		for (int u = 0; u < 4; u++) {
-			xb[u] = xr[4 * (b + 1) + u];
-			wb[u] = wr[4 * (b + 1) + u];
-		}
-#pragma unroll
-		for (int u = 0; u < 4; u++) {
-			acc = __builtin_fmaf(xa[u].x, wa[u].x, acc);
-			acc = __builtin_fmaf(xa[u].y, wa[u].y, acc);
-			acc = __builtin_fmaf(xa[u].z, wa[u].z, acc);
-			acc = __builtin_fmaf(xa[u].w, wa[u].w, acc);
-		}
-		if (b + 2 < nb) {
-#pragma unroll
-			for (int u = 0; u < 4; u++) {
-				xa[u] = xr[4 * (b + 2) + u];
-				wa[u] = wr[4 * (b + 2) + u];
-			}
-		}
-#pragma unroll
-		for (int u = 0; u < 4; u++) {
-			acc = __builtin_fmaf(xb[u].x, wb[u].x, acc);
-			acc = __builtin_fmaf(xb[u].y, wb[u].y, acc);
-			acc = __builtin_fmaf(xb[u].z, wb[u].z, acc);
-			acc = __builtin_fmaf(xb[u].w, wb[u].w, acc);
-		}
+	A.load(xr, wr, 0);
+	if (nb > 1)
+		B.load(xr, wr, 1);
+	for (int b = 0; b < nb; b += 3) {
+		if (b + 2 < nb)
+			C.load(xr, wr, b + 2);
+		acc = A.run(acc);
+		if (b + 1 >= nb)
+			break;
+		if (b + 3 < nb)
+			A.load(xr, wr, b + 3);
+		acc = B.run(acc);
+		if (b + 2 >= nb)
+			break;
+		if (b + 4 < nb)
+			B.load(xr, wr, b + 4);
+		acc = C.run(acc);
 	}
 	return acc;
 }
@@ -312,52 +324,40 @@ __device__ static void router_row(const DecodeArgs &a, int j, u32 prev_epoch, fl
 	}
 }
 
-/* wait for this workgroup's replica, then softmax/top-k of every token into
- * LDS: s_ids/s_w [T*K] */
+/*
+ * Routing of every token from this workgroup's replica: wave w takes tokens
+ * w, w+4, ...; lane j polls entry (t, j) until the whole row carries the
+ * epoch (one hop: the loads that see the epoch also deliver the logits), then
+ * the wave runs softmax + top-k (+ renorm) into s_ids/s_w [T*K].
+ */
 __device__ static void route_local(const DecodeArgs &a, u32 epoch, float *lds, u32 *s_ids,
 				   float *s_w, const uint64_t *s_tab)
 {
 	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-	const int n = a.T * a.NE;
 	const uint64_t *rep = (const uint64_t *)(a.sync + a.off_rep) +
 			      (size_t)(blockIdx.x % NREP) * a.rep_stride;
-	float *slg = lds; /* [T][NE] logits */
-	__shared__ int s_ok;
-	int step = 0;
-	/* one word first: the last router row, usually the last to land */
-	if (threadIdx.x == 0)
-		for (int i = 0; i < SPIN_LIMIT && (u32)(ld_dev_u64(&rep[n - 1]) >> 32) != epoch; i++)
+	float *scr = lds + wave * (MOE_MAX_NE + 2 * MOE_MAX_TOPK);
+	for (int t = wave; t < a.T; t += NTHREADS / WAVE) { /* NE <= 64: one expert per lane */
+		const uint64_t *row = rep + (size_t)t * a.NE;
+		float logit = 0.0f;
+		int step = 0;
+		for (int round = 0;; round++) {
+			const uint64_t v = lane < a.NE ? ld_dev_u64(&row[lane]) : (uint64_t)epoch << 32;
+			if (__all((u32)(v >> 32) == epoch)) {
+				logit = __builtin_bit_cast(float, (u32)v);
+				break;
+			}
+			if (round >= SPIN_LIMIT) {
+				if (lane == 0)
+					st_dev_u32(a.sync + MOE_SYNC_ERR_WORD, 1u);
+				break;
+			}
 			backoff(step);
-	__syncthreads();
-	step = 0;
-	for (int round = 0;; round++) {
-		bool ok = true;
-		for (int i = threadIdx.x; i < n; i += NTHREADS) {
-			uint64_t v = ld_dev_u64(&rep[i]);
-			ok &= (u32)(v >> 32) == epoch;
-			slg[i] = __builtin_bit_cast(float, (u32)v);
 		}
-		if (threadIdx.x == 0)
-			s_ok = 1;
-		__syncthreads();
-		if (!ok)
-			s_ok = 0;
-		__syncthreads();
-		if (s_ok)
-			break;
-		if (round >= SPIN_LIMIT) {
-			if (threadIdx.x == 0)
-				st_dev_u32(a.sync + MOE_SYNC_ERR_WORD, 1u);
-			break;
-		}
-		backoff(step);
-		__syncthreads();
+		wave_softmax_topk64(logit, s_ids + t * a.K, s_w + t * a.K, a.NE, a.K, a.renorm, s_tab,
+				    scr, (u32 *)(scr + MOE_MAX_NE), scr + MOE_MAX_NE + MOE_MAX_TOPK,
+				    lane);
 	}
-	float *scr = lds + ((a.T * a.NE + 15) & ~15) + wave * (MOE_MAX_NE + 2 * MOE_MAX_TOPK);
-	for (int t = wave; t < a.T; t += NTHREADS / WAVE) /* NE <= 64: one expert per lane */
-		wave_softmax_topk64(lane < a.NE ? slg[t * a.NE + lane] : 0.0f, s_ids + t * a.K,
-				    s_w + t * a.K, a.NE, a.K, a.renorm, s_tab, scr,
-				    (u32 *)(scr + MOE_MAX_NE), scr + MOE_MAX_NE + MOE_MAX_TOPK, lane);
 	__syncthreads();
 }
 
@@ -391,10 +391,9 @@ __device__ static inline void down_load(const DecodeArgs &a, int d, const u32 *s
 }
 
 /*
- * Gate/up tile g: h[p][rows] = silu(gate.x) * (up.x).  If pre_d >= 0 the
- * weight loads of down item pre_d are issued right after this tile's own.
- * The last tile of a K-chunk of h[p] (in item order) waits for the chunk's
- * other tiles and raises the chunk's single ready word.
+ * Gate/up tile g: h[p][rows] = silu(gate.x) * (up.x), then the tile's flag.
+ * If pre_d >= 0 the weight loads of down item pre_d are issued after the
+ * flag, to land while this workgroup waits for h.
  */
 template <int WT, int CG, int CD>
 __device__ static void gateup_item(const DecodeArgs &a, int g, const u32 *s_ids, float *sx,
@@ -403,7 +402,6 @@ __device__ static void gateup_item(const DecodeArgs &a, int g, const u32 *s_ids,
 {
 	typedef segq<WT> S;
 	constexpr int RPS = WAVE / CG, RW = GU_ROWS / 4, NS = RW / RPS;
-	constexpr int TPC = down_geo<WT, CD>::CHUNK / GU_ROWS; /* tiles per K-chunk */
 	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
 	const int tiles = a.EI / GU_ROWS;
 	const int p = g / tiles, tile = g % tiles;
@@ -422,8 +420,6 @@ __device__ static void gateup_item(const DecodeArgs &a, int g, const u32 *s_ids,
 		load_dwords<S::DW>(G + ro, dg[s2]);
 		load_dwords<S::DW>(U + ro, du[s2]);
 	}
-	if (pre_d >= 0)
-		down_load<WT, CD>(a, pre_d, s_ids, dd);
 	if (staged != t) {
 		__syncthreads(); /* earlier readers of sx are done */
 		stage_seg<S::COLS>(sx, a.x + (size_t)t * a.E, a.E);
@@ -443,19 +439,16 @@ __device__ static void gateup_item(const DecodeArgs &a, int g, const u32 *s_ids,
 	}
 	__builtin_amdgcn_s_waitcnt(0);
 	__syncthreads();
-	u32 *hf = a.sync + a.off_hf + (size_t)p * tiles;
 	if (threadIdx.x == 0)
-		st_dev_u32(&hf[tile], epoch);
-	if ((tile + 1) % TPC)
-		return;
-	const int kc = tile / TPC;
-	wait_flags(hf + kc * TPC, TPC - 1, epoch, a.sync + MOE_SYNC_ERR_WORD);
-	if (threadIdx.x == 0)
-		st_dev_u32(a.sync + a.off_ready + (size_t)p * a.kch + kc, epoch);
+		st_dev_u32(a.sync + a.off_hf + (size_t)p * tiles + tile, epoch);
+	/* the next down item's weights: issued only now, so they do not compete
+	 * with the gate/up streams everyone is waiting for */
+	if (pre_d >= 0)
+		down_load<WT, CD>(a, pre_d, s_ids, dd);
 }
 
-/* down item d with its weights already in dd: wait for its K-chunk of h[p],
- * write partial y; the last contribution (in item order) of a (token, row
+/* down item d with its weights already in dd: wait for the gate/up tiles of
+ * its K-chunk of h[p], write partial y; the last contribution (in item order) of a (token, row
  * block) waits for the others and combines the slots in order */
 template <int WT, int CD>
 __device__ static void down_item(const DecodeArgs &a, int d, const float *s_w, float *sh,
@@ -463,6 +456,7 @@ __device__ static void down_item(const DecodeArgs &a, int d, const float *s_w, f
 {
 	typedef segq<WT> S;
 	typedef down_geo<WT, CD> DG;
+	constexpr int TPC = DG::CHUNK / GU_ROWS; /* gate/up tiles per K-chunk */
 	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
 	const int nrb = a.E / DN_ROWS;
 	const int p = d / (a.kch * nrb), rem = d % (a.kch * nrb);
@@ -470,40 +464,77 @@ __device__ static void down_item(const DecodeArgs &a, int d, const float *s_w, f
 	const int t = p / a.K, slot = p % a.K;
 	const int row0 = rbk * DN_ROWS + wave * DG::RW;
 	const int seg = lane % CD, sub = lane / CD;
+	const int ncontrib = a.K * a.kch, own = slot * a.kch + kc;
+	const bool combiner = slot == a.K - 1 && kc == a.kch - 1;
+	__shared__ float s_y[DN_ROWS];
 
-	wait_flags(a.sync + a.off_ready + (size_t)p * a.kch + kc, 1, epoch,
+	wait_flags(a.sync + a.off_hf + (size_t)p * (a.EI / GU_ROWS) + (size_t)kc * TPC, TPC, epoch,
 		   a.sync + MOE_SYNC_ERR_WORD);
 	stage_seg_dev<S::COLS>(sh, a.h + (size_t)p * a.EI + (size_t)kc * DG::CHUNK, DG::CHUNK);
 	__syncthreads();
 	float xr[S::COLS];
 	lds_seg<S::COLS>(sh, seg, xr);
+	/* partial y of (token, row block), contribution (slot, kc), tagged with
+	 * the epoch so the combiner can poll the data itself */
+	uint64_t *yq = (uint64_t *)a.ypart + ((size_t)t * nrb + rbk) * ncontrib * DN_ROWS;
 #pragma unroll
 	for (int s2 = 0; s2 < DG::NS; s2++) {
-		const int row = row0 + s2 * DG::RPS + sub;
-		float y = group_sum<CD>(S::dot(dd[s2], xr, kc * CD + seg));
-		if (seg == 0)
-			st_dev(&a.ypart[((size_t)p * a.kch + kc) * a.E + row], y);
+		const int r = wave * DG::RW + s2 * DG::RPS + sub;
+		const float y = group_sum<CD>(S::dot(dd[s2], xr, kc * CD + seg));
+		if (seg == 0) {
+			if (combiner)
+				s_y[r] = y;
+			else
+				st_dev_u64(&yq[(size_t)own * DN_ROWS + r],
+					   ((uint64_t)epoch << 32) | __builtin_bit_cast(u32, y));
+		}
 	}
-	__builtin_amdgcn_s_waitcnt(0);
-	__syncthreads();
-	const int ncontrib = a.K * a.kch;
-	u32 *yf = a.sync + a.off_yf + ((size_t)t * nrb + rbk) * ncontrib;
-	if (threadIdx.x == 0)
-		st_dev_u32(&yf[slot * a.kch + kc], epoch);
-	if (slot != a.K - 1 || kc != a.kch - 1)
+	if (!combiner)
 		return;
-	wait_flags(yf, ncontrib - 1, epoch, a.sync + MOE_SYNC_ERR_WORD);
+	/* the combiner: collect the other contributions, then add the slots in
+	 * order, y = sum of its K-chunks in order, out += y / (1/w) */
+	float *sc = sh; /* [ncontrib][DN_ROWS], once every wave is done reading h */
+	const int n = ncontrib * DN_ROWS;
+	__shared__ int s_ok;
+	int step = 0;
+	__syncthreads();
+	for (int round = 0;; round++) {
+		bool ok = true;
+		for (int i = threadIdx.x; i < n; i += NTHREADS) {
+			if (i / DN_ROWS == own)
+				continue;
+			const uint64_t v = ld_dev_u64(&yq[i]);
+			ok &= (u32)(v >> 32) == epoch;
+			sc[i] = __builtin_bit_cast(float, (u32)v);
+		}
+		if (threadIdx.x == 0)
+			s_ok = 1;
+		__syncthreads();
+		if (!ok)
+			s_ok = 0;
+		__syncthreads();
+		if (s_ok)
+			break;
+		if (round >= SPIN_LIMIT) {
+			if (threadIdx.x == 0)
+				st_dev_u32(a.sync + MOE_SYNC_ERR_WORD, 1u);
+			break;
+		}
+		backoff(step);
+		__syncthreads();
+	}
 	if (threadIdx.x < DN_ROWS) {
-		const int row = rbk * DN_ROWS + threadIdx.x;
+		const int r = threadIdx.x;
+		sc[own * DN_ROWS + r] = s_y[r];
 		float acc = 0.0f;
 		for (int s = 0; s < a.K; s++) {
 			const size_t ps = (size_t)t * a.K + s;
-			float y = ld_dev(&a.ypart[ps * a.kch * a.E + row]);
+			float y = sc[(s * a.kch) * DN_ROWS + r];
 			for (int c = 1; c < a.kch; c++)
-				y += ld_dev(&a.ypart[(ps * a.kch + c) * a.E + row]);
+				y += sc[(s * a.kch + c) * DN_ROWS + r];
 			acc = acc + y / (1.0f / s_w[ps]);
 		}
-		a.out[(size_t)t * a.E + row] = acc;
+		a.out[(size_t)t * a.E + rbk * DN_ROWS + r] = acc;
 	}
 }
 
@@ -531,6 +562,11 @@ void k_moe_decode(DecodeArgs a)
 		s_epoch = prev_epoch + 1;
 	__syncthreads();
 	const u32 epoch = s_epoch;
+	/* this workgroup has read the epoch word: workgroup 0 may advance it
+	 * once every workgroup has said so */
+	u32 *startf = a.sync + a.off_start;
+	if (threadIdx.x == 0 && blockIdx.x != 0)
+		st_dev_u32(&startf[blockIdx.x], epoch);
 	route_local(a, epoch, lds, s_ids, s_w, s_tab);
 	if (blockIdx.x == 0)
 		for (int i = threadIdx.x; i < a.T * a.K; i += NTHREADS) {
@@ -560,14 +596,12 @@ void k_moe_decode(DecodeArgs a)
 		__syncthreads();
 	}
 
-	/* exit: workgroup 0 advances the epoch once every workgroup is out */
-	u32 *exitf = a.sync + a.off_exit;
-	if (blockIdx.x != 0) {
-		if (threadIdx.x == 0)
-			st_dev_u32(&exitf[blockIdx.x], epoch);
+	/* workgroup 0 advances the epoch for the next launch once every
+	 * workgroup has read it (they did so long ago: no wait in practice);
+	 * the next launch starts only after this one has drained */
+	if (blockIdx.x != 0)
 		return;
-	}
-	wait_flags(exitf + 1, (int)gridDim.x - 1, epoch, a.sync + MOE_SYNC_ERR_WORD);
+	wait_flags(startf + 1, (int)gridDim.x - 1, epoch, a.sync + MOE_SYNC_ERR_WORD);
 	if (threadIdx.x == 0)
 		st_dev_u32(a.sync, epoch);
 }
@@ -640,7 +674,7 @@ static size_t decode_lds_bytes(int wtype, size_t E, size_t EI, size_t T, size_t 
 }
 
 struct SyncLayout {
-	size_t off_exit, off_rep, off_hf, off_ready, off_yf, words, rep_stride;
+	size_t off_start, off_rep, off_hf, words, rep_stride;
 };
 
 static SyncLayout sync_layout(int wtype, size_t T, size_t K, size_t E, size_t EI, size_t NE,
@@ -649,12 +683,10 @@ static SyncLayout sync_layout(int wtype, size_t T, size_t K, size_t E, size_t EI
 	Geo g = geometry(wtype, E, EI);
 	SyncLayout s;
 	s.rep_stride = (T * NE + 511) & ~(size_t)511;
-	s.off_exit = 1024;
-	s.off_rep = s.off_exit + (((size_t)grid + 1023) & ~(size_t)1023);
+	s.off_start = 1024;
+	s.off_rep = s.off_start + (((size_t)grid + 1023) & ~(size_t)1023);
 	s.off_hf = s.off_rep + (size_t)NREP * s.rep_stride * 2;
-	s.off_ready = s.off_hf + T * K * (EI / GU_ROWS);
-	s.off_yf = s.off_ready + T * K * (size_t)g.kch;
-	s.words = s.off_yf + T * (E / DN_ROWS) * K * (size_t)g.kch;
+	s.words = s.off_hf + T * K * (EI / GU_ROWS);
 	return s;
 }
 
@@ -664,7 +696,11 @@ extern "C" int moe_fused_supported(int wtype, size_t E, size_t EI, size_t NE, si
 	if (NE > WAVE || T * K > MOE_FUSED_MAX_P || E % DN_ROWS || EI % GU_ROWS || E % 256 ||
 	    EI % 256)
 		return 0;
-	return geometry(wtype, E, EI).fn != NULL;
+	Geo g = geometry(wtype, E, EI);
+	/* the combiner gathers K * kch contributions of DN_ROWS rows in the h chunk's LDS */
+	if (K * (size_t)g.kch * DN_ROWS > (size_t)g.CD * (size_t)(seg_cols(wtype) + 4))
+		return 0;
+	return g.fn != NULL;
 }
 
 extern "C" int moe_fused_kchunks(int wtype, size_t EI)
@@ -733,11 +769,9 @@ extern "C" int moe_launch_fused(int wtype, const float *x, const float *router,
 	a.kch = g.kch;
 	a.n_gu = T * K * (EI / GU_ROWS);
 	a.n_dn = T * K * g.kch * (E / DN_ROWS);
-	a.off_exit = (int)sl.off_exit;
+	a.off_start = (int)sl.off_start;
 	a.off_rep = (int)sl.off_rep;
 	a.off_hf = (int)sl.off_hf;
-	a.off_ready = (int)sl.off_ready;
-	a.off_yf = (int)sl.off_yf;
 	a.rep_stride = (int)sl.rep_stride;
 	void *args[] = {&a};
 	hipError_t rc = hipLaunchKernel(g.fn, dim3(grid), dim3(NTHREADS), args,

@@ -327,22 +327,47 @@ __device__ static inline void wave_softmax_topk(const float *logits, float *prob
 	}
 }
 
+/* DPP lane moves (VALU, no LDS round trip).  Controls: quad_perm [1,0,3,2]
+ * = 0xb1, [2,3,0,1] = 0x4e, row_shl:n = 0x100 + n, row_mirror = 0x140,
+ * row_half_mirror = 0x141.  Lanes whose source falls outside their row of 16
+ * read 0. */
+template <int CTRL>
+__device__ static inline float dpp_f32(float v)
+{
+	return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+								     CTRL, 0xf, 0xf, false));
+}
+
+__device__ static inline float lane_f32(float v, int l)
+{
+	return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+/* max over the wave, in every lane (max is exact, so any order) */
+__device__ static inline float wave_max_f32(float v)
+{
+	v = fmaxf(v, dpp_f32<0xb1>(v));  /* lane ^ 1 */
+	v = fmaxf(v, dpp_f32<0x4e>(v));  /* lane ^ 2 */
+	v = fmaxf(v, dpp_f32<0x141>(v)); /* the other quad of the 8 */
+	v = fmaxf(v, dpp_f32<0x140>(v)); /* the other 8 of the row */
+	return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
+}
+
 /*
  * wave_softmax_topk for NE <= 64: element i lives in lane i.  Same arithmetic
- * and order as wave_softmax_topk; the lane sums fetch their eight inputs with
- * independent shuffles and the ranks come from broadcast LDS reads of integer
- * keys.  tab is the exp table (an LDS copy), sp 128 floats of this wave's LDS
- * (8-byte aligned), ids/w receive the k slots (LDS or global).
+ * and order as wave_softmax_topk: max, e = expf(x - max), lane sums
+ * s_l = e_l + e_{l+8} + ... in order, the tree ((s0+s4)+(s2+s6)) +
+ * ((s1+s5)+(s3+s7)) (vector_avx2.h:126-132), the scalar tail, p = e / sum.
+ * The ranks come from broadcast LDS reads of integer keys.  tab is the exp
+ * table (an LDS copy), sp 128 floats of this wave's LDS (8-byte aligned),
+ * ids/w receive the k slots (LDS or global).
  */
 __device__ static inline void wave_softmax_topk64(float logit, u32 *ids, float *wout, int NE,
 						  int K, int renorm, const uint64_t *tab,
 						  float *sp, u32 *sid, float *sw, int lane)
 {
 	const bool valid = lane < NE;
-	float mx = valid ? logit : -__builtin_inff();
-#pragma unroll
-	for (int off = 32; off >= 1; off >>= 1)
-		mx = fmaxf(mx, __shfl_xor(mx, off, WAVE));
+	const float mx = wave_max_f32(valid ? logit : -__builtin_inff());
 	const float e = valid ? moe_expf_tab(logit - mx, tab) : 0.0f;
 
 	const int nv = NE - NE % 8;
@@ -355,12 +380,12 @@ __device__ static inline void wave_softmax_topk64(float logit, u32 *ids, float *
 	for (int c = 0; c < 8; c++)
 		if (8 * c < nv)
 			s = s + g[c];
-	s = s + __shfl_xor(s, 4, 8);
-	s = s + __shfl_xor(s, 2, 8);
-	s = s + __shfl_xor(s, 1, 8);
+	s = s + dpp_f32<0x104>(s); /* lane l: s_l + s_{l+4} */
+	s = s + dpp_f32<0x102>(s); /* + the pair two lanes up */
+	s = s + dpp_f32<0x101>(s); /* lane 0: the full tree */
+	float sum = lane_f32(s, 0);
 	for (int i = nv; i < NE; i++)
-		s += __shfl(e, i, WAVE);
-	const float sum = __shfl(s, 0, WAVE);
+		sum += lane_f32(e, i);
 	const float p = e / sum;
 
 	/* p >= 0, so its bits order like the values: j beats i iff key_j > key_i,
@@ -379,13 +404,13 @@ __device__ static inline void wave_softmax_topk64(float logit, u32 *ids, float *
 		rank += (int)((key - v.x) >> 63);
 		rank += (int)((key - v.y) >> 63);
 	}
-	const int r0 = __shfl(rank, 0, WAVE);
+	const int r0 = __builtin_amdgcn_readlane(rank, 0);
 	const int lim = r0 < K ? r0 : K;
 	if (lane > 0 && valid && rank < lim) {
 		sid[K - 1 - rank] = (u32)lane;
 		sw[K - 1 - rank] = p;
 	}
-	const float p0 = __shfl(p, 0, WAVE);
+	const float p0 = lane_f32(p, 0);
 	if (r0 < K)
 		for (int slot = lane; slot < K - r0; slot += WAVE) {
 			sid[slot] = 0;

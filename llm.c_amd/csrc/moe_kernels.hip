@@ -24,29 +24,98 @@
 /* router: logits[t][j] = (bias[j] or 0) + dot(x[t], wr[j])            */
 /* ------------------------------------------------------------------ */
 
-/* Eight threads per logit; thread l accumulates elements l, l+8, ... with
- * FMA in increasing order (one AVX2 lane), then the lanes meet in the tree
- * ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) of vector_avx2.h:126-132. */
-__global__ __launch_bounds__(64) void k_router(const float *__restrict__ x,
-					       const float *__restrict__ wr,
-					       const float *__restrict__ bias,
-					       float *__restrict__ logits, int E, int NE)
-{
-	int t = blockIdx.y;
-	int j = blockIdx.x * 8 + (threadIdx.x >> 3);
-	int l = threadIdx.x & 7;
-	float acc = 0.0f;
-	if (j < NE) {
-		const float *xr = x + (size_t)t * E;
-		const float *w = wr + (size_t)j * E;
-		for (int i = l; i < E; i += 8)
-			acc = __builtin_fmaf(xr[i], w[i], acc);
+/*
+ * A workgroup takes RT_TOK tokens (one per wave) x 64 experts (one per lane).
+ * Each thread keeps the 8 AVX2 lane accumulators of its logit: accumulator l
+ * adds x[k]*w[k] for k = l, l+8, l+16, ... in increasing k with FMA
+ * (dot_f32_f32, matmul.c:91-105; the tiled T>1 path of matmul.c:213-238 keeps
+ * the same per-element order), then the lanes meet in the tree
+ * ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) of vector_avx2.h:126-132, and the
+ * logit is fl(bias + dot) (matmul.c:24-32).  Router rows and tokens pass
+ * through LDS in double-buffered chunks of RT_KC columns; a wave reads one
+ * token row (broadcast) and 64 router rows (row stride RT_LD: conflict-free).
+ */
+#define RT_TOK 4
+#define RT_KC 128
+#define RT_LD (RT_KC + 4)
+
+struct router_stage {
+	float4 w[8], x;
+	__device__ inline void load(const float *__restrict__ x_, const float *__restrict__ wr,
+				    int t0, int j0, int T, int E, int NE, int c)
+	{
+		const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+		for (int q = 0; q < 8; q++) {
+			const int f = threadIdx.x + 256 * q, row = f >> 5, c4 = f & 31;
+			w[q] = j0 + row < NE ? *(const float4 *)(wr + (size_t)(j0 + row) * E +
+								 c * RT_KC + 4 * c4)
+					     : z;
+		}
+		const int tr = t0 + (threadIdx.x >> 5), c4 = threadIdx.x & 31;
+		x = threadIdx.x < RT_TOK * 32 && tr < T
+			    ? *(const float4 *)(x_ + (size_t)tr * E + c * RT_KC + 4 * c4)
+			    : z;
 	}
-	acc = acc + __shfl_xor(acc, 4, 8);
-	acc = acc + __shfl_xor(acc, 2, 8);
-	acc = acc + __shfl_xor(acc, 1, 8);
-	if (j < NE && l == 0)
-		logits[(size_t)t * NE + j] = (bias ? bias[j] : 0.0f) + acc;
+	__device__ inline void store(float *sw, float *sx) const
+	{
+#pragma unroll
+		for (int q = 0; q < 8; q++) {
+			const int f = threadIdx.x + 256 * q;
+			*(float4 *)(sw + (f >> 5) * RT_LD + 4 * (f & 31)) = w[q];
+		}
+		if (threadIdx.x < RT_TOK * 32)
+			*(float4 *)(sx + (threadIdx.x >> 5) * RT_LD + 4 * (threadIdx.x & 31)) = x;
+	}
+};
+
+__global__ __launch_bounds__(256) void k_router(const float *__restrict__ x,
+						const float *__restrict__ wr,
+						const float *__restrict__ bias,
+						float *__restrict__ logits, int T, int E, int NE)
+{
+	__shared__ __attribute__((aligned(16))) float sw[2][64 * RT_LD];
+	__shared__ __attribute__((aligned(16))) float sx[2][RT_TOK * RT_LD];
+	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+	const int t0 = blockIdx.x * RT_TOK, j0 = blockIdx.y * 64;
+	const int nc = E / RT_KC;
+	float acc[8];
+#pragma unroll
+	for (int l = 0; l < 8; l++)
+		acc[l] = 0.0f;
+	router_stage st;
+	st.load(x, wr, t0, j0, T, E, NE, 0);
+	st.store(sw[0], sx[0]);
+	__syncthreads();
+	for (int c = 0; c < nc; c++) {
+		const int b = c & 1;
+		if (c + 1 < nc)
+			st.load(x, wr, t0, j0, T, E, NE, c + 1);
+		const float *xr = sx[b] + wave * RT_LD, *wrow = sw[b] + lane * RT_LD;
+#pragma unroll 4
+		for (int k = 0; k < RT_KC; k += 8) {
+			const float4 xa = *(const float4 *)(xr + k), xb = *(const float4 *)(xr + k + 4);
+			const float4 wa = *(const float4 *)(wrow + k),
+				     wb = *(const float4 *)(wrow + k + 4);
+			acc[0] = __builtin_fmaf(xa.x, wa.x, acc[0]);
+			acc[1] = __builtin_fmaf(xa.y, wa.y, acc[1]);
+			acc[2] = __builtin_fmaf(xa.z, wa.z, acc[2]);
+			acc[3] = __builtin_fmaf(xa.w, wa.w, acc[3]);
+			acc[4] = __builtin_fmaf(xb.x, wb.x, acc[4]);
+			acc[5] = __builtin_fmaf(xb.y, wb.y, acc[5]);
+			acc[6] = __builtin_fmaf(xb.z, wb.z, acc[6]);
+			acc[7] = __builtin_fmaf(xb.w, wb.w, acc[7]);
+		}
+		if (c + 1 < nc)
+			st.store(sw[b ^ 1], sx[b ^ 1]);
+		__syncthreads();
+	}
+	const int t = t0 + wave, j = j0 + lane;
+	if (t < T && j < NE) {
+		const float d = ((acc[0] + acc[4]) + (acc[2] + acc[6])) +
+				((acc[1] + acc[5]) + (acc[3] + acc[7]));
+		logits[(size_t)t * NE + j] = (bias ? bias[j] : 0.0f) + d;
+	}
 }
 
 /* ------------------------------------------------------------------ */
@@ -210,9 +279,11 @@ extern "C" int moe_kchunks(size_t K)
 extern "C" int moe_launch_router(const float *x, const float *wr, const float *bias,
 				 float *logits, int T, int E, int NE, void *stream)
 {
-	dim3 grid((NE + 7) / 8, T);
-	hipLaunchKernelGGL(k_router, grid, dim3(64), 0, (hipStream_t)stream, x, wr,
-			   bias, logits, E, NE);
+	if (E % RT_KC)
+		return (int)hipErrorInvalidValue;
+	dim3 grid((T + RT_TOK - 1) / RT_TOK, (NE + 63) / 64);
+	hipLaunchKernelGGL(k_router, grid, dim3(256), 0, (hipStream_t)stream, x, wr,
+			   bias, logits, T, E, NE);
 	return (int)hipGetLastError();
 }
 

@@ -57,46 +57,60 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
  * layout is a deterministic function of ids.  rows[] gets Tmax*PF_MT entries
  * (padding -1) and tile_e[] Tmax entries (-1 past the last tile): every
  * entry is rewritten on every call.
+ *
+ * Thread (e, c) = (tid % NE, tid / NE) owns expert e in chunk c of each
+ * segment of SORT_SEG pairs (ids staged in LDS as bytes): it counts its
+ * expert's pairs in the chunk, takes the exclusive sum of the counts of the
+ * earlier chunks, and writes its pairs' rows in order.
  */
+#define SORT_SEG 16384
+
 __global__ __launch_bounds__(SORT_THREADS) void k_moe_sort(const u32 *__restrict__ ids, int P,
 							   int NE, int Tmax,
 							   int *__restrict__ rows,
 							   int *__restrict__ tile_e)
 {
 	__shared__ int cnt[MOE_MAX_NE], toff[MOE_MAX_NE + 1], run[MOE_MAX_NE];
-	__shared__ int wcnt[SORT_THREADS / WAVE][MOE_MAX_NE];
-	const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+	__shared__ int ccnt[SORT_THREADS];
+	__shared__ __attribute__((aligned(16))) uint8_t sid[SORT_SEG];
+	const int tid = threadIdx.x;
+	const int C = SORT_THREADS / NE; /* chunks per segment */
+	const int e = tid % NE, c = tid / NE;
+	const bool owner = c < C;
 
-	for (int e = tid; e < NE; e += SORT_THREADS) {
-		cnt[e] = 0;
-		run[e] = 0;
+	for (int i = tid; i < NE; i += SORT_THREADS) {
+		cnt[i] = 0;
+		run[i] = 0;
 	}
 	__syncthreads();
-	for (int p = tid; p < P; p += SORT_THREADS)
-		if (ids[p] < (u32)NE) /* always, for ids from the top-k kernel */
-			atomicAdd(&cnt[ids[p]], 1);
+	for (int p = tid; p < P; p += SORT_THREADS) {
+		const u32 v = ids[p];
+		if (v < (u32)NE) /* always, for ids from the top-k kernel */
+			atomicAdd(&cnt[v], 1);
+	}
 	__syncthreads();
-	if (wave == 0) { /* exclusive scan of tiles per expert, 4 experts per lane */
+	if (tid < WAVE) { /* exclusive scan of tiles per expert, 4 experts per lane */
+		const int lane = tid;
 		int t4[4], s = 0;
 #pragma unroll
 		for (int i = 0; i < 4; i++) {
-			int e = 4 * lane + i;
-			t4[i] = e < NE ? (cnt[e] + PF_MT - 1) / PF_MT : 0;
+			const int ex = 4 * lane + i;
+			t4[i] = ex < NE ? (cnt[ex] + PF_MT - 1) / PF_MT : 0;
 			s += t4[i];
 		}
 		int incl = s;
 #pragma unroll
 		for (int d = 1; d < WAVE; d <<= 1) {
-			int v = __shfl_up(incl, d, WAVE);
+			const int v = __shfl_up(incl, d, WAVE);
 			if (lane >= d)
 				incl += v;
 		}
 		int base = incl - s;
 #pragma unroll
 		for (int i = 0; i < 4; i++) {
-			int e = 4 * lane + i;
-			if (e < NE)
-				toff[e] = base;
+			const int ex = 4 * lane + i;
+			if (ex < NE)
+				toff[ex] = base;
 			base += t4[i];
 		}
 		if (lane == WAVE - 1)
@@ -107,59 +121,55 @@ __global__ __launch_bounds__(SORT_THREADS) void k_moe_sort(const u32 *__restrict
 	/* tile table and padding rows */
 	for (int i = tid; i < Tmax * PF_MT; i += SORT_THREADS) {
 		const int tile = i / PF_MT;
-		int e = -1;
-		if (tile < ntiles) { /* largest e with toff[e] <= tile */
+		int ex = -1;
+		if (tile < ntiles) { /* largest ex with toff[ex] <= tile */
 			int lo = 0, hi = NE - 1;
 			while (lo < hi) {
-				int mid = (lo + hi + 1) >> 1;
+				const int mid = (lo + hi + 1) >> 1;
 				if (toff[mid] <= tile)
 					lo = mid;
 				else
 					hi = mid - 1;
 			}
-			e = lo;
+			ex = lo;
 		}
 		if (i % PF_MT == 0)
-			tile_e[tile] = e;
-		if (e < 0 || i - toff[e] * PF_MT >= cnt[e])
+			tile_e[tile] = ex;
+		if (ex < 0 || i - toff[ex] * PF_MT >= cnt[ex])
 			rows[i] = -1;
 	}
-	/* stable scatter, SORT_THREADS pairs at a time */
-	for (int c = 0; c < P; c += SORT_THREADS) {
-		const int p = c + tid;
-		const u32 eid = p < P ? ids[p] : 0xffffffffu;
-		const bool valid = eid < (u32)NE;
-		const int e = valid ? (int)eid : -1;
-		for (int i = lane; i < NE; i += WAVE)
-			wcnt[wave][i] = 0;
-		WAVE_SYNC();
-		int rank = 0;
-		uint64_t todo = __ballot(valid);
-		while (todo) {
-			const int leader = __builtin_ctzll(todo);
-			const int e0 = __shfl(e, leader, WAVE);
-			const uint64_t m = __ballot(valid && e == e0);
-			if (valid && e == e0)
-				rank = __builtin_popcountll(m & ((1ull << lane) - 1ull));
-			if (lane == leader)
-				wcnt[wave][e0] = __builtin_popcountll(m);
-			todo &= ~m;
+	/* stable scatter, segment by segment */
+	for (int s0 = 0; s0 < P; s0 += SORT_SEG) {
+		const int S = P - s0 < SORT_SEG ? P - s0 : SORT_SEG;
+		__syncthreads(); /* earlier readers of sid / ccnt are done */
+		for (int i = tid; i < S; i += SORT_THREADS) {
+			const u32 v = ids[s0 + i];
+			sid[i] = v < (u32)NE ? (uint8_t)v : (uint8_t)255; /* NE <= 256 */
 		}
 		__syncthreads();
-		if (valid) {
-			int pos = toff[e] * PF_MT + run[e] + rank;
-			for (int w = 0; w < wave; w++)
-				pos += wcnt[w][e];
-			rows[pos] = p;
+		const int L = (S + C - 1) / C;
+		const int b0 = c * L, b1 = b0 + L < S ? b0 + L : S;
+		int n = 0;
+		if (owner)
+			for (int i = b0; i < b1; i++)
+				n += sid[i] == (uint8_t)e;
+		ccnt[tid] = n;
+		__syncthreads();
+		if (owner) {
+			int pos = toff[e] * PF_MT + run[e];
+			for (int cc = 0; cc < c; cc++)
+				pos += ccnt[cc * NE + e];
+			for (int i = b0; i < b1; i++)
+				if (sid[i] == (uint8_t)e)
+					rows[pos++] = s0 + i;
 		}
 		__syncthreads();
-		for (int i = tid; i < NE; i += SORT_THREADS) {
-			int s = 0;
-			for (int w = 0; w < SORT_THREADS / WAVE; w++)
-				s += wcnt[w][i];
-			run[i] += s;
+		if (tid < NE) {
+			int tot = 0;
+			for (int cc = 0; cc < C; cc++)
+				tot += ccnt[cc * NE + tid];
+			run[tid] += tot;
 		}
-		__syncthreads();
 	}
 }
 

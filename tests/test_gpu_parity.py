@@ -392,6 +392,24 @@ def test_gpu_fused_many_calls_reset_counters():
         assert rel_l2(out[0], oout[t]) <= TIGHT
 
 
+def test_gpu_fresh_layer_after_freed_layer():
+    """A layer allocated where a freed layer's scratch lived must not take that
+    layer's epoch-tagged partials for its own (its epoch restarts at 1)."""
+    say("fresh layer after a freed one: first decode calls")
+    cfg = "olmoe_q8"
+    wt, E, EI, NE, K, renorm, bias_std = CONFIGS[cfg]
+    lw = layer(cfg)
+    xs = hipmoe.synth_input(SEED, 610, 6, E)
+    oout, oids, ow, _, _ = oracle.moe_ffn(xs, lw, K, False, None)
+    for rnd in range(3):
+        lay = hipmoe.MoeLayer.from_synth(lw, K, False)
+        for t in range(6):
+            out, ids, w = lay.ffn(xs[t:t + 1])
+            assert np.array_equal(ids[0], oids[t])
+            assert rel_l2(out[0], oout[t]) <= TIGHT, (rnd, t)
+        lay.free()
+
+
 def test_gpu_graph_replays_match_eager():
     say("HIP graph of 4 decode calls, replayed 5 times")
     H = hipmoe.hip()
