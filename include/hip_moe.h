@@ -116,11 +116,12 @@ int hip_moe_expert_ffn_dev(hip_moe_layer *L, size_t expert, const float *d_x,
 /*
  * Execution paths of hip_moe_ffn / hip_moe_ffn_dev.  None has a counterpart
  * in the reference, which runs one per-token loop (olmoe.c:364-406):
- *   DECODE   one persistent launch (T*K <= 64, NE <= 64), fp32 arithmetic
+ *   DECODE   one persistent launch (T*k <= 64, NE <= 64), fp32 arithmetic
  *   GEMV     router, top-k, per-pair dequant-GEMV kernels, combine; fp32
  *   GROUPED  router, top-k, sort by expert, f16 MFMA grouped GEMMs, combine
- * AUTO picks DECODE where it applies, else GROUPED when the (token, slot)
- * pairs average at least 4 per expert, else GEMV.  Routing (ids and
+ * AUTO picks DECODE where it applies and the (token, slot) pairs do not
+ * outnumber the experts (T*k <= NE: every pair streams its expert once),
+ * else GROUPED (each touched expert streamed once), else GEMV.  Routing (ids and
  * weights) is bit-identical on every path; outputs agree with the reference
  * within 1e-3 relative L2 (fp32 paths: ~1e-6; GROUPED: ~5e-4 from f16
  * operands).

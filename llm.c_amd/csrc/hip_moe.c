@@ -325,9 +325,12 @@ static int choose_path(const hip_moe_layer *L, size_t T)
 	case HIP_MOE_PATH_GROUPED:
 		return grp ? HIP_MOE_PATH_GROUPED : 0;
 	default:
-		if (dec)
+		/* one launch, but each (token, slot) streams its expert: taken while
+		 * the pairs do not outnumber the experts */
+		if (dec && T * L->topk <= L->NE)
 			return HIP_MOE_PATH_DECODE;
-		if (grp && T * L->topk >= (size_t)MOE_GROUPED_MIN_PER_EXPERT * L->NE)
+		/* more pairs than experts: stream each touched expert once */
+		if (grp)
 			return HIP_MOE_PATH_GROUPED;
 		return HIP_MOE_PATH_GEMV;
 	}

@@ -50,6 +50,7 @@
 #define GU_ROWS 8
 #define DN_ROWS 16
 #define NREP 64 /* == WAVE: one replica per lane of the writing wave */
+#define COMBINE_MAX 1024 /* floats of LDS for the combiner's partials */
 
 struct DecodeArgs {
 	const float *x;
@@ -153,18 +154,21 @@ template <> struct segq<1> {
 	{
 		return row + ((34 * s) & ~3);
 	}
-	__device__ static inline float dot(const u32 (&d)[9], const float (&x)[32], int s)
+	/* block sums of x: one block per lane */
+	__device__ static inline void xsum(const float (&x)[32], float (&xs)[2])
 	{
-		const int sh = (s & 1) ? 32 : 16;
-		float acc = 0.0f;
+		xs[0] = sum32(x);
+		xs[1] = 0.0f;
+	}
+	__device__ static inline float dot(const u32 (&d)[9], const float (&x)[32], int s,
+					   const float (&xs)[2])
+	{
+		u32 q[8];
+		const bool odd = s & 1; /* quants at byte 4 (odd) or 2 (even) of the window */
 #pragma unroll
-		for (int k = 0; k < 8; k++) {
-			u32 q = (u32)((((uint64_t)d[k + 1] << 32) | d[k]) >> sh);
-#pragma unroll
-			for (int b = 0; b < 4; b++)
-				acc = __builtin_fmaf((float)(int)(int8_t)(q >> (8 * b)), x[4 * k + b], acc);
-		}
-		return f16_bits_to_f32(d[0] >> (sh - 16)) * acc;
+		for (int k = 0; k < 8; k++)
+			q[k] = odd ? d[k + 1] : __builtin_amdgcn_alignbit(d[k + 1], d[k], 16);
+		return block_dot_q8_0(q, odd ? d[0] >> 16 : d[0], x, xs[0]);
 	}
 };
 
@@ -175,9 +179,15 @@ template <> struct segq<2> {
 	{
 		return row + 36 * s;
 	}
-	__device__ static inline float dot(const u32 (&d)[9], const float (&x)[64], int)
+	__device__ static inline void xsum(const float (&x)[64], float (&xs)[2])
 	{
-		return seg_dot_q4_0(d, x);
+		xs[0] = sum32(x);
+		xs[1] = sum32(x + 32);
+	}
+	__device__ static inline float dot(const u32 (&d)[9], const float (&x)[64], int,
+					   const float (&xs)[2])
+	{
+		return seg_dot_q4_0(d, x, xs[0], xs[1]);
 	}
 };
 
@@ -203,17 +213,6 @@ __device__ static inline void stage_seg(float *s, const float *g, int n)
 	for (int i = threadIdx.x; i < n / 4; i += NTHREADS) {
 		int k = 4 * i;
 		*(float4 *)(s + (k / COLS) * (COLS + 4) + k % COLS) = g4[i];
-	}
-}
-
-/* the same for data another workgroup produced in this launch */
-template <int COLS>
-__device__ static inline void stage_seg_dev(float *s, const float *g, int n)
-{
-	for (int i = threadIdx.x; i < n / 2; i += NTHREADS) {
-		uint64_t v = ld_dev_u64((const uint64_t *)(g + 2 * i));
-		int k = 2 * i;
-		*(uint64_t *)(s + (k / COLS) * (COLS + 4) + k % COLS) = v;
 	}
 }
 
@@ -368,6 +367,7 @@ __device__ static void route_local(const DecodeArgs &a, u32 epoch, float *lds, u
 template <int WT, int CD> struct down_geo {
 	static constexpr int RPS = WAVE / CD, RW = DN_ROWS / 4, NS = RW / RPS;
 	static constexpr int CHUNK = CD * segq<WT>::COLS; /* columns of one K-chunk */
+	static constexpr int CD_SEGS = CD;                /* segments of one K-chunk */
 };
 
 /* issue the weight loads of down item d (they do not depend on h) */
@@ -390,61 +390,98 @@ __device__ static inline void down_load(const DecodeArgs &a, int d, const u32 *s
 		load_dwords<S::DW>(D + (size_t)(row0 + s2 * DG::RPS + sub) * rb, dd[s2]);
 }
 
-/*
- * Gate/up tile g: h[p][rows] = silu(gate.x) * (up.x), then the tile's flag.
- * If pre_d >= 0 the weight loads of down item pre_d are issued after the
- * flag, to land while this workgroup waits for h.
- */
-template <int WT, int CG, int CD>
-__device__ static void gateup_item(const DecodeArgs &a, int g, const u32 *s_ids, float *sx,
-				   int &staged, u32 epoch, int pre_d,
-				   u32 (&dd)[down_geo<WT, CD>::NS][9], const uint64_t *s_tab)
+/* the weights of one gate/up tile in registers */
+template <int WT, int CG> struct gu_regs {
+	static constexpr int RPS = WAVE / CG, RW = GU_ROWS / 4, NS = RW / RPS;
+	u32 g[NS][segq<WT>::DW], u[NS][segq<WT>::DW];
+};
+
+/* issue the weight loads of gate/up tile g */
+template <int WT, int CG>
+__device__ static inline void gateup_load(const DecodeArgs &a, int g, const u32 *s_ids,
+					  gu_regs<WT, CG> &r)
 {
 	typedef segq<WT> S;
-	constexpr int RPS = WAVE / CG, RW = GU_ROWS / 4, NS = RW / RPS;
+	typedef gu_regs<WT, CG> R;
 	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
 	const int tiles = a.EI / GU_ROWS;
 	const int p = g / tiles, tile = g % tiles;
-	const int row0 = tile * GU_ROWS + wave * RW;
-	const int t = p / a.K;
+	const int row0 = tile * GU_ROWS + wave * R::RW;
 	const int e = (int)s_ids[p];
 	const int seg = lane % CG, sub = lane / CG;
 	const size_t rb = (size_t)(a.E / MOE_QK) * (WT == 1 ? 34 : 18);
 	const uint8_t *G = S::win(a.gate + (size_t)e * a.gu_stride, seg);
 	const uint8_t *U = S::win(a.up + (size_t)e * a.gu_stride, seg);
-
-	u32 dg[NS][S::DW], du[NS][S::DW];
 #pragma unroll
-	for (int s2 = 0; s2 < NS; s2++) {
-		const size_t ro = (size_t)(row0 + s2 * RPS + sub) * rb;
-		load_dwords<S::DW>(G + ro, dg[s2]);
-		load_dwords<S::DW>(U + ro, du[s2]);
+	for (int s2 = 0; s2 < R::NS; s2++) {
+		const size_t ro = (size_t)(row0 + s2 * R::RPS + sub) * rb;
+		load_dwords<S::DW>(G + ro, r.g[s2]);
+		load_dwords<S::DW>(U + ro, r.u[s2]);
 	}
+}
+
+/* Gate/up tile g with its weights in r: h[p][rows] = silu(gate.x) * (up.x)
+ * (the stores; the flag follows in gateup_flag) */
+template <int WT, int CG>
+__device__ static void gateup_compute(const DecodeArgs &a, int g, float *sx, int &staged,
+				      const gu_regs<WT, CG> &r, const uint64_t *s_tab)
+{
+	typedef segq<WT> S;
+	typedef gu_regs<WT, CG> R;
+	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+	const int tiles = a.EI / GU_ROWS;
+	const int p = g / tiles, tile = g % tiles;
+	const int row0 = tile * GU_ROWS + wave * R::RW;
+	const int t = p / a.K;
+	const int seg = lane % CG, sub = lane / CG;
 	if (staged != t) {
 		__syncthreads(); /* earlier readers of sx are done */
 		stage_seg<S::COLS>(sx, a.x + (size_t)t * a.E, a.E);
 		__syncthreads();
 		staged = t;
 	}
-	float xr[S::COLS];
+	float xr[S::COLS], xs[2];
 	lds_seg<S::COLS>(sx, seg, xr);
+	S::xsum(xr, xs);
 #pragma unroll
-	for (int s2 = 0; s2 < NS; s2++) {
-		const int row = row0 + s2 * RPS + sub;
-		float gv = group_sum<CG>(S::dot(dg[s2], xr, seg));
-		float uv = group_sum<CG>(S::dot(du[s2], xr, seg));
+	for (int s2 = 0; s2 < R::NS; s2++) {
+		const int row = row0 + s2 * R::RPS + sub;
+		const float gv = group_sum<CG>(S::dot(r.g[s2], xr, seg, xs));
+		const float uv = group_sum<CG>(S::dot(r.u[s2], xr, seg, xs));
 		if (seg == 0)
 			st_dev(&a.h[(size_t)p * a.EI + row],
 			       (gv / (1.0f + moe_expf_tab(-gv, s_tab))) * uv);
 	}
-	__builtin_amdgcn_s_waitcnt(0);
+	/* keep the h stores ahead of any load the caller issues next */
+	asm volatile("" ::: "memory");
+}
+
+/*
+ * The flag of gate/up tile g, raised once its h stores have completed: wait
+ * until at most N vector memory operations are outstanding.  They retire in
+ * issue order, so N = the loads issued after the stores (the next item's
+ * weights, in flight while this wait covers only older operations).
+ */
+template <int N>
+__device__ static inline void gateup_flag(const DecodeArgs &a, int g, u32 epoch)
+{
+	static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+	__builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 	__syncthreads();
 	if (threadIdx.x == 0)
-		st_dev_u32(a.sync + a.off_hf + (size_t)p * tiles + tile, epoch);
-	/* the next down item's weights: issued only now, so they do not compete
-	 * with the gate/up streams everyone is waiting for */
-	if (pre_d >= 0)
-		down_load<WT, CD>(a, pre_d, s_ids, dd);
+		st_dev_u32(a.sync + a.off_hf + (size_t)g, epoch); /* p * tiles + tile == g */
+}
+
+/* n floats another workgroup produced in this launch, from global into LDS
+ * (COLS-float segments padded by 4) */
+template <int COLS>
+__device__ static inline void stage_seg_dev(float *s, const float *g, int n)
+{
+	for (int i = threadIdx.x; i < n / 2; i += NTHREADS) {
+		uint64_t v = ld_dev_u64((const uint64_t *)(g + 2 * i));
+		int k = 2 * i;
+		*(uint64_t *)(s + (k / COLS) * (COLS + 4) + k % COLS) = v;
+	}
 }
 
 /* down item d with its weights already in dd: wait for the gate/up tiles of
@@ -452,7 +489,8 @@ __device__ static void gateup_item(const DecodeArgs &a, int g, const u32 *s_ids,
  * block) waits for the others and combines the slots in order */
 template <int WT, int CD>
 __device__ static void down_item(const DecodeArgs &a, int d, const float *s_w, float *sh,
-				 u32 epoch, const u32 (&dd)[down_geo<WT, CD>::NS][9])
+				 float *sc, int &hchunk, u32 epoch,
+				 const u32 (&dd)[down_geo<WT, CD>::NS][9])
 {
 	typedef segq<WT> S;
 	typedef down_geo<WT, CD> DG;
@@ -468,19 +506,24 @@ __device__ static void down_item(const DecodeArgs &a, int d, const float *s_w, f
 	const bool combiner = slot == a.K - 1 && kc == a.kch - 1;
 	__shared__ float s_y[DN_ROWS];
 
-	wait_flags(a.sync + a.off_hf + (size_t)p * (a.EI / GU_ROWS) + (size_t)kc * TPC, TPC, epoch,
-		   a.sync + MOE_SYNC_ERR_WORD);
-	stage_seg_dev<S::COLS>(sh, a.h + (size_t)p * a.EI + (size_t)kc * DG::CHUNK, DG::CHUNK);
-	__syncthreads();
-	float xr[S::COLS];
+	if (hchunk != p * a.kch + kc) { /* consecutive items mostly share the chunk */
+		wait_flags(a.sync + a.off_hf + (size_t)p * (a.EI / GU_ROWS) + (size_t)kc * TPC, TPC,
+			   epoch, a.sync + MOE_SYNC_ERR_WORD);
+		stage_seg_dev<S::COLS>(sh, a.h + (size_t)p * a.EI + (size_t)kc * DG::CHUNK,
+				       DG::CHUNK);
+		__syncthreads();
+		hchunk = p * a.kch + kc;
+	}
+	float xr[S::COLS], xs[2];
 	lds_seg<S::COLS>(sh, seg, xr);
+	S::xsum(xr, xs);
 	/* partial y of (token, row block), contribution (slot, kc), tagged with
 	 * the epoch so the combiner can poll the data itself */
 	uint64_t *yq = (uint64_t *)a.ypart + ((size_t)t * nrb + rbk) * ncontrib * DN_ROWS;
 #pragma unroll
 	for (int s2 = 0; s2 < DG::NS; s2++) {
 		const int r = wave * DG::RW + s2 * DG::RPS + sub;
-		const float y = group_sum<CD>(S::dot(dd[s2], xr, kc * CD + seg));
+		const float y = group_sum<CD>(S::dot(dd[s2], xr, kc * CD + seg, xs));
 		if (seg == 0) {
 			if (combiner)
 				s_y[r] = y;
@@ -493,11 +536,9 @@ __device__ static void down_item(const DecodeArgs &a, int d, const float *s_w, f
 		return;
 	/* the combiner: collect the other contributions, then add the slots in
 	 * order, y = sum of its K-chunks in order, out += y / (1/w) */
-	float *sc = sh; /* [ncontrib][DN_ROWS], once every wave is done reading h */
-	const int n = ncontrib * DN_ROWS;
+	const int n = ncontrib * DN_ROWS; /* sc: [ncontrib][DN_ROWS] */
 	__shared__ int s_ok;
 	int step = 0;
-	__syncthreads();
 	for (int round = 0;; round++) {
 		bool ok = true;
 		for (int i = threadIdx.x; i < n; i += NTHREADS) {
@@ -538,8 +579,16 @@ __device__ static void down_item(const DecodeArgs &a, int d, const float *s_w, f
 	}
 }
 
-template <int WT, int CG, int CD>
-__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(4, 4)))
+/*
+ * PIPE = 0: four workgroups per CU (<= 128 VGPRs), items run one after the
+ * other (decode of one OLMoE token: one gate/up and one down item each).
+ * PIPE = 1: two workgroups per CU (<= 256 VGPRs) and the weight loads of the
+ * next item are in flight while the current one computes (Mixtral-sized
+ * layers: several items per workgroup).
+ */
+template <int WT, int CG, int CD, int PIPE>
+__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(PIPE ? 2 : 4,
+									   PIPE ? 2 : 4)))
 void k_moe_decode(DecodeArgs a)
 {
 	extern __shared__ float lds[];
@@ -576,24 +625,83 @@ void k_moe_decode(DecodeArgs a)
 
 	float *sx = lds;                                       /* x, padded segments */
 	float *sh = lds + (a.E / S::COLS) * (S::COLS + 4);     /* h chunk, padded */
-	int staged = -1;
-	const int total = a.n_gu + a.n_dn;
-	u32 dd[down_geo<WT, CD>::NS][9];
-	bool have_dd = false;
-	int item = blockIdx.x;
-	for (; item < a.n_gu; item += gridDim.x) {
-		const int nxt = item + (int)gridDim.x;
-		const int pre = (nxt >= a.n_gu && nxt < total) ? nxt - a.n_gu : -1;
-		gateup_item<WT, CG, CD>(a, item, s_ids, sx, staged, epoch, pre, dd, s_tab);
-		have_dd = pre >= 0;
-		__syncthreads();
-	}
-	for (; item < total; item += gridDim.x) {
-		if (!have_dd)
-			down_load<WT, CD>(a, item - a.n_gu, s_ids, dd);
-		have_dd = false;
-		down_item<WT, CD>(a, item - a.n_gu, s_w, sh, epoch, dd);
-		__syncthreads();
+	typedef down_geo<WT, CD> DG;
+	float *sc = sh + DG::CD_SEGS * (S::COLS + 4);          /* combiner partials */
+	int staged = -1, hchunk = -1;
+	const int G = (int)gridDim.x;
+	/* gate/up tiles cyclically (tile i on workgroup i % G); down tiles in
+	 * contiguous blocks, so consecutive ones share their K-chunk of h.  Each
+	 * workgroup runs its items in increasing index and every wait is for a
+	 * smaller index, so with the grid resident every wait ends. */
+	const int m = (a.n_dn + G - 1) / G;
+	const int d0 = (int)blockIdx.x * m < a.n_dn ? (int)blockIdx.x * m : a.n_dn;
+	const int d1 = d0 + m < a.n_dn ? d0 + m : a.n_dn;
+	if (PIPE) {
+		constexpr int NLD = 6 * gu_regs<WT, CG>::NS; /* loads of one gateup_load */
+		gu_regs<WT, CG> A, B;
+		int item = blockIdx.x;
+		if (item < a.n_gu)
+			gateup_load<WT, CG>(a, item, s_ids, A);
+		if (item + G < a.n_gu)
+			gateup_load<WT, CG>(a, item + G, s_ids, B);
+		for (; item < a.n_gu; item += 2 * G) {
+			gateup_compute<WT, CG>(a, item, sx, staged, A, s_tab);
+			if (item + 2 * G < a.n_gu) {
+				gateup_load<WT, CG>(a, item + 2 * G, s_ids, A);
+				gateup_flag<NLD>(a, item, epoch);
+			} else {
+				gateup_flag<0>(a, item, epoch);
+			}
+			const int n1 = item + G;
+			if (n1 >= a.n_gu)
+				break;
+			gateup_compute<WT, CG>(a, n1, sx, staged, B, s_tab);
+			if (n1 + 2 * G < a.n_gu) {
+				gateup_load<WT, CG>(a, n1 + 2 * G, s_ids, B);
+				gateup_flag<NLD>(a, n1, epoch);
+			} else {
+				gateup_flag<0>(a, n1, epoch);
+			}
+		}
+		u32 dA[DG::NS][9], dB[DG::NS][9];
+		int d = d0;
+		if (d < d1)
+			down_load<WT, CD>(a, d, s_ids, dA);
+		while (d < d1) {
+			if (d + 1 < d1)
+				down_load<WT, CD>(a, d + 1, s_ids, dB);
+			down_item<WT, CD>(a, d, s_w, sh, sc, hchunk, epoch, dA);
+			__syncthreads();
+			if (++d >= d1)
+				break;
+			if (d + 1 < d1)
+				down_load<WT, CD>(a, d + 1, s_ids, dA);
+			down_item<WT, CD>(a, d, s_w, sh, sc, hchunk, epoch, dB);
+			__syncthreads();
+			++d;
+		}
+	} else {
+		u32 dd[DG::NS][9];
+		bool have_dd = false;
+		for (int item = blockIdx.x; item < a.n_gu; item += G) {
+			gu_regs<WT, CG> r;
+			gateup_load<WT, CG>(a, item, s_ids, r);
+			gateup_compute<WT, CG>(a, item, sx, staged, r, s_tab);
+			gateup_flag<0>(a, item, epoch);
+			/* the first down item's weights: issued only now, so they do not
+			 * compete with the gate/up streams everyone is waiting for */
+			if (item + G >= a.n_gu && d0 < d1) {
+				down_load<WT, CD>(a, d0, s_ids, dd);
+				have_dd = true;
+			}
+		}
+		for (int d = d0; d < d1; d++) {
+			if (!have_dd)
+				down_load<WT, CD>(a, d, s_ids, dd);
+			have_dd = false;
+			down_item<WT, CD>(a, d, s_w, sh, sc, hchunk, epoch, dd);
+			__syncthreads();
+		}
 	}
 
 	/* workgroup 0 advances the epoch for the next launch once every
@@ -608,10 +716,11 @@ void k_moe_decode(DecodeArgs a)
 
 /* ---------------------------------------------------------------------- */
 
+/* Q4_0 layers (Mixtral-sized) run the pipelined two-per-CU form */
 template <int WT, int CG, int CD>
 static const void *decode_fn()
 {
-	return (const void *)k_moe_decode<WT, CG, CD>;
+	return (const void *)k_moe_decode<WT, CG, CD, WT == 2 ? 1 : 0>;
 }
 
 /* Q8_0: CG = E/32, CD from EI/32; Q4_0: CG = E/64, CD from EI/64 */
@@ -668,7 +777,9 @@ static size_t decode_lds_bytes(int wtype, size_t E, size_t EI, size_t T, size_t 
 	size_t rt = (size_t)2 * 8 * (E / 8 + 4) * sizeof(float);
 	size_t tk = (((T * NE + 15) & ~(size_t)15) + 4 * (MOE_MAX_NE + 2 * MOE_MAX_TOPK)) *
 		    sizeof(float);
-	size_t ex = (E / cols + g.CD) * (cols + 4) * sizeof(float);
+	/* x, one K-chunk of h, and the combiner's partials (K * kch * DN_ROWS
+	 * <= COMBINE_MAX floats) */
+	size_t ex = ((E / cols + g.CD) * (cols + 4) + COMBINE_MAX) * sizeof(float);
 	size_t m = rt > tk ? rt : tk;
 	return m > ex ? m : ex;
 }
@@ -697,8 +808,8 @@ extern "C" int moe_fused_supported(int wtype, size_t E, size_t EI, size_t NE, si
 	    EI % 256)
 		return 0;
 	Geo g = geometry(wtype, E, EI);
-	/* the combiner gathers K * kch contributions of DN_ROWS rows in the h chunk's LDS */
-	if (K * (size_t)g.kch * DN_ROWS > (size_t)g.CD * (size_t)(seg_cols(wtype) + 4))
+	/* the combiner gathers K * kch contributions of DN_ROWS rows in LDS */
+	if (K * (size_t)g.kch * DN_ROWS > COMBINE_MAX)
 		return 0;
 	return g.fn != NULL;
 }

@@ -59,92 +59,111 @@ __device__ static inline void load_dwords(const uint8_t *p, u32 (&d)[N])
 		d[i] = ((const u32 *)p)[i];
 }
 
+/*
+ * Dequant dots.  A quant byte is converted with v_cvt_f32_ubyte*: for Q8_0
+ * the byte b is read as (b ^ 0x80) = q + 128, for Q4_0 a nibble n = q + 8, so
+ *   sum_i q_i x_i = sum_i (q_i + c) x_i - c * sum_i x_i
+ * with the block's sum_i x_i (xs) computed once per lane and reused for
+ * every row.  Two VALU operations per weight instead of four or five.
+ */
+
+/* the sum of 32 consecutive floats */
+__device__ static inline float sum32(const float *x)
+{
+	float s = 0.0f;
+#pragma unroll
+	for (int i = 0; i < 32; i++)
+		s += x[i];
+	return s;
+}
+
+/* acc + sum over the 4 bytes of u of byte_j * x[j] */
+__device__ static inline float fma_ubytes(u32 u, const float *x, float acc)
+{
+	acc = __builtin_fmaf((float)(u & 0xffu), x[0], acc);
+	acc = __builtin_fmaf((float)((u >> 8) & 0xffu), x[1], acc);
+	acc = __builtin_fmaf((float)((u >> 16) & 0xffu), x[2], acc);
+	acc = __builtin_fmaf((float)(u >> 24), x[3], acc);
+	return acc;
+}
+
+/* Q8_0 block: 8 dwords of quants q0..q31 (already aligned), scale bits */
+__device__ static inline float block_dot_q8_0(const u32 (&q)[8], u32 dbits, const float *x,
+					      float xs)
+{
+	float acc = 0.0f;
+#pragma unroll
+	for (int k = 0; k < 8; k++)
+		acc = fma_ubytes(q[k] ^ 0x80808080u, x + 4 * k, acc);
+	return f16_bits_to_f32(dbits) * __builtin_fmaf(-128.0f, xs, acc);
+}
+
+/* Q4_0 block: 4 dwords of packed bytes (element j low nibble of byte j,
+ * element j+16 high nibble), scale bits */
+__device__ static inline float block_dot_q4_0(const u32 (&q)[4], u32 dbits, const float *x,
+					      float xs)
+{
+	float acc = 0.0f;
+#pragma unroll
+	for (int k = 0; k < 4; k++) {
+		acc = fma_ubytes(q[k] & 0x0f0f0f0fu, x + 4 * k, acc);
+		acc = fma_ubytes((q[k] >> 4) & 0x0f0f0f0fu, x + 16 + 4 * k, acc);
+	}
+	return f16_bits_to_f32(dbits) * __builtin_fmaf(-8.0f, xs, acc);
+}
+
 /* Q8_0 segment: 17 dwords.  Block 0 = bytes 0..33 (scale in bytes 0-1,
  * quants 2..33, i.e. misaligned by 2), block 1 = bytes 34..67 (scale 34-35,
- * quants 36..67 = dwords 9..16). */
-__device__ static inline float seg_dot_q8_0(const u32 (&d)[17], const float (&x)[64])
+ * quants 36..67 = dwords 9..16).  xs0, xs1: sums of x[0..31], x[32..63]. */
+__device__ static inline float seg_dot_q8_0(const u32 (&d)[17], const float (&x)[64], float xs0,
+					    float xs1)
 {
-	float s0 = 0.0f, s1 = 0.0f;
+	u32 q0[8], q1[8];
 #pragma unroll
 	for (int k = 0; k < 8; k++) {
-		u32 q = __builtin_amdgcn_alignbit(d[k + 1], d[k], 16);
-#pragma unroll
-		for (int b = 0; b < 4; b++)
-			s0 = __builtin_fmaf((float)(int)(int8_t)(q >> (8 * b)), x[4 * k + b], s0);
+		q0[k] = __builtin_amdgcn_alignbit(d[k + 1], d[k], 16);
+		q1[k] = d[9 + k];
 	}
-#pragma unroll
-	for (int k = 0; k < 8; k++) {
-		u32 q = d[9 + k];
-#pragma unroll
-		for (int b = 0; b < 4; b++)
-			s1 = __builtin_fmaf((float)(int)(int8_t)(q >> (8 * b)), x[32 + 4 * k + b], s1);
-	}
-	float d0 = f16_bits_to_f32(d[0]);
-	float d1 = f16_bits_to_f32(d[8] >> 16);
-	return __builtin_fmaf(d1, s1, d0 * s0);
+	return block_dot_q8_0(q0, d[0], x, xs0) + block_dot_q8_0(q1, d[8] >> 16, x + 32, xs1);
 }
 
 /* Q4_0 segment: 9 dwords.  Block 0 = bytes 0..17 (scale 0-1, packed nibbles
  * 2..17), block 1 = bytes 18..35 (scale 18-19, nibbles 20..35 = dwords 5..8).
  * Byte j of a block holds element j (low nibble) and j+16 (high nibble),
  * each biased by 8 (quant.c:126-155). */
-__device__ static inline float seg_dot_q4_0(const u32 (&d)[9], const float (&x)[64])
+__device__ static inline float seg_dot_q4_0(const u32 (&d)[9], const float (&x)[64], float xs0,
+					    float xs1)
 {
-	float s0 = 0.0f, s1 = 0.0f;
+	u32 q0[4], q1[4];
 #pragma unroll
 	for (int k = 0; k < 4; k++) {
-		u32 q = __builtin_amdgcn_alignbit(d[k + 1], d[k], 16);
-#pragma unroll
-		for (int b = 0; b < 4; b++) {
-			int lo = (int)((q >> (8 * b)) & 15u) - 8;
-			int hi = (int)((q >> (8 * b + 4)) & 15u) - 8;
-			s0 = __builtin_fmaf((float)lo, x[4 * k + b], s0);
-			s0 = __builtin_fmaf((float)hi, x[16 + 4 * k + b], s0);
-		}
+		q0[k] = __builtin_amdgcn_alignbit(d[k + 1], d[k], 16);
+		q1[k] = d[5 + k];
 	}
-#pragma unroll
-	for (int k = 0; k < 4; k++) {
-		u32 q = d[5 + k];
-#pragma unroll
-		for (int b = 0; b < 4; b++) {
-			int lo = (int)((q >> (8 * b)) & 15u) - 8;
-			int hi = (int)((q >> (8 * b + 4)) & 15u) - 8;
-			s1 = __builtin_fmaf((float)lo, x[32 + 4 * k + b], s1);
-			s1 = __builtin_fmaf((float)hi, x[48 + 4 * k + b], s1);
-		}
-	}
-	float d0 = f16_bits_to_f32(d[0]);
-	float d1 = f16_bits_to_f32(d[4] >> 16);
-	return __builtin_fmaf(d1, s1, d0 * s0);
+	return block_dot_q4_0(q0, d[0], x, xs0) + block_dot_q4_0(q1, d[4] >> 16, x + 32, xs1);
 }
 
 template <int WT> struct qseg;
 template <> struct qseg<1> {
 	static constexpr int BYTES = 68;
 	static constexpr int DW = 17;
-	__device__ static inline float dot(const uint8_t *p, const float (&x)[64])
+	__device__ static inline float dot(const uint8_t *p, const float (&x)[64], float xs0,
+					   float xs1)
 	{
 		u32 d[17];
 		load_dwords<17>(p, d);
-		return seg_dot_q8_0(d, x);
-	}
-	__device__ static inline float dot_regs(const u32 (&d)[17], const float (&x)[64])
-	{
-		return seg_dot_q8_0(d, x);
+		return seg_dot_q8_0(d, x, xs0, xs1);
 	}
 };
 template <> struct qseg<2> {
 	static constexpr int BYTES = 36;
 	static constexpr int DW = 9;
-	__device__ static inline float dot(const uint8_t *p, const float (&x)[64])
+	__device__ static inline float dot(const uint8_t *p, const float (&x)[64], float xs0,
+					   float xs1)
 	{
 		u32 d[9];
 		load_dwords<9>(p, d);
-		return seg_dot_q4_0(d, x);
-	}
-	__device__ static inline float dot_regs(const u32 (&d)[9], const float (&x)[64])
-	{
-		return seg_dot_q4_0(d, x);
+		return seg_dot_q4_0(d, x, xs0, xs1);
 	}
 };
 

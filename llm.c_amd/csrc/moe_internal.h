@@ -54,9 +54,7 @@ int moe_launch_combine(const float *ypart, const float *w, float *out, int T,
 int moe_launch_expf(const float *in, float *out, size_t n, void *stream);
 int moe_launch_copy(const void *src, void *dst, size_t bytes, void *stream);
 
-/* Grouped path (moe_prefill.hip): sort by expert + f16 MFMA GEMMs.  Taken by
- * default when the pairs per expert average at least this many. */
-#define MOE_GROUPED_MIN_PER_EXPERT 4
+/* Grouped path (moe_prefill.hip): sort by expert + f16 MFMA GEMMs. */
 int moe_prefill_supported(int wtype, size_t E, size_t EI, size_t NE);
 int moe_prefill_max_tiles(size_t P, size_t NE);
 int moe_prefill_tile_rows(void);

@@ -168,12 +168,13 @@ __global__ __launch_bounds__(256) void k_gateup(const uint8_t *__restrict__ gate
 
 	float xr[64];
 	load_x64(x + (size_t)t * E + seg * MOE_SEG_COLS, xr);
+	const float xs0 = sum32(xr), xs1 = sum32(xr + 32);
 
 	const int row0 = (blockIdx.x * 4 + wave) * rpw;
 	for (int r = 0; r < rpw; r += RPS) {
 		const int row = row0 + r + sub;
-		float g = qseg<WT>::dot(G + (size_t)row * rb, xr);
-		float u = qseg<WT>::dot(U + (size_t)row * rb, xr);
+		float g = qseg<WT>::dot(G + (size_t)row * rb, xr, xs0, xs1);
+		float u = qseg<WT>::dot(U + (size_t)row * rb, xr, xs0, xs1);
 		g = group_sum<C>(g);
 		u = group_sum<C>(u);
 		if (seg == 0)
@@ -206,11 +207,12 @@ __global__ __launch_bounds__(256) void k_down(const uint8_t *__restrict__ down,
 
 	float xr[64];
 	load_x64(h + (size_t)p * EI + seg * MOE_SEG_COLS, xr);
+	const float xs0 = sum32(xr), xs1 = sum32(xr + 32);
 
 	const int row0 = (blockIdx.x * 4 + wave) * rpw;
 	for (int r = 0; r < rpw; r += RPS) {
 		const int row = row0 + r + sub;
-		float y = group_sum<C>(qseg<WT>::dot(D + (size_t)row * rb, xr));
+		float y = group_sum<C>(qseg<WT>::dot(D + (size_t)row * rb, xr, xs0, xs1));
 		if (lane % C == 0)
 			ypart[((size_t)p * kch + kc) * E + row] = y;
 	}

@@ -340,14 +340,23 @@ def test_gpu_deterministic_and_token_permutation():
 
 
 def test_gpu_decode_equals_batched():
-    say("T=1 calls vs one T=16 call (olmoe_q8)")
+    say("T=1 calls vs one T=16 call on the GEMV and grouped paths (olmoe_q8)")
     lay = gpu_layer("olmoe_q8")
     x = hipmoe.synth_input(SEED, 501, 16, 2048)
-    batched, ib, wb = lay.ffn(x)
+    try:
+        lay.set_path(hipmoe.PATH_GEMV)
+        gemv, ig, wg = lay.ffn(x)
+        lay.set_path(hipmoe.PATH_AUTO)
+        assert lay.path_for(16) == hipmoe.PATH_GROUPED
+        grouped, ib, wb = lay.ffn(x)
+    finally:
+        lay.set_path(hipmoe.PATH_AUTO)
+    assert np.array_equal(ig, ib) and np.array_equal(bits(wg), bits(wb))
     for t in range(16):
         o, i, w = lay.ffn(x[t:t + 1])
         assert np.array_equal(i[0], ib[t]) and np.array_equal(bits(w[0]), bits(wb[t]))
-        assert rel_l2(o[0], batched[t]) <= TIGHT
+        assert rel_l2(o[0], gemv[t]) <= TIGHT
+        assert rel_l2(o[0], grouped[t]) <= REL_L2_TOL
 
 
 def test_gpu_dev_entry_matches_host_entry():
@@ -440,6 +449,8 @@ def test_gpu_graph_replays_match_eager():
 
 
 def test_gpu_mixtral_fused_T2_and_T32():
-    say("mixtral_q4 T=2 and T=32 (persistent path)")
-    _check_layer_vs_oracle("mixtral_q4", 2, 603)
-    _check_layer_vs_oracle("mixtral_q4", 32, 604)
+    say("mixtral_q4 T=2 and T=4 (persistent path), T=32 forced onto it")
+    _check_layer_vs_oracle("mixtral_q4", 2, 603, expect_path=hipmoe.PATH_DECODE)
+    _check_layer_vs_oracle("mixtral_q4", 4, 605, expect_path=hipmoe.PATH_DECODE)
+    _check_layer_vs_oracle("mixtral_q4", 32, 604, path=hipmoe.PATH_DECODE,
+                           expect_path=hipmoe.PATH_DECODE)
