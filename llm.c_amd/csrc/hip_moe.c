@@ -50,6 +50,7 @@ struct hip_moe_layer {
 	int *d_rows;        /* grouped path: sorted pair per row, -1 = padding */
 	int *d_tile_e;      /* grouped path: expert of each m-tile, -1 = unused */
 	void *d_h16;        /* grouped path: f16 h in sorted row order */
+	void *d_xh;         /* grouped path: tokens rounded to f16 [T][E] */
 
 	/* staging for the host-pointer entry point */
 	size_t cap_io;
@@ -117,6 +118,7 @@ void hip_moe_free(hip_moe_layer *L)
 	hipFree(L->d_rows);
 	hipFree(L->d_tile_e);
 	hipFree(L->d_h16);
+	hipFree(L->d_xh);
 	hipFree(L->d_x);
 	hipFree(L->d_out);
 	hipFree(L->d_bias);
@@ -186,11 +188,15 @@ hip_moe_layer *hip_moe_upload(const float *gate_inp, const void *const *gate_e,
 	HIPCHK(hipGetDevice(&L->device), "hipGetDevice");
 	HIPCHK(hipStreamCreateWithFlags(&L->stream, hipStreamNonBlocking), "hipStreamCreate");
 	HIPCHK(hipMalloc((void **)&L->d_router, NE * E * sizeof(float)), "hipMalloc(router)");
-	HIPCHK(hipMalloc((void **)&L->d_weights, NE * (2 * L->gu_stride + L->down_stride)),
+	/* + slack: the grouped GEMMs load 16-byte chunks that may run up to 12
+	 * bytes past the last row */
+	HIPCHK(hipMalloc((void **)&L->d_weights,
+			 NE * (2 * L->gu_stride + L->down_stride) + MOE_WEIGHT_SLACK),
 	       "hipMalloc(experts)");
 	L->d_gate = L->d_weights;
 	L->d_up = L->d_gate + NE * L->gu_stride;
 	L->d_down = L->d_up + NE * L->gu_stride;
+	HIPCHK(hipMemset(L->d_down + NE * L->down_stride, 0, MOE_WEIGHT_SLACK), "clear slack");
 
 	HIPCHK(hipMemcpy(L->d_router, gate_inp, NE * E * sizeof(float), hipMemcpyHostToDevice),
 	       "upload router");
@@ -231,6 +237,8 @@ static int ensure_scratch(hip_moe_layer *L, size_t T)
 	hipFree(L->d_rows);
 	hipFree(L->d_tile_e);
 	hipFree(L->d_h16);
+	hipFree(L->d_xh);
+	L->d_xh = NULL;
 	L->d_rows = NULL;
 	L->d_tile_e = NULL;
 	L->d_h16 = NULL;
@@ -265,6 +273,7 @@ static int ensure_scratch(hip_moe_layer *L, size_t T)
 				 (size_t)moe_prefill_max_tiles(P, L->NE) * sizeof(int)),
 		       "hipMalloc(tiles)");
 		HIPCHK(hipMalloc(&L->d_h16, rows * L->EI * 2), "hipMalloc(h16)");
+		HIPCHK(hipMalloc(&L->d_xh, T * L->E * 2), "hipMalloc(xh)");
 	}
 	L->cap_T = T;
 	return 1;
@@ -287,11 +296,11 @@ static int check_T(size_t T)
 }
 
 static int route(hip_moe_layer *L, const float *d_x, size_t T, const float *d_bias,
-		 float *d_logits, float *d_probs, uint32_t *d_ids, float *d_w,
+		 float *d_logits, float *d_probs, uint32_t *d_ids, float *d_w, void *d_xh,
 		 hipStream_t s)
 {
 	LCHK(moe_launch_router(d_x, L->d_router, d_bias, d_logits, (int)T, (int)L->E,
-			       (int)L->NE, s), "router");
+			       (int)L->NE, d_xh, s), "router");
 	LCHK(moe_launch_softmax_topk(d_logits, d_probs, d_ids, d_w, (int)T, (int)L->NE,
 				     (int)L->topk, L->renorm, s), "softmax/top-k");
 	return 1;
@@ -308,7 +317,7 @@ int hip_moe_route_dev(hip_moe_layer *L, const float *d_x, size_t T,
 	if (!check_T(T) || !ensure_scratch(L, T))
 		return 0;
 	return route(L, d_x, T, d_router_bias, d_logits ? d_logits : L->d_logits, d_probs,
-		     d_ids, d_w, pick_stream(L, stream));
+		     d_ids, d_w, NULL, pick_stream(L, stream));
 }
 
 /* the path a call of T tokens takes (HIP_MOE_PATH_*), 0 if none applies */
@@ -316,7 +325,8 @@ static int choose_path(const hip_moe_layer *L, size_t T)
 {
 	int dec = L->fused_grid > 0 &&
 		  moe_fused_supported(L->wtype, L->E, L->EI, L->NE, T, L->topk);
-	int grp = moe_prefill_supported(L->wtype, L->E, L->EI, L->NE);
+	int grp = moe_prefill_supported(L->wtype, L->E, L->EI, L->NE) &&
+		  moe_prefill_max_tiles(T * L->topk, L->NE) <= moe_prefill_tile_cap();
 	switch (L->path) {
 	case HIP_MOE_PATH_DECODE:
 		return dec ? HIP_MOE_PATH_DECODE : 0;
@@ -381,10 +391,11 @@ int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 				      L->renorm, L->fused_grid, s), "fused layer");
 		return 1;
 	}
-	if (!route(L, d_x, T, d_router_bias, L->d_logits, NULL, ids, w, s))
+	if (!route(L, d_x, T, d_router_bias, L->d_logits, NULL, ids, w,
+		   path == HIP_MOE_PATH_GROUPED ? L->d_xh : NULL, s))
 		return 0;
 	if (path == HIP_MOE_PATH_GROUPED) {
-		LCHK(moe_launch_prefill(L->wtype, d_x, L->d_gate, L->d_up, L->d_down,
+		LCHK(moe_launch_prefill(L->wtype, L->d_xh, L->d_gate, L->d_up, L->d_down,
 					L->gu_stride, L->down_stride, ids, L->d_rows,
 					L->d_tile_e, L->d_h16, L->d_ypart, (int)T, (int)L->topk,
 					(int)L->E, (int)L->EI, (int)L->NE, s), "grouped GEMMs");

@@ -27,8 +27,9 @@ extern "C" {
 int moe_lanes_per_row(size_t K);
 int moe_kchunks(size_t K);
 
+/* xh (optional, f16 [T][E]): also write the tokens rounded to f16 */
 int moe_launch_router(const float *x, const float *wr, const float *bias,
-                      float *logits, int T, int E, int NE, void *stream);
+                      float *logits, int T, int E, int NE, void *xh, void *stream);
 
 int moe_launch_softmax_topk(const float *logits, float *probs, uint32_t *ids,
                             float *w, int T, int NE, int K, int renorm,
@@ -55,11 +56,13 @@ int moe_launch_expf(const float *in, float *out, size_t n, void *stream);
 int moe_launch_copy(const void *src, void *dst, size_t bytes, void *stream);
 
 /* Grouped path (moe_prefill.hip): sort by expert + f16 MFMA GEMMs. */
+#define MOE_WEIGHT_SLACK 256 /* bytes readable past the last weight row */
 int moe_prefill_supported(int wtype, size_t E, size_t EI, size_t NE);
 int moe_prefill_max_tiles(size_t P, size_t NE);
 int moe_prefill_tile_rows(void);
+int moe_prefill_tile_cap(void);
 /* ypart[p][E] (no K-chunks) for every pair p; combine with kchunks = 1 */
-int moe_launch_prefill(int wtype, const float *x, const uint8_t *gate, const uint8_t *up,
+int moe_launch_prefill(int wtype, const void *xh, const uint8_t *gate, const uint8_t *up,
                        const uint8_t *down, size_t gu_stride, size_t dn_stride,
                        const uint32_t *ids, int *rows, int *tile_e, void *h16, float *ypart,
                        int T, int K, int E, int EI, int NE, void *stream);

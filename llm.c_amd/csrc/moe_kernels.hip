@@ -31,72 +31,96 @@
  * (dot_f32_f32, matmul.c:91-105; the tiled T>1 path of matmul.c:213-238 keeps
  * the same per-element order), then the lanes meet in the tree
  * ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) of vector_avx2.h:126-132, and the
- * logit is fl(bias + dot) (matmul.c:24-32).  Router rows and tokens pass
- * through LDS in double-buffered chunks of RT_KC columns; a wave reads one
- * token row (broadcast) and 64 router rows (row stride RT_LD: conflict-free).
+ * logit is fl(bias + dot) (matmul.c:24-32).
+ *
+ * Router rows and tokens stream through an LDS ring of RT_NST stages of
+ * RT_KC columns, filled by LDS-DMA loads (global_load_lds_dwordx4, issued
+ * from inline assembly so the K loop alone decides what to wait for):
+ * router rows [64][RT_KC] with 16-byte chunk c of row r at slot
+ * 16r + (c ^ (r & 15)) (a wave reads 64 rows conflict-free), tokens
+ * [RT_TOK][RT_KC] (a wave reads its token row as a broadcast).
  */
-#define RT_TOK 4
-#define RT_KC 128
-#define RT_LD (RT_KC + 4)
+#define RT_TOK 8
+#define RT_KC 64
+#define RT_NST 5
+#define RT_WSZ (64 * RT_KC * 4)
+#define RT_SSZ (RT_WSZ + RT_TOK * RT_KC * 4)
 
-struct router_stage {
-	float4 w[8], x;
-	__device__ inline void load(const float *__restrict__ x_, const float *__restrict__ wr,
-				    int t0, int j0, int T, int E, int NE, int c)
-	{
-		const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-		for (int q = 0; q < 8; q++) {
-			const int f = threadIdx.x + 256 * q, row = f >> 5, c4 = f & 31;
-			w[q] = j0 + row < NE ? *(const float4 *)(wr + (size_t)(j0 + row) * E +
-								 c * RT_KC + 4 * c4)
-					     : z;
-		}
-		const int tr = t0 + (threadIdx.x >> 5), c4 = threadIdx.x & 31;
-		x = threadIdx.x < RT_TOK * 32 && tr < T
-			    ? *(const float4 *)(x_ + (size_t)tr * E + c * RT_KC + 4 * c4)
-			    : z;
-	}
-	__device__ inline void store(float *sw, float *sx) const
-	{
-#pragma unroll
-		for (int q = 0; q < 8; q++) {
-			const int f = threadIdx.x + 256 * q;
-			*(float4 *)(sw + (f >> 5) * RT_LD + 4 * (f & 31)) = w[q];
-		}
-		if (threadIdx.x < RT_TOK * 32)
-			*(float4 *)(sx + (threadIdx.x >> 5) * RT_LD + 4 * (threadIdx.x & 31)) = x;
-	}
-};
+__device__ static inline void rt_dma16(const void *sbase, u32 voff, u32 lds)
+{
+	asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+		     :
+		     : "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds))
+		     : "memory", "m0");
+}
 
-__global__ __launch_bounds__(256) void k_router(const float *__restrict__ x,
+template <int N>
+__device__ static inline void rt_wait_vm()
+{
+	static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+	__builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+__global__ __launch_bounds__(RT_TOK * 64) void k_router(const float *__restrict__ x,
 						const float *__restrict__ wr,
 						const float *__restrict__ bias,
-						float *__restrict__ logits, int T, int E, int NE)
+						float *__restrict__ logits, int T, int E, int NE,
+						_Float16 *__restrict__ xh)
 {
-	__shared__ __attribute__((aligned(16))) float sw[2][64 * RT_LD];
-	__shared__ __attribute__((aligned(16))) float sx[2][RT_TOK * RT_LD];
+	__shared__ __attribute__((aligned(16))) uint8_t ring[RT_NST * RT_SSZ];
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 	const int t0 = blockIdx.x * RT_TOK, j0 = blockIdx.y * 64;
+	const int t = t0 + wave, j = j0 + lane;
 	const int nc = E / RT_KC;
+	const u32 l0 = (u32)(uintptr_t)(const __attribute__((address_space(3))) char *)ring;
+
+	/* this lane's loads: RT_WQ router chunks (rows r, swizzled chunks) and,
+	 * for lanes < 16, a 16-byte chunk of its wave's token row */
+	constexpr int RT_WQ = 16 / RT_TOK; /* the 64 x RT_KC tile is 16 KB */
+	u32 woff[RT_WQ];
+#pragma unroll
+	for (int q = 0; q < RT_WQ; q++) {
+		const int f = (wave * RT_WQ + q) * 64 + lane, r = f >> 4, c = (f & 15) ^ (r & 15);
+		woff[q] = (u32)(((size_t)(j0 + r < NE ? j0 + r : 0) * E) * 4 + 16 * c);
+	}
+	const u32 xoff = (u32)((size_t)(t < T ? t : 0) * E * 4 + 16 * (lane & 15));
+	auto issue = [&](int s) {
+		const u32 st = l0 + (u32)((s % RT_NST) * RT_SSZ);
+		const float *wb = wr + (size_t)s * RT_KC, *xb = x + (size_t)s * RT_KC;
+#pragma unroll
+		for (int q = 0; q < RT_WQ; q++)
+			rt_dma16(wb, woff[q], st + (u32)((wave * RT_WQ + q) * 1024));
+		if (lane < 16)
+			rt_dma16(xb, xoff, st + RT_WSZ + (u32)(wave * RT_KC * 4));
+	};
+
 	float acc[8];
 #pragma unroll
 	for (int l = 0; l < 8; l++)
 		acc[l] = 0.0f;
-	router_stage st;
-	st.load(x, wr, t0, j0, T, E, NE, 0);
-	st.store(sw[0], sx[0]);
-	__syncthreads();
-	for (int c = 0; c < nc; c++) {
-		const int b = c & 1;
-		if (c + 1 < nc)
-			st.load(x, wr, t0, j0, T, E, NE, c + 1);
-		const float *xr = sx[b] + wave * RT_LD, *wrow = sw[b] + lane * RT_LD;
-#pragma unroll 4
+#pragma unroll
+	for (int s = 0; s < RT_NST - 1; s++)
+		if (s < nc)
+			issue(s);
+	for (int s = 0; s < nc; s++) {
+		if (s + RT_NST - 2 < nc)
+			rt_wait_vm<(RT_NST - 2) * (RT_WQ + 1)>();
+		else
+			rt_wait_vm<0>();
+		__syncthreads(); /* stage s landed for every wave; stage s-1 is free */
+		if (s + RT_NST - 1 < nc)
+			issue(s + RT_NST - 1);
+		const uint8_t *st = ring + (s % RT_NST) * RT_SSZ;
+		const float *xr = (const float *)(st + RT_WSZ) + wave * RT_KC;
+		const uint8_t *wrow = st + lane * (RT_KC * 4);
+		if (xh && blockIdx.y == 0 && t < T)
+			xh[(size_t)t * E + (size_t)s * RT_KC + lane] = (_Float16)xr[lane];
+#pragma unroll
 		for (int k = 0; k < RT_KC; k += 8) {
+			const int c = k >> 2; /* 16-byte chunks c and c+1 */
 			const float4 xa = *(const float4 *)(xr + k), xb = *(const float4 *)(xr + k + 4);
-			const float4 wa = *(const float4 *)(wrow + k),
-				     wb = *(const float4 *)(wrow + k + 4);
+			const float4 wa = *(const float4 *)(wrow + 16 * (c ^ (lane & 15)));
+			const float4 wb = *(const float4 *)(wrow + 16 * ((c + 1) ^ (lane & 15)));
 			acc[0] = __builtin_fmaf(xa.x, wa.x, acc[0]);
 			acc[1] = __builtin_fmaf(xa.y, wa.y, acc[1]);
 			acc[2] = __builtin_fmaf(xa.z, wa.z, acc[2]);
@@ -106,11 +130,7 @@ __global__ __launch_bounds__(256) void k_router(const float *__restrict__ x,
 			acc[6] = __builtin_fmaf(xb.z, wb.z, acc[6]);
 			acc[7] = __builtin_fmaf(xb.w, wb.w, acc[7]);
 		}
-		if (c + 1 < nc)
-			st.store(sw[b ^ 1], sx[b ^ 1]);
-		__syncthreads();
 	}
-	const int t = t0 + wave, j = j0 + lane;
 	if (t < T && j < NE) {
 		const float d = ((acc[0] + acc[4]) + (acc[2] + acc[6])) +
 				((acc[1] + acc[5]) + (acc[3] + acc[7]));
@@ -279,13 +299,13 @@ extern "C" int moe_kchunks(size_t K)
 }
 
 extern "C" int moe_launch_router(const float *x, const float *wr, const float *bias,
-				 float *logits, int T, int E, int NE, void *stream)
+				 float *logits, int T, int E, int NE, void *xh, void *stream)
 {
-	if (E % RT_KC)
+	if (E % RT_KC || (size_t)NE * E * 4 > 0xffffffffull || (size_t)T * E * 4 > 0xffffffffull)
 		return (int)hipErrorInvalidValue;
 	dim3 grid((T + RT_TOK - 1) / RT_TOK, (NE + 63) / 64);
-	hipLaunchKernelGGL(k_router, grid, dim3(256), 0, (hipStream_t)stream, x, wr,
-			   bias, logits, T, E, NE);
+	hipLaunchKernelGGL(k_router, grid, dim3(RT_TOK * 64), 0, (hipStream_t)stream, x, wr,
+			   bias, logits, T, E, NE, (_Float16 *)xh);
 	return (int)hipGetLastError();
 }
 

@@ -6,10 +6,11 @@
  *                  expert into m-tiles of PF_MT rows (the tail of each
  *                  expert's last tile is padding, row id -1), and the tile
  *                  table tile -> expert.
- *   k_pf_gateup    per (m-tile, 128 h columns): G = X Wg^T and U = X Wu^T
+ *   k_pf_gateup    per (m-tile, 256 h columns): G = X Wg^T and U = X Wu^T
  *                  over d_model, h = silu(G) * U  (nn.c:460-478), stored f16
- *                  in sorted row order.
- *   k_pf_down      per (m-tile, 256 output columns): Y = H Wd^T over d_ff,
+ *                  in sorted row order.  X is the f16 copy of the tokens the
+ *                  router kernel writes.
+ *   k_pf_down      per (m-tile, 512 output columns): Y = H Wd^T over d_ff,
  *                  written fp32 to ypart[pair][E]; k_combine then adds the
  *                  slots of each token in order, out += y / (1/w)
  *                  (olmoe.c:401-403).
@@ -42,10 +43,6 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 #define PF_MT 64            /* rows (pairs) per m-tile */
 #define PF_KB 64            /* k per pipeline step: two blocks */
-#define PF_THREADS 256
-#define PF_LDA (PF_KB + 8)  /* halves per LDS row of the activation tile */
-#define PF_GU_COLS 128      /* h columns per gate/up workgroup, 32 per wave */
-#define PF_DN_COLS 256      /* output columns per down workgroup, 64 per wave */
 #define SORT_THREADS 1024
 
 /* ---------------------------------------------------------------------- */
@@ -53,40 +50,41 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 /* ---------------------------------------------------------------------- */
 
 /*
- * One workgroup.  Pairs keep their order inside an expert (stable), so the
- * layout is a deterministic function of ids.  rows[] gets Tmax*PF_MT entries
- * (padding -1) and tile_e[] Tmax entries (-1 past the last tile): every
- * entry is rewritten on every call.
- *
- * Thread (e, c) = (tid % NE, tid / NE) owns expert e in chunk c of each
- * segment of SORT_SEG pairs (ids staged in LDS as bytes): it counts its
- * expert's pairs in the chunk, takes the exclusive sum of the counts of the
- * earlier chunks, and writes its pairs' rows in order.
+ * One workgroup.  Counts per expert, tiles per expert (exclusive scan), the
+ * tile table, padding rows (-1), then every pair's row: toff[e] * PF_MT + a
+ * slot taken with an LDS atomic.  The order of the pairs inside an expert
+ * may differ between calls, but the results do not: every output row of
+ * the GEMMs depends only on its own activation row (the row's MFMA sums do
+ * not involve the other rows of its tile).  rows[] gets Tmax*PF_MT entries
+ * and tile_e[] Tmax entries (-1 past the last tile), all rewritten on every
+ * call.
  */
-#define SORT_SEG 16384
+#define SORT_MAX_TILES 8704 /* Tmax for T*K up to 2^19 pairs and NE <= 256 */
 
 __global__ __launch_bounds__(SORT_THREADS) void k_moe_sort(const u32 *__restrict__ ids, int P,
 							   int NE, int Tmax,
 							   int *__restrict__ rows,
 							   int *__restrict__ tile_e)
 {
-	__shared__ int cnt[MOE_MAX_NE], toff[MOE_MAX_NE + 1], run[MOE_MAX_NE];
-	__shared__ int ccnt[SORT_THREADS];
-	__shared__ __attribute__((aligned(16))) uint8_t sid[SORT_SEG];
+	__shared__ int cnt[MOE_MAX_NE], toff[MOE_MAX_NE + 1], fill[MOE_MAX_NE];
+	__shared__ short stile[SORT_MAX_TILES];
 	const int tid = threadIdx.x;
-	const int C = SORT_THREADS / NE; /* chunks per segment */
-	const int e = tid % NE, c = tid / NE;
-	const bool owner = c < C;
 
 	for (int i = tid; i < NE; i += SORT_THREADS) {
 		cnt[i] = 0;
-		run[i] = 0;
+		fill[i] = 0;
 	}
 	__syncthreads();
-	for (int p = tid; p < P; p += SORT_THREADS) {
-		const u32 v = ids[p];
-		if (v < (u32)NE) /* always, for ids from the top-k kernel */
-			atomicAdd(&cnt[v], 1);
+	/* counts: 16 ids per thread and round, loaded together */
+	for (int p0 = 16 * tid; p0 < P; p0 += 16 * SORT_THREADS) {
+		u32 v[16];
+#pragma unroll
+		for (int k = 0; k < 16; k++)
+			v[k] = p0 + k < P ? ids[p0 + k] : 0xffffffffu;
+#pragma unroll
+		for (int k = 0; k < 16; k++)
+			if (v[k] < (u32)NE) /* always, for ids from the top-k kernel */
+				atomicAdd(&cnt[v[k]], 1);
 	}
 	__syncthreads();
 	if (tid < WAVE) { /* exclusive scan of tiles per expert, 4 experts per lane */
@@ -118,58 +116,40 @@ __global__ __launch_bounds__(SORT_THREADS) void k_moe_sort(const u32 *__restrict
 	}
 	__syncthreads();
 	const int ntiles = toff[NE];
-	/* tile table and padding rows */
-	for (int i = tid; i < Tmax * PF_MT; i += SORT_THREADS) {
-		const int tile = i / PF_MT;
+	/* tile table: the expert of each tile (largest e with toff[e] <= tile) */
+	for (int tl = tid; tl < Tmax; tl += SORT_THREADS) {
 		int ex = -1;
-		if (tile < ntiles) { /* largest ex with toff[ex] <= tile */
+		if (tl < ntiles) {
 			int lo = 0, hi = NE - 1;
 			while (lo < hi) {
 				const int mid = (lo + hi + 1) >> 1;
-				if (toff[mid] <= tile)
+				if (toff[mid] <= tl)
 					lo = mid;
 				else
 					hi = mid - 1;
 			}
 			ex = lo;
 		}
-		if (i % PF_MT == 0)
-			tile_e[tile] = ex;
+		stile[tl] = (short)ex;
+		tile_e[tl] = ex;
+	}
+	__syncthreads();
+	/* padding rows */
+	for (int i = tid; i < Tmax * PF_MT; i += SORT_THREADS) {
+		const int ex = stile[i / PF_MT];
 		if (ex < 0 || i - toff[ex] * PF_MT >= cnt[ex])
 			rows[i] = -1;
 	}
-	/* stable scatter, segment by segment */
-	for (int s0 = 0; s0 < P; s0 += SORT_SEG) {
-		const int S = P - s0 < SORT_SEG ? P - s0 : SORT_SEG;
-		__syncthreads(); /* earlier readers of sid / ccnt are done */
-		for (int i = tid; i < S; i += SORT_THREADS) {
-			const u32 v = ids[s0 + i];
-			sid[i] = v < (u32)NE ? (uint8_t)v : (uint8_t)255; /* NE <= 256 */
-		}
-		__syncthreads();
-		const int L = (S + C - 1) / C;
-		const int b0 = c * L, b1 = b0 + L < S ? b0 + L : S;
-		int n = 0;
-		if (owner)
-			for (int i = b0; i < b1; i++)
-				n += sid[i] == (uint8_t)e;
-		ccnt[tid] = n;
-		__syncthreads();
-		if (owner) {
-			int pos = toff[e] * PF_MT + run[e];
-			for (int cc = 0; cc < c; cc++)
-				pos += ccnt[cc * NE + e];
-			for (int i = b0; i < b1; i++)
-				if (sid[i] == (uint8_t)e)
-					rows[pos++] = s0 + i;
-		}
-		__syncthreads();
-		if (tid < NE) {
-			int tot = 0;
-			for (int cc = 0; cc < C; cc++)
-				tot += ccnt[cc * NE + tid];
-			run[tid] += tot;
-		}
+	/* every pair's row */
+	for (int p0 = 16 * tid; p0 < P; p0 += 16 * SORT_THREADS) {
+		u32 v[16];
+#pragma unroll
+		for (int k = 0; k < 16; k++)
+			v[k] = p0 + k < P ? ids[p0 + k] : 0xffffffffu;
+#pragma unroll
+		for (int k = 0; k < 16; k++)
+			if (v[k] < (u32)NE)
+				rows[toff[v[k]] * PF_MT + atomicAdd(&fill[v[k]], 1)] = p0 + k;
 	}
 }
 
@@ -274,172 +254,189 @@ template <int ODD> struct bsrc<2, ODD> { /* Q4_0 */
 	}
 };
 
-/* the raw weights of one pipeline step: blocks 2s (even) and 2s+1 (odd) of
- * NG row groups of 32 rows */
-template <int WT, int NG> struct bstep {
-	bsrc<WT, 0> ev[NG];
-	bsrc<WT, 1> od[NG];
-	__device__ inline void load(const uint8_t *const (&row)[NG], int s, int h)
-	{
-		constexpr int BB = bsrc<WT, 0>::BB;
-#pragma unroll
-		for (int g = 0; g < NG; g++) {
-			ev[g].load(row[g] + (size_t)(2 * s) * BB, h);
-			od[g].load(row[g] + (size_t)(2 * s + 1) * BB, h);
-		}
-	}
-};
-
 /* ---------------------------------------------------------------------- */
-/* the MFMA step shared by both GEMMs                                      */
+/* the grouped GEMMs                                                       */
 /* ---------------------------------------------------------------------- */
-
-/* acc[mb][g] += A[mb-th 32 rows][64 k of this step] . B_g, A from LDS */
-template <int WT, int NG>
-__device__ static inline void mfma_step(const _Float16 *sa, const bstep<WT, NG> &B,
-					floatx16 (&acc)[2][NG], int lane)
-{
-	const int h = lane >> 5, r = lane & 31;
-#pragma unroll
-	for (int bb = 0; bb < 2; bb++) {
-		half8_t bk[NG][2];
-#pragma unroll
-		for (int g = 0; g < NG; g++) {
-			if (bb == 0)
-				B.ev[g].operands(bk[g][0], bk[g][1]);
-			else
-				B.od[g].operands(bk[g][0], bk[g][1]);
-		}
-#pragma unroll
-		for (int kh = 0; kh < 2; kh++) {
-#pragma unroll
-			for (int mb = 0; mb < 2; mb++) {
-				const half8_t a = *(const half8_t *)(sa + (mb * 32 + r) * PF_LDA +
-								     bb * 32 + kh * 16 + 8 * h);
-#pragma unroll
-				for (int g = 0; g < NG; g++)
-					acc[mb][g] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-						a, bk[g][kh], acc[mb][g], 0, 0, 0);
-			}
-		}
-	}
-}
-
-/* ---------------------------------------------------------------------- */
-/* activation tiles                                                        */
-/* ---------------------------------------------------------------------- */
-
-/* gate/up: thread -> tile row tid/4, 16 k at 16*(tid%4) of the step, from
- * the fp32 token row of the pair (zeros for padding) */
-struct xtile {
-	float4 v[4];
-	__device__ inline void load(const float *src, int s)
-	{
-		if (!src) {
-#pragma unroll
-			for (int i = 0; i < 4; i++)
-				v[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-			return;
-		}
-		const float4 *p = (const float4 *)(src + (size_t)s * PF_KB);
-#pragma unroll
-		for (int i = 0; i < 4; i++)
-			v[i] = p[i];
-	}
-	__device__ inline void store(_Float16 *dst) const
-	{
-		half8_t a, b;
-		a[0] = (_Float16)v[0].x; a[1] = (_Float16)v[0].y; a[2] = (_Float16)v[0].z;
-		a[3] = (_Float16)v[0].w; a[4] = (_Float16)v[1].x; a[5] = (_Float16)v[1].y;
-		a[6] = (_Float16)v[1].z; a[7] = (_Float16)v[1].w;
-		b[0] = (_Float16)v[2].x; b[1] = (_Float16)v[2].y; b[2] = (_Float16)v[2].z;
-		b[3] = (_Float16)v[2].w; b[4] = (_Float16)v[3].x; b[5] = (_Float16)v[3].y;
-		b[6] = (_Float16)v[3].z; b[7] = (_Float16)v[3].w;
-		*(half8_t *)dst = a;
-		*(half8_t *)(dst + 8) = b;
-	}
-};
-
-/* down: the same 64 x 64 tile of h, already f16 */
-struct htile {
-	half8_t v[2];
-	__device__ inline void load(const _Float16 *src, int s)
-	{
-		const half8_t *p = (const half8_t *)(src + (size_t)s * PF_KB);
-		v[0] = p[0];
-		v[1] = p[1];
-	}
-	__device__ inline void store(_Float16 *dst) const
-	{
-		*(half8_t *)dst = v[0];
-		*(half8_t *)(dst + 8) = v[1];
-	}
-};
 
 /*
- * The K loop: activation tile double-buffered in LDS, weights of the next
- * step loaded into registers while this step's MFMAs run.
+ * One workgroup of 8 waves per CU computes a 64-row m-tile against 512
+ * weight rows (2 groups of 32 rows per wave) over the whole K.  Each K-step
+ * (PF_KB = 64: two GGML blocks per row) goes through an LDS ring of NSTAGE
+ * stages filled by LDS-DMA loads (global_load_lds: no registers, so
+ * NSTAGE - 1 stages stay in flight):
+ *   B part: the raw blocks of the 512 rows, [row][16-byte chunks];
+ *   A part: 64 rows x 64 f16 activations, 16-byte chunk c of row r at slot
+ *           8r + (c ^ (r & 7)) (conflict-free MFMA operand reads).
+ * The loads are issued from inline assembly, so the compiler neither tracks
+ * nor waits for them; the K loop waits itself: vmcnt counts this wave's
+ * loads and retires them in issue order, and a barrier then makes every
+ * wave's part of the stage visible.
  */
-template <int WT, int NG, typename ATile, typename ASrc>
-__device__ static inline void gemm_loop(_Float16 (*sa)[PF_MT * PF_LDA], ASrc asrc,
-					const uint8_t *const (&brow)[NG], int nsteps,
-					floatx16 (&acc)[2][NG])
+#define PF_WAVES 8
+#define PF_BROWS 512 /* weight rows per workgroup */
+
+template <int WT> struct pf_geo {
+	static constexpr int BB = WT == 1 ? 34 : 18;    /* block bytes */
+	static constexpr int RBS = 2 * BB;               /* bytes of a row per stage */
+	/* 16-byte chunks loaded per row and stage: they cover the RBS bytes and
+	 * run up to 12 bytes into the next stage's (the weights allocation
+	 * carries slack for the last row) */
+	static constexpr int NCH = (RBS + 15) / 16;
+	static constexpr int RBL = 16 * NCH;             /* LDS bytes per row */
+	static constexpr int JB = PF_BROWS * NCH / (PF_WAVES * WAVE); /* B loads per wave */
+	static constexpr int BSZ = PF_BROWS * RBL;       /* B bytes per stage */
+	static constexpr int ASZ = PF_MT * PF_KB * 2;    /* A bytes per stage */
+	static constexpr int SSZ = BSZ + ASZ;
+	static constexpr int NSTAGE = WT == 1 ? 3 : 4;
+	static constexpr int LOADS = JB + 1;             /* loads per wave per stage */
+};
+
+/* one LDS-DMA load per lane: 16 bytes from sbase + voff into LDS at
+ * lds + 16 * lane (lds wave-uniform) */
+__device__ static inline void dma_dwordx4(const void *sbase, u32 voff, u32 lds)
 {
-	const int lane = threadIdx.x & 63, h = lane >> 5;
-	_Float16 *adst0 = sa[0] + (threadIdx.x >> 2) * PF_LDA + 16 * (threadIdx.x & 3);
-	_Float16 *adst1 = sa[1] + (threadIdx.x >> 2) * PF_LDA + 16 * (threadIdx.x & 3);
-	ATile at;
-	bstep<WT, NG> b0, b1;
-	at.load(asrc, 0);
-	b0.load(brow, 0, h);
-	at.store(adst0);
-	__syncthreads();
-	for (int s = 0; s < nsteps; s += 2) {
-		const bool more1 = s + 1 < nsteps;
-		if (more1) {
-			at.load(asrc, s + 1);
-			b1.load(brow, s + 1, h);
-		}
-		mfma_step<WT, NG>(sa[0], b0, acc, lane);
-		if (more1)
-			at.store(adst1);
-		__syncthreads();
-		if (!more1)
-			break;
-		const bool more2 = s + 2 < nsteps;
-		if (more2) {
-			at.load(asrc, s + 2);
-			b0.load(brow, s + 2, h);
-		}
-		mfma_step<WT, NG>(sa[1], b1, acc, lane);
-		if (more2)
-			at.store(adst0);
-		__syncthreads();
+	asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+		     :
+		     : "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds))
+		     : "memory", "m0");
+}
+
+/* wait until at most N of this wave's vector memory operations are pending */
+template <int N>
+__device__ static inline void wait_vm()
+{
+	static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+	__builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+__device__ static inline u32 lds_addr(const void *p)
+{
+	return (u32)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
+}
+
+/* acc[mb][g] += A[mb-th 32 rows] . B_g over one stage */
+template <int WT>
+__device__ static inline void pf_stage_mfma(const uint8_t *sb, const _Float16 *sa,
+					    const int (&brow)[2], floatx16 (&acc)[2][2], int lane)
+{
+	typedef pf_geo<WT> GG;
+	const int h = lane >> 5, r = lane & 31;
+	half8_t bk[2][2][2]; /* [block][group][k-half] */
+#pragma unroll
+	for (int g = 0; g < 2; g++) {
+		const uint8_t *row = sb + brow[g] * GG::RBL;
+		bsrc<WT, 0> ev;
+		bsrc<WT, 1> od;
+		ev.load(row, h);
+		od.load(row + GG::BB, h);
+		ev.operands(bk[0][g][0], bk[0][g][1]);
+		od.operands(bk[1][g][0], bk[1][g][1]);
+	}
+#pragma unroll
+	for (int bb = 0; bb < 2; bb++)
+#pragma unroll
+		for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+			for (int mb = 0; mb < 2; mb++) {
+				const int ar = mb * 32 + r, c = bb * 4 + kh * 2 + h;
+				const half8_t a = *(const half8_t *)(sa + 8 * (ar * 8 + (c ^ (ar & 7))));
+#pragma unroll
+				for (int g = 0; g < 2; g++)
+					acc[mb][g] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+						a, bk[bb][g][kh], acc[mb][g], 0, 0, 0);
+			}
+}
+
+/*
+ * The K loop.  wbase: weights base (SGPR); woff[j]: this lane's byte offset
+ * of load j of stage 0 (row base + dword); abase/aoff the same for A.  Stage
+ * s adds s * RBS (weights) and s * 128 (A) to the bases.
+ */
+template <int WT>
+__device__ static inline void pf_kloop(uint8_t *lds, const uint8_t *wbase,
+				       const u32 (&woff)[pf_geo<WT>::JB], const uint8_t *abase,
+				       u32 aoff, const int (&brow)[2], int nsteps,
+				       floatx16 (&acc)[2][2])
+{
+	typedef pf_geo<WT> GG;
+	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+	const u32 l0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+	auto issue = [&](int s) {
+		const u32 st = l0 + (u32)((s % GG::NSTAGE) * GG::SSZ);
+		const uint8_t *wb = wbase + (size_t)s * GG::RBS;
+#pragma unroll
+		for (int j = 0; j < GG::JB; j++)
+			dma_dwordx4(wb, woff[j], st + (u32)((wave * GG::JB + j) * 1024));
+		dma_dwordx4(abase + (size_t)s * 128, aoff, st + GG::BSZ + (u32)(wave * 1024));
+	};
+#pragma unroll
+	for (int s = 0; s < GG::NSTAGE - 1; s++)
+		if (s < nsteps)
+			issue(s);
+	for (int s = 0; s < nsteps; s++) {
+		if (s + GG::NSTAGE - 2 < nsteps)
+			wait_vm<(GG::NSTAGE - 2) * GG::LOADS>();
+		else
+			wait_vm<0>();
+		__syncthreads(); /* stage s landed for every wave; stage s-1 is free */
+		if (s + GG::NSTAGE - 1 < nsteps)
+			issue(s + GG::NSTAGE - 1);
+		const uint8_t *sb = lds + (s % GG::NSTAGE) * GG::SSZ;
+		pf_stage_mfma<WT>(sb, (const _Float16 *)(sb + GG::BSZ), brow, acc, lane);
 	}
 }
 
-/* ---------------------------------------------------------------------- */
-/* GEMM kernels                                                            */
-/* ---------------------------------------------------------------------- */
+/* this lane's part of the loads: weight row and 16-byte chunk of load j
+ * (flat chunk f of the stage's [PF_BROWS][NCH] block) and the A chunk
+ * (slot -> row, chunk) */
+template <int WT> struct pf_lanes {
+	int wrow[pf_geo<WT>::JB], wch[pf_geo<WT>::JB];
+	int arow, achunk;
+	__device__ inline pf_lanes()
+	{
+		typedef pf_geo<WT> GG;
+		const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+		for (int j = 0; j < GG::JB; j++) {
+			const int f = (wave * GG::JB + j) * WAVE + lane;
+			wrow[j] = f / GG::NCH;
+			wch[j] = f % GG::NCH;
+		}
+		const int slot = wave * WAVE + lane;
+		arow = slot >> 3;
+		achunk = (slot & 7) ^ (arow & 7);
+	}
+};
 
 template <int WT>
-__global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_pf_gateup(
-	const float *__restrict__ x, const uint8_t *__restrict__ gate,
-	const uint8_t *__restrict__ up, size_t gu_stride, const int *__restrict__ rows,
-	const int *__restrict__ tile_e, int K, int E, int EI, _Float16 *__restrict__ h)
+__global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_gateup(
+	const _Float16 *__restrict__ xh, const uint8_t *__restrict__ gate, size_t up_off,
+	size_t gu_stride, const int *__restrict__ rows, const int *__restrict__ tile_e, int K,
+	int E, int EI, _Float16 *__restrict__ h)
 {
-	__shared__ __attribute__((aligned(16))) _Float16 sa[2][PF_MT * PF_LDA];
+	typedef pf_geo<WT> GG;
+	__shared__ __attribute__((aligned(16))) uint8_t lds[GG::NSTAGE * GG::SSZ];
 	const int tile = blockIdx.y;
 	const int e = tile_e[tile];
 	if (e < 0)
 		return;
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-	const size_t rb = (size_t)(E / MOE_QK) * bsrc<WT, 0>::BB;
-	const int col = blockIdx.x * PF_GU_COLS + wave * 32 + (lane & 31);
-	const uint8_t *const brow[2] = {gate + (size_t)e * gu_stride + (size_t)col * rb,
-					up + (size_t)e * gu_stride + (size_t)col * rb};
-	const int p = rows[tile * PF_MT + (threadIdx.x >> 2)];
-	const float *asrc = p >= 0 ? x + (size_t)(p / K) * E + 16 * (threadIdx.x & 3) : nullptr;
+	const int n0 = blockIdx.x * (PF_BROWS / 2);
+	const size_t rb = (size_t)(E / MOE_QK) * GG::BB;
+	pf_lanes<WT> L;
+	/* weight rows 0..255: gate rows n0.., 256..511: up rows n0.. (offsets
+	 * from the gate base; up = gate + up_off) */
+	u32 woff[GG::JB];
+#pragma unroll
+	for (int j = 0; j < GG::JB; j++) {
+		const int r = L.wrow[j];
+		const size_t o = (r < 256 ? 0 : up_off) + (size_t)e * gu_stride +
+				 (size_t)(n0 + (r & 255)) * rb + 16 * L.wch[j];
+		woff[j] = (u32)o;
+	}
+	const int p = rows[tile * PF_MT + L.arow];
+	const u32 aoff = (u32)((size_t)(p >= 0 ? p / K : 0) * E * 2 + 16 * L.achunk);
+	const int brow[2] = {wave * 32 + (lane & 31), 256 + wave * 32 + (lane & 31)};
 
 	floatx16 acc[2][2];
 #pragma unroll
@@ -449,9 +446,9 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
 #pragma unroll
 			for (int j = 0; j < 16; j++)
 				acc[mb][g][j] = 0.0f;
-	gemm_loop<WT, 2, xtile>(sa, asrc, brow, E / PF_KB, acc);
+	pf_kloop<WT>(lds, gate, woff, (const uint8_t *)xh, aoff, brow, E / PF_KB, acc);
 
-	const int hh = lane >> 5;
+	const int col = n0 + wave * 32 + (lane & 31), hh = lane >> 5;
 #pragma unroll
 	for (int mb = 0; mb < 2; mb++)
 #pragma unroll
@@ -463,12 +460,13 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
 }
 
 template <int WT>
-__global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_pf_down(
+__global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down(
 	const _Float16 *__restrict__ h, const uint8_t *__restrict__ down, size_t dn_stride,
 	const int *__restrict__ rows, const int *__restrict__ tile_e, int E, int EI,
 	float *__restrict__ ypart)
 {
-	__shared__ __attribute__((aligned(16))) _Float16 sa[2][PF_MT * PF_LDA];
+	typedef pf_geo<WT> GG;
+	__shared__ __attribute__((aligned(16))) uint8_t lds[GG::NSTAGE * GG::SSZ];
 	__shared__ int srow[PF_MT];
 	const int tile = blockIdx.y;
 	const int e = tile_e[tile];
@@ -477,12 +475,16 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 	if (threadIdx.x < PF_MT)
 		srow[threadIdx.x] = rows[tile * PF_MT + threadIdx.x];
-	const size_t rb = (size_t)(EI / MOE_QK) * bsrc<WT, 0>::BB;
-	const int col0 = blockIdx.x * PF_DN_COLS + wave * 64 + (lane & 31);
-	const uint8_t *base = down + (size_t)e * dn_stride;
-	const uint8_t *const brow[2] = {base + (size_t)col0 * rb, base + (size_t)(col0 + 32) * rb};
-	const _Float16 *asrc = h + (size_t)(tile * PF_MT + (threadIdx.x >> 2)) * EI +
-			       16 * (threadIdx.x & 3);
+	const int n0 = blockIdx.x * PF_BROWS;
+	const size_t rb = (size_t)(EI / MOE_QK) * GG::BB;
+	pf_lanes<WT> L;
+	u32 woff[GG::JB];
+#pragma unroll
+	for (int j = 0; j < GG::JB; j++)
+		woff[j] = (u32)((size_t)e * dn_stride + (size_t)(n0 + L.wrow[j]) * rb +
+				16 * L.wch[j]);
+	const u32 aoff = (u32)((size_t)(tile * PF_MT + L.arow) * EI * 2 + 16 * L.achunk);
+	const int brow[2] = {wave * 64 + (lane & 31), wave * 64 + 32 + (lane & 31)};
 
 	floatx16 acc[2][2];
 #pragma unroll
@@ -492,7 +494,7 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
 #pragma unroll
 			for (int j = 0; j < 16; j++)
 				acc[mb][g][j] = 0.0f;
-	gemm_loop<WT, 2, htile>(sa, asrc, brow, EI / PF_KB, acc); /* syncs srow too */
+	pf_kloop<WT>(lds, down, woff, (const uint8_t *)h, aoff, brow, EI / PF_KB, acc); /* syncs srow */
 
 	const int hh = lane >> 5;
 #pragma unroll
@@ -504,7 +506,8 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
 				continue;
 #pragma unroll
 			for (int g = 0; g < 2; g++)
-				ypart[(size_t)pr * E + col0 + 32 * g] = acc[mb][g][j];
+				ypart[(size_t)pr * E + n0 + wave * 64 + 32 * g + (lane & 31)] =
+					acc[mb][g][j];
 		}
 }
 
@@ -514,8 +517,10 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
 
 extern "C" int moe_prefill_supported(int wtype, size_t E, size_t EI, size_t NE)
 {
-	return (wtype == 1 || wtype == 2) && NE <= MOE_MAX_NE && E % PF_DN_COLS == 0 &&
-	       EI % PF_GU_COLS == 0 && E % PF_KB == 0 && EI % PF_KB == 0;
+	/* offsets from one weights base stay below 4 GB: checked by the caller's
+	 * layer size; n-tiles of 256 h columns and 512 output columns */
+	return (wtype == 1 || wtype == 2) && NE <= MOE_MAX_NE && E % PF_BROWS == 0 &&
+	       EI % (PF_BROWS / 2) == 0 && E % PF_KB == 0 && EI % PF_KB == 0;
 }
 
 extern "C" int moe_prefill_max_tiles(size_t P, size_t NE)
@@ -529,30 +534,46 @@ extern "C" int moe_prefill_tile_rows(void)
 	return PF_MT;
 }
 
-extern "C" int moe_launch_prefill(int wtype, const float *x, const uint8_t *gate,
+/* the largest tile table the sort kernel handles */
+extern "C" int moe_prefill_tile_cap(void)
+{
+	return SORT_MAX_TILES;
+}
+
+extern "C" int moe_launch_prefill(int wtype, const void *xh_, const uint8_t *gate,
 				  const uint8_t *up, const uint8_t *down, size_t gu_stride,
 				  size_t dn_stride, const uint32_t *ids, int *rows, int *tile_e,
 				  void *h16, float *ypart, int T, int K, int E, int EI, int NE,
 				  void *stream)
 {
-	if (!moe_prefill_supported(wtype, (size_t)E, (size_t)EI, (size_t)NE))
+	if (!moe_prefill_supported(wtype, (size_t)E, (size_t)EI, (size_t)NE) || up < gate)
+		return (int)hipErrorInvalidValue;
+	const size_t up_off = (size_t)(up - gate);
+	/* every weight offset a lane forms must fit 32 bits */
+	if (up_off + (size_t)NE * gu_stride > 0xffffffffull ||
+	    (size_t)NE * dn_stride > 0xffffffffull ||
+	    (size_t)T * E * 2 > 0xffffffffull)
 		return (int)hipErrorInvalidValue;
 	hipStream_t s = (hipStream_t)stream;
+	const _Float16 *xh = (const _Float16 *)xh_;
 	const int P = T * K;
 	const int Tmax = moe_prefill_max_tiles((size_t)P, (size_t)NE);
+	if (Tmax > SORT_MAX_TILES || (size_t)Tmax * PF_MT * EI * 2 > 0xffffffffull)
+		return (int)hipErrorInvalidValue;
 	hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(SORT_THREADS), 0, s, ids, P, NE, Tmax, rows,
 			   tile_e);
 	_Float16 *hh = (_Float16 *)h16;
+	const dim3 ggu(EI / (PF_BROWS / 2), Tmax), gdn(E / PF_BROWS, Tmax);
 	if (wtype == 1) {
-		hipLaunchKernelGGL(k_pf_gateup<1>, dim3(EI / PF_GU_COLS, Tmax), dim3(PF_THREADS), 0,
-				   s, x, gate, up, gu_stride, rows, tile_e, K, E, EI, hh);
-		hipLaunchKernelGGL(k_pf_down<1>, dim3(E / PF_DN_COLS, Tmax), dim3(PF_THREADS), 0, s,
-				   hh, down, dn_stride, rows, tile_e, E, EI, ypart);
+		hipLaunchKernelGGL(k_pf_gateup<1>, ggu, dim3(PF_WAVES * WAVE), 0, s, xh, gate, up_off,
+				   gu_stride, rows, tile_e, K, E, EI, hh);
+		hipLaunchKernelGGL(k_pf_down<1>, gdn, dim3(PF_WAVES * WAVE), 0, s, hh, down, dn_stride,
+				   rows, tile_e, E, EI, ypart);
 	} else {
-		hipLaunchKernelGGL(k_pf_gateup<2>, dim3(EI / PF_GU_COLS, Tmax), dim3(PF_THREADS), 0,
-				   s, x, gate, up, gu_stride, rows, tile_e, K, E, EI, hh);
-		hipLaunchKernelGGL(k_pf_down<2>, dim3(E / PF_DN_COLS, Tmax), dim3(PF_THREADS), 0, s,
-				   hh, down, dn_stride, rows, tile_e, E, EI, ypart);
+		hipLaunchKernelGGL(k_pf_gateup<2>, ggu, dim3(PF_WAVES * WAVE), 0, s, xh, gate, up_off,
+				   gu_stride, rows, tile_e, K, E, EI, hh);
+		hipLaunchKernelGGL(k_pf_down<2>, gdn, dim3(PF_WAVES * WAVE), 0, s, hh, down, dn_stride,
+				   rows, tile_e, E, EI, ypart);
 	}
 	return (int)hipGetLastError();
 }
