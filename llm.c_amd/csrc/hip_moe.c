@@ -395,12 +395,14 @@ int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 		   path == HIP_MOE_PATH_GROUPED ? L->d_xh : NULL, s))
 		return 0;
 	if (path == HIP_MOE_PATH_GROUPED) {
+		int split = 1; /* ypart holds kchunks 64-bit entries per (pair, column) */
 		LCHK(moe_launch_prefill(L->wtype, L->d_xh, L->d_gate, L->d_up, L->d_down,
 					L->gu_stride, L->down_stride, ids, L->d_rows,
 					L->d_tile_e, L->d_h16, L->d_ypart, (int)T, (int)L->topk,
-					(int)L->E, (int)L->EI, (int)L->NE, s), "grouped GEMMs");
-		LCHK(moe_launch_combine(L->d_ypart, w, d_out, (int)T, (int)L->topk, (int)L->E, 1,
-					s), "combine");
+					(int)L->E, (int)L->EI, (int)L->NE, 2 * L->kchunks, &split, s),
+		     "grouped GEMMs");
+		LCHK(moe_launch_combine(L->d_ypart, w, d_out, (int)T, (int)L->topk, (int)L->E,
+					split, s), "combine");
 		return 1;
 	}
 	LCHK(moe_launch_gateup(L->wtype, L->d_gate, L->d_up, L->gu_stride, ids, -1, d_x,

@@ -61,11 +61,13 @@ int moe_prefill_supported(int wtype, size_t E, size_t EI, size_t NE);
 int moe_prefill_max_tiles(size_t P, size_t NE);
 int moe_prefill_tile_rows(void);
 int moe_prefill_tile_cap(void);
-/* ypart[p][E] (no K-chunks) for every pair p; combine with kchunks = 1 */
+/* ypart[p][split][E] for every pair p, *split (<= max_split) K-splits of
+ * the down projection; combine with kchunks = *split */
 int moe_launch_prefill(int wtype, const void *xh, const uint8_t *gate, const uint8_t *up,
                        const uint8_t *down, size_t gu_stride, size_t dn_stride,
                        const uint32_t *ids, int *rows, int *tile_e, void *h16, float *ypart,
-                       int T, int K, int E, int EI, int NE, void *stream);
+                       int T, int K, int E, int EI, int NE, int max_split, int *split,
+                       void *stream);
 
 /* One-launch decode layer (moe_decode.hip) for T*K <= MOE_FUSED_MAX_P. */
 int moe_fused_supported(int wtype, size_t E, size_t EI, size_t NE, size_t T, size_t K);

@@ -10,10 +10,12 @@
  *                  over d_model, h = silu(G) * U  (nn.c:460-478), stored f16
  *                  in sorted row order.  X is the f16 copy of the tokens the
  *                  router kernel writes.
- *   k_pf_down      per (m-tile, 512 output columns): Y = H Wd^T over d_ff,
- *                  written fp32 to ypart[pair][E]; k_combine then adds the
- *                  slots of each token in order, out += y / (1/w)
- *                  (olmoe.c:401-403).
+ *   k_pf_down      per (m-tile, 512 output columns, K-split): Y = H Wd^T
+ *                  over d_ff (or one of S consecutive parts of it, when the
+ *                  tiles alone leave the CUs idle), written fp32 to
+ *                  ypart[pair][split][E]; k_combine then adds the splits in
+ *                  order and the slots of each token in order,
+ *                  out += y / (1/w)  (olmoe.c:401-403).
  *
  * The reference computes every (token, expert) product as its own fp32
  * dequant-dot (fused_ffn_silu per token, olmoe.c:364-395, quant.c:103-155).
@@ -278,11 +280,13 @@ template <int ODD> struct bsrc<2, ODD> { /* Q4_0 */
 template <int WT> struct pf_geo {
 	static constexpr int BB = WT == 1 ? 34 : 18;    /* block bytes */
 	static constexpr int RBS = 2 * BB;               /* bytes of a row per stage */
-	/* 16-byte chunks loaded per row and stage: they cover the RBS bytes and
-	 * run up to 12 bytes into the next stage's (the weights allocation
-	 * carries slack for the last row) */
-	static constexpr int NCH = (RBS + 15) / 16;
-	static constexpr int RBL = 16 * NCH;             /* LDS bytes per row */
+	/* 16-byte chunks loaded per row and stage (LDS-DMA writes one 16-byte
+	 * slot per lane): they cover the RBS bytes and run up to 12 bytes into
+	 * the next stage's (the weights allocation carries slack for the last
+	 * row) */
+	static constexpr int CH = 16;                    /* chunk bytes */
+	static constexpr int NCH = (RBS + CH - 1) / CH;
+	static constexpr int RBL = CH * NCH;             /* LDS bytes per row */
 	static constexpr int JB = PF_BROWS * NCH / (PF_WAVES * WAVE); /* B loads per wave */
 	static constexpr int BSZ = PF_BROWS * RBL;       /* B bytes per stage */
 	static constexpr int ASZ = PF_MT * PF_KB * 2;    /* A bytes per stage */
@@ -314,23 +318,23 @@ __device__ static inline u32 lds_addr(const void *p)
 	return (u32)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
 }
 
-/* acc[mb][g] += A[mb-th 32 rows] . B_g over one stage */
+/* acc[mb][g] += A[mb-th 32 rows] . B_g over one stage.  Every LDS read of
+ * the stage is issued first, so the stage waits for LDS once, not once per
+ * operand. */
 template <int WT>
 __device__ static inline void pf_stage_mfma(const uint8_t *sb, const _Float16 *sa,
 					    const int (&brow)[2], floatx16 (&acc)[2][2], int lane)
 {
 	typedef pf_geo<WT> GG;
 	const int h = lane >> 5, r = lane & 31;
-	half8_t bk[2][2][2]; /* [block][group][k-half] */
+	bsrc<WT, 0> ev[2];
+	bsrc<WT, 1> od[2];
+	half8_t a[2][2][2]; /* [block][k-half][mb] */
 #pragma unroll
 	for (int g = 0; g < 2; g++) {
 		const uint8_t *row = sb + brow[g] * GG::RBL;
-		bsrc<WT, 0> ev;
-		bsrc<WT, 1> od;
-		ev.load(row, h);
-		od.load(row + GG::BB, h);
-		ev.operands(bk[0][g][0], bk[0][g][1]);
-		od.operands(bk[1][g][0], bk[1][g][1]);
+		ev[g].load(row, h);
+		od[g].load(row + GG::BB, h);
 	}
 #pragma unroll
 	for (int bb = 0; bb < 2; bb++)
@@ -339,12 +343,27 @@ __device__ static inline void pf_stage_mfma(const uint8_t *sb, const _Float16 *s
 #pragma unroll
 			for (int mb = 0; mb < 2; mb++) {
 				const int ar = mb * 32 + r, c = bb * 4 + kh * 2 + h;
-				const half8_t a = *(const half8_t *)(sa + 8 * (ar * 8 + (c ^ (ar & 7))));
+				a[bb][kh][mb] = *(const half8_t *)(sa + 8 * (ar * 8 + (c ^ (ar & 7))));
+			}
+#pragma unroll
+	for (int bb = 0; bb < 2; bb++) {
+		half8_t bk[2][2]; /* [group][k-half] */
+#pragma unroll
+		for (int g = 0; g < 2; g++) {
+			if (bb == 0)
+				ev[g].operands(bk[g][0], bk[g][1]);
+			else
+				od[g].operands(bk[g][0], bk[g][1]);
+		}
+#pragma unroll
+		for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+			for (int mb = 0; mb < 2; mb++)
 #pragma unroll
 				for (int g = 0; g < 2; g++)
 					acc[mb][g] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-						a, bk[bb][g][kh], acc[mb][g], 0, 0, 0);
-			}
+						a[bb][kh][mb], bk[g][kh], acc[mb][g], 0, 0, 0);
+	}
 }
 
 /*
@@ -366,7 +385,9 @@ __device__ static inline void pf_kloop(uint8_t *lds, const uint8_t *wbase,
 		const uint8_t *wb = wbase + (size_t)s * GG::RBS;
 #pragma unroll
 		for (int j = 0; j < GG::JB; j++)
-			dma_dwordx4(wb, woff[j], st + (u32)((wave * GG::JB + j) * 1024));
+			dma_dwordx4(wb, woff[j], st + (u32)((wave * GG::JB + j) * WAVE * GG::CH));
+		/* every wave issues the same loads per stage (the waits count
+		 * them); lanes of padding rows all read the same 16 bytes */
 		dma_dwordx4(abase + (size_t)s * 128, aoff, st + GG::BSZ + (u32)(wave * 1024));
 	};
 #pragma unroll
@@ -386,9 +407,9 @@ __device__ static inline void pf_kloop(uint8_t *lds, const uint8_t *wbase,
 	}
 }
 
-/* this lane's part of the loads: weight row and 16-byte chunk of load j
- * (flat chunk f of the stage's [PF_BROWS][NCH] block) and the A chunk
- * (slot -> row, chunk) */
+/* this lane's part of the loads: weight row and chunk of load j (flat
+ * chunk f of the stage's [PF_BROWS][NCH] block) and the A chunk (slot ->
+ * row, chunk) */
 template <int WT> struct pf_lanes {
 	int wrow[pf_geo<WT>::JB], wch[pf_geo<WT>::JB];
 	int arow, achunk;
@@ -431,11 +452,12 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_gateup(
 	for (int j = 0; j < GG::JB; j++) {
 		const int r = L.wrow[j];
 		const size_t o = (r < 256 ? 0 : up_off) + (size_t)e * gu_stride +
-				 (size_t)(n0 + (r & 255)) * rb + 16 * L.wch[j];
+				 (size_t)(n0 + (r & 255)) * rb + GG::CH * L.wch[j];
 		woff[j] = (u32)o;
 	}
 	const int p = rows[tile * PF_MT + L.arow];
-	const u32 aoff = (u32)((size_t)(p >= 0 ? p / K : 0) * E * 2 + 16 * L.achunk);
+	/* padding rows: one shared 16-byte chunk instead of a row each */
+	const u32 aoff = p >= 0 ? (u32)((size_t)(p / K) * E * 2 + 16 * L.achunk) : 0u;
 	const int brow[2] = {wave * 32 + (lane & 31), 256 + wave * 32 + (lane & 31)};
 
 	floatx16 acc[2][2];
@@ -473,6 +495,8 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down(
 	if (e < 0)
 		return;
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+	const int S = gridDim.z, nst = EI / PF_KB;
+	const int s0 = blockIdx.z * nst / S, s1 = (blockIdx.z + 1) * nst / S;
 	if (threadIdx.x < PF_MT)
 		srow[threadIdx.x] = rows[tile * PF_MT + threadIdx.x];
 	const int n0 = blockIdx.x * PF_BROWS;
@@ -482,8 +506,10 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down(
 #pragma unroll
 	for (int j = 0; j < GG::JB; j++)
 		woff[j] = (u32)((size_t)e * dn_stride + (size_t)(n0 + L.wrow[j]) * rb +
-				16 * L.wch[j]);
-	const u32 aoff = (u32)((size_t)(tile * PF_MT + L.arow) * EI * 2 + 16 * L.achunk);
+				GG::CH * L.wch[j]);
+	const u32 aoff = rows[tile * PF_MT + L.arow] >= 0
+				 ? (u32)((size_t)(tile * PF_MT + L.arow) * EI * 2 + 16 * L.achunk)
+				 : 0u;
 	const int brow[2] = {wave * 64 + (lane & 31), wave * 64 + 32 + (lane & 31)};
 
 	floatx16 acc[2][2];
@@ -494,7 +520,8 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down(
 #pragma unroll
 			for (int j = 0; j < 16; j++)
 				acc[mb][g][j] = 0.0f;
-	pf_kloop<WT>(lds, down, woff, (const uint8_t *)h, aoff, brow, EI / PF_KB, acc); /* syncs srow */
+	pf_kloop<WT>(lds, down + (size_t)s0 * GG::RBS, woff, (const uint8_t *)(h + (size_t)s0 * PF_KB),
+		     aoff, brow, s1 - s0, acc); /* syncs srow */
 
 	const int hh = lane >> 5;
 #pragma unroll
@@ -506,8 +533,8 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down(
 				continue;
 #pragma unroll
 			for (int g = 0; g < 2; g++)
-				ypart[(size_t)pr * E + n0 + wave * 64 + 32 * g + (lane & 31)] =
-					acc[mb][g][j];
+				ypart[((size_t)pr * S + blockIdx.z) * E + n0 + wave * 64 + 32 * g +
+				      (lane & 31)] = acc[mb][g][j];
 		}
 }
 
@@ -544,7 +571,7 @@ extern "C" int moe_launch_prefill(int wtype, const void *xh_, const uint8_t *gat
 				  const uint8_t *up, const uint8_t *down, size_t gu_stride,
 				  size_t dn_stride, const uint32_t *ids, int *rows, int *tile_e,
 				  void *h16, float *ypart, int T, int K, int E, int EI, int NE,
-				  void *stream)
+				  int max_split, int *split, void *stream)
 {
 	if (!moe_prefill_supported(wtype, (size_t)E, (size_t)EI, (size_t)NE) || up < gate)
 		return (int)hipErrorInvalidValue;
@@ -563,7 +590,18 @@ extern "C" int moe_launch_prefill(int wtype, const void *xh_, const uint8_t *gat
 	hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(SORT_THREADS), 0, s, ids, P, NE, Tmax, rows,
 			   tile_e);
 	_Float16 *hh = (_Float16 *)h16;
-	const dim3 ggu(EI / (PF_BROWS / 2), Tmax), gdn(E / PF_BROWS, Tmax);
+	/* split the down projection's K when its (m-tile, column block) grid
+	 * would leave most CUs idle (few tokens per expert, large d_ff) */
+	const int nx = E / PF_BROWS, nst = EI / PF_KB;
+	int S = 512 / (nx * Tmax);
+	if (S > max_split)
+		S = max_split;
+	if (S > nst / 8)
+		S = nst / 8;
+	if (S < 1)
+		S = 1;
+	*split = S;
+	const dim3 ggu(EI / (PF_BROWS / 2), Tmax), gdn(nx, Tmax, S);
 	if (wtype == 1) {
 		hipLaunchKernelGGL(k_pf_gateup<1>, ggu, dim3(PF_WAVES * WAVE), 0, s, xh, gate, up_off,
 				   gu_stride, rows, tile_e, K, E, EI, hh);
