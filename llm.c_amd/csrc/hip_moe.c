@@ -1,8 +1,9 @@
 /*
  * hip_moe.c - thin C host layer of the MI355X MoE FFN (see include/hip_moe.h).
  *
- * Owns device residency of one layer's weights (uploaded once, GGUF block
- * layout unchanged), per-layer scratch, and the launch sequence
+ * Owns device residency of one layer's weights (uploaded once as GGUF
+ * blocks: gate/up rows unchanged, down matrices regrouped by whole blocks
+ * into panels, see upload_down), per-layer scratch, and the launch sequence
  *   router -> softmax/top-k -> gate/up + SwiGLU -> down -> combine
  * that replaces the per-token loop of moe_ffn (olmoe.c:359-406,
  * llama.c:409-456).  Errors follow the reference's "return 0, caller falls
@@ -27,7 +28,6 @@ struct hip_moe_layer {
 	size_t rb_mid;      /* bytes of one row with EI columns */
 	size_t gu_stride;   /* bytes of one expert's gate (or up) matrix */
 	size_t down_stride; /* bytes of one expert's down matrix */
-	int kchunks;        /* K-chunks of a down row */
 
 	float *d_router;
 	uint8_t *d_weights; /* [gate NE][up NE][down NE] */
@@ -44,7 +44,10 @@ struct hip_moe_layer {
 	uint32_t *d_ids;
 	float *d_w;
 	float *d_h;
-	float *d_ypart;
+	float *d_ypart;     /* fp32 partials of the GEMV and grouped paths */
+	size_t ypart_cap;   /* floats */
+	uint64_t *d_part;   /* epoch-tagged partials of the decode kernel */
+	size_t part_words;
 	uint32_t *d_sync;   /* epoch and flags of the decode kernel */
 	size_t sync_words;
 	int *d_rows;        /* grouped path: sorted pair per row, -1 = padding */
@@ -103,6 +106,28 @@ static int is_pow2(size_t v)
 	return v && !(v & (v - 1));
 }
 
+/*
+ * Expert e's down matrix [E rows][EI/32 blocks] (GGUF order) goes to the
+ * device as EI/32 panels: panel c = block c of rows 0..E-1, contiguous.
+ * Only whole blocks move, so every block keeps its bytes; a decode item
+ * (32 columns of down for all E rows) then reads one contiguous panel, and
+ * the down GEMV and GEMM read E-row runs of blocks.
+ */
+static int upload_down(hip_moe_layer *L, size_t e, const uint8_t *src, uint8_t *stage)
+{
+	const size_t bb = L->wtype == HIP_MOE_Q8_0 ? 34 : 18, nc = L->EI / MOE_QK;
+	for (size_t i = 0; i < L->E; i++) {
+		const uint8_t *row = src + i * L->rb_mid;
+		for (size_t c = 0; c < nc; c++)
+			memcpy(stage + (c * L->E + i) * bb, row + c * bb, bb);
+	}
+	HIPCHK(hipMemcpy(L->d_down + e * L->down_stride, stage, L->down_stride,
+			 hipMemcpyHostToDevice), "upload down");
+	return 1;
+fail:
+	return 0;
+}
+
 void hip_moe_free(hip_moe_layer *L)
 {
 	if (!L)
@@ -114,6 +139,7 @@ void hip_moe_free(hip_moe_layer *L)
 	hipFree(L->d_w);
 	hipFree(L->d_h);
 	hipFree(L->d_ypart);
+	hipFree(L->d_part);
 	hipFree(L->d_sync);
 	hipFree(L->d_rows);
 	hipFree(L->d_tile_e);
@@ -135,6 +161,7 @@ hip_moe_layer *hip_moe_upload(const float *gate_inp, const void *const *gate_e,
 			      int renorm)
 {
 	hip_moe_layer *L = NULL;
+	uint8_t *stage = NULL;
 	int ndev = 0;
 
 	if (wtype != HIP_MOE_Q8_0 && wtype != HIP_MOE_Q4_0) {
@@ -179,9 +206,6 @@ hip_moe_layer *hip_moe_upload(const float *gate_inp, const void *const *gate_e,
 	L->rb_mid = row_bytes(wtype, EI);
 	L->gu_stride = EI * L->rb_in;
 	L->down_stride = E * L->rb_mid;
-	L->kchunks = moe_kchunks(EI);
-	if (moe_fused_kchunks(wtype, EI) > L->kchunks) /* ypart holds either path's chunks */
-		L->kchunks = moe_fused_kchunks(wtype, EI);
 	L->weight_bytes = NE * E * sizeof(float) + NE * (2 * L->gu_stride + L->down_stride);
 	L->fused_grid = moe_fused_grid(wtype, E, EI, NE);
 
@@ -200,6 +224,11 @@ hip_moe_layer *hip_moe_upload(const float *gate_inp, const void *const *gate_e,
 
 	HIPCHK(hipMemcpy(L->d_router, gate_inp, NE * E * sizeof(float), hipMemcpyHostToDevice),
 	       "upload router");
+	stage = malloc(L->down_stride);
+	if (!stage) {
+		set_err("upload: out of host memory");
+		goto fail;
+	}
 	for (size_t e = 0; e < NE; e++) {
 		if (!gate_e[e] || !up_e[e] || !down_e[e]) {
 			set_err("upload: NULL pointer for expert %zu", e);
@@ -209,11 +238,13 @@ hip_moe_layer *hip_moe_upload(const float *gate_inp, const void *const *gate_e,
 				 hipMemcpyHostToDevice), "upload gate");
 		HIPCHK(hipMemcpy(L->d_up + e * L->gu_stride, up_e[e], L->gu_stride,
 				 hipMemcpyHostToDevice), "upload up");
-		HIPCHK(hipMemcpy(L->d_down + e * L->down_stride, down_e[e], L->down_stride,
-				 hipMemcpyHostToDevice), "upload down");
+		if (!upload_down(L, e, (const uint8_t *)down_e[e], stage))
+			goto fail;
 	}
+	free(stage);
 	return L;
 fail:
+	free(stage);
 	hip_moe_free(L);
 	return NULL;
 }
@@ -233,11 +264,13 @@ static int ensure_scratch(hip_moe_layer *L, size_t T)
 	hipFree(L->d_w);
 	hipFree(L->d_h);
 	hipFree(L->d_ypart);
+	hipFree(L->d_part);
 	hipFree(L->d_sync);
 	hipFree(L->d_rows);
 	hipFree(L->d_tile_e);
 	hipFree(L->d_h16);
 	hipFree(L->d_xh);
+	L->d_part = NULL;
 	L->d_xh = NULL;
 	L->d_rows = NULL;
 	L->d_tile_e = NULL;
@@ -253,19 +286,29 @@ static int ensure_scratch(hip_moe_layer *L, size_t T)
 	HIPCHK(hipMalloc((void **)&L->d_ids, P * sizeof(uint32_t)), "hipMalloc(ids)");
 	HIPCHK(hipMalloc((void **)&L->d_w, P * sizeof(float)), "hipMalloc(w)");
 	HIPCHK(hipMalloc((void **)&L->d_h, P * L->EI * sizeof(float)), "hipMalloc(h)");
-	/* fp32 partials of the GEMV and grouped paths, or epoch-tagged 64-bit
-	 * partials of the decode kernel */
-	HIPCHK(hipMalloc((void **)&L->d_ypart, P * L->kchunks * L->E * sizeof(uint64_t)),
-	       "hipMalloc(ypart)");
-	L->sync_words = moe_fused_sync_words(L->wtype, T, L->topk, L->E, L->EI, L->NE,
-					     L->fused_grid > 0 ? L->fused_grid : 1);
+	/* fp32 partials of the GEMV (its K-chunks) and grouped paths (their
+	 * K-splits: room for several when the pairs are few) */
+	L->ypart_cap = moe_down_part_floats(L->E, L->EI, P);
+	if (L->ypart_cap < P * L->E * 2)
+		L->ypart_cap = P * L->E * 2;
+	if (L->ypart_cap < ((size_t)1 << 22))
+		L->ypart_cap = (size_t)1 << 22;
+	HIPCHK(hipMalloc((void **)&L->d_ypart, L->ypart_cap * sizeof(float)), "hipMalloc(ypart)");
+	/* decode kernel: epoch-tagged partials, for every T it can take up to
+	 * this capacity */
+	L->part_words = 1;
+	for (size_t t = 1; L->fused_grid > 0 && t <= T && t * L->topk <= MOE_FUSED_MAX_P; t++) {
+		size_t w = moe_fused_part_words(t, L->topk, L->E, L->EI, L->fused_grid);
+		L->part_words = w > L->part_words ? w : L->part_words;
+	}
+	HIPCHK(hipMalloc((void **)&L->d_part, L->part_words * sizeof(uint64_t)), "hipMalloc(part)");
+	L->sync_words = moe_fused_sync_words(T, L->NE, L->fused_grid > 0 ? L->fused_grid : 1);
 	HIPCHK(hipMalloc((void **)&L->d_sync, L->sync_words * sizeof(uint32_t)), "hipMalloc(sync)");
 	/* zeroed once here: the decode kernel's flags and its partials carry an
 	 * epoch that starts at 1, and reused device memory may hold tags of an
 	 * earlier layer */
 	HIPCHK(hipMemset(L->d_sync, 0, L->sync_words * sizeof(uint32_t)), "hipMemset(sync)");
-	HIPCHK(hipMemset(L->d_ypart, 0, P * L->kchunks * L->E * sizeof(uint64_t)),
-	       "hipMemset(ypart)");
+	HIPCHK(hipMemset(L->d_part, 0, L->part_words * sizeof(uint64_t)), "hipMemset(part)");
 	if (moe_prefill_supported(L->wtype, L->E, L->EI, L->NE)) {
 		size_t rows = (size_t)moe_prefill_max_tiles(P, L->NE) * moe_prefill_tile_rows();
 		HIPCHK(hipMalloc((void **)&L->d_rows, rows * sizeof(int)), "hipMalloc(rows)");
@@ -386,7 +429,7 @@ int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 	if (path == HIP_MOE_PATH_DECODE) {
 		LCHK(moe_launch_fused(L->wtype, d_x, L->d_router, d_router_bias, L->d_gate,
 				      L->d_up, L->d_down, L->gu_stride, L->down_stride,
-				      ids, w, L->d_h, L->d_ypart, d_out, L->d_sync,
+				      ids, w, L->d_part, d_out, L->d_sync,
 				      (int)T, (int)L->E, (int)L->EI, (int)L->NE, (int)L->topk,
 				      L->renorm, L->fused_grid, s), "fused layer");
 		return 1;
@@ -395,11 +438,12 @@ int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 		   path == HIP_MOE_PATH_GROUPED ? L->d_xh : NULL, s))
 		return 0;
 	if (path == HIP_MOE_PATH_GROUPED) {
-		int split = 1; /* ypart holds kchunks 64-bit entries per (pair, column) */
+		int split = 1;
 		LCHK(moe_launch_prefill(L->wtype, L->d_xh, L->d_gate, L->d_up, L->d_down,
 					L->gu_stride, L->down_stride, ids, L->d_rows,
 					L->d_tile_e, L->d_h16, L->d_ypart, (int)T, (int)L->topk,
-					(int)L->E, (int)L->EI, (int)L->NE, 2 * L->kchunks, &split, s),
+					(int)L->E, (int)L->EI, (int)L->NE,
+					(int)(L->ypart_cap / ((size_t)P * L->E)), &split, s),
 		     "grouped GEMMs");
 		LCHK(moe_launch_combine(L->d_ypart, w, d_out, (int)T, (int)L->topk, (int)L->E,
 					split, s), "combine");
@@ -408,11 +452,12 @@ int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 	LCHK(moe_launch_gateup(L->wtype, L->d_gate, L->d_up, L->gu_stride, ids, -1, d_x,
 			       L->d_h, P, (int)L->topk, (int)L->E, (int)L->EI, s),
 	     "gate/up");
+	int kch = 1;
 	LCHK(moe_launch_down(L->wtype, L->d_down, L->down_stride, ids, -1, L->d_h,
-			     L->d_ypart, P, (int)L->topk, (int)L->E, (int)L->EI, s),
+			     L->d_ypart, L->ypart_cap, P, (int)L->E, (int)L->EI, &kch, s),
 	     "down");
-	LCHK(moe_launch_combine(L->d_ypart, w, d_out, (int)T, (int)L->topk, (int)L->E,
-				L->kchunks, s), "combine");
+	LCHK(moe_launch_combine(L->d_ypart, w, d_out, (int)T, (int)L->topk, (int)L->E, kch, s),
+	     "combine");
 	return 1;
 }
 
@@ -432,10 +477,11 @@ int hip_moe_expert_ffn_dev(hip_moe_layer *L, size_t expert, const float *d_x,
 	hipStream_t s = pick_stream(L, stream);
 	LCHK(moe_launch_gateup(L->wtype, L->d_gate, L->d_up, L->gu_stride, NULL, (int)expert,
 			       d_x, L->d_h, 1, 1, (int)L->E, (int)L->EI, s), "gate/up");
+	int kch = 1;
 	LCHK(moe_launch_down(L->wtype, L->d_down, L->down_stride, NULL, (int)expert, L->d_h,
-			     L->d_ypart, 1, 1, (int)L->E, (int)L->EI, s), "down");
-	LCHK(moe_launch_combine(L->d_ypart, NULL, d_out, 1, 1, (int)L->E, L->kchunks, s),
-	     "combine");
+			     L->d_ypart, L->ypart_cap, 1, (int)L->E, (int)L->EI, &kch, s),
+	     "down");
+	LCHK(moe_launch_combine(L->d_ypart, NULL, d_out, 1, 1, (int)L->E, kch, s), "combine");
 	return 1;
 }
 
@@ -496,8 +542,7 @@ int hip_moe_ffn(hip_moe_layer *L, const float *x, float *out, size_t T,
 				 hipMemcpyDeviceToHost), "read error word");
 		if (err) { /* flags may be left mid-flight: restart the epoch at zero */
 			hipMemset(L->d_sync, 0, L->sync_words * sizeof(uint32_t));
-			hipMemset(L->d_ypart, 0, L->cap_T * L->topk * L->kchunks * L->E *
-						 sizeof(uint64_t));
+			hipMemset(L->d_part, 0, L->part_words * sizeof(uint64_t));
 			set_err("persistent kernel: a dependency wait timed out");
 			return 0;
 		}

@@ -143,6 +143,39 @@ __device__ static inline float seg_dot_q4_0(const u32 (&d)[9], const float (&x)[
 	return block_dot_q4_0(q0, d[0], x, xs0) + block_dot_q4_0(q1, d[4] >> 16, x + 32, xs1);
 }
 
+/*
+ * One block of a down-matrix panel.  The layer keeps each down matrix as
+ * EI/32 panels: panel c holds block c of every row, row i's at BB*i.  The
+ * 4-byte aligned window that holds it starts 2 bytes early for odd i (scale
+ * in the upper half of dword 0) and runs 2 bytes into block i+1 for even i;
+ * E is even, so the last row is odd and no window leaves its panel.
+ */
+template <int WT> struct panel_blk;
+template <> struct panel_blk<1> { /* Q8_0 */
+	static constexpr int BB = 34, DW = 9;
+	__device__ static inline float dot(const u32 (&d)[9], int i, const float *h, float hs)
+	{
+		u32 q[8];
+		const bool odd = i & 1;
+#pragma unroll
+		for (int k = 0; k < 8; k++)
+			q[k] = odd ? d[k + 1] : __builtin_amdgcn_alignbit(d[k + 1], d[k], 16);
+		return block_dot_q8_0(q, odd ? d[0] >> 16 : d[0], h, hs);
+	}
+};
+template <> struct panel_blk<2> { /* Q4_0 */
+	static constexpr int BB = 18, DW = 5;
+	__device__ static inline float dot(const u32 (&d)[5], int i, const float *h, float hs)
+	{
+		u32 q[4];
+		const bool odd = i & 1;
+#pragma unroll
+		for (int k = 0; k < 4; k++)
+			q[k] = odd ? d[k + 1] : __builtin_amdgcn_alignbit(d[k + 1], d[k], 16);
+		return block_dot_q4_0(q, odd ? d[0] >> 16 : d[0], h, hs);
+	}
+};
+
 template <int WT> struct qseg;
 template <> struct qseg<1> {
 	static constexpr int BYTES = 68;

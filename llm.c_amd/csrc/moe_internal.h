@@ -20,10 +20,9 @@ extern "C" {
 #define MOE_MAX_TOPK 64
 #define MOE_FUSED_MAX_P 64  /* T*K handled by the persistent decode kernel */
 #define MOE_SYNC_ERR_WORD 256 /* error word in the persistent kernel's counters */
-#define MOE_FUSED_WG_PER_CU 4 /* workgroups per CU of the decode kernel */
 
-/* lanes per row for a K-long dot: the largest power of two <= 64 that
- * divides K / 64, and the number of K-chunks the row is split into. */
+/* lanes per gate/up row for a K-long dot: the largest power of two <= 64
+ * that divides K / 64, and the number of K-chunks the row is split into. */
 int moe_lanes_per_row(size_t K);
 int moe_kchunks(size_t K);
 
@@ -42,10 +41,15 @@ int moe_launch_gateup(int wtype, const uint8_t *gate, const uint8_t *up,
                       const float *x, float *h, int P, int K, int E, int EI,
                       void *stream);
 
-/* ypart[p][kc][E] = partial dots of down_e rows with h[p] over K-chunk kc. */
+/* Down matrices are stored as EI/32 panels of E blocks each (panel c holds
+ * block c of every row).  ypart[p][kc][E] = partial dots of down_e rows
+ * with h[p] over K-chunk kc, *kchunks chunks, at most ypart_cap floats. */
 int moe_launch_down(int wtype, const uint8_t *down, size_t expert_stride,
                     const uint32_t *ids, int fixed_e, const float *h,
-                    float *ypart, int P, int K, int E, int EI, void *stream);
+                    float *ypart, size_t ypart_cap, int P, int E, int EI, int *kchunks,
+                    void *stream);
+/* ypart floats moe_launch_down may use for any pair count up to P */
+size_t moe_down_part_floats(size_t E, size_t EI, size_t P);
 
 /* out[t][E] = sum over slots s, in order, of y[t*K+s] / (1/w[t*K+s]);
  * y = sum of the kchunks partials in order.  w == NULL means weight 1. */
@@ -69,16 +73,17 @@ int moe_launch_prefill(int wtype, const void *xh, const uint8_t *gate, const uin
                        int T, int K, int E, int EI, int NE, int max_split, int *split,
                        void *stream);
 
-/* One-launch decode layer (moe_decode.hip) for T*K <= MOE_FUSED_MAX_P. */
+/* One-launch decode layer (moe_decode.hip) for T*K <= MOE_FUSED_MAX_P:
+ * grid = one workgroup per CU (0: not applicable), sync words and tagged
+ * 64-bit partial words it needs for T tokens. */
 int moe_fused_supported(int wtype, size_t E, size_t EI, size_t NE, size_t T, size_t K);
-int moe_fused_kchunks(int wtype, size_t EI);
-size_t moe_fused_sync_words(int wtype, size_t T, size_t K, size_t E, size_t EI, size_t NE,
-                            int grid);
 int moe_fused_grid(int wtype, size_t E, size_t EI, size_t NE);
+size_t moe_fused_sync_words(size_t T, size_t NE, int grid);
+size_t moe_fused_part_words(size_t T, size_t K, size_t E, size_t EI, int grid);
 int moe_launch_fused(int wtype, const float *x, const float *router, const float *bias,
                      const uint8_t *gate, const uint8_t *up, const uint8_t *down,
-                     size_t gu_stride, size_t dn_stride, uint32_t *ids, float *w, float *h,
-                     float *ypart, float *out, uint32_t *sync, int T, int E, int EI, int NE,
+                     size_t gu_stride, size_t dn_stride, uint32_t *ids, float *w,
+                     uint64_t *part, float *out, uint32_t *sync, int T, int E, int EI, int NE,
                      int K, int renorm, int grid, void *stream);
 
 #ifdef __cplusplus

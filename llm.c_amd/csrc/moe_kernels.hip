@@ -203,39 +203,90 @@ __global__ __launch_bounds__(256) void k_gateup(const uint8_t *__restrict__ gate
 }
 
 /* ------------------------------------------------------------------ */
-/* down dequant-GEMV (K-chunk partials)                                */
+/* down dequant-GEMV over panels (K-chunk partials)                    */
 /* ------------------------------------------------------------------ */
 
-/* grid (E / (4*rpw), P, kchunks); C lanes per row over chunk kc's
- * C segments (C*64 columns). */
-template <int WT, int C>
+/*
+ * The down matrices are stored panel by panel (panel c = block c of every
+ * row, contiguous), so a thread owns one output row and walks the panels of
+ * its K-chunk: a wave reads 64 consecutive blocks of a panel per load, and
+ * no cross-lane sum is needed.  grid (ceil(E/256), P, kch); chunk kc covers
+ * panels [kc*ppc, (kc+1)*ppc), ppc = (EI/32)/kch <= DN_MAX_PPC, whose h
+ * values are staged in LDS.  Loads go out DN_BATCH panels at a time.
+ */
+#define DN_MAX_PPC 64
+#define DN_BATCH 4
+template <int WT>
 __global__ __launch_bounds__(256) void k_down(const uint8_t *__restrict__ down,
 					      size_t expert_stride,
 					      const u32 *__restrict__ ids, int fixed_e,
 					      const float *__restrict__ h,
-					      float *__restrict__ ypart, int E, int EI,
-					      int rpw)
+					      float *__restrict__ ypart, int E, int EI)
 {
-	constexpr int RPS = WAVE / C;
+	typedef panel_blk<WT> D;
+	__shared__ __attribute__((aligned(16))) float sh[DN_MAX_PPC * MOE_QK];
 	const int p = blockIdx.y, kc = blockIdx.z, kch = gridDim.z;
 	const int e = fixed_e >= 0 ? fixed_e : (int)ids[p];
-	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-	const int seg = kc * C + lane % C, sub = lane / C;
-	const size_t rb = (size_t)(EI / MOE_QK) * (qseg<WT>::BYTES / 2);
+	const int ppc = EI / MOE_QK / kch, c0 = kc * ppc;
+	const int i = blockIdx.x * 256 + threadIdx.x;
+	const int ii = i < E ? i : E - 1; /* rows past E load row E-1 and store nothing */
 
-	const uint8_t *D = down + (size_t)e * expert_stride + (size_t)seg * qseg<WT>::BYTES;
+	const float *hp = h + (size_t)p * EI + (size_t)c0 * MOE_QK;
+	for (int k = threadIdx.x; k < ppc * MOE_QK; k += 256)
+		sh[k] = hp[k];
+	__syncthreads();
 
-	float xr[64];
-	load_x64(h + (size_t)p * EI + seg * MOE_SEG_COLS, xr);
-	const float xs0 = sum32(xr), xs1 = sum32(xr + 32);
-
-	const int row0 = (blockIdx.x * 4 + wave) * rpw;
-	for (int r = 0; r < rpw; r += RPS) {
-		const int row = row0 + r + sub;
-		float y = group_sum<C>(qseg<WT>::dot(D + (size_t)row * rb, xr, xs0, xs1));
-		if (lane % C == 0)
-			ypart[((size_t)p * kch + kc) * E + row] = y;
+	const size_t pstride = (size_t)E * D::BB;
+	const uint8_t *P0 = down + (size_t)e * expert_stride + (size_t)c0 * pstride +
+			    ((D::BB * ii) & ~3);
+	float y = 0.0f;
+	for (int c = 0; c < ppc; c += DN_BATCH) {
+		u32 d[DN_BATCH][D::DW];
+#pragma unroll
+		for (int u = 0; u < DN_BATCH; u++)
+			if (c + u < ppc)
+				load_dwords<D::DW>(P0 + (size_t)(c + u) * pstride, d[u]);
+#pragma unroll
+		for (int u = 0; u < DN_BATCH; u++)
+			if (c + u < ppc) {
+				const float *hc = sh + (c + u) * MOE_QK;
+				y += D::dot(d[u], ii, hc, sum32(hc));
+			}
 	}
+	if (i < E)
+		ypart[((size_t)p * kch + kc) * E + i] = y;
+}
+
+/* K-chunks of the down GEMV for P pairs: the fewest (chunks of at most
+ * DN_MAX_PPC panels) that give >= 1024 workgroups, 0 if even the fewest
+ * need more than cap floats of partials */
+static int down_kchunks(int E, int EI, int P, size_t cap)
+{
+	const int NC = EI / MOE_QK;
+	int best = 0;
+	for (int d = 1; d <= NC; d++) {
+		if (NC % d || NC / d > DN_MAX_PPC)
+			continue;
+		if ((size_t)P * d * E > cap)
+			break;
+		best = d;
+		if ((size_t)((E + 255) / 256) * P * d >= 1024)
+			break;
+	}
+	return best;
+}
+
+/* floats of partials the down GEMV needs for any pair count up to P (the
+ * chunk count falls as P grows; past 2048 pairs it is the minimum) */
+extern "C" size_t moe_down_part_floats(size_t E, size_t EI, size_t P)
+{
+	size_t m = 0, top = P < 2048 ? P : 2048;
+	for (size_t q = 1; q <= top; q++) {
+		size_t v = q * (size_t)down_kchunks((int)E, (int)EI, (int)q, (size_t)-1) * E;
+		m = v > m ? v : m;
+	}
+	size_t v = P * (size_t)down_kchunks((int)E, (int)EI, (int)P, (size_t)-1) * E;
+	return v > m ? v : m;
 }
 
 /* ------------------------------------------------------------------ */
@@ -371,46 +422,28 @@ extern "C" int moe_launch_gateup(int wtype, const uint8_t *gate, const uint8_t *
 	return (int)hipErrorInvalidValue;
 }
 
-template <int WT>
-static int launch_down_t(int C, dim3 grid, hipStream_t s, const uint8_t *down,
-			 size_t es, const u32 *ids, int fe, const float *h, float *yp,
-			 int E, int EI, int rpw)
-{
-#define DN(CC)                                                                      \
-	case CC:                                                                    \
-		hipLaunchKernelGGL((k_down<WT, CC>), grid, dim3(256), 0, s, down, es, \
-				   ids, fe, h, yp, E, EI, rpw);                    \
-		break;
-	switch (C) {
-		DN(4) DN(8) DN(16) DN(32) DN(64)
-	default:
-		return (int)hipErrorInvalidValue;
-	}
-#undef DN
-	return (int)hipGetLastError();
-}
-
 extern "C" int moe_launch_down(int wtype, const uint8_t *down, size_t expert_stride,
 			       const uint32_t *ids, int fixed_e, const float *h,
-			       float *ypart, int P, int K, int E, int EI, void *stream)
+			       float *ypart, size_t ypart_cap, int P, int E, int EI, int *kchunks,
+			       void *stream)
 {
-	(void)K;
-	int C = moe_lanes_per_row((size_t)EI);
-	if (C < 4)
+	if (EI % MOE_QK || E % 2 || E < 2)
 		return (int)hipErrorInvalidValue;
-	int kch = moe_kchunks((size_t)EI);
-	int rpw = pick_rpw(WAVE / C, P * kch, E);
-	if (E % (4 * rpw))
+	const int kch = down_kchunks(E, EI, P, ypart_cap);
+	if (kch < 1)
 		return (int)hipErrorInvalidValue;
-	dim3 grid(E / (4 * rpw), P, kch);
+	*kchunks = kch;
+	dim3 grid((E + 255) / 256, P, kch);
 	hipStream_t s = (hipStream_t)stream;
 	if (wtype == 1)
-		return launch_down_t<1>(C, grid, s, down, expert_stride, ids, fixed_e, h,
-					ypart, E, EI, rpw);
-	if (wtype == 2)
-		return launch_down_t<2>(C, grid, s, down, expert_stride, ids, fixed_e, h,
-					ypart, E, EI, rpw);
-	return (int)hipErrorInvalidValue;
+		hipLaunchKernelGGL(k_down<1>, grid, dim3(256), 0, s, down, expert_stride, ids,
+				   fixed_e, h, ypart, E, EI);
+	else if (wtype == 2)
+		hipLaunchKernelGGL(k_down<2>, grid, dim3(256), 0, s, down, expert_stride, ids,
+				   fixed_e, h, ypart, E, EI);
+	else
+		return (int)hipErrorInvalidValue;
+	return (int)hipGetLastError();
 }
 
 extern "C" int moe_launch_combine(const float *ypart, const float *w, float *out, int T,

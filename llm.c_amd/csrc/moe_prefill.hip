@@ -11,6 +11,9 @@
  *                  in sorted row order.  X is the f16 copy of the tokens the
  *                  router kernel writes.
  *   k_pf_down      per (m-tile, 512 output columns, K-split): Y = H Wd^T
+ *                  (the down matrices are stored as panels: panel c holds
+ *                  block c of every row, so a stage reads two contiguous
+ *                  runs of 512 blocks)
  *                  over d_ff (or one of S consecutive parts of it, when the
  *                  tiles alone leave the CUs idle), written fp32 to
  *                  ypart[pair][split][E]; k_combine then adds the splits in
@@ -366,13 +369,58 @@ __device__ static inline void pf_stage_mfma(const uint8_t *sb, const _Float16 *s
 	}
 }
 
+/* The same for a stage of two down panels: LDS holds rows n0 .. n0+511 of
+ * panel 2s, then of panel 2s+1 (PF_BROWS blocks each, unpadded).  The lane's
+ * column pair is rows n (even: 4-byte aligned blocks) and n+1 (odd: 2 bytes
+ * off), so each group reads blocks of one alignment. */
+template <int WT>
+__device__ static inline void pf_stage_mfma_panel(const uint8_t *sb, const _Float16 *sa, int n,
+						  floatx16 (&acc)[2][2], int lane)
+{
+	typedef pf_geo<WT> GG;
+	constexpr int RUN = PF_BROWS * GG::BB;
+	const int h = lane >> 5, r = lane & 31;
+	bsrc<WT, 0> ev[2]; /* [panel]: row n */
+	bsrc<WT, 1> od[2]; /* [panel]: row n + 1 */
+#pragma unroll
+	for (int pp = 0; pp < 2; pp++) {
+		ev[pp].load(sb + pp * RUN + n * GG::BB, h);
+		od[pp].load(sb + pp * RUN + (n + 1) * GG::BB, h);
+	}
+	half8_t a[2][2][2]; /* [block][k-half][mb] */
+#pragma unroll
+	for (int bb = 0; bb < 2; bb++)
+#pragma unroll
+		for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+			for (int mb = 0; mb < 2; mb++) {
+				const int ar = mb * 32 + r, c = bb * 4 + kh * 2 + h;
+				a[bb][kh][mb] = *(const half8_t *)(sa + 8 * (ar * 8 + (c ^ (ar & 7))));
+			}
+#pragma unroll
+	for (int bb = 0; bb < 2; bb++) {
+		half8_t bk[2][2]; /* [group][k-half] */
+		ev[bb].operands(bk[0][0], bk[0][1]);
+		od[bb].operands(bk[1][0], bk[1][1]);
+#pragma unroll
+		for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+			for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+				for (int g = 0; g < 2; g++)
+					acc[mb][g] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+						a[bb][kh][mb], bk[g][kh], acc[mb][g], 0, 0, 0);
+	}
+}
+
 /*
  * The K loop.  wbase: weights base (SGPR); woff[j]: this lane's byte offset
- * of load j of stage 0 (row base + dword); abase/aoff the same for A.  Stage
- * s adds s * RBS (weights) and s * 128 (A) to the bases.
+ * of load j of stage 0; abase/aoff the same for A.  Stage s adds s * wstep
+ * (weights) and s * 128 (A) to the bases.  PANEL: the stage holds two down
+ * panels (brow[0] = the lane's even row) instead of [row][chunk] rows.
  */
-template <int WT>
-__device__ static inline void pf_kloop(uint8_t *lds, const uint8_t *wbase,
+template <int WT, int PANEL>
+__device__ static inline void pf_kloop(uint8_t *lds, const uint8_t *wbase, size_t wstep,
 				       const u32 (&woff)[pf_geo<WT>::JB], const uint8_t *abase,
 				       u32 aoff, const int (&brow)[2], int nsteps,
 				       floatx16 (&acc)[2][2])
@@ -382,7 +430,7 @@ __device__ static inline void pf_kloop(uint8_t *lds, const uint8_t *wbase,
 	const u32 l0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
 	auto issue = [&](int s) {
 		const u32 st = l0 + (u32)((s % GG::NSTAGE) * GG::SSZ);
-		const uint8_t *wb = wbase + (size_t)s * GG::RBS;
+		const uint8_t *wb = wbase + (size_t)s * wstep;
 #pragma unroll
 		for (int j = 0; j < GG::JB; j++)
 			dma_dwordx4(wb, woff[j], st + (u32)((wave * GG::JB + j) * WAVE * GG::CH));
@@ -403,7 +451,11 @@ __device__ static inline void pf_kloop(uint8_t *lds, const uint8_t *wbase,
 		if (s + GG::NSTAGE - 1 < nsteps)
 			issue(s + GG::NSTAGE - 1);
 		const uint8_t *sb = lds + (s % GG::NSTAGE) * GG::SSZ;
-		pf_stage_mfma<WT>(sb, (const _Float16 *)(sb + GG::BSZ), brow, acc, lane);
+		if (PANEL)
+			pf_stage_mfma_panel<WT>(sb, (const _Float16 *)(sb + GG::BSZ), brow[0], acc,
+						lane);
+		else
+			pf_stage_mfma<WT>(sb, (const _Float16 *)(sb + GG::BSZ), brow, acc, lane);
 	}
 }
 
@@ -468,7 +520,7 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_gateup(
 #pragma unroll
 			for (int j = 0; j < 16; j++)
 				acc[mb][g][j] = 0.0f;
-	pf_kloop<WT>(lds, gate, woff, (const uint8_t *)xh, aoff, brow, E / PF_KB, acc);
+	pf_kloop<WT, 0>(lds, gate, GG::RBS, woff, (const uint8_t *)xh, aoff, brow, E / PF_KB, acc);
 
 	const int col = n0 + wave * 32 + (lane & 31), hh = lane >> 5;
 #pragma unroll
@@ -500,17 +552,24 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down(
 	if (threadIdx.x < PF_MT)
 		srow[threadIdx.x] = rows[tile * PF_MT + threadIdx.x];
 	const int n0 = blockIdx.x * PF_BROWS;
-	const size_t rb = (size_t)(EI / MOE_QK) * GG::BB;
+	/* stage s = rows n0 .. n0+511 of panels 2s and 2s+1: two contiguous runs
+	 * of RUN bytes, loaded as 16-byte chunks; chunks past them (the last
+	 * wave's spare lanes) reload chunk 0 into unused LDS */
+	const size_t RUN = (size_t)PF_BROWS * GG::BB, PANEL = (size_t)E * GG::BB;
 	pf_lanes<WT> L;
 	u32 woff[GG::JB];
 #pragma unroll
-	for (int j = 0; j < GG::JB; j++)
-		woff[j] = (u32)((size_t)e * dn_stride + (size_t)(n0 + L.wrow[j]) * rb +
-				GG::CH * L.wch[j]);
+	for (int j = 0; j < GG::JB; j++) {
+		const size_t f = (size_t)((wave * GG::JB + j) * WAVE + lane) * GG::CH;
+		woff[j] = (u32)((size_t)e * dn_stride +
+				(f < 2 * RUN ? (f / RUN) * PANEL + (size_t)n0 * GG::BB + f % RUN
+					     : (size_t)n0 * GG::BB));
+	}
 	const u32 aoff = rows[tile * PF_MT + L.arow] >= 0
 				 ? (u32)((size_t)(tile * PF_MT + L.arow) * EI * 2 + 16 * L.achunk)
 				 : 0u;
-	const int brow[2] = {wave * 64 + (lane & 31), wave * 64 + 32 + (lane & 31)};
+	/* MFMA column r of group g = output row wave*64 + 2r + g */
+	const int brow[2] = {wave * 64 + 2 * (lane & 31), wave * 64 + 2 * (lane & 31) + 1};
 
 	floatx16 acc[2][2];
 #pragma unroll
@@ -520,8 +579,9 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down(
 #pragma unroll
 			for (int j = 0; j < 16; j++)
 				acc[mb][g][j] = 0.0f;
-	pf_kloop<WT>(lds, down + (size_t)s0 * GG::RBS, woff, (const uint8_t *)(h + (size_t)s0 * PF_KB),
-		     aoff, brow, s1 - s0, acc); /* syncs srow */
+	pf_kloop<WT, 1>(lds, down + (size_t)s0 * 2 * PANEL, 2 * PANEL, woff,
+			(const uint8_t *)(h + (size_t)s0 * PF_KB), aoff, brow, s1 - s0,
+			acc); /* syncs srow */
 
 	const int hh = lane >> 5;
 #pragma unroll
@@ -533,8 +593,8 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down(
 				continue;
 #pragma unroll
 			for (int g = 0; g < 2; g++)
-				ypart[((size_t)pr * S + blockIdx.z) * E + n0 + wave * 64 + 32 * g +
-				      (lane & 31)] = acc[mb][g][j];
+				ypart[((size_t)pr * S + blockIdx.z) * E + n0 + wave * 64 +
+				      2 * (lane & 31) + g] = acc[mb][g][j];
 		}
 }
 
