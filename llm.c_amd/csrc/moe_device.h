@@ -453,8 +453,8 @@ __device__ static inline void wave_softmax_topk64(float logit, u32 *ids, float *
 #pragma unroll
 	for (int q = 0; q < 32; q++) {
 		const ulonglong2 v = sk2[q];
-		rank += (int)((key - v.x) >> 63);
-		rank += (int)((key - v.y) >> 63);
+		rank += (int)(v.x > key);
+		rank += (int)(v.y > key);
 	}
 	const int r0 = __builtin_amdgcn_readlane(rank, 0);
 	const int lim = r0 < K ? r0 : K;
