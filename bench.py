@@ -206,10 +206,11 @@ def main():
     # the path the library takes for this T: one launch of k_moe_decode, or
     # router, top-k, sort and the grouped GEMMs, or router, top-k, GEMVs
     path = layers[0].path_for(T)
+    # (layer_grouped / layer_gemv: the whole call, whose kernels the counter
+    # summaries add up)
     kernel = {hipmoe.PATH_DECODE: "k_moe_decode",
-              hipmoe.PATH_GROUPED: "whole layer call (router, top-k, sort, k_pf_gateup, "
-                                   "k_pf_down, combine)",
-              hipmoe.PATH_GEMV: "whole layer call (router, top-k, gate/up, down, combine)"}[path]
+              hipmoe.PATH_GROUPED: "layer_grouped",
+              hipmoe.PATH_GEMV: "layer_gemv"}[path]
 
     cpu = None
     if not args.no_cpu_baseline:
