@@ -64,6 +64,7 @@
 #define PSLICE 8     /* outputs per combine slice */
 #define DEC_TOKS 2   /* tokens one workgroup's item range can span (T <= G) */
 #define DEC_CHUNK 32 /* d_ff rows per item: one down block per row */
+#define CMB_MAX 16   /* combine entries per thread: grid * PSLICE <= CMB_MAX * NT */
 
 struct DecodeArgs {
 	const float *x;
@@ -610,39 +611,40 @@ void k_moe_decode(DecodeArgs a)
 		const int bf = item_owner(t * IPT, N, G), bl = item_owner((t + 1) * IPT - 1, N, G);
 		const int n = (bl - bf + 1) * PSLICE;
 		const uint64_t *src = a.part + (size_t)sl * a.ncon * PSLICE;
-		/* this thread's entries, skipping workgroups without items */
-		unsigned live = 0;
-		for (int e = threadIdx.x, k = 0; e < n; e += NT, k++) {
-			const int wb = bf + e / PSLICE;
-			live |= (unsigned)(item_lo(wb, N, G) != item_lo(wb + 1, N, G)) << k;
+		/* this thread's entries (at most CMB_MAX), skipping workgroups
+		 * without items; each thread polls its own until their tags show
+		 * the epoch, with no workgroup barrier per poll */
+		unsigned pending = 0;
+#pragma unroll
+		for (int k = 0; k < CMB_MAX; k++) {
+			const int e = threadIdx.x + NT * k, wb = bf + e / PSLICE;
+			if (e < n && item_lo(wb, N, G) != item_lo(wb + 1, N, G))
+				pending |= 1u << k;
 		}
-		float sum = 0.0f;
-		for (int round = 0;; round++) {
-			bool ok = true;
-			sum = 0.0f;
-			for (int e = threadIdx.x, k = 0; e < n; e += NT, k++) {
-				if (!((live >> k) & 1u))
-					continue;
-				const uint64_t v = ld_dev_u64(&src[e]);
-				ok &= (u32)(v >> 32) == epoch;
-				sum += __builtin_bit_cast(float, (u32)v);
-			}
-			if (threadIdx.x == 0)
-				s_ok = 1;
-			__syncthreads();
-			if (!ok)
-				s_ok = 0;
-			__syncthreads();
-			if (s_ok)
+		const unsigned live = pending;
+		float vals[CMB_MAX];
+		for (int round = 0; pending; round++) {
+#pragma unroll
+			for (int k = 0; k < CMB_MAX; k++)
+				if ((pending >> k) & 1u) {
+					const uint64_t v = ld_dev_u64(&src[threadIdx.x + NT * k]);
+					vals[k] = __builtin_bit_cast(float, (u32)v);
+					if ((u32)(v >> 32) == epoch)
+						pending &= ~(1u << k);
+				}
+			if (!pending)
 				break;
 			if (round >= SPIN_LIMIT) {
-				if (threadIdx.x == 0)
-					st_dev_u32(a.sync + MOE_SYNC_ERR_WORD, 1u);
+				st_dev_u32(a.sync + MOE_SYNC_ERR_WORD, 1u);
 				break;
 			}
 			__builtin_amdgcn_s_sleep(1);
-			__syncthreads();
 		}
+		float sum = 0.0f;
+#pragma unroll
+		for (int k = 0; k < CMB_MAX; k++)
+			if ((live >> k) & 1u)
+				sum += vals[k];
 		sum += __shfl_xor(sum, 8, WAVE);
 		sum += __shfl_xor(sum, 16, WAVE);
 		sum += __shfl_xor(sum, 32, WAVE);
@@ -770,8 +772,9 @@ extern "C" int moe_fused_grid(int wtype, size_t E, size_t EI, size_t NE)
 		return 0;
 	/* one workgroup per CU; the router rows need one workgroup each, a
 	 * workgroup's items must span at most DEC_TOKS tokens (T <= grid), and
-	 * a combine thread covers at most 32 contributors (grid <= 2048) */
-	return ncu >= (int)NE && ncu >= MOE_FUSED_MAX_P && ncu <= 2048 ? ncu : 0;
+	 * a combine thread covers at most CMB_MAX entries */
+	return ncu >= (int)NE && ncu >= MOE_FUSED_MAX_P && ncu * PSLICE <= CMB_MAX * g.NT ? ncu
+												: 0;
 }
 
 extern "C" int moe_launch_fused(int wtype, const float *x, const float *router,
