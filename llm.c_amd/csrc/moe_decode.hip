@@ -211,6 +211,170 @@ template <> struct segq<2> {
 	}
 };
 
+/* ---------------------------------------------------------------------- */
+/* integer dots                                                           */
+/* ---------------------------------------------------------------------- */
+
+/*
+ * An activation block (32 values of a token, or an item's 32 h values) is
+ * held as X_k = rint(v_k * 2^s), s chosen per block so |X_k| < 2^22, split
+ * into three balanced signed base-256 digits X = D2*65536 + D1*256 + D0
+ * (each in [-128, 127]).  A weight block's quants meet the digits in
+ * v_dot4c_i32_i8 (four products per instruction, exact int32 sums), and
+ *   sum q*v = 2^-s * (65536*S2 + (256*S1 + S0)),
+ * rounded once when the two parts meet in fp32.  The rounding of v to 22
+ * bits below its block's largest magnitude keeps a dot within ~1e-6 of the
+ * fp32 one; the reference's own fp32 sums differ by as much.  One weight
+ * byte costs 3/4 of an instruction instead of a conversion and an FMA.
+ *
+ * A staged block is DBLK dwords: d2[8] d1[8] d0[8] (element 4k+i in byte i
+ * of dword k), 2^-s, and the block sums of each digit (Q4_0 stores q + 8).
+ */
+#define DBLK 28
+
+__device__ static inline int digit_lo(int &x)
+{
+	const int d = ((x + 128) & 255) - 128;
+	x = (x - d) >> 8;
+	return d;
+}
+
+/* 4 values of a block held by one of its 8 staging lanes (lanes 8j..8j+7 of
+ * a wave hold block j): the block's digits and scale into dst[DBLK] */
+__device__ static inline void stage_digits4(u32 *dst, float4 v, int sub)
+{
+	float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+	m = fmaxf(m, __shfl_xor(m, 1, 8));
+	m = fmaxf(m, __shfl_xor(m, 2, 8));
+	m = fmaxf(m, __shfl_xor(m, 4, 8));
+	/* 2^s * m < 2^22; a block of zeros (or denormals) takes s = 120 */
+	const int e = (int)((__builtin_bit_cast(u32, m) >> 23) & 0xffu) - 127;
+	const int sh = 21 - e < 120 ? 21 - e : 120;
+	const float sc = __builtin_bit_cast(float, (u32)(sh + 127) << 23);
+	const float vv[4] = {v.x, v.y, v.z, v.w};
+	u32 p2 = 0, p1 = 0, p0 = 0;
+	int s2 = 0, s1 = 0, s0 = 0;
+#pragma unroll
+	for (int i = 0; i < 4; i++) {
+		int x = __float2int_rn(vv[i] * sc);
+		const int d0 = digit_lo(x), d1 = digit_lo(x), d2 = x;
+		p0 |= (u32)(d0 & 255) << (8 * i);
+		p1 |= (u32)(d1 & 255) << (8 * i);
+		p2 |= (u32)(d2 & 255) << (8 * i);
+		s0 += d0;
+		s1 += d1;
+		s2 += d2;
+	}
+#pragma unroll
+	for (int o = 1; o < 8; o <<= 1) {
+		s0 += __shfl_xor(s0, o, 8);
+		s1 += __shfl_xor(s1, o, 8);
+		s2 += __shfl_xor(s2, o, 8);
+	}
+	dst[sub] = p2;
+	dst[8 + sub] = p1;
+	dst[16 + sub] = p0;
+	if (sub == 0) {
+		dst[24] = (u32)(127 - sh) << 23; /* 2^-s */
+		dst[25] = (u32)s2;
+		dst[26] = (u32)s1;
+		dst[27] = (u32)s0;
+	}
+}
+
+/* n floats (a multiple of 32) into staged digit blocks */
+template <int NT>
+__device__ static inline void stage_digits(u32 *dst, const float *src, int n)
+{
+	const float4 *s4 = (const float4 *)src;
+	for (int i = threadIdx.x; i < n / 4; i += NT)
+		stage_digits4(dst + (i / 8) * DBLK, s4[i], i & 7);
+}
+
+/* sum_k q_k v_k of one block: q as 8 dwords of signed bytes (Q8_0) */
+__device__ static inline float idot_q8(const u32 (&q)[8], const u32 *x)
+{
+	int S2 = 0, S1 = 0, S0 = 0;
+#pragma unroll
+	for (int k = 0; k < 8; k++) {
+		S2 = __builtin_amdgcn_sdot4((int)q[k], (int)x[k], S2, false);
+		S1 = __builtin_amdgcn_sdot4((int)q[k], (int)x[8 + k], S1, false);
+		S0 = __builtin_amdgcn_sdot4((int)q[k], (int)x[16 + k], S0, false);
+	}
+	return ((float)S2 * 65536.0f + (float)(S1 * 256 + S0)) * __builtin_bit_cast(float, x[24]);
+}
+
+/* the same for Q4_0: 4 dwords of packed nibbles n = q + 8 (byte j: element
+ * j low, j + 16 high) */
+__device__ static inline float idot_q4(const u32 (&w)[4], const u32 *x)
+{
+	int S2 = 0, S1 = 0, S0 = 0;
+#pragma unroll
+	for (int k = 0; k < 4; k++) {
+		const int lo = (int)(w[k] & 0x0f0f0f0fu), hi = (int)((w[k] >> 4) & 0x0f0f0f0fu);
+		S2 = __builtin_amdgcn_sdot4(lo, (int)x[k], S2, false);
+		S2 = __builtin_amdgcn_sdot4(hi, (int)x[4 + k], S2, false);
+		S1 = __builtin_amdgcn_sdot4(lo, (int)x[8 + k], S1, false);
+		S1 = __builtin_amdgcn_sdot4(hi, (int)x[12 + k], S1, false);
+		S0 = __builtin_amdgcn_sdot4(lo, (int)x[16 + k], S0, false);
+		S0 = __builtin_amdgcn_sdot4(hi, (int)x[20 + k], S0, false);
+	}
+	S2 -= 8 * (int)x[25];
+	S1 -= 8 * (int)x[26];
+	S0 -= 8 * (int)x[27];
+	return ((float)S2 * 65536.0f + (float)(S1 * 256 + S0)) * __builtin_bit_cast(float, x[24]);
+}
+
+/* a lane's gate/up segment against staged digits: Q8_0 one block (window
+ * parity = block parity), Q4_0 a pair of blocks */
+template <int WT> struct idig;
+template <> struct idig<1> {
+	static constexpr int NB = 1;
+	__device__ static inline float dot(const u32 (&d)[9], const u32 *x, int s)
+	{
+		u32 q[8];
+		const bool odd = s & 1;
+#pragma unroll
+		for (int k = 0; k < 8; k++)
+			q[k] = odd ? d[k + 1] : __builtin_amdgcn_alignbit(d[k + 1], d[k], 16);
+		return f16_bits_to_f32(odd ? d[0] >> 16 : d[0]) * idot_q8(q, x);
+	}
+};
+template <> struct idig<2> {
+	static constexpr int NB = 2;
+	__device__ static inline float dot(const u32 (&d)[9], const u32 *x, int)
+	{
+		u32 q0[4], q1[4];
+#pragma unroll
+		for (int k = 0; k < 4; k++) {
+			q0[k] = __builtin_amdgcn_alignbit(d[k + 1], d[k], 16);
+			q1[k] = d[5 + k];
+		}
+		return f16_bits_to_f32(d[0]) * idot_q4(q0, x) +
+		       f16_bits_to_f32(d[4] >> 16) * idot_q4(q1, x + DBLK);
+	}
+};
+
+/* a down-panel block (row i) against the item's h digits */
+template <int WT> struct pdig;
+template <> struct pdig<1> {
+	__device__ static inline float dot(const u32 (&d)[9], int i, const u32 *h)
+	{
+		return idig<1>::dot(d, h, i);
+	}
+};
+template <> struct pdig<2> {
+	__device__ static inline float dot(const u32 (&d)[5], int i, const u32 *h)
+	{
+		u32 q[4];
+		const bool odd = i & 1;
+#pragma unroll
+		for (int k = 0; k < 4; k++)
+			q[k] = odd ? d[k + 1] : __builtin_amdgcn_alignbit(d[k + 1], d[k], 16);
+		return f16_bits_to_f32(odd ? d[0] >> 16 : d[0]) * idot_q4(q, h);
+	}
+};
+
 template <int COLS>
 __device__ static inline void lds_seg(const float *s, int seg, float (&x)[COLS])
 {
@@ -384,6 +548,51 @@ __device__ static void route_local(const DecodeArgs &a, u32 epoch, float *lds, u
 	const uint64_t *rep = (const uint64_t *)(a.sync + a.off_rep) +
 			      (size_t)(blockIdx.x % NREP) * a.rep_stride;
 	float *scr = lds + wave * (MOE_MAX_NE + 2 * MOE_MAX_TOPK);
+	if (a.T == 1) {
+		/* one token: wave 0 polls; every wave runs the softmax (the same
+		 * bits) and ranks each key against 64 / NW of the others; wave 0
+		 * adds the parts and fills the slots */
+		constexpr int NW = NT / WAVE, PER = WAVE / NW;
+		static_assert(PER % 2 == 0, "keys are read in pairs");
+		__shared__ float s_lg[WAVE];
+		__shared__ __attribute__((aligned(16))) uint64_t s_key[WAVE];
+		__shared__ int s_rk[NW][WAVE];
+		if (wave == 0) {
+			const uint64_t idle = (uint64_t)epoch << 32;
+			uint64_t v = 0;
+			int step = 0;
+			for (int round = 0;; round++) {
+				v = lane < a.NE ? ld_dev_u64(&rep[lane]) : idle;
+				if (__all((u32)(v >> 32) == epoch))
+					break;
+				if (round >= SPIN_LIMIT) {
+					if (lane == 0)
+						st_dev_u32(a.sync + MOE_SYNC_ERR_WORD, 1u);
+					break;
+				}
+				backoff(step);
+			}
+			s_lg[lane] = __builtin_bit_cast(float, (u32)v);
+		}
+		__syncthreads();
+		uint64_t key;
+		const float p = softmax64(s_lg[lane], a.NE, s_tab, lane, key);
+		if (wave == 0)
+			s_key[lane] = key;
+		__syncthreads();
+		s_rk[wave][lane] = rank_part64(s_key + wave * PER, PER, key);
+		__syncthreads();
+		if (wave == 0) {
+			int rank = 0;
+#pragma unroll
+			for (int w = 0; w < NW; w++)
+				rank += s_rk[w][lane];
+			topk_finish64(rank, p, s_ids, s_w, a.NE, a.K, a.renorm,
+				      (u32 *)(scr + MOE_MAX_NE), scr + MOE_MAX_NE + MOE_MAX_TOPK, lane);
+		}
+		__syncthreads();
+		return;
+	}
 	for (int t = wave; t < a.T; t += NT / WAVE) { /* NE <= 64: one expert per lane */
 		const uint64_t *row = rep + (size_t)t * a.NE;
 		float logit = 0.0f;
@@ -480,6 +689,7 @@ void k_moe_decode(DecodeArgs a)
 	__shared__ u32 s_epoch;
 	__shared__ uint64_t s_tab[32];
 	__shared__ __attribute__((aligned(16))) float s_h[DEC_CHUNK];
+	__shared__ __attribute__((aligned(16))) u32 s_hd[NT / WAVE][DBLK];
 	__shared__ int s_ok;
 
 	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
@@ -487,8 +697,8 @@ void k_moe_decode(DecodeArgs a)
 	const int NC = a.EI / DEC_CHUNK, IPT = a.K * NC, N = a.n_items;
 	const int q0 = item_lo(b, N, G), q1 = item_lo(b + 1, N, G);
 	const int t0 = q0 / IPT;
-	const int XS = (a.E / S::COLS) * (S::COLS + 4); /* floats of one staged token */
-	float *sx = lds;                                /* [DEC_TOKS][XS] tokens */
+	const int XS = (a.E / MOE_QK) * DBLK;           /* dwords of one staged token */
+	u32 *sx = (u32 *)lds;                           /* [DEC_TOKS][XS] token digits */
 	float *rl = lds + DEC_TOKS * XS;                /* routing scratch */
 
 	if (threadIdx.x < 32)
@@ -504,7 +714,7 @@ void k_moe_decode(DecodeArgs a)
 	 * router workgroups stage them after their router row) */
 	if (q0 < q1)
 		for (int t = t0; t <= (q1 - 1) / IPT; t++)
-			stage_seg<NT, S::COLS>(sx + (t - t0) * XS, a.x + (size_t)t * a.E, a.E);
+			stage_digits<NT>(sx + (t - t0) * XS, a.x + (size_t)t * a.E, a.E);
 	if (threadIdx.x == 0)
 		s_epoch = prev_epoch + 1;
 	__syncthreads();
@@ -532,13 +742,23 @@ void k_moe_decode(DecodeArgs a)
 	/* h rows of this wave: silu(gate . x) * (up . x) */
 	auto gateup = [&](int q) {
 		const int t = q / NC / a.K;
-		float xr[S::COLS], xs[2];
-		lds_seg<S::COLS>(sx + (t - t0) * XS, seg, xr);
-		S::xsum(xr, xs);
+		typedef idig<WT> I;
+		u32 xd[I::NB * DBLK]; /* this lane's segment: NB staged blocks */
+		{
+			const uint4 *s4 = (const uint4 *)(sx + (t - t0) * XS + seg * I::NB * DBLK);
+#pragma unroll
+			for (int k = 0; k < I::NB * DBLK / 4; k++) {
+				const uint4 v = s4[k];
+				xd[4 * k + 0] = v.x;
+				xd[4 * k + 1] = v.y;
+				xd[4 * k + 2] = v.z;
+				xd[4 * k + 3] = v.w;
+			}
+		}
 #pragma unroll
 		for (int s2 = 0; s2 < GG::NS; s2++) {
-			const float gv = group_sum<CG>(S::dot(R.g[s2], xr, seg, xs));
-			const float uv = group_sum<CG>(S::dot(R.u[s2], xr, seg, xs));
+			const float gv = group_sum<CG>(I::dot(R.g[s2], xd, seg));
+			const float uv = group_sum<CG>(I::dot(R.u[s2], xd, seg));
 			if (seg == 0)
 				s_h[wave * GG::HR + s2 * GG::RPS + sub] =
 					(gv / (1.0f + moe_expf_tab(-gv, s_tab))) * uv;
@@ -546,21 +766,29 @@ void k_moe_decode(DecodeArgs a)
 	};
 	/* this item's share of every output row: down panel . h, scaled */
 	auto down = [&](int q) {
-		float hr[DEC_CHUNK];
-		const float4 *h4 = (const float4 *)s_h;
+		/* every wave turns the 32 h values into digits itself (lanes 0-31,
+		 * its own LDS copy): no second workgroup barrier */
+		u32 *hw = s_hd[wave];
+		if (lane < DEC_CHUNK / 4)
+			stage_digits4(hw, ((const float4 *)s_h)[lane], lane);
+		WAVE_SYNC();
+		u32 hd[DBLK];
+		{
+			const uint4 *s4 = (const uint4 *)hw;
 #pragma unroll
-		for (int k = 0; k < DEC_CHUNK / 4; k++) {
-			const float4 v = h4[k];
-			hr[4 * k + 0] = v.x;
-			hr[4 * k + 1] = v.y;
-			hr[4 * k + 2] = v.z;
-			hr[4 * k + 3] = v.w;
+			for (int k = 0; k < DBLK / 4; k++) {
+				const uint4 v = s4[k];
+				hd[4 * k + 0] = v.x;
+				hd[4 * k + 1] = v.y;
+				hd[4 * k + 2] = v.z;
+				hd[4 * k + 3] = v.w;
+			}
 		}
-		const float hs = sum32(hr);
 		const float inv = 1.0f / s_w[q / NC];
 #pragma unroll
 		for (int r2 = 0; r2 < RPT; r2++)
-			acc[r2] = acc[r2] + D::dot(R.d[r2], (int)threadIdx.x + NT * r2, hr, hs) / inv;
+			acc[r2] = acc[r2] +
+				  pdig<WT>::dot(R.d[r2], (int)threadIdx.x + NT * r2, hd) / inv;
 	};
 	/* publish token t's accumulated outputs */
 	auto flush = [&](int t) {
@@ -706,7 +934,7 @@ static Geo geometry(int wtype, size_t E, size_t EI)
  * front (one PSLICE-float partial per wave) */
 static size_t decode_lds_bytes(const Geo &g, size_t E)
 {
-	size_t xs = DEC_TOKS * (E / (size_t)g.cols) * (size_t)(g.cols + 4);
+	size_t xs = DEC_TOKS * (E / MOE_QK) * DBLK;
 	size_t rt = (size_t)2 * 8 * (E / 8 + 4) + CHAIN_OVERRUN;
 	size_t tk = (size_t)(g.NT / WAVE) * (MOE_MAX_NE + 2 * MOE_MAX_TOPK);
 	return (xs + (rt > tk ? rt : tk)) * sizeof(float);

@@ -410,13 +410,12 @@ __device__ static inline float wave_max_f32(float v)
  * and order as wave_softmax_topk: max, e = expf(x - max), lane sums
  * s_l = e_l + e_{l+8} + ... in order, the tree ((s0+s4)+(s2+s6)) +
  * ((s1+s5)+(s3+s7)) (vector_avx2.h:126-132), the scalar tail, p = e / sum.
- * The ranks come from broadcast LDS reads of integer keys.  tab is the exp
- * table (an LDS copy), sp 128 floats of this wave's LDS (8-byte aligned),
- * ids/w receive the k slots (LDS or global).
+ * softmax64 returns p and the lane's rank key; keys order like the
+ * probabilities, ties broken towards the lower index:
+ * key = (bits(p) + 1) << 6 | (63 - index), 0 for lanes past NE.
  */
-__device__ static inline void wave_softmax_topk64(float logit, u32 *ids, float *wout, int NE,
-						  int K, int renorm, const uint64_t *tab,
-						  float *sp, u32 *sid, float *sw, int lane)
+__device__ static inline float softmax64(float logit, int NE, const uint64_t *tab, int lane,
+					 uint64_t &key)
 {
 	const bool valid = lane < NE;
 	const float mx = wave_max_f32(valid ? logit : -__builtin_inff());
@@ -439,23 +438,35 @@ __device__ static inline void wave_softmax_topk64(float logit, u32 *ids, float *
 	for (int i = nv; i < NE; i++)
 		sum += lane_f32(e, i);
 	const float p = e / sum;
+	/* p >= 0, so its bits order like the values: j beats i iff key_j > key_i */
+	key = valid ? ((uint64_t)(__builtin_bit_cast(u32, p) + 1u) << 6) | (uint64_t)(63 - lane) : 0;
+	return p;
+}
 
-	/* p >= 0, so its bits order like the values: j beats i iff key_j > key_i,
-	 * key = (bits(p) + 1) << 6 | (63 - index), 0 for lanes past NE */
-	uint64_t *sk = (uint64_t *)sp;
-	const uint64_t key = valid ? ((uint64_t)(__builtin_bit_cast(u32, p) + 1u) << 6) |
-					     (uint64_t)(63 - lane)
-				   : 0;
-	sk[lane] = key;
-	WAVE_SYNC();
+/* number of the n keys sk[0..n) (LDS, read as broadcasts) above key */
+__device__ static inline int rank_part64(const uint64_t *sk, int n, uint64_t key)
+{
 	int rank = 0;
 	const ulonglong2 *sk2 = (const ulonglong2 *)sk;
-#pragma unroll
-	for (int q = 0; q < 32; q++) {
+	for (int q = 0; q < n / 2; q++) {
 		const ulonglong2 v = sk2[q];
 		rank += (int)(v.x > key);
 		rank += (int)(v.y > key);
 	}
+	return rank;
+}
+
+/*
+ * top_k (nn.c:276-308) from the ranks: element i != 0 lands in slot k-1-rank_i
+ * iff rank_i < min(rank_0, k); the slots left over hold element 0 (every slot
+ * is seeded with it and only strictly greater values are inserted).  Then
+ * the Mixtral renorm (sequential sum, then divide: llama.c:422-427).  sid/sw
+ * are k entries of this wave's LDS; ids/w receive the slots (LDS or global).
+ */
+__device__ static inline void topk_finish64(int rank, float p, u32 *ids, float *wout, int NE,
+					    int K, int renorm, u32 *sid, float *sw, int lane)
+{
+	const bool valid = lane < NE;
 	const int r0 = __builtin_amdgcn_readlane(rank, 0);
 	const int lim = r0 < K ? r0 : K;
 	if (lane > 0 && valid && rank < lim) {
@@ -481,6 +492,20 @@ __device__ static inline void wave_softmax_topk64(float logit, u32 *ids, float *
 		ids[k] = sid[k];
 		wout[k] = sw[k];
 	}
+}
+
+/* all of it in one wave: sp 128 floats of this wave's LDS (8-byte aligned) */
+__device__ static inline void wave_softmax_topk64(float logit, u32 *ids, float *wout, int NE,
+						  int K, int renorm, const uint64_t *tab,
+						  float *sp, u32 *sid, float *sw, int lane)
+{
+	uint64_t key;
+	const float p = softmax64(logit, NE, tab, lane, key);
+	uint64_t *sk = (uint64_t *)sp;
+	sk[lane] = key;
+	WAVE_SYNC();
+	const int rank = rank_part64(sk, 64, key);
+	topk_finish64(rank, p, ids, wout, NE, K, renorm, sid, sw, lane);
 }
 
 #endif
