@@ -543,7 +543,10 @@ int hip_moe_ffn(hip_moe_layer *L, const float *x, float *out, size_t T,
 		if (err) { /* flags may be left mid-flight: restart the epoch at zero */
 			hipMemset(L->d_sync, 0, L->sync_words * sizeof(uint32_t));
 			hipMemset(L->d_part, 0, L->part_words * sizeof(uint64_t));
-			set_err("persistent kernel: a dependency wait timed out");
+			static const char *what[] = {"", "router logits", "partial sums",
+						     "start flags"};
+			set_err("persistent kernel: a dependency wait timed out (%s)",
+				err < 4 ? what[err] : "unknown");
 			return 0;
 		}
 	}

@@ -133,7 +133,7 @@ __host__ __device__ static inline int item_owner(int x, int n, int G)
  * Each thread checks n / NT of them per round.
  */
 template <int NT>
-__device__ static inline void wait_flags(const u32 *f, int n, u32 epoch, u32 *err)
+__device__ static inline void wait_flags(const u32 *f, int n, u32 epoch, u32 *err, u32 code)
 {
 	__shared__ int s_ok;
 	int step = 0;
@@ -151,7 +151,7 @@ __device__ static inline void wait_flags(const u32 *f, int n, u32 epoch, u32 *er
 			return;
 		if (round >= SPIN_LIMIT) {
 			if (threadIdx.x == 0)
-				st_dev_u32(err, 1u);
+				st_dev_u32(err, code);
 			return;
 		}
 		backoff(step);
@@ -567,7 +567,7 @@ __device__ static void route_local(const DecodeArgs &a, u32 epoch, float *lds, u
 					break;
 				if (round >= SPIN_LIMIT) {
 					if (lane == 0)
-						st_dev_u32(a.sync + MOE_SYNC_ERR_WORD, 1u);
+						st_dev_u32(a.sync + MOE_SYNC_ERR_WORD, MOE_ERR_ROUTE);
 					break;
 				}
 				backoff(step);
@@ -605,7 +605,7 @@ __device__ static void route_local(const DecodeArgs &a, u32 epoch, float *lds, u
 			}
 			if (round >= SPIN_LIMIT) {
 				if (lane == 0)
-					st_dev_u32(a.sync + MOE_SYNC_ERR_WORD, 1u);
+					st_dev_u32(a.sync + MOE_SYNC_ERR_WORD, MOE_ERR_ROUTE);
 				break;
 			}
 			backoff(step);
@@ -863,7 +863,7 @@ void k_moe_decode(DecodeArgs a)
 			if (!pending)
 				break;
 			if (round >= SPIN_LIMIT) {
-				st_dev_u32(a.sync + MOE_SYNC_ERR_WORD, 1u);
+				st_dev_u32(a.sync + MOE_SYNC_ERR_WORD, MOE_ERR_COMBINE);
 				break;
 			}
 			__builtin_amdgcn_s_sleep(1);
@@ -893,7 +893,7 @@ void k_moe_decode(DecodeArgs a)
 	 * the next launch starts only after this one drains */
 	if (b != 0)
 		return;
-	wait_flags<NT>(startf + 1, G - 1, epoch, a.sync + MOE_SYNC_ERR_WORD);
+	wait_flags<NT>(startf + 1, G - 1, epoch, a.sync + MOE_SYNC_ERR_WORD, MOE_ERR_FLAGS);
 	if (threadIdx.x == 0)
 		st_dev_u32(a.sync, epoch);
 }

@@ -19,7 +19,10 @@ extern "C" {
 #define MOE_MAX_NE 256
 #define MOE_MAX_TOPK 64
 #define MOE_FUSED_MAX_P 64  /* T*K handled by the persistent decode kernel */
-#define MOE_SYNC_ERR_WORD 256 /* error word in the persistent kernel's counters */
+#define MOE_SYNC_ERR_WORD 256 /* error word in the persistent kernel's counters: */
+#define MOE_ERR_ROUTE 1   /* a wait for router logits ran out */
+#define MOE_ERR_COMBINE 2 /* a wait for partial sums ran out */
+#define MOE_ERR_FLAGS 3   /* the end-of-launch start-flag check ran out */
 
 /* lanes per gate/up row for a K-long dot: the largest power of two <= 64
  * that divides K / 64, and the number of K-chunks the row is split into. */
