@@ -25,26 +25,27 @@
 /* ------------------------------------------------------------------ */
 
 /*
- * A workgroup takes RT_TOK tokens (one per wave) x 64 experts (one per lane).
- * Each thread keeps the 8 AVX2 lane accumulators of its logit: accumulator l
- * adds x[k]*w[k] for k = l, l+8, l+16, ... in increasing k with FMA
- * (dot_f32_f32, matmul.c:91-105; the tiled T>1 path of matmul.c:213-238 keeps
- * the same per-element order), then the lanes meet in the tree
- * ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) of vector_avx2.h:126-132, and the
- * logit is fl(bias + dot) (matmul.c:24-32).
+ * A workgroup of 4 waves computes a tile of JT experts x TT tokens.  Lane
+ * (token, expert j, half hf) keeps four of the 8 AVX2 lane accumulators of
+ * its logit: accumulator l (l = 4hf .. 4hf+3) adds x[k]*w[k] for k = l,
+ * l+8, l+16, ... in increasing k with FMA (dot_f32_f32, matmul.c:91-105;
+ * the tiled T>1 path of matmul.c:213-238 keeps the same per-element order).
+ * At the end the two halves meet in the tree
+ * ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) of vector_avx2.h:126-132 and the
+ * logit is fl(bias + dot) (matmul.c:24-32).  A lane reads its four
+ * accumulators' operands as one 16-byte LDS read each of w and x, so 1024
+ * FMAs per lane (d_model 2048) and one wave per (4 tokens or 1 token) x
+ * (8 or 32 experts): many waves, short chains.
  *
  * Router rows and tokens stream through an LDS ring of RT_NST stages of
- * RT_KC columns, filled by LDS-DMA loads (global_load_lds_dwordx4, issued
- * from inline assembly so the K loop alone decides what to wait for):
- * router rows [64][RT_KC] with 16-byte chunk c of row r at slot
- * 16r + (c ^ (r & 15)) (a wave reads 64 rows conflict-free), tokens
- * [RT_TOK][RT_KC] (a wave reads its token row as a broadcast).
+ * RT_KC = 256 columns (one 1 KB row piece per wave-wide LDS-DMA load,
+ * global_load_lds_dwordx4, issued from inline assembly so the K loop alone
+ * decides what to wait for); rows are padded to RT_RS bytes so the 16-byte
+ * reads of 8 experts x 2 halves hit distinct banks.
  */
-#define RT_TOK 8
-#define RT_KC 64
-#define RT_NST 5
-#define RT_WSZ (64 * RT_KC * 4)
-#define RT_SSZ (RT_WSZ + RT_TOK * RT_KC * 4)
+#define RT_KC 256
+#define RT_RS (RT_KC * 4 + 32)
+#define RT_NST 4
 
 __device__ static inline void rt_dma16(const void *sbase, u32 voff, u32 lds)
 {
@@ -61,79 +62,91 @@ __device__ static inline void rt_wait_vm()
 	__builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
-__global__ __launch_bounds__(RT_TOK * 64) void k_router(const float *__restrict__ x,
+template <int JT> struct rt_geo {
+	static constexpr int TPW = WAVE / (2 * JT); /* tokens per wave */
+	static constexpr int TT = 4 * TPW;          /* tokens per workgroup */
+	static constexpr int ROWS = JT + TT;        /* LDS rows per stage */
+	static constexpr int PER = ROWS / 4;        /* row loads per wave and stage */
+	static constexpr int SSZ = ROWS * RT_RS;
+	static_assert(ROWS % 4 == 0, "every wave issues the same loads");
+};
+
+template <int JT>
+__global__ __launch_bounds__(256) void k_router(const float *__restrict__ x,
 						const float *__restrict__ wr,
 						const float *__restrict__ bias,
 						float *__restrict__ logits, int T, int E, int NE,
 						_Float16 *__restrict__ xh)
 {
-	__shared__ __attribute__((aligned(16))) uint8_t ring[RT_NST * RT_SSZ];
-	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-	const int t0 = blockIdx.x * RT_TOK, j0 = blockIdx.y * 64;
-	const int t = t0 + wave, j = j0 + lane;
-	const int nc = E / RT_KC;
+	typedef rt_geo<JT> RG;
+	__shared__ __attribute__((aligned(16))) uint8_t ring[RT_NST * RG::SSZ];
+	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+	const int t0 = blockIdx.x * RG::TT, j0 = blockIdx.y * JT;
+	const int tw = lane / (2 * JT), jl = (lane >> 1) % JT, hf = lane & 1;
+	const int tl = wave * RG::TPW + tw; /* token row of the tile */
+	const int t = t0 + tl, j = j0 + jl;
+	const int ns = E / RT_KC;
 	const u32 l0 = (u32)(uintptr_t)(const __attribute__((address_space(3))) char *)ring;
 
-	/* this lane's loads: RT_WQ router chunks (rows r, swizzled chunks) and,
-	 * for lanes < 16, a 16-byte chunk of its wave's token row */
-	constexpr int RT_WQ = 16 / RT_TOK; /* the 64 x RT_KC tile is 16 KB */
-	u32 woff[RT_WQ];
+	/* row loads of this wave: rows wave, wave + 4, ... of [w rows | x rows];
+	 * rows past NE or T repeat the last one (their results are not kept) */
+	u32 roff[RG::PER];
+	bool isw[RG::PER];
 #pragma unroll
-	for (int q = 0; q < RT_WQ; q++) {
-		const int f = (wave * RT_WQ + q) * 64 + lane, r = f >> 4, c = (f & 15) ^ (r & 15);
-		woff[q] = (u32)(((size_t)(j0 + r < NE ? j0 + r : 0) * E) * 4 + 16 * c);
+	for (int q = 0; q < RG::PER; q++) {
+		const int r = wave + 4 * q;
+		isw[q] = r < JT;
+		const int src = isw[q] ? min(j0 + r, NE - 1) : min(t0 + r - JT, T - 1);
+		roff[q] = (u32)((size_t)src * E * 4 + 16 * lane);
 	}
-	const u32 xoff = (u32)((size_t)(t < T ? t : 0) * E * 4 + 16 * (lane & 15));
 	auto issue = [&](int s) {
-		const u32 st = l0 + (u32)((s % RT_NST) * RT_SSZ);
-		const float *wb = wr + (size_t)s * RT_KC, *xb = x + (size_t)s * RT_KC;
+		const u32 st = l0 + (u32)((s % RT_NST) * RG::SSZ);
 #pragma unroll
-		for (int q = 0; q < RT_WQ; q++)
-			rt_dma16(wb, woff[q], st + (u32)((wave * RT_WQ + q) * 1024));
-		if (lane < 16)
-			rt_dma16(xb, xoff, st + RT_WSZ + (u32)(wave * RT_KC * 4));
+		for (int q = 0; q < RG::PER; q++)
+			rt_dma16((isw[q] ? wr : x) + (size_t)s * RT_KC, roff[q],
+				 st + (u32)((wave + 4 * q) * RT_RS));
 	};
 
-	float acc[8];
-#pragma unroll
-	for (int l = 0; l < 8; l++)
-		acc[l] = 0.0f;
+	float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
 	for (int s = 0; s < RT_NST - 1; s++)
-		if (s < nc)
+		if (s < ns)
 			issue(s);
-	for (int s = 0; s < nc; s++) {
-		if (s + RT_NST - 2 < nc)
-			rt_wait_vm<(RT_NST - 2) * (RT_WQ + 1)>();
+	for (int s = 0; s < ns; s++) {
+		if (s + RT_NST - 2 < ns)
+			rt_wait_vm<(RT_NST - 2) * RG::PER>();
 		else
 			rt_wait_vm<0>();
 		__syncthreads(); /* stage s landed for every wave; stage s-1 is free */
-		if (s + RT_NST - 1 < nc)
+		if (s + RT_NST - 1 < ns)
 			issue(s + RT_NST - 1);
-		const uint8_t *st = ring + (s % RT_NST) * RT_SSZ;
-		const float *xr = (const float *)(st + RT_WSZ) + wave * RT_KC;
-		const uint8_t *wrow = st + lane * (RT_KC * 4);
-		if (xh && blockIdx.y == 0 && t < T)
-			xh[(size_t)t * E + (size_t)s * RT_KC + lane] = (_Float16)xr[lane];
-#pragma unroll
-		for (int k = 0; k < RT_KC; k += 8) {
-			const int c = k >> 2; /* 16-byte chunks c and c+1 */
-			const float4 xa = *(const float4 *)(xr + k), xb = *(const float4 *)(xr + k + 4);
-			const float4 wa = *(const float4 *)(wrow + 16 * (c ^ (lane & 15)));
-			const float4 wb = *(const float4 *)(wrow + 16 * ((c + 1) ^ (lane & 15)));
-			acc[0] = __builtin_fmaf(xa.x, wa.x, acc[0]);
-			acc[1] = __builtin_fmaf(xa.y, wa.y, acc[1]);
-			acc[2] = __builtin_fmaf(xa.z, wa.z, acc[2]);
-			acc[3] = __builtin_fmaf(xa.w, wa.w, acc[3]);
-			acc[4] = __builtin_fmaf(xb.x, wb.x, acc[4]);
-			acc[5] = __builtin_fmaf(xb.y, wb.y, acc[5]);
-			acc[6] = __builtin_fmaf(xb.z, wb.z, acc[6]);
-			acc[7] = __builtin_fmaf(xb.w, wb.w, acc[7]);
+		const uint8_t *st = ring + (s % RT_NST) * RG::SSZ;
+		const float *wrow = (const float *)(st + jl * RT_RS) + 4 * hf;
+		const float *xrow = (const float *)(st + (JT + tl) * RT_RS) + 4 * hf;
+		if (xh && blockIdx.y == 0)
+			for (int i = threadIdx.x; i < RG::TT * RT_KC; i += 256) {
+				const int r = i / RT_KC, c = i % RT_KC;
+				if (t0 + r < T)
+					xh[(size_t)(t0 + r) * E + (size_t)s * RT_KC + c] =
+						(_Float16)((const float *)(st + (JT + r) * RT_RS))[c];
+			}
+#pragma unroll 8
+		for (int i = 0; i < RT_KC / 8; i++) {
+			const float4 wv = *(const float4 *)(wrow + 8 * i);
+			const float4 xv = *(const float4 *)(xrow + 8 * i);
+			acc[0] = __builtin_fmaf(xv.x, wv.x, acc[0]);
+			acc[1] = __builtin_fmaf(xv.y, wv.y, acc[1]);
+			acc[2] = __builtin_fmaf(xv.z, wv.z, acc[2]);
+			acc[3] = __builtin_fmaf(xv.w, wv.w, acc[3]);
 		}
 	}
-	if (t < T && j < NE) {
-		const float d = ((acc[0] + acc[4]) + (acc[2] + acc[6])) +
-				((acc[1] + acc[5]) + (acc[3] + acc[7]));
+	/* accumulators 4..7 from the partner lane (hf = 1) */
+	float b[4];
+#pragma unroll
+	for (int c = 0; c < 4; c++)
+		b[c] = __shfl_xor(acc[c], 1, WAVE);
+	if (hf == 0 && t < T && j < NE) {
+		const float d = ((acc[0] + b[0]) + (acc[2] + b[2])) + ((acc[1] + b[1]) + (acc[3] + b[3]));
 		logits[(size_t)t * NE + j] = (bias ? bias[j] : 0.0f) + d;
 	}
 }
@@ -155,6 +168,38 @@ __global__ __launch_bounds__(64) void k_softmax_topk(const float *__restrict__ l
 	wave_softmax_topk(logits + (size_t)t * NE, probs ? probs + (size_t)t * NE : NULL,
 			  ids + (size_t)t * K, wout + (size_t)t * K, NE, K, renorm, sp, sid, sw,
 			  threadIdx.x);
+}
+
+/* NE <= 64: one wave per token, expert i in lane i, four tokens per
+ * workgroup (softmax64 / rank_part64 / topk_finish64: the same arithmetic
+ * and slots as wave_softmax_topk) */
+__global__ __launch_bounds__(256) void k_softmax_topk64(const float *__restrict__ logits,
+							float *__restrict__ probs,
+							u32 *__restrict__ ids,
+							float *__restrict__ wout, int T, int NE,
+							int K, int renorm)
+{
+	__shared__ uint64_t s_tab[32];
+	__shared__ __attribute__((aligned(16))) uint64_t s_key[4][WAVE];
+	__shared__ u32 s_id[4][MOE_MAX_TOPK];
+	__shared__ float s_w[4][MOE_MAX_TOPK];
+	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+	const int t = blockIdx.x * 4 + wave;
+	const float logit = t < T && lane < NE ? logits[(size_t)t * NE + lane] : 0.0f;
+	if (threadIdx.x < 32)
+		s_tab[threadIdx.x] = moe_exp2_tab[threadIdx.x];
+	__syncthreads();
+	if (t >= T)
+		return;
+	uint64_t key;
+	const float p = softmax64(logit, NE, s_tab, lane, key);
+	if (probs && lane < NE)
+		probs[(size_t)t * NE + lane] = p;
+	s_key[wave][lane] = key;
+	WAVE_SYNC();
+	const int rank = rank_part64(s_key[wave], WAVE, key);
+	topk_finish64(rank, p, ids + (size_t)t * K, wout + (size_t)t * K, NE, K, renorm,
+		      s_id[wave], s_w[wave], lane);
 }
 
 /* ------------------------------------------------------------------ */
@@ -293,25 +338,55 @@ extern "C" size_t moe_down_part_floats(size_t E, size_t EI, size_t P)
 /* combine                                                             */
 /* ------------------------------------------------------------------ */
 
+/* four output columns per thread; the loads of up to 8 slots (and their
+ * K-chunks) are issued together, then added in slot order */
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypart,
 						 const float *__restrict__ w,
 						 float *__restrict__ out, int K, int E,
 						 int kchunks)
 {
 	const int t = blockIdx.y;
-	const int i = blockIdx.x * 256 + threadIdx.x;
+	const int i = 4 * (blockIdx.x * 256 + threadIdx.x);
 	if (i >= E)
 		return;
-	float acc = 0.0f;
-	for (int s = 0; s < K; s++) {
-		const size_t p = (size_t)t * K + s;
-		float y = ypart[p * kchunks * E + i];
+	float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+	for (int s0 = 0; s0 < K; s0 += 8) {
+		const int ns = K - s0 < 8 ? K - s0 : 8;
+		float4 y[8];
+#pragma unroll
+		for (int s = 0; s < 8; s++)
+			if (s < ns)
+				y[s] = *(const float4 *)&ypart[((size_t)t * K + s0 + s) * kchunks * E + i];
 		for (int kc = 1; kc < kchunks; kc++)
-			y += ypart[(p * kchunks + kc) * E + i];
-		float inv = 1.0f / (w ? w[p] : 1.0f);
-		acc = acc + y / inv;
+#pragma unroll
+			for (int s = 0; s < 8; s++)
+				if (s < ns) {
+					const float4 v = *(const float4 *)&ypart
+						[(((size_t)t * K + s0 + s) * kchunks + kc) * E + i];
+					y[s].x += v.x;
+					y[s].y += v.y;
+					y[s].z += v.z;
+					y[s].w += v.w;
+				}
+#pragma unroll
+		for (int s = 0; s < 8; s++)
+			if (s < ns) {
+				const float inv = 1.0f / (w ? w[(size_t)t * K + s0 + s] : 1.0f);
+				acc.x = acc.x + y[s].x / inv;
+				acc.y = acc.y + y[s].y / inv;
+				acc.z = acc.z + y[s].z / inv;
+				acc.w = acc.w + y[s].w / inv;
+			}
 	}
-	out[(size_t)t * E + i] = acc;
+	float *o = &out[(size_t)t * E + i];
+	if (((uintptr_t)out & 15) == 0) {
+		*(float4 *)o = acc;
+	} else { /* a caller's output that is not 16-byte aligned */
+		o[0] = acc.x;
+		o[1] = acc.y;
+		o[2] = acc.z;
+		o[3] = acc.w;
+	}
 }
 
 __global__ __launch_bounds__(256) void k_expf(const float *__restrict__ in,
@@ -352,11 +427,21 @@ extern "C" int moe_kchunks(size_t K)
 extern "C" int moe_launch_router(const float *x, const float *wr, const float *bias,
 				 float *logits, int T, int E, int NE, void *xh, void *stream)
 {
-	if (E % RT_KC || (size_t)NE * E * 4 > 0xffffffffull || (size_t)T * E * 4 > 0xffffffffull)
+	if (T < 1 || NE < 1 || E % RT_KC || (size_t)NE * E * 4 > 0xffffffffull ||
+	    (size_t)T * E * 4 > 0xffffffffull)
 		return (int)hipErrorInvalidValue;
-	dim3 grid((T + RT_TOK - 1) / RT_TOK, (NE + 63) / 64);
-	hipLaunchKernelGGL(k_router, grid, dim3(RT_TOK * 64), 0, (hipStream_t)stream, x, wr,
-			   bias, logits, T, E, NE, (_Float16 *)xh);
+	/* 32 experts per tile; 8 (and 4 tokens per wave) for small expert counts */
+	if (NE <= 8) {
+		typedef rt_geo<8> RG;
+		dim3 grid((T + RG::TT - 1) / RG::TT, (NE + 7) / 8);
+		hipLaunchKernelGGL(k_router<8>, grid, dim3(256), 0,
+				   (hipStream_t)stream, x, wr, bias, logits, T, E, NE, (_Float16 *)xh);
+	} else {
+		typedef rt_geo<32> RG;
+		dim3 grid((T + RG::TT - 1) / RG::TT, (NE + 31) / 32);
+		hipLaunchKernelGGL(k_router<32>, grid, dim3(256), 0,
+				   (hipStream_t)stream, x, wr, bias, logits, T, E, NE, (_Float16 *)xh);
+	}
 	return (int)hipGetLastError();
 }
 
@@ -364,8 +449,12 @@ extern "C" int moe_launch_softmax_topk(const float *logits, float *probs, uint32
 				       float *w, int T, int NE, int K, int renorm,
 				       void *stream)
 {
-	hipLaunchKernelGGL(k_softmax_topk, dim3(T), dim3(64), 0, (hipStream_t)stream,
-			   logits, probs, ids, w, NE, K, renorm);
+	if (NE <= WAVE)
+		hipLaunchKernelGGL(k_softmax_topk64, dim3((T + 3) / 4), dim3(256), 0,
+				   (hipStream_t)stream, logits, probs, ids, w, T, NE, K, renorm);
+	else
+		hipLaunchKernelGGL(k_softmax_topk, dim3(T), dim3(64), 0, (hipStream_t)stream,
+				   logits, probs, ids, w, NE, K, renorm);
 	return (int)hipGetLastError();
 }
 
@@ -449,7 +538,9 @@ extern "C" int moe_launch_down(int wtype, const uint8_t *down, size_t expert_str
 extern "C" int moe_launch_combine(const float *ypart, const float *w, float *out, int T,
 				  int K, int E, int kchunks, void *stream)
 {
-	dim3 grid((E + 255) / 256, T);
+	if (E % 4)
+		return (int)hipErrorInvalidValue;
+	dim3 grid((E + 1023) / 1024, T);
 	hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, (hipStream_t)stream, ypart, w,
 			   out, K, E, kchunks);
 	return (int)hipGetLastError();
