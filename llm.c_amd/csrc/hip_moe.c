@@ -343,9 +343,10 @@ static int route(hip_moe_layer *L, const float *d_x, size_t T, const float *d_bi
 		 hipStream_t s)
 {
 	LCHK(moe_launch_router(d_x, L->d_router, d_bias, d_logits, (int)T, (int)L->E,
-			       (int)L->NE, d_xh, s), "router");
+			       (int)L->NE, s), "router");
 	LCHK(moe_launch_softmax_topk(d_logits, d_probs, d_ids, d_w, (int)T, (int)L->NE,
-				     (int)L->topk, L->renorm, s), "softmax/top-k");
+				     (int)L->topk, L->renorm, d_x, d_xh, (int)L->E, s),
+	     "softmax/top-k");
 	return 1;
 }
 

@@ -29,13 +29,13 @@ extern "C" {
 int moe_lanes_per_row(size_t K);
 int moe_kchunks(size_t K);
 
-/* xh (optional, f16 [T][E]): also write the tokens rounded to f16 */
 int moe_launch_router(const float *x, const float *wr, const float *bias,
-                      float *logits, int T, int E, int NE, void *xh, void *stream);
+                      float *logits, int T, int E, int NE, void *stream);
 
+/* xh (optional, f16 [T][E]): also write the tokens x [T][E] rounded to f16 */
 int moe_launch_softmax_topk(const float *logits, float *probs, uint32_t *ids,
                             float *w, int T, int NE, int K, int renorm,
-                            void *stream);
+                            const float *x, void *xh, int E, void *stream);
 
 /* h[p][EI] = silu(gate_e . x_t) * (up_e . x_t), p = t*K + s, e = ids[p]
  * (or fixed_e >= 0 for every p). */

@@ -25,27 +25,30 @@
 /* ------------------------------------------------------------------ */
 
 /*
- * A workgroup of 4 waves computes a tile of JT experts x TT tokens.  Lane
- * (token, expert j, half hf) keeps four of the 8 AVX2 lane accumulators of
- * its logit: accumulator l (l = 4hf .. 4hf+3) adds x[k]*w[k] for k = l,
- * l+8, l+16, ... in increasing k with FMA (dot_f32_f32, matmul.c:91-105;
- * the tiled T>1 path of matmul.c:213-238 keeps the same per-element order).
- * At the end the two halves meet in the tree
- * ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) of vector_avx2.h:126-132 and the
- * logit is fl(bias + dot) (matmul.c:24-32).  A lane reads its four
- * accumulators' operands as one 16-byte LDS read each of w and x, so 1024
- * FMAs per lane (d_model 2048) and one wave per (4 tokens or 1 token) x
- * (8 or 32 experts): many waves, short chains.
+ * A workgroup of NW waves computes a tile of JT experts x TT tokens.  Each
+ * logit is the 8 AVX2 lane accumulators of dot_f32_f32 (matmul.c:91-105):
+ * accumulator l adds x[k]*w[k] for k = l, l+8, l+16, ... in increasing k
+ * with FMA (the tiled T>1 path of matmul.c:213-238 keeps the same
+ * per-element order); then the tree ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7))
+ * of vector_avx2.h:126-132 and logit = fl(bias + dot) (matmul.c:24-32).
+ *   CH = 4: lane (token, expert, half h) runs accumulators 4h .. 4h+3,
+ *           reading each step's operands as one 16-byte LDS read of w and
+ *           of x; the halves meet through one lane shuffle.  Many tokens.
+ *   CH = 1: lane (token, expert, l) runs accumulator l alone (8 lanes per
+ *           logit, the shortest chain); the tree is three lane shuffles.
+ *           Few tokens: more workgroups.
  *
- * Router rows and tokens stream through an LDS ring of RT_NST stages of
+ * Router rows and tokens stream through an LDS ring of NST stages of
  * RT_KC = 256 columns (one 1 KB row piece per wave-wide LDS-DMA load,
  * global_load_lds_dwordx4, issued from inline assembly so the K loop alone
- * decides what to wait for); rows are padded to RT_RS bytes so the 16-byte
- * reads of 8 experts x 2 halves hit distinct banks.
+ * decides what to wait for); rows are padded to RT_RS bytes so the reads of
+ * one wave hit distinct banks.  Every workgroup of an expert block reads
+ * the same router rows at the same time, so first each one pulls a slice of
+ * the block into its XCD's L2 (workgroups are dealt round-robin over the 8
+ * XCDs: slice (blockIdx.x / 8) % nsl), and the ring's loads then hit there.
  */
 #define RT_KC 256
 #define RT_RS (RT_KC * 4 + 32)
-#define RT_NST 4
 
 __device__ static inline void rt_dma16(const void *sbase, u32 voff, u32 lds)
 {
@@ -62,105 +65,146 @@ __device__ static inline void rt_wait_vm()
 	__builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
-template <int JT> struct rt_geo {
-	static constexpr int TPW = WAVE / (2 * JT); /* tokens per wave */
-	static constexpr int TT = 4 * TPW;          /* tokens per workgroup */
-	static constexpr int ROWS = JT + TT;        /* LDS rows per stage */
-	static constexpr int PER = ROWS / 4;        /* row loads per wave and stage */
+template <int JT, int CH, int NW> struct rt_geo {
+	static constexpr int LPL = 8 / CH;                /* lanes per logit */
+	static constexpr int TPW = WAVE / (LPL * JT);     /* tokens per wave */
+	static constexpr int TT = NW * TPW;               /* tokens per workgroup */
+	static constexpr int ROWS = JT + TT;              /* LDS rows per stage */
+	static constexpr int PER = ROWS / NW;             /* row loads per wave and stage */
 	static constexpr int SSZ = ROWS * RT_RS;
-	static_assert(ROWS % 4 == 0, "every wave issues the same loads");
+	static constexpr int NST1 = 150 * 1024 / SSZ, NST2 = 63 / PER + 2;
+	static constexpr int NST = NST1 < NST2 ? NST1 : NST2; /* ring stages */
+	static_assert(ROWS % NW == 0 && TPW >= 1 && NST >= 3, "router tile geometry");
 };
 
-template <int JT>
-__global__ __launch_bounds__(256) void k_router(const float *__restrict__ x,
-						const float *__restrict__ wr,
-						const float *__restrict__ bias,
-						float *__restrict__ logits, int T, int E, int NE,
-						_Float16 *__restrict__ xh)
+template <int JT, int CH, int NW>
+__global__ __launch_bounds__(NW * WAVE) void k_router(const float *__restrict__ x,
+						      const float *__restrict__ wr,
+						      const float *__restrict__ bias,
+						      float *__restrict__ logits, int T, int E, int NE)
 {
-	typedef rt_geo<JT> RG;
-	__shared__ __attribute__((aligned(16))) uint8_t ring[RT_NST * RG::SSZ];
+	typedef rt_geo<JT, CH, NW> RG;
+	constexpr int NST = RG::NST;
+	__shared__ __attribute__((aligned(16))) uint8_t ring[NST * RG::SSZ + 1024];
 	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
 	const int t0 = blockIdx.x * RG::TT, j0 = blockIdx.y * JT;
-	const int tw = lane / (2 * JT), jl = (lane >> 1) % JT, hf = lane & 1;
+	const int tw = lane / (RG::LPL * JT), jl = (lane / RG::LPL) % JT, sub = lane % RG::LPL;
 	const int tl = wave * RG::TPW + tw; /* token row of the tile */
 	const int t = t0 + tl, j = j0 + jl;
 	const int ns = E / RT_KC;
 	const u32 l0 = (u32)(uintptr_t)(const __attribute__((address_space(3))) char *)ring;
 
-	/* row loads of this wave: rows wave, wave + 4, ... of [w rows | x rows];
+	/* this workgroup's slice of the expert block, into L2: one 4-byte piece
+	 * per 128-byte line, landing in a scratch kilobyte of LDS */
+	{
+		const int nrow = min(JT, NE - j0);
+		const int nlines = nrow * E / 32;
+		const int nsl = max(1, min(16, (int)gridDim.x / 8)), sl = (blockIdx.x / 8) % nsl;
+		const float *blk = wr + (size_t)j0 * E;
+		for (int q = wave; q * WAVE < nlines / nsl; q += NW) {
+			const int line = sl + nsl * min(q * WAVE + lane, nlines / nsl - 1);
+			rt_dma16(blk, (u32)line * 128u, l0 + (u32)(NST * RG::SSZ));
+		}
+	}
+
+	/* row loads of this wave: rows wave, wave + NW, ... of [w rows | x rows];
 	 * rows past NE or T repeat the last one (their results are not kept) */
 	u32 roff[RG::PER];
 	bool isw[RG::PER];
 #pragma unroll
 	for (int q = 0; q < RG::PER; q++) {
-		const int r = wave + 4 * q;
+		const int r = wave + NW * q;
 		isw[q] = r < JT;
 		const int src = isw[q] ? min(j0 + r, NE - 1) : min(t0 + r - JT, T - 1);
 		roff[q] = (u32)((size_t)src * E * 4 + 16 * lane);
 	}
 	auto issue = [&](int s) {
-		const u32 st = l0 + (u32)((s % RT_NST) * RG::SSZ);
+		const u32 st = l0 + (u32)((s % NST) * RG::SSZ);
 #pragma unroll
 		for (int q = 0; q < RG::PER; q++)
 			rt_dma16((isw[q] ? wr : x) + (size_t)s * RT_KC, roff[q],
-				 st + (u32)((wave + 4 * q) * RT_RS));
+				 st + (u32)((wave + NW * q) * RT_RS));
 	};
 
-	float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+	float acc[CH];
 #pragma unroll
-	for (int s = 0; s < RT_NST - 1; s++)
+	for (int c = 0; c < CH; c++)
+		acc[c] = 0.0f;
+#pragma unroll
+	for (int s = 0; s < NST - 1; s++)
 		if (s < ns)
 			issue(s);
 	for (int s = 0; s < ns; s++) {
-		if (s + RT_NST - 2 < ns)
-			rt_wait_vm<(RT_NST - 2) * RG::PER>();
+		if (s + NST - 2 < ns)
+			rt_wait_vm<(NST - 2) * RG::PER>();
 		else
 			rt_wait_vm<0>();
 		__syncthreads(); /* stage s landed for every wave; stage s-1 is free */
-		if (s + RT_NST - 1 < ns)
-			issue(s + RT_NST - 1);
-		const uint8_t *st = ring + (s % RT_NST) * RG::SSZ;
-		const float *wrow = (const float *)(st + jl * RT_RS) + 4 * hf;
-		const float *xrow = (const float *)(st + (JT + tl) * RT_RS) + 4 * hf;
-		if (xh && blockIdx.y == 0)
-			for (int i = threadIdx.x; i < RG::TT * RT_KC; i += 256) {
-				const int r = i / RT_KC, c = i % RT_KC;
-				if (t0 + r < T)
-					xh[(size_t)(t0 + r) * E + (size_t)s * RT_KC + c] =
-						(_Float16)((const float *)(st + (JT + r) * RT_RS))[c];
-			}
+		if (s + NST - 1 < ns)
+			issue(s + NST - 1);
+		const uint8_t *st = ring + (s % NST) * RG::SSZ;
+		const float *wrow = (const float *)(st + jl * RT_RS) + CH * sub;
+		const float *xrow = (const float *)(st + (JT + tl) * RT_RS) + CH * sub;
+		if (CH == 4) {
 #pragma unroll 8
-		for (int i = 0; i < RT_KC / 8; i++) {
-			const float4 wv = *(const float4 *)(wrow + 8 * i);
-			const float4 xv = *(const float4 *)(xrow + 8 * i);
-			acc[0] = __builtin_fmaf(xv.x, wv.x, acc[0]);
-			acc[1] = __builtin_fmaf(xv.y, wv.y, acc[1]);
-			acc[2] = __builtin_fmaf(xv.z, wv.z, acc[2]);
-			acc[3] = __builtin_fmaf(xv.w, wv.w, acc[3]);
+			for (int i = 0; i < RT_KC / 8; i++) {
+				const float4 wv = *(const float4 *)(wrow + 8 * i);
+				const float4 xv = *(const float4 *)(xrow + 8 * i);
+				acc[0] = __builtin_fmaf(xv.x, wv.x, acc[0]);
+				acc[1 % CH] = __builtin_fmaf(xv.y, wv.y, acc[1 % CH]);
+				acc[2 % CH] = __builtin_fmaf(xv.z, wv.z, acc[2 % CH]);
+				acc[3 % CH] = __builtin_fmaf(xv.w, wv.w, acc[3 % CH]);
+			}
+		} else {
+#pragma unroll 8
+			for (int i = 0; i < RT_KC / 8; i++)
+				acc[0] = __builtin_fmaf(xrow[8 * i], wrow[8 * i], acc[0]);
 		}
 	}
-	/* accumulators 4..7 from the partner lane (hf = 1) */
-	float b[4];
+	float d;
+	if (CH == 4) { /* accumulators 4..7 from the partner lane (sub = 1) */
+		float b[4];
 #pragma unroll
-	for (int c = 0; c < 4; c++)
-		b[c] = __shfl_xor(acc[c], 1, WAVE);
-	if (hf == 0 && t < T && j < NE) {
-		const float d = ((acc[0] + b[0]) + (acc[2] + b[2])) + ((acc[1] + b[1]) + (acc[3] + b[3]));
-		logits[(size_t)t * NE + j] = (bias ? bias[j] : 0.0f) + d;
+		for (int c = 0; c < 4; c++)
+			b[c] = __shfl_xor(acc[c % CH], 1, WAVE);
+		d = ((acc[0] + b[0]) + (acc[2 % CH] + b[2])) + ((acc[1 % CH] + b[1]) + (acc[3 % CH] + b[3]));
+	} else { /* lane l holds a_l: (a_l + a_l+4), then pairs, then the two halves */
+		float v = acc[0];
+		v = v + __shfl_xor(v, 4, 8);
+		v = v + __shfl_xor(v, 2, 8);
+		d = v + __shfl_xor(v, 1, 8);
 	}
+	if (sub == 0 && t < T && j < NE)
+		logits[(size_t)t * NE + j] = (bias ? bias[j] : 0.0f) + d;
 }
 
 /* ------------------------------------------------------------------ */
 /* softmax + top-k, one wave per token (wave_softmax_topk)             */
 /* ------------------------------------------------------------------ */
 
+/* rows [r0, r1) of x (E floats each) rounded to f16 into xh, NT threads */
+template <int NT>
+__device__ static inline void rows_to_f16(const float *x, _Float16 *xh, int r0, int r1, int E)
+{
+	const size_t n4 = (size_t)(r1 - r0) * E / 4, o4 = (size_t)r0 * E / 4;
+	for (size_t i = threadIdx.x; i < n4; i += NT) {
+		const float4 v = ((const float4 *)x)[o4 + i];
+		typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+		half4_t h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+		((half4_t *)xh)[o4 + i] = h;
+	}
+}
+
 __global__ __launch_bounds__(64) void k_softmax_topk(const float *__restrict__ logits,
 						     float *__restrict__ probs,
 						     u32 *__restrict__ ids,
 						     float *__restrict__ wout,
-						     int NE, int K, int renorm)
+						     int NE, int K, int renorm,
+						     const float *__restrict__ x,
+						     _Float16 *__restrict__ xh, int E)
 {
+	if (xh)
+		rows_to_f16<64>(x, xh, blockIdx.x, blockIdx.x + 1, E);
 	__shared__ float sp[MOE_MAX_NE];
 	__shared__ u32 sid[MOE_MAX_TOPK];
 	__shared__ float sw[MOE_MAX_TOPK];
@@ -177,8 +221,12 @@ __global__ __launch_bounds__(256) void k_softmax_topk64(const float *__restrict_
 							float *__restrict__ probs,
 							u32 *__restrict__ ids,
 							float *__restrict__ wout, int T, int NE,
-							int K, int renorm)
+							int K, int renorm,
+							const float *__restrict__ x,
+							_Float16 *__restrict__ xh, int E)
 {
+	if (xh)
+		rows_to_f16<256>(x, xh, blockIdx.x * 4, min(blockIdx.x * 4 + 4, T), E);
 	__shared__ uint64_t s_tab[32];
 	__shared__ __attribute__((aligned(16))) uint64_t s_key[4][WAVE];
 	__shared__ u32 s_id[4][MOE_MAX_TOPK];
@@ -425,36 +473,39 @@ extern "C" int moe_kchunks(size_t K)
 }
 
 extern "C" int moe_launch_router(const float *x, const float *wr, const float *bias,
-				 float *logits, int T, int E, int NE, void *xh, void *stream)
+				 float *logits, int T, int E, int NE, void *stream)
 {
 	if (T < 1 || NE < 1 || E % RT_KC || (size_t)NE * E * 4 > 0xffffffffull ||
 	    (size_t)T * E * 4 > 0xffffffffull)
 		return (int)hipErrorInvalidValue;
-	/* 32 experts per tile; 8 (and 4 tokens per wave) for small expert counts */
-	if (NE <= 8) {
-		typedef rt_geo<8> RG;
-		dim3 grid((T + RG::TT - 1) / RG::TT, (NE + 7) / 8);
-		hipLaunchKernelGGL(k_router<8>, grid, dim3(256), 0,
-				   (hipStream_t)stream, x, wr, bias, logits, T, E, NE, (_Float16 *)xh);
+	/* 4 chains a lane, tiles of 32 experts x 4 tokens, while they fill the
+	 * CUs; else a chain a lane, tiles of 8 experts x 1 token */
+	const int wide = ((T + 3) / 4) * ((NE + 31) / 32);
+	if (NE > 8 && wide >= 192) {
+		dim3 grid((T + 3) / 4, (NE + 31) / 32);
+		hipLaunchKernelGGL((k_router<32, 4, 4>), grid, dim3(256), 0, (hipStream_t)stream, x,
+				   wr, bias, logits, T, E, NE);
 	} else {
-		typedef rt_geo<32> RG;
-		dim3 grid((T + RG::TT - 1) / RG::TT, (NE + 31) / 32);
-		hipLaunchKernelGGL(k_router<32>, grid, dim3(256), 0,
-				   (hipStream_t)stream, x, wr, bias, logits, T, E, NE, (_Float16 *)xh);
+		dim3 grid(T, (NE + 7) / 8);
+		hipLaunchKernelGGL((k_router<8, 1, 1>), grid, dim3(64), 0, (hipStream_t)stream, x,
+				   wr, bias, logits, T, E, NE);
 	}
 	return (int)hipGetLastError();
 }
 
 extern "C" int moe_launch_softmax_topk(const float *logits, float *probs, uint32_t *ids,
 				       float *w, int T, int NE, int K, int renorm,
-				       void *stream)
+				       const float *x, void *xh, int E, void *stream)
 {
+	if (xh && E % 4)
+		return (int)hipErrorInvalidValue;
 	if (NE <= WAVE)
 		hipLaunchKernelGGL(k_softmax_topk64, dim3((T + 3) / 4), dim3(256), 0,
-				   (hipStream_t)stream, logits, probs, ids, w, T, NE, K, renorm);
+				   (hipStream_t)stream, logits, probs, ids, w, T, NE, K, renorm, x,
+				   (_Float16 *)xh, E);
 	else
 		hipLaunchKernelGGL(k_softmax_topk, dim3(T), dim3(64), 0, (hipStream_t)stream,
-				   logits, probs, ids, w, NE, K, renorm);
+				   logits, probs, ids, w, NE, K, renorm, x, (_Float16 *)xh, E);
 	return (int)hipGetLastError();
 }
 
