@@ -264,11 +264,14 @@ template <int ODD> struct bsrc<2, ODD> { /* Q4_0 */
 /* ---------------------------------------------------------------------- */
 
 /*
- * One workgroup of 8 waves per CU computes a 64-row m-tile against 512
- * weight rows (2 groups of 32 rows per wave) over the whole K.  Each K-step
- * (PF_KB = 64: two GGML blocks per row) goes through an LDS ring of NSTAGE
+ * A workgroup of 8 waves computes a 64-row m-tile against 512 weight rows
+ * (2 groups of 32 rows per wave) over the whole K: one per CU with a deep
+ * ring (weight streaming, mostly padding rows), or two per CU with a
+ * 2-stage ring, so that one dequantizes while the other's MFMAs run (full
+ * tiles).  Each K-step
+ * (PF_KB = 64: two GGML blocks per row) goes through an LDS ring of NS
  * stages filled by LDS-DMA loads (global_load_lds: no registers, so
- * NSTAGE - 1 stages stay in flight):
+ * NS - 1 stages stay in flight):
  *   B part: the raw blocks of the 512 rows, [row][16-byte chunks];
  *   A part: 64 rows x 64 f16 activations, 16-byte chunk c of row r at slot
  *           8r + (c ^ (r & 7)) (conflict-free MFMA operand reads).
@@ -294,7 +297,6 @@ template <int WT> struct pf_geo {
 	static constexpr int BSZ = PF_BROWS * RBL;       /* B bytes per stage */
 	static constexpr int ASZ = PF_MT * PF_KB * 2;    /* A bytes per stage */
 	static constexpr int SSZ = BSZ + ASZ;
-	static constexpr int NSTAGE = WT == 1 ? 3 : 4;
 	static constexpr int LOADS = JB + 1;             /* loads per wave per stage */
 };
 
@@ -419,7 +421,7 @@ __device__ static inline void pf_stage_mfma_panel(const uint8_t *sb, const _Floa
  * (weights) and s * 128 (A) to the bases.  PANEL: the stage holds two down
  * panels (brow[0] = the lane's even row) instead of [row][chunk] rows.
  */
-template <int WT, int PANEL>
+template <int WT, int PANEL, int NS>
 __device__ static inline void pf_kloop(uint8_t *lds, const uint8_t *wbase, size_t wstep,
 				       const u32 (&woff)[pf_geo<WT>::JB], const uint8_t *abase,
 				       u32 aoff, const int (&brow)[2], int nsteps,
@@ -429,7 +431,7 @@ __device__ static inline void pf_kloop(uint8_t *lds, const uint8_t *wbase, size_
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 	const u32 l0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
 	auto issue = [&](int s) {
-		const u32 st = l0 + (u32)((s % GG::NSTAGE) * GG::SSZ);
+		const u32 st = l0 + (u32)((s % NS) * GG::SSZ);
 		const uint8_t *wb = wbase + (size_t)s * wstep;
 #pragma unroll
 		for (int j = 0; j < GG::JB; j++)
@@ -439,18 +441,18 @@ __device__ static inline void pf_kloop(uint8_t *lds, const uint8_t *wbase, size_
 		dma_dwordx4(abase + (size_t)s * 128, aoff, st + GG::BSZ + (u32)(wave * 1024));
 	};
 #pragma unroll
-	for (int s = 0; s < GG::NSTAGE - 1; s++)
+	for (int s = 0; s < NS - 1; s++)
 		if (s < nsteps)
 			issue(s);
 	for (int s = 0; s < nsteps; s++) {
-		if (s + GG::NSTAGE - 2 < nsteps)
-			wait_vm<(GG::NSTAGE - 2) * GG::LOADS>();
+		if (s + NS - 2 < nsteps)
+			wait_vm<(NS - 2) * GG::LOADS>();
 		else
 			wait_vm<0>();
 		__syncthreads(); /* stage s landed for every wave; stage s-1 is free */
-		if (s + GG::NSTAGE - 1 < nsteps)
-			issue(s + GG::NSTAGE - 1);
-		const uint8_t *sb = lds + (s % GG::NSTAGE) * GG::SSZ;
+		if (s + NS - 1 < nsteps)
+			issue(s + NS - 1);
+		const uint8_t *sb = lds + (s % NS) * GG::SSZ;
 		if (PANEL)
 			pf_stage_mfma_panel<WT>(sb, (const _Float16 *)(sb + GG::BSZ), brow[0], acc,
 						lane);
@@ -481,14 +483,14 @@ template <int WT> struct pf_lanes {
 	}
 };
 
-template <int WT>
+template <int WT, int NS>
 __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_gateup(
 	const _Float16 *__restrict__ xh, const uint8_t *__restrict__ gate, size_t up_off,
 	size_t gu_stride, const int *__restrict__ rows, const int *__restrict__ tile_e, int K,
 	int E, int EI, _Float16 *__restrict__ h)
 {
 	typedef pf_geo<WT> GG;
-	__shared__ __attribute__((aligned(16))) uint8_t lds[GG::NSTAGE * GG::SSZ];
+	__shared__ __attribute__((aligned(16))) uint8_t lds[NS * GG::SSZ];
 	const int tile = blockIdx.y;
 	const int e = tile_e[tile];
 	if (e < 0)
@@ -520,7 +522,7 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_gateup(
 #pragma unroll
 			for (int j = 0; j < 16; j++)
 				acc[mb][g][j] = 0.0f;
-	pf_kloop<WT, 0>(lds, gate, GG::RBS, woff, (const uint8_t *)xh, aoff, brow, E / PF_KB, acc);
+	pf_kloop<WT, 0, NS>(lds, gate, GG::RBS, woff, (const uint8_t *)xh, aoff, brow, E / PF_KB, acc);
 
 	const int col = n0 + wave * 32 + (lane & 31), hh = lane >> 5;
 #pragma unroll
@@ -533,14 +535,14 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_gateup(
 		}
 }
 
-template <int WT>
+template <int WT, int NS>
 __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down(
 	const _Float16 *__restrict__ h, const uint8_t *__restrict__ down, size_t dn_stride,
 	const int *__restrict__ rows, const int *__restrict__ tile_e, int E, int EI,
 	float *__restrict__ ypart)
 {
 	typedef pf_geo<WT> GG;
-	__shared__ __attribute__((aligned(16))) uint8_t lds[GG::NSTAGE * GG::SSZ];
+	__shared__ __attribute__((aligned(16))) uint8_t lds[NS * GG::SSZ];
 	__shared__ int srow[PF_MT];
 	const int tile = blockIdx.y;
 	const int e = tile_e[tile];
@@ -579,7 +581,7 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down(
 #pragma unroll
 			for (int j = 0; j < 16; j++)
 				acc[mb][g][j] = 0.0f;
-	pf_kloop<WT, 1>(lds, down + (size_t)s0 * 2 * PANEL, 2 * PANEL, woff,
+	pf_kloop<WT, 1, NS>(lds, down + (size_t)s0 * 2 * PANEL, 2 * PANEL, woff,
 			(const uint8_t *)(h + (size_t)s0 * PF_KB), aoff, brow, s1 - s0,
 			acc); /* syncs srow */
 
@@ -662,16 +664,24 @@ extern "C" int moe_launch_prefill(int wtype, const void *xh_, const uint8_t *gat
 		S = 1;
 	*split = S;
 	const dim3 ggu(EI / (PF_BROWS / 2), Tmax), gdn(nx, Tmax, S);
-	if (wtype == 1) {
-		hipLaunchKernelGGL(k_pf_gateup<1>, ggu, dim3(PF_WAVES * WAVE), 0, s, xh, gate, up_off,
-				   gu_stride, rows, tile_e, K, E, EI, hh);
-		hipLaunchKernelGGL(k_pf_down<1>, gdn, dim3(PF_WAVES * WAVE), 0, s, hh, down, dn_stride,
-				   rows, tile_e, E, EI, ypart);
-	} else {
-		hipLaunchKernelGGL(k_pf_gateup<2>, ggu, dim3(PF_WAVES * WAVE), 0, s, xh, gate, up_off,
-				   gu_stride, rows, tile_e, K, E, EI, hh);
-		hipLaunchKernelGGL(k_pf_down<2>, gdn, dim3(PF_WAVES * WAVE), 0, s, hh, down, dn_stride,
-				   rows, tile_e, E, EI, ypart);
+	const dim3 blk(PF_WAVES * WAVE);
+	if (wtype == 1) { /* 3 stages (144 KB): one workgroup per CU */
+		hipLaunchKernelGGL((k_pf_gateup<1, 3>), ggu, blk, 0, s, xh, gate, up_off, gu_stride,
+				   rows, tile_e, K, E, EI, hh);
+		hipLaunchKernelGGL((k_pf_down<1, 3>), gdn, blk, 0, s, hh, down, dn_stride, rows,
+				   tile_e, E, EI, ypart);
+	} else if (P >= 32 * Tmax) {
+		/* tiles at least half full on average: two 2-stage workgroups per
+		 * CU, one dequantizing while the other runs its MFMAs */
+		hipLaunchKernelGGL((k_pf_gateup<2, 2>), ggu, blk, 0, s, xh, gate, up_off, gu_stride,
+				   rows, tile_e, K, E, EI, hh);
+		hipLaunchKernelGGL((k_pf_down<2, 2>), gdn, blk, 0, s, hh, down, dn_stride, rows,
+				   tile_e, E, EI, ypart);
+	} else { /* mostly padding rows: weight streaming, deeper ring */
+		hipLaunchKernelGGL((k_pf_gateup<2, 4>), ggu, blk, 0, s, xh, gate, up_off, gu_stride,
+				   rows, tile_e, K, E, EI, hh);
+		hipLaunchKernelGGL((k_pf_down<2, 4>), gdn, blk, 0, s, hh, down, dn_stride, rows,
+				   tile_e, E, EI, ypart);
 	}
 	return (int)hipGetLastError();
 }
