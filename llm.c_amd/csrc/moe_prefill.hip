@@ -80,16 +80,21 @@ __global__ __launch_bounds__(SORT_THREADS) void k_moe_sort(const u32 *__restrict
 		fill[i] = 0;
 	}
 	__syncthreads();
-	/* counts: 16 ids per thread and round, loaded together */
+	/* counts: 16 ids per thread and round, loaded together; the first
+	 * round's ids stay in registers for the placement below */
+	u32 v0[16];
 	for (int p0 = 16 * tid; p0 < P; p0 += 16 * SORT_THREADS) {
 		u32 v[16];
 #pragma unroll
 		for (int k = 0; k < 16; k++)
 			v[k] = p0 + k < P ? ids[p0 + k] : 0xffffffffu;
 #pragma unroll
-		for (int k = 0; k < 16; k++)
+		for (int k = 0; k < 16; k++) {
+			if (p0 == 16 * tid)
+				v0[k] = v[k];
 			if (v[k] < (u32)NE) /* always, for ids from the top-k kernel */
 				atomicAdd(&cnt[v[k]], 1);
+		}
 	}
 	__syncthreads();
 	if (tid < WAVE) { /* exclusive scan of tiles per expert, 4 experts per lane */
@@ -150,7 +155,7 @@ __global__ __launch_bounds__(SORT_THREADS) void k_moe_sort(const u32 *__restrict
 		u32 v[16];
 #pragma unroll
 		for (int k = 0; k < 16; k++)
-			v[k] = p0 + k < P ? ids[p0 + k] : 0xffffffffu;
+			v[k] = p0 == 16 * tid ? v0[k] : p0 + k < P ? ids[p0 + k] : 0xffffffffu;
 #pragma unroll
 		for (int k = 0; k < 16; k++)
 			if (v[k] < (u32)NE)
