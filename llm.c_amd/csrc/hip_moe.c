@@ -313,7 +313,7 @@ static int ensure_scratch(hip_moe_layer *L, size_t T)
 		size_t rows = (size_t)moe_prefill_max_tiles(P, L->NE) * moe_prefill_tile_rows();
 		HIPCHK(hipMalloc((void **)&L->d_rows, rows * sizeof(int)), "hipMalloc(rows)");
 		HIPCHK(hipMalloc((void **)&L->d_tile_e,
-				 (size_t)moe_prefill_max_tiles(P, L->NE) * sizeof(int)),
+				 ((size_t)moe_prefill_max_tiles(P, L->NE) + 1) * sizeof(int)),
 		       "hipMalloc(tiles)");
 		HIPCHK(hipMalloc(&L->d_h16, rows * L->EI * 2), "hipMalloc(h16)");
 		HIPCHK(hipMalloc(&L->d_xh, T * L->E * 2), "hipMalloc(xh)");

@@ -61,8 +61,8 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
  * may differ between calls, but the results do not: every output row of
  * the GEMMs depends only on its own activation row (the row's MFMA sums do
  * not involve the other rows of its tile).  rows[] gets Tmax*PF_MT entries
- * and tile_e[] Tmax entries (-1 past the last tile), all rewritten on every
- * call.
+ * and tile_e[] Tmax + 1 entries (-1 past the last tile, then the number of
+ * tiles in use), all rewritten on every call.
  */
 #define SORT_MAX_TILES 8704 /* Tmax for T*K up to 2^19 pairs and NE <= 256 */
 
@@ -126,6 +126,8 @@ __global__ __launch_bounds__(SORT_THREADS) void k_moe_sort(const u32 *__restrict
 	}
 	__syncthreads();
 	const int ntiles = toff[NE];
+	if (tid == 0)
+		tile_e[Tmax] = ntiles;
 	/* tile table: the expert of each tile (largest e with toff[e] <= tile) */
 	for (int tl = tid; tl < Tmax; tl += SORT_THREADS) {
 		int ex = -1;
@@ -466,6 +468,32 @@ __device__ static inline void pf_kloop(uint8_t *lds, const uint8_t *wbase, size_
 	}
 }
 
+/*
+ * Work order of a GEMM grid (nb column blocks fastest, then tiles): the
+ * workgroups are dealt round-robin over the 8 XCDs, so workgroup class
+ * id % 8 shares one L2; each class takes a contiguous run of the
+ * nb * ntiles items in use, so an expert's m-tiles run side by side on one
+ * L2 and read its weights once from HBM.  Returns false for a workgroup
+ * without an item.
+ */
+__device__ static inline bool pf_item(int ntiles, int &tile, int &nb)
+{
+	const int NB = (int)gridDim.x, G = NB * (int)gridDim.y;
+	const int id = (int)blockIdx.x + NB * (int)blockIdx.y, U = NB * ntiles;
+	int L = id;
+	if (G % 8 == 0) {
+		const int share = (U + 7) / 8;
+		if (id / 8 >= share)
+			return false;
+		L = (id % 8) * share + id / 8;
+	}
+	if (L >= U)
+		return false;
+	tile = L / NB;
+	nb = L % NB;
+	return true;
+}
+
 /* this lane's part of the loads: weight row and chunk of load j (flat
  * chunk f of the stage's [PF_BROWS][NCH] block) and the A chunk (slot ->
  * row, chunk) */
@@ -496,12 +524,12 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_gateup(
 {
 	typedef pf_geo<WT> GG;
 	__shared__ __attribute__((aligned(16))) uint8_t lds[NS * GG::SSZ];
-	const int tile = blockIdx.y;
-	const int e = tile_e[tile];
-	if (e < 0)
+	int tile, nb;
+	if (!pf_item(tile_e[gridDim.y], tile, nb))
 		return;
+	const int e = tile_e[tile];
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-	const int n0 = blockIdx.x * (PF_BROWS / 2);
+	const int n0 = nb * (PF_BROWS / 2);
 	const size_t rb = (size_t)(E / MOE_QK) * GG::BB;
 	pf_lanes<WT> L;
 	/* weight rows 0..255: gate rows n0.., 256..511: up rows n0.. (offsets
@@ -549,16 +577,16 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down(
 	typedef pf_geo<WT> GG;
 	__shared__ __attribute__((aligned(16))) uint8_t lds[NS * GG::SSZ];
 	__shared__ int srow[PF_MT];
-	const int tile = blockIdx.y;
-	const int e = tile_e[tile];
-	if (e < 0)
+	int tile, nb;
+	if (!pf_item(tile_e[gridDim.y], tile, nb))
 		return;
+	const int e = tile_e[tile];
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 	const int S = gridDim.z, nst = EI / PF_KB;
 	const int s0 = blockIdx.z * nst / S, s1 = (blockIdx.z + 1) * nst / S;
 	if (threadIdx.x < PF_MT)
 		srow[threadIdx.x] = rows[tile * PF_MT + threadIdx.x];
-	const int n0 = blockIdx.x * PF_BROWS;
+	const int n0 = nb * PF_BROWS;
 	/* stage s = rows n0 .. n0+511 of panels 2s and 2s+1: two contiguous runs
 	 * of RUN bytes, loaded as 16-byte chunks; chunks past them (the last
 	 * wave's spare lanes) reload chunk 0 into unused LDS */
