@@ -460,11 +460,13 @@ __device__ static inline void pf_kloop(uint8_t *lds, const uint8_t *wbase, size_
 		if (s + NS - 1 < nsteps)
 			issue(s + NS - 1);
 		const uint8_t *sb = lds + (s % NS) * GG::SSZ;
+		__builtin_amdgcn_s_setprio(1);
 		if (PANEL)
 			pf_stage_mfma_panel<WT>(sb, (const _Float16 *)(sb + GG::BSZ), brow[0], acc,
 						lane);
 		else
 			pf_stage_mfma<WT>(sb, (const _Float16 *)(sb + GG::BSZ), brow, acc, lane);
+		__builtin_amdgcn_s_setprio(0);
 	}
 }
 
