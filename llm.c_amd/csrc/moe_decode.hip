@@ -27,11 +27,14 @@
  *     and runs softmax + top-k (+ renorm) itself (nn.c:221-308,
  *     llama.c:422-427).  The tokens its items need are staged into LDS
  *     meanwhile.
- *  2. items item_lo(b) <= q < item_lo(b+1): a balanced contiguous range of
- *     the T*K*(EI/32) items in (token, slot, chunk) order, so one workgroup's
- *     items belong to at most DEC_TOKS tokens.  Thread i accumulates outputs
- *     i, i + NT, ... of a token over its items in registers and publishes
- *     them once per token as epoch-tagged partials.
+ *  2. items: a balanced contiguous range of the T*K*(EI/32) items in
+ *     (token, slot, chunk) order, dealt in half items (16 rows of d_ff) so
+ *     that shares stay equal when the items do not divide evenly over the
+ *     workgroups; a half streams its 16 gate/up rows and the whole down
+ *     panel.  One workgroup's items belong to at most DEC_TOKS tokens.
+ *     Thread i accumulates outputs i, i + NT, ... of a token over its items
+ *     in registers and publishes them once per token as epoch-tagged
+ *     partials.
  *  3. combine.  The T*E outputs form slices of PSLICE; for each of its slices
  *     a workgroup polls the partials of every workgroup holding items of the
  *     slice's token (one hop: the loads that see the epoch deliver the
@@ -638,8 +641,10 @@ template <int WT, int CG, int NT, int RPT> struct item_regs {
 
 template <int WT, int CG, int NT, int RPT>
 __device__ static inline void load_gateup(const DecodeArgs &a, int q, const u32 *s_ids,
-					  item_regs<WT, CG, NT, RPT> &r)
+					  item_regs<WT, CG, NT, RPT> &r, bool active)
 {
+	if (!active)
+		return;
 	typedef segq<WT> S;
 	typedef gu_geo<WT, CG, NT> GG;
 	const int NC = a.EI / DEC_CHUNK, p = q / NC, c = q % NC;
@@ -695,8 +700,12 @@ void k_moe_decode(DecodeArgs a)
 	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
 	const int G = (int)gridDim.x, b = (int)blockIdx.x;
 	const int NC = a.EI / DEC_CHUNK, IPT = a.K * NC, N = a.n_items;
-	const int q0 = item_lo(b, N, G), q1 = item_lo(b + 1, N, G);
-	const int t0 = q0 / IPT;
+	/* work is dealt in half items (16 rows of d_ff), so that every
+	 * workgroup gets the same share when the items do not divide evenly
+	 * (Mixtral: 3.5 items each); x0 .. x1 are this workgroup's halves */
+	const int N2 = 2 * N;
+	const int x0 = item_lo(b, N2, G), x1 = item_lo(b + 1, N2, G);
+	const int t0 = x0 / 2 / IPT;
 	const int XS = (a.E / MOE_QK) * DBLK;           /* dwords of one staged token */
 	u32 *sx = (u32 *)lds;                           /* [DEC_TOKS][XS] token digits */
 	float *rl = lds + DEC_TOKS * XS;                /* routing scratch */
@@ -712,8 +721,8 @@ void k_moe_decode(DecodeArgs a)
 	}
 	/* the tokens of this workgroup's items (they do not depend on routing;
 	 * router workgroups stage them after their router row) */
-	if (q0 < q1)
-		for (int t = t0; t <= (q1 - 1) / IPT; t++)
+	if (x0 < x1)
+		for (int t = t0; t <= (x1 - 1) / 2 / IPT; t++)
 			stage_digits<NT>(sx + (t - t0) * XS, a.x + (size_t)t * a.E, a.E);
 	if (threadIdx.x == 0)
 		s_epoch = prev_epoch + 1;
@@ -739,8 +748,16 @@ void k_moe_decode(DecodeArgs a)
 		acc[r2] = 0.0f;
 	item_regs<WT, CG, NT, RPT> R;
 
-	/* h rows of this wave: silu(gate . x) * (up . x) */
-	auto gateup = [&](int q) {
+	/* h rows of this wave: silu(gate . x) * (up . x), or zeros when the
+	 * unit is the other half of the item */
+	auto gateup = [&](int q, bool active) {
+		if (!active) {
+			if (seg == 0)
+#pragma unroll
+				for (int s2 = 0; s2 < GG::NS; s2++)
+					s_h[wave * GG::HR + s2 * GG::RPS + sub] = 0.0f;
+			return;
+		}
 		const int t = q / NC / a.K;
 		typedef idig<WT> I;
 		u32 xd[I::NB * DBLK]; /* this lane's segment: NB staged blocks */
@@ -792,7 +809,7 @@ void k_moe_decode(DecodeArgs a)
 	};
 	/* publish token t's accumulated outputs */
 	auto flush = [&](int t) {
-		const int con = b - item_owner(t * IPT, N, G);
+		const int con = b - item_owner(2 * t * IPT, N2, G);
 		uint64_t *pt = a.part + (size_t)t * a.E * a.ncon;
 #pragma unroll
 		for (int r2 = 0; r2 < RPT; r2++) {
@@ -803,29 +820,50 @@ void k_moe_decode(DecodeArgs a)
 		}
 	};
 
-	if (q0 < q1) {
-		load_gateup<WT, CG, NT, RPT>(a, q0, s_ids, R);
-		load_down<WT, CG, NT, RPT>(a, q0, s_ids, R);
-		/* items before the last: the next item's loads go into R right
+	/* the units of [x0, x1): the second half of item x0 / 2 when x0 is odd,
+	 * whole items, the first half of item x1 / 2 when x1 is odd.  A half
+	 * streams its 16 gate/up rows (the other waves' h rows are zero) and
+	 * the whole down panel. */
+	const int head = x0 & 1, full0 = (x0 + 1) / 2, nfull = x1 / 2 - full0;
+	const int nu = x0 < x1 ? head + nfull + (x1 & 1) : 0;
+	auto unit = [&](int u, int &m) -> int { /* item; m: bit h = rows 16h .. 16h+15 */
+		if (head && u == 0) {
+			m = 2;
+			return x0 / 2;
+		}
+		const int k = u - head;
+		m = k < nfull ? 3 : 1;
+		return k < nfull ? full0 + k : x1 / 2;
+	};
+	const int hw = wave / (NT / WAVE / 2); /* the half of the item's rows this wave holds */
+	if (nu > 0) {
+		int m, mn;
+		int q = unit(0, m);
+		load_gateup<WT, CG, NT, RPT>(a, q, s_ids, R, (m >> hw) & 1);
+		load_down<WT, CG, NT, RPT>(a, q, s_ids, R);
+		/* units before the last: the next unit's loads go into R right
 		 * after the last reads of each part of it (the scheduling barriers
 		 * keep them there, so R needs no copies and no waits at the loop's
 		 * end) */
-		for (int q = q0; q + 1 < q1; q++) {
-			gateup(q);
+		for (int u = 0; u + 1 < nu; u++) {
+			const int qn = unit(u + 1, mn);
+			gateup(q, (m >> hw) & 1);
 			__builtin_amdgcn_sched_barrier(0);
-			load_gateup<WT, CG, NT, RPT>(a, q + 1, s_ids, R);
+			load_gateup<WT, CG, NT, RPT>(a, qn, s_ids, R, (mn >> hw) & 1);
 			__syncthreads(); /* s_h complete */
 			down(q);
 			__builtin_amdgcn_sched_barrier(0);
-			load_down<WT, CG, NT, RPT>(a, q + 1, s_ids, R);
-			if ((q + 1) / IPT != q / IPT)
+			load_down<WT, CG, NT, RPT>(a, qn, s_ids, R);
+			if (qn / IPT != q / IPT)
 				flush(q / IPT);
 			__syncthreads(); /* s_h is rewritten next */
+			q = qn;
+			m = mn;
 		}
-		gateup(q1 - 1);
+		gateup(q, (m >> hw) & 1);
 		__syncthreads();
-		down(q1 - 1);
-		flush((q1 - 1) / IPT);
+		down(q);
+		flush(q / IPT);
 	}
 
 	/* ---- combine: slices b, b + G, ... of the T*E outputs ----
@@ -836,7 +874,8 @@ void k_moe_decode(DecodeArgs a)
 	const int NSL = a.E / PSLICE;
 	for (int sl = b; sl < a.T * NSL; sl += G) {
 		const int t = sl / NSL, j = sl % NSL;
-		const int bf = item_owner(t * IPT, N, G), bl = item_owner((t + 1) * IPT - 1, N, G);
+		const int bf = item_owner(2 * t * IPT, N2, G),
+			  bl = item_owner(2 * (t + 1) * IPT - 1, N2, G);
 		const int n = (bl - bf + 1) * PSLICE;
 		const uint64_t *src = a.part + (size_t)sl * a.ncon * PSLICE;
 		/* this thread's entries (at most CMB_MAX), skipping workgroups
@@ -846,7 +885,7 @@ void k_moe_decode(DecodeArgs a)
 #pragma unroll
 		for (int k = 0; k < CMB_MAX; k++) {
 			const int e = threadIdx.x + NT * k, wb = bf + e / PSLICE;
-			if (e < n && item_lo(wb, N, G) != item_lo(wb + 1, N, G))
+			if (e < n && item_lo(wb, N2, G) != item_lo(wb + 1, N2, G))
 				pending |= 1u << k;
 		}
 		const unsigned live = pending;
@@ -943,10 +982,10 @@ static size_t decode_lds_bytes(const Geo &g, size_t E)
 /* the largest number of workgroups holding items of one token */
 static int decode_ncon(size_t T, size_t K, size_t EI, int grid)
 {
-	const int IPT = (int)(K * (EI / DEC_CHUNK)), N = (int)T * IPT;
+	const int IPT = (int)(K * (EI / DEC_CHUNK)), N2 = 2 * (int)T * IPT; /* half items */
 	int m = 1;
 	for (int t = 0; t < (int)T; t++) {
-		int c = item_owner((t + 1) * IPT - 1, N, grid) - item_owner(t * IPT, N, grid) + 1;
+		int c = item_owner(2 * (t + 1) * IPT - 1, N2, grid) - item_owner(2 * t * IPT, N2, grid) + 1;
 		if (c > m)
 			m = c;
 	}
