@@ -86,8 +86,17 @@ int hip_moe_ffn(hip_moe_layer *L, const float *x, float *out, size_t T,
 
 /*
  * Same as hip_moe_ffn with every pointer in device memory, enqueued on
- * `stream` (a hipStream_t; NULL = the layer's own stream) without waiting.
- * This is the form a device-resident forward pass (and a HIP graph) uses.
+ * `stream` (a hipStream_t) without waiting.  NULL = the library's stream for
+ * the current device, shared by every layer, so calls without a stream run
+ * in call order.  This is the form a device-resident forward pass (and a
+ * HIP graph) uses.
+ *
+ * The decode path (T*topk <= 64) is one persistent launch that keeps a
+ * workgroup on every CU, and its workgroups wait on one another: do not
+ * let two such calls run at once on different streams (order them by
+ * stream or event).  Overlapping ones can each hold CUs the other needs;
+ * they end on bounded waits, and the next hip_moe_ffn on the layer reports
+ * the error.
  */
 int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
                     const float *d_router_bias, uint32_t *d_ids_out,

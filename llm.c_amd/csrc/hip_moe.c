@@ -13,6 +13,7 @@
 #include "moe_internal.h"
 
 #include <hip/hip_runtime_api.h>
+#include <pthread.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -96,6 +97,39 @@ const char *hip_moe_last_error(void)
 		}                                                                 \
 	} while (0)
 
+/*
+ * One library stream per device, shared by every layer: calls that pass no
+ * stream run in call order, as the reference's layers do.  A decode launch
+ * keeps one workgroup on every CU and its workgroups wait on one another, so
+ * two decode launches in flight at once (two streams) can each hold CUs the
+ * other needs; they then end on their bounded waits with an error instead of
+ * finishing.  One stream rules that out for the default.
+ */
+#define MOE_MAX_DEVICES 64
+static hipStream_t g_dev_stream[MOE_MAX_DEVICES];
+static pthread_mutex_t g_dev_stream_mu = PTHREAD_MUTEX_INITIALIZER;
+
+static hipStream_t device_stream(int dev)
+{
+	hipStream_t s = NULL;
+	if (dev < 0 || dev >= MOE_MAX_DEVICES) {
+		set_err("device %d: beyond the %d devices this library serves", dev,
+			MOE_MAX_DEVICES);
+		return NULL;
+	}
+	pthread_mutex_lock(&g_dev_stream_mu);
+	if (!g_dev_stream[dev]) {
+		hipError_t e = hipStreamCreateWithFlags(&g_dev_stream[dev], hipStreamNonBlocking);
+		if (e != hipSuccess) {
+			g_dev_stream[dev] = NULL;
+			set_err("hipStreamCreate: %s", hipGetErrorString(e));
+		}
+	}
+	s = g_dev_stream[dev];
+	pthread_mutex_unlock(&g_dev_stream_mu);
+	return s;
+}
+
 static size_t row_bytes(int wtype, size_t n)
 {
 	return (n / MOE_QK) * (wtype == HIP_MOE_Q8_0 ? 34 : 18);
@@ -150,9 +184,7 @@ void hip_moe_free(hip_moe_layer *L)
 	hipFree(L->d_bias);
 	hipFree(L->d_ids_io);
 	hipFree(L->d_w_io);
-	if (L->stream)
-		hipStreamDestroy(L->stream);
-	free(L);
+	free(L); /* L->stream is the device's shared stream: it stays */
 }
 
 hip_moe_layer *hip_moe_upload(const float *gate_inp, const void *const *gate_e,
@@ -210,7 +242,9 @@ hip_moe_layer *hip_moe_upload(const float *gate_inp, const void *const *gate_e,
 	L->fused_grid = moe_fused_grid(wtype, E, EI, NE);
 
 	HIPCHK(hipGetDevice(&L->device), "hipGetDevice");
-	HIPCHK(hipStreamCreateWithFlags(&L->stream, hipStreamNonBlocking), "hipStreamCreate");
+	L->stream = device_stream(L->device);
+	if (!L->stream)
+		goto fail;
 	HIPCHK(hipMalloc((void **)&L->d_router, NE * E * sizeof(float)), "hipMalloc(router)");
 	/* + slack: the grouped GEMMs load 16-byte chunks that may run up to 12
 	 * bytes past the last row */
@@ -259,6 +293,8 @@ static int ensure_scratch(hip_moe_layer *L, size_t T)
 	if (T <= L->cap_T)
 		return 1;
 	size_t P = T * L->topk;
+	/* calls enqueued earlier may still use the buffers freed here */
+	HIPCHK(hipDeviceSynchronize(), "synchronize before growing scratch");
 	hipFree(L->d_logits);
 	hipFree(L->d_ids);
 	hipFree(L->d_w);
@@ -309,6 +345,9 @@ static int ensure_scratch(hip_moe_layer *L, size_t T)
 	 * earlier layer */
 	HIPCHK(hipMemset(L->d_sync, 0, L->sync_words * sizeof(uint32_t)), "hipMemset(sync)");
 	HIPCHK(hipMemset(L->d_part, 0, L->part_words * sizeof(uint64_t)), "hipMemset(part)");
+	/* the clears run on the null stream, which the layer's non-blocking
+	 * stream does not wait for */
+	HIPCHK(hipDeviceSynchronize(), "synchronize after clearing scratch");
 	if (moe_prefill_supported(L->wtype, L->E, L->EI, L->NE)) {
 		size_t rows = (size_t)moe_prefill_max_tiles(P, L->NE) * moe_prefill_tile_rows();
 		HIPCHK(hipMalloc((void **)&L->d_rows, rows * sizeof(int)), "hipMalloc(rows)");
@@ -544,6 +583,7 @@ int hip_moe_ffn(hip_moe_layer *L, const float *x, float *out, size_t T,
 		if (err) { /* flags may be left mid-flight: restart the epoch at zero */
 			hipMemset(L->d_sync, 0, L->sync_words * sizeof(uint32_t));
 			hipMemset(L->d_part, 0, L->part_words * sizeof(uint64_t));
+			hipDeviceSynchronize(); /* before the next launch on L->stream */
 			static const char *what[] = {"", "router logits", "partial sums",
 						     "start flags"};
 			set_err("persistent kernel: a dependency wait timed out (%s)",

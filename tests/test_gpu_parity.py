@@ -419,6 +419,39 @@ def test_gpu_fresh_layer_after_freed_layer():
         lay.free()
 
 
+def test_gpu_default_stream_orders_layers():
+    """Calls without a stream on different layers share one stream per
+    device: decode launches of several layers, enqueued back to back without
+    waiting, must not overlap (a persistent grid needs every CU) and must
+    each give the eager result."""
+    say("4 layers x 6 rounds of T=1 decode calls on the default stream")
+    H = hipmoe.hip()
+    cfg = "olmoe_q8"
+    wt, E, EI, NE, K, renorm, bias_std = CONFIGS[cfg]
+    lw = layer(cfg)
+    lays = [gpu_layer(cfg)] + [hipmoe.MoeLayer.from_synth(lw, K, False) for _ in range(3)]
+    xs = hipmoe.synth_input(SEED, 612, 6, E)
+    eager = [lays[0].ffn(xs[r:r + 1])[0][0] for r in range(6)]
+    d_x = H.upload(xs)
+    d_o = H.malloc(6 * 4 * E * 4)
+    try:
+        for r in range(6):
+            for i, lay in enumerate(lays):
+                lay.ffn_dev(d_x + r * E * 4, d_o + (r * 4 + i) * E * 4, 1)
+        H.sync()
+        got = H.download(d_o, (6, 4, E), np.float32)
+        for r in range(6):
+            for i in range(4):
+                assert np.array_equal(bits(got[r, i]), bits(eager[r])), (r, i)
+        for lay in lays:  # a synchronous call reports any expired wait
+            lay.ffn(xs[:1])
+    finally:
+        H.free(d_x)
+        H.free(d_o)
+        for lay in lays[1:]:
+            lay.free()
+
+
 def test_gpu_graph_replays_match_eager():
     say("HIP graph of 4 decode calls, replayed 5 times")
     H = hipmoe.hip()
