@@ -294,6 +294,19 @@ __device__ static inline void stage_digits(u32 *dst, const float *src, int n)
 		stage_digits4(dst + (i / 8) * DBLK, s4[i], i & 7);
 }
 
+/* the same from a token held transposed in LDS: element k at
+ * src[(k % 8) * RS + k / 8] */
+template <int NT>
+__device__ static inline void stage_digits_lds(u32 *dst, const float *src, int n, int RS)
+{
+	for (int i = threadIdx.x; i < n / 4; i += NT) {
+		const int r = (4 * i) & 7, c = (4 * i) >> 3;
+		const float4 v = {src[r * RS + c], src[(r + 1) * RS + c], src[(r + 2) * RS + c],
+				  src[(r + 3) * RS + c]};
+		stage_digits4(dst + (i / 8) * DBLK, v, i & 7);
+	}
+}
+
 /* sum_k q_k v_k of one block: q as 8 dwords of signed bytes (Q8_0) */
 __device__ static inline float idot_q8(const u32 (&q)[8], const u32 *x)
 {
@@ -715,13 +728,19 @@ void k_moe_decode(DecodeArgs a)
 	u32 prev_epoch = 0;
 	if (threadIdx.x == 0)
 		prev_epoch = ld_dev_u32(a.sync); /* consumed late: the load overlaps routing */
+	/* one token: a router workgroup stages it from its router row's LDS
+	 * copy (no second round trip) */
+	const bool st0 = b < a.NE && x0 < x1 && a.T == 1;
 	if (b < a.NE) {
 		router_row<NT, CG * S::COLS>(a, b, prev_epoch, rl);
 		__syncthreads();
+		if (st0) {
+			constexpr int RS = CG * S::COLS / 8 + 4;
+			stage_digits_lds<NT>(sx, rl + 8 * RS, a.E, RS);
+		}
 	}
-	/* the tokens of this workgroup's items (they do not depend on routing;
-	 * router workgroups stage them after their router row) */
-	if (x0 < x1)
+	/* the tokens of this workgroup's items (they do not depend on routing) */
+	if (x0 < x1 && !st0)
 		for (int t = t0; t <= (x1 - 1) / 2 / IPT; t++)
 			stage_digits<NT>(sx + (t - t0) * XS, a.x + (size_t)t * a.E, a.E);
 	if (threadIdx.x == 0)
