@@ -910,12 +910,17 @@ void k_moe_decode(DecodeArgs a)
 		const unsigned live = pending;
 		float vals[CMB_MAX];
 		for (int round = 0; pending; round++) {
+			/* every pending load is issued before any is checked: one
+			 * round trip per round, not one per entry */
+			uint64_t v[CMB_MAX];
+#pragma unroll
+			for (int k = 0; k < CMB_MAX; k++)
+				v[k] = (pending >> k) & 1u ? ld_dev_u64(&src[threadIdx.x + NT * k]) : 0;
 #pragma unroll
 			for (int k = 0; k < CMB_MAX; k++)
 				if ((pending >> k) & 1u) {
-					const uint64_t v = ld_dev_u64(&src[threadIdx.x + NT * k]);
-					vals[k] = __builtin_bit_cast(float, (u32)v);
-					if ((u32)(v >> 32) == epoch)
+					vals[k] = __builtin_bit_cast(float, (u32)v[k]);
+					if ((u32)(v[k] >> 32) == epoch)
 						pending &= ~(1u << k);
 				}
 			if (!pending)
