@@ -156,9 +156,17 @@ __global__ __launch_bounds__(NW * WAVE) void k_router(const float *__restrict__ 
 				acc[3 % CH] = __builtin_fmaf(xv.w, wv.w, acc[3 % CH]);
 			}
 		} else {
-#pragma unroll 8
+			/* one wave: all 64 operand reads of the stage go out before
+			 * the chain, one LDS latency per stage */
+			float xs[RT_KC / 8], ws[RT_KC / 8];
+#pragma unroll
+			for (int i = 0; i < RT_KC / 8; i++) {
+				xs[i] = xrow[8 * i];
+				ws[i] = wrow[8 * i];
+			}
+#pragma unroll
 			for (int i = 0; i < RT_KC / 8; i++)
-				acc[0] = __builtin_fmaf(xrow[8 * i], wrow[8 * i], acc[0]);
+				acc[0] = __builtin_fmaf(xs[i], ws[i], acc[0]);
 		}
 	}
 	float d;
@@ -225,8 +233,13 @@ __global__ __launch_bounds__(256) void k_softmax_topk64(const float *__restrict_
 							const float *__restrict__ x,
 							_Float16 *__restrict__ xh, int E)
 {
-	if (xh)
-		rows_to_f16<256>(x, xh, blockIdx.x * 4, min(blockIdx.x * 4 + 4, T), E);
+	if (xh) { /* the f16 tokens, split over the whole grid */
+		const int rows = (T + (int)gridDim.x - 1) / (int)gridDim.x;
+		const int r0 = min((int)blockIdx.x * rows, T), r1 = min(r0 + rows, T);
+		rows_to_f16<256>(x, xh, r0, r1, E);
+	}
+	if ((int)blockIdx.x * 4 >= T)
+		return;
 	__shared__ uint64_t s_tab[32];
 	__shared__ __attribute__((aligned(16))) uint64_t s_key[4][WAVE];
 	__shared__ u32 s_id[4][MOE_MAX_TOPK];
@@ -499,8 +512,11 @@ extern "C" int moe_launch_softmax_topk(const float *logits, float *probs, uint32
 {
 	if (xh && E % 4)
 		return (int)hipErrorInvalidValue;
+	/* with f16 tokens: at least one workgroup per token (up to 256), so the
+	 * copy is not held to the few CUs the routing needs */
+	const int g64 = xh ? max((T + 3) / 4, min(T, 256)) : (T + 3) / 4;
 	if (NE <= WAVE)
-		hipLaunchKernelGGL(k_softmax_topk64, dim3((T + 3) / 4), dim3(256), 0,
+		hipLaunchKernelGGL(k_softmax_topk64, dim3(g64), dim3(256), 0,
 				   (hipStream_t)stream, logits, probs, ids, w, T, NE, K, renorm, x,
 				   (_Float16 *)xh, E);
 	else
