@@ -272,10 +272,9 @@ template <int ODD> struct bsrc<2, ODD> { /* Q4_0 */
 
 /*
  * A workgroup of 8 waves computes a 64-row m-tile against 512 weight rows
- * (2 groups of 32 rows per wave) over the whole K: one per CU with a deep
- * ring (weight streaming, mostly padding rows), or two per CU with a
- * 2-stage ring, so that one dequantizes while the other's MFMAs run (full
- * tiles).  Each K-step
+ * (2 groups of 32 rows per wave) over the whole K: Q8_0 one per CU with a
+ * 3-stage ring, Q4_0 two per CU with a 2-stage ring, so that one
+ * dequantizes while the other's MFMAs run.  Each K-step
  * (PF_KB = 64: two GGML blocks per row) goes through an LDS ring of NS
  * stages filled by LDS-DMA loads (global_load_lds: no registers, so
  * NS - 1 stages stay in flight):
@@ -705,17 +704,15 @@ extern "C" int moe_launch_prefill(int wtype, const void *xh_, const uint8_t *gat
 				   rows, tile_e, K, E, EI, hh);
 		hipLaunchKernelGGL((k_pf_down<1, 3>), gdn, blk, 0, s, hh, down, dn_stride, rows,
 				   tile_e, E, EI, ypart);
-	} else if (P >= 32 * Tmax) {
-		/* tiles at least half full on average: two 2-stage workgroups per
-		 * CU, one dequantizing while the other runs its MFMAs */
+	} else {
+		/* two 2-stage workgroups per CU, one dequantizing while the other
+		 * runs its MFMAs; it also fits grids of 1.5-2 workgroups per CU
+		 * (Mixtral T=16/64) in one round.  Measured against one 4-stage
+		 * workgroup per CU for tiles of mostly padding rows: Mixtral T=64
+		 * 342.4 -> 337.4 us, T=16 330.3 -> 326.8 us. */
 		hipLaunchKernelGGL((k_pf_gateup<2, 2>), ggu, blk, 0, s, xh, gate, up_off, gu_stride,
 				   rows, tile_e, K, E, EI, hh);
 		hipLaunchKernelGGL((k_pf_down<2, 2>), gdn, blk, 0, s, hh, down, dn_stride, rows,
-				   tile_e, E, EI, ypart);
-	} else { /* mostly padding rows: weight streaming, deeper ring */
-		hipLaunchKernelGGL((k_pf_gateup<2, 4>), ggu, blk, 0, s, xh, gate, up_off, gu_stride,
-				   rows, tile_e, K, E, EI, hh);
-		hipLaunchKernelGGL((k_pf_down<2, 4>), gdn, blk, 0, s, hh, down, dn_stride, rows,
 				   tile_e, E, EI, ypart);
 	}
 	return (int)hipGetLastError();
