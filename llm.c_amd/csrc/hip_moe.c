@@ -349,7 +349,7 @@ static int ensure_scratch(hip_moe_layer *L, size_t T)
 	 * stream does not wait for */
 	HIPCHK(hipDeviceSynchronize(), "synchronize after clearing scratch");
 	if (moe_prefill_supported(L->wtype, L->E, L->EI, L->NE)) {
-		size_t rows = (size_t)moe_prefill_max_tiles(P, L->NE) * moe_prefill_tile_rows();
+		size_t rows = moe_prefill_max_rows(P, L->NE);
 		HIPCHK(hipMalloc((void **)&L->d_rows, rows * sizeof(int)), "hipMalloc(rows)");
 		HIPCHK(hipMalloc((void **)&L->d_tile_e,
 				 ((size_t)moe_prefill_max_tiles(P, L->NE) + 1) * sizeof(int)),

@@ -3,9 +3,11 @@
  * on the f16 matrix cores.
  *
  *   k_moe_sort     stable counting sort of the T*K (token, slot) pairs by
- *                  expert into m-tiles of PF_MT rows (the tail of each
+ *                  expert into m-tiles of MT rows (the tail of each
  *                  expert's last tile is padding, row id -1), and the tile
- *                  table tile -> expert.
+ *                  table tile -> expert.  MT = 64, or 32 when the experts
+ *                  average fewer than 32 pairs (the MFMAs of a tile's
+ *                  second 32 rows would be padding).
  *   k_pf_gateup    per (m-tile, 256 h columns): G = X Wg^T and U = X Wu^T
  *                  over d_model, h = silu(G) * U  (nn.c:460-478), stored f16
  *                  in sorted row order.  X is the f16 copy of the tokens the
@@ -46,7 +48,7 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-#define PF_MT 64            /* rows (pairs) per m-tile */
+#define PF_MT_MAX 64        /* rows (pairs) per m-tile: 32 or 64 */
 #define PF_KB 64            /* k per pipeline step: two blocks */
 #define SORT_THREADS 1024
 
@@ -56,16 +58,17 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 /*
  * One workgroup.  Counts per expert, tiles per expert (exclusive scan), the
- * tile table, padding rows (-1), then every pair's row: toff[e] * PF_MT + a
+ * tile table, padding rows (-1), then every pair's row: toff[e] * MT + a
  * slot taken with an LDS atomic.  The order of the pairs inside an expert
  * may differ between calls, but the results do not: every output row of
  * the GEMMs depends only on its own activation row (the row's MFMA sums do
- * not involve the other rows of its tile).  rows[] gets Tmax*PF_MT entries
+ * not involve the other rows of its tile).  rows[] gets Tmax*MT entries
  * and tile_e[] Tmax + 1 entries (-1 past the last tile, then the number of
  * tiles in use), all rewritten on every call.
  */
 #define SORT_MAX_TILES 8704 /* Tmax for T*K up to 2^19 pairs and NE <= 256 */
 
+template <int MT>
 __global__ __launch_bounds__(SORT_THREADS) void k_moe_sort(const u32 *__restrict__ ids, int P,
 							   int NE, int Tmax,
 							   int *__restrict__ rows,
@@ -103,7 +106,7 @@ __global__ __launch_bounds__(SORT_THREADS) void k_moe_sort(const u32 *__restrict
 #pragma unroll
 		for (int i = 0; i < 4; i++) {
 			const int ex = 4 * lane + i;
-			t4[i] = ex < NE ? (cnt[ex] + PF_MT - 1) / PF_MT : 0;
+			t4[i] = ex < NE ? (cnt[ex] + MT - 1) / MT : 0;
 			s += t4[i];
 		}
 		int incl = s;
@@ -147,9 +150,9 @@ __global__ __launch_bounds__(SORT_THREADS) void k_moe_sort(const u32 *__restrict
 	}
 	__syncthreads();
 	/* padding rows */
-	for (int i = tid; i < Tmax * PF_MT; i += SORT_THREADS) {
-		const int ex = stile[i / PF_MT];
-		if (ex < 0 || i - toff[ex] * PF_MT >= cnt[ex])
+	for (int i = tid; i < Tmax * MT; i += SORT_THREADS) {
+		const int ex = stile[i / MT];
+		if (ex < 0 || i - toff[ex] * MT >= cnt[ex])
 			rows[i] = -1;
 	}
 	/* every pair's row */
@@ -161,7 +164,7 @@ __global__ __launch_bounds__(SORT_THREADS) void k_moe_sort(const u32 *__restrict
 #pragma unroll
 		for (int k = 0; k < 16; k++)
 			if (v[k] < (u32)NE)
-				rows[toff[v[k]] * PF_MT + atomicAdd(&fill[v[k]], 1)] = p0 + k;
+				rows[toff[v[k]] * MT + atomicAdd(&fill[v[k]], 1)] = p0 + k;
 	}
 }
 
@@ -301,7 +304,7 @@ template <int WT> struct pf_geo {
 	static constexpr int RBL = CH * NCH;             /* LDS bytes per row */
 	static constexpr int JB = PF_BROWS * NCH / (PF_WAVES * WAVE); /* B loads per wave */
 	static constexpr int BSZ = PF_BROWS * RBL;       /* B bytes per stage */
-	static constexpr int ASZ = PF_MT * PF_KB * 2;    /* A bytes per stage */
+	static constexpr int ASZ = PF_MT_MAX * PF_KB * 2; /* A bytes per stage */
 	static constexpr int SSZ = BSZ + ASZ;
 	static constexpr int LOADS = JB + 1;             /* loads per wave per stage */
 };
@@ -329,10 +332,10 @@ __device__ static inline u32 lds_addr(const void *p)
 	return (u32)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
 }
 
-/* acc[mb][g] += A[mb-th 32 rows] . B_g over one stage.  Every LDS read of
- * the stage is issued first, so the stage waits for LDS once, not once per
- * operand. */
-template <int WT>
+/* acc[mb][g] += A[mb-th 32 rows] . B_g over one stage, mb < MB.  Every LDS
+ * read of the stage is issued first, so the stage waits for LDS once, not
+ * once per operand. */
+template <int WT, int MB>
 __device__ static inline void pf_stage_mfma(const uint8_t *sb, const _Float16 *sa,
 					    const int (&brow)[2], floatx16 (&acc)[2][2], int lane)
 {
@@ -352,7 +355,7 @@ __device__ static inline void pf_stage_mfma(const uint8_t *sb, const _Float16 *s
 #pragma unroll
 		for (int kh = 0; kh < 2; kh++)
 #pragma unroll
-			for (int mb = 0; mb < 2; mb++) {
+			for (int mb = 0; mb < MB; mb++) {
 				const int ar = mb * 32 + r, c = bb * 4 + kh * 2 + h;
 				a[bb][kh][mb] = *(const half8_t *)(sa + 8 * (ar * 8 + (c ^ (ar & 7))));
 			}
@@ -369,7 +372,7 @@ __device__ static inline void pf_stage_mfma(const uint8_t *sb, const _Float16 *s
 #pragma unroll
 		for (int kh = 0; kh < 2; kh++)
 #pragma unroll
-			for (int mb = 0; mb < 2; mb++)
+			for (int mb = 0; mb < MB; mb++)
 #pragma unroll
 				for (int g = 0; g < 2; g++)
 					acc[mb][g] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
@@ -381,7 +384,7 @@ __device__ static inline void pf_stage_mfma(const uint8_t *sb, const _Float16 *s
  * panel 2s, then of panel 2s+1 (PF_BROWS blocks each, unpadded).  The lane's
  * column pair is rows n (even: 4-byte aligned blocks) and n+1 (odd: 2 bytes
  * off), so each group reads blocks of one alignment. */
-template <int WT>
+template <int WT, int MB>
 __device__ static inline void pf_stage_mfma_panel(const uint8_t *sb, const _Float16 *sa, int n,
 						  floatx16 (&acc)[2][2], int lane)
 {
@@ -401,7 +404,7 @@ __device__ static inline void pf_stage_mfma_panel(const uint8_t *sb, const _Floa
 #pragma unroll
 		for (int kh = 0; kh < 2; kh++)
 #pragma unroll
-			for (int mb = 0; mb < 2; mb++) {
+			for (int mb = 0; mb < MB; mb++) {
 				const int ar = mb * 32 + r, c = bb * 4 + kh * 2 + h;
 				a[bb][kh][mb] = *(const half8_t *)(sa + 8 * (ar * 8 + (c ^ (ar & 7))));
 			}
@@ -413,7 +416,7 @@ __device__ static inline void pf_stage_mfma_panel(const uint8_t *sb, const _Floa
 #pragma unroll
 		for (int kh = 0; kh < 2; kh++)
 #pragma unroll
-			for (int mb = 0; mb < 2; mb++)
+			for (int mb = 0; mb < MB; mb++)
 #pragma unroll
 				for (int g = 0; g < 2; g++)
 					acc[mb][g] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
@@ -427,7 +430,7 @@ __device__ static inline void pf_stage_mfma_panel(const uint8_t *sb, const _Floa
  * (weights) and s * 128 (A) to the bases.  PANEL: the stage holds two down
  * panels (brow[0] = the lane's even row) instead of [row][chunk] rows.
  */
-template <int WT, int PANEL, int NS>
+template <int WT, int PANEL, int NS, int MB>
 __device__ static inline void pf_kloop(uint8_t *lds, const uint8_t *wbase, size_t wstep,
 				       const u32 (&woff)[pf_geo<WT>::JB], const uint8_t *abase,
 				       u32 aoff, const int (&brow)[2], int nsteps,
@@ -461,10 +464,10 @@ __device__ static inline void pf_kloop(uint8_t *lds, const uint8_t *wbase, size_
 		const uint8_t *sb = lds + (s % NS) * GG::SSZ;
 		__builtin_amdgcn_s_setprio(1);
 		if (PANEL)
-			pf_stage_mfma_panel<WT>(sb, (const _Float16 *)(sb + GG::BSZ), brow[0], acc,
-						lane);
+			pf_stage_mfma_panel<WT, MB>(sb, (const _Float16 *)(sb + GG::BSZ), brow[0],
+						    acc, lane);
 		else
-			pf_stage_mfma<WT>(sb, (const _Float16 *)(sb + GG::BSZ), brow, acc, lane);
+			pf_stage_mfma<WT, MB>(sb, (const _Float16 *)(sb + GG::BSZ), brow, acc, lane);
 		__builtin_amdgcn_s_setprio(0);
 	}
 }
@@ -517,7 +520,7 @@ template <int WT> struct pf_lanes {
 	}
 };
 
-template <int WT, int NS>
+template <int WT, int NS, int MB>
 __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_gateup(
 	const _Float16 *__restrict__ xh, const uint8_t *__restrict__ gate, size_t up_off,
 	size_t gu_stride, const int *__restrict__ rows, const int *__restrict__ tile_e, int K,
@@ -543,8 +546,10 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_gateup(
 				 (size_t)(n0 + (r & 255)) * rb + GG::CH * L.wch[j];
 		woff[j] = (u32)o;
 	}
-	const int p = rows[tile * PF_MT + L.arow];
-	/* padding rows: one shared 16-byte chunk instead of a row each */
+	constexpr int MT = 32 * MB;
+	const int p = L.arow < MT ? rows[tile * MT + L.arow] : -1;
+	/* padding rows (and the stage's rows past MT): one shared 16-byte chunk
+	 * instead of a row each */
 	const u32 aoff = p >= 0 ? (u32)((size_t)(p / K) * E * 2 + 16 * L.achunk) : 0u;
 	const int brow[2] = {wave * 32 + (lane & 31), 256 + wave * 32 + (lane & 31)};
 
@@ -556,20 +561,21 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_gateup(
 #pragma unroll
 			for (int j = 0; j < 16; j++)
 				acc[mb][g][j] = 0.0f;
-	pf_kloop<WT, 0, NS>(lds, gate, GG::RBS, woff, (const uint8_t *)xh, aoff, brow, E / PF_KB, acc);
+	pf_kloop<WT, 0, NS, MB>(lds, gate, GG::RBS, woff, (const uint8_t *)xh, aoff, brow, E / PF_KB,
+				acc);
 
 	const int col = n0 + wave * 32 + (lane & 31), hh = lane >> 5;
 #pragma unroll
-	for (int mb = 0; mb < 2; mb++)
+	for (int mb = 0; mb < MB; mb++)
 #pragma unroll
 		for (int j = 0; j < 16; j++) {
-			const int row = tile * PF_MT + mb * 32 + 8 * (j / 4) + 4 * hh + (j % 4);
+			const int row = tile * MT + mb * 32 + 8 * (j / 4) + 4 * hh + (j % 4);
 			const float g = acc[mb][0][j], u = acc[mb][1][j];
 			h[(size_t)row * EI + col] = (_Float16)((g / (1.0f + moe_expf(-g))) * u);
 		}
 }
 
-template <int WT, int NS>
+template <int WT, int NS, int MB>
 __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down(
 	const _Float16 *__restrict__ h, const uint8_t *__restrict__ down, size_t dn_stride,
 	const int *__restrict__ rows, const int *__restrict__ tile_e, int E, int EI,
@@ -577,7 +583,8 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down(
 {
 	typedef pf_geo<WT> GG;
 	__shared__ __attribute__((aligned(16))) uint8_t lds[NS * GG::SSZ];
-	__shared__ int srow[PF_MT];
+	constexpr int MT = 32 * MB;
+	__shared__ int srow[MT];
 	int tile, nb;
 	if (!pf_item(tile_e[gridDim.y], tile, nb))
 		return;
@@ -585,8 +592,8 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down(
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 	const int S = gridDim.z, nst = EI / PF_KB;
 	const int s0 = blockIdx.z * nst / S, s1 = (blockIdx.z + 1) * nst / S;
-	if (threadIdx.x < PF_MT)
-		srow[threadIdx.x] = rows[tile * PF_MT + threadIdx.x];
+	if (threadIdx.x < MT)
+		srow[threadIdx.x] = rows[tile * MT + threadIdx.x];
 	const int n0 = nb * PF_BROWS;
 	/* stage s = rows n0 .. n0+511 of panels 2s and 2s+1: two contiguous runs
 	 * of RUN bytes, loaded as 16-byte chunks; chunks past them (the last
@@ -601,8 +608,8 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down(
 				(f < 2 * RUN ? (f / RUN) * PANEL + (size_t)n0 * GG::BB + f % RUN
 					     : (size_t)n0 * GG::BB));
 	}
-	const u32 aoff = rows[tile * PF_MT + L.arow] >= 0
-				 ? (u32)((size_t)(tile * PF_MT + L.arow) * EI * 2 + 16 * L.achunk)
+	const u32 aoff = L.arow < MT && rows[tile * MT + L.arow] >= 0
+				 ? (u32)((size_t)(tile * MT + L.arow) * EI * 2 + 16 * L.achunk)
 				 : 0u;
 	/* MFMA column r of group g = output row wave*64 + 2r + g */
 	const int brow[2] = {wave * 64 + 2 * (lane & 31), wave * 64 + 2 * (lane & 31) + 1};
@@ -615,13 +622,13 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down(
 #pragma unroll
 			for (int j = 0; j < 16; j++)
 				acc[mb][g][j] = 0.0f;
-	pf_kloop<WT, 1, NS>(lds, down + (size_t)s0 * 2 * PANEL, 2 * PANEL, woff,
+	pf_kloop<WT, 1, NS, MB>(lds, down + (size_t)s0 * 2 * PANEL, 2 * PANEL, woff,
 			(const uint8_t *)(h + (size_t)s0 * PF_KB), aoff, brow, s1 - s0,
 			acc); /* syncs srow */
 
 	const int hh = lane >> 5;
 #pragma unroll
-	for (int mb = 0; mb < 2; mb++)
+	for (int mb = 0; mb < MB; mb++)
 #pragma unroll
 		for (int j = 0; j < 16; j++) {
 			const int pr = srow[mb * 32 + 8 * (j / 4) + 4 * hh + (j % 4)];
@@ -646,15 +653,33 @@ extern "C" int moe_prefill_supported(int wtype, size_t E, size_t EI, size_t NE)
 	       EI % (PF_BROWS / 2) == 0 && E % PF_KB == 0 && EI % PF_KB == 0;
 }
 
-extern "C" int moe_prefill_max_tiles(size_t P, size_t NE)
+/* m-tile rows for P pairs over NE experts: 32 while the experts average
+ * fewer than 32 pairs */
+static int pf_mt(size_t P, size_t NE)
 {
-	size_t t = (P + PF_MT - 1) / PF_MT + (NE < P ? NE : P);
-	return (int)t;
+	return P < 32 * NE ? 32 : 64;
 }
 
-extern "C" int moe_prefill_tile_rows(void)
+/* tiles a sort of P pairs into MT-row tiles can use */
+static size_t pf_tiles(size_t P, size_t NE, size_t mt)
 {
-	return PF_MT;
+	return (P + mt - 1) / mt + (NE < P ? NE : P);
+}
+
+/* capacities for every call of at most P pairs (both tile sizes; each term
+ * grows with P, so a smaller call always fits) */
+extern "C" int moe_prefill_max_tiles(size_t P, size_t NE)
+{
+	const size_t p32 = P < 32 * NE ? P : 32 * NE;
+	const size_t a = pf_tiles(P, NE, 64), b = pf_tiles(p32, NE, 32);
+	return (int)(a > b ? a : b);
+}
+
+extern "C" size_t moe_prefill_max_rows(size_t P, size_t NE)
+{
+	const size_t p32 = P < 32 * NE ? P : 32 * NE;
+	const size_t a = pf_tiles(P, NE, 64) * 64, b = pf_tiles(p32, NE, 32) * 32;
+	return a > b ? a : b;
 }
 
 /* the largest tile table the sort kernel handles */
@@ -680,11 +705,16 @@ extern "C" int moe_launch_prefill(int wtype, const void *xh_, const uint8_t *gat
 	hipStream_t s = (hipStream_t)stream;
 	const _Float16 *xh = (const _Float16 *)xh_;
 	const int P = T * K;
-	const int Tmax = moe_prefill_max_tiles((size_t)P, (size_t)NE);
-	if (Tmax > SORT_MAX_TILES || (size_t)Tmax * PF_MT * EI * 2 > 0xffffffffull)
+	const int mt = pf_mt((size_t)P, (size_t)NE);
+	const int Tmax = (int)pf_tiles((size_t)P, (size_t)NE, (size_t)mt);
+	if (Tmax > SORT_MAX_TILES || (size_t)Tmax * mt * EI * 2 > 0xffffffffull)
 		return (int)hipErrorInvalidValue;
-	hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(SORT_THREADS), 0, s, ids, P, NE, Tmax, rows,
-			   tile_e);
+	if (mt == 32)
+		hipLaunchKernelGGL(k_moe_sort<32>, dim3(1), dim3(SORT_THREADS), 0, s, ids, P, NE, Tmax,
+				   rows, tile_e);
+	else
+		hipLaunchKernelGGL(k_moe_sort<64>, dim3(1), dim3(SORT_THREADS), 0, s, ids, P, NE, Tmax,
+				   rows, tile_e);
 	_Float16 *hh = (_Float16 *)h16;
 	/* split the down projection's K when its (m-tile, column block) grid
 	 * would leave most CUs idle (few tokens per expert, large d_ff) */
@@ -699,21 +729,29 @@ extern "C" int moe_launch_prefill(int wtype, const void *xh_, const uint8_t *gat
 	*split = S;
 	const dim3 ggu(EI / (PF_BROWS / 2), Tmax), gdn(nx, Tmax, S);
 	const dim3 blk(PF_WAVES * WAVE);
+#define PF_LAUNCH(W, NS, MB)                                                                 \
+	do {                                                                                 \
+		hipLaunchKernelGGL((k_pf_gateup<W, NS, MB>), ggu, blk, 0, s, xh, gate, up_off,    \
+				   gu_stride, rows, tile_e, K, E, EI, hh);                        \
+		hipLaunchKernelGGL((k_pf_down<W, NS, MB>), gdn, blk, 0, s, hh, down, dn_stride,   \
+				   rows, tile_e, E, EI, ypart);                                   \
+	} while (0)
 	if (wtype == 1) { /* 3 stages (144 KB): one workgroup per CU */
-		hipLaunchKernelGGL((k_pf_gateup<1, 3>), ggu, blk, 0, s, xh, gate, up_off, gu_stride,
-				   rows, tile_e, K, E, EI, hh);
-		hipLaunchKernelGGL((k_pf_down<1, 3>), gdn, blk, 0, s, hh, down, dn_stride, rows,
-				   tile_e, E, EI, ypart);
+		if (mt == 32)
+			PF_LAUNCH(1, 3, 1);
+		else
+			PF_LAUNCH(1, 3, 2);
 	} else {
 		/* two 2-stage workgroups per CU, one dequantizing while the other
 		 * runs its MFMAs; it also fits grids of 1.5-2 workgroups per CU
 		 * (Mixtral T=16/64) in one round.  Measured against one 4-stage
 		 * workgroup per CU for tiles of mostly padding rows: Mixtral T=64
 		 * 342.4 -> 337.4 us, T=16 330.3 -> 326.8 us. */
-		hipLaunchKernelGGL((k_pf_gateup<2, 2>), ggu, blk, 0, s, xh, gate, up_off, gu_stride,
-				   rows, tile_e, K, E, EI, hh);
-		hipLaunchKernelGGL((k_pf_down<2, 2>), gdn, blk, 0, s, hh, down, dn_stride, rows,
-				   tile_e, E, EI, ypart);
+		if (mt == 32)
+			PF_LAUNCH(2, 2, 1);
+		else
+			PF_LAUNCH(2, 2, 2);
 	}
+#undef PF_LAUNCH
 	return (int)hipGetLastError();
 }

@@ -271,8 +271,9 @@ def test_gpu_grouped_q8_prefill_512():
 
 
 def test_gpu_grouped_full_tiles():
-    """Every token picks the same experts, so each expert's row count is an
-    exact multiple of the 64-row tile (no padding rows)."""
+    """Every token picks the same experts, so each expert's row count (128)
+    is an exact multiple of the m-tile (32 rows here: 8 experts of 64
+    average 16 pairs; no padding rows)."""
     say("grouped path, identical tokens: full tiles")
     cfg = "olmoe_q8"
     wt, E, EI, NE, K, renorm, bias_std = CONFIGS[cfg]
