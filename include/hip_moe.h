@@ -19,9 +19,10 @@
  * the fp32 paths (decode, GEMV) and ~5e-4 on the grouped f16-MFMA path taken
  * for many tokens per expert (bound: 1e-3).  See HIP_MOE_PATH_* below.
  *
- * Threading: a layer object owns one HIP stream and device scratch; calls on
- * the same layer object must not overlap (the reference is single-threaded
- * per model too, thread_pool.c:45).
+ * Threading: a layer object owns device scratch; calls on the same layer
+ * object must not overlap (the reference is single-threaded per model too,
+ * thread_pool.c:45).  Calls that pass no stream share one library stream per
+ * device.
  */
 #ifndef HIP_MOE_H
 #define HIP_MOE_H
@@ -42,8 +43,10 @@ extern "C" {
 typedef struct hip_moe_layer hip_moe_layer;
 
 /*
- * Upload one MoE layer's weights to device memory, once, in their native GGUF
- * block layout.  Replaces the residency of
+ * Upload one MoE layer's weights to device memory, once, as GGUF blocks that
+ * keep their bytes (gate/up rows as they are, plus a second gate/up copy in
+ * 32-row groups for the grouped GEMMs; down matrices regrouped into panels
+ * of one block per row).  Replaces the residency of
  *   olmoe_load  (olmoe.c:179-182: ffn_gate_inp + stacked *_exps tensors) and
  *   llama_load  (llama.c:157-166: ffn_gate_inp + per-expert tensors).
  *
@@ -150,7 +153,9 @@ int hip_moe_path_for(const hip_moe_layer *L, size_t T);
 /* Release the device copies and scratch of a layer (NULL is a no-op). */
 void hip_moe_free(hip_moe_layer *L);
 
-/* Device bytes held by the layer's weights (router + experts). */
+/* Device bytes held by the layer's weights (router + experts; where the
+ * grouped path applies, gate/up are held twice: once as GGML rows for the
+ * decode and GEMV kernels, once in the grouped GEMMs' row-group layout). */
 size_t hip_moe_weight_bytes(const hip_moe_layer *L);
 
 /* The last error message of this library ("" if none). */

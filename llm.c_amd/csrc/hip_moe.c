@@ -31,8 +31,9 @@ struct hip_moe_layer {
 	size_t down_stride; /* bytes of one expert's down matrix */
 
 	float *d_router;
-	uint8_t *d_weights; /* [gate NE][up NE][down NE] */
+	uint8_t *d_weights; /* [gate NE][up NE][down NE] ([gate NE][up NE] grouped) */
 	uint8_t *d_gate, *d_up, *d_down;
+	uint8_t *d_gate_g, *d_up_g; /* gate/up in MOE_GU_GROUP-row groups (grouped path) */
 	size_t weight_bytes;
 
 	hipStream_t stream;
@@ -147,6 +148,26 @@ static int is_pow2(size_t v)
  * (32 columns of down for all E rows) then reads one contiguous panel, and
  * the down GEMV and GEMM read E-row runs of blocks.
  */
+/*
+ * One expert's gate or up matrix [EI][E] (GGML rows) into MOE_GU_GROUP-row
+ * groups, piece-major inside a group: piece s (blocks 2s, 2s+1) of row r
+ * goes to (r / G) * G * rb + s * G * pb + (r % G) * pb.  Blocks keep their
+ * bytes; only their order changes.
+ */
+static int upload_gu(hip_moe_layer *L, uint8_t *dst, const uint8_t *src, uint8_t *stage)
+{
+	const size_t G = MOE_GU_GROUP, rb = L->rb_in, pb = 2 * (rb / (L->E / MOE_QK));
+	const size_t np = L->E / (2 * MOE_QK);
+	for (size_t r = 0; r < L->EI; r++)
+		for (size_t s = 0; s < np; s++)
+			memcpy(stage + (r / G) * G * rb + s * G * pb + (r % G) * pb,
+			       src + r * rb + s * pb, pb);
+	HIPCHK(hipMemcpy(dst, stage, L->gu_stride, hipMemcpyHostToDevice), "upload gate/up");
+	return 1;
+fail:
+	return 0;
+}
+
 static int upload_down(hip_moe_layer *L, size_t e, const uint8_t *src, uint8_t *stage)
 {
 	const size_t bb = L->wtype == HIP_MOE_Q8_0 ? 34 : 18, nc = L->EI / MOE_QK;
@@ -238,7 +259,13 @@ hip_moe_layer *hip_moe_upload(const float *gate_inp, const void *const *gate_e,
 	L->rb_mid = row_bytes(wtype, EI);
 	L->gu_stride = EI * L->rb_in;
 	L->down_stride = E * L->rb_mid;
-	L->weight_bytes = NE * E * sizeof(float) + NE * (2 * L->gu_stride + L->down_stride);
+	/* the grouped GEMMs read gate/up from a second copy in MOE_GU_GROUP-row
+	 * groups (a K-step is one contiguous run per group); the decode and GEMV
+	 * kernels read whole rows from the first */
+	const int grouped = moe_prefill_supported(wtype, E, EI, NE);
+	const size_t wbytes = NE * (2 * L->gu_stride + L->down_stride) +
+			      (grouped ? 2 * NE * L->gu_stride : 0);
+	L->weight_bytes = NE * E * sizeof(float) + wbytes;
 	L->fused_grid = moe_fused_grid(wtype, E, EI, NE);
 
 	HIPCHK(hipGetDevice(&L->device), "hipGetDevice");
@@ -246,15 +273,16 @@ hip_moe_layer *hip_moe_upload(const float *gate_inp, const void *const *gate_e,
 	if (!L->stream)
 		goto fail;
 	HIPCHK(hipMalloc((void **)&L->d_router, NE * E * sizeof(float)), "hipMalloc(router)");
-	/* + slack: the grouped GEMMs load 16-byte chunks that may run up to 12
-	 * bytes past the last row */
-	HIPCHK(hipMalloc((void **)&L->d_weights,
-			 NE * (2 * L->gu_stride + L->down_stride) + MOE_WEIGHT_SLACK),
-	       "hipMalloc(experts)");
+	/* + slack: readable bytes past the last weight */
+	HIPCHK(hipMalloc((void **)&L->d_weights, wbytes + MOE_WEIGHT_SLACK), "hipMalloc(experts)");
 	L->d_gate = L->d_weights;
 	L->d_up = L->d_gate + NE * L->gu_stride;
 	L->d_down = L->d_up + NE * L->gu_stride;
-	HIPCHK(hipMemset(L->d_down + NE * L->down_stride, 0, MOE_WEIGHT_SLACK), "clear slack");
+	if (grouped) {
+		L->d_gate_g = L->d_down + NE * L->down_stride;
+		L->d_up_g = L->d_gate_g + NE * L->gu_stride;
+	}
+	HIPCHK(hipMemset(L->d_weights + wbytes, 0, MOE_WEIGHT_SLACK), "clear slack");
 
 	HIPCHK(hipMemcpy(L->d_router, gate_inp, NE * E * sizeof(float), hipMemcpyHostToDevice),
 	       "upload router");
@@ -273,6 +301,10 @@ hip_moe_layer *hip_moe_upload(const float *gate_inp, const void *const *gate_e,
 		HIPCHK(hipMemcpy(L->d_up + e * L->gu_stride, up_e[e], L->gu_stride,
 				 hipMemcpyHostToDevice), "upload up");
 		if (!upload_down(L, e, (const uint8_t *)down_e[e], stage))
+			goto fail;
+		if (grouped &&
+		    (!upload_gu(L, L->d_gate_g + e * L->gu_stride, (const uint8_t *)gate_e[e], stage) ||
+		     !upload_gu(L, L->d_up_g + e * L->gu_stride, (const uint8_t *)up_e[e], stage)))
 			goto fail;
 	}
 	free(stage);
@@ -479,7 +511,7 @@ int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 		return 0;
 	if (path == HIP_MOE_PATH_GROUPED) {
 		int split = 1;
-		LCHK(moe_launch_prefill(L->wtype, L->d_xh, L->d_gate, L->d_up, L->d_down,
+		LCHK(moe_launch_prefill(L->wtype, L->d_xh, L->d_gate_g, L->d_up_g, L->d_down,
 					L->gu_stride, L->down_stride, ids, L->d_rows,
 					L->d_tile_e, L->d_h16, L->d_ypart, (int)T, (int)L->topk,
 					(int)L->E, (int)L->EI, (int)L->NE,

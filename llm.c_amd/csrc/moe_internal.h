@@ -17,6 +17,12 @@ extern "C" {
 #define MOE_QK 32           /* elements per block */
 #define MOE_SEG_COLS 64     /* columns one lane holds: a pair of blocks */
 #define MOE_MAX_NE 256
+/* Gate and up matrices are stored in groups of MOE_GU_GROUP rows; inside a
+ * group, piece-major: for piece s (GGML blocks 2s and 2s+1, 64 columns) the
+ * pieces of the group's rows follow each other.  A decode item (32 rows of
+ * d_ff) is then one contiguous run, and a K-step of the grouped GEMMs reads
+ * one contiguous run per group. */
+#define MOE_GU_GROUP 32
 #define MOE_MAX_TOPK 64
 #define MOE_FUSED_MAX_P 64  /* T*K handled by the persistent decode kernel */
 #define MOE_SYNC_ERR_WORD 256 /* error word in the persistent kernel's counters: */

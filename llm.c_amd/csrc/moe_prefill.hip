@@ -346,7 +346,7 @@ __device__ static inline void pf_stage_mfma(const uint8_t *sb, const _Float16 *s
 	half8_t a[2][2][2]; /* [block][k-half][mb] */
 #pragma unroll
 	for (int g = 0; g < 2; g++) {
-		const uint8_t *row = sb + brow[g] * GG::RBL;
+		const uint8_t *row = sb + brow[g] * GG::RBS;
 		ev[g].load(row, h);
 		od[g].load(row + GG::BB, h);
 	}
@@ -498,22 +498,12 @@ __device__ static inline bool pf_item(int ntiles, int &tile, int &nb)
 	return true;
 }
 
-/* this lane's part of the loads: weight row and chunk of load j (flat
- * chunk f of the stage's [PF_BROWS][NCH] block) and the A chunk (slot ->
- * row, chunk) */
+/* this lane's A chunk of a stage (slot -> row, chunk) */
 template <int WT> struct pf_lanes {
-	int wrow[pf_geo<WT>::JB], wch[pf_geo<WT>::JB];
 	int arow, achunk;
 	__device__ inline pf_lanes()
 	{
-		typedef pf_geo<WT> GG;
 		const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-#pragma unroll
-		for (int j = 0; j < GG::JB; j++) {
-			const int f = (wave * GG::JB + j) * WAVE + lane;
-			wrow[j] = f / GG::NCH;
-			wch[j] = f % GG::NCH;
-		}
 		const int slot = wave * WAVE + lane;
 		arow = slot >> 3;
 		achunk = (slot & 7) ^ (arow & 7);
@@ -537,13 +527,23 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_gateup(
 	const size_t rb = (size_t)(E / MOE_QK) * GG::BB;
 	pf_lanes<WT> L;
 	/* weight rows 0..255: gate rows n0.., 256..511: up rows n0.. (offsets
-	 * from the gate base; up = gate + up_off) */
+	 * from the gate base; up = gate + up_off).  A stage is piece s of every
+	 * row: with the weights in MOE_GU_GROUP-row groups, one contiguous run
+	 * of CPG 16-byte chunks per group (8 gate, then 8 up groups), landing
+	 * as rows of RBS bytes; the spare lanes of the last loads reload the
+	 * first chunk into LDS past the rows. */
+	constexpr int CPG = MOE_GU_GROUP * GG::RBS / GG::CH;
+	static_assert(MOE_GU_GROUP * GG::RBS % GG::CH == 0 && 16 * CPG <= GG::JB * PF_WAVES * WAVE,
+		      "a stage's group runs fit the loads");
 	u32 woff[GG::JB];
 #pragma unroll
 	for (int j = 0; j < GG::JB; j++) {
-		const int r = L.wrow[j];
-		const size_t o = (r < 256 ? 0 : up_off) + (size_t)e * gu_stride +
-				 (size_t)(n0 + (r & 255)) * rb + GG::CH * L.wch[j];
+		const int f = (wave * GG::JB + j) * WAVE + lane, lg = f / CPG; /* its LDS slot */
+		const size_t o = f < 16 * CPG
+					 ? (lg < 8 ? 0 : up_off) + (size_t)e * gu_stride +
+						   (size_t)(n0 + MOE_GU_GROUP * (lg & 7)) * rb +
+						   (size_t)GG::CH * (f % CPG)
+					 : (size_t)e * gu_stride + (size_t)n0 * rb;
 		woff[j] = (u32)o;
 	}
 	constexpr int MT = 32 * MB;
@@ -561,8 +561,8 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_gateup(
 #pragma unroll
 			for (int j = 0; j < 16; j++)
 				acc[mb][g][j] = 0.0f;
-	pf_kloop<WT, 0, NS, MB>(lds, gate, GG::RBS, woff, (const uint8_t *)xh, aoff, brow, E / PF_KB,
-				acc);
+	pf_kloop<WT, 0, NS, MB>(lds, gate, MOE_GU_GROUP * GG::RBS, woff, (const uint8_t *)xh, aoff,
+				brow, E / PF_KB, acc);
 
 	const int col = n0 + wave * 32 + (lane & 31), hh = lane >> 5;
 #pragma unroll
