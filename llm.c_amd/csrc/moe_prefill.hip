@@ -717,9 +717,15 @@ extern "C" int moe_launch_prefill(int wtype, const void *xh_, const uint8_t *gat
 				   rows, tile_e);
 	_Float16 *hh = (_Float16 *)h16;
 	/* split the down projection's K when its (m-tile, column block) grid
-	 * would leave most CUs idle (few tokens per expert, large d_ff) */
+	 * would leave most CUs idle (few tokens per expert, large d_ff), aiming
+	 * at two workgroups per CU.  Tiles counted: with 32-row tiles nearly
+	 * every touched expert has one, so the experts touched (Mixtral T=64:
+	 * 8, where the bound says 12; 207.9 -> 200.6 us); with 64-row tiles
+	 * the bound, since skewed experts add ragged tails (counting fewer
+	 * measured 8% slower at OLMoE T=512). */
 	const int nx = E / PF_BROWS, nst = EI / PF_KB;
-	int S = 512 / (nx * Tmax);
+	const int tiles = mt == 32 ? max((P + mt - 1) / mt, min(NE, P)) : Tmax;
+	int S = 512 / (nx * tiles);
 	if (S > max_split)
 		S = max_split;
 	if (S > nst / 8)
