@@ -265,6 +265,30 @@ def test_gpu_grouped_forced_small_and_ragged(cfg, T):
                            expect_path=hipmoe.PATH_GROUPED)
 
 
+def test_gpu_grouped_tile_size_switch():
+    """The m-tile shrinks from 64 to 32 rows below 32 pairs per expert, and
+    the smaller call then needs more tiles: T=256 (2048 pairs, 64-row tiles)
+    sizes a fresh layer's scratch, then T=255 (2040 pairs, 32-row tiles,
+    up to 64 + 64 = 128 tiles) must fit it."""
+    say("grouped path: T=256 then T=255 on a fresh layer (tile size switch)")
+    cfg = "olmoe_q4_skew"
+    wt, E, EI, NE, K, renorm, bias_std = CONFIGS[cfg]
+    lw = layer(cfg)
+    lay = hipmoe.MoeLayer.from_synth(lw, K, bool(renorm))
+    try:
+        for T, call in ((256, 750), (255, 751)):
+            x = hipmoe.synth_input(SEED, call, T, E)
+            assert lay.path_for(T) == hipmoe.PATH_GROUPED
+            out, ids, w = lay.ffn(x, lw["bias"])
+            oout, oids, ow, _, _ = oracle.moe_ffn(x, lw, K, bool(renorm), lw["bias"])
+            assert np.array_equal(ids, oids) and np.array_equal(bits(w), bits(ow))
+            err = rel_l2(out, oout)
+            say(f"{cfg} T={T}: rel L2 {err:.3e}")
+            assert err <= REL_L2_TOL
+    finally:
+        lay.free()
+
+
 def test_gpu_grouped_q8_prefill_512():
     say("olmoe_q8 prefill T=512 (grouped, Q8_0)")
     _check_layer_vs_oracle("olmoe_q8", 512, 710, expect_path=hipmoe.PATH_GROUPED)
