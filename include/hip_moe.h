@@ -131,9 +131,10 @@ int hip_moe_expert_ffn_dev(hip_moe_layer *L, size_t expert, const float *d_x,
  *   DECODE   one persistent launch (T*k <= 64, NE <= 64), fp32 arithmetic
  *   GEMV     router, top-k, per-pair dequant-GEMV kernels, combine; fp32
  *   GROUPED  router, top-k, sort by expert, f16 MFMA grouped GEMMs, combine
- * AUTO picks DECODE where it applies and the (token, slot) pairs do not
- * outnumber the experts (T*k <= NE: every pair streams its expert once),
- * else GROUPED (each touched expert streamed once), else GEMV.  Routing (ids and
+ * AUTO picks DECODE where it applies and the (token, slot) pairs stay at
+ * 3/4 of the experts (4*T*k <= 3*NE: OLMoE T <= 6, Mixtral T <= 3; every
+ * pair streams its expert once), else GROUPED (each touched expert streamed
+ * once), else GEMV.  Routing (ids and
  * weights) is bit-identical on every path; outputs agree with the reference
  * within 1e-3 relative L2 (fp32 paths: ~1e-6; GROUPED: ~5e-4 from f16
  * operands).

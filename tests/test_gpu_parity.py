@@ -411,7 +411,17 @@ def test_gpu_dev_entry_matches_host_entry():
 
 def test_gpu_fused_boundary_T8():
     say("olmoe_q8 T=8 (T*K = 64, largest persistent launch)")
-    _check_layer_vs_oracle("olmoe_q8", 8, 600)
+    _check_layer_vs_oracle("olmoe_q8", 8, 600, path=hipmoe.PATH_DECODE,
+                           expect_path=hipmoe.PATH_DECODE)
+
+
+def test_gpu_auto_path_boundaries():
+    """AUTO takes the decode launch while 4*T*k <= 3*NE, the grouped path
+    above it."""
+    for cfg, t_dec in (("olmoe_q8", 6), ("mixtral_q4", 3)):
+        lay = gpu_layer(cfg)
+        assert lay.path_for(t_dec) == hipmoe.PATH_DECODE, cfg
+        assert lay.path_for(t_dec + 1) == hipmoe.PATH_GROUPED, cfg
 
 
 def test_gpu_fused_many_calls_reset_counters():
@@ -507,8 +517,9 @@ def test_gpu_graph_replays_match_eager():
 
 
 def test_gpu_mixtral_fused_T2_and_T32():
-    say("mixtral_q4 T=2 and T=4 (persistent path), T=32 forced onto it")
+    say("mixtral_q4 T=2 (persistent path), T=4 and T=32 forced onto it")
     _check_layer_vs_oracle("mixtral_q4", 2, 603, expect_path=hipmoe.PATH_DECODE)
-    _check_layer_vs_oracle("mixtral_q4", 4, 605, expect_path=hipmoe.PATH_DECODE)
+    _check_layer_vs_oracle("mixtral_q4", 4, 605, path=hipmoe.PATH_DECODE,
+                           expect_path=hipmoe.PATH_DECODE)
     _check_layer_vs_oracle("mixtral_q4", 32, 604, path=hipmoe.PATH_DECODE,
                            expect_path=hipmoe.PATH_DECODE)
