@@ -516,6 +516,42 @@ def test_gpu_graph_replays_match_eager():
         H.free(d_o)
 
 
+def test_gpu_graph_replays_grouped():
+    """The grouped path (router, top-k, sort, GEMMs, combine) in a HIP graph:
+    every replay equals the eager call, with eager calls of other sizes on
+    the same scratch between the replays."""
+    say("HIP graph of grouped calls (mixtral_q4 T=64 and T=16), replayed 3 times")
+    H = hipmoe.hip()
+    lay = gpu_layer("mixtral_q4")
+    E = 4096
+    xa = hipmoe.synth_input(SEED, 606, 64, E)
+    xb = hipmoe.synth_input(SEED, 607, 16, E)
+    assert lay.path_for(64) == hipmoe.PATH_GROUPED and lay.path_for(16) == hipmoe.PATH_GROUPED
+    ea, eb = lay.ffn(xa)[0], lay.ffn(xb)[0]
+    s = H.stream()
+    d_a, d_b = H.upload(xa), H.upload(xb)
+    d_oa, d_ob = H.malloc(xa.nbytes), H.malloc(xb.nbytes)
+    try:
+        lay.ffn_dev(d_a, d_oa, 64, None, None, None, s)  # eager warm-up on the stream
+        lay.ffn_dev(d_b, d_ob, 16, None, None, None, s)
+        H.stream_sync(s)
+        H.begin_capture(s)
+        lay.ffn_dev(d_a, d_oa, 64, None, None, None, s)
+        lay.ffn_dev(d_b, d_ob, 16, None, None, None, s)
+        ge = H.end_capture(s)
+        for rep in range(3):
+            H.check(H.h.hipMemsetAsync(d_oa, 0, xa.nbytes, s), "memset")
+            H.check(H.h.hipMemsetAsync(d_ob, 0, xb.nbytes, s), "memset")
+            H.graph_launch(ge, s)
+            H.stream_sync(s)
+            assert np.array_equal(bits(H.download(d_oa, xa.shape, np.float32)), bits(ea)), rep
+            assert np.array_equal(bits(H.download(d_ob, xb.shape, np.float32)), bits(eb)), rep
+            lay.ffn(xb[:9])  # eager grouped work of another size between replays
+    finally:
+        for p in (d_a, d_b, d_oa, d_ob):
+            H.free(p)
+
+
 def test_gpu_mixtral_fused_T2_and_T32():
     say("mixtral_q4 T=2 (persistent path), T=4 and T=32 forced onto it")
     _check_layer_vs_oracle("mixtral_q4", 2, 603, expect_path=hipmoe.PATH_DECODE)
