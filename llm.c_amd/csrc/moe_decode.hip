@@ -67,7 +67,7 @@
 #define PSLICE 8     /* outputs per combine slice */
 #define DEC_TOKS 2   /* tokens one workgroup's item range can span (T <= G) */
 #define DEC_CHUNK 32 /* d_ff rows per item: one down block per row */
-#define CMB_MAX 16   /* combine entries per thread: grid * PSLICE <= CMB_MAX * NT */
+#define CMB_MAX 16   /* combine entries per thread, two slices: grid * PSLICE <= CMB_MAX / 2 * NT */
 
 struct DecodeArgs {
 	const float *x;
@@ -885,70 +885,93 @@ void k_moe_decode(DecodeArgs a)
 		flush(q / IPT);
 	}
 
-	/* ---- combine: slices b, b + G, ... of the T*E outputs ----
+	/* ---- combine: slices b, b + G, ... of the T*E outputs, NP at a time
+	 * (two where a token's E outputs give each workgroup two or more
+	 * slices, E = 4096: polled together; Mixtral T=1 58.1 -> 56.5 us) ----
 	 * thread tid takes the entries e = tid + NT*k of a slice (contributor
 	 * e / PSLICE, output e % PSLICE = tid % PSLICE) and adds them in k order;
 	 * lanes of one output meet in an xor tree, waves in wave order */
-	float *sc = lds; /* [NT / WAVE][PSLICE] */
-	const int NSL = a.E / PSLICE;
-	for (int sl = b; sl < a.T * NSL; sl += G) {
-		const int t = sl / NSL, j = sl % NSL;
-		const int bf = item_owner(2 * t * IPT, N2, G),
-			  bl = item_owner(2 * (t + 1) * IPT - 1, N2, G);
-		const int n = (bl - bf + 1) * PSLICE;
-		const uint64_t *src = a.part + (size_t)sl * a.ncon * PSLICE;
-		/* this thread's entries (at most CMB_MAX), skipping workgroups
-		 * without items; each thread polls its own until their tags show
-		 * the epoch, with no workgroup barrier per poll */
-		unsigned pending = 0;
+	float *sc = lds; /* [NT / WAVE][NP][PSLICE] */
+	const int NSL = a.E / PSLICE, NS_ALL = a.T * NSL;
+	{
+		constexpr int NP = RPT >= 8 ? 2 : 1; /* slices per workgroup and token: RPT / 4 */
+		constexpr int KH = CMB_MAX / NP; /* entries per thread and slice */
+		for (int sl0 = b; sl0 < NS_ALL; sl0 += NP * G) {
+			const uint64_t *src[NP];
+			unsigned pending = 0;
 #pragma unroll
-		for (int k = 0; k < CMB_MAX; k++) {
-			const int e = threadIdx.x + NT * k, wb = bf + e / PSLICE;
-			if (e < n && item_lo(wb, N2, G) != item_lo(wb + 1, N2, G))
-				pending |= 1u << k;
-		}
-		const unsigned live = pending;
-		float vals[CMB_MAX];
-		for (int round = 0; pending; round++) {
-			/* every pending load is issued before any is checked: one
-			 * round trip per round, not one per entry */
-			uint64_t v[CMB_MAX];
+			for (int hs = 0; hs < NP; hs++) {
+				const int sl = sl0 + hs * G;
+				src[hs] = a.part + (size_t)min(sl, NS_ALL - 1) * a.ncon * PSLICE;
+				if (sl >= NS_ALL)
+					continue;
+				const int t = sl / NSL;
+				const int bf = item_owner(2 * t * IPT, N2, G),
+					  bl = item_owner(2 * (t + 1) * IPT - 1, N2, G);
+				const int n = (bl - bf + 1) * PSLICE;
+				/* this thread's entries (at most KH), skipping workgroups
+				 * without items */
 #pragma unroll
-			for (int k = 0; k < CMB_MAX; k++)
-				v[k] = (pending >> k) & 1u ? ld_dev_u64(&src[threadIdx.x + NT * k]) : 0;
-#pragma unroll
-			for (int k = 0; k < CMB_MAX; k++)
-				if ((pending >> k) & 1u) {
-					vals[k] = __builtin_bit_cast(float, (u32)v[k]);
-					if ((u32)(v[k] >> 32) == epoch)
-						pending &= ~(1u << k);
+				for (int k = 0; k < KH; k++) {
+					const int e = threadIdx.x + NT * k, wb = bf + e / PSLICE;
+					if (e < n && item_lo(wb, N2, G) != item_lo(wb + 1, N2, G))
+						pending |= 1u << (hs * KH + k);
 				}
-			if (!pending)
-				break;
-			if (round >= SPIN_LIMIT) {
-				st_dev_u32(a.sync + MOE_SYNC_ERR_WORD, MOE_ERR_COMBINE);
-				break;
 			}
-			__builtin_amdgcn_s_sleep(1);
-		}
-		float sum = 0.0f;
+			/* each thread polls its own entries until their tags show the
+			 * epoch, with no workgroup barrier per poll */
+			const unsigned live = pending;
+			float vals[CMB_MAX];
+			for (int round = 0; pending; round++) {
+				/* every pending load is issued before any is checked: one
+				 * round trip per round, not one per entry */
+				uint64_t v[CMB_MAX];
 #pragma unroll
-		for (int k = 0; k < CMB_MAX; k++)
-			if ((live >> k) & 1u)
-				sum += vals[k];
-		sum += __shfl_xor(sum, 8, WAVE);
-		sum += __shfl_xor(sum, 16, WAVE);
-		sum += __shfl_xor(sum, 32, WAVE);
-		if (lane < PSLICE)
-			sc[wave * PSLICE + lane] = sum;
-		__syncthreads();
-		if (threadIdx.x < PSLICE) {
-			float o = 0.0f;
-			for (int w = 0; w < NT / WAVE; w++)
-				o += sc[w * PSLICE + threadIdx.x];
-			a.out[(size_t)t * a.E + j * PSLICE + threadIdx.x] = o;
+				for (int k = 0; k < CMB_MAX; k++)
+					v[k] = (pending >> k) & 1u
+						       ? ld_dev_u64(&src[k / KH][threadIdx.x + NT * (k % KH)])
+						       : 0;
+#pragma unroll
+				for (int k = 0; k < CMB_MAX; k++)
+					if ((pending >> k) & 1u) {
+						vals[k] = __builtin_bit_cast(float, (u32)v[k]);
+						if ((u32)(v[k] >> 32) == epoch)
+							pending &= ~(1u << k);
+					}
+				if (!pending)
+					break;
+				if (round >= SPIN_LIMIT) {
+					st_dev_u32(a.sync + MOE_SYNC_ERR_WORD, MOE_ERR_COMBINE);
+					break;
+				}
+				__builtin_amdgcn_s_sleep(1);
+			}
+#pragma unroll
+			for (int hs = 0; hs < NP; hs++) {
+				float sum = 0.0f;
+#pragma unroll
+				for (int k = 0; k < KH; k++)
+					if ((live >> (hs * KH + k)) & 1u)
+						sum += vals[hs * KH + k];
+				sum += __shfl_xor(sum, 8, WAVE);
+				sum += __shfl_xor(sum, 16, WAVE);
+				sum += __shfl_xor(sum, 32, WAVE);
+				if (lane < PSLICE)
+					sc[(wave * NP + hs) * PSLICE + lane] = sum;
+			}
+			__syncthreads();
+			if (threadIdx.x < NP * PSLICE) {
+				const int hs = threadIdx.x / PSLICE, sl = sl0 + hs * G;
+				if (sl < NS_ALL) {
+					float o = 0.0f;
+					for (int w = 0; w < NT / WAVE; w++)
+						o += sc[(w * NP + hs) * PSLICE + threadIdx.x % PSLICE];
+					a.out[(size_t)(sl / NSL) * a.E + (sl % NSL) * PSLICE +
+					      threadIdx.x % PSLICE] = o;
+				}
+			}
+			__syncthreads();
 		}
-		__syncthreads();
 	}
 
 	/* workgroup 0 advances the epoch for the next launch once every
@@ -1063,9 +1086,10 @@ extern "C" int moe_fused_grid(int wtype, size_t E, size_t EI, size_t NE)
 		return 0;
 	/* one workgroup per CU; the router rows need one workgroup each, a
 	 * workgroup's items must span at most DEC_TOKS tokens (T <= grid), and
-	 * a combine thread covers at most CMB_MAX entries */
-	return ncu >= (int)NE && ncu >= MOE_FUSED_MAX_P && ncu * PSLICE <= CMB_MAX * g.NT ? ncu
-												: 0;
+	 * a combine thread covers at most CMB_MAX / 2 entries of a slice */
+	return ncu >= (int)NE && ncu >= MOE_FUSED_MAX_P && ncu * PSLICE <= CMB_MAX / 2 * g.NT
+		       ? ncu
+		       : 0;
 }
 
 extern "C" int moe_launch_fused(int wtype, const float *x, const float *router,
