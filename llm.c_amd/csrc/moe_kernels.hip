@@ -491,15 +491,16 @@ extern "C" int moe_launch_router(const float *x, const float *wr, const float *b
 	if (T < 1 || NE < 1 || E % RT_KC || (size_t)NE * E * 4 > 0xffffffffull ||
 	    (size_t)T * E * 4 > 0xffffffffull)
 		return (int)hipErrorInvalidValue;
-	/* 4 chains a lane, tiles of 32 experts x 4 tokens; for few tokens a chain
-	 * a lane, tiles of 8 experts x 1 token (more workgroups, but every
-	 * token's workgroups load the router rows again: 4x the LDS fill).
+	/* 4 chains a lane, tiles of 16 experts x 8 tokens (a 6-stage ring); for
+	 * few tokens a chain a lane, tiles of 8 experts x 1 token (more
+	 * workgroups, but every token's workgroups load the router rows again).
 	 * Routing stage at NE = 64: one-token tiles 7.8 us up to T = 32, 11.5
-	 * at 64, 15.2 at 96, 39.6 at 320; 32x4 tiles ~12.8 us throughout. */
-	const int wide = ((T + 3) / 4) * ((NE + 31) / 32);
+	 * at 64, 15.2 at 96, 39.6 at 320; 16x8 tiles 12.4-13.4 us from T = 128
+	 * to 512 (32x4 tiles with a 4-stage ring: 12.7-13.5). */
+	const int wide = ((T + 7) / 8) * ((NE + 15) / 16);
 	if (NE > 8 && wide >= 36) {
-		dim3 grid((T + 3) / 4, (NE + 31) / 32);
-		hipLaunchKernelGGL((k_router<32, 4, 4>), grid, dim3(256), 0, (hipStream_t)stream, x,
+		dim3 grid((T + 7) / 8, (NE + 15) / 16);
+		hipLaunchKernelGGL((k_router<16, 4, 4>), grid, dim3(256), 0, (hipStream_t)stream, x,
 				   wr, bias, logits, T, E, NE);
 	} else {
 		dim3 grid(T, (NE + 7) / 8);
