@@ -13,6 +13,11 @@ Infinity Cache, so the timed loop rotates over `--layers` copies of the layer
 distinct tokens: consecutive calls touch different memory and the figure is
 an HBM figure.  Calls are replayed from HIP graphs of one call per layer copy.
 
+The `*_lm_head` workloads time the dense quantized product instead
+(hip_moe_qmat_mul_dev: the reference's tensor_mma_transposed_2x2 on a Q8_0 or
+Q4_0 matrix, here the lm_head of each model for one token), rotating over
+`--layers` copies of the matrix in the same way.
+
 Prints one JSON line on stdout (progress goes to stderr).
 """
 import argparse
@@ -28,6 +33,7 @@ sys.path.insert(0, os.path.join(REPO, "llm.c_amd"))
 import hipmoe  # noqa: E402
 
 METRIC = "MoE-layer tokens/s & % of HBM roofline; OLMoE-shaped decode tok/s"
+QMAT_METRIC = "dense quantized product tokens/s & % of HBM roofline"
 HBM_PEAK_GBS = 8000.0
 SEED = 1337
 
@@ -42,6 +48,9 @@ WORKLOADS = {
                            bias_std=None),
     "mixtral_q4_T64": dict(wtype=hipmoe.Q4_0, E=4096, EI=14336, NE=8, K=2, renorm=1, T=64,
                            bias_std=None),
+    # dense quantized products: N rows of K columns, T tokens
+    "olmoe_q8_lm_head": dict(kind="qmat", wtype=hipmoe.Q8_0, N=50304, Kc=2048, T=1),
+    "mixtral_q4_lm_head": dict(kind="qmat", wtype=hipmoe.Q4_0, N=32000, Kc=4096, T=1),
 }
 
 
@@ -93,6 +102,107 @@ def traffic_bytes(kernel, workload):
     return None
 
 
+def bench_qmat(args, w, H):
+    """Dense quantized product: out[T][N] = x[T][K] . W^T per call, W one of
+    `--layers` copies in turn.  Algorithmic bytes per call: the matrix's
+    blocks + x + out."""
+    wt, N, Kc, T = w["wtype"], w["N"], w["Kc"], w["T"]
+    q = hipmoe.synth_quant_matrix(SEED, 0x7700 + wt, 0.02, wt, N, Kc)
+    nl = max(1, args.layers)
+    mats = [hipmoe.QMat(q, wt, N, Kc) for _ in range(nl)]
+    log(f"uploaded {nl} matrix copies ({nl * mats[0].bytes() / 1e9:.2f} GB)")
+    ntok = max(1, args.tokens)
+    xs = [hipmoe.synth_input(SEED, 2000 + i, T, Kc) for i in range(ntok)]
+    d_x = H.upload(np.stack(xs))
+    d_out = H.malloc(T * N * 4)
+    s = H.stream()
+    xbytes = T * Kc * 4
+    bytes_per_call = mats[0].bytes() + xbytes + T * N * 4
+
+    def call(i):
+        mats[i % nl].mul_dev(d_x + (i % ntok) * xbytes, T, d_out, None, 0, s)
+
+    if args.copy_calib_mb > 0:
+        nb = args.copy_calib_mb << 20
+        c_src, c_dst = H.malloc(nb), H.malloc(nb)
+        for _ in range(4):
+            if hipmoe.lib().hip_moe_copy_dev(c_src, c_dst, nb, s) != 1:
+                sys.exit("hip_moe_copy_dev: " + hipmoe.last_error())
+        H.stream_sync(s)
+        H.free(c_src)
+        H.free(c_dst)
+        log(f"copy calibration: 4 x {nb} bytes")
+    for i in range(max(nl, args.warmup)):
+        call(i)
+    H.stream_sync(s)
+    graphs = []
+    if not args.eager:
+        ngraphs = max(1, min(4, ntok // nl)) if ntok >= nl else 1
+        for g in range(ngraphs):
+            H.begin_capture(s)
+            for i in range(nl):
+                call(g * nl + i)
+            graphs.append(H.end_capture(s))
+        for ge in graphs:
+            H.graph_launch(ge, s)
+        H.stream_sync(s)
+        log(f"captured {len(graphs)} graphs of {nl} calls")
+    steps = args.steps
+    e0, e1 = H.event(), H.event()
+    H.sync()
+    H.record(e0, s)
+    if graphs:
+        full, rem = divmod(steps, nl)
+        for r in range(full):
+            H.graph_launch(graphs[r % len(graphs)], s)
+        for i in range(rem):
+            call(i)
+    else:
+        for i in range(steps):
+            call(i)
+    H.record(e1, s)
+    ms = H.elapsed_ms(e0, e1)
+    H.sync()
+    ms_per_step = ms / steps
+    tokens_per_s = steps * T / (ms / 1e3)
+    achieved_gbs = bytes_per_call / (ms_per_step / 1e3) / 1e9
+    log(f"{steps} steps in {ms:.2f} ms: {ms_per_step * 1e3:.2f} us/step, "
+        f"{tokens_per_s:.1f} tokens/s, {achieved_gbs:.1f} GB/s algorithmic")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(REPO, "oracle"))
+        import oracle
+        done, i, t0 = 0, 0, time.perf_counter()
+        while True:
+            oracle.qmat_mul(xs[i % ntok], q, wt, N, Kc)
+            done += T
+            i += 1
+            el = time.perf_counter() - t0
+            if el >= args.cpu_seconds:
+                break
+        cpu = dict(value=done / el, unit="tokens/s", cores=1, kind="port",
+                   sample=f"{done} tokens in {i} calls, {el:.1f} s, 1 thread, "
+                          f"oracle/moe_oracle.c orc_qmat_mul built -O3 -mavx2 -mfma")
+        log(f"cpu baseline: {cpu['value']:.2f} tokens/s")
+    line = {
+        "metric": QMAT_METRIC, "value": round(tokens_per_s, 2), "unit": "tokens/s",
+        "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": args.workload, "rows": N, "cols": Kc, "tokens_per_call": T,
+                   "weights": "Q8_0" if wt == hipmoe.Q8_0 else "Q4_0",
+                   "matrix_copies": nl, "distinct_inputs": ntok, "graphs": bool(graphs),
+                   "algorithmic_bytes_per_call": int(bytes_per_call)},
+        "roofline": {"bound": "hbm", "kernel": "k_qgemv", "achieved": round(achieved_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_bytes("k_qgemv", args.workload)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -119,6 +229,8 @@ def main():
     H = hipmoe.hip()
     if H.device_count() < 1:
         sys.exit("no HIP device")
+    if w.get("kind") == "qmat":
+        return bench_qmat(args, w, H)
     E, T, K = w["E"], w["T"], w["K"]
 
     t0 = time.perf_counter()

@@ -178,6 +178,47 @@ int hip_moe_expf_dev(const float *d_in, float *d_out, size_t n, void *stream);
  */
 int hip_moe_copy_dev(const void *d_src, void *d_dst, size_t bytes, void *stream);
 
+/*
+ * Dense quantized matrices: the reference's tensor_mma_transposed_2x2 with a
+ * Q8_0/Q4_0 right operand (matmul.c:451-462 -> 270-324), as its models use
+ * it for the attention projections (olmoe.c:448-450, llama.c:498-505), the
+ * output projection and the lm_head (olmoe.c:563,577), and its fused_gemv2/3
+ * (nn.c:399-425: one such product per weight segment, which map to calls in
+ * a row on one stream).
+ *
+ * hip_moe_qmat_upload copies one matrix of N rows of K columns (the tensor's
+ * qdata: GGUF blocks, row-major) to the current device, once, unchanged.
+ * K/64 must be a power of two from 4 to 64 (K = 256 .. 4096: OLMoE 2048,
+ * Mixtral 4096).  NULL if not applicable.
+ */
+typedef struct hip_moe_qmat hip_moe_qmat;
+
+hip_moe_qmat *hip_moe_qmat_upload(const void *qdata, int wtype, size_t N, size_t K);
+
+/*
+ * out[T][N] = add + x[T][K] . W^T, host fp32 buffers, synchronous:
+ * tensor_mma_transposed_2x2(out, x, W, add).  As mma_init (matmul.c:13-33)
+ * does, add holds add_len = T*N values (one per output) or N (the same row
+ * for every token), or is NULL (zero); any other add_len returns 0.  Each
+ * output is fl(add + dot), the dot in fp32 in another order than the
+ * reference's dot_f32_quant (which its default -DQ8_DOT build takes for
+ * every T: matmul.c:107-131,145-165,285-312, quant.c:656-668): ~1e-6
+ * relative.  Returns 1 on success, 0 if not applicable.
+ */
+int hip_moe_qmat_mul(hip_moe_qmat *W, const float *x, size_t T, const float *add,
+                     size_t add_len, float *out);
+
+/* The same on device pointers (d_x 16-byte aligned), enqueued on `stream`
+ * without waiting (NULL = the library's stream for W's device). */
+int hip_moe_qmat_mul_dev(const hip_moe_qmat *W, const float *d_x, size_t T,
+                         const float *d_add, size_t add_len, float *d_out, void *stream);
+
+/* Device bytes of the matrix's blocks. */
+size_t hip_moe_qmat_bytes(const hip_moe_qmat *W);
+
+/* Release the device copy (NULL is a no-op). */
+void hip_moe_qmat_free(hip_moe_qmat *W);
+
 #ifdef __cplusplus
 }
 #endif

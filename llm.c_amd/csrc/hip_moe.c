@@ -645,3 +645,158 @@ int hip_moe_copy_dev(const void *d_src, void *d_dst, size_t bytes, void *stream)
 	LCHK(moe_launch_copy(d_src, d_dst, bytes, stream), "copy");
 	return 1;
 }
+
+/* ------------------------------------------------------------------ */
+/* dense quantized matrices (tensor_mma_transposed_2x2 on Q8_0/Q4_0)   */
+/* ------------------------------------------------------------------ */
+
+struct hip_moe_qmat {
+	int wtype, device;
+	size_t N, K, bytes;
+	uint8_t *d_w;       /* the GGUF blocks, row-major, unchanged */
+	hipStream_t stream; /* the device's shared library stream */
+	int grid1, grid;    /* workgroups for T == 1 and T > 1 (moe_qgemv_grid) */
+	/* staging for the host-pointer entry point */
+	size_t cap_T;
+	float *d_x, *d_add, *d_out;
+};
+
+hip_moe_qmat *hip_moe_qmat_upload(const void *qdata, int wtype, size_t N, size_t K)
+{
+	hip_moe_qmat *W = NULL;
+	int ndev = 0;
+
+	if (wtype != HIP_MOE_Q8_0 && wtype != HIP_MOE_Q4_0) {
+		set_err("qmat_upload: unsupported weight type %d (Q8_0=1, Q4_0=2)", wtype);
+		return NULL;
+	}
+	if (!qdata) {
+		set_err("qmat_upload: NULL weight pointer");
+		return NULL;
+	}
+	/* one wave of K/64 lanes covers a row, no K-split */
+	if (N == 0 || N > 0x7fffffff || K < 256 || K % 256 || !is_pow2(K / MOE_SEG_COLS) ||
+	    K / MOE_SEG_COLS > 64) {
+		set_err("qmat_upload: N=%zu K=%zu not supported (N >= 1, K/64 a power of two "
+			"4..64)", N, K);
+		return NULL;
+	}
+	if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1) {
+		set_err("qmat_upload: no HIP device");
+		return NULL;
+	}
+	W = calloc(1, sizeof(*W));
+	if (!W) {
+		set_err("qmat_upload: out of host memory");
+		return NULL;
+	}
+	W->wtype = wtype;
+	W->N = N;
+	W->K = K;
+	W->bytes = N * row_bytes(wtype, K);
+	HIPCHK(hipGetDevice(&W->device), "hipGetDevice");
+	W->stream = device_stream(W->device);
+	if (!W->stream)
+		goto fail;
+	/* resident workgroups, queried here rather than at a call that may be
+	 * under graph capture */
+	W->grid1 = moe_qgemv_grid(wtype, (int)K, 1);
+	W->grid = moe_qgemv_grid(wtype, (int)K, 0);
+	HIPCHK(hipMalloc((void **)&W->d_w, W->bytes), "hipMalloc(qmat)");
+	HIPCHK(hipMemcpy(W->d_w, qdata, W->bytes, hipMemcpyHostToDevice), "upload qmat");
+	return W;
+fail:
+	hip_moe_qmat_free(W);
+	return NULL;
+}
+
+/* mma_init (matmul.c:13-33): add holds T*N values (copied) or N (every row) */
+static int check_add(const hip_moe_qmat *W, size_t T, const float *add, size_t add_len)
+{
+	if (add && add_len != W->N && add_len != T * W->N) {
+		set_err("qmat_mul: add holds %zu values, not N=%zu or T*N=%zu", add_len, W->N,
+			T * W->N);
+		return 0;
+	}
+	return 1;
+}
+
+int hip_moe_qmat_mul_dev(const hip_moe_qmat *W, const float *d_x, size_t T,
+			 const float *d_add, size_t add_len, float *d_out, void *stream)
+{
+	if (!W || !d_x || !d_out) {
+		set_err("qmat_mul: NULL argument");
+		return 0;
+	}
+	if (T == 0 || T > 65535 || T * W->N > ((size_t)1 << 40)) {
+		set_err("qmat_mul: token count %zu out of range 1..65535", T);
+		return 0;
+	}
+	if ((uintptr_t)d_x % 16) {
+		set_err("qmat_mul: x must be 16-byte aligned");
+		return 0;
+	}
+	if (!check_add(W, T, d_add, add_len))
+		return 0;
+	LCHK(moe_launch_qgemv(W->wtype, W->d_w, (int)W->N, (int)W->K, d_x, (int)T, d_add,
+			      add_len == T * W->N, d_out, T == 1 ? W->grid1 : W->grid,
+			      stream ? stream : (void *)W->stream),
+	     "qgemv");
+	return 1;
+}
+
+int hip_moe_qmat_mul(hip_moe_qmat *W, const float *x, size_t T, const float *add,
+		     size_t add_len, float *out)
+{
+	if (!W || !x || !out) {
+		set_err("qmat_mul: NULL argument");
+		return 0;
+	}
+	if (T == 0 || T > 65535) {
+		set_err("qmat_mul: token count %zu out of range 1..65535", T);
+		return 0;
+	}
+	if (!check_add(W, T, add, add_len))
+		return 0;
+	hipStream_t s = W->stream;
+	if (T > W->cap_T) {
+		hipFree(W->d_x);
+		hipFree(W->d_add);
+		hipFree(W->d_out);
+		W->d_x = W->d_add = W->d_out = NULL;
+		W->cap_T = 0;
+		HIPCHK(hipMalloc((void **)&W->d_x, T * W->K * sizeof(float)), "hipMalloc(x)");
+		HIPCHK(hipMalloc((void **)&W->d_add, T * W->N * sizeof(float)), "hipMalloc(add)");
+		HIPCHK(hipMalloc((void **)&W->d_out, T * W->N * sizeof(float)), "hipMalloc(out)");
+		W->cap_T = T;
+	}
+	HIPCHK(hipMemcpyAsync(W->d_x, x, T * W->K * sizeof(float), hipMemcpyHostToDevice, s),
+	       "copy x");
+	if (add)
+		HIPCHK(hipMemcpyAsync(W->d_add, add, add_len * sizeof(float),
+				      hipMemcpyHostToDevice, s), "copy add");
+	if (!hip_moe_qmat_mul_dev(W, W->d_x, T, add ? W->d_add : NULL, add_len, W->d_out, s))
+		return 0;
+	HIPCHK(hipMemcpyAsync(out, W->d_out, T * W->N * sizeof(float), hipMemcpyDeviceToHost, s),
+	       "copy out");
+	HIPCHK(hipStreamSynchronize(s), "synchronize");
+	return 1;
+fail:
+	return 0;
+}
+
+size_t hip_moe_qmat_bytes(const hip_moe_qmat *W)
+{
+	return W ? W->bytes : 0;
+}
+
+void hip_moe_qmat_free(hip_moe_qmat *W)
+{
+	if (!W)
+		return;
+	hipFree(W->d_w);
+	hipFree(W->d_x);
+	hipFree(W->d_add);
+	hipFree(W->d_out);
+	free(W); /* W->stream is the device's shared stream: it stays */
+}

@@ -57,6 +57,15 @@ int moe_launch_down(int wtype, const uint8_t *down, size_t expert_stride,
                     const uint32_t *ids, int fixed_e, const float *h,
                     float *ypart, size_t ypart_cap, int P, int E, int EI, int *kchunks,
                     void *stream);
+/* out[t][j] = (add ? add[add_rows ? t*N + j : j] : 0) + dot(x[t], W row j),
+ * W of N rows of K columns in Q8_0 (wtype 1) or Q4_0 (2) blocks; K/64 a
+ * power of two 4..64; x 16-byte aligned (moe_qgemv.hip).  nwg workgroups
+ * (moe_qgemv_grid; <= 0: a fixed default). */
+int moe_launch_qgemv(int wtype, const uint8_t *W, int N, int K, const float *x, int T,
+                     const float *add, int add_rows, float *out, int nwg, void *stream);
+/* workgroups the device holds at once for the (wtype, K, T == 1) instance */
+int moe_qgemv_grid(int wtype, int K, int one);
+
 /* ypart floats moe_launch_down may use for any pair count up to P */
 size_t moe_down_part_floats(size_t E, size_t EI, size_t P);
 

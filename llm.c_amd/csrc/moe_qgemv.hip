@@ -1,0 +1,213 @@
+/*
+ * moe_qgemv.hip - dense quantized matrix product for gfx950:
+ *   out[t][j] = add[t][j] (or add[j]) + dot(x[t], W[j])      (add optional)
+ * with W a row-major matrix of N rows of K columns in Q8_0 or Q4_0 blocks.
+ *
+ * This is the reference's tensor_mma_transposed_2x2 with a quantized right
+ * operand (matmul.c:451-462 -> 270-324: result = add or 0, then
+ * result[t][j] += dot, matmul.c:13-33), which its models call for the
+ * attention projections (olmoe.c:448-450), the output projection and the
+ * lm_head (olmoe.c:563,577), and its fused_gemv2/3 (nn.c:340-425: the same
+ * dots over consecutive weight segments).  The reference's default build
+ * (-DQ8_DOT, Makefile:29) takes dot_q8_quant per element for any T
+ * (matmul.c:107-131,145-165,285-312), which for Q8_0/Q4_0 is dot_f32_quant
+ * (quant.c:577-614,656-668).  The dots here are the same products in
+ * another order (two blocks per lane, then a lane tree), ~1e-6 relative.
+ *
+ * Bound: HBM.  Algorithmic bytes per call: N * K/32 * block bytes (34 for
+ * Q8_0, 18 for Q4_0) + T*K*4 (x) + T*N*4 (out) (+ T*N*4 with add).
+ *
+ * Geometry: C = K/64 lanes per row (a power of two, 4..64), each lane one
+ * 64-column segment (two blocks) of a row; a row group is 64/C rows per
+ * wave, four waves.  As many workgroups as the chip holds at once (the
+ * occupancy of the instance times the CUs, moe_qgemv_grid) walk the row
+ * groups (g, g + grid, ...), loading the next group's segments while the
+ * current one's dots run.  Measured with fixed grids of 512 / 768 / 1024 /
+ * 2048: OLMoE lm_head (Q8_0, 3 workgroups per CU) 24.5 / 22.0 / 27.1 /
+ * 24.8 us, Mixtral lm_head (Q4_0, 5 per CU) 23.5 / 20.5 / 19.8 / 20.8 us:
+ * a grid past what is resident leaves a second partial round.  The tokens are staged in LDS tg at a time (up to 4, within
+ * QG_LDS_MAX; each segment padded by 4 floats so the C lanes of a row read
+ * distinct banks): once per workgroup when they all fit, and for one token
+ * a lane keeps its 64 columns in registers.  Every token reuses the
+ * registers' weights, so W is read from HBM once for any T.  (One pass of a
+ * workgroup per row group measured 26.3 us for the OLMoE lm_head and 32.2
+ * for Mixtral's: every workgroup staged the token again, 51 and 128 MB of
+ * L2 reads.)
+ */
+#include "moe_device.h"
+#include "moe_internal.h"
+
+#define QG_WAVES 4
+#define QG_LDS_MAX 65536 /* bytes of staged tokens: QG_LDS_MAX / (K/64 * 68 * 4) at a time */
+#define QG_GRID 768      /* workgroups when the caller passes no grid */
+
+template <int WT, int C, bool ONE> /* ONE: T == 1 */
+__global__ __launch_bounds__(QG_WAVES * WAVE) void k_qgemv(const uint8_t *__restrict__ W,
+							   size_t rb, int N, int K,
+							   const float *__restrict__ x, int T,
+							   int tgmax,
+							   const float *__restrict__ add,
+							   int add_rows,
+							   float *__restrict__ out)
+{
+	constexpr int RPS = WAVE / C; /* rows per wave and group */
+	constexpr int DW = qseg<WT>::DW;
+	extern __shared__ __attribute__((aligned(16))) float sx[];
+	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+	const int seg = lane % C, sub = lane / C;
+	const int nseg = K / MOE_SEG_COLS; /* == C */
+	const int tstride = nseg * SEG_STRIDE;
+	const int ngroups = (N + QG_WAVES * RPS - 1) / (QG_WAVES * RPS);
+	const bool once = T <= tgmax; /* every token fits in LDS: stage them once */
+
+	auto stage = [&](int t0, int tg) {
+		for (int i = threadIdx.x; i < tg * K / 4; i += QG_WAVES * WAVE) {
+			const int t = i / (K / 4), c4 = i % (K / 4); /* float4 c4 of token t */
+			const float4 v = ((const float4 *)(x + (size_t)(t0 + t) * K))[c4];
+			*(float4 *)(sx + t * tstride + (c4 / 16) * SEG_STRIDE + 4 * (c4 % 16)) = v;
+		}
+	};
+	/* rows past N repeat the last row (their results are not stored) */
+	auto load = [&](int g, u32(&d)[DW]) {
+		const int row = min(g * (QG_WAVES * RPS) + wave * RPS + sub, N - 1);
+		load_dwords<DW>(W + (size_t)row * rb + (size_t)seg * qseg<WT>::BYTES, d);
+	};
+	auto dot = [&](const u32(&d)[DW], const float(&xr)[64], float xs0, float xs1) {
+		float v;
+		if constexpr (WT == 1)
+			v = seg_dot_q8_0(d, xr, xs0, xs1);
+		else
+			v = seg_dot_q4_0(d, xr, xs0, xs1);
+		return group_sum<C>(v);
+	};
+	auto store = [&](int g, int t, float v) {
+		const int row = g * (QG_WAVES * RPS) + wave * RPS + sub;
+		if (seg == 0 && row < N) {
+			const size_t o = (size_t)t * N + row;
+			out[o] = (add ? add[add_rows ? o : (size_t)row] : 0.0f) + v;
+		}
+	};
+
+	int g = blockIdx.x;
+	if (g >= ngroups)
+		return; /* the whole workgroup: no barrier below is left waiting */
+	u32 dn[DW];
+	load(g, dn);
+	if (once) {
+		stage(0, T);
+		__syncthreads();
+	}
+	float x1[ONE ? 64 : 1], x1s0 = 0.0f, x1s1 = 0.0f; /* the one token, in registers */
+	if constexpr (ONE) {
+		lds_x64(sx, seg, x1);
+		x1s0 = sum32(x1);
+		x1s1 = sum32(x1 + 32);
+	}
+	/* groups blockIdx.x, + gridDim.x, ...: the next group's weights load
+	 * while this one's dots run */
+	for (; g < ngroups; g += gridDim.x) {
+		u32 d[DW];
+#pragma unroll
+		for (int i = 0; i < DW; i++)
+			d[i] = dn[i];
+		if (g + (int)gridDim.x < ngroups)
+			load(g + gridDim.x, dn);
+		if constexpr (ONE) {
+			store(g, 0, dot(d, x1, x1s0, x1s1));
+			continue;
+		}
+		for (int t0 = 0; t0 < T; t0 += tgmax) {
+			const int tg = min(tgmax, T - t0);
+			if (!once) {
+				__syncthreads(); /* the previous group's readers are done */
+				stage(t0, tg);
+				__syncthreads();
+			}
+			for (int t = 0; t < tg; t++) {
+				float xr[64];
+				lds_x64(sx + t * tstride, seg, xr);
+				store(g, t0 + t, dot(d, xr, sum32(xr), sum32(xr + 32)));
+			}
+		}
+	}
+}
+
+static size_t qg_tok_bytes(int K)
+{
+	return (size_t)(K / MOE_SEG_COLS) * SEG_STRIDE * sizeof(float);
+}
+
+static int qg_tgmax(int K, int T)
+{
+	return min(T, min(4, (int)(QG_LDS_MAX / qg_tok_bytes(K))));
+}
+
+template <int WT>
+static int launch_qgemv_t(int C, const uint8_t *W, size_t rb, int N, int K, const float *x,
+			  int T, const float *add, int add_rows, float *out, int nwg,
+			  hipStream_t s)
+{
+	const int ngroups = (N + QG_WAVES * (WAVE / C) - 1) / (QG_WAVES * (WAVE / C));
+	const dim3 grid(min(ngroups, nwg > 0 ? nwg : QG_GRID));
+	const int tgmax = qg_tgmax(K, T);
+	const size_t lds = (size_t)tgmax * qg_tok_bytes(K);
+#define QG(CC)                                                                          \
+	case CC:                                                                        \
+		if (T == 1)                                                             \
+			hipLaunchKernelGGL((k_qgemv<WT, CC, true>), grid, dim3(QG_WAVES * WAVE), \
+					   lds, s, W, rb, N, K, x, T, tgmax, add, add_rows, \
+					   out);                                        \
+		else                                                                    \
+			hipLaunchKernelGGL((k_qgemv<WT, CC, false>), grid,               \
+					   dim3(QG_WAVES * WAVE), lds, s, W, rb, N, K, x, T, \
+					   tgmax, add, add_rows, out);                  \
+		break;
+	switch (C) {
+		QG(4) QG(8) QG(16) QG(32) QG(64)
+	default:
+		return (int)hipErrorInvalidValue;
+	}
+#undef QG
+	return (int)hipGetLastError();
+}
+
+/* resident workgroups of the instance for (wtype, K, T == 1 or not) times
+ * the CUs of the current device; 0 if the query fails */
+extern "C" int moe_qgemv_grid(int wtype, int K, int one)
+{
+	const int C = moe_lanes_per_row((size_t)K);
+	const size_t lds = (size_t)qg_tgmax(K, one ? 1 : 4) * qg_tok_bytes(K);
+	int dev = 0, ncu = 0, per = 0;
+	hipError_t e = hipSuccess;
+	if (hipGetDevice(&dev) != hipSuccess ||
+	    hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+		return 0;
+#define OCC(WTT, CC)                                                                        \
+	if (wtype == WTT && C == CC)                                                        \
+		e = one ? hipOccupancyMaxActiveBlocksPerMultiprocessor(                      \
+				  &per, k_qgemv<WTT, CC, true>, QG_WAVES * WAVE, lds)      \
+			: hipOccupancyMaxActiveBlocksPerMultiprocessor(                      \
+				  &per, k_qgemv<WTT, CC, false>, QG_WAVES * WAVE, lds);
+	OCC(1, 4) OCC(1, 8) OCC(1, 16) OCC(1, 32) OCC(1, 64)
+	OCC(2, 4) OCC(2, 8) OCC(2, 16) OCC(2, 32) OCC(2, 64)
+#undef OCC
+	if (e != hipSuccess || per < 1)
+		return 0;
+	return per * ncu;
+}
+
+extern "C" int moe_launch_qgemv(int wtype, const uint8_t *W, int N, int K, const float *x,
+				int T, const float *add, int add_rows, float *out, int nwg,
+				void *stream)
+{
+	const int C = moe_lanes_per_row((size_t)K);
+	if (N < 1 || T < 1 || K < 256 || K % 256 || moe_kchunks((size_t)K) != 1 || C < 4)
+		return (int)hipErrorInvalidValue;
+	const size_t rb = (size_t)(K / MOE_QK) * (wtype == 1 ? 34 : 18);
+	hipStream_t s = (hipStream_t)stream;
+	if (wtype == 1)
+		return launch_qgemv_t<1>(C, W, rb, N, K, x, T, add, add_rows, out, nwg, s);
+	if (wtype == 2)
+		return launch_qgemv_t<2>(C, W, rb, N, K, x, T, add, add_rows, out, nwg, s);
+	return (int)hipErrorInvalidValue;
+}

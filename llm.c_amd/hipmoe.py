@@ -68,6 +68,16 @@ def lib():
     L.hip_moe_path_for.restype = i32
     L.hip_moe_path_for.argtypes = [vp, sz]
     L.hip_moe_copy_dev.argtypes = [vp, vp, sz, vp]
+    L.hip_moe_qmat_upload.restype = vp
+    L.hip_moe_qmat_upload.argtypes = [vp, i32, sz, sz]
+    L.hip_moe_qmat_mul.restype = i32
+    L.hip_moe_qmat_mul.argtypes = [vp, f32p, sz, f32p, sz, f32p]
+    L.hip_moe_qmat_mul_dev.restype = i32
+    L.hip_moe_qmat_mul_dev.argtypes = [vp, vp, sz, vp, sz, vp, vp]
+    L.hip_moe_qmat_bytes.restype = sz
+    L.hip_moe_qmat_bytes.argtypes = [vp]
+    L.hip_moe_qmat_free.restype = None
+    L.hip_moe_qmat_free.argtypes = [vp]
     # synthetic inputs
     L.moe_row_bytes.restype = sz
     L.moe_row_bytes.argtypes = [i32, sz]
@@ -396,6 +406,50 @@ class MoeLayer:
     def free(self):
         if self.h:
             lib().hip_moe_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class QMat:
+    """One uploaded Q8_0/Q4_0 matrix of N rows of K columns (hip_moe_qmat_upload)."""
+
+    def __init__(self, q: np.ndarray, wtype: int, N: int, K: int):
+        self.q = np.ascontiguousarray(q, np.uint8)
+        if self.q.size != N * row_bytes(wtype, K):
+            raise ValueError("qmat: block bytes do not match N x K")
+        self.wtype, self.N, self.K = wtype, N, K
+        self.h = lib().hip_moe_qmat_upload(_ptr(self.q), wtype, N, K)
+        if not self.h:
+            raise HipMoeError("hip_moe_qmat_upload: " + last_error())
+
+    def mul(self, x: np.ndarray, add: np.ndarray | None = None) -> np.ndarray:
+        """Host-pointer entry point: add + x[T][K] . W^T, add None, [N] or [T][N]."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.K)
+        T = x.shape[0]
+        out = np.empty((T, self.N), np.float32)
+        a = None if add is None else np.ascontiguousarray(add, np.float32).ravel()
+        rc = lib().hip_moe_qmat_mul(self.h, _ptr(x), T, None if a is None else _ptr(a),
+                                    0 if a is None else a.size, _ptr(out))
+        if rc != 1:
+            raise HipMoeError("hip_moe_qmat_mul: " + last_error())
+        return out
+
+    def mul_dev(self, d_x, T, d_out, d_add=None, add_len=0, stream=None):
+        rc = lib().hip_moe_qmat_mul_dev(self.h, d_x, T, d_add, add_len, d_out, stream)
+        if rc != 1:
+            raise HipMoeError("hip_moe_qmat_mul_dev: " + last_error())
+
+    def bytes(self) -> int:
+        return lib().hip_moe_qmat_bytes(self.h)
+
+    def free(self):
+        if self.h:
+            lib().hip_moe_qmat_free(self.h)
             self.h = None
 
     def __del__(self):

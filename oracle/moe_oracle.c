@@ -217,6 +217,27 @@ float orc_dot_quant(const float *x, const void *qrow, int wtype, size_t n)
 	abort();
 }
 
+/*
+ * tensor_mma_transposed_2x2 with a Q8_0/Q4_0 right operand, as the
+ * reference's default build (-DQ8_DOT, Makefile:29) runs it when K % 256 ==
+ * 0: mma_init (matmul.c:13-33) seeds out with add ([T][N] copied, or [N] for
+ * every row) or zero, then each element gets += dot_q8_quant
+ * (matmul.c:107-131 for T = 1, 145-165 for T > 1), which for Q8_0/Q4_0 is
+ * dot_f32_quant (quant.c:656-668, 577-614).
+ */
+void orc_qmat_mul(const float *x, size_t T, const void *q, int wtype, size_t N, size_t K,
+		  const float *add, size_t add_len, float *out)
+{
+	const size_t rb = row_bytes(wtype, K);
+	for (size_t t = 0; t < T; t++)
+		for (size_t j = 0; j < N; j++) {
+			float init = !add ? 0.0f : add_len == N ? add[j] : add[t * N + j];
+			out[t * N + j] = init + orc_dot_quant(&x[t * K],
+							      (const uint8_t *)q + j * rb,
+							      wtype, K);
+		}
+}
+
 void orc_dequant_row(const void *qrow, int wtype, float *dst, size_t n)
 {
 	const uint8_t *row = qrow;

@@ -42,6 +42,11 @@ void orc_top_k(const float *row, size_t n, uint32_t *ids, float *w, size_t k);
 /* fp32-activation dot with one quantized row (quant.c:103-155). */
 float orc_dot_quant(const float *x, const void *qrow, int wtype, size_t n);
 
+/* out[T][N] = add + x[T][K] . W^T, W = N rows of K columns in blocks; add
+ * NULL, [N] (add_len == N) or [T][N] (matmul.c:13-33,285-312) */
+void orc_qmat_mul(const float *x, size_t T, const void *q, int wtype, size_t N, size_t K,
+		  const float *add, size_t add_len, float *out);
+
 /* Dequantize one row of n elements (quant.c:157-196). */
 void orc_dequant_row(const void *qrow, int wtype, float *dst, size_t n);
 

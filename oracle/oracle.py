@@ -32,6 +32,8 @@ def lib():
         L.orc_top_k.restype = None
         L.orc_dot_quant.argtypes = [vp, vp, i32, sz]
         L.orc_dot_quant.restype = C.c_float
+        L.orc_qmat_mul.argtypes = [vp, sz, vp, i32, sz, sz, vp, sz, vp]
+        L.orc_qmat_mul.restype = None
         L.orc_dequant_row.argtypes = [vp, i32, vp, sz]
         L.orc_dequant_row.restype = None
         L.orc_fused_ffn.argtypes = [vp, vp, vp, vp, i32, sz, sz, vp, vp]
@@ -91,6 +93,19 @@ def dot(x, qrow, wtype):
     x = np.ascontiguousarray(x, np.float32)
     q = np.ascontiguousarray(qrow, np.uint8)
     return np.float32(lib().orc_dot_quant(_p(x), _p(q), wtype, x.size))
+
+
+def qmat_mul(x, q, wtype, N, K, add=None):
+    """out[T][N] = add + x[T][K] . W^T for a Q8_0/Q4_0 matrix of N rows
+    (moe_oracle.c orc_qmat_mul); add None, [N] or [T][N]."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, K)
+    q = np.ascontiguousarray(q, np.uint8)
+    T = x.shape[0]
+    a = None if add is None else np.ascontiguousarray(add, np.float32).ravel()
+    out = np.empty((T, N), np.float32)
+    lib().orc_qmat_mul(_p(x), T, _p(q), wtype, N, K, None if a is None else _p(a),
+                       0 if a is None else a.size, _p(out))
+    return out
 
 
 def dequant(qrow, wtype, n):

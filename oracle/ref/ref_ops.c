@@ -3,6 +3,7 @@
  * functions (tensor_mma_transposed_2x2 matmul.c:451-462, softmax_1d
  * nn.c:221-262, top_k nn.c:276-308, fused_ffn_silu nn.c:496-539,
  * dot_f32_quant quant.c:577-614, quantize_row_q8_0 quant.c:62-78,
+ * tensor_mma_transposed_2x2 with a Q8_0/Q4_0 right operand,
  * tensor_div_scalar / tensor_add tensor.c:334-353,435-456), linked against
  * the reference's own objects.  ref_moe_ffn_composed runs moe_ffn's loop
  * (olmoe.c:355-406, llama.c:407-456) over those functions with the router
@@ -155,4 +156,29 @@ void ref_expf(const float *in, float *out, size_t n)
 {
 	for (size_t i = 0; i < n; i++)
 		out[i] = expf(in[i]);
+}
+
+/* out[T][N] = tensor_mma_transposed_2x2(x[T][K], W[N][K] blocks, add), add
+ * NULL, [N] or [T][N] (mma_init matmul.c:13-33) */
+void ref_qmat_mul(const float *x, size_t T, const void *q, int wtype, size_t N, size_t K,
+		  const float *add, size_t add_len, float *out)
+{
+	tensor_t *in = map2(x, T, K, TENSOR_F32);
+	tensor_t *w = map2(q, N, K, wtype);
+	tensor_t *o = map2(out, T, N, TENSOR_F32);
+	tensor_t *a = NULL;
+	if (add) {
+		if (add_len == N) {
+			a = tensor_new_mapped((void *)add, N, TENSOR_F32);
+			tensor_reshape_1d(a, N);
+		} else {
+			a = map2(add, T, N, TENSOR_F32);
+		}
+	}
+	tensor_mma_transposed_2x2(o, in, w, a);
+	tensor_free_mapped(in);
+	tensor_free_mapped(w);
+	tensor_free_mapped(o);
+	if (a)
+		tensor_free_mapped(a);
 }

@@ -96,3 +96,27 @@ def top_k_closed_form(p: np.ndarray, k: int):
             ids[k - 1 - rank[i]] = i
             w[k - 1 - rank[i]] = p[i]
     return ids, w
+
+
+def qmat_cases():
+    """The dense quantized-product cases of tests/golden/make_golden.py and
+    their seeded input generator (the fixture stores the inputs' digests)."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("make_golden",
+                                                  os.path.join(GOLDEN, "make_golden.py"))
+    mg = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mg)
+    return mg.QMAT_CASES, mg.qmat_inputs
+
+
+def qmat_case(i: int, name: str):
+    """(wtype, T, N, K, q, x, add, expected out) of fixture case `name`,
+    after checking the regenerated inputs are the fixture's bytes."""
+    cases, gen = qmat_cases()
+    wt, T, N, K, add = cases[name]
+    assert list(cases).index(name) == i
+    q, x, a = gen(i, wt, T, N, K, add)
+    g = golden("qmat.npz")
+    assert sha(q) == str(g[f"{name}_sha_w"]) and sha(x) == str(g[f"{name}_sha_x"])
+    assert (sha(a) if a is not None else "") == str(g[f"{name}_sha_add"])
+    return wt, T, N, K, q, x, a, g[f"{name}_out"]

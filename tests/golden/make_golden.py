@@ -22,6 +22,10 @@ same bytes.  Outputs are the reference's own results:
   moe_<cfg>.npz      full moe_ffn layer outputs (olmoe.c:343-407,
                      llama.c:393-457; with a router bias through the add
                      argument of tensor_mma_transposed_2x2)
+  qmat.npz           tensor_mma_transposed_2x2 with a Q8_0/Q4_0 right operand
+                     (matmul.c:13-33,285-312) for T = 1..9, add NULL/[N]/[T][N]
+
+`python tests/golden/make_golden.py qmat` writes qmat.npz alone.
 """
 from __future__ import annotations
 
@@ -62,6 +66,7 @@ def ref():
     L.ref_llama_moe_ffn.argtypes = [vp, vp, sz, vp, vp, vp, vp, i32, sz, sz, sz, sz]
     L.ref_fused_ffn.argtypes = [vp, vp, vp, vp, i32, sz, sz, vp]
     L.ref_dot.argtypes = [vp, vp, i32, sz]
+    L.ref_qmat_mul.argtypes = [vp, sz, vp, i32, sz, sz, vp, sz, vp]
     L.ref_dot.restype = C.c_float
     L.ref_quantize_q8_0.argtypes = [vp, vp, sz]
     L.ref_quantize_q4_0.argtypes = [vp, vp, sz]
@@ -88,10 +93,47 @@ def quant_blocks() -> np.ndarray:
     return np.stack(rng_blocks + edge).astype(np.float32)
 
 
+# name: (wtype, T, N, K, add: None | "bcast" ([N]) | "rows" ([T][N]))
+QMAT_CASES = {
+    "q8_t1": (hipmoe.Q8_0, 1, 203, 2048, None),
+    "q8_t5_rows": (hipmoe.Q8_0, 5, 77, 512, "rows"),
+    "q8_t9": (hipmoe.Q8_0, 9, 50, 256, None),
+    "q4_t1": (hipmoe.Q4_0, 1, 130, 4096, None),
+    "q4_t3_bcast": (hipmoe.Q4_0, 3, 64, 4096, "bcast"),
+    "q4_t7_rows": (hipmoe.Q4_0, 7, 33, 1024, "rows"),
+}
+
+
+def qmat_inputs(i: int, wt: int, T: int, N: int, K: int, add):
+    q = hipmoe.synth_quant_matrix(SEED, 0x7400 + i, 0.02, wt, N, K)
+    x = hipmoe.synth_normal(SEED, 0x7500 + i, T * K).reshape(T, K)
+    a = None
+    if add is not None:
+        a = hipmoe.synth_normal(SEED, 0x7600 + i, N if add == "bcast" else T * N)
+    return q, x, a
+
+
+def qmat_goldens(R):
+    fx = {}
+    for i, (name, (wt, T, N, K, add)) in enumerate(QMAT_CASES.items()):
+        q, x, a = qmat_inputs(i, wt, T, N, K, add)
+        out = np.empty((T, N), np.float32)
+        R.ref_qmat_mul(p(x), T, p(q), wt, N, K, p(a), 0 if a is None else a.size, p(out))
+        fx[f"{name}_sha_w"] = sha(q)
+        fx[f"{name}_sha_x"] = sha(x)
+        fx[f"{name}_sha_add"] = sha(a) if a is not None else ""
+        fx[f"{name}_out"] = out
+        print(f"qmat {name}: T={T} N={N} K={K} add={add} |out|={np.linalg.norm(out):.4f}")
+    np.savez(os.path.join(HERE, "qmat.npz"), seed=SEED, **fx)
+
+
 def main():
     if not os.path.exists(REF_LIB):
         sys.exit(f"{REF_LIB} missing: run oracle/ref/build_ref.sh first")
     R = ref()
+    qmat_goldens(R)
+    if sys.argv[1:] == ["qmat"]:
+        return
 
     # ---- quantizers -----------------------------------------------------
     blocks = quant_blocks()

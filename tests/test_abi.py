@@ -92,3 +92,25 @@ def test_oracle_library_is_separate_from_product():
     assert "oracle" not in out
     syms = subprocess.run(["nm", "-D", hipmoe.LIB_PATH], capture_output=True, text=True).stdout
     assert "orc_" not in syms and "ref_" not in syms
+
+
+@pytest.mark.parametrize("wtype,N,K,msg", [
+    (3, 64, 2048, "unsupported weight type"),
+    (1, 64, 14336, "not supported"),
+    (1, 64, 768, "not supported"),
+    (2, 64, 128, "not supported"),
+    (1, 0, 2048, "not supported"),
+])
+def test_qmat_upload_rejects_unsupported(wtype, N, K, msg):
+    q = np.zeros(max(1, N) * hipmoe.row_bytes(1, max(K, 256)), np.uint8)
+    assert not hipmoe.lib().hip_moe_qmat_upload(q.ctypes.data, wtype, N, K)
+    assert msg in hipmoe.last_error()
+
+
+def test_qmat_calls_on_null_return_zero():
+    L = hipmoe.lib()
+    x = np.zeros(256, np.float32)
+    assert L.hip_moe_qmat_mul(None, x.ctypes.data, 1, None, 0, x.ctypes.data) == 0
+    assert L.hip_moe_qmat_mul_dev(None, 1, 1, None, 0, 1, None) == 0
+    assert L.hip_moe_qmat_bytes(None) == 0
+    L.hip_moe_qmat_free(None)

@@ -18,8 +18,8 @@ import pytest
 
 import hipmoe
 import oracle
-from common import (CONFIGS, REL_L2_TOL, SEED, bits, golden, layer, rel_l2,
-                    router_inputs, sha)
+from common import (CONFIGS, REL_L2_TOL, SEED, bits, golden, layer, qmat_case, qmat_cases,
+                    rel_l2, router_inputs, sha)
 
 pytestmark = pytest.mark.gpu
 TIGHT = 2e-5
@@ -559,3 +559,76 @@ def test_gpu_mixtral_fused_T2_and_T32():
                            expect_path=hipmoe.PATH_DECODE)
     _check_layer_vs_oracle("mixtral_q4", 32, 604, path=hipmoe.PATH_DECODE,
                            expect_path=hipmoe.PATH_DECODE)
+
+
+# --------------------------------------------------------------------------
+# dense quantized products (tensor_mma_transposed_2x2 on Q8_0/Q4_0)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("i,name", list(enumerate(qmat_cases()[0])))
+def test_gpu_qmat_vs_reference_golden(i, name):
+    """hip_moe_qmat_mul against the compiled reference's product (fixture):
+    fp32 dots in another order, held to the fp32 bar TIGHT."""
+    wt, T, N, K, q, x, a, want = qmat_case(i, name)
+    say(f"qmat {name}: T={T} N={N} K={K}")
+    W = hipmoe.QMat(q, wt, N, K)
+    got = W.mul(x, a)
+    W.free()
+    err = rel_l2(got, want)
+    say(f"qmat {name}: rel L2 {err:.3e}")
+    assert err <= TIGHT
+
+
+@pytest.mark.parametrize("wt,N,K", [(hipmoe.Q8_0, 50304, 2048), (hipmoe.Q4_0, 32000, 4096)])
+def test_gpu_qmat_lm_head_full_size(wt, N, K):
+    """The lm_head shapes (OLMoE Q8_0 50304 x 2048, Mixtral Q4_0 32000 x
+    4096), one token: every logit within the fp32 bar of the oracle, and the
+    same greedy token where the top two logits are apart."""
+    say(f"qmat lm_head wt={wt} N={N} K={K}")
+    q = hipmoe.synth_quant_matrix(SEED, 0x7700 + wt, 0.02, wt, N, K)
+    x = hipmoe.synth_normal(SEED, 0x7701 + wt, K).reshape(1, K)
+    W = hipmoe.QMat(q, wt, N, K)
+    assert W.bytes() == N * hipmoe.row_bytes(wt, K)
+    got = W.mul(x)
+    W.free()
+    want = oracle.qmat_mul(x, q, wt, N, K)
+    err = rel_l2(got, want)
+    say(f"qmat lm_head: rel L2 {err:.3e}")
+    assert err <= TIGHT
+    assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))
+    top2 = np.sort(want[0])[-2:]
+    if top2[1] - top2[0] > 1e-4 * abs(top2[1]):
+        assert int(np.argmax(got)) == int(np.argmax(want))
+
+
+def test_gpu_qmat_dev_token_groups_on_stream():
+    """Device-pointer entry point on a caller's stream, T = 8 at K = 4096
+    (tokens staged in LDS three at a time: three groups), N = 257 (a partial
+    last workgroup), add [T][N], then add [N] on the same buffers."""
+    H = hipmoe.hip()
+    wt, N, K, T = hipmoe.Q4_0, 257, 4096, 8
+    q = hipmoe.synth_quant_matrix(SEED, 0x7800, 0.02, wt, N, K)
+    x = hipmoe.synth_normal(SEED, 0x7801, T * K).reshape(T, K)
+    a_rows = hipmoe.synth_normal(SEED, 0x7802, T * N)
+    a_bc = hipmoe.synth_normal(SEED, 0x7803, N)
+    W = hipmoe.QMat(q, wt, N, K)
+    s = H.stream()
+    d_x, d_ar, d_ab = H.upload(x), H.upload(a_rows), H.upload(a_bc)
+    d_o = H.malloc(T * N * 4)
+    try:
+        for d_a, a in ((d_ar, a_rows), (d_ab, a_bc)):
+            say(f"qmat dev: add of {a.size}")
+            W.mul_dev(d_x, T, d_o, d_a, a.size, s)
+            H.stream_sync(s)
+            got = H.download(d_o, (T, N), np.float32)
+            err = rel_l2(got, oracle.qmat_mul(x, q, wt, N, K, a))
+            say(f"qmat dev: rel L2 {err:.3e}")
+            assert err <= TIGHT
+        with pytest.raises(hipmoe.HipMoeError, match="16-byte aligned"):
+            W.mul_dev(d_x + 4, 1, d_o, None, 0, s)
+        with pytest.raises(hipmoe.HipMoeError, match="add holds"):
+            W.mul_dev(d_x, T, d_o, d_ab, N + 1, s)
+    finally:
+        for p in (d_x, d_ar, d_ab, d_o):
+            H.free(p)
+        W.free()

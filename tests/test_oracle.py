@@ -14,8 +14,8 @@ import pytest
 
 import hipmoe
 import oracle
-from common import (CONFIGS, SEED, bits, golden, host_expf_lib, layer, rel_l2,
-                    router_inputs, sha, top_k_closed_form)
+from common import (CONFIGS, SEED, bits, golden, host_expf_lib, layer, qmat_case,
+                    qmat_cases, rel_l2, router_inputs, sha, top_k_closed_form)
 import ctypes as C
 
 
@@ -106,6 +106,30 @@ def test_dot_matches_reference_bits(wtype, name, n):
         d64 = float(np.dot(w64, x[r].astype(np.float64)))
         scale = float(np.dot(np.abs(w64), np.abs(x[r].astype(np.float64))))
         assert abs(float(got[r]) - d64) <= 1e-6 * scale
+
+
+# --------------------------------------------------------------------------
+# dense quantized products (tensor_mma_transposed_2x2 on Q8_0/Q4_0)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("i,name", list(enumerate(qmat_cases()[0])))
+def test_qmat_matches_reference_bits(i, name):
+    """The oracle's product equals the compiled reference's
+    tensor_mma_transposed_2x2 bit for bit (T = 1..9, add NULL / [N] /
+    [T][N]), and a float64 product of the closed-form block decoding."""
+    wt, T, N, K, q, x, a, want = qmat_case(i, name)
+    got = oracle.qmat_mul(x, q, wt, N, K, a)
+    assert np.array_equal(bits(got), bits(want))
+    rb = hipmoe.row_bytes(wt, K)
+    w64 = np.stack([_decode_blocks(q[j * rb:(j + 1) * rb], wt, K) for j in range(N)])
+    x64 = x.astype(np.float64)
+    ref64 = x64 @ w64.T
+    scale = np.abs(x64) @ np.abs(w64).T
+    if a is not None:
+        a64 = a.astype(np.float64).reshape(-1, N)
+        ref64 = ref64 + a64
+        scale = scale + np.abs(a64)
+    assert np.all(np.abs(got - ref64) <= 1e-6 * scale + 1e-30)
 
 
 # --------------------------------------------------------------------------
