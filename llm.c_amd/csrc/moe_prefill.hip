@@ -2,12 +2,14 @@
  * Prefill-sized MoE FFN layer: tokens sorted by expert, then grouped GEMMs
  * on the f16 matrix cores.
  *
- *   k_moe_sort     stable counting sort of the T*K (token, slot) pairs by
+ *   k_moe_sort     counting sort of the T*K (token, slot) pairs by
  *                  expert into m-tiles of MT rows (the tail of each
  *                  expert's last tile is padding, row id -1), and the tile
  *                  table tile -> expert.  MT = 64, or 32 when the experts
  *                  average fewer than 32 pairs (the MFMAs of a tile's
- *                  second 32 rows would be padding).
+ *                  second 32 rows would be padding).  Inside an expert
+ *                  the pairs land in the order the LDS atomics give; a
+ *                  row's products do not depend on its place in the tile.
  *   k_pf_gateup    per (m-tile, 256 h columns): G = X Wg^T and U = X Wu^T
  *                  over d_model, h = silu(G) * U  (nn.c:460-478), stored f16
  *                  in sorted row order.  X is the f16 copy of the tokens the
