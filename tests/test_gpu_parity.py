@@ -632,3 +632,39 @@ def test_gpu_qmat_dev_token_groups_on_stream():
         for p in (d_x, d_ar, d_ab, d_o):
             H.free(p)
         W.free()
+
+
+def test_gpu_qmat_graph_replays():
+    """The dense product in a HIP graph (T = 1 and T = 6 with add [T][N]: two
+    LDS token groups at K = 2048): every replay equals the eager call, with
+    eager calls of another size between the replays."""
+    say("HIP graph of dense products (Q8_0 1000 x 2048, T=1 and T=6), replayed 3 times")
+    H = hipmoe.hip()
+    wt, N, K = hipmoe.Q8_0, 1000, 2048
+    q = hipmoe.synth_quant_matrix(SEED, 0x7900, 0.02, wt, N, K)
+    x1 = hipmoe.synth_normal(SEED, 0x7901, K).reshape(1, K)
+    x6 = hipmoe.synth_normal(SEED, 0x7902, 6 * K).reshape(6, K)
+    a6 = hipmoe.synth_normal(SEED, 0x7903, 6 * N)
+    W = hipmoe.QMat(q, wt, N, K)
+    e1, e6 = W.mul(x1), W.mul(x6, a6)
+    s = H.stream()
+    d_x1, d_x6, d_a6 = H.upload(x1), H.upload(x6), H.upload(a6)
+    d_o1, d_o6 = H.malloc(N * 4), H.malloc(6 * N * 4)
+    try:
+        H.begin_capture(s)
+        W.mul_dev(d_x1, 1, d_o1, None, 0, s)
+        W.mul_dev(d_x6, 6, d_o6, d_a6, 6 * N, s)
+        ge = H.end_capture(s)
+        for rep in range(3):
+            H.check(H.h.hipMemsetAsync(d_o1, 0, N * 4, s), "memset")
+            H.check(H.h.hipMemsetAsync(d_o6, 0, 6 * N * 4, s), "memset")
+            H.graph_launch(ge, s)
+            H.stream_sync(s)
+            assert np.array_equal(bits(H.download(d_o1, (1, N), np.float32)), bits(e1)), rep
+            assert np.array_equal(bits(H.download(d_o6, (6, N), np.float32)), bits(e6)), rep
+            W.mul(x6[:3])  # eager work of another size between replays
+        assert rel_l2(e6, oracle.qmat_mul(x6, q, wt, N, K, a6)) <= TIGHT
+    finally:
+        for p in (d_x1, d_x6, d_a6, d_o1, d_o6):
+            H.free(p)
+        W.free()
