@@ -27,8 +27,8 @@
  * 24.8 us, Mixtral lm_head (Q4_0, 5 per CU) 23.5 / 20.5 / 19.8 / 20.8 us:
  * a grid past what is resident leaves a second partial round.  The tokens are staged in LDS tg at a time (up to 4, within
  * QG_LDS_MAX; each segment padded by 4 floats so the C lanes of a row read
- * distinct banks): once per workgroup when they all fit, and for one token
- * a lane keeps its 64 columns in registers.  Every token reuses the
+ * distinct banks): once per workgroup when they all fit (one token: see
+ * k_qgemv1).  Every token reuses the
  * registers' weights, so W is read from HBM once for any T.  (One pass of a
  * workgroup per row group measured 26.3 us for the OLMoE lm_head and 32.2
  * for Mixtral's: every workgroup staged the token again, 51 and 128 MB of
@@ -41,18 +41,16 @@
 #define QG_LDS_MAX 65536 /* bytes of staged tokens: QG_LDS_MAX / (K/64 * 68 * 4) at a time */
 #define QG_GRID 768      /* workgroups when the caller passes no grid */
 
+#define QG_ARGS                                                                         \
+	const uint8_t *__restrict__ W, size_t rb, int N, int K, const float *__restrict__ x, \
+		int T, int tgmax, const float *__restrict__ add, int add_rows,             \
+		float *__restrict__ out
+
 template <int WT, int C, bool ONE> /* ONE: T == 1 */
-__global__ __launch_bounds__(QG_WAVES * WAVE) void k_qgemv(const uint8_t *__restrict__ W,
-							   size_t rb, int N, int K,
-							   const float *__restrict__ x, int T,
-							   int tgmax,
-							   const float *__restrict__ add,
-							   int add_rows,
-							   float *__restrict__ out)
+__device__ __forceinline__ static void qgemv_body(float *sx, QG_ARGS)
 {
 	constexpr int RPS = WAVE / C; /* rows per wave and group */
 	constexpr int DW = qseg<WT>::DW;
-	extern __shared__ __attribute__((aligned(16))) float sx[];
 	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
 	const int seg = lane % C, sub = lane / C;
 	const int nseg = K / MOE_SEG_COLS; /* == C */
@@ -97,11 +95,13 @@ __global__ __launch_bounds__(QG_WAVES * WAVE) void k_qgemv(const uint8_t *__rest
 		stage(0, T);
 		__syncthreads();
 	}
-	float x1[ONE ? 64 : 1], x1s0 = 0.0f, x1s1 = 0.0f; /* the one token, in registers */
+	float x1s0 = 0.0f, x1s1 = 0.0f; /* the one token's block sums; its columns stay in LDS */
+	const float(&x1)[64] = *(const float(*)[64])(sx + seg * SEG_STRIDE);
 	if constexpr (ONE) {
-		lds_x64(sx, seg, x1);
-		x1s0 = sum32(x1);
-		x1s1 = sum32(x1 + 32);
+		float xr[64];
+		lds_x64(sx, seg, xr);
+		x1s0 = sum32(xr);
+		x1s1 = sum32(xr + 32);
 	}
 	/* groups blockIdx.x, + gridDim.x, ...: the next group's weights load
 	 * while this one's dots run */
@@ -142,6 +142,27 @@ static int qg_tgmax(int K, int T)
 	return min(T, min(4, (int)(QG_LDS_MAX / qg_tok_bytes(K))));
 }
 
+/* one token: its columns stay in LDS (read at each use), which with a
+ * request for 4 waves per SIMD keeps the Q8_0 instance at ~111 VGPRs
+ * without spills (3 waves per SIMD at 138 VGPRs with the columns held in
+ * registers: 22.1 us against 20.8 for the OLMoE lm_head); the Q4_0
+ * instance stays at 5 waves either way */
+template <int WT, int C>
+__global__ __launch_bounds__(QG_WAVES * WAVE)
+__attribute__((amdgpu_waves_per_eu(4))) void k_qgemv1(QG_ARGS)
+{
+	extern __shared__ __attribute__((aligned(16))) float sx1[];
+	qgemv_body<WT, C, true>(sx1, W, rb, N, K, x, T, tgmax, add, add_rows, out);
+}
+
+/* several tokens (requesting 4 waves per SIMD here spills the Q8_0 instance) */
+template <int WT, int C>
+__global__ __launch_bounds__(QG_WAVES * WAVE) void k_qgemv(QG_ARGS)
+{
+	extern __shared__ __attribute__((aligned(16))) float sxn[];
+	qgemv_body<WT, C, false>(sxn, W, rb, N, K, x, T, tgmax, add, add_rows, out);
+}
+
 template <int WT>
 static int launch_qgemv_t(int C, const uint8_t *W, size_t rb, int N, int K, const float *x,
 			  int T, const float *add, int add_rows, float *out, int nwg,
@@ -154,11 +175,11 @@ static int launch_qgemv_t(int C, const uint8_t *W, size_t rb, int N, int K, cons
 #define QG(CC)                                                                          \
 	case CC:                                                                        \
 		if (T == 1)                                                             \
-			hipLaunchKernelGGL((k_qgemv<WT, CC, true>), grid, dim3(QG_WAVES * WAVE), \
+			hipLaunchKernelGGL((k_qgemv1<WT, CC>), grid, dim3(QG_WAVES * WAVE),      \
 					   lds, s, W, rb, N, K, x, T, tgmax, add, add_rows, \
 					   out);                                        \
 		else                                                                    \
-			hipLaunchKernelGGL((k_qgemv<WT, CC, false>), grid,               \
+			hipLaunchKernelGGL((k_qgemv<WT, CC>), grid,                      \
 					   dim3(QG_WAVES * WAVE), lds, s, W, rb, N, K, x, T, \
 					   tgmax, add, add_rows, out);                  \
 		break;
@@ -185,9 +206,9 @@ extern "C" int moe_qgemv_grid(int wtype, int K, int one)
 #define OCC(WTT, CC)                                                                        \
 	if (wtype == WTT && C == CC)                                                        \
 		e = one ? hipOccupancyMaxActiveBlocksPerMultiprocessor(                      \
-				  &per, k_qgemv<WTT, CC, true>, QG_WAVES * WAVE, lds)      \
+				  &per, k_qgemv1<WTT, CC>, QG_WAVES * WAVE, lds)           \
 			: hipOccupancyMaxActiveBlocksPerMultiprocessor(                      \
-				  &per, k_qgemv<WTT, CC, false>, QG_WAVES * WAVE, lds);
+				  &per, k_qgemv<WTT, CC>, QG_WAVES * WAVE, lds);
 	OCC(1, 4) OCC(1, 8) OCC(1, 16) OCC(1, 32) OCC(1, 64)
 	OCC(2, 4) OCC(2, 8) OCC(2, 16) OCC(2, 32) OCC(2, 64)
 #undef OCC
