@@ -98,12 +98,45 @@ int hip_moe_ffn(hip_moe_layer *L, const float *x, float *out, size_t T,
  * workgroup on every CU, and its workgroups wait on one another: do not
  * let two such calls run at once on different streams (order them by
  * stream or event).  Overlapping ones can each hold CUs the other needs;
- * they end on bounded waits, and the next hip_moe_ffn on the layer reports
- * the error.
+ * they end on bounded waits and set the layer's error word.  The error is
+ * sticky: from then on every decode call of the layer writes NaN outputs
+ * (ids 0, weights NaN) until hip_moe_status (or the synchronous
+ * hip_moe_ffn) reports it and resets the layer.
+ *
+ * Scratch grows to the largest T seen.  A call that would grow it while
+ * `stream` is being captured into a HIP graph returns 0 (growth frees
+ * buffers the graph would name): call hip_moe_reserve before capturing.
  */
 int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
                     const float *d_router_bias, uint32_t *d_ids_out,
                     float *d_w_out, void *stream);
+
+/*
+ * Size the layer's scratch for calls of up to T tokens now (synchronous).
+ * No counterpart in the reference (its scratch tensors are sized at load,
+ * olmoe.c:185-199); device-pointer and graph callers use it so that no call
+ * allocates later.  1 = ok.
+ */
+int hip_moe_reserve(hip_moe_layer *L, size_t T);
+
+/*
+ * Wait for `stream` (NULL = the library's stream) and report whether a
+ * bounded wait of the decode kernel ran out since the last report:
+ * 0 = no, 1 = router logits, 2 = partial sums, 3 = start flags, -1 = the
+ * query failed.  On an error it also resets the layer's sync words, so
+ * later calls compute again; the outputs of the failed call and of every
+ * call since were invalid.  The reference has no asynchronous entry point
+ * and no counterpart; hip_moe_ffn runs this check itself.
+ */
+int hip_moe_status(hip_moe_layer *L, void *stream);
+
+/*
+ * Diagnostic: bound every wait of the layer's decode kernel at `polls`
+ * poll rounds (0 = the default, 2^20).  Tests force the error path with a
+ * tiny bound; every wait still ends and the kernel exits normally.  No
+ * counterpart in the reference.  1 = ok.
+ */
+int hip_moe_set_wait_limit(hip_moe_layer *L, int polls);
 
 /*
  * Routing stage alone, device pointers, enqueued on `stream`:

@@ -39,6 +39,7 @@ struct hip_moe_layer {
 	hipStream_t stream;
 	int fused_grid;     /* workgroups of the persistent kernel, 0 = none */
 	int path;           /* HIP_MOE_PATH_*, AUTO unless set */
+	int spin;           /* poll rounds of a decode-kernel wait, 0 = MOE_SPIN_DEFAULT */
 
 	/* scratch for up to cap_T tokens */
 	size_t cap_T;
@@ -320,11 +321,24 @@ size_t hip_moe_weight_bytes(const hip_moe_layer *L)
 	return L ? L->weight_bytes : 0;
 }
 
-static int ensure_scratch(hip_moe_layer *L, size_t T)
+/*
+ * Scratch for calls of up to T tokens.  Growing it frees the old buffers,
+ * which a HIP graph captured earlier would still name, so growth is refused
+ * while `s` is capturing: reserve first (hip_moe_reserve).
+ */
+static int ensure_scratch(hip_moe_layer *L, size_t T, hipStream_t s)
 {
 	if (T <= L->cap_T)
 		return 1;
 	size_t P = T * L->topk;
+	hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+	HIPCHK(hipStreamIsCapturing(s, &cs), "hipStreamIsCapturing");
+	if (cs != hipStreamCaptureStatusNone) {
+		set_err("scratch holds %zu tokens, the call has %zu: growing it under stream "
+			"capture would free buffers a graph names (reserve with hip_moe_reserve "
+			"before capturing)", L->cap_T, T);
+		return 0;
+	}
 	/* calls enqueued earlier may still use the buffers freed here */
 	HIPCHK(hipDeviceSynchronize(), "synchronize before growing scratch");
 	hipFree(L->d_logits);
@@ -400,6 +414,69 @@ static hipStream_t pick_stream(hip_moe_layer *L, void *stream)
 	return stream ? (hipStream_t)stream : L->stream;
 }
 
+int hip_moe_reserve(hip_moe_layer *L, size_t T)
+{
+	if (!L) {
+		set_err("reserve: NULL layer");
+		return 0;
+	}
+	if (T == 0 || T > 65535) {
+		set_err("reserve: token count %zu out of range 1..65535", T);
+		return 0;
+	}
+	return ensure_scratch(L, T, L->stream);
+}
+
+int hip_moe_set_wait_limit(hip_moe_layer *L, int polls)
+{
+	if (!L || polls < 0) {
+		set_err("set_wait_limit: bad layer or poll count %d", polls);
+		return 0;
+	}
+	L->spin = polls;
+	return 1;
+}
+
+/*
+ * Read the decode kernel's error word after `s` drains; if a wait ran out,
+ * clear the sync words and partials (the device is idle then) so that the
+ * epoch restarts, and report the code.  0 = no error, > 0 = MOE_ERR_*,
+ * -1 = the query itself failed.
+ */
+static int check_and_reset(hip_moe_layer *L, hipStream_t s)
+{
+	uint32_t err = 0;
+	HIPCHK(hipStreamSynchronize(s), "synchronize");
+	if (!L->d_sync)
+		return 0;
+	HIPCHK(hipMemcpy(&err, L->d_sync + MOE_SYNC_ERR_WORD, sizeof(err), hipMemcpyDeviceToHost),
+	       "read error word");
+	if (!err)
+		return 0;
+	/* every launch since the failed one returned NaN outputs; flags may be
+	 * left mid-flight: restart the epoch at zero */
+	HIPCHK(hipDeviceSynchronize(), "synchronize before reset");
+	HIPCHK(hipMemset(L->d_sync, 0, L->sync_words * sizeof(uint32_t)), "clear sync words");
+	HIPCHK(hipMemset(L->d_part, 0, L->part_words * sizeof(uint64_t)), "clear partials");
+	HIPCHK(hipDeviceSynchronize(), "synchronize after reset");
+	static const char *what[] = {"", "router logits", "partial sums", "start flags"};
+	set_err("persistent kernel: a dependency wait timed out (%s); outputs of that call "
+		"and of the calls after it until this report are invalid (NaN)",
+		err < 4 ? what[err] : "unknown");
+	return (int)err;
+fail:
+	return -1;
+}
+
+int hip_moe_status(hip_moe_layer *L, void *stream)
+{
+	if (!L) {
+		set_err("status: NULL layer");
+		return -1;
+	}
+	return check_and_reset(L, pick_stream(L, stream));
+}
+
 static int check_T(size_t T)
 {
 	if (T == 0 || T > 65535) {
@@ -429,7 +506,7 @@ int hip_moe_route_dev(hip_moe_layer *L, const float *d_x, size_t T,
 		set_err("route: NULL argument");
 		return 0;
 	}
-	if (!check_T(T) || !ensure_scratch(L, T))
+	if (!check_T(T) || !ensure_scratch(L, T, pick_stream(L, stream)))
 		return 0;
 	return route(L, d_x, T, d_router_bias, d_logits ? d_logits : L->d_logits, d_probs,
 		     d_ids, d_w, NULL, pick_stream(L, stream));
@@ -488,9 +565,9 @@ int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 		set_err("ffn: NULL argument");
 		return 0;
 	}
-	if (!check_T(T) || !ensure_scratch(L, T))
-		return 0;
 	hipStream_t s = pick_stream(L, stream);
+	if (!check_T(T) || !ensure_scratch(L, T, s))
+		return 0;
 	uint32_t *ids = d_ids_out ? d_ids_out : L->d_ids;
 	float *w = d_w_out ? d_w_out : L->d_w;
 	int P = (int)(T * L->topk);
@@ -505,7 +582,7 @@ int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 				      L->d_up, L->d_down, L->gu_stride, L->down_stride,
 				      ids, w, L->d_part, d_out, L->d_sync,
 				      (int)T, (int)L->E, (int)L->EI, (int)L->NE, (int)L->topk,
-				      L->renorm, L->fused_grid, s), "fused layer");
+				      L->renorm, L->fused_grid, L->spin, s), "fused layer");
 		return 1;
 	}
 	if (!route(L, d_x, T, d_router_bias, L->d_logits, NULL, ids, w,
@@ -546,9 +623,9 @@ int hip_moe_expert_ffn_dev(hip_moe_layer *L, size_t expert, const float *d_x,
 		set_err("expert_ffn: expert %zu >= NE %zu", expert, L->NE);
 		return 0;
 	}
-	if (!ensure_scratch(L, 1))
-		return 0;
 	hipStream_t s = pick_stream(L, stream);
+	if (!ensure_scratch(L, 1, s))
+		return 0;
 	LCHK(moe_launch_gateup(L->wtype, L->d_gate, L->d_up, L->gu_stride, NULL, (int)expert,
 			       d_x, L->d_h, 1, 1, (int)L->E, (int)L->EI, s), "gate/up");
 	int kch = 1;
@@ -609,22 +686,9 @@ int hip_moe_ffn(hip_moe_layer *L, const float *x, float *out, size_t T,
 	if (w_out)
 		HIPCHK(hipMemcpyAsync(w_out, L->d_w_io, T * L->topk * sizeof(float),
 				      hipMemcpyDeviceToHost, s), "copy w");
-	HIPCHK(hipStreamSynchronize(s), "synchronize");
-	if (L->d_sync) { /* a bounded wait inside the decode kernel ran out */
-		uint32_t err = 0;
-		HIPCHK(hipMemcpy(&err, L->d_sync + MOE_SYNC_ERR_WORD, sizeof(err),
-				 hipMemcpyDeviceToHost), "read error word");
-		if (err) { /* flags may be left mid-flight: restart the epoch at zero */
-			hipMemset(L->d_sync, 0, L->sync_words * sizeof(uint32_t));
-			hipMemset(L->d_part, 0, L->part_words * sizeof(uint64_t));
-			hipDeviceSynchronize(); /* before the next launch on L->stream */
-			static const char *what[] = {"", "router logits", "partial sums",
-						     "start flags"};
-			set_err("persistent kernel: a dependency wait timed out (%s)",
-				err < 4 ? what[err] : "unknown");
-			return 0;
-		}
-	}
+	/* a bounded wait inside the decode kernel ran out: report and reset */
+	if (check_and_reset(L, s) != 0)
+		return 0;
 	return 1;
 fail:
 	return 0;

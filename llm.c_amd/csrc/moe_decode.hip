@@ -84,9 +84,8 @@ struct DecodeArgs {
 	int n_items, ncon;
 	int off_start, off_rep;
 	int rep_stride; /* u64 entries between replicas (a multiple of 512: 4 KB) */
+	int spin;       /* poll rounds after which a wait gives up (MOE_SPIN_DEFAULT) */
 };
-
-#define SPIN_LIMIT (1 << 20)
 
 /* device-coherent accesses (global_{load,store} ... sc1) */
 __device__ static inline void st_dev_u32(u32 *p, u32 v)
@@ -136,7 +135,8 @@ __host__ __device__ static inline int item_owner(int x, int n, int G)
  * Each thread checks n / NT of them per round.
  */
 template <int NT>
-__device__ static inline void wait_flags(const u32 *f, int n, u32 epoch, u32 *err, u32 code)
+__device__ static inline bool wait_flags(const u32 *f, int n, u32 epoch, u32 *err, u32 code,
+					 int spin)
 {
 	__shared__ int s_ok;
 	int step = 0;
@@ -151,11 +151,11 @@ __device__ static inline void wait_flags(const u32 *f, int n, u32 epoch, u32 *er
 			s_ok = 0;
 		__syncthreads();
 		if (s_ok)
-			return;
-		if (round >= SPIN_LIMIT) {
+			return true;
+		if (round >= spin) {
 			if (threadIdx.x == 0)
 				st_dev_u32(err, code);
-			return;
+			return false;
 		}
 		backoff(step);
 		__syncthreads();
@@ -581,7 +581,7 @@ __device__ static void route_local(const DecodeArgs &a, u32 epoch, float *lds, u
 				v = lane < a.NE ? ld_dev_u64(&rep[lane]) : idle;
 				if (__all((u32)(v >> 32) == epoch))
 					break;
-				if (round >= SPIN_LIMIT) {
+				if (round >= a.spin) {
 					if (lane == 0)
 						st_dev_u32(a.sync + MOE_SYNC_ERR_WORD, MOE_ERR_ROUTE);
 					break;
@@ -619,7 +619,7 @@ __device__ static void route_local(const DecodeArgs &a, u32 epoch, float *lds, u
 				logit = __builtin_bit_cast(float, (u32)v);
 				break;
 			}
-			if (round >= SPIN_LIMIT) {
+			if (round >= a.spin) {
 				if (lane == 0)
 					st_dev_u32(a.sync + MOE_SYNC_ERR_WORD, MOE_ERR_ROUTE);
 				break;
@@ -705,6 +705,7 @@ void k_moe_decode(DecodeArgs a)
 	__shared__ u32 s_ids[MOE_FUSED_MAX_P];
 	__shared__ float s_w[MOE_FUSED_MAX_P];
 	__shared__ u32 s_epoch;
+	__shared__ u32 s_poison;
 	__shared__ uint64_t s_tab[32];
 	__shared__ __attribute__((aligned(16))) float s_h[DEC_CHUNK];
 	__shared__ __attribute__((aligned(16))) u32 s_hd[NT / WAVE][DBLK];
@@ -725,9 +726,11 @@ void k_moe_decode(DecodeArgs a)
 
 	if (threadIdx.x < 32)
 		s_tab[threadIdx.x] = moe_exp2_tab[threadIdx.x];
-	u32 prev_epoch = 0;
-	if (threadIdx.x == 0)
-		prev_epoch = ld_dev_u32(a.sync); /* consumed late: the load overlaps routing */
+	u32 prev_epoch = 0, err0 = 0;
+	if (threadIdx.x == 0) { /* consumed late: the loads overlap routing */
+		prev_epoch = ld_dev_u32(a.sync);
+		err0 = ld_dev_u32(a.sync + MOE_SYNC_ERR_WORD);
+	}
 	/* one token: a router workgroup stages it from its router row's LDS
 	 * copy (no second round trip) */
 	const bool st0 = b < a.NE && x0 < x1 && a.T == 1;
@@ -743,10 +746,27 @@ void k_moe_decode(DecodeArgs a)
 	if (x0 < x1 && !st0)
 		for (int t = t0; t <= (x1 - 1) / 2 / IPT; t++)
 			stage_digits<NT>(sx + (t - t0) * XS, a.x + (size_t)t * a.E, a.E);
-	if (threadIdx.x == 0)
+	if (threadIdx.x == 0) {
 		s_epoch = prev_epoch + 1;
+		s_poison = err0;
+	}
 	__syncthreads();
 	const u32 epoch = s_epoch;
+	/* a wait of an earlier launch ran out: the flags, replicas and partials
+	 * may hold tags this epoch would accept, so every launch until the host
+	 * clears the sync words (hip_moe_status) writes NaN outputs and returns
+	 * without raising its start flag or advancing the epoch */
+	if (s_poison) {
+		const float nan = __builtin_nanf("");
+		for (int i = b * NT + (int)threadIdx.x; i < a.T * a.E; i += G * NT)
+			a.out[i] = nan;
+		if (b == 0)
+			for (int i = threadIdx.x; i < a.T * a.K; i += NT) {
+				a.ids_out[i] = 0;
+				a.w_out[i] = nan;
+			}
+		return;
+	}
 	/* this workgroup has read the epoch word: workgroup 0 may advance it
 	 * once every workgroup has said so */
 	u32 *startf = a.sync + a.off_start;
@@ -940,7 +960,7 @@ void k_moe_decode(DecodeArgs a)
 					}
 				if (!pending)
 					break;
-				if (round >= SPIN_LIMIT) {
+				if (round >= a.spin) {
 					st_dev_u32(a.sync + MOE_SYNC_ERR_WORD, MOE_ERR_COMBINE);
 					break;
 				}
@@ -979,8 +999,12 @@ void k_moe_decode(DecodeArgs a)
 	 * the next launch starts only after this one drains */
 	if (b != 0)
 		return;
-	wait_flags<NT>(startf + 1, G - 1, epoch, a.sync + MOE_SYNC_ERR_WORD, MOE_ERR_FLAGS);
-	if (threadIdx.x == 0)
+	/* a workgroup that has not started by now would read the advanced
+	 * epoch and tag its data for the next launch: the epoch stays, and the
+	 * error word (sticky) stops every launch until the host resets */
+	if (wait_flags<NT>(startf + 1, G - 1, epoch, a.sync + MOE_SYNC_ERR_WORD, MOE_ERR_FLAGS,
+			   a.spin) &&
+	    threadIdx.x == 0)
 		st_dev_u32(a.sync, epoch);
 }
 
@@ -1097,7 +1121,7 @@ extern "C" int moe_launch_fused(int wtype, const float *x, const float *router,
 				const uint8_t *down, size_t gu_stride, size_t dn_stride,
 				uint32_t *ids, float *w, uint64_t *part, float *out, uint32_t *sync,
 				int T, int E, int EI, int NE, int K, int renorm, int grid,
-				void *stream)
+				int spin, void *stream)
 {
 	Geo g = geometry(wtype, (size_t)E, (size_t)EI);
 	if (!g.fn || grid < NE || grid < T)
@@ -1128,6 +1152,7 @@ extern "C" int moe_launch_fused(int wtype, const float *x, const float *router,
 	a.off_start = (int)sl.off_start;
 	a.off_rep = (int)sl.off_rep;
 	a.rep_stride = (int)sl.rep_stride;
+	a.spin = spin > 0 ? spin : MOE_SPIN_DEFAULT;
 	void *args[] = {&a};
 	hipError_t rc = hipLaunchKernel(g.fn, dim3(grid), dim3(g.NT), args,
 					decode_lds_bytes(g, (size_t)E), (hipStream_t)stream);

@@ -29,6 +29,7 @@ extern "C" {
 #define MOE_ERR_ROUTE 1   /* a wait for router logits ran out */
 #define MOE_ERR_COMBINE 2 /* a wait for partial sums ran out */
 #define MOE_ERR_FLAGS 3   /* the end-of-launch start-flag check ran out */
+#define MOE_SPIN_DEFAULT (1 << 20) /* poll rounds before a decode-kernel wait gives up */
 
 /* lanes per gate/up row for a K-long dot: the largest power of two <= 64
  * that divides K / 64, and the number of K-chunks the row is split into. */
@@ -103,7 +104,7 @@ int moe_launch_fused(int wtype, const float *x, const float *router, const float
                      const uint8_t *gate, const uint8_t *up, const uint8_t *down,
                      size_t gu_stride, size_t dn_stride, uint32_t *ids, float *w,
                      uint64_t *part, float *out, uint32_t *sync, int T, int E, int EI, int NE,
-                     int K, int renorm, int grid, void *stream);
+                     int K, int renorm, int grid, int spin, void *stream);
 
 #ifdef __cplusplus
 }

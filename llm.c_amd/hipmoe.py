@@ -50,6 +50,12 @@ def lib():
     L.hip_moe_ffn.argtypes = [vp, f32p, f32p, sz, f32p, u32p, f32p]
     L.hip_moe_ffn_dev.restype = i32
     L.hip_moe_ffn_dev.argtypes = [vp, vp, vp, sz, vp, vp, vp, vp]
+    L.hip_moe_reserve.restype = i32
+    L.hip_moe_reserve.argtypes = [vp, sz]
+    L.hip_moe_status.restype = i32
+    L.hip_moe_status.argtypes = [vp, vp]
+    L.hip_moe_set_wait_limit.restype = i32
+    L.hip_moe_set_wait_limit.argtypes = [vp, i32]
     L.hip_moe_route_dev.restype = i32
     L.hip_moe_route_dev.argtypes = [vp, vp, sz, vp, vp, vp, vp, vp, vp]
     L.hip_moe_expert_ffn_dev.restype = i32
@@ -351,6 +357,19 @@ class MoeLayer:
         rc = lib().hip_moe_ffn_dev(self.h, d_x, d_out, T, d_bias, d_ids, d_w, stream)
         if rc != 1:
             raise HipMoeError("hip_moe_ffn_dev: " + last_error())
+
+    def reserve(self, T: int):
+        """Size the scratch for calls of up to T tokens (before a graph capture)."""
+        if lib().hip_moe_reserve(self.h, T) != 1:
+            raise HipMoeError("hip_moe_reserve: " + last_error())
+
+    def status(self, stream=None) -> int:
+        """0, or the code of a decode-kernel wait that ran out (the layer is reset)."""
+        return lib().hip_moe_status(self.h, stream)
+
+    def set_wait_limit(self, polls: int):
+        if lib().hip_moe_set_wait_limit(self.h, polls) != 1:
+            raise HipMoeError("hip_moe_set_wait_limit: " + last_error())
 
     def route(self, x: np.ndarray, bias: np.ndarray | None = None):
         """Routing stage through hip_moe_route_dev: (logits, probs, ids, w)."""

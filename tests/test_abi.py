@@ -68,6 +68,9 @@ def test_calls_on_null_layer_return_zero():
     assert L.hip_moe_expert_ffn_dev(None, 0, 1, 1, None) == 0
     L.hip_moe_free(None)
     assert L.hip_moe_weight_bytes(None) == 0
+    assert L.hip_moe_reserve(None, 1) == 0
+    assert L.hip_moe_status(None, None) == -1
+    assert L.hip_moe_set_wait_limit(None, 1) == 0
 
 
 def test_upload_without_device_returns_null():
