@@ -112,6 +112,25 @@ int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
                     float *d_w_out, void *stream);
 
 /*
+ * hip_moe_ffn_dev without allocating: the decode path only (T*topk <= 64,
+ * where hip_moe_path_for gives HIP_MOE_PATH_DECODE or the path is forced to
+ * it), its scratch (sync words, tagged partials, and ids/weights when
+ * d_ids_out/d_w_out are NULL) in a static device array of 12 MiB per GPU,
+ * set up by the first hip_moe_upload on that GPU.  It calls no hipMalloc,
+ * hipFree, memset or synchronisation, so it can be captured into a HIP
+ * graph with no reserve step.  A call whose scratch would exceed the array
+ * returns 0 with an error.  Every call on one GPU shares the array: calls
+ * that overlap on one GPU (two streams, any layers) race.  An expired wait
+ * is sticky as on hip_moe_ffn_dev; hip_moe_status on any layer of that GPU
+ * reports and clears it.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under graph capture, serving loops, harnesses that forbid it).
+ */
+int hip_moe_ffn_dev_noalloc(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
+                            const float *d_router_bias, uint32_t *d_ids_out,
+                            float *d_w_out, void *stream);
+
+/*
  * Size the layer's scratch for calls of up to T tokens now (synchronous).
  * No counterpart in the reference (its scratch tensors are sized at load,
  * olmoe.c:185-199); device-pointer and graph callers use it so that no call
@@ -121,7 +140,8 @@ int hip_moe_reserve(hip_moe_layer *L, size_t T);
 
 /*
  * Wait for `stream` (NULL = the library's stream) and report whether a
- * bounded wait of the decode kernel ran out since the last report:
+ * bounded wait of the decode kernel ran out since the last report (in the
+ * layer's scratch, or in the static scratch of its GPU):
  * 0 = no, 1 = router logits, 2 = partial sums, 3 = start flags, -1 = the
  * query failed.  On an error it also resets the layer's sync words, so
  * later calls compute again; the outputs of the failed call and of every

@@ -273,6 +273,8 @@ hip_moe_layer *hip_moe_upload(const float *gate_inp, const void *const *gate_e,
 	L->stream = device_stream(L->device);
 	if (!L->stream)
 		goto fail;
+	/* once per device: the static scratch of hip_moe_ffn_dev_noalloc */
+	HIPCHK((hipError_t)moe_static_scratch_setup(L->device), "static scratch set-up");
 	HIPCHK(hipMalloc((void **)&L->d_router, NE * E * sizeof(float)), "hipMalloc(router)");
 	/* + slack: readable bytes past the last weight */
 	HIPCHK(hipMalloc((void **)&L->d_weights, wbytes + MOE_WEIGHT_SLACK), "hipMalloc(experts)");
@@ -409,6 +411,8 @@ fail:
 	return 0;
 }
 
+static int check_T(size_t T);
+
 static hipStream_t pick_stream(hip_moe_layer *L, void *stream)
 {
 	return stream ? (hipStream_t)stream : L->stream;
@@ -468,13 +472,91 @@ fail:
 	return -1;
 }
 
+/* the same check for the device's static scratch (hip_moe_ffn_dev_noalloc) */
+static int check_and_reset_static(int dev)
+{
+	uint8_t *base = (uint8_t *)moe_static_scratch(dev);
+	uint32_t err = 0;
+	if (!base)
+		return 0;
+	HIPCHK(hipMemcpy(&err, base + MOE_SYNC_ERR_WORD * sizeof(uint32_t), sizeof(err),
+			 hipMemcpyDeviceToHost), "read static error word");
+	if (!err)
+		return 0;
+	HIPCHK(hipDeviceSynchronize(), "synchronize before reset");
+	HIPCHK(hipMemset(base, 0, MOE_STATIC_SCRATCH_BYTES), "clear static scratch");
+	HIPCHK(hipDeviceSynchronize(), "synchronize after reset");
+	set_err("persistent kernel (static scratch): a dependency wait timed out (code %u); "
+		"outputs of hip_moe_ffn_dev_noalloc since then are invalid (NaN)", err);
+	return (int)err;
+fail:
+	return -1;
+}
+
 int hip_moe_status(hip_moe_layer *L, void *stream)
 {
 	if (!L) {
 		set_err("status: NULL layer");
 		return -1;
 	}
-	return check_and_reset(L, pick_stream(L, stream));
+	int rc = check_and_reset(L, pick_stream(L, stream));
+	int rs = rc < 0 ? 0 : check_and_reset_static(L->device);
+	return rc != 0 ? rc : rs;
+}
+
+/*
+ * The decode path of hip_moe_ffn_dev with its scratch (sync words, tagged
+ * partials, ids and weights when the caller passes none) in the device's
+ * static array instead of the layer's buffers: no allocation, no memset,
+ * no synchronisation.  Layout in the array: sync words at 0, partials from
+ * the sync size of the layer's largest decode call (256-byte aligned), then
+ * ids and weights.  Every call on a device shares that array; the epoch
+ * tags make the contents a previous call left (of any size or layer) stale.
+ */
+int hip_moe_ffn_dev_noalloc(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
+			    const float *d_router_bias, uint32_t *d_ids_out, float *d_w_out,
+			    void *stream)
+{
+	if (!L || !d_x || !d_out) {
+		set_err("ffn_noalloc: NULL argument");
+		return 0;
+	}
+	if (!check_T(T))
+		return 0;
+	if (L->fused_grid <= 0 ||
+	    !moe_fused_supported(L->wtype, L->E, L->EI, L->NE, T, L->topk) ||
+	    (L->path != HIP_MOE_PATH_AUTO && L->path != HIP_MOE_PATH_DECODE)) {
+		set_err("ffn_noalloc: only the decode path (T*topk <= %d) runs without "
+			"allocation; T=%zu topk=%zu does not take it", MOE_FUSED_MAX_P, T, L->topk);
+		return 0;
+	}
+	uint8_t *base = (uint8_t *)moe_static_scratch(L->device);
+	if (!base) {
+		set_err("ffn_noalloc: the static scratch of device %d is not set up", L->device);
+		return 0;
+	}
+	const size_t tmax = MOE_FUSED_MAX_P / L->topk;
+	const size_t part_off =
+		(moe_fused_sync_words(tmax, L->NE, L->fused_grid) * sizeof(uint32_t) + 255) &
+		~(size_t)255;
+	const size_t part_bytes =
+		moe_fused_part_words(T, L->topk, L->E, L->EI, L->fused_grid) * sizeof(uint64_t);
+	const size_t ids_off = part_off + part_bytes, P = T * L->topk;
+	const size_t need = ids_off + 2 * P * sizeof(uint32_t);
+	if (need > MOE_STATIC_SCRATCH_BYTES) {
+		set_err("ffn_noalloc: T=%zu needs %zu bytes of scratch, beyond the %zu-byte "
+			"static array", T, need, (size_t)MOE_STATIC_SCRATCH_BYTES);
+		return 0;
+	}
+	uint32_t *ids = d_ids_out ? d_ids_out : (uint32_t *)(base + ids_off);
+	float *w = d_w_out ? d_w_out : (float *)(base + ids_off + P * sizeof(uint32_t));
+	LCHK(moe_launch_fused(L->wtype, d_x, L->d_router, d_router_bias, L->d_gate, L->d_up,
+			      L->d_down, L->gu_stride, L->down_stride, ids, w,
+			      (uint64_t *)(base + part_off), d_out, (uint32_t *)base, (int)T,
+			      (int)L->E, (int)L->EI, (int)L->NE, (int)L->topk, L->renorm,
+			      L->fused_grid, L->spin, pick_stream(L, stream)),
+	     "fused layer (static scratch)");
+	return 1;
 }
 
 static int check_T(size_t T)

@@ -63,6 +63,8 @@
  */
 #include "moe_device.h"
 
+#include <pthread.h>
+
 #define NREP 64      /* == WAVE: one replica per lane of the writing wave */
 #define PSLICE 8     /* outputs per combine slice */
 #define DEC_TOKS 2   /* tokens one workgroup's item range can span (T <= G) */
@@ -1159,4 +1161,57 @@ extern "C" int moe_launch_fused(int wtype, const float *x, const float *router,
 	if (rc != hipSuccess)
 		return (int)rc;
 	return (int)hipGetLastError();
+}
+
+/* ---------------------------------------------------------------------- */
+/* static scratch of the allocation-free decode entry point               */
+/* ---------------------------------------------------------------------- */
+
+/*
+ * The sync words, tagged partials, ids and weights of
+ * hip_moe_ffn_dev_noalloc live here instead of in memory the layer
+ * allocates.  Each device holds its own copy, at its own address, from the
+ * time the module loads until the process ends.  In host code `scratch`
+ * names a host-side stand-in, not device memory: host code only ever uses
+ * the address hipGetSymbolAddress returns for the current device, kept per
+ * device in g_scratch.
+ */
+static __device__ __align__(256) uint8_t scratch[MOE_STATIC_SCRATCH_BYTES];
+
+#define MOE_SCRATCH_DEVICES 64
+static void *g_scratch[MOE_SCRATCH_DEVICES];
+static pthread_mutex_t g_scratch_mu = PTHREAD_MUTEX_INITIALIZER;
+
+/* Once per device, with `dev` current: look up this device's copy of the
+ * array and clear it (the epoch, error word and flags start at zero). */
+extern "C" int moe_static_scratch_setup(int dev)
+{
+	if (dev < 0 || dev >= MOE_SCRATCH_DEVICES)
+		return (int)hipErrorInvalidDevice;
+	int rc = 0;
+	pthread_mutex_lock(&g_scratch_mu);
+	if (!g_scratch[dev]) {
+		void *p = NULL;
+		hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+		if (e == hipSuccess && p)
+			e = hipMemset(p, 0, MOE_STATIC_SCRATCH_BYTES);
+		if (e == hipSuccess)
+			e = hipDeviceSynchronize();
+		if (e == hipSuccess)
+			g_scratch[dev] = p;
+		rc = (int)e;
+	}
+	pthread_mutex_unlock(&g_scratch_mu);
+	return rc;
+}
+
+/* This device's copy of the array, NULL before moe_static_scratch_setup. */
+extern "C" void *moe_static_scratch(int dev)
+{
+	if (dev < 0 || dev >= MOE_SCRATCH_DEVICES)
+		return NULL;
+	pthread_mutex_lock(&g_scratch_mu);
+	void *p = g_scratch[dev];
+	pthread_mutex_unlock(&g_scratch_mu);
+	return p;
 }

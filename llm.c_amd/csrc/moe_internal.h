@@ -106,6 +106,14 @@ int moe_launch_fused(int wtype, const float *x, const float *router, const float
                      uint64_t *part, float *out, uint32_t *sync, int T, int E, int EI, int NE,
                      int K, int renorm, int grid, int spin, void *stream);
 
+/* Static device scratch of the allocation-free decode entry point
+ * (moe_decode.hip): MOE_STATIC_SCRATCH_BYTES per device, looked up and
+ * cleared once per device by moe_static_scratch_setup (with that device
+ * current), then addressed through moe_static_scratch(dev) only. */
+#define MOE_STATIC_SCRATCH_BYTES ((size_t)12 << 20)
+int moe_static_scratch_setup(int dev);
+void *moe_static_scratch(int dev);
+
 #ifdef __cplusplus
 }
 #endif

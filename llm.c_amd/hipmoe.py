@@ -50,6 +50,8 @@ def lib():
     L.hip_moe_ffn.argtypes = [vp, f32p, f32p, sz, f32p, u32p, f32p]
     L.hip_moe_ffn_dev.restype = i32
     L.hip_moe_ffn_dev.argtypes = [vp, vp, vp, sz, vp, vp, vp, vp]
+    L.hip_moe_ffn_dev_noalloc.restype = i32
+    L.hip_moe_ffn_dev_noalloc.argtypes = [vp, vp, vp, sz, vp, vp, vp, vp]
     L.hip_moe_reserve.restype = i32
     L.hip_moe_reserve.argtypes = [vp, sz]
     L.hip_moe_status.restype = i32
@@ -357,6 +359,12 @@ class MoeLayer:
         rc = lib().hip_moe_ffn_dev(self.h, d_x, d_out, T, d_bias, d_ids, d_w, stream)
         if rc != 1:
             raise HipMoeError("hip_moe_ffn_dev: " + last_error())
+
+    def ffn_dev_noalloc(self, d_x, d_out, T, d_bias=None, d_ids=None, d_w=None, stream=None):
+        """hip_moe_ffn_dev_noalloc: the decode path on the GPU's static scratch."""
+        rc = lib().hip_moe_ffn_dev_noalloc(self.h, d_x, d_out, T, d_bias, d_ids, d_w, stream)
+        if rc != 1:
+            raise HipMoeError("hip_moe_ffn_dev_noalloc: " + last_error())
 
     def reserve(self, T: int):
         """Size the scratch for calls of up to T tokens (before a graph capture)."""
