@@ -48,6 +48,22 @@ uint64_t moe_stream_gate(uint64_t layer, uint64_t expert);
 uint64_t moe_stream_up(uint64_t layer, uint64_t expert);
 uint64_t moe_stream_down(uint64_t layer, uint64_t expert);
 uint64_t moe_stream_input(uint64_t call);
+/* The model tensors around the MoE layers: layer l's tensor of kind k
+ * (MOE_T_*); tensors outside the layers use layer MOE_T_GLOBAL. */
+uint64_t moe_stream_tensor(uint64_t layer, uint64_t kind);
+#define MOE_T_ATTN_Q 0
+#define MOE_T_ATTN_K 1
+#define MOE_T_ATTN_V 2
+#define MOE_T_ATTN_O 3
+#define MOE_T_ATTN_NORM 4
+#define MOE_T_Q_NORM 5
+#define MOE_T_K_NORM 6
+#define MOE_T_FFN_NORM 7
+#define MOE_T_TOKEN_EMBD 8
+#define MOE_T_OUTPUT 9
+#define MOE_T_OUTPUT_NORM 10
+#define MOE_T_PROMPT 11
+#define MOE_T_GLOBAL 0xffffffffu
 
 /* f32 -> f16 round-to-nearest-even (as F16C _cvtss_sh(x, 0)) and the exact
  * f16 -> f32, exposed for tests. */

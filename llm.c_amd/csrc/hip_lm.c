@@ -1,0 +1,594 @@
+/*
+ * hip_lm.c - host layer of the whole-model decode (include/hip_lm.h).
+ *
+ * Owns the device copies of every tensor, the fp32 KV cache, the step's
+ * buffers and a small device state block (token, position, cache row), and
+ * enqueues one decode step as
+ *   embed -> per layer [rmsnorm -> qkv product -> q/k norm + RoPE + cache
+ *   row -> attention -> output product + residual -> rmsnorm -> MoE layer]
+ *   -> residual + final rmsnorm -> lm_head product -> greedy pick
+ * (olmoe_forward for one token, olmoe.c:409-500, then olmoe.c:558-564 and
+ * main.c:189-193).  The residual adds ride on other steps: the output
+ * product's `add` operand is the residual stream, and the MoE output is
+ * added to it in front of the next RMSNorm.  Every step kernel reads its
+ * counters from the device, so generate captures a step once per shape
+ * (with and without the lm_head) and replays it.
+ */
+#include "hip_lm.h"
+#include "lm_internal.h"
+#include "moe_internal.h"
+
+#include <hip/hip_runtime_api.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+struct lm_layer {
+	float *attn_norm, *q_norm, *k_norm, *ffn_norm;
+	uint8_t *wqkv; /* [q rows | k rows | v rows][E] blocks */
+	uint8_t *wo;   /* [E][heads * 128] blocks */
+	hip_moe_layer *moe;
+};
+
+struct hip_lm {
+	int arch, wtype, device;
+	size_t L, E, H, KH, HL, V, C, NE, K, EI, window;
+	float theta, scale_div;
+	size_t EQ, EKV; /* rows of q, and of k (= of v) */
+	size_t weight_bytes;
+	hipStream_t stream;
+
+	uint8_t *d_wte, *d_head;
+	float *d_onorm;
+	struct lm_layer *ly;
+	int grid_qkv, grid_o, grid_head; /* resident workgroups of the one-token products */
+
+	float *d_kc, *d_vc; /* [L][KH][C][HL] */
+	float *d_freq;      /* [HL / 2] rope frequencies */
+	float *d_h0, *d_h1, *d_x, *d_qkv, *d_attn, *d_moe_in, *d_moe_out, *d_part, *d_logits;
+	uint32_t *d_ids;   /* [L][K] */
+	float *d_w;        /* [L][K] */
+	LmState *d_st;
+	int *d_prompt, *d_tokens;
+	size_t prompt_cap, tokens_cap;
+
+	/* host mirror of the counters */
+	LmState st;
+	hipGraphExec_t g_body, g_head; /* captured steps without / with the lm_head */
+	hipEvent_t ev0, ev1;
+};
+
+static void lm_err(const char *fmt, ...)
+{
+	char buf[512];
+	va_list ap;
+	va_start(ap, fmt);
+	vsnprintf(buf, sizeof(buf), fmt, ap);
+	va_end(ap);
+	moe_set_error(buf);
+}
+
+#define HIPCHK(call, what)                                                        \
+	do {                                                                      \
+		hipError_t e_ = (call);                                           \
+		if (e_ != hipSuccess) {                                           \
+			lm_err("%s: %s", what, hipGetErrorString(e_));             \
+			goto fail;                                                \
+		}                                                                 \
+	} while (0)
+
+#define LCHK(rc, what)                                                            \
+	do {                                                                      \
+		int r_ = (rc);                                                    \
+		if (r_ != 0) {                                                    \
+			lm_err("%s: %s", what, hipGetErrorString((hipError_t)r_));  \
+			return 0;                                                 \
+		}                                                                 \
+	} while (0)
+
+static size_t qbytes(int wtype, size_t rows, size_t cols)
+{
+	return rows * (cols / 32) * (wtype == HIP_MOE_Q8_0 ? 34 : 18);
+}
+
+static int upload(void **dst, const void *src, size_t bytes, const char *what)
+{
+	HIPCHK(hipMalloc(dst, bytes), what);
+	HIPCHK(hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice), what);
+	return 1;
+fail:
+	return 0;
+}
+
+static void drop_graphs(hip_lm *M)
+{
+	if (M->g_body)
+		hipGraphExecDestroy(M->g_body);
+	if (M->g_head)
+		hipGraphExecDestroy(M->g_head);
+	M->g_body = M->g_head = NULL;
+}
+
+void hip_lm_free(hip_lm *M)
+{
+	if (!M)
+		return;
+	drop_graphs(M);
+	if (M->ly) {
+		for (size_t l = 0; l < M->L; l++) {
+			struct lm_layer *y = &M->ly[l];
+			hipFree(y->attn_norm);
+			hipFree(y->q_norm);
+			hipFree(y->k_norm);
+			hipFree(y->ffn_norm);
+			hipFree(y->wqkv);
+			hipFree(y->wo);
+			hip_moe_free(y->moe);
+		}
+		free(M->ly);
+	}
+	void *bufs[] = {M->d_wte, M->d_head, M->d_onorm, M->d_kc, M->d_vc, M->d_freq, M->d_h0,
+			M->d_h1, M->d_x, M->d_qkv, M->d_attn, M->d_moe_in, M->d_moe_out,
+			M->d_part, M->d_logits, M->d_ids, M->d_w, M->d_st, M->d_prompt,
+			M->d_tokens};
+	for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
+		hipFree(bufs[i]);
+	if (M->ev0)
+		hipEventDestroy(M->ev0);
+	if (M->ev1)
+		hipEventDestroy(M->ev1);
+	if (M->stream)
+		hipStreamDestroy(M->stream);
+	free(M);
+}
+
+static int check_desc(const hip_lm_desc *d)
+{
+	if (!d) {
+		lm_err("lm_upload: NULL descriptor");
+		return 0;
+	}
+	if (d->arch != HIP_LM_OLMOE && d->arch != HIP_LM_MIXTRAL) {
+		lm_err("lm_upload: unknown arch %d", d->arch);
+		return 0;
+	}
+	if (d->wtype != HIP_MOE_Q8_0 && d->wtype != HIP_MOE_Q4_0) {
+		lm_err("lm_upload: unsupported weight type %d", d->wtype);
+		return 0;
+	}
+	if (!d->layers || !d->E || !d->heads || !d->kv_heads || d->heads % d->kv_heads ||
+	    !d->vocab || d->vocab > 0x7fffffff || d->context < 2 || d->context > (1u << 24)) {
+		lm_err("lm_upload: bad sizes (layers %zu, E %zu, heads %zu/%zu, vocab %zu, "
+		       "context %zu)", d->layers, d->E, d->heads, d->kv_heads, d->vocab, d->context);
+		return 0;
+	}
+	if (d->arch == HIP_LM_OLMOE && d->heads * LM_HLEN != d->E) {
+		lm_err("lm_upload: OLMoE needs heads * %d == E", LM_HLEN);
+		return 0;
+	}
+	if (!d->token_embd || !d->output || !d->output_norm || !d->attn_norm || !d->attn_q ||
+	    !d->attn_k || !d->attn_v || !d->attn_o || !d->ffn_norm || !d->gate_inp ||
+	    !d->gate_e || !d->up_e || !d->down_e ||
+	    (d->arch == HIP_LM_OLMOE && (!d->q_norm || !d->k_norm))) {
+		lm_err("lm_upload: NULL tensor pointer");
+		return 0;
+	}
+	return 1;
+}
+
+hip_lm *hip_lm_upload(const hip_lm_desc *d)
+{
+	hip_lm *M = NULL;
+	uint8_t *stage = NULL;
+	int ndev = 0;
+	if (!check_desc(d))
+		return NULL;
+	if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1) {
+		lm_err("lm_upload: no HIP device");
+		return NULL;
+	}
+	M = calloc(1, sizeof(*M));
+	if (!M) {
+		lm_err("lm_upload: out of host memory");
+		return NULL;
+	}
+	M->arch = d->arch;
+	M->wtype = d->wtype;
+	M->L = d->layers;
+	M->E = d->E;
+	M->H = d->heads;
+	M->KH = d->kv_heads;
+	M->HL = LM_HLEN;
+	M->V = d->vocab;
+	M->C = d->context;
+	M->NE = d->NE;
+	M->K = d->topk;
+	M->EI = d->EI;
+	M->window = d->sliding_window;
+	M->theta = d->rope_theta;
+	/* hlen_sq = sqrt((scalar_t)HLEN) (olmoe.c:150) */
+	M->scale_div = (float)sqrt((double)(float)M->HL);
+	M->EQ = M->H * M->HL;
+	M->EKV = M->KH * M->HL;
+	const int wt = d->wtype;
+	const size_t E = M->E;
+
+	HIPCHK(hipGetDevice(&M->device), "hipGetDevice");
+	HIPCHK(hipStreamCreateWithFlags(&M->stream, hipStreamNonBlocking), "hipStreamCreate");
+	HIPCHK(hipEventCreate(&M->ev0), "hipEventCreate");
+	HIPCHK(hipEventCreate(&M->ev1), "hipEventCreate");
+
+	/* products: one token, K = E (qkv) and heads * 128 (output); the
+	 * workgroups resident at once, queried here, not under capture */
+	M->grid_qkv = moe_qgemv_grid(wt, (int)E, 1);
+	M->grid_o = moe_qgemv_grid(wt, (int)M->EQ, 1);
+	M->grid_head = M->grid_qkv;
+	if (M->grid_qkv <= 0 || M->grid_o <= 0) {
+		lm_err("lm_upload: E=%zu / heads*128=%zu not supported by the dense product", E,
+		       M->EQ);
+		goto fail;
+	}
+
+	if (!upload((void **)&M->d_wte, d->token_embd, qbytes(wt, M->V, E), "upload token_embd") ||
+	    !upload((void **)&M->d_head, d->output, qbytes(wt, M->V, E), "upload output") ||
+	    !upload((void **)&M->d_onorm, d->output_norm, E * sizeof(float), "upload output_norm"))
+		goto fail;
+	M->weight_bytes = 2 * qbytes(wt, M->V, E) + E * sizeof(float);
+
+	M->ly = calloc(M->L, sizeof(*M->ly));
+	const size_t qb = qbytes(wt, M->EQ, E), kb = qbytes(wt, M->EKV, E);
+	stage = malloc(qb + 2 * kb);
+	if (!M->ly || !stage) {
+		lm_err("lm_upload: out of host memory");
+		goto fail;
+	}
+	for (size_t l = 0; l < M->L; l++) {
+		struct lm_layer *y = &M->ly[l];
+		if (!d->attn_norm[l] || !d->attn_q[l] || !d->attn_k[l] || !d->attn_v[l] ||
+		    !d->attn_o[l] || !d->ffn_norm[l] || !d->gate_inp[l]) {
+			lm_err("lm_upload: NULL tensor of layer %zu", l);
+			goto fail;
+		}
+		memcpy(stage, d->attn_q[l], qb);
+		memcpy(stage + qb, d->attn_k[l], kb);
+		memcpy(stage + qb + kb, d->attn_v[l], kb);
+		if (!upload((void **)&y->wqkv, stage, qb + 2 * kb, "upload attn_q/k/v") ||
+		    !upload((void **)&y->wo, d->attn_o[l], qbytes(wt, E, M->EQ), "upload attn_output") ||
+		    !upload((void **)&y->attn_norm, d->attn_norm[l], E * 4, "upload attn_norm") ||
+		    !upload((void **)&y->ffn_norm, d->ffn_norm[l], E * 4, "upload ffn_norm"))
+			goto fail;
+		if (d->arch == HIP_LM_OLMOE &&
+		    (!upload((void **)&y->q_norm, d->q_norm[l], M->EQ * 4, "upload attn_q_norm") ||
+		     !upload((void **)&y->k_norm, d->k_norm[l], M->EKV * 4, "upload attn_k_norm")))
+			goto fail;
+		y->moe = hip_moe_upload(d->gate_inp[l], d->gate_e + l * M->NE, d->up_e + l * M->NE,
+					d->down_e + l * M->NE, wt, E, M->EI, M->NE, M->K,
+					d->arch == HIP_LM_MIXTRAL);
+		if (!y->moe)
+			goto fail; /* hip_moe_upload recorded why */
+		/* scratch for one token now: never allocated under capture */
+		if (!hip_moe_reserve(y->moe, 1))
+			goto fail;
+		M->weight_bytes += qb + 2 * kb + qbytes(wt, E, M->EQ) + 2 * E * 4 +
+				   (y->q_norm ? (M->EQ + M->EKV) * 4 : 0) +
+				   hip_moe_weight_bytes(y->moe);
+	}
+	free(stage);
+	stage = NULL;
+
+	/* rope frequencies 1 / powf(theta, 2i / HLEN) (nn.c:205), the host's libm */
+	{
+		float fr[LM_HLEN / 2];
+		for (size_t i = 0; i < M->HL / 2; i++)
+			fr[i] = 1.0f / powf(M->theta, (float)(2 * i) / (float)M->HL);
+		if (!upload((void **)&M->d_freq, fr, sizeof(fr), "upload rope frequencies"))
+			goto fail;
+	}
+	const size_t cache = M->L * M->KH * M->C * M->HL * sizeof(float);
+	HIPCHK(hipMalloc((void **)&M->d_kc, cache), "hipMalloc(k cache)");
+	HIPCHK(hipMalloc((void **)&M->d_vc, cache), "hipMalloc(v cache)");
+	HIPCHK(hipMemset(M->d_kc, 0, cache), "clear k cache");
+	HIPCHK(hipMemset(M->d_vc, 0, cache), "clear v cache");
+	const size_t EA = E > M->EQ ? E : M->EQ;
+	HIPCHK(hipMalloc((void **)&M->d_h0, E * 4), "hipMalloc(h0)");
+	HIPCHK(hipMalloc((void **)&M->d_h1, E * 4), "hipMalloc(h1)");
+	HIPCHK(hipMalloc((void **)&M->d_x, EA * 4), "hipMalloc(x)");
+	HIPCHK(hipMalloc((void **)&M->d_qkv, (M->EQ + 2 * M->EKV) * 4), "hipMalloc(qkv)");
+	HIPCHK(hipMalloc((void **)&M->d_attn, EA * 4), "hipMalloc(attn)");
+	HIPCHK(hipMalloc((void **)&M->d_moe_in, M->L * E * 4), "hipMalloc(moe_in)");
+	HIPCHK(hipMalloc((void **)&M->d_moe_out, E * 4), "hipMalloc(moe_out)");
+	HIPCHK(hipMalloc((void **)&M->d_part,
+			 M->H * (size_t)lm_attn_chunks((int)M->C, (int)M->window) * (LM_HLEN + 2) * 4),
+	       "hipMalloc(attention partials)");
+	HIPCHK(hipMalloc((void **)&M->d_logits, M->V * 4), "hipMalloc(logits)");
+	HIPCHK(hipMalloc((void **)&M->d_ids, M->L * M->K * 4), "hipMalloc(ids)");
+	HIPCHK(hipMalloc((void **)&M->d_w, M->L * M->K * 4), "hipMalloc(w)");
+	HIPCHK(hipMalloc((void **)&M->d_st, sizeof(LmState)), "hipMalloc(state)");
+	HIPCHK(hipMemset(M->d_st, 0, sizeof(LmState)), "clear state");
+	HIPCHK(hipDeviceSynchronize(), "synchronize after upload");
+	return M;
+fail:
+	free(stage);
+	hip_lm_free(M);
+	return NULL;
+}
+
+size_t hip_lm_weight_bytes(const hip_lm *M)
+{
+	return M ? M->weight_bytes : 0;
+}
+
+/* kvcache_rotate (kvcache.c:31-56) when the cache is full, before a step;
+ * the host mirror of the counters is exact (one row per step) */
+static int rotate_if_full(hip_lm *M)
+{
+	if ((size_t)M->st.size < M->C)
+		return 1;
+	size_t keep = M->window ? M->window : M->C / 2;
+	if (keep > (size_t)M->st.size)
+		keep = (size_t)M->st.size;
+	const size_t drop = (size_t)M->st.size - keep;
+	const size_t slab = M->C * M->HL, slabs = M->L * M->KH;
+	if (drop > 0) {
+		for (int kv = 0; kv < 2; kv++) {
+			float *base = kv ? M->d_vc : M->d_kc;
+			if (drop >= keep) {
+				LCHK(lm_launch_copy_rows(base + drop * M->HL, base, slab, keep * M->HL,
+							 slabs, M->stream), "kv rotate");
+			} else { /* overlapping: row blocks of `drop` rows, front to back */
+				for (size_t r = 0; r < keep; r += drop) {
+					size_t n = keep - r < drop ? keep - r : drop;
+					LCHK(lm_launch_copy_rows(base + (r + drop) * M->HL,
+								 base + r * M->HL, slab, n * M->HL,
+								 slabs, M->stream), "kv rotate");
+				}
+			}
+		}
+	}
+	M->st.size = (int)keep;
+	HIPCHK(hipMemcpyAsync(&M->d_st->size, &M->st.size, sizeof(int), hipMemcpyHostToDevice,
+			      M->stream), "set cache size");
+	/* the pageable source must stay put until the copy has been taken */
+	HIPCHK(hipStreamSynchronize(M->stream), "synchronize after rotate");
+	return 1;
+fail:
+	return 0;
+}
+
+/* one step on M->stream; head: also the lm_head product and the pick */
+static int enqueue_step(hip_lm *M, int head)
+{
+	const int wt = M->wtype, E = (int)M->E;
+	hipStream_t s = M->stream;
+	LCHK(lm_launch_embed(wt, M->d_wte, E, M->d_st, M->d_prompt, M->d_h0, s), "embed");
+	for (size_t l = 0; l < M->L; l++) {
+		struct lm_layer *y = &M->ly[l];
+		const size_t co = l * M->KH * M->C * M->HL;
+		/* h0 = h1 + moe_out (the previous layer's residual), x = rms_norm(h0) */
+		LCHK(lm_launch_add_rmsnorm(l ? M->d_h1 : M->d_h0, l ? M->d_moe_out : NULL, M->d_h0,
+					   y->attn_norm, M->d_x, E, s), "attn_norm");
+		LCHK(moe_launch_qgemv(wt, y->wqkv, (int)(M->EQ + 2 * M->EKV), E, M->d_x, 1, NULL, 0,
+				      M->d_qkv, M->grid_qkv, s), "q/k/v");
+		LCHK(lm_launch_qk_rope_kv(M->d_qkv, y->q_norm, y->k_norm, M->d_freq, M->d_st,
+					  M->d_kc + co, M->d_vc + co, (int)M->H, (int)M->KH,
+					  (int)M->HL, (int)M->C, s), "q/k norm, rope, cache row");
+		LCHK(lm_launch_attention(M->d_qkv, M->d_kc + co, M->d_vc + co, M->d_st, M->d_part,
+					 M->d_attn, (int)M->H, (int)M->KH, (int)M->C,
+					 (int)M->window, M->scale_div, s), "attention");
+		/* h1 = h0 + attn . Wo^T */
+		LCHK(moe_launch_qgemv(wt, y->wo, E, (int)M->EQ, M->d_attn, 1, M->d_h0, 0, M->d_h1,
+				      M->grid_o, s), "attn_output");
+		LCHK(lm_launch_add_rmsnorm(M->d_h1, NULL, NULL, y->ffn_norm, M->d_moe_in + l * M->E,
+					   E, s), "ffn_norm");
+		if (!hip_moe_ffn_dev(y->moe, M->d_moe_in + l * M->E, M->d_moe_out, 1, NULL,
+				     M->d_ids + l * M->K, M->d_w + l * M->K, s))
+			return 0;
+	}
+	LCHK(lm_launch_add_rmsnorm(M->d_h1, M->d_moe_out, M->d_h0, M->d_onorm, M->d_x, E, s),
+	     "output_norm");
+	if (head) {
+		LCHK(moe_launch_qgemv(wt, M->d_head, (int)M->V, E, M->d_x, 1, NULL, 0, M->d_logits,
+				      M->grid_head, s), "lm_head");
+		LCHK(lm_launch_argmax(M->d_logits, (int)M->V, M->d_st, M->d_tokens, s), "pick");
+	}
+	LCHK(lm_launch_step_end(M->d_st, s), "step end");
+	return 1;
+}
+
+/* the prompt and token buffers hold n ids; growing them drops the graphs
+ * (their nodes name the old buffers) */
+static int ensure_io(hip_lm *M, size_t n_prompt, size_t n_tokens)
+{
+	if (n_prompt > M->prompt_cap) {
+		drop_graphs(M);
+		hipFree(M->d_prompt);
+		M->d_prompt = NULL;
+		M->prompt_cap = 0;
+		HIPCHK(hipMalloc((void **)&M->d_prompt, n_prompt * sizeof(int)), "hipMalloc(prompt)");
+		M->prompt_cap = n_prompt;
+	}
+	if (n_tokens > M->tokens_cap) {
+		drop_graphs(M);
+		hipFree(M->d_tokens);
+		M->d_tokens = NULL;
+		M->tokens_cap = 0;
+		HIPCHK(hipMalloc((void **)&M->d_tokens, n_tokens * sizeof(int)), "hipMalloc(tokens)");
+		M->tokens_cap = n_tokens;
+	}
+	return 1;
+fail:
+	return 0;
+}
+
+/* set the device counters for a run of n_prompt prompt steps */
+static int start_run(hip_lm *M, const int *prompt, size_t n_prompt)
+{
+	/* earlier steps on the (non-blocking) stream read these buffers */
+	HIPCHK(hipStreamSynchronize(M->stream), "synchronize");
+	M->st.step = 0;
+	M->st.n_prompt = (int)n_prompt;
+	if (n_prompt)
+		HIPCHK(hipMemcpy(M->d_prompt, prompt, n_prompt * sizeof(int), hipMemcpyHostToDevice),
+		       "copy prompt");
+	HIPCHK(hipMemcpy(M->d_st, &M->st, sizeof(LmState), hipMemcpyHostToDevice), "set state");
+	return 1;
+fail:
+	return 0;
+}
+
+static void advance_host(hip_lm *M)
+{
+	M->st.step++;
+	M->st.pos++;
+	M->st.size++;
+}
+
+static int check_token(const hip_lm *M, int tok)
+{
+	if (tok < 0 || (size_t)tok >= M->V) {
+		lm_err("lm: token %d outside the vocabulary of %zu", tok, M->V);
+		return 0;
+	}
+	return 1;
+}
+
+int hip_lm_decode(hip_lm *M, int tok, float *logits, int *next)
+{
+	if (!M) {
+		lm_err("lm_decode: NULL model");
+		return 0;
+	}
+	if (!check_token(M, tok) || !ensure_io(M, 1, 1) || !rotate_if_full(M) ||
+	    !start_run(M, &tok, 1) || !enqueue_step(M, 1))
+		return 0;
+	advance_host(M);
+	HIPCHK(hipStreamSynchronize(M->stream), "synchronize");
+	for (size_t l = 0; l < M->L; l++) {
+		int rc = hip_moe_status(M->ly[l].moe, M->stream);
+		if (rc != 0) {
+			lm_err("lm_decode: layer %zu: MoE decode wait failed (%d)", l, rc);
+			return 0;
+		}
+	}
+	if (logits)
+		HIPCHK(hipMemcpy(logits, M->d_logits, M->V * 4, hipMemcpyDeviceToHost), "copy logits");
+	if (next) {
+		LmState st;
+		HIPCHK(hipMemcpy(&st, M->d_st, sizeof(st), hipMemcpyDeviceToHost), "read state");
+		*next = st.tok;
+	}
+	return 1;
+fail:
+	return 0;
+}
+
+static int capture(hip_lm *M, int head, hipGraphExec_t *out)
+{
+	hipGraph_t g = NULL;
+	HIPCHK(hipStreamBeginCapture(M->stream, hipStreamCaptureModeThreadLocal), "begin capture");
+	if (!enqueue_step(M, head)) {
+		hipStreamEndCapture(M->stream, &g);
+		if (g)
+			hipGraphDestroy(g);
+		return 0;
+	}
+	HIPCHK(hipStreamEndCapture(M->stream, &g), "end capture");
+	HIPCHK(hipGraphInstantiate(out, g, NULL, NULL, 0), "instantiate step graph");
+	hipGraphDestroy(g);
+	return 1;
+fail:
+	if (g)
+		hipGraphDestroy(g);
+	return 0;
+}
+
+int hip_lm_generate(hip_lm *M, const int *prompt, size_t n_prompt, size_t n_gen, int *tokens,
+		    float *decode_ms)
+{
+	if (!M || !prompt || !tokens || n_prompt == 0) {
+		lm_err("lm_generate: NULL argument or empty prompt");
+		return 0;
+	}
+	for (size_t i = 0; i < n_prompt; i++)
+		if (!check_token(M, prompt[i]))
+			return 0;
+	const size_t steps = n_prompt + n_gen;
+	if (steps > 0x7fffffff) {
+		lm_err("lm_generate: too many steps");
+		return 0;
+	}
+	if (!ensure_io(M, n_prompt, steps) || !start_run(M, prompt, n_prompt))
+		return 0;
+	if (!M->g_body && !capture(M, 0, &M->g_body))
+		return 0;
+	if (!M->g_head && !capture(M, 1, &M->g_head))
+		return 0;
+	for (size_t i = 0; i < steps; i++) {
+		if (!rotate_if_full(M))
+			return 0;
+		if (i == n_prompt)
+			HIPCHK(hipEventRecord(M->ev0, M->stream), "event");
+		/* prompt steps before the last need no lm_head */
+		HIPCHK(hipGraphLaunch(i + 1 < n_prompt ? M->g_body : M->g_head, M->stream),
+		       "step graph");
+		advance_host(M);
+	}
+	HIPCHK(hipEventRecord(M->ev1, M->stream), "event");
+	HIPCHK(hipStreamSynchronize(M->stream), "synchronize");
+	for (size_t l = 0; l < M->L; l++) {
+		int rc = hip_moe_status(M->ly[l].moe, M->stream);
+		if (rc != 0) {
+			lm_err("lm_generate: layer %zu: MoE decode wait failed (%d)", l, rc);
+			return 0;
+		}
+	}
+	if (decode_ms) {
+		*decode_ms = 0.0f;
+		if (n_gen)
+			HIPCHK(hipEventElapsedTime(decode_ms, M->ev0, M->ev1), "event time");
+	}
+	HIPCHK(hipMemcpy(tokens, M->d_tokens + (n_prompt - 1), (n_gen + 1) * sizeof(int),
+			 hipMemcpyDeviceToHost), "copy tokens");
+	return 1;
+fail:
+	return 0;
+}
+
+int hip_lm_trace(hip_lm *M, float *moe_in, uint32_t *ids, float *w)
+{
+	if (!M) {
+		lm_err("lm_trace: NULL model");
+		return 0;
+	}
+	HIPCHK(hipStreamSynchronize(M->stream), "synchronize");
+	if (moe_in)
+		HIPCHK(hipMemcpy(moe_in, M->d_moe_in, M->L * M->E * 4, hipMemcpyDeviceToHost),
+		       "copy moe_in");
+	if (ids)
+		HIPCHK(hipMemcpy(ids, M->d_ids, M->L * M->K * 4, hipMemcpyDeviceToHost), "copy ids");
+	if (w)
+		HIPCHK(hipMemcpy(w, M->d_w, M->L * M->K * 4, hipMemcpyDeviceToHost), "copy w");
+	return 1;
+fail:
+	return 0;
+}
+
+int hip_lm_reset(hip_lm *M)
+{
+	if (!M) {
+		lm_err("lm_reset: NULL model");
+		return 0;
+	}
+	const size_t cache = M->L * M->KH * M->C * M->HL * sizeof(float);
+	HIPCHK(hipStreamSynchronize(M->stream), "synchronize");
+	HIPCHK(hipMemset(M->d_kc, 0, cache), "clear k cache");
+	HIPCHK(hipMemset(M->d_vc, 0, cache), "clear v cache");
+	memset(&M->st, 0, sizeof(M->st));
+	HIPCHK(hipMemcpy(M->d_st, &M->st, sizeof(LmState), hipMemcpyHostToDevice), "clear state");
+	HIPCHK(hipDeviceSynchronize(), "synchronize");
+	return 1;
+fail:
+	return 0;
+}

@@ -81,6 +81,11 @@ const char *hip_moe_last_error(void)
 	return g_err;
 }
 
+void moe_set_error(const char *msg)
+{
+	set_err("%s", msg);
+}
+
 #define HIPCHK(call, what)                                                        \
 	do {                                                                      \
 		hipError_t e_ = (call);                                           \

@@ -106,6 +106,9 @@ int moe_launch_fused(int wtype, const float *x, const float *router, const float
                      uint64_t *part, float *out, uint32_t *sync, int T, int E, int EI, int NE,
                      int K, int renorm, int grid, int spin, void *stream);
 
+/* Record an error message for hip_moe_last_error (and print it). */
+void moe_set_error(const char *msg);
+
 /* Static device scratch of the allocation-free decode entry point
  * (moe_decode.hip): MOE_STATIC_SCRATCH_BYTES per device, looked up and
  * cleared once per device by moe_static_scratch_setup (with that device

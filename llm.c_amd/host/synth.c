@@ -273,3 +273,4 @@ uint64_t moe_stream_gate(uint64_t layer, uint64_t e) { return (layer << 32) | (0
 uint64_t moe_stream_up(uint64_t layer, uint64_t e) { return (layer << 32) | (0x20000u + e); }
 uint64_t moe_stream_down(uint64_t layer, uint64_t e) { return (layer << 32) | (0x30000u + e); }
 uint64_t moe_stream_input(uint64_t call) { return 0xa0000000u + call; }
+uint64_t moe_stream_tensor(uint64_t layer, uint64_t kind) { return (layer << 32) | (0x400u + kind); }

@@ -89,6 +89,11 @@ static float dot_f32(const float *x, const float *y, size_t n)
 	return sum;
 }
 
+float orc_dot_f32(const float *x, const float *y, size_t n)
+{
+	return dot_f32(x, y, n);
+}
+
 void orc_router(const float *x, const float *wr, const float *bias,
 		size_t T, size_t E, size_t NE, float *logits)
 {

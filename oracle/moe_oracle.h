@@ -32,6 +32,10 @@ extern "C" {
 void orc_router(const float *x, const float *wr, const float *bias,
                 size_t T, size_t E, size_t NE, float *logits);
 
+/* dot_f32_f32 (matmul.c:91-105): 8 FMA lane chains, the lane tree, an FMA
+ * scalar tail. */
+float orc_dot_f32(const float *x, const float *y, size_t n);
+
 /* In-place softmax over n values (nn.c:221-262, tensor.c:479-517). */
 void orc_softmax_1d(float *row, size_t n);
 
@@ -74,6 +78,37 @@ void orc_expf_array(const float *in, float *out, size_t n);
 
 /* glibc expf of every float whose bit pattern lies in [bits0, bits0+n). */
 void orc_expf_bits(uint32_t bits0, size_t n, float *out, int nthreads);
+
+/*
+ * The OLMoE model (models/olmoe/olmoe.c) in decode mode, one token per
+ * call: embedding (tensor_pick_rows tensor.c:263-294), per layer RMSNorm
+ * (nn.c:8-51), q/k/v products, full-vector q/k RMSNorm, RoPE (nn.c:192-219),
+ * attention over the fp32 KV cache (olmoe.c:214-341, kvcache.c), output
+ * product and residual, RMSNorm, moe_ffn (olmoe.c:343-407), residual; the
+ * final RMSNorm and the lm_head product (olmoe.c:497-501,558-564).
+ * ptrs: 3 + 12 * layers pointers, token_embd, output, output_norm, then per
+ * layer attn_norm, attn_q, attn_k, attn_v, attn_q_norm, attn_k_norm,
+ * attn_output, ffn_norm, ffn_gate_inp, ffn_gate_exps, ffn_up_exps,
+ * ffn_down_exps (quantized in wtype blocks; norms and router fp32).
+ */
+typedef struct orc_olmoe orc_olmoe;
+
+orc_olmoe *orc_olmoe_new(size_t layers, size_t E, size_t H, size_t V, size_t NE, size_t topk,
+                         size_t EI, size_t C, float theta, int wtype, const void *const *ptrs);
+
+/* olmoe_decode (olmoe.c:509-520) of token tok at position pos, then the
+ * lm_head product into logits[V] (optional).  Optional traces per layer:
+ * moe_in [layers][E] (the router's input), ids/w [layers][topk].
+ * Returns the greedy pick (main.c:189-193: first maximum). */
+int orc_olmoe_decode(orc_olmoe *m, int tok, int pos, float *logits, float *trace_moe_in,
+                     uint32_t *trace_ids, float *trace_w, int nthreads);
+
+/* The prompt token by token, then n_gen greedy steps (the model's own
+ * position counter advances): tokens[0..n_gen], logits [n_gen+1][V]. */
+void orc_olmoe_run(orc_olmoe *m, const int *prompt, size_t n_prompt, size_t n_gen,
+                   float *logits, int *tokens, int nthreads);
+
+void orc_olmoe_free(orc_olmoe *m);
 
 #ifdef __cplusplus
 }

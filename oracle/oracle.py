@@ -45,6 +45,16 @@ def lib():
         L.orc_expf_array.restype = None
         L.orc_expf_bits.argtypes = [C.c_uint32, sz, vp, i32]
         L.orc_expf_bits.restype = None
+        L.orc_dot_f32.argtypes = [vp, vp, sz]
+        L.orc_dot_f32.restype = C.c_float
+        L.orc_olmoe_new.argtypes = [sz, sz, sz, sz, sz, sz, sz, sz, C.c_float, i32, vp]
+        L.orc_olmoe_new.restype = vp
+        L.orc_olmoe_decode.argtypes = [vp, i32, i32, vp, vp, vp, vp, i32]
+        L.orc_olmoe_decode.restype = i32
+        L.orc_olmoe_run.argtypes = [vp, vp, sz, sz, vp, vp, i32]
+        L.orc_olmoe_run.restype = None
+        L.orc_olmoe_free.argtypes = [vp]
+        L.orc_olmoe_free.restype = None
         _lib = L
     return _lib
 
@@ -152,3 +162,48 @@ def expf_bits(bits0: int, n: int, nthreads=None):
     out = np.empty(n, np.float32)
     lib().orc_expf_bits(bits0, n, _p(out), nthreads or threads())
     return out
+
+
+class OlmoeModel:
+    """The OLMoE decode step of the reference (orc_olmoe_*): md is a model
+    dict of llm.c_amd/hiplm.py (synth_olmoe), C the context length."""
+
+    def __init__(self, md: dict, C_ctx: int, table):
+        self.md = md
+        self.V, self.E, self.L, self.K = md["V"], md["E"], md["layers"], md["K"]
+        self.table = table  # keeps the pointer table alive
+        self.h = lib().orc_olmoe_new(md["layers"], md["E"], md["H"], md["V"], md["NE"], md["K"],
+                                     md["EI"], C_ctx, md["theta"], md["wtype"], table)
+        self.pos = 0
+
+    def decode(self, tok: int, trace: bool = False):
+        """(greedy pick, logits [V]) and, with trace, (moe_in [L][E], ids [L][K], w [L][K])."""
+        lg = np.empty(self.V, np.float32)
+        mi = np.empty((self.L, self.E), np.float32) if trace else None
+        ids = np.empty((self.L, self.K), np.uint32) if trace else None
+        w = np.empty((self.L, self.K), np.float32) if trace else None
+        nxt = lib().orc_olmoe_decode(self.h, int(tok), self.pos, _p(lg), _p(mi), _p(ids), _p(w),
+                                     threads())
+        self.pos += 1
+        return (nxt, lg, (mi, ids, w)) if trace else (nxt, lg)
+
+    def run(self, prompt, n_gen: int):
+        """The prompt token by token then n_gen greedy steps: (tokens [n_gen+1],
+        logits [n_gen+1][V])."""
+        pr = np.ascontiguousarray(prompt, np.int32)
+        lg = np.empty((n_gen + 1, self.V), np.float32)
+        toks = np.empty(n_gen + 1, np.int32)
+        lib().orc_olmoe_run(self.h, _p(pr), pr.size, n_gen, _p(lg), _p(toks), threads())
+        self.pos += pr.size + n_gen
+        return toks, lg
+
+    def free(self):
+        if self.h:
+            lib().orc_olmoe_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

@@ -120,3 +120,24 @@ def qmat_case(i: int, name: str):
     assert sha(q) == str(g[f"{name}_sha_w"]) and sha(x) == str(g[f"{name}_sha_x"])
     assert (sha(a) if a is not None else "") == str(g[f"{name}_sha_add"])
     return wt, T, N, K, q, x, a, g[f"{name}_out"]
+
+
+def _make_golden_module():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("make_golden",
+                                                  os.path.join(GOLDEN, "make_golden.py"))
+    mg = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mg)
+    return mg
+
+
+@functools.lru_cache(maxsize=1)
+def model_case(name: str):
+    """(model dict, prompt, case tuple, fixture) of model fixture `name`,
+    after checking the regenerated weights are the fixture's bytes."""
+    mg = _make_golden_module()
+    md, prompt, case = mg.model_case(name)
+    g = golden(f"model_{name}.npz")
+    assert np.array_equal(prompt, g["prompt"])
+    assert mg.model_digest(md) == str(g["sha_model"]), "regenerated model differs from fixture"
+    return md, prompt, case, g

@@ -24,8 +24,13 @@ same bytes.  Outputs are the reference's own results:
                      argument of tensor_mma_transposed_2x2)
   qmat.npz           tensor_mma_transposed_2x2 with a Q8_0/Q4_0 right operand
                      (matmul.c:13-33,285-312) for T = 1..9, add NULL/[N]/[T][N]
+  model_<case>.npz   the whole OLMoE model (olmoe.c:409-580): greedy tokens
+                     and per-step logits of the reference's olmoe_decode run
+                     over the prompt then n_gen steps, and of its generate
+                     order (one olmoe_prefill of the prompt, then decode)
 
-`python tests/golden/make_golden.py qmat` writes qmat.npz alone.
+`python tests/golden/make_golden.py qmat` writes qmat.npz alone, `... model`
+the model fixtures alone.
 """
 from __future__ import annotations
 
@@ -127,10 +132,73 @@ def qmat_goldens(R):
     np.savez(os.path.join(HERE, "qmat.npz"), seed=SEED, **fx)
 
 
+# name: (layers, E, H, V, NE, K, EI, C, wtype, norm_std, n_prompt, n_gen, logit stride)
+# The small case runs past its context (48 positions, C = 32: one
+# kvcache_rotate) with non-unit norms; the full case is the OLMoE-1B-7B shape
+# with unit norms, its logits kept at every 16th id plus each step's top 32.
+MODEL_CASES = {
+    "olmoe_small": (2, 1024, 8, 512, 64, 8, 512, 32, hipmoe.Q8_0, 0.1, 8, 40, 1),
+    "olmoe_full": (16, 2048, 16, 50304, 64, 8, 1024, 2048, hipmoe.Q8_0, 0.0, 4, 4, 16),
+}
+MODEL_TOPN = 32
+
+
+def model_case(name: str):
+    """(model dict, prompt, case tuple) of a MODEL_CASES entry, regenerated
+    from the seed."""
+    import hiplm
+    L, E, H, V, NE, K, EI, Cx, wt, nstd, n_prompt, n_gen, stride = MODEL_CASES[name]
+    md = hiplm.synth_olmoe(SEED, L, E, H, V, NE, K, EI, wt, 0.02, nstd)
+    prompt = hiplm.synth_prompt(SEED, n_prompt, V)
+    return md, prompt, MODEL_CASES[name]
+
+
+def model_digest(md: dict) -> str:
+    h = hashlib.sha256()
+    for k in ("token_embd", "output", "output_norm"):
+        h.update(md[k].tobytes())
+    for b in md["blk"]:
+        for k in ("attn_norm", "q", "k", "v", "q_norm", "k_norm", "o", "ffn_norm", "router",
+                  "gate", "up", "down"):
+            h.update(np.ascontiguousarray(b[k]).tobytes())
+    return h.hexdigest()
+
+
+def model_goldens(R, names):
+    import hiplm
+    vp, sz, i32 = C.c_void_p, C.c_size_t, C.c_int
+    R.ref_olmoe_model_new.argtypes = [sz, sz, sz, sz, sz, sz, sz, sz, C.c_float, i32, vp]
+    R.ref_olmoe_model_new.restype = vp
+    R.ref_olmoe_model_run.argtypes = [vp, vp, sz, i32, sz, vp, vp]
+    R.ref_olmoe_model_free.argtypes = [vp]
+    for name in names:
+        md, prompt, case = model_case(name)
+        L, E, H, V, NE, K, EI, Cx, wt, nstd, n_prompt, n_gen, stride = case
+        tab = hiplm.ptr_table(md)
+        fx = dict(seed=SEED, prompt=prompt, sha_model=model_digest(md), stride=stride)
+        for mode, prefill in (("dec", 0), ("pre", 1)):
+            h = R.ref_olmoe_model_new(L, E, H, V, NE, K, EI, Cx, md["theta"], wt, tab)
+            lg = np.empty((n_gen + 1, V), np.float32)
+            toks = np.empty(n_gen + 1, np.int32)
+            R.ref_olmoe_model_run(h, p(prompt), n_prompt, prefill, n_gen, p(lg), p(toks))
+            R.ref_olmoe_model_free(h)
+            top = np.argsort(-lg, axis=1, kind="stable")[:, :MODEL_TOPN].astype(np.int32)
+            fx[f"{mode}_tokens"] = toks
+            fx[f"{mode}_logits"] = np.ascontiguousarray(lg[:, ::stride])
+            fx[f"{mode}_top_ids"] = top
+            fx[f"{mode}_top_logits"] = np.take_along_axis(lg, top, axis=1)
+            print(f"model {name} [{mode}]: tokens {toks.tolist()}")
+        np.savez_compressed(os.path.join(HERE, f"model_{name}.npz"), **fx)
+        del md
+
+
 def main():
     if not os.path.exists(REF_LIB):
         sys.exit(f"{REF_LIB} missing: run oracle/ref/build_ref.sh first")
     R = ref()
+    if sys.argv[1:2] == ["model"]:
+        model_goldens(R, sys.argv[2:] or list(MODEL_CASES))
+        return
     qmat_goldens(R)
     if sys.argv[1:] == ["qmat"]:
         return

@@ -16,10 +16,10 @@ def declared_functions(header: str):
     text = open(os.path.join(REPO, "include", header)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     names = re.findall(r"\b([a-z_][a-z0-9_]*)\s*\(", text)
-    return sorted({n for n in names if n.startswith(("hip_moe_", "moe_"))})
+    return sorted({n for n in names if n.startswith(("hip_moe_", "moe_", "hip_lm_"))})
 
 
-@pytest.mark.parametrize("header", ["hip_moe.h", "moe_synth.h"])
+@pytest.mark.parametrize("header", ["hip_moe.h", "moe_synth.h", "hip_lm.h"])
 def test_library_exports_every_declared_symbol(header):
     L = hipmoe.lib()
     names = declared_functions(header)
@@ -117,3 +117,32 @@ def test_qmat_calls_on_null_return_zero():
     assert L.hip_moe_qmat_mul_dev(None, 1, 1, None, 0, 1, None) == 0
     assert L.hip_moe_qmat_bytes(None) == 0
     L.hip_moe_qmat_free(None)
+
+
+def test_lm_calls_on_null_return_zero():
+    import hiplm
+    L = hiplm._bind()
+    assert not L.hip_lm_upload(None)
+    assert "NULL descriptor" in hipmoe.last_error()
+    assert L.hip_lm_decode(None, 0, None, None) == 0
+    assert L.hip_lm_generate(None, None, 0, 0, None, None) == 0
+    assert L.hip_lm_trace(None, None, None, None) == 0
+    assert L.hip_lm_reset(None) == 0
+    assert L.hip_lm_weight_bytes(None) == 0
+    L.hip_lm_free(None)
+
+
+def test_lm_upload_rejects_bad_descriptors():
+    import hiplm
+    L = hiplm._bind()
+    d = hiplm.Desc()
+    d.arch = 7
+    assert not L.hip_lm_upload(C.byref(d))
+    assert "unknown arch" in hipmoe.last_error()
+    d.arch, d.wtype = hiplm.ARCH_OLMOE, 1
+    d.layers, d.E, d.heads, d.kv_heads, d.vocab, d.context = 2, 1024, 4, 4, 10, 8
+    assert not L.hip_lm_upload(C.byref(d))
+    assert "heads * 128 == E" in hipmoe.last_error()
+    d.heads = d.kv_heads = 8
+    assert not L.hip_lm_upload(C.byref(d))
+    assert "NULL tensor pointer" in hipmoe.last_error()

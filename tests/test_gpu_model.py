@@ -1,0 +1,103 @@
+"""GPU parity of the whole-model decode (include/hip_lm.h) through the C ABI,
+against the compiled reference's own OLMoE decode (tests/golden/model_*.npz,
+to which the model oracle is pinned bit for bit) and the oracle:
+
+  * teacher-forced steps (the prompt, then the reference's own picks as
+    inputs): every step's logits within 1e-3 relative L2 of the
+    reference's (fp32 dots in another order land near 1e-6, held to 2e-5
+    on the reduced model), the greedy pick equal wherever the reference's
+    top two logits are apart;
+  * routing bit-exact in every layer: the ids and weights each layer's MoE
+    took equal the oracle's routing of that layer's own router input;
+  * generate (device-side greedy loop on replayed step graphs) gives the
+    reference's tokens;
+  * the reduced model runs past its context (one kvcache_rotate); the
+    full OLMoE-1B-7B shape (16 layers, vocab 50304) checks the stored
+    logits (every 16th id and each step's top 32).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import hiplm
+import oracle
+from common import bits, model_case, rel_l2
+
+pytestmark = pytest.mark.gpu
+TIGHT = 2e-5
+
+
+def say(msg):
+    print(f"[gpu-test] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def need_gpu():
+    import hipmoe
+    assert hipmoe.hip().device_count() >= 1, "no HIP device visible: GPU tests need an MI355X"
+
+
+def safe_steps(top_logits):
+    """Steps whose top-two reference logits differ by more than 1e-4 relative:
+    there the greedy pick must agree."""
+    t = np.asarray(top_logits, np.float64)
+    return np.abs(t[:, 0] - t[:, 1]) > 1e-4 * np.abs(t[:, 0])
+
+
+def check_routing(md, case, M):
+    L, E, H, V, NE, K, EI, Cx, wt, nstd, n_prompt, n_gen, stride = case
+    mi, ids, w = M.trace()
+    for l in range(L):
+        b = md["blk"][l]
+        lay = dict(router=b["router"], gate=b["gate"], up=b["up"], down=b["down"], wtype=wt,
+                   E=E, EI=EI, NE=NE)
+        oi, ow = oracle.moe_ffn(mi[l:l + 1], lay, K, False, None)[1:3]
+        assert np.array_equal(ids[l], oi[0]), f"layer {l}: ids"
+        assert np.array_equal(bits(w[l]), bits(ow[0])), f"layer {l}: weights"
+
+
+def teacher_forced(name, tol, route_steps=()):
+    md, prompt, case, g = model_case(name)
+    L, E, H, V, NE, K, EI, Cx, wt, nstd, n_prompt, n_gen, stride = case
+    say(f"{name}: upload ({L} layers, E={E}, vocab {V}, context {Cx})")
+    M = hiplm.LmModel(md, Cx)
+    try:
+        seq = list(prompt) + list(g["dec_tokens"][:-1])
+        safe = safe_steps(g["dec_top_logits"])
+        worst = 0.0
+        for i, tok in enumerate(seq):
+            nxt, lg = M.decode(int(tok))
+            s = i - (n_prompt - 1)
+            if i in route_steps:
+                check_routing(md, case, M)
+            if s < 0:
+                continue
+            err = rel_l2(lg[::stride], g["dec_logits"][s])
+            top = lg[g["dec_top_ids"][s]]
+            err_top = rel_l2(top, g["dec_top_logits"][s])
+            worst = max(worst, err, err_top)
+            assert err <= tol and err_top <= tol, f"step {s}: rel L2 {err:.3e} / {err_top:.3e}"
+            if safe[s]:
+                assert nxt == int(g["dec_tokens"][s]), f"step {s}: pick {nxt}"
+        say(f"{name}: {len(seq)} teacher-forced steps, worst logit rel L2 {worst:.3e}")
+        # the device-side greedy loop from a fresh cache
+        M.reset()
+        toks, ms = M.generate(prompt, n_gen)
+        bad = np.nonzero(~safe)[0]
+        upto = int(bad[0]) + 1 if bad.size else n_gen + 1
+        assert np.array_equal(toks[:upto], g["dec_tokens"][:upto]), (toks, g["dec_tokens"])
+        say(f"{name}: generate {n_gen} steps: tokens equal the reference's "
+            f"({upto} checked), {ms:.2f} ms")
+    finally:
+        M.free()
+
+
+def test_gpu_model_small_vs_reference():
+    teacher_forced("olmoe_small", TIGHT, route_steps=(0, 7, 20, 40))
+
+
+@pytest.mark.timeout(900)
+def test_gpu_model_full_shape_vs_reference():
+    teacher_forced("olmoe_full", 1e-3, route_steps=(3, 7))

@@ -1,0 +1,67 @@
+"""Pins the model oracle (oracle/lm_oracle.c: the OLMoE decode step around
+the MoE oracle) against the compiled reference before it is trusted as the
+checker of the GPU model: per-step logits and greedy tokens of the
+reference's own olmoe_decode (driven by oracle/ref/ref_olmoe.c over seeded
+weights, tests/golden/model_*.npz) bit for bit, on a reduced model with
+non-unit norms that runs past its context (one kvcache_rotate), and at the
+full OLMoE shape; and the reference's generate order (one olmoe_prefill of
+the prompt) within fp32 rounding."""
+import numpy as np
+import pytest
+
+import hiplm
+import oracle
+from common import bits, model_case, rel_l2
+
+
+def _run(name):
+    md, prompt, case, g = model_case(name)
+    L, E, H, V, NE, K, EI, Cx, wt, nstd, n_prompt, n_gen, stride = case
+    tab = hiplm.ptr_table(md)
+    m = oracle.OlmoeModel(md, Cx, tab)
+    try:
+        toks, lg = m.run(prompt, n_gen)
+    finally:
+        m.free()
+    return toks, lg, g, stride
+
+
+def test_model_oracle_matches_reference_decode_bits_small():
+    toks, lg, g, stride = _run("olmoe_small")
+    assert np.array_equal(toks, g["dec_tokens"])
+    assert np.array_equal(bits(lg[:, ::stride]), bits(g["dec_logits"]))
+    # the reference's own generate (prefill of the prompt) lands within fp32 rounding
+    assert np.array_equal(toks, g["pre_tokens"])
+    for s in range(lg.shape[0]):
+        assert rel_l2(lg[s], g["pre_logits"][s]) <= 1e-5
+
+
+@pytest.mark.slow
+def test_model_oracle_matches_reference_decode_bits_full_shape():
+    toks, lg, g, stride = _run("olmoe_full")
+    assert np.array_equal(toks, g["dec_tokens"])
+    assert np.array_equal(bits(lg[:, ::stride]), bits(g["dec_logits"]))
+    top = np.take_along_axis(lg, g["dec_top_ids"].astype(np.int64), axis=1)
+    assert np.array_equal(bits(top), bits(g["dec_top_logits"]))
+    for s in range(lg.shape[0]):
+        assert rel_l2(lg[s, ::stride], g["pre_logits"][s]) <= 1e-5
+
+
+def test_model_oracle_routing_trace_is_the_layer_oracle():
+    """The per-layer routing the model oracle reports is the MoE oracle's
+    routing of the reported router input (a trace the GPU test relies on)."""
+    md, prompt, case, g = model_case("olmoe_small")
+    L, E, H, V, NE, K, EI, Cx, wt, nstd, n_prompt, n_gen, stride = case
+    tab = hiplm.ptr_table(md)
+    m = oracle.OlmoeModel(md, Cx, tab)
+    try:
+        for t in prompt[:3]:
+            nxt, lg, (mi, ids, w) = m.decode(int(t), trace=True)
+            for l in range(L):
+                b = md["blk"][l]
+                lay = dict(router=b["router"], gate=b["gate"], up=b["up"], down=b["down"],
+                           wtype=wt, E=E, EI=EI, NE=NE)
+                _, oids, ow, _, _ = oracle.moe_ffn(mi[l:l + 1], lay, K, False, None)
+                assert np.array_equal(ids[l], oids[0]) and np.array_equal(bits(w[l]), bits(ow[0]))
+    finally:
+        m.free()
