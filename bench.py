@@ -18,6 +18,17 @@ The `*_lm_head` workloads time the dense quantized product instead
 Q4_0 matrix, here the lm_head of each model for one token), rotating over
 `--layers` copies of the matrix in the same way.
 
+`olmoe_full_decode` times the whole OLMoE-1B-7B-shaped model (hip_lm.h: 16
+layers, d_model 2048, 16 heads of 128, 64 experts top-8 d_ff 1024, vocab
+50304, Q8_0 weights N(0, 0.02), unit norms, fp32 KV cache of context 2048)
+decoding greedily after a 16-token random-id prompt: a step is one
+generated token, the whole step (embedding to greedy pick) replayed from a
+captured HIP graph with the token fed back on the device.
+
+The CPU baseline runs in a process of its own (oracle/cpu_baseline.py): the
+oracle with the reference's threading on this host's cores, after the GPU
+measurement.
+
 Prints one JSON line on stdout (progress goes to stderr).
 """
 import argparse
@@ -51,7 +62,11 @@ WORKLOADS = {
     # dense quantized products: N rows of K columns, T tokens
     "olmoe_q8_lm_head": dict(kind="qmat", wtype=hipmoe.Q8_0, N=50304, Kc=2048, T=1),
     "mixtral_q4_lm_head": dict(kind="qmat", wtype=hipmoe.Q4_0, N=32000, Kc=4096, T=1),
+    # the whole model, one generated token per step
+    "olmoe_full_decode": dict(kind="model", wtype=hipmoe.Q8_0, layers=16, E=2048, H=16,
+                              V=50304, NE=64, K=8, EI=1024, C=2048, prompt=16),
 }
+MODEL_METRIC = "OLMoE-shaped full-model decode tok/s & % of HBM roofline"
 
 
 def log(msg):
@@ -63,29 +78,22 @@ def expert_bytes(w):
         w["E"] * hipmoe.row_bytes(w["wtype"], w["EI"])
 
 
-def cpu_baseline(lw, w, xs, seconds):
-    """The oracle (a C restatement of the reference's AVX2 CPU path) on this
-    host, one thread: the reference runs the OLMoE router (T < 64) and the
-    expert FFN (2*2048*1024 flops < 16 Mi, thread_pool.c:25,178-185) on one
-    thread.  Bounded by `seconds`."""
-    sys.path.insert(0, os.path.join(REPO, "oracle"))
-    import oracle
-    T = w["T"]
-    sample_T = min(T, 8)
-    done_tokens = 0
-    t0 = time.perf_counter()
-    i = 0
-    while True:
-        x = xs[i % len(xs)][:sample_T]
-        oracle.moe_ffn(x, lw, w["K"], bool(w["renorm"]), lw["bias"], nthreads=1)
-        done_tokens += sample_T
-        i += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return dict(value=done_tokens / el, unit="tokens/s", cores=1, kind="port",
-                sample=f"{done_tokens} tokens in {i} layer calls of {sample_T} token(s), "
-                       f"{el:.1f} s, 1 thread, oracle/moe_oracle.c built -O3 -mavx2 -mfma")
+def cpu_baseline(w, seconds):
+    """The oracle (a C restatement of the reference's AVX2 CPU path) timed on
+    this host's cores with the reference's threading, in a process of its
+    own (oracle/cpu_baseline.py), over a bounded sample of `seconds`."""
+    import subprocess
+    spec = {k: v for k, v in w.items()}
+    spec.setdefault("kind", "moe")
+    if spec["kind"] == "model":
+        spec["gen"] = 256
+    cmd = [sys.executable, os.path.join(REPO, "oracle", "cpu_baseline.py"),
+           "--spec", json.dumps(spec), "--seconds", str(seconds)]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600 + 4 * seconds)
+    if r.returncode != 0:
+        log(f"cpu baseline failed ({r.returncode}): {r.stderr.strip()[-400:]}")
+        return None
+    return json.loads(r.stdout.strip().splitlines()[-1])
 
 
 def traffic_bytes(kernel, workload):
@@ -171,20 +179,10 @@ def bench_qmat(args, w, H):
 
     cpu = None
     if not args.no_cpu_baseline:
-        sys.path.insert(0, os.path.join(REPO, "oracle"))
-        import oracle
-        done, i, t0 = 0, 0, time.perf_counter()
-        while True:
-            oracle.qmat_mul(xs[i % ntok], q, wt, N, Kc)
-            done += T
-            i += 1
-            el = time.perf_counter() - t0
-            if el >= args.cpu_seconds:
-                break
-        cpu = dict(value=done / el, unit="tokens/s", cores=1, kind="port",
-                   sample=f"{done} tokens in {i} calls, {el:.1f} s, 1 thread, "
-                          f"oracle/moe_oracle.c orc_qmat_mul built -O3 -mavx2 -mfma")
-        log(f"cpu baseline: {cpu['value']:.2f} tokens/s")
+        log(f"cpu baseline ({args.cpu_seconds:.0f} s, own process)")
+        cpu = cpu_baseline(w, args.cpu_seconds)
+        if cpu:
+            log(f"cpu baseline: {cpu['value']:.2f} tokens/s on {cpu['cores']} threads")
     line = {
         "metric": QMAT_METRIC, "value": round(tokens_per_s, 2), "unit": "tokens/s",
         "n_gpus": 1, "steps": steps, "warmup": args.warmup,
@@ -198,6 +196,76 @@ def bench_qmat(args, w, H):
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic_bytes("k_qgemv", args.workload)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def bench_model(args, w, H):
+    """The whole model: `--steps` greedy tokens after the prompt, every step
+    from a replayed graph, timed with HIP events on the model's stream (by
+    hip_lm_generate).  Algorithmic bytes per token: per layer the q/k/v and
+    output matrices, the router, the unique experts the token's routing
+    picked and the KV rows attention reads (k and v, 4 bytes, at the step's
+    cache length); then the lm_head and one embedding row."""
+    import hiplm
+    wt, Lh, E, V, NE, K, EI, Cx = (w["wtype"], w["layers"], w["E"], w["V"], w["NE"], w["K"],
+                                   w["EI"], w["C"])
+    t0 = time.perf_counter()
+    md = hiplm.synth_olmoe(SEED, Lh, E, w["H"], V, NE, K, EI, wt)
+    prompt = hiplm.synth_prompt(SEED, w["prompt"], V)
+    log(f"generated the model in {time.perf_counter() - t0:.1f} s")
+    M = hiplm.LmModel(md, Cx)
+    log(f"uploaded ({M.weight_bytes() / 1e9:.2f} GB on the device)")
+    steps, warm = args.steps, max(1, args.warmup)
+    if w["prompt"] + steps + 1 > Cx:
+        sys.exit(f"--steps {steps} runs past the context {Cx}")
+    # unique experts per layer and step, from eager steps' routing traces
+    uniq = []
+    tok = 0
+    for i, t in enumerate(list(prompt) + [None] * 8):
+        tok, _ = M.decode(int(t) if t is not None else tok)
+        if t is None:
+            uniq.append(np.mean([len(np.unique(r)) for r in M.trace()[1]]))
+    mean_uniq = float(np.mean(uniq))
+    M.reset()
+    M.generate(prompt, warm)  # captures the step graphs
+    M.reset()
+    toks, ms = M.generate(prompt, steps)
+    ms_per_step = ms / steps
+    tokens_per_s = steps / (ms / 1e3)
+    bpw = 34 / 32 if wt == hipmoe.Q8_0 else 18 / 32
+    expert = 3 * E * EI * bpw
+    attn_w = 4 * E * E * bpw
+    kv_rows = np.mean([w["prompt"] + s + 1 for s in range(1, steps + 1)])
+    per_layer = attn_w + NE * E * 4 + mean_uniq * expert + 2 * kv_rows * E * 4
+    bytes_per_tok = Lh * per_layer + V * E * bpw + E * bpw
+    achieved_gbs = bytes_per_tok / (ms_per_step / 1e3) / 1e9
+    log(f"{steps} tokens in {ms:.2f} ms: {ms_per_step * 1e3:.1f} us/token, "
+        f"{tokens_per_s:.1f} tokens/s, {achieved_gbs:.1f} GB/s algorithmic "
+        f"({bytes_per_tok / 1e9:.3f} GB/token)")
+    M.free()
+    cpu = None
+    if not args.no_cpu_baseline:
+        log(f"cpu baseline ({args.cpu_seconds:.0f} s, own process)")
+        cpu = cpu_baseline(w, args.cpu_seconds)
+        if cpu:
+            log(f"cpu baseline: {cpu['value']:.2f} tokens/s on {cpu['cores']} threads")
+    line = {
+        "metric": MODEL_METRIC, "value": round(tokens_per_s, 2), "unit": "tokens/s",
+        "n_gpus": 1, "steps": steps, "warmup": warm, "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": args.workload, "layers": Lh, "d_model": E, "heads": w["H"],
+                   "vocab": V, "experts": NE, "topk": K, "d_ff": EI, "context": Cx,
+                   "weights": "Q8_0" if wt == hipmoe.Q8_0 else "Q4_0",
+                   "prompt_tokens": w["prompt"], "graphs": True,
+                   "mean_unique_experts": round(mean_uniq, 3),
+                   "algorithmic_bytes_per_token": int(bytes_per_tok)},
+        "roofline": {"bound": "hbm", "kernel": "decode_step", "achieved": round(achieved_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_bytes("decode_step", args.workload)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
@@ -231,6 +299,8 @@ def main():
         sys.exit("no HIP device")
     if w.get("kind") == "qmat":
         return bench_qmat(args, w, H)
+    if w.get("kind") == "model":
+        return bench_model(args, w, H)
     E, T, K = w["E"], w["T"], w["K"]
 
     t0 = time.perf_counter()
@@ -326,9 +396,10 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        log(f"cpu baseline ({args.cpu_seconds:.0f} s)")
-        cpu = cpu_baseline(lw, w, xs, args.cpu_seconds)
-        log(f"cpu baseline: {cpu['value']:.2f} tokens/s")
+        log(f"cpu baseline ({args.cpu_seconds:.0f} s, own process)")
+        cpu = cpu_baseline(w, args.cpu_seconds)
+        if cpu:
+            log(f"cpu baseline: {cpu['value']:.2f} tokens/s on {cpu['cores']} threads")
 
     line = {
         "metric": METRIC,

@@ -47,7 +47,11 @@ struct hip_lm {
 
 	float *d_kc, *d_vc; /* [L][KH][C][HL] */
 	float *d_freq;      /* [HL / 2] rope frequencies */
-	float *d_h0, *d_h1, *d_x, *d_qkv, *d_attn, *d_moe_in, *d_moe_out, *d_part, *d_logits;
+	float *d_h0, *d_h1, *d_qkv, *d_attn, *d_moe_in, *d_moe_out, *d_logits;
+	uint64_t *d_part;   /* tagged attention partials [H][chunks][HL + 2] */
+	uint64_t *d_rows_t; /* tagged output-product rows [E] */
+	uint64_t *d_best;   /* tagged per-workgroup maxima of the lm_head [2 * grid] */
+	uint32_t *d_cnt;    /* arrival counters: [H] attention, output product, lm_head */
 	uint32_t *d_ids;   /* [L][K] */
 	float *d_w;        /* [L][K] */
 	LmState *d_st;
@@ -56,7 +60,10 @@ struct hip_lm {
 
 	/* host mirror of the counters */
 	LmState st;
-	hipGraphExec_t g_body, g_head; /* captured steps without / with the lm_head */
+	/* captured steps without / with the lm_head, one per count of active
+	 * attention chunks (the attention grid), captured when first needed */
+	int nch;
+	hipGraphExec_t *g_body, *g_head;
 	hipEvent_t ev0, ev1;
 };
 
@@ -104,11 +111,13 @@ fail:
 
 static void drop_graphs(hip_lm *M)
 {
-	if (M->g_body)
-		hipGraphExecDestroy(M->g_body);
-	if (M->g_head)
-		hipGraphExecDestroy(M->g_head);
-	M->g_body = M->g_head = NULL;
+	for (int i = 0; M->g_body && i <= M->nch; i++) {
+		if (M->g_body[i])
+			hipGraphExecDestroy(M->g_body[i]);
+		if (M->g_head[i])
+			hipGraphExecDestroy(M->g_head[i]);
+		M->g_body[i] = M->g_head[i] = NULL;
+	}
 }
 
 void hip_lm_free(hip_lm *M)
@@ -116,6 +125,8 @@ void hip_lm_free(hip_lm *M)
 	if (!M)
 		return;
 	drop_graphs(M);
+	free(M->g_body);
+	free(M->g_head);
 	if (M->ly) {
 		for (size_t l = 0; l < M->L; l++) {
 			struct lm_layer *y = &M->ly[l];
@@ -130,9 +141,9 @@ void hip_lm_free(hip_lm *M)
 		free(M->ly);
 	}
 	void *bufs[] = {M->d_wte, M->d_head, M->d_onorm, M->d_kc, M->d_vc, M->d_freq, M->d_h0,
-			M->d_h1, M->d_x, M->d_qkv, M->d_attn, M->d_moe_in, M->d_moe_out,
-			M->d_part, M->d_logits, M->d_ids, M->d_w, M->d_st, M->d_prompt,
-			M->d_tokens};
+			M->d_h1, M->d_qkv, M->d_attn, M->d_moe_in, M->d_moe_out, M->d_part,
+			M->d_rows_t, M->d_best, M->d_cnt, M->d_logits, M->d_ids, M->d_w,
+			M->d_st, M->d_prompt, M->d_tokens};
 	for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
 		hipFree(bufs[i]);
 	if (M->ev0)
@@ -162,6 +173,15 @@ static int check_desc(const hip_lm_desc *d)
 	    !d->vocab || d->vocab > 0x7fffffff || d->context < 2 || d->context > (1u << 24)) {
 		lm_err("lm_upload: bad sizes (layers %zu, E %zu, heads %zu/%zu, vocab %zu, "
 		       "context %zu)", d->layers, d->E, d->heads, d->kv_heads, d->vocab, d->context);
+		return 0;
+	}
+	if (d->layers >= LM_HEAD_SLOT) {
+		lm_err("lm_upload: at most %d layers", LM_HEAD_SLOT - 1);
+		return 0;
+	}
+	if (lm_attn_chunks((int)d->context, (int)d->sliding_window) > LM_MAX_CHUNKS) {
+		lm_err("lm_upload: context %zu (window %zu) beyond %d attention chunks",
+		       d->context, d->sliding_window, LM_MAX_CHUNKS);
 		return 0;
 	}
 	if (d->arch == HIP_LM_OLMOE && d->heads * LM_HLEN != d->E) {
@@ -212,6 +232,13 @@ hip_lm *hip_lm_upload(const hip_lm_desc *d)
 	M->scale_div = (float)sqrt((double)(float)M->HL);
 	M->EQ = M->H * M->HL;
 	M->EKV = M->KH * M->HL;
+	M->nch = lm_attn_chunks((int)M->C, (int)M->window);
+	M->g_body = calloc((size_t)M->nch + 1, sizeof(hipGraphExec_t));
+	M->g_head = calloc((size_t)M->nch + 1, sizeof(hipGraphExec_t));
+	if (!M->g_body || !M->g_head) {
+		lm_err("lm_upload: out of host memory");
+		goto fail;
+	}
 	const int wt = d->wtype;
 	const size_t E = M->E;
 
@@ -222,10 +249,13 @@ hip_lm *hip_lm_upload(const hip_lm_desc *d)
 
 	/* products: one token, K = E (qkv) and heads * 128 (output); the
 	 * workgroups resident at once, queried here, not under capture */
-	M->grid_qkv = moe_qgemv_grid(wt, (int)E, 1);
-	M->grid_o = moe_qgemv_grid(wt, (int)M->EQ, 1);
-	M->grid_head = M->grid_qkv;
-	if (M->grid_qkv <= 0 || M->grid_o <= 0) {
+	M->grid_qkv = lm_gemv_grid(0, wt, (int)E, (int)(M->EQ + 2 * M->EKV));
+	M->grid_o = lm_gemv_grid(1, wt, (int)M->EQ, (int)E);
+	M->grid_head = lm_gemv_grid(2, wt, (int)E, (int)M->V);
+	/* (the output product's last workgroup gathers E rows in the LDS that
+	 * staged its heads * 128 inputs) */
+	if (M->grid_qkv <= 0 || M->grid_o <= 0 || M->grid_head <= 0 ||
+	    M->grid_head > LM_MAX_HEAD_WG || E * 64 > M->EQ * 68) {
 		lm_err("lm_upload: E=%zu / heads*128=%zu not supported by the dense product", E,
 		       M->EQ);
 		goto fail;
@@ -294,19 +324,28 @@ hip_lm *hip_lm_upload(const hip_lm_desc *d)
 	const size_t EA = E > M->EQ ? E : M->EQ;
 	HIPCHK(hipMalloc((void **)&M->d_h0, E * 4), "hipMalloc(h0)");
 	HIPCHK(hipMalloc((void **)&M->d_h1, E * 4), "hipMalloc(h1)");
-	HIPCHK(hipMalloc((void **)&M->d_x, EA * 4), "hipMalloc(x)");
 	HIPCHK(hipMalloc((void **)&M->d_qkv, (M->EQ + 2 * M->EKV) * 4), "hipMalloc(qkv)");
 	HIPCHK(hipMalloc((void **)&M->d_attn, EA * 4), "hipMalloc(attn)");
 	HIPCHK(hipMalloc((void **)&M->d_moe_in, M->L * E * 4), "hipMalloc(moe_in)");
 	HIPCHK(hipMalloc((void **)&M->d_moe_out, E * 4), "hipMalloc(moe_out)");
-	HIPCHK(hipMalloc((void **)&M->d_part,
-			 M->H * (size_t)lm_attn_chunks((int)M->C, (int)M->window) * (LM_HLEN + 2) * 4),
-	       "hipMalloc(attention partials)");
+	const size_t part = M->H * (size_t)lm_attn_chunks((int)M->C, (int)M->window) *
+			    (LM_HLEN + 2) * sizeof(uint64_t);
+	HIPCHK(hipMalloc((void **)&M->d_part, part), "hipMalloc(attention partials)");
+	HIPCHK(hipMemset(M->d_part, 0, part), "clear attention partials");
+	HIPCHK(hipMalloc((void **)&M->d_rows_t, E * sizeof(uint64_t)), "hipMalloc(rows)");
+	HIPCHK(hipMemset(M->d_rows_t, 0, E * sizeof(uint64_t)), "clear rows");
+	HIPCHK(hipMalloc((void **)&M->d_best, 2 * LM_MAX_HEAD_WG * sizeof(uint64_t)),
+	       "hipMalloc(best)");
+	HIPCHK(hipMemset(M->d_best, 0, 2 * LM_MAX_HEAD_WG * sizeof(uint64_t)), "clear best");
+	HIPCHK(hipMalloc((void **)&M->d_cnt, (M->H + 2) * sizeof(uint32_t)), "hipMalloc(counters)");
+	HIPCHK(hipMemset(M->d_cnt, 0, (M->H + 2) * sizeof(uint32_t)), "clear counters");
 	HIPCHK(hipMalloc((void **)&M->d_logits, M->V * 4), "hipMalloc(logits)");
 	HIPCHK(hipMalloc((void **)&M->d_ids, M->L * M->K * 4), "hipMalloc(ids)");
 	HIPCHK(hipMalloc((void **)&M->d_w, M->L * M->K * 4), "hipMalloc(w)");
 	HIPCHK(hipMalloc((void **)&M->d_st, sizeof(LmState)), "hipMalloc(state)");
-	HIPCHK(hipMemset(M->d_st, 0, sizeof(LmState)), "clear state");
+	/* epoch 1: tags never match the zeroed gather buffers */
+	M->st.epoch = 1;
+	HIPCHK(hipMemcpy(M->d_st, &M->st, sizeof(LmState), hipMemcpyHostToDevice), "set state");
 	HIPCHK(hipDeviceSynchronize(), "synchronize after upload");
 	return M;
 fail:
@@ -357,43 +396,39 @@ fail:
 	return 0;
 }
 
-/* one step on M->stream; head: also the lm_head product and the pick */
-static int enqueue_step(hip_lm *M, int head)
+/* one step on M->stream; head: also the lm_head product and the pick;
+ * nact: the attention chunks of this step (lm_attn_active) */
+static int enqueue_step(hip_lm *M, int head, int nact)
 {
-	const int wt = M->wtype, E = (int)M->E;
+	const int wt = M->wtype, E = (int)M->E, NQKV = (int)(M->EQ + 2 * M->EKV);
 	hipStream_t s = M->stream;
-	LCHK(lm_launch_embed(wt, M->d_wte, E, M->d_st, M->d_prompt, M->d_h0, s), "embed");
+	uint32_t *cnt_attn = M->d_cnt, *cnt_o = M->d_cnt + M->H, *cnt_head = cnt_o + 1;
 	for (size_t l = 0; l < M->L; l++) {
 		struct lm_layer *y = &M->ly[l];
 		const size_t co = l * M->KH * M->C * M->HL;
-		/* h0 = h1 + moe_out (the previous layer's residual), x = rms_norm(h0) */
-		LCHK(lm_launch_add_rmsnorm(l ? M->d_h1 : M->d_h0, l ? M->d_moe_out : NULL, M->d_h0,
-					   y->attn_norm, M->d_x, E, s), "attn_norm");
-		LCHK(moe_launch_qgemv(wt, y->wqkv, (int)(M->EQ + 2 * M->EKV), E, M->d_x, 1, NULL, 0,
-				      M->d_qkv, M->grid_qkv, s), "q/k/v");
-		LCHK(lm_launch_qk_rope_kv(M->d_qkv, y->q_norm, y->k_norm, M->d_freq, M->d_st,
-					  M->d_kc + co, M->d_vc + co, (int)M->H, (int)M->KH,
-					  (int)M->HL, (int)M->C, s), "q/k norm, rope, cache row");
-		LCHK(lm_launch_attention(M->d_qkv, M->d_kc + co, M->d_vc + co, M->d_st, M->d_part,
-					 M->d_attn, (int)M->H, (int)M->KH, (int)M->C,
-					 (int)M->window, M->scale_div, s), "attention");
-		/* h1 = h0 + attn . Wo^T */
-		LCHK(moe_launch_qgemv(wt, y->wo, E, (int)M->EQ, M->d_attn, 1, M->d_h0, 0, M->d_h1,
-				      M->grid_o, s), "attn_output");
-		LCHK(lm_launch_add_rmsnorm(M->d_h1, NULL, NULL, y->ffn_norm, M->d_moe_in + l * M->E,
-					   E, s), "ffn_norm");
+		/* layer 0: the token's embedding; then h0 = h1 + moe_out (the
+		 * previous layer's residual); qkv = rms_norm(h0) . Wqkv^T */
+		LCHK(lm_launch_qkv(wt, y->wqkv, NQKV, E, l ? M->d_h1 : NULL, l ? M->d_moe_out : NULL,
+				   y->attn_norm, M->d_h0, M->d_wte, M->d_st, M->d_prompt, M->d_qkv,
+				   M->grid_qkv, s), "norm + q/k/v");
+		LCHK(lm_launch_attn(M->d_qkv, y->q_norm, y->k_norm, M->d_freq, M->d_st, M->d_kc + co,
+				    M->d_vc + co, M->d_part, cnt_attn, M->d_attn, (int)M->H,
+				    (int)M->KH, (int)M->C, (int)M->window, M->scale_div, (int)l, nact,
+				    s), "attention");
+		/* h1 = h0 + attn . Wo^T, moe_in = rms_norm(h1) */
+		LCHK(lm_launch_oproj(wt, y->wo, E, (int)M->EQ, M->d_attn, M->d_h0, M->d_h1,
+				     M->d_rows_t, cnt_o, y->ffn_norm, M->d_moe_in + l * M->E,
+				     M->d_st, (int)l, M->grid_o, s), "output product + norm");
 		if (!hip_moe_ffn_dev(y->moe, M->d_moe_in + l * M->E, M->d_moe_out, 1, NULL,
 				     M->d_ids + l * M->K, M->d_w + l * M->K, s))
 			return 0;
 	}
-	LCHK(lm_launch_add_rmsnorm(M->d_h1, M->d_moe_out, M->d_h0, M->d_onorm, M->d_x, E, s),
-	     "output_norm");
-	if (head) {
-		LCHK(moe_launch_qgemv(wt, M->d_head, (int)M->V, E, M->d_x, 1, NULL, 0, M->d_logits,
-				      M->grid_head, s), "lm_head");
-		LCHK(lm_launch_argmax(M->d_logits, (int)M->V, M->d_st, M->d_tokens, s), "pick");
-	}
-	LCHK(lm_launch_step_end(M->d_st, s), "step end");
+	if (head) /* logits = rms_norm(h1 + moe_out) . lm_head^T, pick, advance */
+		LCHK(lm_launch_head(wt, M->d_head, (int)M->V, E, M->d_h1, M->d_moe_out, M->d_onorm,
+				    M->d_logits, M->d_best, cnt_head, M->d_st, M->d_tokens,
+				    M->grid_head, s), "lm_head + pick");
+	else
+		LCHK(lm_launch_step_end(M->d_st, s), "step end");
 	return 1;
 }
 
@@ -432,7 +467,8 @@ static int start_run(hip_lm *M, const int *prompt, size_t n_prompt)
 	if (n_prompt)
 		HIPCHK(hipMemcpy(M->d_prompt, prompt, n_prompt * sizeof(int), hipMemcpyHostToDevice),
 		       "copy prompt");
-	HIPCHK(hipMemcpy(M->d_st, &M->st, sizeof(LmState), hipMemcpyHostToDevice), "set state");
+	/* the host's four counters; tok, epoch and err stay the device's */
+	HIPCHK(hipMemcpy(M->d_st, &M->st, 4 * sizeof(int), hipMemcpyHostToDevice), "set state");
 	return 1;
 fail:
 	return 0;
@@ -443,6 +479,32 @@ static void advance_host(hip_lm *M)
 	M->st.step++;
 	M->st.pos++;
 	M->st.size++;
+}
+
+/* after the stream drains: a bounded wait of a gather or of a MoE layer's
+ * decode kernel that ran out makes the run's results invalid */
+static int check_errors(hip_lm *M, const char *what)
+{
+	int err = 0;
+	HIPCHK(hipStreamSynchronize(M->stream), "synchronize");
+	HIPCHK(hipMemcpy(&err, &M->d_st->err, sizeof(int), hipMemcpyDeviceToHost), "read error");
+	if (err) {
+		const int zero = 0;
+		HIPCHK(hipMemcpy(&M->d_st->err, &zero, sizeof(int), hipMemcpyHostToDevice),
+		       "clear error");
+		lm_err("%s: a gather of the step kernels ran out of polls (%d)", what, err);
+		return 0;
+	}
+	for (size_t l = 0; l < M->L; l++) {
+		int rc = hip_moe_status(M->ly[l].moe, M->stream);
+		if (rc != 0) {
+			lm_err("%s: layer %zu: MoE decode wait failed (%d)", what, l, rc);
+			return 0;
+		}
+	}
+	return 1;
+fail:
+	return 0;
 }
 
 static int check_token(const hip_lm *M, int tok)
@@ -461,17 +523,12 @@ int hip_lm_decode(hip_lm *M, int tok, float *logits, int *next)
 		return 0;
 	}
 	if (!check_token(M, tok) || !ensure_io(M, 1, 1) || !rotate_if_full(M) ||
-	    !start_run(M, &tok, 1) || !enqueue_step(M, 1))
+	    !start_run(M, &tok, 1) ||
+	    !enqueue_step(M, 1, lm_attn_active(M->st.size, (int)M->window)))
 		return 0;
 	advance_host(M);
-	HIPCHK(hipStreamSynchronize(M->stream), "synchronize");
-	for (size_t l = 0; l < M->L; l++) {
-		int rc = hip_moe_status(M->ly[l].moe, M->stream);
-		if (rc != 0) {
-			lm_err("lm_decode: layer %zu: MoE decode wait failed (%d)", l, rc);
-			return 0;
-		}
-	}
+	if (!check_errors(M, "lm_decode"))
+		return 0;
 	if (logits)
 		HIPCHK(hipMemcpy(logits, M->d_logits, M->V * 4, hipMemcpyDeviceToHost), "copy logits");
 	if (next) {
@@ -484,11 +541,11 @@ fail:
 	return 0;
 }
 
-static int capture(hip_lm *M, int head, hipGraphExec_t *out)
+static int capture(hip_lm *M, int head, int nact, hipGraphExec_t *out)
 {
 	hipGraph_t g = NULL;
 	HIPCHK(hipStreamBeginCapture(M->stream, hipStreamCaptureModeThreadLocal), "begin capture");
-	if (!enqueue_step(M, head)) {
+	if (!enqueue_step(M, head, nact)) {
 		hipStreamEndCapture(M->stream, &g);
 		if (g)
 			hipGraphDestroy(g);
@@ -521,29 +578,39 @@ int hip_lm_generate(hip_lm *M, const int *prompt, size_t n_prompt, size_t n_gen,
 	}
 	if (!ensure_io(M, n_prompt, steps) || !start_run(M, prompt, n_prompt))
 		return 0;
-	if (!M->g_body && !capture(M, 0, &M->g_body))
-		return 0;
-	if (!M->g_head && !capture(M, 1, &M->g_head))
-		return 0;
+	/* capture every step shape the run needs before its first launch: the
+	 * cache size of each step is known here (one row per step, and
+	 * kvcache_rotate's keep when full) */
+	{
+		size_t size = (size_t)M->st.size;
+		for (size_t i = 0; i < steps; i++) {
+			if (size >= M->C) {
+				size_t keep = M->window ? M->window : M->C / 2;
+				size = keep < size ? keep : size;
+			}
+			const int head = i + 1 >= n_prompt;
+			const int nact = lm_attn_active((int)size, (int)M->window);
+			hipGraphExec_t *ge = head ? &M->g_head[nact] : &M->g_body[nact];
+			if (!*ge && !capture(M, head, nact, ge))
+				return 0;
+			size++;
+		}
+	}
 	for (size_t i = 0; i < steps; i++) {
 		if (!rotate_if_full(M))
 			return 0;
+		/* prompt steps before the last need no lm_head */
+		const int head = i + 1 >= n_prompt;
+		const int nact = lm_attn_active(M->st.size, (int)M->window);
+		hipGraphExec_t *ge = head ? &M->g_head[nact] : &M->g_body[nact];
 		if (i == n_prompt)
 			HIPCHK(hipEventRecord(M->ev0, M->stream), "event");
-		/* prompt steps before the last need no lm_head */
-		HIPCHK(hipGraphLaunch(i + 1 < n_prompt ? M->g_body : M->g_head, M->stream),
-		       "step graph");
+		HIPCHK(hipGraphLaunch(*ge, M->stream), "step graph");
 		advance_host(M);
 	}
 	HIPCHK(hipEventRecord(M->ev1, M->stream), "event");
-	HIPCHK(hipStreamSynchronize(M->stream), "synchronize");
-	for (size_t l = 0; l < M->L; l++) {
-		int rc = hip_moe_status(M->ly[l].moe, M->stream);
-		if (rc != 0) {
-			lm_err("lm_generate: layer %zu: MoE decode wait failed (%d)", l, rc);
-			return 0;
-		}
-	}
+	if (!check_errors(M, "lm_generate"))
+		return 0;
 	if (decode_ms) {
 		*decode_ms = 0.0f;
 		if (n_gen)
@@ -586,7 +653,8 @@ int hip_lm_reset(hip_lm *M)
 	HIPCHK(hipMemset(M->d_kc, 0, cache), "clear k cache");
 	HIPCHK(hipMemset(M->d_vc, 0, cache), "clear v cache");
 	memset(&M->st, 0, sizeof(M->st));
-	HIPCHK(hipMemcpy(M->d_st, &M->st, sizeof(LmState), hipMemcpyHostToDevice), "clear state");
+	/* the host's counters and tok; the epoch keeps counting */
+	HIPCHK(hipMemcpy(M->d_st, &M->st, 5 * sizeof(int), hipMemcpyHostToDevice), "clear state");
 	HIPCHK(hipDeviceSynchronize(), "synchronize");
 	return 1;
 fail:

@@ -13,34 +13,63 @@
 extern "C" {
 #endif
 
-#define LM_HLEN 128   /* head length the attention kernels take */
-#define LM_CHUNK 64   /* cache positions per attention workgroup */
-#define LM_ARG_NT 1024
+#define LM_HLEN 128        /* head length the attention kernel takes */
+#define LM_CHUNK 64        /* cache positions per attention workgroup */
+#define LM_MAX_CHUNKS 256  /* chunks of one head (context or window <= 16384) */
+#define LM_TAG_SLOTS 64    /* gather tags: epoch * 64 + slot */
+#define LM_HEAD_SLOT 63    /* the lm_head's slot; layers use 0 .. 62 */
+#define LM_MAX_HEAD_WG 4096
+#define LM_ERR_GATHER 1    /* a gather's poll ran out */
 
-/* The step's counters, in device memory, read by every step kernel so that
- * one captured graph serves every step. */
+/* The step's counters in device memory, read by every step kernel so that
+ * one captured graph serves every step.  The host writes the first four
+ * (it mirrors them exactly); the rest belong to the device. */
 typedef struct LmState {
-	int step;     /* steps run since the last reset (prompt + generated) */
+	int step;     /* steps since the run began (prompt + generated) */
 	int n_prompt; /* steps that take their token from the prompt */
 	int pos;      /* the model's position counter (olmoe.c:95) */
 	int size;     /* KV cache rows in use (kvcache.h:14) */
 	int tok;      /* the last greedy pick */
-	int pad[3];
+	int epoch;    /* steps since upload, never reset: the gathers' tags */
+	int err;      /* LM_ERR_* set by a kernel, 0 if none */
+	int pad;
 } LmState;
 
-int lm_launch_embed(int wtype, const uint8_t *wte, int E, const LmState *st, const int *prompt,
-                    float *hidden, void *stream);
-int lm_launch_add_rmsnorm(const float *a, const float *b, float *h, const float *w, float *x,
-                          int E, void *stream);
-int lm_launch_qk_rope_kv(float *qkv, const float *q_norm, const float *k_norm,
-                         const float *freq, const LmState *st, float *kc, float *vc, int H,
-                         int KH, int HL, int C, void *stream);
-/* attention partials hold H * lm_attn_chunks(C, window) * (LM_HLEN + 2) floats */
+/* workgroups of the one-token product kind (0 qkv, 1 output, 2 lm_head)
+ * over N rows of K columns: the row groups or what the device holds at
+ * once, whichever is fewer; 0 if the shape is not supported */
+int lm_gemv_grid(int kind, int wtype, int K, int N);
+/* out[N] = rms_norm(a + b) * w . W^T (b may be NULL; a NULL: the step's
+ * token row of wte); h_out (may be NULL) receives a + b */
+int lm_launch_qkv(int wtype, const uint8_t *W, int N, int K, const float *a, const float *b,
+                  const float *w, float *h_out, const uint8_t *wte, const LmState *st,
+                  const int *prompt, float *out, int grid, void *stream);
+/* attention partials hold H * lm_attn_chunks(C, window) * (LM_HLEN + 2)
+ * tagged words; cnt holds H zeroed counters.  nact: the chunks of
+ * LM_CHUNK rows covering the step's cache rows (lm_attn_active). */
 int lm_attn_chunks(int C, int window);
-int lm_launch_attention(const float *q, const float *kc, const float *vc, const LmState *st,
-                        float *part, float *out, int H, int KH, int C, int window,
-                        float scale_div, void *stream);
-int lm_launch_argmax(const float *logits, int V, LmState *st, int *tokens, void *stream);
+int lm_launch_attn(const float *qkv, const float *q_norm, const float *k_norm,
+                   const float *freq, LmState *st, float *kc, float *vc, uint64_t *part,
+                   uint32_t *cnt, float *out, int H, int KH, int C, int window,
+                   float scale_div, int layer, int nact, void *stream);
+
+/* chunks a step over a cache of `size` rows (before the step) reads */
+static inline int lm_attn_active(int size, int window)
+{
+	const int AT = size + 1, lo = window > 0 && AT > window ? AT - window : 0;
+	return (AT - lo + LM_CHUNK - 1) / LM_CHUNK;
+}
+/* out[N] = add + x . W^T, then x_out = rms_norm(out) * w (rows_t: N tagged
+ * words, cnt one zeroed counter) */
+int lm_launch_oproj(int wtype, const uint8_t *W, int N, int K, const float *x,
+                    const float *add, float *out, uint64_t *rows_t, uint32_t *cnt,
+                    const float *w, float *x_out, LmState *st, int layer, int grid,
+                    void *stream);
+/* logits out[N] = rms_norm(a + b) * w . W^T, the greedy pick and the
+ * counters' advance (best: 2 * grid tagged words, cnt one zeroed counter) */
+int lm_launch_head(int wtype, const uint8_t *W, int N, int K, const float *a, const float *b,
+                   const float *w, float *out, uint64_t *best, uint32_t *cnt, LmState *st,
+                   int *tokens, int grid, void *stream);
 int lm_launch_step_end(LmState *st, void *stream);
 /* dst[s * slab + i] = src[s * slab + i], i < n, s < slabs (ranges must not
  * overlap within a slab) */

@@ -1,32 +1,46 @@
 /*
- * Kernels of the whole-model decode step around the MoE layer (hip_lm.c):
+ * Kernels of the whole-model decode step around the MoE layer (hip_lm.c),
+ * four launches per layer plus one for the head:
  *
- *   k_embed          token row of token_embd, dequantized (tensor_pick_rows,
- *                    tensor.c:263-294), the token taken from the prompt or
- *                    from the previous step's greedy pick
- *   k_add_rmsnorm    h = a (+ b), x = rms_norm(h) * w (nn.c:8-51 with the
- *                    residual tensor_add, tensor.c:334-353, in front)
- *   k_qk_rope_kv     full-vector RMSNorm of q and k (OLMoE's attn_q_norm /
- *                    attn_k_norm, olmoe.c:454-458), RoPE on consecutive pairs
- *                    (rope_apply, nn.c:192-219), k and v into the cache row
- *   k_attn_part      one (head, chunk of positions): scores q.k / sqrt(HLEN),
- *                    the chunk's max, sum of exp and exp-weighted sum of v
- *   k_attn_merge     the chunks of a head merged into softmax(scores) . V
- *                    (olmoe.c:302-320; the flash-decoding split of it)
- *   k_argmax         the greedy pick over the logits (main.c:189-193: the
- *                    first maximum wins), and the step's counters advanced
- *   k_kv_rotate      kvcache_rotate (kvcache.c:31-56): keep the last entries
+ *   k_lm_qkv      the residual add (tensor_add, tensor.c:334-353) or the
+ *                 token's embedding row (tensor_pick_rows, tensor.c:263-294),
+ *                 rms_norm (nn.c:8-51) into LDS by every workgroup, then the
+ *                 one-token product with the stacked [q; k; v] matrix
+ *                 (olmoe.c:448-450)
+ *   k_lm_attn     one (head, chunk of cache positions): the full-vector
+ *                 RMSNorm of q and k (olmoe.c:454-458), RoPE on consecutive
+ *                 pairs (rope_apply, nn.c:192-219), the new k/v row into the
+ *                 cache (olmoe.c:240-262), then scores / sqrt(HLEN), the
+ *                 chunk's max, exp-sum and exp-weighted v; the last chunk of
+ *                 a head to finish merges the chunks into softmax . V
+ *                 (olmoe.c:296-320, flash-decoding form)
+ *   k_lm_oproj    the output product with the residual as its add operand
+ *                 (olmoe.c:476-478); the last workgroup to finish computes
+ *                 the pre-MoE rms_norm (olmoe.c:482) for the MoE layer
+ *   k_lm_head     the residual add and the final rms_norm into LDS, the
+ *                 lm_head product (olmoe.c:558-564), and the greedy pick
+ *                 (main.c:189-193, the first maximum) by the last workgroup,
+ *                 which also advances the step's counters
  *
- * Every kernel reads the step's token, position and cache row from a small
+ * Every kernel reads the step's token, position and cache row from the
  * device state block (LmState), so one captured HIP graph serves every step.
+ *
+ * Results that a last workgroup gathers from the others (attention
+ * partials, the output product's rows, the workgroups' best logits) travel
+ * as 64-bit words tagged with the step's epoch and the layer, written with
+ * device-coherent stores and polled with device-coherent loads: no fence,
+ * no reliance on store order.  A counter per gather picks the last
+ * workgroup (relaxed device atomics) and is reset by it.  Every poll is
+ * bounded; one that runs out sets LmState.err, which the host reports.
+ *
  * Compiled with -ffp-contract=off: fused multiply-adds only where written.
  */
-#include "moe_device.h"
+#include "moe_qgemv.h"
 #include "lm_internal.h"
 
-#define LM_NT 256 /* threads of the single-workgroup kernels */
+#define LM_NT (QG_WAVES * WAVE) /* threads of every kernel here */
+#define LM_SPIN (1 << 22)       /* poll rounds of a gather before it gives up */
 
-/* sum over the workgroup of one float per thread (LM_NT threads) */
 __device__ static inline float block_sum(float v, float *red)
 {
 	for (int o = WAVE / 2; o > 0; o >>= 1)
@@ -59,7 +73,71 @@ __device__ static inline float block_max(float v, float *red)
 	return m;
 }
 
-/* ---------------------------------------------------------------------- */
+/* the tag of gather `slot` (a layer, or LM_HEAD_SLOT) in this step */
+__device__ static inline u32 lm_tag(const LmState *st, int slot)
+{
+	return (u32)st->epoch * LM_TAG_SLOTS + (u32)slot;
+}
+
+__device__ static inline uint64_t tagged(u32 tag, float v)
+{
+	return ((uint64_t)tag << 32) | __builtin_bit_cast(u32, v);
+}
+
+/* poll p until its tag is `tag`; its value, or 0 and the error word set */
+__device__ static inline u32 poll_tag(const uint64_t *p, u32 tag, LmState *st)
+{
+	int step = 0;
+	for (int round = 0;; round++) {
+		const uint64_t v = ld_dev_u64(p);
+		if ((u32)(v >> 32) == tag)
+			return (u32)v;
+		if (round >= LM_SPIN) {
+			st_dev_u32((u32 *)&st->err, LM_ERR_GATHER);
+			return 0;
+		}
+		backoff(step);
+	}
+}
+
+/* v[i] = the value of p[i * stride] for the thread's entries i = tid,
+ * tid + LM_NT, ... < n, its loads issued eight at a time before any is
+ * checked; a late entry is polled on its own.  fn(i, value) consumes them. */
+template <class Fn>
+__device__ static inline void gather_tagged(const uint64_t *p, size_t stride, int n, u32 tag,
+					    LmState *st, Fn fn)
+{
+	for (int i0 = threadIdx.x; i0 < n; i0 += 8 * LM_NT) {
+		uint64_t v[8];
+#pragma unroll
+		for (int u = 0; u < 8; u++) {
+			const int i = i0 + u * LM_NT;
+			v[u] = i < n ? ld_dev_u64(&p[(size_t)i * stride]) : 0;
+		}
+#pragma unroll
+		for (int u = 0; u < 8; u++) {
+			const int i = i0 + u * LM_NT;
+			if (i < n)
+				fn(i, (u32)(v[u] >> 32) == tag ? (u32)v[u]
+							       : poll_tag(&p[(size_t)i * stride], tag, st));
+		}
+	}
+}
+
+/* the last of n workgroups to arrive at counter *cnt (which it resets) */
+__device__ static inline bool last_to_arrive(u32 *cnt, u32 n, int *s_flag)
+{
+	__syncthreads(); /* every thread's tagged stores are issued */
+	if (threadIdx.x == 0) {
+		const u32 old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED,
+						       __HIP_MEMORY_SCOPE_AGENT);
+		*s_flag = old == n - 1;
+		if (old == n - 1)
+			__hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+	}
+	__syncthreads();
+	return *s_flag != 0;
+}
 
 /* the step's token: the prompt's while it lasts, then the last pick */
 __device__ static inline int step_token(const LmState *st, const int *prompt)
@@ -67,306 +145,435 @@ __device__ static inline int step_token(const LmState *st, const int *prompt)
 	return st->step < st->n_prompt ? prompt[st->step] : st->tok;
 }
 
-/* hidden[E] = dequantized row tok of token_embd (quant.c:157-196: d * q) */
+/* four consecutive values (float4 index c4) of a dequantized row:
+ * d * q (quant.c:157-196) */
 template <int WT>
-__global__ __launch_bounds__(LM_NT) void k_embed(const uint8_t *__restrict__ wte, int E,
-						 const LmState *__restrict__ st,
-						 const int *__restrict__ prompt, float *__restrict__ hidden)
+__device__ static inline float4 dequant4(const uint8_t *row, int c4)
 {
-	const int tok = step_token(st, prompt);
 	constexpr int BB = WT == 1 ? 34 : 18;
-	const uint8_t *row = wte + (size_t)tok * (size_t)(E / 32) * BB;
-	for (int i = threadIdx.x; i < E; i += LM_NT) {
-		const uint8_t *b = row + (size_t)(i / 32) * BB;
-		const float d = f16_bits_to_f32((u32)b[0] | ((u32)b[1] << 8));
-		const int j = i % 32;
-		float q;
+	const uint8_t *b = row + (size_t)(c4 / 8) * BB;
+	const float d = f16_bits_to_f32((u32)b[0] | ((u32)b[1] << 8));
+	const int j = (c4 % 8) * 4;
+	float q[4];
+#pragma unroll
+	for (int u = 0; u < 4; u++) {
 		if (WT == 1)
-			q = (float)(int8_t)b[2 + j];
+			q[u] = (float)(int8_t)b[2 + j + u];
 		else
-			q = (float)((j < 16 ? (b[2 + j] & 15) : (b[2 + j - 16] >> 4)) - 8);
-		hidden[i] = d * q;
+			q[u] = (float)((j < 16 ? (b[2 + j + u] & 15) : (b[2 + j + u - 16] >> 4)) - 8);
 	}
+	return make_float4(d * q[0], d * q[1], d * q[2], d * q[3]);
 }
 
 /*
- * h = a + b (b may be NULL: h = a, not written back), x = (h / rms) * w,
- * rms = sqrtf(sum(h^2) / E + 1e-5f).  One workgroup; E <= 32 * LM_NT.
+ * Every workgroup puts x = rms_norm(v) * w into LDS (segment layout) with
+ * v = a + b (b may be NULL), or v = the dequantized row `emb`.  h_out (one
+ * workgroup passes it) receives v.  rms = sqrtf(sum(v^2) / E + 1e-5f),
+ * x = (v / rms) * w, as nn.c:8-51.
  */
-__global__ __launch_bounds__(LM_NT) void k_add_rmsnorm(const float *__restrict__ a,
-						       const float *__restrict__ b,
-						       float *__restrict__ h,
-						       const float *__restrict__ w,
-						       float *__restrict__ x, int E)
+template <int WT>
+__device__ static void stage_norm(float *sx, float *red, int E, const float *a, const float *b,
+				  const uint8_t *emb, const float *w, float *h_out)
 {
-	__shared__ float red[LM_NT / WAVE];
-	float v[32];
-	float s = 0.0f;
-#pragma unroll
-	for (int k = 0; k < 32; k++) {
-		const int i = threadIdx.x + k * LM_NT;
-		v[k] = 0.0f;
-		if (i < E) {
-			v[k] = b ? a[i] + b[i] : a[i];
-			const float sq = v[k] * v[k];
-			s = s + sq;
+	float ss = 0.0f;
+	for (int c4 = threadIdx.x; c4 < E / 4; c4 += LM_NT) {
+		float4 v;
+		if (emb) {
+			v = dequant4<WT>(emb, c4);
+		} else {
+			v = ((const float4 *)a)[c4];
+			if (b) {
+				const float4 u = ((const float4 *)b)[c4];
+				v.x = v.x + u.x;
+				v.y = v.y + u.y;
+				v.z = v.z + u.z;
+				v.w = v.w + u.w;
+			}
 		}
+		if (h_out)
+			((float4 *)h_out)[c4] = v;
+		*(float4 *)(sx + (c4 >> 4) * SEG_STRIDE + (c4 & 15) * 4) = v;
+		const float q0 = v.x * v.x, q1 = v.y * v.y, q2 = v.z * v.z, q3 = v.w * v.w;
+		ss = ss + q0;
+		ss = ss + q1;
+		ss = ss + q2;
+		ss = ss + q3;
 	}
-	const float sum = block_sum(s, red);
-	const float rms = sqrtf(sum / (float)E + 1e-5f);
-#pragma unroll
-	for (int k = 0; k < 32; k++) {
-		const int i = threadIdx.x + k * LM_NT;
-		if (i < E) {
-			if (b)
-				h[i] = v[k];
-			const float r = v[k] / rms;
-			x[i] = r * w[i];
-		}
+	const float rms = sqrtf(block_sum(ss, red) / (float)E + 1e-5f);
+	for (int c4 = threadIdx.x; c4 < E / 4; c4 += LM_NT) {
+		float4 *p = (float4 *)(sx + (c4 >> 4) * SEG_STRIDE + (c4 & 15) * 4);
+		float4 v = *p;
+		const float4 wv = ((const float4 *)w)[c4];
+		v.x = (v.x / rms) * wv.x;
+		v.y = (v.y / rms) * wv.y;
+		v.z = (v.z / rms) * wv.z;
+		v.w = (v.w / rms) * wv.w;
+		*p = v;
 	}
+	__syncthreads();
 }
 
-/*
- * qkv = [q (H*HL) | k (KH*HL) | v (KH*HL)].  With q_norm / k_norm: the
- * full-vector RMSNorm of q and of k first.  Then RoPE at the step's
- * position on q and k: pair (2i, 2i+1) of each head turns by pos * freq[i]
- * (freq from the host: 1 / powf(theta, 2i / HL), nn.c:205), x0' =
- * x0 cos - x1 sin, x1' = x0 sin + x1 cos (the reference's clang build
- * contracts each into one FMA, left product first).  k and v go to cache
- * row `size` of every kv head ([KH][C][HL] per layer).
- */
-__global__ __launch_bounds__(LM_NT) void k_qk_rope_kv(float *__restrict__ qkv,
-						      const float *__restrict__ q_norm,
-						      const float *__restrict__ k_norm,
-						      const float *__restrict__ freq,
-						      const LmState *__restrict__ st,
-						      float *__restrict__ kc, float *__restrict__ vc,
-						      int H, int KH, int HL, int C)
+/* ---------------------------------------------------------------------- */
+/* k_lm_qkv                                                               */
+/* ---------------------------------------------------------------------- */
+
+/* qkv = rms_norm(src) * w . Wqkv^T; src = a + b, or the step's token row of
+ * wte when a is NULL; workgroup 0 writes src to h_out */
+template <int WT, int C>
+__global__ __launch_bounds__(LM_NT) __attribute__((amdgpu_waves_per_eu(4)))
+void k_lm_qkv(const uint8_t *__restrict__ W, size_t rb, int N, int K, const float *a,
+	      const float *b, const float *__restrict__ w, float *h_out,
+	      const uint8_t *__restrict__ wte, const LmState *__restrict__ st,
+	      const int *__restrict__ prompt, float *__restrict__ out)
 {
+	extern __shared__ __attribute__((aligned(16))) float sx[];
 	__shared__ float red[LM_NT / WAVE];
-	const int EQ = H * HL, EK = KH * HL;
-	float *q = qkv, *k = qkv + EQ;
-	const float *v = qkv + EQ + EK;
-	/* olmoe_decode: a position past the context is replaced by the cache
-	 * size (olmoe.c:514-515) */
-	const int pos = st->pos < C ? st->pos : st->size;
-	const int row = st->size;
-	if (q_norm) {
-		for (int part = 0; part < 2; part++) {
-			float *t = part ? k : q;
-			const float *w = part ? k_norm : q_norm;
-			const int n = part ? EK : EQ;
-			float s = 0.0f;
-			for (int i = threadIdx.x; i < n; i += LM_NT) {
-				const float sq = t[i] * t[i];
-				s = s + sq;
-			}
-			const float rms = sqrtf(block_sum(s, red) / (float)n + 1e-5f);
-			for (int i = threadIdx.x; i < n; i += LM_NT) {
-				const float r = t[i] / rms;
-				t[i] = r * w[i];
-			}
-			__syncthreads();
-		}
-	}
-	const int half = HL / 2;
-	for (int p = threadIdx.x; p < (H + KH) * half; p += LM_NT) {
-		const int hh = p / half, i = p % half;
-		float *x = hh < H ? q + hh * HL : k + (hh - H) * HL;
-		const float angle = (float)pos * freq[i];
-		const float c = cosf(angle), s = sinf(angle);
-		const float x0 = x[2 * i], x1 = x[2 * i + 1];
-		const float y0 = __builtin_fmaf(x0, c, -(x1 * s));
-		const float y1 = __builtin_fmaf(x0, s, x1 * c);
-		x[2 * i] = y0;
-		x[2 * i + 1] = y1;
-		if (hh >= H) {
-			float *kr = kc + ((size_t)(hh - H) * C + row) * HL;
-			kr[2 * i] = y0;
-			kr[2 * i + 1] = y1;
-		}
-	}
-	for (int i = threadIdx.x; i < EK; i += LM_NT)
-		vc[((size_t)(i / HL) * C + row) * HL + i % HL] = v[i];
+	constexpr int BB = WT == 1 ? 34 : 18;
+	const uint8_t *emb =
+		a ? nullptr : wte + (size_t)step_token(st, prompt) * (size_t)(K / 32) * BB;
+	stage_norm<WT>(sx, red, K, a, b, emb, w, blockIdx.x == 0 ? h_out : nullptr);
+	qgemv_body<WT, C, true, true>(sx, W, rb, N, K, nullptr, 1, 1, nullptr, 0, out);
 }
 
+/* ---------------------------------------------------------------------- */
+/* k_lm_attn                                                              */
+/* ---------------------------------------------------------------------- */
+
 /*
- * One (query head h, chunk c of LM_CHUNK positions) of decode attention
- * over the cache rows [lo, AT), AT = size + 1 (lo > 0 with a sliding
- * window).  Thread t: position t / 4 of the chunk, dims (t % 4) * 32 ..
- * +31 for the scores; then dim t % HL over half the chunk's positions for
- * the v sum.  Writes part[h][c] = {max m, sum l of exp(s - m), o[HL] =
- * sum exp(s - m) v}; an empty chunk writes m = -inf, l = 0.
+ * Grid (H, nact): nact = the chunks of LM_CHUNK rows that cover the cache
+ * rows [lo, AT), AT = size + 1 (lo > 0 past a sliding window), which the
+ * host knows for every step.  Workgroup (h, c) covers rows [j0, j0 + n);
+ * the row `size` is this step's k and v, which the chunk holding it takes
+ * from LDS (the workgroup of the kv head's first query head also writes it
+ * to the cache).  Scores: 4 threads per position, 32 dims each; v sums: one
+ * dim per thread over half the positions.  One chunk writes
+ * out[h] = o / l itself; with more, partials part[h][c] = {m, l, o[HL]}
+ * (stride nstride chunks) go out tagged, and the last of the head's chunks
+ * merges them: out[h][d] = sum_c exp(m_c - M) o_c[d] / sum_c exp(m_c - M) l_c.
  */
-__global__ __launch_bounds__(LM_NT) void k_attn_part(const float *__restrict__ q,
-						     const float *__restrict__ kc,
-						     const float *__restrict__ vc,
-						     const LmState *__restrict__ st,
-						     float *__restrict__ part, int H, int KH, int C,
-						     int window, float scale_div)
+__global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv,
+						   const float *__restrict__ q_norm,
+						   const float *__restrict__ k_norm,
+						   const float *__restrict__ freq, LmState *st,
+						   float *__restrict__ kc, float *__restrict__ vc,
+						   uint64_t *part, u32 *cnt, float *__restrict__ out,
+						   int H, int KH, int C, int window, float scale_div,
+						   int layer, int nstride)
 {
 	constexpr int HL = LM_HLEN, CH = LM_CHUNK;
-	__shared__ float sq[HL];
-	__shared__ float sp[CH];
+	__shared__ float cs[HL / 2], sn[HL / 2], sq[HL], sk[HL], sv[HL], sp[CH], so[LM_NT];
 	__shared__ float red[LM_NT / WAVE];
-	__shared__ float so[LM_NT];
-	const int h = blockIdx.x, c = blockIdx.y, nchunk = gridDim.y;
-	const int AT = st->size + 1;
+	__shared__ float s_f[LM_MAX_CHUNKS], s_l[LM_MAX_CHUNKS];
+	__shared__ int s_flag;
+	const int h = blockIdx.x, c = blockIdx.y, nact = gridDim.y;
+	const int G = H / KH, kh = h / G;
+	const int EQ = H * HL, EK = KH * HL;
+	const float *q = qkv, *k = qkv + EQ, *v = qkv + EQ + EK;
+	const int tid = threadIdx.x;
+
+	/* every load that does not depend on the counters goes out first */
+	float qx = 0.0f, kx = 0.0f, vx = 0.0f, qw = 1.0f, kw = 1.0f, fr = 0.0f;
+	if (tid < HL) {
+		qx = q[h * HL + tid];
+		kx = k[kh * HL + tid];
+		vx = v[kh * HL + tid];
+		if (q_norm) {
+			qw = q_norm[h * HL + tid];
+			kw = k_norm[kh * HL + tid];
+		}
+	}
+	if (tid < HL / 2)
+		fr = freq[tid];
+	float s1 = 0.0f, s2 = 0.0f;
+	if (q_norm) {
+		for (int i = tid; i < EQ; i += LM_NT) {
+			const float t = q[i] * q[i];
+			s1 = s1 + t;
+		}
+		for (int i = tid; i < EK; i += LM_NT) {
+			const float t = k[i] * k[i];
+			s2 = s2 + t;
+		}
+	}
+	const int size = st->size, spos = st->pos;
+	const u32 tag = lm_tag(st, layer);
+	const int AT = size + 1;
 	const int lo = window > 0 && AT > window ? AT - window : 0;
 	const int j0 = lo + c * CH;
-	float *pp = part + ((size_t)h * nchunk + c) * (HL + 2);
-	if (j0 >= AT) {
-		if (threadIdx.x == 0) {
-			pp[0] = -INFINITY;
-			pp[1] = 0.0f;
-		}
-		return;
+	const int n = max(0, min(CH, AT - j0));
+	/* olmoe_decode: a position past the context is the cache size
+	 * (olmoe.c:514-515) */
+	const int pos = spos < C ? spos : size;
+
+	if (tid < HL / 2) {
+		const float ang = (float)pos * fr;
+		cs[tid] = cosf(ang);
+		sn[tid] = sinf(ang);
 	}
-	const int n = min(CH, AT - j0);
-	const int kh = h / (H / KH);
-	const float *K = kc + ((size_t)kh * C + j0) * HL, *V = vc + ((size_t)kh * C + j0) * HL;
-	if (threadIdx.x < HL)
-		sq[threadIdx.x] = q[h * HL + threadIdx.x];
+	if (q_norm) {
+		const float rq = sqrtf(block_sum(s1, red) / (float)EQ + 1e-5f);
+		const float rk = sqrtf(block_sum(s2, red) / (float)EK + 1e-5f);
+		const float r = qx / rq, t = kx / rk;
+		qx = r * qw;
+		kx = t * kw;
+	}
+	if (tid < HL) {
+		sq[tid] = qx;
+		sk[tid] = kx;
+		sv[tid] = vx;
+	}
 	__syncthreads();
-	/* scores: 4 threads per position, 32 dims each */
+	if (tid < HL / 2) { /* x0' = x0 cos - x1 sin, x1' = x0 sin + x1 cos (one FMA each) */
+		const float co = cs[tid], si = sn[tid];
+		float x0 = sq[2 * tid], x1 = sq[2 * tid + 1];
+		sq[2 * tid] = __builtin_fmaf(x0, co, -(x1 * si));
+		sq[2 * tid + 1] = __builtin_fmaf(x0, si, x1 * co);
+		x0 = sk[2 * tid];
+		x1 = sk[2 * tid + 1];
+		sk[2 * tid] = __builtin_fmaf(x0, co, -(x1 * si));
+		sk[2 * tid + 1] = __builtin_fmaf(x0, si, x1 * co);
+	}
+	__syncthreads();
+	const int jn = size - j0; /* the new row's place in this chunk, if 0 <= jn < n */
+	if (jn >= 0 && jn < n && h % G == 0 && tid < HL) {
+		kc[((size_t)kh * C + size) * HL + tid] = sk[tid];
+		vc[((size_t)kh * C + size) * HL + tid] = sv[tid];
+	}
+	const float *K = kc + ((size_t)kh * C + j0) * HL, *V = vc + ((size_t)kh * C + j0) * HL;
 	{
-		const int j = threadIdx.x / 4, d0 = (threadIdx.x % 4) * 32;
+		const int j = tid / 4, d0 = (tid % 4) * 32;
 		float acc = 0.0f;
 		if (j < n) {
-			const float4 *k4 = (const float4 *)(K + (size_t)j * HL + d0);
+			if (j == jn) {
 #pragma unroll
-			for (int u = 0; u < 8; u++) {
-				const float4 kv = k4[u];
-				acc = __builtin_fmaf(sq[d0 + 4 * u + 0], kv.x, acc);
-				acc = __builtin_fmaf(sq[d0 + 4 * u + 1], kv.y, acc);
-				acc = __builtin_fmaf(sq[d0 + 4 * u + 2], kv.z, acc);
-				acc = __builtin_fmaf(sq[d0 + 4 * u + 3], kv.w, acc);
+				for (int u = 0; u < 32; u++)
+					acc = __builtin_fmaf(sq[d0 + u], sk[d0 + u], acc);
+			} else {
+				const float4 *k4 = (const float4 *)(K + (size_t)j * HL + d0);
+#pragma unroll
+				for (int u = 0; u < 8; u++) {
+					const float4 kv = k4[u];
+					acc = __builtin_fmaf(sq[d0 + 4 * u + 0], kv.x, acc);
+					acc = __builtin_fmaf(sq[d0 + 4 * u + 1], kv.y, acc);
+					acc = __builtin_fmaf(sq[d0 + 4 * u + 2], kv.z, acc);
+					acc = __builtin_fmaf(sq[d0 + 4 * u + 3], kv.w, acc);
+				}
 			}
 		}
 		acc += __shfl_xor(acc, 1, WAVE);
 		acc += __shfl_xor(acc, 2, WAVE);
-		if (threadIdx.x % 4 == 0 && j < CH)
+		if (tid % 4 == 0)
 			sp[j] = j < n ? acc / scale_div : -INFINITY;
 	}
 	__syncthreads();
-	const float m = block_max(threadIdx.x < CH ? sp[threadIdx.x] : -INFINITY, red);
+	const float m = block_max(tid < CH ? sp[tid] : -INFINITY, red);
 	float e = 0.0f;
-	if (threadIdx.x < CH) {
-		e = threadIdx.x < n ? moe_expf(sp[threadIdx.x] - m) : 0.0f;
-		sp[threadIdx.x] = e;
+	if (tid < CH) {
+		e = tid < n ? moe_expf(sp[tid] - m) : 0.0f;
+		sp[tid] = e;
 	}
 	const float l = block_sum(e, red); /* its barriers also publish sp */
-	/* o[d] = sum_j e_j v[j][d]: two halves of the positions */
 	{
-		const int d = threadIdx.x % HL, half = threadIdx.x / HL;
+		const int d = tid % HL, half = tid / HL;
 		float o = 0.0f;
 		for (int j = half; j < n; j += LM_NT / HL)
-			o = __builtin_fmaf(sp[j], V[(size_t)j * HL + d], o);
-		so[threadIdx.x] = o;
+			o = __builtin_fmaf(sp[j], j == jn ? sv[d] : V[(size_t)j * HL + d], o);
+		so[tid] = o;
 	}
 	__syncthreads();
-	if (threadIdx.x < HL) {
-		float o = so[threadIdx.x];
-		for (int k = 1; k < LM_NT / HL; k++)
-			o += so[threadIdx.x + k * HL];
-		pp[2 + threadIdx.x] = o;
+	float o = 0.0f;
+	if (tid < HL) {
+		o = so[tid];
+		for (int u = 1; u < LM_NT / HL; u++)
+			o += so[tid + u * HL];
 	}
-	if (threadIdx.x == 0) {
-		pp[0] = m;
-		pp[1] = l;
+	if (nact == 1) { /* the whole context in one chunk: no merge */
+		if (tid < HL)
+			out[h * HL + tid] = o / l;
+		return;
+	}
+	uint64_t *pp = part + ((size_t)h * nstride + c) * (HL + 2);
+	if (tid < HL)
+		st_dev_u64(&pp[2 + tid], tagged(tag, o));
+	if (tid == 0) {
+		st_dev_u64(&pp[0], tagged(tag, n > 0 ? m : -INFINITY));
+		st_dev_u64(&pp[1], tagged(tag, l));
+	}
+	if (!last_to_arrive(&cnt[h], (u32)nact, &s_flag))
+		return;
+	/* merge the head's nact chunks */
+	const uint64_t *ph = part + (size_t)h * nstride * (HL + 2);
+	gather_tagged(ph, HL + 2, nact, tag, st,
+		      [&](int cc, u32 b) { s_f[cc] = __builtin_bit_cast(float, b); });
+	gather_tagged(ph + 1, HL + 2, nact, tag, st,
+		      [&](int cc, u32 b) { s_l[cc] = __builtin_bit_cast(float, b); });
+	__syncthreads();
+	float M = -INFINITY;
+	for (int cc = 0; cc < nact; cc++)
+		M = fmaxf(M, s_f[cc]);
+	__syncthreads();
+	for (int cc = tid; cc < nact; cc += LM_NT)
+		s_f[cc] = s_l[cc] > 0.0f ? moe_expf(s_f[cc] - M) : 0.0f;
+	__syncthreads();
+	if (tid < HL) {
+		float L = 0.0f, acc = 0.0f;
+		for (int c0 = 0; c0 < nact; c0 += 8) {
+			/* eight loads in flight, then a poll only for a late one */
+			uint64_t vv[8];
+#pragma unroll
+			for (int u = 0; u < 8; u++)
+				vv[u] = c0 + u < nact ? ld_dev_u64(&ph[(size_t)(c0 + u) * (HL + 2) + 2 + tid])
+						      : 0;
+#pragma unroll
+			for (int u = 0; u < 8; u++) {
+				const int cc = c0 + u;
+				if (cc >= nact)
+					break;
+				const u32 ob = (u32)(vv[u] >> 32) == tag
+						       ? (u32)vv[u]
+						       : poll_tag(&ph[(size_t)cc * (HL + 2) + 2 + tid], tag, st);
+				const float f = s_f[cc];
+				L = __builtin_fmaf(f, s_l[cc], L);
+				acc = __builtin_fmaf(f, __builtin_bit_cast(float, ob), acc);
+			}
+		}
+		out[h * HL + tid] = acc / L;
 	}
 }
 
-/* out[h * HL + d] = sum_c exp(m_c - M) o_c[d] / sum_c exp(m_c - M) l_c:
- * one workgroup of HL threads per head */
-__global__ __launch_bounds__(LM_HLEN) void k_attn_merge(const float *__restrict__ part,
-							float *__restrict__ out, int nchunk)
+/* ---------------------------------------------------------------------- */
+/* k_lm_oproj                                                             */
+/* ---------------------------------------------------------------------- */
+
+/*
+ * out[E] = add + x . Wo^T (the residual stream after attention), each row
+ * also stored tagged in rows_t; the last workgroup to finish reads them
+ * all back and writes x_out = rms_norm(out) * w (the MoE layer's input).
+ */
+template <int WT, int C>
+__global__ __launch_bounds__(LM_NT) __attribute__((amdgpu_waves_per_eu(4)))
+void k_lm_oproj(const uint8_t *__restrict__ W, size_t rb, int N, int K,
+		const float *__restrict__ x, const float *__restrict__ add, float *__restrict__ out,
+		uint64_t *rows_t, u32 *cnt, const float *__restrict__ w, float *__restrict__ x_out,
+		LmState *st, int layer)
 {
-	constexpr int HL = LM_HLEN;
-	const int h = blockIdx.x, d = threadIdx.x;
-	const float *pp = part + (size_t)h * nchunk * (HL + 2);
-	float M = -INFINITY;
-	for (int c = 0; c < nchunk; c++)
-		M = fmaxf(M, pp[(size_t)c * (HL + 2)]);
-	float L = 0.0f, o = 0.0f;
-	for (int c = 0; c < nchunk; c++) {
-		const float *pc = pp + (size_t)c * (HL + 2);
-		if (pc[1] == 0.0f)
-			continue;
-		const float f = moe_expf(pc[0] - M);
-		L = __builtin_fmaf(f, pc[1], L);
-		o = __builtin_fmaf(f, pc[2 + d], o);
+	extern __shared__ __attribute__((aligned(16))) float sx[];
+	__shared__ float red[LM_NT / WAVE];
+	__shared__ int s_flag;
+	const u32 tag = lm_tag(st, layer);
+	auto hook = [=](int row, float r) { st_dev_u64(&rows_t[row], tagged(tag, r)); };
+	qgemv_body<WT, C, true>(sx, W, rb, N, K, x, 1, 1, add, 0, out, hook);
+	if (!last_to_arrive(cnt, gridDim.x, &s_flag))
+		return;
+	float ss = 0.0f;
+	gather_tagged(rows_t, 1, N, tag, st, [&](int i, u32 b) {
+		const float v = __builtin_bit_cast(float, b);
+		sx[i] = v;
+		const float t = v * v;
+		ss = ss + t;
+	});
+	const float rms = sqrtf(block_sum(ss, red) / (float)N + 1e-5f);
+	for (int i = threadIdx.x; i < N; i += LM_NT) {
+		const float r = sx[i] / rms;
+		x_out[i] = r * w[i];
 	}
-	out[h * HL + d] = o / L;
+}
+
+/* ---------------------------------------------------------------------- */
+/* k_lm_head                                                              */
+/* ---------------------------------------------------------------------- */
+
+__device__ static inline void better(float &bv, int &bi, float v, int i)
+{
+	if (v > bv || (v == bv && i < bi)) {
+		bv = v;
+		bi = i;
+	}
 }
 
 /*
- * The greedy pick: the first index of the maximum (main.c:189-193 keeps
- * the lowest index among equal maxima), written as the next token and into
- * tokens[step]; then the counters advance (step, pos, size).  One
- * workgroup of LM_ARG_NT threads.
+ * logits[V] = rms_norm(a + b) * w . lm_head^T; every workgroup's first
+ * maximum goes out tagged, and the last workgroup picks the first maximum
+ * of all (main.c:189-193), writes it as the next token and tokens[step],
+ * and advances the counters (olmoe_generate: model->pos++, the cache row,
+ * the step and the epoch).
  */
-__global__ __launch_bounds__(LM_ARG_NT) void k_argmax(const float *__restrict__ logits, int V,
-						      LmState *__restrict__ st,
-						      int *__restrict__ tokens)
+template <int WT, int C>
+__global__ __launch_bounds__(LM_NT) __attribute__((amdgpu_waves_per_eu(4)))
+void k_lm_head(const uint8_t *__restrict__ W, size_t rb, int N, int K, const float *a,
+	       const float *b, const float *__restrict__ w, float *__restrict__ out,
+	       uint64_t *best, u32 *cnt, LmState *st, int *tokens)
 {
-	__shared__ float sv[LM_ARG_NT / WAVE];
-	__shared__ int si[LM_ARG_NT / WAVE];
+	extern __shared__ __attribute__((aligned(16))) float sx[];
+	__shared__ float red[LM_NT / WAVE];
+	__shared__ float s_v[LM_NT / WAVE];
+	__shared__ int s_i[LM_NT / WAVE];
+	__shared__ int s_flag;
+	const u32 tag = lm_tag(st, LM_HEAD_SLOT);
+	stage_norm<WT>(sx, red, K, a, b, nullptr, w, nullptr);
 	float bv = -INFINITY;
 	int bi = 0x7fffffff;
-	for (int i = threadIdx.x; i < V; i += LM_ARG_NT) {
-		const float v = logits[i];
-		if (v > bv) { /* increasing i: keeps the first of equal values */
-			bv = v;
-			bi = i;
-		}
-	}
-	for (int o = WAVE / 2; o > 0; o >>= 1) {
-		const float ov = __shfl_xor(bv, o, WAVE);
-		const int oi = __shfl_xor(bi, o, WAVE);
-		if (ov > bv || (ov == bv && oi < bi)) {
-			bv = ov;
-			bi = oi;
-		}
-	}
+	auto hook = [&](int row, float r) { better(bv, bi, r, row); };
+	qgemv_body<WT, C, true, true>(sx, W, rb, N, K, nullptr, 1, 1, nullptr, 0, out, hook);
+	for (int o = WAVE / 2; o > 0; o >>= 1)
+		better(bv, bi, __shfl_xor(bv, o, WAVE), __shfl_xor(bi, o, WAVE));
 	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
 	if (lane == 0) {
-		sv[wave] = bv;
-		si[wave] = bi;
+		s_v[wave] = bv;
+		s_i[wave] = bi;
 	}
 	__syncthreads();
 	if (threadIdx.x == 0) {
-		for (int w = 1; w < LM_ARG_NT / WAVE; w++)
-			if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) {
-				bv = sv[w];
-				bi = si[w];
-			}
-		/* no value above -inf (all NaN or -inf): index 0, as the loop of
-		 * main.c leaves it */
+		for (int u = 1; u < LM_NT / WAVE; u++)
+			better(bv, bi, s_v[u], s_i[u]);
+		st_dev_u64(&best[2 * blockIdx.x], tagged(tag, bv));
+		st_dev_u64(&best[2 * blockIdx.x + 1], ((uint64_t)tag << 32) | (u32)bi);
+	}
+	if (!last_to_arrive(cnt, gridDim.x, &s_flag))
+		return;
+	bv = -INFINITY;
+	bi = 0x7fffffff;
+	/* entries 2g (value) and 2g + 1 (index) of workgroup g */
+	__shared__ float s_bv[LM_MAX_HEAD_WG];
+	gather_tagged(best, 2, (int)gridDim.x, tag, st,
+		      [&](int g, u32 b) { s_bv[g] = __builtin_bit_cast(float, b); });
+	gather_tagged(best + 1, 2, (int)gridDim.x, tag, st,
+		      [&](int g, u32 b) { better(bv, bi, s_bv[g], (int)b); });
+	for (int o = WAVE / 2; o > 0; o >>= 1)
+		better(bv, bi, __shfl_xor(bv, o, WAVE), __shfl_xor(bi, o, WAVE));
+	if (lane == 0) {
+		s_v[wave] = bv;
+		s_i[wave] = bi;
+	}
+	__syncthreads();
+	if (threadIdx.x == 0) {
+		for (int u = 1; u < LM_NT / WAVE; u++)
+			better(bv, bi, s_v[u], s_i[u]);
+		/* no value above -inf (all NaN): index 0, as main.c's loop leaves it */
 		const int tok = bi == 0x7fffffff ? 0 : bi;
 		st->tok = tok;
 		if (tokens)
 			tokens[st->step] = tok;
+		st->step += 1;
+		st->pos += 1;
+		st->size += 1;
+		st->epoch += 1;
 	}
 }
 
-/* the step's counters advance: step, pos, cache size */
-__global__ void k_step_end(LmState *st)
+/* the step's counters advance (a step without the lm_head) */
+__global__ void k_lm_step_end(LmState *st)
 {
 	if (threadIdx.x == 0) {
 		st->step += 1;
 		st->pos += 1;
 		st->size += 1;
+		st->epoch += 1;
 	}
 }
 
-/* kvcache_rotate: rows [drop, drop + keep) of every (layer, kv head) move
- * to [0, keep); grid (rows of one move, heads * layers).  Reads all rows of
- * a (layer, head) slab before writing (rows are copied through registers
- * in order of the destination, so drop >= keep or a copy per row keeps
- * sources intact: the host guarantees drop >= keep or uses a staging
- * buffer). */
-__global__ void k_kv_copy_rows(const float *__restrict__ src, float *__restrict__ dst,
+/* kvcache_rotate's moves: dst[s * slab + i] = src[s * slab + i] */
+__global__ void k_lm_copy_rows(const float *__restrict__ src, float *__restrict__ dst,
 			       size_t slab, size_t n)
 {
 	const size_t s = blockIdx.y;
@@ -376,39 +583,82 @@ __global__ void k_kv_copy_rows(const float *__restrict__ src, float *__restrict_
 }
 
 /* ---------------------------------------------------------------------- */
+/* launchers                                                              */
+/* ---------------------------------------------------------------------- */
 
-extern "C" int lm_launch_embed(int wtype, const uint8_t *wte, int E, const LmState *st,
-			       const int *prompt, float *hidden, void *stream)
+static size_t tok_lds(int K)
 {
-	hipStream_t s = (hipStream_t)stream;
-	if (wtype == 1)
-		hipLaunchKernelGGL(k_embed<1>, dim3(1), dim3(LM_NT), 0, s, wte, E, st, prompt, hidden);
-	else if (wtype == 2)
-		hipLaunchKernelGGL(k_embed<2>, dim3(1), dim3(LM_NT), 0, s, wte, E, st, prompt, hidden);
-	else
-		return (int)hipErrorInvalidValue;
-	return (int)hipGetLastError();
+	return (size_t)(K / MOE_SEG_COLS) * SEG_STRIDE * sizeof(float);
 }
 
-extern "C" int lm_launch_add_rmsnorm(const float *a, const float *b, float *h, const float *w,
-				     float *x, int E, void *stream)
+/* the instance of kind k (0 qkv, 1 oproj, 2 head) for (wtype, K) */
+static const void *lm_kernel(int kind, int wtype, int K)
 {
-	if (E < 1 || E > 32 * LM_NT)
-		return (int)hipErrorInvalidValue;
-	hipLaunchKernelGGL(k_add_rmsnorm, dim3(1), dim3(LM_NT), 0, (hipStream_t)stream, a, b, h, w,
-			   x, E);
-	return (int)hipGetLastError();
+	const int C = moe_lanes_per_row((size_t)K);
+#define LMK(WTT, CC)                                                                    \
+	if (wtype == WTT && C == CC)                                                    \
+		return kind == 0 ? (const void *)k_lm_qkv<WTT, CC>                       \
+		       : kind == 1 ? (const void *)k_lm_oproj<WTT, CC>                   \
+				   : (const void *)k_lm_head<WTT, CC>;
+	LMK(1, 4) LMK(1, 8) LMK(1, 16) LMK(1, 32) LMK(1, 64)
+	LMK(2, 4) LMK(2, 8) LMK(2, 16) LMK(2, 32) LMK(2, 64)
+#undef LMK
+	return nullptr;
 }
 
-extern "C" int lm_launch_qk_rope_kv(float *qkv, const float *q_norm, const float *k_norm,
-				    const float *freq, const LmState *st, float *kc, float *vc,
-				    int H, int KH, int HL, int C, void *stream)
+extern "C" int lm_gemv_grid(int kind, int wtype, int K, int N)
 {
-	if (HL != LM_HLEN || KH < 1 || H % KH)
+	const void *fn = lm_kernel(kind, wtype, K);
+	int dev = 0, ncu = 0, per = 0;
+	if (!fn || hipGetDevice(&dev) != hipSuccess ||
+	    hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+	    hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, fn, LM_NT, tok_lds(K)) != hipSuccess ||
+	    per < 1)
+		return 0;
+	const int C = moe_lanes_per_row((size_t)K);
+	const int ngroups = (N + QG_WAVES * (WAVE / C) - 1) / (QG_WAVES * (WAVE / C));
+	return min(ngroups, per * ncu);
+}
+
+extern "C" int lm_launch_qkv(int wtype, const uint8_t *W, int N, int K, const float *a,
+			     const float *b, const float *w, float *h_out, const uint8_t *wte,
+			     const LmState *st, const int *prompt, float *out, int grid,
+			     void *stream)
+{
+	const void *fn = lm_kernel(0, wtype, K);
+	if (!fn || grid < 1)
 		return (int)hipErrorInvalidValue;
-	hipLaunchKernelGGL(k_qk_rope_kv, dim3(1), dim3(LM_NT), 0, (hipStream_t)stream, qkv, q_norm,
-			   k_norm, freq, st, kc, vc, H, KH, HL, C);
-	return (int)hipGetLastError();
+	size_t rb = (size_t)(K / MOE_QK) * (wtype == 1 ? 34 : 18);
+	void *args[] = {&W, &rb, &N, &K, &a, &b, &w, &h_out, &wte, &st, &prompt, &out};
+	return (int)hipLaunchKernel(fn, dim3(grid), dim3(LM_NT), args, tok_lds(K),
+				    (hipStream_t)stream);
+}
+
+extern "C" int lm_launch_oproj(int wtype, const uint8_t *W, int N, int K, const float *x,
+			       const float *add, float *out, uint64_t *rows_t, uint32_t *cnt,
+			       const float *w, float *x_out, LmState *st, int layer, int grid,
+			       void *stream)
+{
+	const void *fn = lm_kernel(1, wtype, K);
+	if (!fn || grid < 1 || N > (int)(tok_lds(K) / sizeof(float)))
+		return (int)hipErrorInvalidValue;
+	size_t rb = (size_t)(K / MOE_QK) * (wtype == 1 ? 34 : 18);
+	void *args[] = {&W, &rb, &N, &K, &x, &add, &out, &rows_t, &cnt, &w, &x_out, &st, &layer};
+	return (int)hipLaunchKernel(fn, dim3(grid), dim3(LM_NT), args, tok_lds(K),
+				    (hipStream_t)stream);
+}
+
+extern "C" int lm_launch_head(int wtype, const uint8_t *W, int N, int K, const float *a,
+			      const float *b, const float *w, float *out, uint64_t *best,
+			      uint32_t *cnt, LmState *st, int *tokens, int grid, void *stream)
+{
+	const void *fn = lm_kernel(2, wtype, K);
+	if (!fn || grid < 1 || grid > LM_MAX_HEAD_WG)
+		return (int)hipErrorInvalidValue;
+	size_t rb = (size_t)(K / MOE_QK) * (wtype == 1 ? 34 : 18);
+	void *args[] = {&W, &rb, &N, &K, &a, &b, &w, &out, &best, &cnt, &st, &tokens};
+	return (int)hipLaunchKernel(fn, dim3(grid), dim3(LM_NT), args, tok_lds(K),
+				    (hipStream_t)stream);
 }
 
 extern "C" int lm_attn_chunks(int C, int window)
@@ -417,34 +667,24 @@ extern "C" int lm_attn_chunks(int C, int window)
 	return (span + LM_CHUNK - 1) / LM_CHUNK;
 }
 
-extern "C" int lm_launch_attention(const float *q, const float *kc, const float *vc,
-				   const LmState *st, float *part, float *out, int H, int KH,
-				   int C, int window, float scale_div, void *stream)
+extern "C" int lm_launch_attn(const float *qkv, const float *q_norm, const float *k_norm,
+			      const float *freq, LmState *st, float *kc, float *vc,
+			      uint64_t *part, uint32_t *cnt, float *out, int H, int KH, int C,
+			      int window, float scale_div, int layer, int nact, void *stream)
 {
-	hipStream_t s = (hipStream_t)stream;
 	const int nch = lm_attn_chunks(C, window);
-	if (KH < 1 || H % KH)
+	if (KH < 1 || H % KH || nch > LM_MAX_CHUNKS || nact < 1 || nact > nch || layer < 0 ||
+	    layer >= LM_HEAD_SLOT)
 		return (int)hipErrorInvalidValue;
-	hipLaunchKernelGGL(k_attn_part, dim3(H, nch), dim3(LM_NT), 0, s, q, kc, vc, st, part, H,
-			   KH, C, window, scale_div);
-	hipError_t e = hipGetLastError();
-	if (e != hipSuccess)
-		return (int)e;
-	hipLaunchKernelGGL(k_attn_merge, dim3(H), dim3(LM_HLEN), 0, s, part, out, nch);
-	return (int)hipGetLastError();
-}
-
-extern "C" int lm_launch_argmax(const float *logits, int V, LmState *st, int *tokens,
-				void *stream)
-{
-	hipLaunchKernelGGL(k_argmax, dim3(1), dim3(LM_ARG_NT), 0, (hipStream_t)stream, logits, V,
-			   st, tokens);
+	hipLaunchKernelGGL(k_lm_attn, dim3(H, nact), dim3(LM_NT), 0, (hipStream_t)stream, qkv,
+			   q_norm, k_norm, freq, st, kc, vc, part, cnt, out, H, KH, C, window,
+			   scale_div, layer, nch);
 	return (int)hipGetLastError();
 }
 
 extern "C" int lm_launch_step_end(LmState *st, void *stream)
 {
-	hipLaunchKernelGGL(k_step_end, dim3(1), dim3(64), 0, (hipStream_t)stream, st);
+	hipLaunchKernelGGL(k_lm_step_end, dim3(1), dim3(64), 0, (hipStream_t)stream, st);
 	return (int)hipGetLastError();
 }
 
@@ -453,7 +693,7 @@ extern "C" int lm_launch_copy_rows(const float *src, float *dst, size_t slab, si
 {
 	if (slabs == 0 || n == 0)
 		return 0;
-	hipLaunchKernelGGL(k_kv_copy_rows, dim3(64, (unsigned)slabs), dim3(256), 0,
+	hipLaunchKernelGGL(k_lm_copy_rows, dim3(64, (unsigned)slabs), dim3(256), 0,
 			   (hipStream_t)stream, src, dst, slab, n);
 	return (int)hipGetLastError();
 }

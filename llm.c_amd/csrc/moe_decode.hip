@@ -89,35 +89,6 @@ struct DecodeArgs {
 	int spin;       /* poll rounds after which a wait gives up (MOE_SPIN_DEFAULT) */
 };
 
-/* device-coherent accesses (global_{load,store} ... sc1) */
-__device__ static inline void st_dev_u32(u32 *p, u32 v)
-{
-	__hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ static inline void st_dev_u64(uint64_t *p, uint64_t v)
-{
-	__hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ static inline u32 ld_dev_u32(const u32 *p)
-{
-	return __hip_atomic_load((u32 *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ static inline uint64_t ld_dev_u64(const uint64_t *p)
-{
-	return __hip_atomic_load((uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ static inline void backoff(int &step)
-{
-	switch (step) {
-	case 0: __builtin_amdgcn_s_sleep(1); break;
-	case 1: __builtin_amdgcn_s_sleep(2); break;
-	case 2: __builtin_amdgcn_s_sleep(4); break;
-	default: __builtin_amdgcn_s_sleep(8); break;
-	}
-	step += step < 3;
-}
-
 /* balanced split of n items over G workgroups: b gets [item_lo(b), item_lo(b+1));
  * n * G < 2^31 (n <= 64 pairs * 2048 chunks, G <= 4096) */
 __host__ __device__ static inline int item_lo(int b, int n, int G)

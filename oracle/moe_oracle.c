@@ -23,6 +23,7 @@
  */
 #define _GNU_SOURCE
 #include "moe_oracle.h"
+#include "oracle_pool.h"
 
 #include <math.h>
 #include <pthread.h>
@@ -94,17 +95,33 @@ float orc_dot_f32(const float *x, const float *y, size_t n)
 	return dot_f32(x, y, n);
 }
 
+struct router_job {
+	const float *x, *wr, *bias;
+	size_t T, E, NE;
+	float *logits;
+};
+
+/* thread tidx takes a contiguous chunk of the T * NE logits */
+static void router_task(void *arg, int tidx, int nt)
+{
+	const struct router_job *w = arg;
+	const size_t n = w->T * w->NE, chunk = (n + nt - 1) / nt;
+	const size_t i0 = tidx * chunk, i1 = i0 + chunk < n ? i0 + chunk : n;
+	for (size_t i = i0; i < i1; i++) {
+		const size_t t = i / w->NE, j = i % w->NE;
+		float init = w->bias ? w->bias[j] : 0.0f;
+		w->logits[i] = init + dot_f32(&w->x[t * w->E], &w->wr[j * w->E], w->E);
+	}
+}
+
 void orc_router(const float *x, const float *wr, const float *bias,
 		size_t T, size_t E, size_t NE, float *logits)
 {
 	/* mma_init (matmul.c:13-33) seeds with the bias row or zero; the GEMV
 	 * (matmul.c:115-118) and the tiled path (matmul.c:213-238) then add one
 	 * complete dot per element, in the same per-element order. */
-	for (size_t t = 0; t < T; t++)
-		for (size_t j = 0; j < NE; j++) {
-			float init = bias ? bias[j] : 0.0f;
-			logits[t * NE + j] = init + dot_f32(&x[t * E], &wr[j * E], E);
-		}
+	struct router_job w = {x, wr, bias, T, E, NE, logits};
+	orc_pool_run(router_task, &w, orc_pool_threads(T, E, NE));
 }
 
 /* tensor.c:479-517 (value only) */
@@ -230,17 +247,38 @@ float orc_dot_quant(const float *x, const void *qrow, int wtype, size_t n)
  * (matmul.c:107-131 for T = 1, 145-165 for T > 1), which for Q8_0/Q4_0 is
  * dot_f32_quant (quant.c:656-668, 577-614).
  */
+struct qmat_job {
+	const float *x;
+	const void *q;
+	int wtype;
+	size_t T, N, K;
+	const float *add;
+	size_t add_len;
+	float *out;
+};
+
+/* thread tidx of nt takes output columns [tidx * ceil(N/nt), ...) of every
+ * token (transposed_gemv_thread_fn, matmul.c:107-114) */
+static void qmat_task(void *arg, int tidx, int nt)
+{
+	const struct qmat_job *w = arg;
+	const size_t rb = row_bytes(w->wtype, w->K), chunk = (w->N + nt - 1) / nt;
+	const size_t j0 = tidx * chunk, j1 = j0 + chunk < w->N ? j0 + chunk : w->N;
+	for (size_t t = 0; t < w->T; t++)
+		for (size_t j = j0; j < j1; j++) {
+			float init = !w->add ? 0.0f
+					     : w->add_len == w->N ? w->add[j] : w->add[t * w->N + j];
+			w->out[t * w->N + j] =
+				init + orc_dot_quant(&w->x[t * w->K], (const uint8_t *)w->q + j * rb,
+						     w->wtype, w->K);
+		}
+}
+
 void orc_qmat_mul(const float *x, size_t T, const void *q, int wtype, size_t N, size_t K,
 		  const float *add, size_t add_len, float *out)
 {
-	const size_t rb = row_bytes(wtype, K);
-	for (size_t t = 0; t < T; t++)
-		for (size_t j = 0; j < N; j++) {
-			float init = !add ? 0.0f : add_len == N ? add[j] : add[t * N + j];
-			out[t * N + j] = init + orc_dot_quant(&x[t * K],
-							      (const uint8_t *)q + j * rb,
-							      wtype, K);
-		}
+	struct qmat_job w = {x, q, wtype, T, N, K, add, add_len, out};
+	orc_pool_run(qmat_task, &w, orc_pool_threads(T, K, N));
 }
 
 void orc_dequant_row(const void *qrow, int wtype, float *dst, size_t n)
@@ -265,22 +303,46 @@ void orc_dequant_row(const void *qrow, int wtype, float *dst, size_t n)
 	}
 }
 
+struct ffn_job {
+	const float *x;
+	const uint8_t *g8, *u8, *d8;
+	int wtype;
+	size_t E, EI;
+	float *h, *out;
+};
+
+/* nn.c:455-478: thread tidx's chunk of gate/up rows, then SwiGLU in place */
+static void ffn_gateup_task(void *arg, int tidx, int nt)
+{
+	const struct ffn_job *w = arg;
+	const size_t rb_in = row_bytes(w->wtype, w->E), chunk = (w->EI + nt - 1) / nt;
+	const size_t j0 = tidx * chunk, j1 = j0 + chunk < w->EI ? j0 + chunk : w->EI;
+	for (size_t j = j0; j < j1; j++) {
+		float g = orc_dot_quant(w->x, w->g8 + j * rb_in, w->wtype, w->E);
+		float u = orc_dot_quant(w->x, w->u8 + j * rb_in, w->wtype, w->E);
+		w->h[j] = (g / (1.0f + expf(-g))) * u;
+	}
+}
+
+/* nn.c:483-492: after the barrier, thread tidx's chunk of down rows */
+static void ffn_down_task(void *arg, int tidx, int nt)
+{
+	const struct ffn_job *w = arg;
+	const size_t rb_mid = row_bytes(w->wtype, w->EI), chunk = (w->E + nt - 1) / nt;
+	const size_t i0 = tidx * chunk, i1 = i0 + chunk < w->E ? i0 + chunk : w->E;
+	for (size_t i = i0; i < i1; i++)
+		w->out[i] = orc_dot_quant(w->h, w->d8 + i * rb_mid, w->wtype, w->EI);
+}
+
 void orc_fused_ffn(const float *x, const void *gate, const void *up,
 		   const void *down, int wtype, size_t E, size_t EI,
 		   float *h, float *out)
 {
-	const uint8_t *g8 = gate, *u8 = up, *d8 = down;
-	size_t rb_in = row_bytes(wtype, E), rb_mid = row_bytes(wtype, EI);
-
-	/* nn.c:460-478: gate/up rows, then SwiGLU in place */
-	for (size_t j = 0; j < EI; j++) {
-		float g = orc_dot_quant(x, g8 + j * rb_in, wtype, E);
-		float u = orc_dot_quant(x, u8 + j * rb_in, wtype, E);
-		h[j] = (g / (1.0f + expf(-g))) * u;
-	}
-	/* nn.c:490-492: down rows */
-	for (size_t i = 0; i < E; i++)
-		out[i] = orc_dot_quant(h, d8 + i * rb_mid, wtype, EI);
+	struct ffn_job w = {x, gate, up, down, wtype, E, EI, h, out};
+	/* fused_ffn_silu's thread_pool_run(.., 1, k, inter) (nn.c:534) */
+	const int nt = orc_pool_threads(1, E, EI);
+	orc_pool_run(ffn_gateup_task, &w, nt);
+	orc_pool_run(ffn_down_task, &w, nt);
 }
 
 struct moe_job {
@@ -360,8 +422,8 @@ void orc_moe_ffn(const float *x, float *out, size_t T,
 	float *logits = logits_out ? logits_out : malloc(T * NE * sizeof(float));
 	orc_router(x, wr, bias, T, E, NE, logits);
 
-	if (nthreads < 1)
-		nthreads = 1;
+	if (nthreads < 1 || orc_pool_active())
+		nthreads = 1; /* the pool threads each operation instead */
 	if ((size_t)nthreads > T)
 		nthreads = (int)T;
 	struct moe_job *jobs = calloc((size_t)nthreads, sizeof(*jobs));

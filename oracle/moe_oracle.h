@@ -80,6 +80,17 @@ void orc_expf_array(const float *in, float *out, size_t n);
 void orc_expf_bits(uint32_t bits0, size_t n, float *out, int nthreads);
 
 /*
+ * The reference's threading for timing the oracle as the CPU baseline: a
+ * persistent pool of nthreads spinning workers (the calling thread is one
+ * of them); each operation then runs on one thread below 16 Mi flops and
+ * on all of them above (thread_pool.c:25,178-185,208-238).  nthreads <= 1
+ * turns it off (the default: operations run on the calling thread; the
+ * nthreads arguments below split tokens instead).  Results do not change.
+ * Returns the pool size, 0 when off, -1 on failure.
+ */
+int orc_set_pool(int nthreads);
+
+/*
  * The OLMoE model (models/olmoe/olmoe.c) in decode mode, one token per
  * call: embedding (tensor_pick_rows tensor.c:263-294), per layer RMSNorm
  * (nn.c:8-51), q/k/v products, full-vector q/k RMSNorm, RoPE (nn.c:192-219),
