@@ -255,8 +255,11 @@ hip_moe_qmat *hip_moe_qmat_upload(const void *qdata, int wtype, size_t N, size_t
  * for every token), or is NULL (zero); any other add_len returns 0.  Each
  * output is fl(add + dot), the dot in fp32 in another order than the
  * reference's dot_f32_quant (which its default -DQ8_DOT build takes for
- * every T: matmul.c:107-131,145-165,285-312, quant.c:656-668): ~1e-6
- * relative.  Returns 1 on success, 0 if not applicable.
+ * every T: matmul.c:107-131,145-165,285-312, quant.c:656-668), each block
+ * as d * (sum((q + c) x) - c * sum(x)), c = 128 (Q8_0) or 8 (Q4_0):
+ * absolute error per output within 2^-24 * (32 (127 + c) + 31 c + 64 * 255)
+ * * (sum over blocks of |d| * sum |x|) to first order; ~1e-6 relative L2 on
+ * zero-mean activations.  Returns 1 on success, 0 if not applicable.
  */
 int hip_moe_qmat_mul(hip_moe_qmat *W, const float *x, size_t T, const float *add,
                      size_t add_len, float *out);

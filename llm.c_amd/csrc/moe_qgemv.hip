@@ -12,7 +12,13 @@
  * (-DQ8_DOT, Makefile:29) takes dot_q8_quant per element for any T
  * (matmul.c:107-131,145-165,285-312), which for Q8_0/Q4_0 is dot_f32_quant
  * (quant.c:577-614,656-668).  The dots here are the same products in
- * another order (two blocks per lane, then a lane tree), ~1e-6 relative.
+ * another order (two blocks per lane, then a lane tree), and each block's
+ * sum is taken as d * (sum((q + c) x) - c * sum(x)) with c = 128 (Q8_0) or
+ * 8 (Q4_0), the biased quant bytes converted directly.  Error bound, first
+ * order, per output: 2^-24 * (32 (127 + c) + 31 c + 64 * 255) * B with
+ * B = sum over blocks of |d| * sum |x| (the offset's cancellation makes it
+ * grow with sum |x|, not with |sum q x|).  Measured: ~1e-6 relative L2 on
+ * zero-mean activations, 1e-5 or less with a mean 16 times the spread.
  *
  * Bound: HBM.  Algorithmic bytes per call: N * K/32 * block bytes (34 for
  * Q8_0, 18 for Q4_0) + T*K*4 (x) + T*N*4 (out) (+ T*N*4 with add).

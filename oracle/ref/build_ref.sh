@@ -30,3 +30,18 @@ for f in ref_olmoe ref_llama ref_ops ref_q4; do
 done
 $CC -shared -o "$OUT/libref_moe.so" $OBJS -lm -lpthread
 echo "build_ref: built $OUT/libref_moe.so"
+
+# The integration lines of INTEGRATION.md around the reference's olmoe.c,
+# linked against the product library (tests/test_dropin.py).
+LIBDIR=$HERE/../../llm.c_amd
+if [ -f "$LIBDIR/libhip_moe.so" ]; then
+	$CC $FLAGS -I$HERE/../../include -c "$HERE/../../tests/native/dropin_olmoe.c" \
+		-o "$OUT/obj/dropin_olmoe.o"
+	DOBJS=""
+	for o in $OBJS; do
+		case "$o" in */ref_*) ;; *) DOBJS="$DOBJS $o" ;; esac
+	done
+	$CC -shared -o "$OUT/libdropin_olmoe.so" $DOBJS "$OUT/obj/dropin_olmoe.o" \
+		-L"$LIBDIR" -lhip_moe -Wl,-rpath,"\$ORIGIN/../../llm.c_amd" -lm -lpthread
+	echo "build_ref: built $OUT/libdropin_olmoe.so"
+fi

@@ -668,3 +668,38 @@ def test_gpu_qmat_graph_replays():
         for p in (d_x1, d_x6, d_a6, d_o1, d_o6):
             H.free(p)
         W.free()
+
+
+@pytest.mark.parametrize("wt,c", [(hipmoe.Q8_0, 128.0), (hipmoe.Q4_0, 8.0)])
+def test_gpu_qmat_mean_shifted_activations(wt, c):
+    """The product's dots take sum((q + c) x) - c * sum(x) per block (c = 128
+    for Q8_0, 8 for Q4_0), so their rounding grows with c * sum|x| rather
+    than with |sum q x|.  Activations with a mean far above their spread
+    (N(4, 0.25)) make that cancellation largest.  Bar: every output within
+    the first-order bound 2^-24 * (32 * (127 + c) + 31 * c + 64 * 255) *
+    B_j, with B_j = sum over blocks of |d_b| * sum over the block of |x_i|;
+    and the whole output within 1e-5 relative L2 of the oracle."""
+    N, K, T = 512, 2048, 2
+    q = hipmoe.synth_quant_matrix(SEED, 0x7a00 + wt, 0.02, wt, N, K)
+    x = hipmoe.synth_normal(SEED, 0x7a10 + wt, T * K, 4.0, 0.25).reshape(T, K)
+    W = hipmoe.QMat(q, wt, N, K)
+    got = W.mul(x)
+    W.free()
+    want = oracle.qmat_mul(x, q, wt, N, K)
+    # the exact product: d * q is exact in fp32 (|q| <= 127, fp16 d)
+    Wd = np.stack([oracle.dequant(q[j * hipmoe.row_bytes(wt, K):
+                                        (j + 1) * hipmoe.row_bytes(wt, K)], wt, K)
+                   for j in range(N)]).astype(np.float64)
+    exact = x.astype(np.float64) @ Wd.T
+    bb = 34 if wt == hipmoe.Q8_0 else 18
+    d = np.abs(q.reshape(N, K // 32, bb)[:, :, :2].copy().view(np.float16)[..., 0]
+               .astype(np.float64))                                    # [N][K/32]
+    xs = np.abs(x.astype(np.float64)).reshape(T, K // 32, 32).sum(axis=2)  # [T][K/32]
+    B = xs @ d.T                                                         # [T][N]
+    bound = 2.0 ** -24 * (32 * (127 + c) + 31 * c + 64 * 255) * B
+    dev = np.abs(got.astype(np.float64) - exact)
+    err = rel_l2(got, want)
+    say(f"qmat mean-shifted wt={wt}: rel L2 {err:.3e}, worst |err|/bound "
+        f"{float(np.max(dev / bound)):.3e}")
+    assert (dev <= bound).all()
+    assert err <= 1e-5
