@@ -63,10 +63,13 @@ WORKLOADS = {
     "olmoe_q8_lm_head": dict(kind="qmat", wtype=hipmoe.Q8_0, N=50304, Kc=2048, T=1),
     "mixtral_q4_lm_head": dict(kind="qmat", wtype=hipmoe.Q4_0, N=32000, Kc=4096, T=1),
     # the whole model, one generated token per step
-    "olmoe_full_decode": dict(kind="model", wtype=hipmoe.Q8_0, layers=16, E=2048, H=16,
-                              V=50304, NE=64, K=8, EI=1024, C=2048, prompt=16),
+    "olmoe_full_decode": dict(kind="model", arch="olmoe", wtype=hipmoe.Q8_0, layers=16, E=2048,
+                              H=16, KH=16, V=50304, NE=64, K=8, EI=1024, C=2048, prompt=16),
+    "mixtral_full_decode": dict(kind="model", arch="mixtral", wtype=hipmoe.Q4_0, layers=32,
+                                E=4096, H=32, KH=8, V=32000, NE=8, K=2, EI=14336, C=4096,
+                                prompt=1024, window=0, theta=1e6),
 }
-MODEL_METRIC = "OLMoE-shaped full-model decode tok/s & % of HBM roofline"
+MODEL_METRIC = "full-model decode tok/s & % of HBM roofline"
 
 
 def log(msg):
@@ -211,8 +214,16 @@ def bench_model(args, w, H):
     import hiplm
     wt, Lh, E, V, NE, K, EI, Cx = (w["wtype"], w["layers"], w["E"], w["V"], w["NE"], w["K"],
                                    w["EI"], w["C"])
+    H, KH = w["H"], w["KH"]
     t0 = time.perf_counter()
-    md = hiplm.synth_olmoe(SEED, Lh, E, w["H"], V, NE, K, EI, wt)
+    if w["arch"] == "olmoe":
+        md = hiplm.synth_olmoe(SEED, Lh, E, H, V, NE, K, EI, wt)
+    else:
+        # 32 layers of 8 Mixtral experts are ~26 GB of Q4_0: the layers share
+        # one generated set of values on the host, each uploaded to its own
+        # device memory (the bytes a step streams are those of 32 layers)
+        md = hiplm.synth_mixtral(SEED, Lh, E, H, KH, V, NE, K, EI, wt, theta=w["theta"],
+                                 window=w["window"], share_layers=True)
     prompt = hiplm.synth_prompt(SEED, w["prompt"], V)
     log(f"generated the model in {time.perf_counter() - t0:.1f} s")
     M = hiplm.LmModel(md, Cx)
@@ -223,22 +234,23 @@ def bench_model(args, w, H):
     # unique experts per layer and step, from eager steps' routing traces
     uniq = []
     tok = 0
-    for i, t in enumerate(list(prompt) + [None] * 8):
+    for i, t in enumerate(list(prompt[:16]) + [None] * 8):
         tok, _ = M.decode(int(t) if t is not None else tok)
         if t is None:
             uniq.append(np.mean([len(np.unique(r)) for r in M.trace()[1]]))
     mean_uniq = float(np.mean(uniq))
     M.reset()
-    M.generate(prompt, warm)  # captures the step graphs
+    M.generate(prompt[:16], warm)  # captures the step graphs of short contexts
     M.reset()
     toks, ms = M.generate(prompt, steps)
     ms_per_step = ms / steps
     tokens_per_s = steps / (ms / 1e3)
     bpw = 34 / 32 if wt == hipmoe.Q8_0 else 18 / 32
     expert = 3 * E * EI * bpw
-    attn_w = 4 * E * E * bpw
+    EQ, EKV = H * 128, KH * 128
+    attn_w = (2 * EQ + 2 * EKV) * E * bpw  # q, k, v rows of E columns, output E x EQ
     kv_rows = np.mean([w["prompt"] + s + 1 for s in range(1, steps + 1)])
-    per_layer = attn_w + NE * E * 4 + mean_uniq * expert + 2 * kv_rows * E * 4
+    per_layer = attn_w + NE * E * 4 + mean_uniq * expert + 2 * kv_rows * EKV * 4
     bytes_per_tok = Lh * per_layer + V * E * bpw + E * bpw
     achieved_gbs = bytes_per_tok / (ms_per_step / 1e3) / 1e9
     log(f"{steps} tokens in {ms:.2f} ms: {ms_per_step * 1e3:.1f} us/token, "
@@ -256,8 +268,9 @@ def bench_model(args, w, H):
         "n_gpus": 1, "steps": steps, "warmup": warm, "ms_per_step": round(ms_per_step, 6),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": args.workload, "layers": Lh, "d_model": E, "heads": w["H"],
-                   "vocab": V, "experts": NE, "topk": K, "d_ff": EI, "context": Cx,
+        "config": {"workload": args.workload, "layers": Lh, "d_model": E, "heads": H,
+                   "kv_heads": KH, "vocab": V, "experts": NE, "topk": K, "d_ff": EI,
+                   "context": Cx,
                    "weights": "Q8_0" if wt == hipmoe.Q8_0 else "Q4_0",
                    "prompt_tokens": w["prompt"], "graphs": True,
                    "mean_unique_experts": round(mean_uniq, 3),

@@ -35,7 +35,7 @@ struct lm_layer {
 struct hip_lm {
 	int arch, wtype, device;
 	size_t L, E, H, KH, HL, V, C, NE, K, EI, window;
-	float theta, scale_div;
+	float theta, scale; /* attention: scores / scale (OLMoE) or * scale (Mixtral) */
 	size_t EQ, EKV; /* rows of q, and of k (= of v) */
 	size_t weight_bytes;
 	hipStream_t stream;
@@ -228,8 +228,13 @@ hip_lm *hip_lm_upload(const hip_lm_desc *d)
 	M->EI = d->EI;
 	M->window = d->sliding_window;
 	M->theta = d->rope_theta;
-	/* hlen_sq = sqrt((scalar_t)HLEN) (olmoe.c:150) */
-	M->scale_div = (float)sqrt((double)(float)M->HL);
+	/* hlen_sq = sqrt((scalar_t)HLEN) (olmoe.c:150, llama.c:118): OLMoE
+	 * divides the scores by it, Mixtral's flash_attention multiplies them
+	 * by 1.0f / hlen_sq (llama.c:324) */
+	{
+		const float hlen_sq = (float)sqrt((double)(float)M->HL);
+		M->scale = d->arch == HIP_LM_OLMOE ? hlen_sq : 1.0f / hlen_sq;
+	}
 	M->EQ = M->H * M->HL;
 	M->EKV = M->KH * M->HL;
 	M->nch = lm_attn_chunks((int)M->C, (int)M->window);
@@ -413,8 +418,8 @@ static int enqueue_step(hip_lm *M, int head, int nact)
 				   M->grid_qkv, s), "norm + q/k/v");
 		LCHK(lm_launch_attn(M->d_qkv, y->q_norm, y->k_norm, M->d_freq, M->d_st, M->d_kc + co,
 				    M->d_vc + co, M->d_part, cnt_attn, M->d_attn, (int)M->H,
-				    (int)M->KH, (int)M->C, (int)M->window, M->scale_div, (int)l, nact,
-				    s), "attention");
+				    (int)M->KH, (int)M->C, (int)M->window, M->scale,
+				    M->arch != HIP_LM_OLMOE, (int)l, nact, s), "attention");
 		/* h1 = h0 + attn . Wo^T, moe_in = rms_norm(h1) */
 		LCHK(lm_launch_oproj(wt, y->wo, E, (int)M->EQ, M->d_attn, M->d_h0, M->d_h1,
 				     M->d_rows_t, cnt_o, y->ffn_norm, M->d_moe_in + l * M->E,

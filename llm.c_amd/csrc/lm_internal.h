@@ -51,7 +51,7 @@ int lm_attn_chunks(int C, int window);
 int lm_launch_attn(const float *qkv, const float *q_norm, const float *k_norm,
                    const float *freq, LmState *st, float *kc, float *vc, uint64_t *part,
                    uint32_t *cnt, float *out, int H, int KH, int C, int window,
-                   float scale_div, int layer, int nact, void *stream);
+                   float scale, int scale_mul, int layer, int nact, void *stream);
 
 /* chunks a step over a cache of `size` rows (before the step) reads */
 static inline int lm_attn_active(int size, int window)

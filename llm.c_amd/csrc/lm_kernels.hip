@@ -240,6 +240,10 @@ void k_lm_qkv(const uint8_t *__restrict__ W, size_t rb, int N, int K, const floa
 /* ---------------------------------------------------------------------- */
 
 /*
+ * Scores are q . k / scale (OLMoE's tensor_div_scalar by sqrt(HLEN),
+ * olmoe.c:295) or q . k * scale (Mixtral's flash_attention, scale =
+ * 1 / sqrt(HLEN), nn.c:578) as scale_mul says.
+ *
  * Grid (H, nact): nact = the chunks of LM_CHUNK rows that cover the cache
  * rows [lo, AT), AT = size + 1 (lo > 0 past a sliding window), which the
  * host knows for every step.  Workgroup (h, c) covers rows [j0, j0 + n);
@@ -257,8 +261,8 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 						   const float *__restrict__ freq, LmState *st,
 						   float *__restrict__ kc, float *__restrict__ vc,
 						   uint64_t *part, u32 *cnt, float *__restrict__ out,
-						   int H, int KH, int C, int window, float scale_div,
-						   int layer, int nstride)
+						   int H, int KH, int C, int window, float scale,
+						   int scale_mul, int layer, int nstride)
 {
 	constexpr int HL = LM_HLEN, CH = LM_CHUNK;
 	__shared__ float cs[HL / 2], sn[HL / 2], sq[HL], sk[HL], sv[HL], sp[CH], so[LM_NT];
@@ -363,7 +367,7 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 		acc += __shfl_xor(acc, 1, WAVE);
 		acc += __shfl_xor(acc, 2, WAVE);
 		if (tid % 4 == 0)
-			sp[j] = j < n ? acc / scale_div : -INFINITY;
+			sp[j] = j < n ? (scale_mul ? acc * scale : acc / scale) : -INFINITY;
 	}
 	__syncthreads();
 	const float m = block_max(tid < CH ? sp[tid] : -INFINITY, red);
@@ -670,15 +674,16 @@ extern "C" int lm_attn_chunks(int C, int window)
 extern "C" int lm_launch_attn(const float *qkv, const float *q_norm, const float *k_norm,
 			      const float *freq, LmState *st, float *kc, float *vc,
 			      uint64_t *part, uint32_t *cnt, float *out, int H, int KH, int C,
-			      int window, float scale_div, int layer, int nact, void *stream)
+			      int window, float scale, int scale_mul, int layer, int nact,
+			      void *stream)
 {
 	const int nch = lm_attn_chunks(C, window);
 	if (KH < 1 || H % KH || nch > LM_MAX_CHUNKS || nact < 1 || nact > nch || layer < 0 ||
 	    layer >= LM_HEAD_SLOT)
 		return (int)hipErrorInvalidValue;
 	hipLaunchKernelGGL(k_lm_attn, dim3(H, nact), dim3(LM_NT), 0, (hipStream_t)stream, qkv,
-			   q_norm, k_norm, freq, st, kc, vc, part, cnt, out, H, KH, C, window,
-			   scale_div, layer, nch);
+			   q_norm, k_norm, freq, st, kc, vc, part, cnt, out, H, KH, C, window, scale,
+			   scale_mul, layer, nch);
 	return (int)hipGetLastError();
 }
 

@@ -62,6 +62,56 @@ def synth_olmoe(seed: int, layers: int, E: int, H: int, V: int, NE: int, K: int,
     return md
 
 
+def synth_mixtral(seed: int, layers: int, E: int, H: int, KH: int, V: int, NE: int, K: int,
+                  EI: int, wtype: int = Q4_0, std: float = 0.02, norm_std: float = 0.0,
+                  theta: float = 1e6, window: int = 0, share_layers: bool = False) -> dict:
+    """A Mixtral-shaped model (models/llama/llama.c:80-175 tensors): H query
+    heads and KH kv heads of 128, NE experts in separate tensors (kept
+    stacked here, one row per expert), every matrix N(0, std) quantized to
+    wtype, the router fp32, norms 1 or N(1, norm_std).  share_layers: every
+    layer holds layer 0's arrays (the same values, still uploaded once per
+    layer) - for benchmarks of models too large to generate layer by layer."""
+    G = T_GLOBAL
+    HL = 128
+    md = dict(arch="mixtral", layers=layers, E=E, H=H, KH=KH, V=V, NE=NE, K=K, EI=EI,
+              wtype=wtype, theta=theta, window=window)
+    md["token_embd"] = hipmoe.synth_quant_matrix(seed, _stream(G, T_TOKEN_EMBD), std, wtype, V, E)
+    md["output"] = hipmoe.synth_quant_matrix(seed, _stream(G, T_OUTPUT), std, wtype, V, E)
+    md["output_norm"] = _norm(seed, G, T_OUTPUT_NORM, E, norm_std)
+    md["blk"] = []
+    for l in range(layers):
+        if share_layers and l > 0:
+            md["blk"].append(md["blk"][0])
+            continue
+        b = {}
+        for key, kind, rows, cols in (("q", T_ATTN_Q, H * HL, E), ("k", T_ATTN_K, KH * HL, E),
+                                      ("v", T_ATTN_V, KH * HL, E), ("o", T_ATTN_O, E, H * HL)):
+            b[key] = hipmoe.synth_quant_matrix(seed, _stream(l, kind), std, wtype, rows, cols)
+        for key, kind in (("attn_norm", T_ATTN_NORM), ("ffn_norm", T_FFN_NORM)):
+            b[key] = _norm(seed, l, kind, E, norm_std)
+        moe = hipmoe.synth_layer(seed, l, wtype, E, EI, NE, std, None)
+        b["router"], b["gate"], b["up"], b["down"] = (moe["router"], moe["gate"], moe["up"],
+                                                      moe["down"])
+        md["blk"].append(b)
+    return md
+
+
+def ptr_table_llama(md: dict):
+    """The flat table the llama oracle and harness take: token_embd, output,
+    output_norm, then per layer attn_norm, q, k, v, o, ffn_norm, router, the
+    NE gate experts, the NE up experts, the NE down experts."""
+    arrs = [md["token_embd"], md["output"], md["output_norm"]]
+    for b in md["blk"]:
+        arrs += [b[k] for k in ("attn_norm", "q", "k", "v", "o", "ffn_norm", "router")]
+        for key in ("gate", "up", "down"):
+            arrs += [b[key][e] for e in range(md["NE"])]
+    tab = (C.c_void_p * len(arrs))()
+    for i, a in enumerate(arrs):
+        assert a.flags["C_CONTIGUOUS"]
+        tab[i] = a.ctypes.data
+    return tab
+
+
 def synth_prompt(seed: int, n: int, V: int) -> np.ndarray:
     """n token ids in [0, V), a pure function of (seed, n, V)."""
     u = hipmoe.synth_normal(seed, _stream(T_GLOBAL, T_PROMPT), n, 0.0, 1.0).astype(np.float64)

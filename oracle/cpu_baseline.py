@@ -147,10 +147,18 @@ def bench_qmat(spec, seconds, pool):
 def bench_model(spec, seconds, pool):
     import hiplm
     import oracle
-    md = hiplm.synth_olmoe(SEED, spec["layers"], spec["E"], spec["H"], spec["V"], spec["NE"],
-                           spec["K"], spec["EI"], spec["wtype"])
+    if spec.get("arch", "olmoe") == "olmoe":
+        md = hiplm.synth_olmoe(SEED, spec["layers"], spec["E"], spec["H"], spec["V"],
+                               spec["NE"], spec["K"], spec["EI"], spec["wtype"])
+        tab = hiplm.ptr_table(md)
+    else:
+        md = hiplm.synth_mixtral(SEED, spec["layers"], spec["E"], spec["H"], spec["KH"],
+                                 spec["V"], spec["NE"], spec["K"], spec["EI"], spec["wtype"],
+                                 theta=spec["theta"], window=spec["window"], share_layers=True)
+        tab = hiplm.ptr_table_llama(md)
+    # a bounded sample: at most 16 prompt steps (untimed) before the timed ones
+    spec = dict(spec, prompt=min(spec["prompt"], 16))
     prompt = hiplm.synth_prompt(SEED, spec["prompt"], spec["V"])
-    tab = hiplm.ptr_table(md)
     m = oracle.OlmoeModel(md, spec["C"], tab)
     tok = 0
     for t in prompt:  # the prompt, untimed
@@ -164,7 +172,7 @@ def bench_model(spec, seconds, pool):
             break
     m.free()
     E, V = spec["E"], spec["V"]
-    ops = {"attn_products": nthreads_for(2 * E * E, pool),
+    ops = {"attn_products": nthreads_for(2 * E * spec["H"] * 128, pool),
            "expert_ffn": nthreads_for(2 * E * spec["EI"], pool),
            "lm_head": nthreads_for(2 * E * V, pool), "attention": 1}
     return done / el, (f"{done} greedy decode steps after a {spec['prompt']}-token prompt, "

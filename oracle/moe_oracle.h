@@ -121,6 +121,27 @@ void orc_olmoe_run(orc_olmoe *m, const int *prompt, size_t n_prompt, size_t n_ge
 
 void orc_olmoe_free(orc_olmoe *m);
 
+/*
+ * The Mixtral model (models/llama/llama.c with experts) in decode mode:
+ * as the OLMoE model without q/k norms, with QH query and KVH kv heads of
+ * E / QH (grouped-query attention), the FLASH_ATTENTION build's
+ * flash_attention (nn.c:544-655) with an optional sliding window, and
+ * renormalised top-k routing (llama.c:422-427).  ptrs: 3 + layers * (7 + 3
+ * * NE) pointers, token_embd, output, output_norm, then per layer
+ * attn_norm, attn_q, attn_k, attn_v, attn_output, ffn_norm, ffn_gate_inp,
+ * the NE gate, NE up and NE down expert matrices.
+ */
+typedef struct orc_llama orc_llama;
+
+orc_llama *orc_llama_new(size_t layers, size_t E, size_t QH, size_t KVH, size_t V, size_t NE,
+                         size_t topk, size_t EI, size_t C, float theta, size_t window,
+                         int wtype, const void *const *ptrs);
+int orc_llama_decode(orc_llama *m, int tok, int pos, float *logits, float *trace_moe_in,
+                     uint32_t *trace_ids, float *trace_w, int nthreads);
+void orc_llama_run(orc_llama *m, const int *prompt, size_t n_prompt, size_t n_gen,
+                   float *logits, int *tokens, int nthreads);
+void orc_llama_free(orc_llama *m);
+
 #ifdef __cplusplus
 }
 #endif

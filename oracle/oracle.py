@@ -55,6 +55,14 @@ def lib():
         L.orc_olmoe_run.restype = None
         L.orc_olmoe_free.argtypes = [vp]
         L.orc_olmoe_free.restype = None
+        L.orc_llama_new.argtypes = [sz, sz, sz, sz, sz, sz, sz, sz, sz, C.c_float, sz, i32, vp]
+        L.orc_llama_new.restype = vp
+        L.orc_llama_decode.argtypes = [vp, i32, i32, vp, vp, vp, vp, i32]
+        L.orc_llama_decode.restype = i32
+        L.orc_llama_run.argtypes = [vp, vp, sz, sz, vp, vp, i32]
+        L.orc_llama_run.restype = None
+        L.orc_llama_free.argtypes = [vp]
+        L.orc_llama_free.restype = None
         _lib = L
     return _lib
 
@@ -165,15 +173,25 @@ def expf_bits(bits0: int, n: int, nthreads=None):
 
 
 class OlmoeModel:
-    """The OLMoE decode step of the reference (orc_olmoe_*): md is a model
-    dict of llm.c_amd/hiplm.py (synth_olmoe), C the context length."""
+    """The decode step of the reference's OLMoE (orc_olmoe_*) or Mixtral
+    (orc_llama_*) model: md is a model dict of llm.c_amd/hiplm.py
+    (synth_olmoe / synth_mixtral), C the context length, table its pointer
+    table (hiplm.ptr_table / ptr_table_llama)."""
 
     def __init__(self, md: dict, C_ctx: int, table):
         self.md = md
         self.V, self.E, self.L, self.K = md["V"], md["E"], md["layers"], md["K"]
         self.table = table  # keeps the pointer table alive
-        self.h = lib().orc_olmoe_new(md["layers"], md["E"], md["H"], md["V"], md["NE"], md["K"],
+        L = lib()
+        if md["arch"] == "olmoe":
+            self._dec, self._run, self._free = L.orc_olmoe_decode, L.orc_olmoe_run, L.orc_olmoe_free
+            self.h = L.orc_olmoe_new(md["layers"], md["E"], md["H"], md["V"], md["NE"], md["K"],
                                      md["EI"], C_ctx, md["theta"], md["wtype"], table)
+        else:
+            self._dec, self._run, self._free = L.orc_llama_decode, L.orc_llama_run, L.orc_llama_free
+            self.h = L.orc_llama_new(md["layers"], md["E"], md["H"], md["KH"], md["V"], md["NE"],
+                                     md["K"], md["EI"], C_ctx, md["theta"], md["window"],
+                                     md["wtype"], table)
         self.pos = 0
 
     def decode(self, tok: int, trace: bool = False):
@@ -182,8 +200,7 @@ class OlmoeModel:
         mi = np.empty((self.L, self.E), np.float32) if trace else None
         ids = np.empty((self.L, self.K), np.uint32) if trace else None
         w = np.empty((self.L, self.K), np.float32) if trace else None
-        nxt = lib().orc_olmoe_decode(self.h, int(tok), self.pos, _p(lg), _p(mi), _p(ids), _p(w),
-                                     threads())
+        nxt = self._dec(self.h, int(tok), self.pos, _p(lg), _p(mi), _p(ids), _p(w), threads())
         self.pos += 1
         return (nxt, lg, (mi, ids, w)) if trace else (nxt, lg)
 
@@ -193,13 +210,13 @@ class OlmoeModel:
         pr = np.ascontiguousarray(prompt, np.int32)
         lg = np.empty((n_gen + 1, self.V), np.float32)
         toks = np.empty(n_gen + 1, np.int32)
-        lib().orc_olmoe_run(self.h, _p(pr), pr.size, n_gen, _p(lg), _p(toks), threads())
+        self._run(self.h, _p(pr), pr.size, n_gen, _p(lg), _p(toks), threads())
         self.pos += pr.size + n_gen
         return toks, lg
 
     def free(self):
         if self.h:
-            lib().orc_olmoe_free(self.h)
+            self._free(self.h)
             self.h = None
 
     def __del__(self):

@@ -133,12 +133,23 @@ def qmat_goldens(R):
 
 
 # name: (layers, E, H, V, NE, K, EI, C, wtype, norm_std, n_prompt, n_gen, logit stride)
-# The small case runs past its context (48 positions, C = 32: one
-# kvcache_rotate) with non-unit norms; the full case is the OLMoE-1B-7B shape
-# with unit norms, its logits kept at every 16th id plus each step's top 32.
+# (Mixtral cases add kv heads and the sliding window in MIXTRAL_EXTRA.)
+# The small cases run past their context (48 positions, C = 32: one
+# kvcache_rotate; Mixtral's with a sliding window of 20, the rows it keeps)
+# with non-unit norms; olmoe_full is the OLMoE-1B-7B shape with unit norms;
+# mixtral_2l two layers of the Mixtral-8x7B shape (32 query / 8 kv heads,
+# d_ff 14336, vocab 32000).  Logits are kept at every `stride`-th id plus
+# each step's top 32.
 MODEL_CASES = {
     "olmoe_small": (2, 1024, 8, 512, 64, 8, 512, 32, hipmoe.Q8_0, 0.1, 8, 40, 1),
     "olmoe_full": (16, 2048, 16, 50304, 64, 8, 1024, 2048, hipmoe.Q8_0, 0.0, 4, 4, 16),
+    "mixtral_small": (2, 2048, 16, 512, 8, 2, 1024, 32, hipmoe.Q4_0, 0.1, 8, 40, 1),
+    "mixtral_2l": (2, 4096, 32, 32000, 8, 2, 14336, 64, hipmoe.Q4_0, 0.0, 4, 4, 16),
+}
+# Mixtral cases: (kv heads, sliding window, rope theta)
+MIXTRAL_EXTRA = {
+    "mixtral_small": (4, 20, 1e6),
+    "mixtral_2l": (8, 0, 1e6),
 }
 MODEL_TOPN = 32
 
@@ -148,9 +159,18 @@ def model_case(name: str):
     from the seed."""
     import hiplm
     L, E, H, V, NE, K, EI, Cx, wt, nstd, n_prompt, n_gen, stride = MODEL_CASES[name]
-    md = hiplm.synth_olmoe(SEED, L, E, H, V, NE, K, EI, wt, 0.02, nstd)
+    if name in MIXTRAL_EXTRA:
+        KH, window, theta = MIXTRAL_EXTRA[name]
+        md = hiplm.synth_mixtral(SEED, L, E, H, KH, V, NE, K, EI, wt, 0.02, nstd, theta, window)
+    else:
+        md = hiplm.synth_olmoe(SEED, L, E, H, V, NE, K, EI, wt, 0.02, nstd)
     prompt = hiplm.synth_prompt(SEED, n_prompt, V)
     return md, prompt, MODEL_CASES[name]
+
+
+def model_table(md: dict):
+    import hiplm
+    return hiplm.ptr_table(md) if md["arch"] == "olmoe" else hiplm.ptr_table_llama(md)
 
 
 def model_digest(md: dict) -> str:
@@ -160,7 +180,8 @@ def model_digest(md: dict) -> str:
     for b in md["blk"]:
         for k in ("attn_norm", "q", "k", "v", "q_norm", "k_norm", "o", "ffn_norm", "router",
                   "gate", "up", "down"):
-            h.update(np.ascontiguousarray(b[k]).tobytes())
+            if k in b:
+                h.update(np.ascontiguousarray(b[k]).tobytes())
     return h.hexdigest()
 
 
@@ -171,17 +192,27 @@ def model_goldens(R, names):
     R.ref_olmoe_model_new.restype = vp
     R.ref_olmoe_model_run.argtypes = [vp, vp, sz, i32, sz, vp, vp]
     R.ref_olmoe_model_free.argtypes = [vp]
+    R.ref_llama_model_new.argtypes = [sz, sz, sz, sz, sz, sz, sz, sz, sz, C.c_float, sz, i32, vp]
+    R.ref_llama_model_new.restype = vp
+    R.ref_llama_model_run.argtypes = [vp, vp, sz, i32, sz, vp, vp]
+    R.ref_llama_model_free.argtypes = [vp]
     for name in names:
         md, prompt, case = model_case(name)
         L, E, H, V, NE, K, EI, Cx, wt, nstd, n_prompt, n_gen, stride = case
-        tab = hiplm.ptr_table(md)
+        tab = model_table(md)
         fx = dict(seed=SEED, prompt=prompt, sha_model=model_digest(md), stride=stride)
         for mode, prefill in (("dec", 0), ("pre", 1)):
-            h = R.ref_olmoe_model_new(L, E, H, V, NE, K, EI, Cx, md["theta"], wt, tab)
+            if md["arch"] == "olmoe":
+                h = R.ref_olmoe_model_new(L, E, H, V, NE, K, EI, Cx, md["theta"], wt, tab)
+                run, free = R.ref_olmoe_model_run, R.ref_olmoe_model_free
+            else:
+                h = R.ref_llama_model_new(L, E, H, md["KH"], V, NE, K, EI, Cx, md["theta"],
+                                          md["window"], wt, tab)
+                run, free = R.ref_llama_model_run, R.ref_llama_model_free
             lg = np.empty((n_gen + 1, V), np.float32)
             toks = np.empty(n_gen + 1, np.int32)
-            R.ref_olmoe_model_run(h, p(prompt), n_prompt, prefill, n_gen, p(lg), p(toks))
-            R.ref_olmoe_model_free(h)
+            run(h, p(prompt), n_prompt, prefill, n_gen, p(lg), p(toks))
+            free(h)
             top = np.argsort(-lg, axis=1, kind="stable")[:, :MODEL_TOPN].astype(np.int32)
             fx[f"{mode}_tokens"] = toks
             fx[f"{mode}_logits"] = np.ascontiguousarray(lg[:, ::stride])

@@ -1,6 +1,7 @@
 """GPU parity of the whole-model decode (include/hip_lm.h) through the C ABI,
-against the compiled reference's own OLMoE decode (tests/golden/model_*.npz,
-to which the model oracle is pinned bit for bit) and the oracle:
+against the compiled reference's own OLMoE and Mixtral decode
+(tests/golden/model_*.npz, to which the model oracle is pinned bit for bit)
+and the oracle:
 
   * teacher-forced steps (the prompt, then the reference's own picks as
     inputs): every step's logits within 1e-3 relative L2 of the
@@ -11,9 +12,12 @@ to which the model oracle is pinned bit for bit) and the oracle:
     took equal the oracle's routing of that layer's own router input;
   * generate (device-side greedy loop on replayed step graphs) gives the
     reference's tokens;
-  * the reduced model runs past its context (one kvcache_rotate); the
-    full OLMoE-1B-7B shape (16 layers, vocab 50304) checks the stored
-    logits (every 16th id and each step's top 32).
+  * the reduced models run past their context (one kvcache_rotate; the
+    Mixtral one keeps its sliding window of 20 rows, with grouped-query
+    attention, 16 query / 4 kv heads); the full OLMoE-1B-7B shape (16
+    layers, vocab 50304) and two layers of the Mixtral-8x7B shape (32 / 8
+    heads, d_ff 14336, vocab 32000) check the stored logits (every 16th id
+    and each step's top 32).
 """
 import sys
 
@@ -49,11 +53,12 @@ def safe_steps(top_logits):
 def check_routing(md, case, M):
     L, E, H, V, NE, K, EI, Cx, wt, nstd, n_prompt, n_gen, stride = case
     mi, ids, w = M.trace()
+    renorm = md["arch"] != "olmoe"
     for l in range(L):
         b = md["blk"][l]
         lay = dict(router=b["router"], gate=b["gate"], up=b["up"], down=b["down"], wtype=wt,
                    E=E, EI=EI, NE=NE)
-        oi, ow = oracle.moe_ffn(mi[l:l + 1], lay, K, False, None)[1:3]
+        oi, ow = oracle.moe_ffn(mi[l:l + 1], lay, K, renorm, None)[1:3]
         assert np.array_equal(ids[l], oi[0]), f"layer {l}: ids"
         assert np.array_equal(bits(w[l]), bits(ow[0])), f"layer {l}: weights"
 
@@ -61,7 +66,8 @@ def check_routing(md, case, M):
 def teacher_forced(name, tol, route_steps=()):
     md, prompt, case, g = model_case(name)
     L, E, H, V, NE, K, EI, Cx, wt, nstd, n_prompt, n_gen, stride = case
-    say(f"{name}: upload ({L} layers, E={E}, vocab {V}, context {Cx})")
+    say(f"{name}: upload ({L} layers, E={E}, heads {H}/{md.get('KH', H)}, vocab {V}, "
+        f"context {Cx}, window {md.get('window', 0)})")
     M = hiplm.LmModel(md, Cx)
     try:
         seq = list(prompt) + list(g["dec_tokens"][:-1])
@@ -101,3 +107,12 @@ def test_gpu_model_small_vs_reference():
 @pytest.mark.timeout(900)
 def test_gpu_model_full_shape_vs_reference():
     teacher_forced("olmoe_full", 1e-3, route_steps=(3, 7))
+
+
+def test_gpu_model_mixtral_small_vs_reference():
+    teacher_forced("mixtral_small", TIGHT, route_steps=(0, 7, 20, 40))
+
+
+@pytest.mark.timeout(900)
+def test_gpu_model_mixtral_layer_shape_vs_reference():
+    teacher_forced("mixtral_2l", 1e-3, route_steps=(3, 7))

@@ -1,11 +1,13 @@
-"""Pins the model oracle (oracle/lm_oracle.c: the OLMoE decode step around
-the MoE oracle) against the compiled reference before it is trusted as the
-checker of the GPU model: per-step logits and greedy tokens of the
-reference's own olmoe_decode (driven by oracle/ref/ref_olmoe.c over seeded
-weights, tests/golden/model_*.npz) bit for bit, on a reduced model with
-non-unit norms that runs past its context (one kvcache_rotate), and at the
-full OLMoE shape; and the reference's generate order (one olmoe_prefill of
-the prompt) within fp32 rounding."""
+"""Pins the model oracle (oracle/lm_oracle.c: the OLMoE and Mixtral decode
+steps around the MoE oracle) against the compiled reference before it is
+trusted as the checker of the GPU model: per-step logits and greedy tokens of
+the reference's own olmoe_decode / llama_decode (driven by
+oracle/ref/ref_olmoe.c and ref_llama.c over seeded weights,
+tests/golden/model_*.npz) bit for bit, on reduced models with non-unit norms
+that run past their context (kvcache_rotate; Mixtral's keeps its sliding
+window, and its flash_attention masks), at the full OLMoE shape and on two
+layers of the Mixtral-8x7B shape; and the reference's generate order (one
+prefill of the prompt) within fp32 rounding."""
 import numpy as np
 import pytest
 
@@ -17,7 +19,7 @@ from common import bits, model_case, rel_l2
 def _run(name):
     md, prompt, case, g = model_case(name)
     L, E, H, V, NE, K, EI, Cx, wt, nstd, n_prompt, n_gen, stride = case
-    tab = hiplm.ptr_table(md)
+    tab = hiplm.ptr_table(md) if md["arch"] == "olmoe" else hiplm.ptr_table_llama(md)
     m = oracle.OlmoeModel(md, Cx, tab)
     try:
         toks, lg = m.run(prompt, n_gen)
@@ -65,3 +67,21 @@ def test_model_oracle_routing_trace_is_the_layer_oracle():
                 assert np.array_equal(ids[l], oids[0]) and np.array_equal(bits(w[l]), bits(ow[0]))
     finally:
         m.free()
+
+
+def test_model_oracle_matches_reference_decode_bits_mixtral_small():
+    toks, lg, g, stride = _run("mixtral_small")
+    assert np.array_equal(toks, g["dec_tokens"])
+    assert np.array_equal(bits(lg[:, ::stride]), bits(g["dec_logits"]))
+    assert np.array_equal(toks, g["pre_tokens"])
+    for s in range(lg.shape[0]):
+        assert rel_l2(lg[s], g["pre_logits"][s]) <= 1e-5
+
+
+@pytest.mark.slow
+def test_model_oracle_matches_reference_decode_bits_mixtral_layer_shape():
+    toks, lg, g, stride = _run("mixtral_2l")
+    assert np.array_equal(toks, g["dec_tokens"])
+    assert np.array_equal(bits(lg[:, ::stride]), bits(g["dec_logits"]))
+    top = np.take_along_axis(lg, g["dec_top_ids"].astype(np.int64), axis=1)
+    assert np.array_equal(bits(top), bits(g["dec_top_logits"]))
