@@ -14,9 +14,9 @@ distinct tokens: consecutive calls touch different memory and the figure is
 an HBM figure.  Calls are replayed from HIP graphs of one call per layer copy.
 
 The `*_lm_head` workloads time the dense quantized product instead
-(hip_moe_qmat_mul_dev: the reference's tensor_mma_transposed_2x2 on a Q8_0 or
-Q4_0 matrix, here the lm_head of each model for one token), rotating over
-`--layers` copies of the matrix in the same way.
+(hip_moe_qmat_mul_dev: the reference's tensor_mma_transposed_2x2 on a Q8_0,
+Q4_0, Q4_K or Q6_K matrix, here the lm_head of each model for one token),
+rotating over `--layers` copies of the matrix in the same way.
 
 `olmoe_full_decode` times the whole OLMoE-1B-7B-shaped model (hip_lm.h: 16
 layers, d_model 2048, 16 heads of 128, 64 experts top-8 d_ff 1024, vocab
@@ -62,6 +62,10 @@ WORKLOADS = {
     # dense quantized products: N rows of K columns, T tokens
     "olmoe_q8_lm_head": dict(kind="qmat", wtype=hipmoe.Q8_0, N=50304, Kc=2048, T=1),
     "mixtral_q4_lm_head": dict(kind="qmat", wtype=hipmoe.Q4_0, N=32000, Kc=4096, T=1),
+    # K-quant matrices (the Q8_K path, bit-exact): the lm_head of a Q4_K_M
+    # Mixtral file is Q6_K; OLMoE's as Q4_K
+    "mixtral_q6k_lm_head": dict(kind="qmat", wtype=hipmoe.Q6_K, N=32000, Kc=4096, T=1),
+    "olmoe_q4k_lm_head": dict(kind="qmat", wtype=hipmoe.Q4_K, N=50304, Kc=2048, T=1),
     # the whole model, one generated token per step
     "olmoe_full_decode": dict(kind="model", arch="olmoe", wtype=hipmoe.Q8_0, layers=16, E=2048,
                               H=16, KH=16, V=50304, NE=64, K=8, EI=1024, C=2048, prompt=16),
@@ -118,6 +122,7 @@ def bench_qmat(args, w, H):
     `--layers` copies in turn.  Algorithmic bytes per call: the matrix's
     blocks + x + out."""
     wt, N, Kc, T = w["wtype"], w["N"], w["Kc"], w["T"]
+    kname = "k_kq_gemv" if wt in (hipmoe.Q4_K, hipmoe.Q6_K) else "k_qgemv"
     q = hipmoe.synth_quant_matrix(SEED, 0x7700 + wt, 0.02, wt, N, Kc)
     nl = max(1, args.layers)
     mats = [hipmoe.QMat(q, wt, N, Kc) for _ in range(nl)]
@@ -190,15 +195,17 @@ def bench_qmat(args, w, H):
         "metric": QMAT_METRIC, "value": round(tokens_per_s, 2), "unit": "tokens/s",
         "n_gpus": 1, "steps": steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 6), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "vs_baseline": None, "dtype": "i8" if kname == "k_kq_gemv" else "f32",
+        "data": "synthetic",
         "config": {"workload": args.workload, "rows": N, "cols": Kc, "tokens_per_call": T,
-                   "weights": "Q8_0" if wt == hipmoe.Q8_0 else "Q4_0",
+                   "weights": {hipmoe.Q8_0: "Q8_0", hipmoe.Q4_0: "Q4_0", hipmoe.Q4_K: "Q4_K",
+                               hipmoe.Q6_K: "Q6_K"}[wt],
                    "matrix_copies": nl, "distinct_inputs": ntok, "graphs": bool(graphs),
                    "algorithmic_bytes_per_call": int(bytes_per_call)},
-        "roofline": {"bound": "hbm", "kernel": "k_qgemv", "achieved": round(achieved_gbs, 1),
+        "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(achieved_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_bytes("k_qgemv", args.workload)},
+                     "traffic": traffic_bytes(kname, args.workload)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
@@ -271,7 +278,8 @@ def bench_model(args, w, H):
         "config": {"workload": args.workload, "layers": Lh, "d_model": E, "heads": H,
                    "kv_heads": KH, "vocab": V, "experts": NE, "topk": K, "d_ff": EI,
                    "context": Cx,
-                   "weights": "Q8_0" if wt == hipmoe.Q8_0 else "Q4_0",
+                   "weights": {hipmoe.Q8_0: "Q8_0", hipmoe.Q4_0: "Q4_0", hipmoe.Q4_K: "Q4_K",
+                               hipmoe.Q6_K: "Q6_K"}[wt],
                    "prompt_tokens": w["prompt"], "graphs": True,
                    "mean_unique_experts": round(mean_uniq, 3),
                    "algorithmic_bytes_per_token": int(bytes_per_tok)},

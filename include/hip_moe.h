@@ -39,6 +39,8 @@ extern "C" {
  * {f16 d; uint8 qs[16]} (quant.h:14-26), rows of cols/32 blocks, row-major. */
 #define HIP_MOE_Q8_0 1
 #define HIP_MOE_Q4_0 2
+#define HIP_MOE_Q4_K 3 /* dense product only (hip_moe_qmat_*) */
+#define HIP_MOE_Q6_K 5 /* dense product only (hip_moe_qmat_*) */
 
 typedef struct hip_moe_layer hip_moe_layer;
 
@@ -241,8 +243,9 @@ int hip_moe_copy_dev(const void *d_src, void *d_dst, size_t bytes, void *stream)
  *
  * hip_moe_qmat_upload copies one matrix of N rows of K columns (the tensor's
  * qdata: GGUF blocks, row-major) to the current device, once, unchanged.
- * K/64 must be a power of two from 4 to 64 (K = 256 .. 4096: OLMoE 2048,
- * Mixtral 4096).  NULL if not applicable.
+ * Q8_0/Q4_0: K/64 must be a power of two from 4 to 64 (K = 256 .. 4096:
+ * OLMoE 2048, Mixtral 4096).  Q4_K/Q6_K: K a multiple of 256 up to 32768
+ * (Mixtral's 14336 included).  NULL if not applicable.
  */
 typedef struct hip_moe_qmat hip_moe_qmat;
 
@@ -259,7 +262,12 @@ hip_moe_qmat *hip_moe_qmat_upload(const void *qdata, int wtype, size_t N, size_t
  * as d * (sum((q + c) x) - c * sum(x)), c = 128 (Q8_0) or 8 (Q4_0):
  * absolute error per output within 2^-24 * (32 (127 + c) + 31 c + 64 * 255)
  * * (sum over blocks of |d| * sum |x|) to first order; ~1e-6 relative L2 on
- * zero-mean activations.  Returns 1 on success, 0 if not applicable.
+ * zero-mean activations.  Q4_K/Q6_K matrices take the reference's Q8_K
+ * path (matmul.c:291-297: each token quantized by quantize_row_q8, then
+ * dot_q4_K_q8_K / dot_q6_K_q8_K, quant_avx2.h:8-209): there every output
+ * equals the reference's bit for bit (the integer sums are exact and the
+ * fp32 steps are the reference's, in its order).  Returns 1 on success, 0
+ * if not applicable.
  */
 int hip_moe_qmat_mul(hip_moe_qmat *W, const float *x, size_t T, const float *add,
                      size_t add_len, float *out);
@@ -271,6 +279,16 @@ int hip_moe_qmat_mul_dev(const hip_moe_qmat *W, const float *d_x, size_t T,
 
 /* Device bytes of the matrix's blocks. */
 size_t hip_moe_qmat_bytes(const hip_moe_qmat *W);
+
+/*
+ * quantize_row_q8 (quant.c:627-654) of T rows of K values on the current
+ * device, bit for bit: d[T][K/256] scales, qs[T][K] quants, bsums
+ * [T][K/256][16] sums of 16 quants (block_q8_K's fields, quant.h:80-85,
+ * unpacked).  The step the K-quant products run on their tokens, exposed
+ * for checking.  K a multiple of 256; x 16-byte and qs 4-byte aligned.
+ */
+int hip_moe_quantize_q8k_dev(const float *d_x, size_t T, size_t K, float *d_d, int8_t *d_qs,
+                             int16_t *d_bsums, void *stream);
 
 /* Release the device copy (NULL is a no-op). */
 void hip_moe_qmat_free(hip_moe_qmat *W);

@@ -10,6 +10,8 @@
  *         even as F16C _cvtss_sh does, quant.c:46-60)
  *   Q4_0: quantize_q4_0_block (test/quant.c:45-79; truncating fp16 scale,
  *         nibble = clamp(roundf(x*7/amax) + 8, 0, 15))
+ *   Q4_K, Q6_K: min/max quantizers into the reference's block formats
+ *         (quant.h:30-57; the reference itself only reads such blocks)
  * Element i of stream s under seed k is a pure function of (k, s, i), so
  * generation can be split over threads without changing a bit.
  */
@@ -23,7 +25,8 @@
 extern "C" {
 #endif
 
-/* Bytes of one row of n elements in block type wtype (1 = Q8_0, 2 = Q4_0). */
+/* Bytes of one row of n elements in block type wtype (1 = Q8_0, 2 = Q4_0,
+ * 3 = Q4_K, 5 = Q6_K). */
 size_t moe_row_bytes(int wtype, size_t n);
 
 /* out[i] = (float)(mean + std * N_i), i in [0, n), N_i ~ N(0,1). */
@@ -34,6 +37,10 @@ void moe_synth_normal(uint64_t seed, uint64_t stream, float mean, float std,
 void moe_quantize_q8_0(const float *x, void *blocks, size_t n);
 /* test/quant.c:45-79 */
 void moe_quantize_q4_0(const float *x, void *blocks, size_t n);
+/* K-quant block formats (quant.h:30-57) by min/max quantizers of this
+ * library's own: Q4_K per-32 scale and min, Q6_K signed per-16 scales. */
+void moe_quantize_q4_K(const float *x, void *blocks, size_t n);
+void moe_quantize_q6_K(const float *x, void *blocks, size_t n);
 
 /* rows x cols matrix of N(0, std) values, quantized row by row into
  * rows * moe_row_bytes(wtype, cols) bytes at blocks. */

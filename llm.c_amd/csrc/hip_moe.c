@@ -139,7 +139,14 @@ static hipStream_t device_stream(int dev)
 
 static size_t row_bytes(int wtype, size_t n)
 {
+	if (wtype == HIP_MOE_Q4_K || wtype == HIP_MOE_Q6_K)
+		return (n / 256) * (wtype == HIP_MOE_Q4_K ? 144 : 210);
 	return (n / MOE_QK) * (wtype == HIP_MOE_Q8_0 ? 34 : 18);
+}
+
+static int is_kquant(int wtype)
+{
+	return wtype == HIP_MOE_Q4_K || wtype == HIP_MOE_Q6_K;
 }
 
 static int is_pow2(size_t v)
@@ -817,17 +824,25 @@ hip_moe_qmat *hip_moe_qmat_upload(const void *qdata, int wtype, size_t N, size_t
 	hip_moe_qmat *W = NULL;
 	int ndev = 0;
 
-	if (wtype != HIP_MOE_Q8_0 && wtype != HIP_MOE_Q4_0) {
-		set_err("qmat_upload: unsupported weight type %d (Q8_0=1, Q4_0=2)", wtype);
+	if (wtype != HIP_MOE_Q8_0 && wtype != HIP_MOE_Q4_0 && !is_kquant(wtype)) {
+		set_err("qmat_upload: unsupported weight type %d (Q8_0=1, Q4_0=2, Q4_K=3, "
+			"Q6_K=5)", wtype);
 		return NULL;
 	}
 	if (!qdata) {
 		set_err("qmat_upload: NULL weight pointer");
 		return NULL;
 	}
-	/* one wave of K/64 lanes covers a row, no K-split */
-	if (N == 0 || N > 0x7fffffff || K < 256 || K % 256 || !is_pow2(K / MOE_SEG_COLS) ||
-	    K / MOE_SEG_COLS > 64) {
+	if (is_kquant(wtype)) {
+		/* a thread per 256-value super-block; the tokens' Q8_K blocks in LDS */
+		if (N == 0 || N > 0x7fffffff || K > 0x7fffffff || !moe_kq_supported(wtype, (int)K)) {
+			set_err("qmat_upload: N=%zu K=%zu not supported for K-quants (N >= 1, K a "
+				"multiple of 256 up to 32768)", N, K);
+			return NULL;
+		}
+	} else if (N == 0 || N > 0x7fffffff || K < 256 || K % 256 ||
+		   !is_pow2(K / MOE_SEG_COLS) || K / MOE_SEG_COLS > 64) {
+		/* one wave of K/64 lanes covers a row, no K-split */
 		set_err("qmat_upload: N=%zu K=%zu not supported (N >= 1, K/64 a power of two "
 			"4..64)", N, K);
 		return NULL;
@@ -851,9 +866,16 @@ hip_moe_qmat *hip_moe_qmat_upload(const void *qdata, int wtype, size_t N, size_t
 		goto fail;
 	/* resident workgroups, queried here rather than at a call that may be
 	 * under graph capture */
-	W->grid1 = moe_qgemv_grid(wtype, (int)K, 1);
-	W->grid = moe_qgemv_grid(wtype, (int)K, 0);
-	HIPCHK(hipMalloc((void **)&W->d_w, W->bytes), "hipMalloc(qmat)");
+	if (is_kquant(wtype)) {
+		W->grid1 = moe_kq_grid(wtype, (int)K, 1);
+		W->grid = moe_kq_grid(wtype, (int)K, 8);
+	} else {
+		W->grid1 = moe_qgemv_grid(wtype, (int)K, 1);
+		W->grid = moe_qgemv_grid(wtype, (int)K, 0);
+	}
+	/* the K-quant loads read up to MOE_KQ_SLACK bytes past the last block */
+	HIPCHK(hipMalloc((void **)&W->d_w, W->bytes + MOE_KQ_SLACK), "hipMalloc(qmat)");
+	HIPCHK(hipMemset(W->d_w + W->bytes, 0, MOE_KQ_SLACK), "clear qmat slack");
 	HIPCHK(hipMemcpy(W->d_w, qdata, W->bytes, hipMemcpyHostToDevice), "upload qmat");
 	return W;
 fail:
@@ -889,10 +911,16 @@ int hip_moe_qmat_mul_dev(const hip_moe_qmat *W, const float *d_x, size_t T,
 	}
 	if (!check_add(W, T, d_add, add_len))
 		return 0;
-	LCHK(moe_launch_qgemv(W->wtype, W->d_w, (int)W->N, (int)W->K, d_x, (int)T, d_add,
-			      add_len == T * W->N, d_out, T == 1 ? W->grid1 : W->grid,
-			      stream ? stream : (void *)W->stream),
-	     "qgemv");
+	if (is_kquant(W->wtype))
+		LCHK(moe_launch_kq_gemv(W->wtype, W->d_w, (int)W->N, (int)W->K, d_x, (int)T, d_add,
+					add_len == T * W->N, d_out, T == 1 ? W->grid1 : W->grid,
+					stream ? stream : (void *)W->stream),
+		     "kq_gemv");
+	else
+		LCHK(moe_launch_qgemv(W->wtype, W->d_w, (int)W->N, (int)W->K, d_x, (int)T, d_add,
+				      add_len == T * W->N, d_out, T == 1 ? W->grid1 : W->grid,
+				      stream ? stream : (void *)W->stream),
+		     "qgemv");
 	return 1;
 }
 
@@ -950,4 +978,30 @@ void hip_moe_qmat_free(hip_moe_qmat *W)
 	hipFree(W->d_add);
 	hipFree(W->d_out);
 	free(W); /* W->stream is the device's shared stream: it stays */
+}
+
+int hip_moe_quantize_q8k_dev(const float *d_x, size_t T, size_t K, float *d_d, int8_t *d_qs,
+			     int16_t *d_bsums, void *stream)
+{
+	if (!d_x || !d_d || !d_qs || !d_bsums) {
+		set_err("quantize_q8k: NULL argument");
+		return 0;
+	}
+	if (T == 0 || K == 0 || K % 256 || T * K > ((size_t)1 << 31)) {
+		set_err("quantize_q8k: T=%zu K=%zu not supported (K a multiple of 256, T*K < 2^31)",
+			T, K);
+		return 0;
+	}
+	if ((uintptr_t)d_x % 16 || (uintptr_t)d_qs % 4) {
+		set_err("quantize_q8k: x must be 16-byte and qs 4-byte aligned");
+		return 0;
+	}
+	int dev = 0;
+	if (hipGetDevice(&dev) != hipSuccess) {
+		set_err("quantize_q8k: no HIP device");
+		return 0;
+	}
+	hipStream_t s = stream ? (hipStream_t)stream : device_stream(dev);
+	LCHK(moe_launch_q8k_quantize(d_x, (int)T, (int)K, d_d, d_qs, d_bsums, s), "q8k_quantize");
+	return 1;
 }

@@ -67,6 +67,19 @@ int moe_launch_qgemv(int wtype, const uint8_t *W, int N, int K, const float *x, 
 /* workgroups the device holds at once for the (wtype, K, T == 1) instance */
 int moe_qgemv_grid(int wtype, int K, int one);
 
+/* The same product on a Q4_K (wtype 3) or Q6_K (5) matrix through Q8_K
+ * activations, bit for bit the reference's (kquant.hip); the matrix buffer
+ * needs MOE_KQ_SLACK bytes past its end.  moe_kq_supported: K a multiple of
+ * 256 whose staging fits in LDS. */
+#define MOE_KQ_SLACK 16
+int moe_kq_supported(int wtype, int K);
+int moe_kq_grid(int wtype, int K, int T);
+int moe_launch_kq_gemv(int wtype, const uint8_t *W, int N, int K, const float *x, int T,
+                       const float *add, int add_rows, float *out, int nwg, void *stream);
+/* quantize_row_q8 of T rows of K values: d[T][K/256], qs[T][K], bsums[T][K/256][16] */
+int moe_launch_q8k_quantize(const float *x, int T, int K, float *d, int8_t *qs,
+                            int16_t *bsums, void *stream);
+
 /* ypart floats moe_launch_down may use for any pair count up to P */
 size_t moe_down_part_floats(size_t E, size_t EI, size_t P);
 

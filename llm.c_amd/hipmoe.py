@@ -19,6 +19,8 @@ LIB_PATH = os.path.join(HERE, "libhip_moe.so")
 
 Q8_0 = 1
 Q4_0 = 2
+Q4_K = 3
+Q6_K = 5
 # execution paths (include/hip_moe.h)
 PATH_AUTO, PATH_DECODE, PATH_GEMV, PATH_GROUPED = 0, 1, 2, 3
 QK = 32
@@ -32,6 +34,8 @@ class HipMoeError(RuntimeError):
 
 
 def row_bytes(wtype: int, n: int) -> int:
+    if wtype in (Q4_K, Q6_K):
+        return (n // 256) * (144 if wtype == Q4_K else 210)
     return (n // QK) * (34 if wtype == Q8_0 else 18)
 
 
@@ -86,6 +90,8 @@ def lib():
     L.hip_moe_qmat_bytes.argtypes = [vp]
     L.hip_moe_qmat_free.restype = None
     L.hip_moe_qmat_free.argtypes = [vp]
+    L.hip_moe_quantize_q8k_dev.restype = i32
+    L.hip_moe_quantize_q8k_dev.argtypes = [vp, sz, sz, vp, vp, vp, vp]
     # synthetic inputs
     L.moe_row_bytes.restype = sz
     L.moe_row_bytes.argtypes = [i32, sz]
@@ -443,7 +449,8 @@ class MoeLayer:
 
 
 class QMat:
-    """One uploaded Q8_0/Q4_0 matrix of N rows of K columns (hip_moe_qmat_upload)."""
+    """One uploaded Q8_0/Q4_0/Q4_K/Q6_K matrix of N rows of K columns
+    (hip_moe_qmat_upload)."""
 
     def __init__(self, q: np.ndarray, wtype: int, N: int, K: int):
         self.q = np.ascontiguousarray(q, np.uint8)
@@ -484,6 +491,26 @@ class QMat:
             self.free()
         except Exception:
             pass
+
+
+def quantize_q8k_dev(x: np.ndarray):
+    """quantize_row_q8 of each row of x[T][K] on the GPU
+    (hip_moe_quantize_q8k_dev): (d[T][K/256], qs[T][K], bsums[T][K/256][16])."""
+    H = hip()
+    x = np.ascontiguousarray(x, np.float32)
+    T, K = x.reshape(-1, x.shape[-1]).shape
+    nb = K // 256
+    d_x = H.upload(x)
+    d_d, d_q, d_b = H.malloc(T * nb * 4), H.malloc(T * K), H.malloc(T * nb * 32)
+    try:
+        if lib().hip_moe_quantize_q8k_dev(d_x, T, K, d_d, d_q, d_b, None) != 1:
+            raise HipMoeError("hip_moe_quantize_q8k_dev: " + last_error())
+        H.sync()
+        return (H.download(d_d, (T, nb), np.float32), H.download(d_q, (T, K), np.int8),
+                H.download(d_b, (T, nb, 16), np.int16))
+    finally:
+        for q in (d_x, d_d, d_q, d_b):
+            H.free(q)
 
 
 def expf_dev(x: np.ndarray) -> np.ndarray:

@@ -4,6 +4,8 @@
  * Quantizers follow the reference:
  *   quantize_row_q8_0   quant.c:62-78 (fp16 scale via f32_to_f16, quant.c:46-60)
  *   quantize_q4_0_block test/quant.c:45-79
+ * and, for the K-quant block formats (quant.h:30-57), min/max quantizers of
+ * this file's own (moe_quantize_q4_K / q6_K below).
  * Built with -ffp-contract=off so every product is rounded as written.
  */
 #define _GNU_SOURCE
@@ -15,6 +17,7 @@
 #include <string.h>
 
 #define QK 32
+#define QKK 256
 
 size_t moe_row_bytes(int wtype, size_t n)
 {
@@ -23,6 +26,10 @@ size_t moe_row_bytes(int wtype, size_t n)
 		return nb * 34;
 	if (wtype == 2)
 		return nb * 18;
+	if (wtype == 3)
+		return n / QKK * 144;
+	if (wtype == 5)
+		return n / QKK * 210;
 	return 0;
 }
 
@@ -215,6 +222,124 @@ void moe_quantize_q4_0(const float *x, void *blocks, size_t n)
 	}
 }
 
+static int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+static void put16(uint8_t *p, uint16_t h)
+{
+	p[0] = (uint8_t)(h & 0xff);
+	p[1] = (uint8_t)(h >> 8);
+}
+
+/*
+ * Q4_K (144 bytes per 256 values: f16 d, f16 dmin, 12 bytes of 6-bit
+ * sub-block scales and mins, 128 bytes of nibbles; quant.h:30-36).  Each
+ * sub-block of 32 spans [lo, hi] with lo = min(0, min x): scale (hi - lo)/15
+ * and min -lo, both as 6-bit multiples of the super-block's d = max scale/63
+ * and dmin = max min/63 (f16, nearest even); values q = clamp(round((x + m) /
+ * s), 0, 15).  The packing is the one get_scale_min_k4 (quant.h:63-73)
+ * reads: bytes 0-3 scales 0-3 (6 bits) with scales 4-7's top 2 bits above,
+ * bytes 4-7 mins 0-3 likewise, bytes 8-11 scales 4-7's low nibble with mins
+ * 4-7's low nibble above; nibble byte j*32+k holds value j*64+k below and
+ * j*64+32+k above.
+ */
+void moe_quantize_q4_K(const float *x, void *blocks, size_t n)
+{
+	uint8_t *out = blocks;
+	for (size_t b = 0; b < n / QKK; b++) {
+		const float *xb = &x[b * QKK];
+		uint8_t *blk = out + b * 144;
+		float sub_s[8], sub_m[8], smax = 0, mmax = 0;
+		for (int j = 0; j < 8; j++) {
+			float lo = 0, hi = -INFINITY;
+			for (int k = 0; k < 32; k++) {
+				float v = xb[j * 32 + k];
+				lo = v < lo ? v : lo;
+				hi = v > hi ? v : hi;
+			}
+			sub_s[j] = (hi - lo) / 15.0f;
+			sub_m[j] = -lo;
+			smax = sub_s[j] > smax ? sub_s[j] : smax;
+			mmax = sub_m[j] > mmax ? sub_m[j] : mmax;
+		}
+		uint16_t hd = moe_f32_to_f16_rne(smax / 63.0f), hm = moe_f32_to_f16_rne(mmax / 63.0f);
+		float d = moe_f16_to_f32(hd), dmin = moe_f16_to_f32(hm);
+		put16(blk, hd);
+		put16(blk + 2, hm);
+		int sc[8], mn[8];
+		for (int j = 0; j < 8; j++) {
+			sc[j] = d > 0 ? clampi((int)roundf(sub_s[j] / d), 0, 63) : 0;
+			mn[j] = dmin > 0 ? clampi((int)roundf(sub_m[j] / dmin), 0, 63) : 0;
+		}
+		uint8_t *p = blk + 4;
+		for (int j = 0; j < 4; j++) {
+			p[j] = (uint8_t)(sc[j] | ((sc[j + 4] >> 4) << 6));
+			p[j + 4] = (uint8_t)(mn[j] | ((mn[j + 4] >> 4) << 6));
+			p[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4));
+		}
+		int q[QKK];
+		for (int j = 0; j < 8; j++) {
+			float s = d * (float)sc[j], m = dmin * (float)mn[j];
+			for (int k = 0; k < 32; k++)
+				q[j * 32 + k] = s > 0 ? clampi((int)roundf((xb[j * 32 + k] + m) / s), 0, 15) : 0;
+		}
+		uint8_t *qs = blk + 16;
+		for (int j = 0; j < 4; j++)
+			for (int k = 0; k < 32; k++)
+				qs[j * 32 + k] = (uint8_t)(q[j * 64 + k] | (q[j * 64 + 32 + k] << 4));
+	}
+}
+
+/*
+ * Q6_K (210 bytes per 256 values: 128 bytes of low nibbles, 64 bytes of
+ * 2-bit highs, 16 int8 sub-block scales, f16 d; quant.h:47-53).  Each
+ * sub-block of 16 takes scale s = -v/32 for its value v of largest
+ * magnitude (so v lands on -32 and scales carry either sign), stored as
+ * int8 multiples of d = -(the s of largest magnitude)/128 (f16, nearest
+ * even); values q = clamp(round(x / s), -32, 31), stored as q + 32.  Value
+ * c*128 + g*32 + l (g = 0..3, l = 0..31) keeps its low nibble in byte
+ * c*64 + (g & 1)*32 + l (below for g < 2, above otherwise) and its top two
+ * bits in bits 2g..2g+1 of byte 128 + c*32 + l.
+ */
+void moe_quantize_q6_K(const float *x, void *blocks, size_t n)
+{
+	uint8_t *out = blocks;
+	for (size_t b = 0; b < n / QKK; b++) {
+		const float *xb = &x[b * QKK];
+		uint8_t *blk = out + b * 210;
+		float sub[16], smax = 0, sval = 0;
+		for (int j = 0; j < 16; j++) {
+			float amax = 0, v = 0;
+			for (int k = 0; k < 16; k++) {
+				float a = fabsf(xb[j * 16 + k]);
+				if (a > amax) {
+					amax = a;
+					v = xb[j * 16 + k];
+				}
+			}
+			sub[j] = -v / 32.0f;
+			if (fabsf(sub[j]) > smax) {
+				smax = fabsf(sub[j]);
+				sval = sub[j];
+			}
+		}
+		uint16_t hd = moe_f32_to_f16_rne(-sval / 128.0f);
+		float d = moe_f16_to_f32(hd);
+		memset(blk, 0, 192);
+		int8_t *sc = (int8_t *)(blk + 192);
+		for (int j = 0; j < 16; j++)
+			sc[j] = (int8_t)(d != 0 ? clampi((int)roundf(sub[j] / d), -128, 127) : 0);
+		put16(blk + 208, hd);
+		for (int e = 0; e < QKK; e++) {
+			float s = d * (float)sc[e / 16];
+			int q = s != 0 ? clampi((int)roundf(xb[e] / s), -32, 31) : 0;
+			int u = q + 32, c = e / 128, g = (e % 128) / 32, l = e % 32;
+			uint8_t *lo = blk + c * 64 + (g & 1) * 32 + l;
+			*lo |= (uint8_t)(g < 2 ? (u & 0xF) : ((u & 0xF) << 4));
+			blk[128 + c * 32 + l] |= (uint8_t)((u >> 4) << (2 * g));
+		}
+	}
+}
+
 struct quant_job {
 	uint64_t key;
 	float std;
@@ -232,8 +357,12 @@ static void *quant_thread(void *arg)
 		fill_normal(j->key, (uint64_t)r * j->cols, 0.0f, j->std, row, j->cols);
 		if (j->wtype == 1)
 			moe_quantize_q8_0(row, j->blocks + r * rb, j->cols);
-		else
+		else if (j->wtype == 2)
 			moe_quantize_q4_0(row, j->blocks + r * rb, j->cols);
+		else if (j->wtype == 3)
+			moe_quantize_q4_K(row, j->blocks + r * rb, j->cols);
+		else
+			moe_quantize_q6_K(row, j->blocks + r * rb, j->cols);
 	}
 	free(row);
 	return NULL;

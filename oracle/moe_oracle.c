@@ -32,6 +32,7 @@
 
 #define LANES 8  /* AVX2_BATCH, vector_avx2.h:13 */
 #define QK 32    /* GGML_QK, quant.h:11 */
+#define QKK 256  /* QK_K, quant.h:28 */
 
 /* f16 -> f32 is exact (F16C _cvtsh_ss, quant.h:71-75). */
 static float h2f(uint16_t h)
@@ -227,8 +228,17 @@ static float dot_q4_0(const float *x, const uint8_t *row, size_t n)
 
 static size_t row_bytes(int wtype, size_t n)
 {
-	return (n / QK) * (wtype == ORC_Q8_0 ? 34 : 18);
+	switch (wtype) {
+	case ORC_Q8_0: return (n / QK) * 34;
+	case ORC_Q4_0: return (n / QK) * 18;
+	case ORC_Q4_K: return (n / QKK) * 144;
+	case ORC_Q6_K: return (n / QKK) * 210;
+	}
+	abort();
 }
+
+static float dot_q4_K_f32(const float *x, const uint8_t *row, size_t n);
+static float dot_q6_K_f32(const float *x, const uint8_t *row, size_t n);
 
 float orc_dot_quant(const float *x, const void *qrow, int wtype, size_t n)
 {
@@ -236,6 +246,10 @@ float orc_dot_quant(const float *x, const void *qrow, int wtype, size_t n)
 		return dot_q8_0(x, qrow, n);
 	if (wtype == ORC_Q4_0)
 		return dot_q4_0(x, qrow, n);
+	if (wtype == ORC_Q4_K)
+		return dot_q4_K_f32(x, qrow, n);
+	if (wtype == ORC_Q6_K)
+		return dot_q6_K_f32(x, qrow, n);
 	abort();
 }
 
@@ -255,31 +269,57 @@ struct qmat_job {
 	const float *add;
 	size_t add_len;
 	float *out;
+	float *q8d;     /* K-quants: the tokens in Q8_K, [T][K/256] scales, */
+	int8_t *q8s;    /* [T][K] quants */
+	int16_t *q8b;   /* [T][K/256][16] sums of 16 */
 };
 
 /* thread tidx of nt takes output columns [tidx * ceil(N/nt), ...) of every
- * token (transposed_gemv_thread_fn, matmul.c:107-114) */
+ * token (transposed_gemv_thread_fn, matmul.c:107-114; for K-quants the
+ * Q8_K dots of matmul.c:121-124,145-165 on the tokens quantized once) */
 static void qmat_task(void *arg, int tidx, int nt)
 {
 	const struct qmat_job *w = arg;
 	const size_t rb = row_bytes(w->wtype, w->K), chunk = (w->N + nt - 1) / nt;
 	const size_t j0 = tidx * chunk, j1 = j0 + chunk < w->N ? j0 + chunk : w->N;
+	const size_t nb = w->K / QKK;
 	for (size_t t = 0; t < w->T; t++)
 		for (size_t j = j0; j < j1; j++) {
 			float init = !w->add ? 0.0f
 					     : w->add_len == w->N ? w->add[j] : w->add[t * w->N + j];
-			w->out[t * w->N + j] =
-				init + orc_dot_quant(&w->x[t * w->K], (const uint8_t *)w->q + j * rb,
-						     w->wtype, w->K);
+			const uint8_t *qr = (const uint8_t *)w->q + j * rb;
+			float dot = w->q8d ? orc_dot_q8k(w->q8d + t * nb, w->q8s + t * w->K,
+							 w->q8b + t * nb * 16, qr, w->wtype, w->K)
+					   : orc_dot_quant(&w->x[t * w->K], qr, w->wtype, w->K);
+			w->out[t * w->N + j] = init + dot;
 		}
 }
 
 void orc_qmat_mul(const float *x, size_t T, const void *q, int wtype, size_t N, size_t K,
 		  const float *add, size_t add_len, float *out)
 {
-	struct qmat_job w = {x, q, wtype, T, N, K, add, add_len, out};
+	struct qmat_job w = {x, q, wtype, T, N, K, add, add_len, out, NULL, NULL, NULL};
+	/* the default -DQ8_DOT build quantizes the tokens to Q8_K once when
+	 * K % 256 == 0 (matmul.c:291-297); dot_q8_quant takes the integer dots
+	 * for K-quants and the fp32 dots otherwise (quant.c:656-668) */
+	const int kq = (wtype == ORC_Q4_K || wtype == ORC_Q6_K) && K % QKK == 0;
+	if (kq) {
+		w.q8d = malloc(T * (K / QKK) * sizeof(float));
+		w.q8s = malloc(T * K);
+		w.q8b = malloc(T * (K / QKK) * 16 * sizeof(int16_t));
+		for (size_t t = 0; t < T; t++)
+			orc_quantize_q8k(x + t * K, K, w.q8d + t * (K / QKK), w.q8s + t * K,
+					 w.q8b + t * (K / QKK) * 16);
+	}
 	orc_pool_run(qmat_task, &w, orc_pool_threads(T, K, N));
+	if (kq) {
+		free(w.q8d);
+		free(w.q8s);
+		free(w.q8b);
+	}
 }
+
+static void dequant_kquant(const uint8_t *row, int wtype, float *dst, size_t n);
 
 void orc_dequant_row(const void *qrow, int wtype, float *dst, size_t n)
 {
@@ -297,6 +337,9 @@ void orc_dequant_row(const void *qrow, int wtype, float *dst, size_t n)
 				dst[b * QK + j] = d * (float)((int)(blk[2 + j] & 0x0f) - 8);
 				dst[b * QK + j + QK / 2] = d * (float)((int)(blk[2 + j] >> 4) - 8);
 			}
+		} else if (wtype == ORC_Q4_K || wtype == ORC_Q6_K) {
+			dequant_kquant(row, wtype, dst, n);
+			return;
 		} else {
 			abort();
 		}
@@ -507,4 +550,240 @@ void orc_expf_bits(uint32_t bits0, size_t n, float *out, int nthreads)
 		pthread_join(th[i], NULL);
 	free(jobs);
 	free(th);
+}
+
+/* ---------------------------------------------------------------------- */
+/* K-quants: Q4_K (144-byte blocks of 256), Q6_K (210-byte blocks of 256)  */
+/* and the Q8_K activation blocks of the -DQ8_DOT build                    */
+/* ---------------------------------------------------------------------- */
+
+/* get_scale_min_k4 (quant.h:63-73): sub-block j's 6-bit scale and min */
+static void scale_min_k4(int j, const uint8_t *q, int *d, int *m)
+{
+	if (j < 4) {
+		*d = q[j] & 63;
+		*m = q[j + 4] & 63;
+	} else {
+		*d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+		*m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+	}
+}
+
+/*
+ * quantize_row_q8 (quant.c:627-654): per 256 values, mval = the first value
+ * of largest magnitude, iscale = -127 / mval, d = 1 / iscale, q =
+ * min(127, (int)roundf(iscale * x)), bsums = sums of 16 quants; an all-zero
+ * block is all zero.
+ */
+void orc_quantize_q8k(const float *x, size_t n, float *d, int8_t *qs, int16_t *bsums)
+{
+	for (size_t i = 0; i < n / QKK; i++) {
+		const float *xb = x + i * QKK;
+		float amax = 0, mval = 0;
+		for (int j = 0; j < QKK; j++) {
+			float a = fabsf(xb[j]);
+			if (a > amax) {
+				amax = a;
+				mval = xb[j];
+			}
+		}
+		if (amax == 0) {
+			d[i] = 0.0f;
+			memset(qs + i * QKK, 0, QKK);
+			memset(bsums + i * 16, 0, 16 * sizeof(int16_t));
+			continue;
+		}
+		float iscale = -127.0f / mval;
+		d[i] = 1.0f / iscale;
+		for (int j = 0; j < QKK; j++) {
+			int v = (int)roundf(iscale * xb[j]);
+			qs[i * QKK + j] = (int8_t)(v < 127 ? v : 127);
+		}
+		for (int j = 0; j < 16; j++) {
+			int sum = 0;
+			for (int k = 0; k < 16; k++)
+				sum += qs[i * QKK + j * 16 + k];
+			bsums[i * 16 + j] = (int16_t)sum;
+		}
+	}
+}
+
+/*
+ * dot_q4_K_q8_K (quant_cpu.h:7-60, which quant_avx2.h:8-106 equals bit for
+ * bit): per super-block the exact integer sums sumi = sum over sub-blocks of
+ * scale * sum(q4 * q8) and min_sum = sum over sub-blocks of min * (bsum pair),
+ * then acc = fma(yd * d, sumi, acc) and acc_m = fma(-yd * dmin, min_sum,
+ * acc_m) (clang -ffp-contract=on fuses `acc += d * sumi`); the result is
+ * acc + acc_m.  dot_q6_K_q8_K (quant_cpu.h:62-120): sumi =
+ * sum over 16-value groups of scale * sum((q6 - 32) * q8); acc += (yd * d) *
+ * sumi.
+ */
+float orc_dot_q8k(const float *yd, const int8_t *q8, const int16_t *bsums, const void *qrow,
+		  int wtype, size_t n)
+{
+	const uint8_t *row = qrow;
+	float acc = 0, acc_m = 0;
+	for (size_t i = 0; i < n / QKK; i++) {
+		const int8_t *y = q8 + i * QKK;
+		if (wtype == ORC_Q4_K) {
+			const uint8_t *b = row + i * 144;
+			const float d = yd[i] * h2f(rd16(b)), dmin = -yd[i] * h2f(rd16(b + 2));
+			const uint8_t *sc = b + 4, *qs = b + 16;
+			int32_t sumi = 0, min_sum = 0;
+			for (int j = 0; j < 4; j++) {
+				int s1, m1, s2, m2;
+				scale_min_k4(2 * j, sc, &s1, &m1);
+				scale_min_k4(2 * j + 1, sc, &s2, &m2);
+				int32_t a = 0, c = 0;
+				for (int k = 0; k < 32; k++) {
+					a += (qs[j * 32 + k] & 0xF) * y[j * 64 + k];
+					c += (qs[j * 32 + k] >> 4) * y[j * 64 + 32 + k];
+				}
+				sumi += s1 * a + s2 * c;
+				min_sum += m1 * (bsums[i * 16 + 4 * j] + bsums[i * 16 + 4 * j + 1]) +
+					   m2 * (bsums[i * 16 + 4 * j + 2] + bsums[i * 16 + 4 * j + 3]);
+			}
+			/* the reference's clang build contracts both updates into FMAs */
+			acc_m = fmaf(dmin, (float)min_sum, acc_m);
+			acc = fmaf(d, (float)sumi, acc);
+		} else {
+			const uint8_t *b = row + i * 210;
+			const uint8_t *ql = b, *qh = b + 128;
+			const int8_t *sc = (const int8_t *)(b + 192);
+			const float d = yd[i] * h2f(rd16(b + 208));
+			int32_t sumi = 0;
+			for (int c = 0; c < 2; c++)
+				for (int g = 0; g < 4; g++) /* 32 values: ql low/high nibble, qh 2 bits */
+					for (int half = 0; half < 2; half++) {
+						int32_t s = 0;
+						for (int k = 0; k < 16; k++) {
+							const int l = half * 16 + k;
+							const int lo = g & 1 ? ql[c * 64 + 32 + l]
+									     : ql[c * 64 + l];
+							const int q = ((g < 2 ? lo & 0xF : lo >> 4) |
+								       (((qh[c * 32 + l] >> (2 * g)) & 3) << 4)) -
+								      32;
+							s += q * y[c * 128 + g * 32 + l];
+						}
+						sumi += sc[c * 8 + g * 2 + half] * s;
+					}
+			acc = fmaf(d, (float)sumi, acc);
+		}
+	}
+	return acc + acc_m;
+}
+
+/*
+ * dot_f32_q4_K (quant.c:198-251): 8 lanes, lane l the elements k = l mod 8
+ * in increasing k, each weight fl(fl(d * sc) * q) - fl(dmin * m), then an
+ * FMA with x; the lane tree.  dot_f32_q6_K (quant.c:298-418): weights
+ * fl((q - 32) * fl(d * sc)), FMAs in the same lane order.
+ */
+static float dot_q4_K_f32(const float *x, const uint8_t *row, size_t n)
+{
+	float acc[LANES] = {0};
+	for (size_t i = 0; i < n / QKK; i++) {
+		const uint8_t *b = row + i * 144;
+		const float d = h2f(rd16(b)), dmin = h2f(rd16(b + 2));
+		const uint8_t *q = b + 16;
+		const float *xb = x + i * QKK;
+		for (int j = 0; j < 4; j++) {
+			int s1, m1, s2, m2;
+			scale_min_k4(2 * j, b + 4, &s1, &m1);
+			scale_min_k4(2 * j + 1, b + 4, &s2, &m2);
+			const float d1 = d * (float)s1, n1 = dmin * (float)m1;
+			const float d2 = d * (float)s2, n2 = dmin * (float)m2;
+			for (int g = 0; g < 32; g += LANES)
+				for (int l = 0; l < LANES; l++) {
+					float v = d1 * (float)(q[j * 32 + g + l] & 0xF);
+					v = v - n1;
+					acc[l] = fmaf(v, xb[j * 64 + g + l], acc[l]);
+				}
+			for (int g = 0; g < 32; g += LANES)
+				for (int l = 0; l < LANES; l++) {
+					float v = d2 * (float)(q[j * 32 + g + l] >> 4);
+					v = v - n2;
+					acc[l] = fmaf(v, xb[j * 64 + 32 + g + l], acc[l]);
+				}
+		}
+	}
+	return lane_sum(acc);
+}
+
+static float dot_q6_K_f32(const float *x, const uint8_t *row, size_t n)
+{
+	float acc[LANES] = {0};
+	for (size_t i = 0; i < n / QKK; i++) {
+		const uint8_t *b = row + i * 210;
+		const uint8_t *ql0 = b, *qh0 = b + 128;
+		const int8_t *sc = (const int8_t *)(b + 192);
+		const float d = h2f(rd16(b + 208));
+		const float *xb = x + i * QKK;
+		for (int c = 0; c < 2; c++) {
+			const uint8_t *ql = ql0 + c * 64, *qh = qh0 + c * 32;
+			for (int g = 0; g < 4; g++) {
+				float tmp[32];
+				for (int l = 0; l < 32; l++) {
+					const int lo = g & 1 ? ql[l + 32] : ql[l];
+					tmp[l] = (float)(((g < 2 ? lo & 0xF : lo >> 4) |
+							  (((qh[l] >> (2 * g)) & 3) << 4)) -
+							 32);
+				}
+				for (int half = 0; half < 2; half++) {
+					const float vs = d * (float)sc[c * 8 + g * 2 + half];
+					for (int u = 0; u < 16; u += LANES)
+						for (int l = 0; l < LANES; l++) {
+							const float vt = tmp[half * 16 + u + l] * vs;
+							acc[l] = fmaf(vt, xb[c * 128 + g * 32 + half * 16 + u + l],
+								      acc[l]);
+						}
+				}
+			}
+		}
+	}
+	return lane_sum(acc);
+}
+
+/* dequant_row_q4_K / q6_K (quant.c:420-531) */
+static void dequant_kquant(const uint8_t *row, int wtype, float *dst, size_t n)
+{
+	for (size_t i = 0; i < n / QKK; i++) {
+		float *o = dst + i * QKK;
+		if (wtype == ORC_Q4_K) {
+			const uint8_t *b = row + i * 144;
+			const float d = h2f(rd16(b)), dmin = h2f(rd16(b + 2));
+			for (int j = 0; j < 4; j++) {
+				int s1, m1, s2, m2;
+				scale_min_k4(2 * j, b + 4, &s1, &m1);
+				scale_min_k4(2 * j + 1, b + 4, &s2, &m2);
+				const float d1 = d * (float)s1, n1 = dmin * (float)m1;
+				const float d2 = d * (float)s2, n2 = dmin * (float)m2;
+				for (int k = 0; k < 32; k++) {
+					float v = d1 * (float)(b[16 + j * 32 + k] & 0xF);
+					o[j * 64 + k] = v - n1;
+					v = d2 * (float)(b[16 + j * 32 + k] >> 4);
+					o[j * 64 + 32 + k] = v - n2;
+				}
+			}
+		} else {
+			const uint8_t *b = row + i * 210;
+			const int8_t *sc = (const int8_t *)(b + 192);
+			const float d = h2f(rd16(b + 208));
+			for (int c = 0; c < 2; c++) {
+				const uint8_t *ql = b + c * 64, *qh = b + 128 + c * 32;
+				for (int l = 0; l < 32; l++) {
+					const int is = c * 8 + l / 16;
+					const int q1 = (int)((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+					const int q2 = (int)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+					const int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+					const int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+					/* d * scale * q: (d * scale) first, then * q (int -> float) */
+					o[c * 128 + l + 0] = d * (float)sc[is + 0] * (float)q1;
+					o[c * 128 + l + 32] = d * (float)sc[is + 2] * (float)q2;
+					o[c * 128 + l + 64] = d * (float)sc[is + 4] * (float)q3;
+					o[c * 128 + l + 96] = d * (float)sc[is + 6] * (float)q4;
+				}
+			}
+		}
+	}
 }

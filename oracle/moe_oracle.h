@@ -26,6 +26,8 @@ extern "C" {
 /* values of the reference's enum tensor_dtype (tensor.h:10-17) */
 #define ORC_Q8_0 1
 #define ORC_Q4_0 2
+#define ORC_Q4_K 3
+#define ORC_Q6_K 5
 
 /* Router logits[T][NE] = (bias or 0) + x[T][E] . wr[NE][E]^T
  * (matmul.c:13-33 mma_init, 91-131 GEMV, 169-245 tiled path). */
@@ -43,16 +45,27 @@ void orc_softmax_1d(float *row, size_t n);
  * (nn.c:276-308). ids/w are ascending by weight; slot k-1 is the max. */
 void orc_top_k(const float *row, size_t n, uint32_t *ids, float *w, size_t k);
 
-/* fp32-activation dot with one quantized row (quant.c:103-155). */
+/* fp32-activation dot with one quantized row (quant.c:103-155, 198-418;
+ * dot_f32_quant, quant.c:577-614). */
 float orc_dot_quant(const float *x, const void *qrow, int wtype, size_t n);
 
 /* out[T][N] = add + x[T][K] . W^T, W = N rows of K columns in blocks; add
- * NULL, [N] (add_len == N) or [T][N] (matmul.c:13-33,285-312) */
+ * NULL, [N] (add_len == N) or [T][N] (matmul.c:13-33,285-312); K-quant
+ * matrices with K % 256 == 0 take the Q8_K path of the -DQ8_DOT build */
 void orc_qmat_mul(const float *x, size_t T, const void *q, int wtype, size_t N, size_t K,
 		  const float *add, size_t add_len, float *out);
 
-/* Dequantize one row of n elements (quant.c:157-196). */
+/* Dequantize one row of n elements (quant.c:157-196, 420-531). */
 void orc_dequant_row(const void *qrow, int wtype, float *dst, size_t n);
+
+/* quantize_row_q8 (quant.c:627-654): n/256 Q8_K blocks as d[n/256],
+ * qs[n], bsums[n/256][16]. */
+void orc_quantize_q8k(const float *x, size_t n, float *d, int8_t *qs, int16_t *bsums);
+
+/* dot_q4_K_q8_K / dot_q6_K_q8_K (quant_cpu.h:7-120 = quant_avx2.h:8-209) of
+ * one Q4_K/Q6_K row of n values with Q8_K activations. */
+float orc_dot_q8k(const float *yd, const int8_t *q8, const int16_t *bsums, const void *qrow,
+                  int wtype, size_t n);
 
 /* One expert, one token: out[E] = down . (silu(gate . x) * (up . x))
  * (nn.c:449-493 fused_ffn_fn).  h is a caller scratch of EI floats. */

@@ -36,6 +36,10 @@ def lib():
         L.orc_qmat_mul.restype = None
         L.orc_dequant_row.argtypes = [vp, i32, vp, sz]
         L.orc_dequant_row.restype = None
+        L.orc_quantize_q8k.argtypes = [vp, sz, vp, vp, vp]
+        L.orc_quantize_q8k.restype = None
+        L.orc_dot_q8k.argtypes = [vp, vp, vp, vp, i32, sz]
+        L.orc_dot_q8k.restype = C.c_float
         L.orc_fused_ffn.argtypes = [vp, vp, vp, vp, i32, sz, sz, vp, vp]
         L.orc_fused_ffn.restype = None
         L.orc_moe_ffn.argtypes = [vp, vp, sz, vp, vp, vp, vp, vp, i32, sz, sz, sz, sz, i32,
@@ -113,9 +117,29 @@ def dot(x, qrow, wtype):
     return np.float32(lib().orc_dot_quant(_p(x), _p(q), wtype, x.size))
 
 
+def quantize_q8k(x):
+    """Q8_K blocks of x (quantize_row_q8): (d[n/256], qs[n], bsums[n/256,16])."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    nb = x.size // 256
+    d = np.empty(nb, np.float32)
+    qs = np.empty(x.size, np.int8)
+    bs = np.empty((nb, 16), np.int16)
+    lib().orc_quantize_q8k(_p(x), x.size, _p(d), _p(qs), _p(bs))
+    return d, qs, bs
+
+
+def dot_q8k(x, qrow, wtype):
+    """The -DQ8_DOT product of x with one Q4_K/Q6_K row: x quantized to
+    Q8_K, then the integer dot (dot_q8_quant)."""
+    d, qs, bs = quantize_q8k(x)
+    q = np.ascontiguousarray(qrow, np.uint8)
+    return np.float32(lib().orc_dot_q8k(_p(d), _p(qs), _p(bs), _p(q), wtype, qs.size))
+
+
 def qmat_mul(x, q, wtype, N, K, add=None):
-    """out[T][N] = add + x[T][K] . W^T for a Q8_0/Q4_0 matrix of N rows
-    (moe_oracle.c orc_qmat_mul); add None, [N] or [T][N]."""
+    """out[T][N] = add + x[T][K] . W^T for a Q8_0/Q4_0/Q4_K/Q6_K matrix of N
+    rows (moe_oracle.c orc_qmat_mul; K-quants with K % 256 == 0 through Q8_K);
+    add None, [N] or [T][N]."""
     x = np.ascontiguousarray(x, np.float32).reshape(-1, K)
     q = np.ascontiguousarray(q, np.uint8)
     T = x.shape[0]

@@ -4,7 +4,8 @@
  * nn.c:221-262, top_k nn.c:276-308, fused_ffn_silu nn.c:496-539,
  * dot_f32_quant quant.c:577-614, quantize_row_q8_0 quant.c:62-78,
  * tensor_mma_transposed_2x2 with a Q8_0/Q4_0 right operand,
- * tensor_div_scalar / tensor_add tensor.c:334-353,435-456), linked against
+ * tensor_div_scalar / tensor_add tensor.c:334-353,435-456, quantize_row_q8
+ * and dot_q8_quant quant.c:627-668, dequant_row quant.c:533-575), linked against
  * the reference's own objects.  ref_moe_ffn_composed runs moe_ffn's loop
  * (olmoe.c:355-406, llama.c:407-456) over those functions with the router
  * bias passed through tensor_mma_transposed_2x2's add argument; with a NULL
@@ -181,4 +182,36 @@ void ref_qmat_mul(const float *x, size_t T, const void *q, int wtype, size_t N, 
 	tensor_free_mapped(o);
 	if (a)
 		tensor_free_mapped(a);
+}
+
+/* quantize_row_q8 (quant.c:627-654), unpacked to d[n/256], qs[n],
+ * bsums[n/256][16] */
+void ref_quantize_q8k(const float *x, size_t n, float *d, int8_t *qs, int16_t *bsums)
+{
+	size_t nb = n / QK_K;
+	block_q8_K *y = malloc(nb * sizeof(block_q8_K));
+	quantize_row_q8(x, y, n);
+	for (size_t i = 0; i < nb; i++) {
+		d[i] = y[i].d;
+		memcpy(qs + i * QK_K, y[i].qs, QK_K);
+		memcpy(bsums + i * 16, y[i].bsums, 16 * sizeof(int16_t));
+	}
+	free(y);
+}
+
+/* dot_q8_quant (quant.c:656-668) of row 0 of qrow with x quantized by
+ * quantize_row_q8, as tensor_mma_transposed_2x2 calls it */
+float ref_dot_q8k(const float *x, const void *qrow, int wtype, size_t n)
+{
+	size_t nb = n / QK_K;
+	block_q8_K *y = malloc(nb * sizeof(block_q8_K));
+	quantize_row_q8(x, y, n);
+	float r = dot_q8_quant(y, x, qrow, wtype, 0, n);
+	free(y);
+	return r;
+}
+
+void ref_dequant(const void *qrow, int wtype, float *dst, size_t n)
+{
+	dequant_row(qrow, wtype, 0, dst, n);
 }

@@ -122,6 +122,19 @@ def qmat_case(i: int, name: str):
     return wt, T, N, K, q, x, a, g[f"{name}_out"]
 
 
+def kq_case(name: str):
+    """(wtype, T, N, K, q, x, add, expected out) of K-quant product case
+    `name` (tests/golden/kquant.npz), after checking the regenerated inputs
+    are the fixture's bytes."""
+    mg = _make_golden_module()
+    wt, T, N, K, add = mg.KQ_CASES[name]
+    q, x, a = mg.kq_inputs(list(mg.KQ_CASES).index(name), wt, T, N, K, add)
+    g = golden("kquant.npz")
+    assert sha(q) == str(g[f"{name}_sha_w"]) and sha(x) == str(g[f"{name}_sha_x"])
+    assert (sha(a) if a is not None else "") == str(g[f"{name}_sha_add"])
+    return wt, T, N, K, q, x, a, g[f"{name}_out"]
+
+
 def _make_golden_module():
     import importlib.util
     spec = importlib.util.spec_from_file_location("make_golden",

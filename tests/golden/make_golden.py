@@ -24,13 +24,19 @@ same bytes.  Outputs are the reference's own results:
                      argument of tensor_mma_transposed_2x2)
   qmat.npz           tensor_mma_transposed_2x2 with a Q8_0/Q4_0 right operand
                      (matmul.c:13-33,285-312) for T = 1..9, add NULL/[N]/[T][N]
+  kquant.npz         the K-quant path of the default -DQ8_DOT build:
+                     quantize_row_q8 (quant.c:627-654) on seeded and edge
+                     blocks; dot_q8_quant / dot_f32_quant / dequant_row on
+                     Q4_K/Q6_K rows (the fill patterns of test/quant_dot.c:
+                     12-34 and seeded rows); tensor_mma_transposed_2x2 with
+                     a Q4_K/Q6_K right operand (matmul.c:285-312)
   model_<case>.npz   the whole OLMoE model (olmoe.c:409-580): greedy tokens
                      and per-step logits of the reference's olmoe_decode run
                      over the prompt then n_gen steps, and of its generate
                      order (one olmoe_prefill of the prompt, then decode)
 
-`python tests/golden/make_golden.py qmat` writes qmat.npz alone, `... model`
-the model fixtures alone.
+`python tests/golden/make_golden.py qmat` writes qmat.npz alone, `... kquant`
+kquant.npz alone, `... model` the model fixtures alone.
 """
 from __future__ import annotations
 
@@ -75,6 +81,12 @@ def ref():
     L.ref_dot.restype = C.c_float
     L.ref_quantize_q8_0.argtypes = [vp, vp, sz]
     L.ref_quantize_q4_0.argtypes = [vp, vp, sz]
+    L.ref_quantize_q8k.argtypes = [vp, sz, vp, vp, vp]
+    L.ref_quantize_q8k.restype = None
+    L.ref_dot_q8k.argtypes = [vp, vp, i32, sz]
+    L.ref_dot_q8k.restype = C.c_float
+    L.ref_dequant.argtypes = [vp, i32, vp, sz]
+    L.ref_dequant.restype = None
     return L
 
 
@@ -116,6 +128,128 @@ def qmat_inputs(i: int, wt: int, T: int, N: int, K: int, add):
     if add is not None:
         a = hipmoe.synth_normal(SEED, 0x7600 + i, N if add == "bcast" else T * N)
     return q, x, a
+
+
+# K-quant products: name: (wtype, T, N, K, add) as QMAT_CASES.  K = 768
+# (three super-blocks) puts odd Q6_K blocks and rows at 2-byte offsets;
+# 14336 is Mixtral's d_ff; 256 one super-block a row.
+KQ_CASES = {
+    "q4k_t1": (hipmoe.Q4_K, 1, 203, 2048, None),
+    "q4k_t5_rows": (hipmoe.Q4_K, 5, 77, 4096, "rows"),
+    "q4k_t2_bcast_14336": (hipmoe.Q4_K, 2, 40, 14336, "bcast"),
+    "q4k_t1_256": (hipmoe.Q4_K, 1, 300, 256, None),
+    "q6k_t1": (hipmoe.Q6_K, 1, 130, 4096, None),
+    "q6k_t3_bcast": (hipmoe.Q6_K, 3, 64, 2048, "bcast"),
+    "q6k_t9_rows_768": (hipmoe.Q6_K, 9, 33, 768, "rows"),
+    "q6k_t1_14336": (hipmoe.Q6_K, 1, 24, 14336, None),
+}
+
+
+def kq_inputs(i: int, wt: int, T: int, N: int, K: int, add):
+    q = hipmoe.synth_quant_matrix(SEED, 0x7a00 + i, 0.02, wt, N, K)
+    x = hipmoe.synth_normal(SEED, 0x7b00 + i, T * K).reshape(T, K)
+    a = None
+    if add is not None:
+        a = hipmoe.synth_normal(SEED, 0x7c00 + i, N if add == "bcast" else T * N)
+    return q, x, a
+
+
+def fill_q4_K(nb: int) -> np.ndarray:
+    """The deterministic Q4_K blocks of test/quant_dot.c:12-22."""
+    out = np.zeros((nb, 144), np.uint8)
+    for i in range(nb):
+        out[i, 0:2] = (0x00, 0x3C)   # d = 1.0 (f16 0x3C00, little-endian)
+        out[i, 2:4] = (0x00, 0x38)   # dmin = 0.5
+        out[i, 4:16] = [5 + (j * 3) % 40 for j in range(12)]
+        out[i, 16:144] = [((i + j) * 7 + 3) & 0xFF for j in range(128)]
+    return out.reshape(-1)
+
+
+def fill_q6_K(nb: int) -> np.ndarray:
+    """The deterministic Q6_K blocks of test/quant_dot.c:24-34."""
+    out = np.zeros((nb, 210), np.uint8)
+    for i in range(nb):
+        out[i, 0:128] = [((i + j) * 11 + 7) & 0xFF for j in range(128)]
+        out[i, 128:192] = [((i + j) * 5 + 2) & 0xFF for j in range(64)]
+        out[i, 192:208] = np.array([((i + j) * 3) % 61 - 30 for j in range(16)],
+                                   np.int8).view(np.uint8)
+        out[i, 208:210] = (0x00, 0x3C)
+    return out.reshape(-1)
+
+
+def q8k_blocks() -> np.ndarray:
+    """Seeded 256-value blocks plus edge cases for quantize_row_q8."""
+    blocks = [hipmoe.synth_normal(SEED, 0x7d00 + i, 256, 0.0, s)
+              for i, s in enumerate([0.02] * 6 + [1.0] * 6 + [1e-3, 40.0, 3e4, 1e-30])]
+    i = np.arange(256, dtype=np.float32)
+    blocks.append(np.sin(i * np.float32(0.1)).astype(np.float32) * np.float32(0.5))
+    blocks.append(np.zeros(256, np.float32))                  # amax = 0: zero block
+    b = np.zeros(256, np.float32); b[77] = -2.5; blocks.append(b)   # one negative spike
+    b = hipmoe.synth_normal(SEED, 0x7e00, 256, 0.0, 0.1)
+    b[10], b[200] = 3.0, -3.0; blocks.append(b)               # tie: the first wins (+)
+    b = hipmoe.synth_normal(SEED, 0x7e01, 256, 0.0, 0.1)
+    b[10], b[200] = -3.0, 3.0; blocks.append(b)               # tie: the first wins (-)
+    b = np.full(256, 0.25, np.float32); b[3] = -0.5; blocks.append(b)  # +63.5 rounds away
+    blocks.append((i - 128) / np.float32(64.0))               # ramp with x.5 products
+    return np.stack(blocks).astype(np.float32)
+
+
+def kquant_goldens(R):
+    fx = {}
+    # quantize_row_q8
+    xb = q8k_blocks()
+    flat = np.ascontiguousarray(xb.reshape(-1))
+    nb = xb.shape[0]
+    d = np.empty(nb, np.float32)
+    qs = np.empty(flat.size, np.int8)
+    bs = np.empty((nb, 16), np.int16)
+    R.ref_quantize_q8k(p(flat), flat.size, p(d), p(qs), p(bs))
+    fx.update(q8k_x=xb, q8k_d=d, q8k_qs=qs, q8k_bsums=bs)
+    # the reference test's rows (test/quant_dot.c:62-153): dots and dequant
+    for wt, name, fill in ((hipmoe.Q4_K, "q4k", fill_q4_K), (hipmoe.Q6_K, "q6k", fill_q6_K)):
+        for nbk in (1, 16):
+            n = 256 * nbk
+            row = fill(nbk)
+            x = (np.sin(np.arange(n, dtype=np.float32) * np.float32(0.037))
+                 * np.float32(0.1)).astype(np.float32)
+            deq = np.empty(n, np.float32)
+            R.ref_dequant(p(row), wt, p(deq), n)
+            fx[f"fill_{name}_{nbk}_w"] = row
+            fx[f"fill_{name}_{nbk}_x"] = x
+            fx[f"fill_{name}_{nbk}_dot_q8"] = np.float32(R.ref_dot_q8k(p(x), p(row), wt, n))
+            fx[f"fill_{name}_{nbk}_dot_f32"] = np.float32(R.ref_dot(p(x), p(row), wt, n))
+            fx[f"fill_{name}_{nbk}_deq"] = deq
+        # seeded rows: every K the products use
+        for n in (256, 768, 2048, 4096, 14336):
+            rows = 3
+            qm = hipmoe.synth_quant_matrix(SEED, 0x7f00 + n + wt, 0.02, wt, rows, n)
+            x = hipmoe.synth_normal(SEED, 0x7f80 + n + wt, rows * n).reshape(rows, n)
+            rb = hipmoe.row_bytes(wt, n)
+            q8 = np.empty(rows, np.float32)
+            f32 = np.empty(rows, np.float32)
+            deq = np.empty((rows, n), np.float32)
+            for r in range(rows):
+                xr = np.ascontiguousarray(x[r])
+                wr = np.ascontiguousarray(qm[r * rb:(r + 1) * rb])
+                q8[r] = R.ref_dot_q8k(p(xr), p(wr), wt, n)
+                f32[r] = R.ref_dot(p(xr), p(wr), wt, n)
+                R.ref_dequant(p(wr), wt, p(deq[r]), n)
+            fx[f"rows_{name}_{n}_sha_w"] = sha(qm)
+            fx[f"rows_{name}_{n}_sha_x"] = sha(x)
+            fx[f"rows_{name}_{n}_dot_q8"] = q8
+            fx[f"rows_{name}_{n}_dot_f32"] = f32
+            fx[f"rows_{name}_{n}_deq0"] = deq[0]
+    # the product
+    for i, (name, (wt, T, N, K, add)) in enumerate(KQ_CASES.items()):
+        q, x, a = kq_inputs(i, wt, T, N, K, add)
+        out = np.empty((T, N), np.float32)
+        R.ref_qmat_mul(p(x), T, p(q), wt, N, K, p(a), 0 if a is None else a.size, p(out))
+        fx[f"{name}_sha_w"] = sha(q)
+        fx[f"{name}_sha_x"] = sha(x)
+        fx[f"{name}_sha_add"] = sha(a) if a is not None else ""
+        fx[f"{name}_out"] = out
+        print(f"kquant {name}: T={T} N={N} K={K} add={add} |out|={np.linalg.norm(out):.4f}")
+    np.savez(os.path.join(HERE, "kquant.npz"), seed=SEED, **fx)
 
 
 def qmat_goldens(R):
@@ -230,9 +364,13 @@ def main():
     if sys.argv[1:2] == ["model"]:
         model_goldens(R, sys.argv[2:] or list(MODEL_CASES))
         return
+    if sys.argv[1:] == ["kquant"]:
+        kquant_goldens(R)
+        return
     qmat_goldens(R)
     if sys.argv[1:] == ["qmat"]:
         return
+    kquant_goldens(R)
 
     # ---- quantizers -----------------------------------------------------
     blocks = quant_blocks()

@@ -98,7 +98,11 @@ def test_oracle_library_is_separate_from_product():
 
 
 @pytest.mark.parametrize("wtype,N,K,msg", [
-    (3, 64, 2048, "unsupported weight type"),
+    (4, 64, 2048, "unsupported weight type"),
+    (0, 64, 2048, "unsupported weight type"),
+    (3, 64, 2000, "not supported for K-quants"),
+    (5, 64, 65536, "not supported for K-quants"),
+    (5, 0, 2048, "not supported for K-quants"),
     (1, 64, 14336, "not supported"),
     (1, 64, 768, "not supported"),
     (2, 64, 128, "not supported"),
@@ -117,6 +121,10 @@ def test_qmat_calls_on_null_return_zero():
     assert L.hip_moe_qmat_mul_dev(None, 1, 1, None, 0, 1, None) == 0
     assert L.hip_moe_qmat_bytes(None) == 0
     L.hip_moe_qmat_free(None)
+    assert L.hip_moe_quantize_q8k_dev(None, 1, 256, None, None, None, None) == 0
+    assert "NULL" in hipmoe.last_error()
+    assert L.hip_moe_quantize_q8k_dev(16, 1, 200, 16, 16, 16, None) == 0
+    assert "multiple of 256" in hipmoe.last_error()
 
 
 def test_lm_calls_on_null_return_zero():

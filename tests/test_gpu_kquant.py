@@ -1,0 +1,124 @@
+"""GPU parity of the K-quant dense product (Q4_K / Q6_K matrices through
+Q8_K activations: hip_moe_qmat_* and hip_moe_quantize_q8k_dev, kquant.hip)
+through the C ABI.  The bar is bit-exact everywhere: the per-super-block
+sums are exact integers and the fp32 steps (scale products, the sequential
+fma over super-blocks, the final add) are the reference's own.
+
+  * quantize_row_q8 of the fixture's seeded and edge blocks equals the
+    compiled reference's (tests/golden/kquant.npz) bit for bit, and the
+    oracle's on a large seeded input (Mixtral's d_ff, 4 tokens);
+  * the product equals the compiled reference's output on every fixture case
+    (K = 256 .. 14336, T = 1..9, add NULL / [N] / [T][N], odd Q6_K blocks at
+    2-byte offsets);
+  * full sizes: the Mixtral lm_head as Q6_K (32000 x 4096) and a Q4_K
+    attention projection (4096 x 4096), T = 1, against the oracle; T = 12 at
+    K = 4096 (more tokens than one LDS pass holds: two passes);
+  * a HIP graph of the product replays bit-identically.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import hipmoe
+import oracle
+from common import bits, golden, kq_case, rel_l2
+
+pytestmark = pytest.mark.gpu
+SEED = 1337
+KQ_NAMES = ["q4k_t1", "q4k_t5_rows", "q4k_t2_bcast_14336", "q4k_t1_256", "q6k_t1",
+            "q6k_t3_bcast", "q6k_t9_rows_768", "q6k_t1_14336"]
+
+
+def say(msg):
+    print(f"[gpu-test] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def need_gpu():
+    assert hipmoe.hip().device_count() >= 1, "no HIP device visible: GPU tests need an MI355X"
+
+
+def test_gpu_q8k_quantize_vs_reference():
+    g = golden("kquant.npz")
+    x = g["q8k_x"]
+    say(f"quantize_q8k: {x.shape[0]} fixture blocks")
+    d, qs, bs = hipmoe.quantize_q8k_dev(x.reshape(1, -1))
+    assert np.array_equal(bits(d.ravel()), bits(g["q8k_d"]))
+    assert np.array_equal(qs.ravel(), g["q8k_qs"])
+    assert np.array_equal(bs.reshape(-1, 16), g["q8k_bsums"])
+    x2 = hipmoe.synth_normal(SEED, 0x7e20, 4 * 14336, 0.0, 1.0).reshape(4, 14336)
+    say("quantize_q8k: 4 x 14336 seeded")
+    d, qs, bs = hipmoe.quantize_q8k_dev(x2)
+    od, oq, ob = oracle.quantize_q8k(x2.ravel())
+    assert np.array_equal(bits(d.ravel()), bits(od))
+    assert np.array_equal(qs.ravel(), oq) and np.array_equal(bs.reshape(-1, 16), ob)
+
+
+@pytest.mark.parametrize("name", KQ_NAMES)
+def test_gpu_kquant_qmat_vs_reference_golden(name):
+    wt, T, N, K, q, x, a, want = kq_case(name)
+    say(f"kquant qmat {name}: wt={wt} T={T} N={N} K={K}")
+    W = hipmoe.QMat(q, wt, N, K)
+    try:
+        got = W.mul(x, a)
+    finally:
+        W.free()
+    same = np.array_equal(bits(got), bits(want))
+    say(f"kquant qmat {name}: bitwise {same}, rel L2 {rel_l2(got, want):.3e}")
+    assert same
+
+
+@pytest.mark.parametrize("wt,N,K,T", [(hipmoe.Q6_K, 32000, 4096, 1),
+                                      (hipmoe.Q4_K, 4096, 4096, 1),
+                                      (hipmoe.Q4_K, 1000, 4096, 12),
+                                      (hipmoe.Q6_K, 4096, 14336, 1)])
+def test_gpu_kquant_qmat_full_size(wt, N, K, T):
+    say(f"kquant qmat full size wt={wt} N={N} K={K} T={T}")
+    q = hipmoe.synth_quant_matrix(SEED, 0x7e30 + wt, 0.02, wt, N, K)
+    x = hipmoe.synth_normal(SEED, 0x7e31 + T, T * K).reshape(T, K)
+    W = hipmoe.QMat(q, wt, N, K)
+    try:
+        got = W.mul(x)
+    finally:
+        W.free()
+    want = oracle.qmat_mul(x, q, wt, N, K)
+    nbad = int(np.sum(bits(got) != bits(want)))
+    say(f"kquant qmat full size: {nbad} of {want.size} outputs differ")
+    assert nbad == 0
+
+
+def test_gpu_kquant_qmat_graph_replays():
+    say("HIP graph of K-quant products (Q6_K 2000 x 2048 T=1, Q4_K 2000 x 2048 T=3)")
+    H = hipmoe.hip()
+    N, K = 2000, 2048
+    q6 = hipmoe.synth_quant_matrix(SEED, 0x7e40, 0.02, hipmoe.Q6_K, N, K)
+    q4 = hipmoe.synth_quant_matrix(SEED, 0x7e41, 0.02, hipmoe.Q4_K, N, K)
+    x1 = hipmoe.synth_normal(SEED, 0x7e42, K).reshape(1, K)
+    x3 = hipmoe.synth_normal(SEED, 0x7e43, 3 * K).reshape(3, K)
+    W6, W4 = hipmoe.QMat(q6, hipmoe.Q6_K, N, K), hipmoe.QMat(q4, hipmoe.Q4_K, N, K)
+    e1, e3 = W6.mul(x1), W4.mul(x3)
+    s = H.stream()
+    d_x1, d_x3 = H.upload(x1), H.upload(x3)
+    d_o1, d_o3 = H.malloc(N * 4), H.malloc(3 * N * 4)
+    try:
+        H.begin_capture(s)
+        W6.mul_dev(d_x1, 1, d_o1, None, 0, s)
+        W4.mul_dev(d_x3, 3, d_o3, None, 0, s)
+        ge = H.end_capture(s)
+        for rep in range(3):
+            H.check(H.h.hipMemsetAsync(d_o1, 0, N * 4, s), "memset")
+            H.check(H.h.hipMemsetAsync(d_o3, 0, 3 * N * 4, s), "memset")
+            H.graph_launch(ge, s)
+            H.stream_sync(s)
+            assert np.array_equal(bits(H.download(d_o1, (1, N), np.float32)), bits(e1)), rep
+            assert np.array_equal(bits(H.download(d_o3, (3, N), np.float32)), bits(e3)), rep
+            W4.mul(x3[:2])
+        assert np.array_equal(bits(e1), bits(oracle.qmat_mul(x1, q6, hipmoe.Q6_K, N, K)))
+        assert np.array_equal(bits(e3), bits(oracle.qmat_mul(x3, q4, hipmoe.Q4_K, N, K)))
+    finally:
+        for p in (d_x1, d_x3, d_o1, d_o3):
+            H.free(p)
+        W6.free()
+        W4.free()
