@@ -268,11 +268,13 @@ __device__ static inline void stage_digits(u32 *dst, const float *src, int n)
 }
 
 /* the same from a token held transposed in LDS: element k at
- * src[(k % 8) * RS + k / 8] */
-template <int NT>
-__device__ static inline void stage_digits_lds(u32 *dst, const float *src, int n, int RS)
+ * src[(k % 8) * RS + k / 8]; NTH threads, this one numbered tid (NTH a
+ * multiple of 8: a block's 8 staging lanes are consecutive lanes of a wave) */
+template <int NTH>
+__device__ static inline void stage_digits_lds(u32 *dst, const float *src, int n, int RS,
+					       int tid)
 {
-	for (int i = threadIdx.x; i < n / 4; i += NT) {
+	for (int i = tid; i < n / 4; i += NTH) {
 		const int r = (4 * i) & 7, c = (4 * i) >> 3;
 		const float4 v = {src[r * RS + c], src[(r + 1) * RS + c], src[(r + 2) * RS + c],
 				  src[(r + 3) * RS + c]};
@@ -410,8 +412,9 @@ __device__ static inline void stage_transposed(float *dst, const float *src, int
 
 /* acc = fma(x[k], w[k], acc) over k = 0, 8, 16, ... of one transposed row
  * pair (E8 floats each).  The chain is 256 dependent FMAs for E = 2048; its
- * LDS operands come in batches of 8 FMAs (4 reads), three batches in flight
- * (12 reads: the LDS counter, 4 bits, can wait for exactly the oldest). */
+ * LDS operands come in batches of 8 FMAs (4 reads), four batches in
+ * rotation, each loaded three batches ahead of its FMAs (12 reads in
+ * flight: the LDS counter, 4 bits, can wait for exactly the oldest). */
 struct chain_batch {
 	float4 x[2], w[2];
 	__device__ inline void load(const float4 *xr, const float4 *wr, int b)
@@ -435,35 +438,41 @@ struct chain_batch {
 	}
 };
 
-/* the loads run up to 5 batches (40 floats) past a row's E8: the rows are
- * followed by RS - E8 = 4 floats of padding and the staging area by
- * CHAIN_OVERRUN floats */
+/* NB (batches) a multiple of 4: the loop has no early exit, which keeps
+ * the compiler's LDS waits at "all but the two younger batches" (an exit
+ * inside the loop made them wait for every read: 12.8 -> 10.2 clocks per
+ * FMA measured alone).  The loads run up to 3 batches (24 floats) past a
+ * row's E8: the rows are followed by RS - E8 = 4 floats of padding and the
+ * staging area by CHAIN_OVERRUN floats. */
 #define CHAIN_OVERRUN 64
 __device__ static inline float router_chain(const float *xrow, const float *wrow, int NB)
 {
 	const float4 *xr = (const float4 *)xrow, *wr = (const float4 *)wrow;
-	chain_batch A, B, C;
+	chain_batch A, B, C, D;
 	float acc = 0.0f;
 	/* the scheduling barriers keep each batch's reads where they are
-	 * issued: two batches ahead of their FMAs */
+	 * issued: three batches ahead of their FMAs */
 	A.load(xr, wr, 0);
 	B.load(xr, wr, 1);
 	C.load(xr, wr, 2);
 	__builtin_amdgcn_sched_barrier(0);
 #pragma unroll 1
-	for (int b = 0; b < NB; b += 3) {
+	for (int b = 0; b < NB; b += 4) {
+		D.load(xr, wr, b + 3);
+		__builtin_amdgcn_sched_barrier(0);
 		acc = A.run(acc);
-		A.load(xr, wr, b + 3);
 		__builtin_amdgcn_sched_barrier(0);
-		if (b + 1 >= NB)
-			break;
+		A.load(xr, wr, b + 4);
+		__builtin_amdgcn_sched_barrier(0);
 		acc = B.run(acc);
-		B.load(xr, wr, b + 4);
 		__builtin_amdgcn_sched_barrier(0);
-		if (b + 2 >= NB)
-			break;
+		B.load(xr, wr, b + 5);
+		__builtin_amdgcn_sched_barrier(0);
 		acc = C.run(acc);
-		C.load(xr, wr, b + 5);
+		__builtin_amdgcn_sched_barrier(0);
+		C.load(xr, wr, b + 6);
+		__builtin_amdgcn_sched_barrier(0);
+		acc = D.run(acc);
 		__builtin_amdgcn_sched_barrier(0);
 	}
 	return acc;
@@ -471,10 +480,14 @@ __device__ static inline float router_chain(const float *xrow, const float *wrow
 
 /* router row j for every token, published into every replica by wave 0;
  * prev_epoch (the launch's epoch minus one, valid in thread 0) is consumed
- * only after the chain, so its load is in flight meanwhile */
+ * only after the chain, so its load is in flight meanwhile.  dig (one
+ * token): the other waves stage the token's digit blocks there while wave
+ * 0 runs the chain. */
 template <int NT, int E>
-__device__ static void router_row(const DecodeArgs &a, int j, u32 prev_epoch, float *lds)
+__device__ static void router_row(const DecodeArgs &a, int j, u32 prev_epoch, float *lds,
+				  u32 *dig)
 {
+	static_assert(E % 256 == 0, "the chain runs whole rounds of four batches");
 	constexpr int E8 = E / 8, RS = E8 + 4;
 	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
 	float *sw = lds;          /* [8][RS] router row, transposed */
@@ -511,6 +524,8 @@ __device__ static void router_row(const DecodeArgs &a, int j, u32 prev_epoch, fl
 			acc = acc + __shfl_xor(acc, 1, 8);
 			if (lane == 0)
 				s_logit = (a.bias ? a.bias[j] : 0.0f) + acc;
+		} else if (t == 0 && dig) {
+			stage_digits_lds<NT - WAVE>(dig, sx, E, RS, (int)threadIdx.x - WAVE);
 		}
 		__syncthreads();
 		if (wave == 0) { /* NREP == WAVE: lane r writes replica r */
@@ -538,14 +553,14 @@ __device__ static void route_local(const DecodeArgs &a, u32 epoch, float *lds, u
 			      (size_t)(blockIdx.x % NREP) * a.rep_stride;
 	float *scr = lds + wave * (MOE_MAX_NE + 2 * MOE_MAX_TOPK);
 	if (a.T == 1) {
-		/* one token: wave 0 polls; every wave runs the softmax (the same
-		 * bits) and ranks each key against 64 / NW of the others; wave 0
-		 * adds the parts and fills the slots */
+		/* one token: wave 0 polls and runs the softmax; every wave ranks
+		 * each key against 64 / NW of the others; wave 0 adds the parts
+		 * and fills the slots */
 		constexpr int NW = NT / WAVE, PER = WAVE / NW;
 		static_assert(PER % 2 == 0, "keys are read in pairs");
-		__shared__ float s_lg[WAVE];
 		__shared__ __attribute__((aligned(16))) uint64_t s_key[WAVE];
 		__shared__ int s_rk[NW][WAVE];
+		float p = 0.0f;
 		if (wave == 0) {
 			const uint64_t idle = (uint64_t)epoch << 32;
 			uint64_t v = 0;
@@ -561,15 +576,12 @@ __device__ static void route_local(const DecodeArgs &a, u32 epoch, float *lds, u
 				}
 				backoff(step);
 			}
-			s_lg[lane] = __builtin_bit_cast(float, (u32)v);
+			uint64_t key;
+			p = softmax64(__builtin_bit_cast(float, (u32)v), a.NE, s_tab, lane, key);
+			s_key[lane] = key;
 		}
 		__syncthreads();
-		uint64_t key;
-		const float p = softmax64(s_lg[lane], a.NE, s_tab, lane, key);
-		if (wave == 0)
-			s_key[lane] = key;
-		__syncthreads();
-		s_rk[wave][lane] = rank_part64(s_key + wave * PER, PER, key);
+		s_rk[wave][lane] = rank_part64(s_key + wave * PER, PER, s_key[lane]);
 		__syncthreads();
 		if (wave == 0) {
 			int rank = 0;
@@ -707,14 +719,8 @@ void k_moe_decode(DecodeArgs a)
 	/* one token: a router workgroup stages it from its router row's LDS
 	 * copy (no second round trip) */
 	const bool st0 = b < a.NE && x0 < x1 && a.T == 1;
-	if (b < a.NE) {
-		router_row<NT, CG * S::COLS>(a, b, prev_epoch, rl);
-		__syncthreads();
-		if (st0) {
-			constexpr int RS = CG * S::COLS / 8 + 4;
-			stage_digits_lds<NT>(sx, rl + 8 * RS, a.E, RS);
-		}
-	}
+	if (b < a.NE)
+		router_row<NT, CG * S::COLS>(a, b, prev_epoch, rl, st0 ? sx : nullptr);
 	/* the tokens of this workgroup's items (they do not depend on routing) */
 	if (x0 < x1 && !st0)
 		for (int t = t0; t <= (x1 - 1) / 2 / IPT; t++)
