@@ -35,7 +35,9 @@
  * the tokens itself into LDS (Q8_K blocks padded to 68 dwords so the lanes
  * reading different blocks hit different banks), TT tokens at a time; the
  * weights of a block stay in registers for all TT tokens, and the next
- * block's weights load while the current one's dots run.
+ * block's weights load while the current one's dots run.  A Q6_K product
+ * for one token instead streams the matrix through an LDS ring
+ * (k_kq_stream below).
  *
  * Bound: HBM.  Algorithmic bytes per call: N * K/256 * (144 | 210) + T*K*4
  * (x) + T*N*4 (out) (+ T*N*4 with add).
@@ -112,11 +114,28 @@ struct KqTok {
 	int *sb;
 };
 
+/* one token held in LDS (xl, K floats) into its staged Q8_K blocks */
+__device__ static inline void kq_stage_lds(const KqTok &st, const float *xl, int K)
+{
+	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, nb = K / 256;
+	for (int b = wave; b < nb; b += (int)blockDim.x / WAVE) {
+		const float4 v = ((const float4 *)(xl + (size_t)b * 256))[lane];
+		float d;
+		int bs;
+		const u32 q = q8k_block(v, lane, &d, &bs);
+		st.sq[b * KQ_QSTRIDE + lane] = (int)q;
+		if (lane % 4 == 0)
+			st.sb[b * 16 + lane / 4] = bs;
+		if (lane == 0)
+			st.sd[b] = d;
+	}
+}
+
 __device__ static inline void kq_stage(const KqTok &st, const float *__restrict__ x, int K,
 				       int t0, int TT)
 {
 	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, nb = K / 256;
-	for (int b = wave; b < TT * nb; b += KQ_THREADS / WAVE) {
+	for (int b = wave; b < TT * nb; b += (int)blockDim.x / WAVE) {
 		const int tok = b / nb, i = b % nb;
 		const float4 v = ((const float4 *)(x + (size_t)(t0 + tok) * K + (size_t)i * 256))[lane];
 		float d;
@@ -331,6 +350,234 @@ __global__ __launch_bounds__(KQ_THREADS) void k_kq_gemv(KQ_ARGS)
 	}
 }
 
+/*
+ * Q6_K, one token, no add: the matrix streams through an LDS ring by LDS-DMA.
+ * A tile is RT = 128 / nb rows (RT * nb <= 128 super-blocks, contiguous
+ * bytes); each of the 8 waves moves its share of a tile with RG::PW
+ * wave-wide global_load_lds_dwordx4 loads (1 KB each, the pieces past the
+ * tile's end repeat its last one), NST - 1 tiles stay in flight, and a
+ * workgroup (one per CU) takes tiles blockIdx.x, + gridDim.x, ...  Four
+ * threads share a super-block, a quarter (64 values) each, and add their
+ * exact integer sums across lanes; the row sums of the tile before (one
+ * thread per row, nb sequential steps) run in waves 6-7 ahead of their
+ * quarters.  Global loads inside the loop would make the compiler wait for
+ * every DMA: the loop has none (the token is staged before it, the outputs
+ * are stores).  Whole blocks per thread (128 of 256 threads busy) measured
+ * 45 us for the Q6_K Mixtral lm_head against 34 for the register path:
+ * the tile's dots, not the ring, were the bound (the ring alone streams at
+ * ~6 TB/s).
+ */
+#define KQ_STHREADS 512
+template <int WT> struct kq_ring;
+template <> struct kq_ring<5> {
+	static constexpr int PW = 4, NST = 4; /* 128 * 210 B = 26.3 KB a tile, 32 KB slots */
+};
+#define KQ_TB 128       /* super-blocks a tile holds at most */
+#define KQ_STREAM_NB 32 /* super-blocks a row holds at most (K <= 8192) */
+#define KQ_OBUF 1024    /* outputs a workgroup keeps in LDS until its last tile */
+
+/* dwords at LDS address p (2-byte aligned): n of them, realigned.  The
+ * aligned pointer is derived from p itself (not through an integer), so
+ * the compiler keeps it in LDS: a flat load would also count in vmcnt and
+ * make every read wait for the tiles in flight. */
+template <int N>
+__device__ static inline void lds_dwords_u16(const uint8_t *p, u32 (&w)[N])
+{
+	const u32 sh = (u32)((uintptr_t)p & 3);
+	const u32 *q = (const u32 *)(p - sh);
+	u32 raw[N + 1];
+#pragma unroll
+	for (int k = 0; k <= N; k++)
+		raw[k] = q[k];
+#pragma unroll
+	for (int k = 0; k < N; k++)
+		w[k] = __builtin_amdgcn_alignbyte(raw[k + 1], raw[k], sh);
+}
+
+/* quarter qt = (chunk c = qt / 2, half hf = qt % 2) of a Q6_K block in LDS:
+ * values c*128 + g*32 + hf*16 + (0..15) for g = 0..3 */
+__device__ static inline int q6k_quarter(const uint8_t *blk, int qt, const int *q8, const int *bs)
+{
+	const int c = qt >> 1, hf = qt & 1;
+	u32 la[4], lb[4], hq[4];
+	lds_dwords_u16<4>(blk + 64 * c + 16 * hf, la);      /* ql[l], l = 16hf .. 16hf+15 */
+	lds_dwords_u16<4>(blk + 64 * c + 32 + 16 * hf, lb); /* ql[l + 32] */
+	lds_dwords_u16<4>(blk + 128 + 32 * c + 16 * hf, hq); /* qh[l] */
+	int si = 0;
+#pragma unroll
+	for (int g = 0; g < 4; g++) {
+		const int4 a = *(const int4 *)(q8 + 32 * c + 8 * g + 4 * hf);
+		const int av[4] = {a.x, a.y, a.z, a.w};
+		int sm = 0;
+#pragma unroll
+		for (int m = 0; m < 4; m++) {
+			const u32 lq = (g & 1) ? lb[m] : la[m];
+			const u32 lo = g < 2 ? lq & 0x0f0f0f0fu : (lq >> 4) & 0x0f0f0f0fu;
+			const u32 hi = ((hq[m] >> (2 * g)) & 0x03030303u) << 4;
+			sm = __builtin_amdgcn_sdot4((int)(lo | hi), av[m], sm, false);
+		}
+		const int j = 8 * c + 2 * g + hf;
+		const int sc = (int)(int8_t)blk[192 + j];
+		si += sc * (sm - 32 * bs[j]);
+	}
+	return si;
+}
+
+template <int WT>
+__global__ __launch_bounds__(KQ_STHREADS, 1) void k_kq_stream(const uint8_t *__restrict__ W, int N,
+							      int K, const float *__restrict__ x,
+							      float *__restrict__ out)
+{
+	constexpr int BYTES = kq<WT>::BYTES;
+	using RG = kq_ring<WT>;
+	constexpr int SLOT = RG::PW * 8192, NST = RG::NST;
+	constexpr int NREC = WT == 3 ? 4 : 2;
+	/* ring, staged token (up to KQ_STREAM_NB super-blocks) and two record
+	 * sets of up to KQ_TB blocks and KQ_TB / 8 rows (nb >= 8): static, so
+	 * the ~140-160 KB need no launch attribute */
+	__shared__ __attribute__((aligned(16)))
+	uint8_t kq_ring_lds[NST * SLOT + KQ_STREAM_NB * (KQ_QSTRIDE + 1 + 16) * 4 +
+			    2 * NREC * (KQ_TB + KQ_TB / 8) * 4];
+	/* the outputs: a store inside the loop would sit in this wave's vmcnt
+	 * until acknowledged and hold back its next tile wait */
+	__shared__ float obuf[KQ_OBUF];
+	/* the DMA asm clobbers memory, after which the compiler would reload
+	 * kernel arguments and the grid size with scalar loads and wait for
+	 * them with lgkmcnt(0), which on gfx950 also waits for every LDS-DMA
+	 * in flight (the ring ran at 3.5 TB/s instead of 6): they are pinned
+	 * in registers once here */
+	int G = (int)gridDim.x;
+	asm volatile("" : "+s"(G));
+	asm volatile("" : "+s"(N), "+s"(K), "+s"(W), "+s"(x), "+s"(out));
+	const int nb = K / 256, RT = KQ_TB / nb, TB = RT * nb;
+	const int tid = threadIdx.x, wave = tid / WAVE;
+	const size_t rb = (size_t)nb * BYTES;
+	const int ntiles = (N + RT - 1) / RT;
+	const int mine = ((int)blockIdx.x < ntiles) ? (ntiles - (int)blockIdx.x + G - 1) / G : 0;
+	uint8_t *ring = kq_ring_lds;
+	KqTok st;
+	st.sq = (int *)(ring + NST * SLOT);
+	st.sd = (float *)(st.sq + nb * KQ_QSTRIDE);
+	st.sb = st.sq + nb * (KQ_QSTRIDE + 1);
+	int *rec = st.sb + nb * 16; /* [2][NREC][TB + RT] */
+	const int rw = TB + RT, rstride = nb + 1;
+	const u32 ring0 = __builtin_amdgcn_readfirstlane(lds_addr(ring));
+
+	if (mine == 0)
+		return; /* the whole workgroup */
+	auto issue = [&](int i) { /* the DMA loads of this workgroup's tile i into slot i % NST */
+		const int t = blockIdx.x + i * G;
+		const int rows = min(RT, N - t * RT);
+		const int np = (int)((rows * rb + 15) / 16); /* 16-byte pieces (the buffer has slack) */
+		const uint8_t *base = W + (size_t)t * RT * rb;
+		const u32 sl = ring0 + (u32)((i % NST) * SLOT) + (u32)(wave * 1024);
+#pragma unroll
+		for (int k = 0; k < RG::PW; k++) {
+			const int pc = min(k * KQ_STHREADS + tid, np - 1);
+			dma_dwordx4(base, (u32)pc * 16u, sl + (u32)(k * 8192));
+		}
+	};
+	/* the row sums of tile i (records set i & 1), thread u per row; the
+	 * records are read 8 super-blocks at a time ahead of their FMAs (nb is
+	 * a multiple of 8 here) */
+	auto finish = [&](int i, int u) {
+		const int t = blockIdx.x + i * G;
+		if (u >= 0 && u < RT && t * RT + u < N) {
+			const int *r = rec + (i & 1) * NREC * rw + u * rstride;
+			float acc = 0.0f, acc_m = 0.0f;
+			for (int j0 = 0; j0 < nb; j0 += 8) {
+				float d[8], dm[8];
+				int si[8], mi[8];
+#pragma unroll
+				for (int k = 0; k < 8; k++) {
+					d[k] = ((const float *)r)[j0 + k];
+					si[k] = r[rw + j0 + k];
+					if constexpr (NREC == 4) {
+						dm[k] = ((const float *)r)[2 * rw + j0 + k];
+						mi[k] = r[3 * rw + j0 + k];
+					}
+				}
+#pragma unroll
+				for (int k = 0; k < 8; k++) {
+					acc = fmaf(d[k], (float)si[k], acc);
+					if constexpr (NREC == 4)
+						acc_m = fmaf(dm[k], (float)mi[k], acc_m);
+				}
+			}
+			const float v = 0.0f + (NREC == 4 ? acc + acc_m : acc);
+			if ((i + 1) * RT <= KQ_OBUF)
+				obuf[i * RT + u] = v;
+			else
+				out[(size_t)t * RT + u] = v; /* past the buffer (vocabularies above 256k) */
+		}
+	};
+
+	/* the token comes by LDS-DMA too, into the last slot (its first tile is
+	 * issued in iteration 0), ahead of the first tiles: waiting for it
+	 * leaves the tiles in flight (a plain load here made the compiler
+	 * wait for every tile, and the ring started empty) */
+	{
+		const u32 xs = ring0 + (u32)((NST - 1) * SLOT) + (u32)(wave * 1024);
+		for (int k = 0; k < K / (4 * KQ_STHREADS); k++)
+			dma_dwordx4(x, (u32)(k * KQ_STHREADS + tid) * 16u, xs + (u32)(k * 8192));
+	}
+	for (int i = 0; i < NST - 1; i++)
+		if (i < mine)
+			issue(i);
+	if (mine >= NST - 1)
+		wait_vm<RG::PW *(NST - 1)>();
+	else
+		wait_vm<0>();
+	__syncthreads();
+	kq_stage_lds(st, (const float *)(ring + (NST - 1) * SLOT), K);
+	__syncthreads(); /* the slot is free again and the token staged */
+	const int bk = tid >> 2, qt = tid & 3; /* super-block of the tile, quarter */
+	for (int i = 0; i < mine; i++) {
+		if (i + NST - 2 < mine)
+			wait_vm<RG::PW *(NST - 2)>(); /* this wave's pieces of tile i are in LDS */
+		else
+			wait_vm<0>();
+		__syncthreads(); /* every wave's pieces; tile i - 1's readers are done */
+		if (i + NST - 1 < mine)
+			issue(i + NST - 1); /* into the slot tile i - 1 used */
+		if (i > 0)
+			finish(i - 1, tid - (KQ_STHREADS - KQ_TB));
+		const int t = blockIdx.x + i * G;
+		const bool live = bk < TB && t * RT + bk / nb < N;
+		const int j = bk % nb;
+		const uint8_t *blk = ring + (i % NST) * SLOT + (live ? bk : 0) * BYTES;
+		static_assert(WT == 5, "the ring instance is Q6_K's");
+		int sumi = q6k_quarter(blk, qt, st.sq + j * KQ_QSTRIDE, st.sb + j * 16), msum = 0;
+		sumi += __shfl_xor(sumi, 1, WAVE);
+		sumi += __shfl_xor(sumi, 2, WAVE);
+		if constexpr (NREC == 4) {
+			msum += __shfl_xor(msum, 1, WAVE);
+			msum += __shfl_xor(msum, 2, WAVE);
+		}
+		if (live && qt == 0) {
+			const int slot = (bk / nb) * rstride + j;
+			const float yd = st.sd[j];
+			int *r = rec + (i & 1) * NREC * rw;
+			const u32 hd = WT == 3 ? *(const u32 *)blk
+					       : (u32)blk[208] | ((u32)blk[209] << 8);
+			((float *)r)[slot] = yd * f16_bits_to_f32(hd);
+			r[rw + slot] = sumi;
+			if constexpr (NREC == 4) {
+				((float *)r)[2 * rw + slot] = -yd * f16_bits_to_f32(hd >> 16);
+				r[3 * rw + slot] = msum;
+			}
+		}
+	}
+	__syncthreads();
+	finish(mine - 1, tid);
+	__syncthreads();
+	for (int o = tid; o < min(mine * RT, KQ_OBUF - KQ_OBUF % RT); o += KQ_STHREADS) {
+		const int i = o / RT, u = o % RT, row = (blockIdx.x + i * G) * RT + u;
+		if (row < N)
+			out[row] = obuf[o];
+	}
+}
+
 /* one wave per 256-value block: quantize_row_q8 into d[T][nb], qs[T][K],
  * bsums[T][nb][16] */
 __global__ __launch_bounds__(KQ_THREADS) void k_q8k_quantize(const float *__restrict__ x, int T,
@@ -417,12 +664,41 @@ extern "C" int moe_kq_grid(int wtype, int K, int T)
 	return per * ncu;
 }
 
+/* the streamed instance: one token, no add, K <= 128 * 256 with whole
+ * 16-byte tiles */
+/* Measured (Mixtral lm_head Q6_K 32000 x 4096 / OLMoE lm_head as Q4_K
+ * 50304 x 2048, one token): the ring 29.4 / 20.5 us, the register path
+ * 34 / 17.4 us.  Per tile the waves' dots and the barrier take ~1.5 us
+ * against ~1.15 us of streaming, so the ring pays off only where the
+ * register path's loads are costliest (Q6_K's 210-byte blocks at 2-byte
+ * offsets): Q4_K keeps the register path. */
+static int kq_stream_ok(int wt, int K, int T, const float *add)
+{
+	const int nb = K / 256;
+	if (wt != 5 || T != 1 || add || nb > KQ_STREAM_NB || nb % 8 || K * 4 > 4 * 8192)
+		return 0; /* the token must fit one ring slot */
+	const int TB = (KQ_TB / nb) * nb;
+	return (TB * (wt == 3 ? 144 : 210)) % 16 == 0;
+}
+
 extern "C" int moe_launch_kq_gemv(int wtype, const uint8_t *W, int N, int K, const float *x,
 				  int T, const float *add, int add_rows, float *out, int nwg,
 				  void *stream)
 {
 	if (!moe_kq_supported(wtype, K) || N < 1 || T < 1)
 		return (int)hipErrorInvalidValue;
+	if (kq_stream_ok(wtype, K, T, add)) {
+		int dev = 0, ncu = 0;
+		if (hipGetDevice(&dev) != hipSuccess ||
+		    hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) !=
+			    hipSuccess)
+			return (int)hipErrorInvalidValue;
+		const int RT = KQ_TB / (K / 256), ntiles = (N + RT - 1) / RT;
+		const dim3 grid(min(ntiles, ncu));
+		hipStream_t s = (hipStream_t)stream;
+		hipLaunchKernelGGL(k_kq_stream<5>, grid, dim3(KQ_STHREADS), 0, s, W, N, K, x, out);
+		return (int)hipGetLastError();
+	}
 	const int nb = K / 256, R = kq_rows(nb), TT = kq_tt(wtype, K, T);
 	const int ngroups = (N + R - 1) / R;
 	const dim3 grid(min(ngroups, nwg > 0 ? nwg : KQ_GRID));

@@ -37,6 +37,39 @@ __device__ static inline float f16_bits_to_f32(u32 h)
 	return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xffffu));
 }
 
+/* One LDS-DMA load per lane (global_load_lds_dwordx4): 16 bytes from
+ * sbase + voff into LDS at lds + 16 * lane (lds wave-uniform).  Issued from
+ * inline assembly, so the compiler's own waits do not count it: callers
+ * wait with wait_vm. */
+__device__ static inline void dma_dwordx4(const void *sbase, u32 voff, u32 lds)
+{
+	/* the base is wave-uniform by contract: pinned to SGPRs (the builtin
+	 * returns int: each half goes through u32, so none is sign-extended) */
+	const uint64_t b = (uint64_t)(uintptr_t)sbase;
+	const uint64_t bs = (uint64_t)(u32)__builtin_amdgcn_readfirstlane((int)(u32)b) |
+			    ((uint64_t)(u32)__builtin_amdgcn_readfirstlane((int)(u32)(b >> 32)) << 32);
+	asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+		     :
+		     : "v"(voff), "s"((const void *)(uintptr_t)bs),
+		       "s"(__builtin_amdgcn_readfirstlane(lds))
+		     : "memory", "m0");
+}
+
+/* wait until at most N of this wave's vector memory operations are pending
+ * (loads return in order, so the older ones are then complete) */
+template <int N>
+__device__ static inline void wait_vm()
+{
+	static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+	__builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+/* the LDS address of a shared-memory pointer */
+__device__ static inline u32 lds_addr(const void *p)
+{
+	return (u32)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
+}
+
 /* 16 bytes read from a 4-byte aligned address (one global_load_dwordx4). */
 struct __attribute__((packed, aligned(4))) dw4 {
 	u32 v[4];

@@ -50,20 +50,6 @@
 #define RT_KC 256
 #define RT_RS (RT_KC * 4 + 32)
 
-__device__ static inline void rt_dma16(const void *sbase, u32 voff, u32 lds)
-{
-	asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-		     :
-		     : "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds))
-		     : "memory", "m0");
-}
-
-template <int N>
-__device__ static inline void rt_wait_vm()
-{
-	static_assert(N >= 0 && N < 64, "vmcnt is six bits");
-	__builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-}
 
 template <int JT, int CH, int NW> struct rt_geo {
 	static constexpr int LPL = 8 / CH;                /* lanes per logit */
@@ -103,7 +89,7 @@ __global__ __launch_bounds__(NW * WAVE) void k_router(const float *__restrict__ 
 		const float *blk = wr + (size_t)j0 * E;
 		for (int q = wave; q * WAVE < nlines / nsl; q += NW) {
 			const int line = sl + nsl * min(q * WAVE + lane, nlines / nsl - 1);
-			rt_dma16(blk, (u32)line * 128u, l0 + (u32)(NST * RG::SSZ));
+			dma_dwordx4(blk, (u32)line * 128u, l0 + (u32)(NST * RG::SSZ));
 		}
 	}
 
@@ -122,7 +108,7 @@ __global__ __launch_bounds__(NW * WAVE) void k_router(const float *__restrict__ 
 		const u32 st = l0 + (u32)((s % NST) * RG::SSZ);
 #pragma unroll
 		for (int q = 0; q < RG::PER; q++)
-			rt_dma16((isw[q] ? wr : x) + (size_t)s * RT_KC, roff[q],
+			dma_dwordx4((isw[q] ? wr : x) + (size_t)s * RT_KC, roff[q],
 				 st + (u32)((wave + NW * q) * RT_RS));
 	};
 
@@ -136,9 +122,9 @@ __global__ __launch_bounds__(NW * WAVE) void k_router(const float *__restrict__ 
 			issue(s);
 	for (int s = 0; s < ns; s++) {
 		if (s + NST - 2 < ns)
-			rt_wait_vm<(NST - 2) * RG::PER>();
+			wait_vm<(NST - 2) * RG::PER>();
 		else
-			rt_wait_vm<0>();
+			wait_vm<0>();
 		__syncthreads(); /* stage s landed for every wave; stage s-1 is free */
 		if (s + NST - 1 < ns)
 			issue(s + NST - 1);

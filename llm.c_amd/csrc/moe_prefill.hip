@@ -311,28 +311,6 @@ template <int WT> struct pf_geo {
 	static constexpr int LOADS = JB + 1;             /* loads per wave per stage */
 };
 
-/* one LDS-DMA load per lane: 16 bytes from sbase + voff into LDS at
- * lds + 16 * lane (lds wave-uniform) */
-__device__ static inline void dma_dwordx4(const void *sbase, u32 voff, u32 lds)
-{
-	asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-		     :
-		     : "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds))
-		     : "memory", "m0");
-}
-
-/* wait until at most N of this wave's vector memory operations are pending */
-template <int N>
-__device__ static inline void wait_vm()
-{
-	static_assert(N >= 0 && N < 64, "vmcnt is six bits");
-	__builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-}
-
-__device__ static inline u32 lds_addr(const void *p)
-{
-	return (u32)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
-}
 
 /* acc[mb][g] += A[mb-th 32 rows] . B_g over one stage, mb < MB.  Every LDS
  * read of the stage is issued first, so the stage waits for LDS once, not
