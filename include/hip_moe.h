@@ -39,8 +39,8 @@ extern "C" {
  * {f16 d; uint8 qs[16]} (quant.h:14-26), rows of cols/32 blocks, row-major. */
 #define HIP_MOE_Q8_0 1
 #define HIP_MOE_Q4_0 2
-#define HIP_MOE_Q4_K 3 /* dense product only (hip_moe_qmat_*) */
-#define HIP_MOE_Q6_K 5 /* dense product only (hip_moe_qmat_*) */
+#define HIP_MOE_Q4_K 3 /* hip_moe_upload_typed and hip_moe_qmat_* */
+#define HIP_MOE_Q6_K 5 /* hip_moe_upload_typed and hip_moe_qmat_* */
 
 typedef struct hip_moe_layer hip_moe_layer;
 
@@ -73,6 +73,25 @@ hip_moe_layer *hip_moe_upload(const float *gate_inp,
                               const void *const *down_e,
                               int wtype, size_t E, size_t EI, size_t NE,
                               size_t topk, int renorm);
+
+/*
+ * The same with the gate/up and down block types given apart, as the
+ * reference's tensors carry them (hl->gate_exps->type, hl->down_exps->type):
+ * a Q4_K_M GGUF keeps gate/up in Q4_K and down in Q6_K or Q4_K.  Q8_0/Q4_0
+ * need gate_type == down_type (then this is hip_moe_upload).  K-quant
+ * experts (gate/up and down each HIP_MOE_Q4_K or HIP_MOE_Q6_K; E a multiple
+ * of 256 up to 8192, EI up to 16384) stay as the tensors' rows and take one
+ * path for every T: routing, then per (token, slot) the Q8_K integer
+ * gate/up dots of the reference's -DQ8_DOT build, SwiGLU, and the fp32 down
+ * dot in the reference's own order (fused_ffn_silu, nn.c:449-539), then the
+ * combine; outputs, ids and weights equal the reference's bit for bit.
+ */
+hip_moe_layer *hip_moe_upload_typed(const float *gate_inp,
+                                    const void *const *gate_e,
+                                    const void *const *up_e,
+                                    const void *const *down_e,
+                                    int gate_type, int down_type, size_t E, size_t EI,
+                                    size_t NE, size_t topk, int renorm);
 
 /*
  * out[T][E] = moe_ffn(x[T][E]), synchronous, host fp32 buffers (the contract

@@ -20,7 +20,9 @@
 #include <string.h>
 
 struct hip_moe_layer {
-	int wtype;
+	int wtype;          /* the gate/up block type */
+	int dtype;          /* the down block type */
+	int kq;             /* K-quant experts: the kq_moe.hip path */
 	size_t E, EI, NE, topk;
 	int renorm;
 	int device;
@@ -226,12 +228,26 @@ hip_moe_layer *hip_moe_upload(const float *gate_inp, const void *const *gate_e,
 			      int wtype, size_t E, size_t EI, size_t NE, size_t topk,
 			      int renorm)
 {
+	return hip_moe_upload_typed(gate_inp, gate_e, up_e, down_e, wtype, wtype, E, EI, NE,
+				    topk, renorm);
+}
+
+hip_moe_layer *hip_moe_upload_typed(const float *gate_inp, const void *const *gate_e,
+				    const void *const *up_e, const void *const *down_e,
+				    int gate_type, int down_type, size_t E, size_t EI, size_t NE,
+				    size_t topk, int renorm)
+{
 	hip_moe_layer *L = NULL;
 	uint8_t *stage = NULL;
 	int ndev = 0;
+	const int wtype = gate_type;
+	const int kq = is_kquant(gate_type) && is_kquant(down_type);
 
-	if (wtype != HIP_MOE_Q8_0 && wtype != HIP_MOE_Q4_0) {
-		set_err("upload: unsupported weight type %d (Q8_0=1, Q4_0=2)", wtype);
+	if (!kq && (gate_type != down_type ||
+		    (gate_type != HIP_MOE_Q8_0 && gate_type != HIP_MOE_Q4_0))) {
+		set_err("upload: unsupported weight types %d/%d (Q8_0=1 or Q4_0=2 for all three "
+			"matrices; Q4_K=3 / Q6_K=5 for gate/up and down in any mix)", gate_type,
+			down_type);
 		return NULL;
 	}
 	if (!gate_inp || !gate_e || !up_e || !down_e) {
@@ -243,8 +259,13 @@ hip_moe_layer *hip_moe_upload(const float *gate_inp, const void *const *gate_e,
 		return NULL;
 	}
 	/* gate/up rows are covered by one wave without K-split: E/64 lanes */
-	if (!is_pow2(E / MOE_SEG_COLS) || E / MOE_SEG_COLS > 64) {
+	if (!kq && (!is_pow2(E / MOE_SEG_COLS) || E / MOE_SEG_COLS > 64)) {
 		set_err("upload: E=%zu not supported (needs E/64 a power of two <= 64)", E);
+		return NULL;
+	}
+	if (kq && !moe_kq_layer_supported(gate_type, down_type, E, EI)) {
+		set_err("upload: E=%zu EI=%zu not supported for K-quant experts (E <= 8192, "
+			"EI <= 16384)", E, EI);
 		return NULL;
 	}
 	if (NE == 0 || NE > MOE_MAX_NE || topk == 0 || topk > NE || topk > MOE_MAX_TOPK) {
@@ -263,23 +284,26 @@ hip_moe_layer *hip_moe_upload(const float *gate_inp, const void *const *gate_e,
 		return NULL;
 	}
 	L->wtype = wtype;
+	L->dtype = down_type;
+	L->kq = kq;
 	L->E = E;
 	L->EI = EI;
 	L->NE = NE;
 	L->topk = topk;
 	L->renorm = renorm ? 1 : 0;
 	L->rb_in = row_bytes(wtype, E);
-	L->rb_mid = row_bytes(wtype, EI);
+	L->rb_mid = row_bytes(down_type, EI);
 	L->gu_stride = EI * L->rb_in;
 	L->down_stride = E * L->rb_mid;
 	/* the grouped GEMMs read gate/up from a second copy in MOE_GU_GROUP-row
 	 * groups (a K-step is one contiguous run per group); the decode and GEMV
-	 * kernels read whole rows from the first */
-	const int grouped = moe_prefill_supported(wtype, E, EI, NE);
+	 * kernels read whole rows from the first.  K-quant experts stay as
+	 * they are (rows of super-blocks), for the kq_moe.hip kernels only. */
+	const int grouped = !kq && moe_prefill_supported(wtype, E, EI, NE);
 	const size_t wbytes = NE * (2 * L->gu_stride + L->down_stride) +
 			      (grouped ? 2 * NE * L->gu_stride : 0);
 	L->weight_bytes = NE * E * sizeof(float) + wbytes;
-	L->fused_grid = moe_fused_grid(wtype, E, EI, NE);
+	L->fused_grid = kq ? 0 : moe_fused_grid(wtype, E, EI, NE);
 
 	HIPCHK(hipGetDevice(&L->device), "hipGetDevice");
 	L->stream = device_stream(L->device);
@@ -315,7 +339,10 @@ hip_moe_layer *hip_moe_upload(const float *gate_inp, const void *const *gate_e,
 				 hipMemcpyHostToDevice), "upload gate");
 		HIPCHK(hipMemcpy(L->d_up + e * L->gu_stride, up_e[e], L->gu_stride,
 				 hipMemcpyHostToDevice), "upload up");
-		if (!upload_down(L, e, (const uint8_t *)down_e[e], stage))
+		if (kq)
+			HIPCHK(hipMemcpy(L->d_down + e * L->down_stride, down_e[e], L->down_stride,
+					 hipMemcpyHostToDevice), "upload down");
+		else if (!upload_down(L, e, (const uint8_t *)down_e[e], stage))
 			goto fail;
 		if (grouped &&
 		    (!upload_gu(L, L->d_gate_g + e * L->gu_stride, (const uint8_t *)gate_e[e], stage) ||
@@ -408,7 +435,7 @@ static int ensure_scratch(hip_moe_layer *L, size_t T, hipStream_t s)
 	/* the clears run on the null stream, which the layer's non-blocking
 	 * stream does not wait for */
 	HIPCHK(hipDeviceSynchronize(), "synchronize after clearing scratch");
-	if (moe_prefill_supported(L->wtype, L->E, L->EI, L->NE)) {
+	if (!L->kq && moe_prefill_supported(L->wtype, L->E, L->EI, L->NE)) {
 		size_t rows = moe_prefill_max_rows(P, L->NE);
 		HIPCHK(hipMalloc((void **)&L->d_rows, rows * sizeof(int)), "hipMalloc(rows)");
 		HIPCHK(hipMalloc((void **)&L->d_tile_e,
@@ -609,6 +636,11 @@ int hip_moe_route_dev(hip_moe_layer *L, const float *d_x, size_t T,
 /* the path a call of T tokens takes (HIP_MOE_PATH_*), 0 if none applies */
 static int choose_path(const hip_moe_layer *L, size_t T)
 {
+	/* K-quant experts: the per-pair products of kq_moe.hip for every T */
+	if (L->kq)
+		return L->path == HIP_MOE_PATH_AUTO || L->path == HIP_MOE_PATH_GEMV
+			       ? HIP_MOE_PATH_GEMV
+			       : 0;
 	int dec = L->fused_grid > 0 &&
 		  moe_fused_supported(L->wtype, L->E, L->EI, L->NE, T, L->topk);
 	int grp = moe_prefill_supported(L->wtype, L->E, L->EI, L->NE) &&
@@ -694,6 +726,17 @@ int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 					split, s), "combine");
 		return 1;
 	}
+	if (L->kq) {
+		LCHK(moe_launch_kq_gateup(L->wtype, L->d_gate, L->d_up, L->gu_stride, ids, d_x,
+					  L->d_h, P, (int)L->topk, (int)L->E, (int)L->EI, s),
+		     "K-quant gate/up");
+		LCHK(moe_launch_kq_down(L->dtype, L->d_down, L->down_stride, ids, L->d_h,
+					L->d_ypart, P, (int)L->E, (int)L->EI, s),
+		     "K-quant down");
+		LCHK(moe_launch_combine(L->d_ypart, w, d_out, (int)T, (int)L->topk, (int)L->E, 1, s),
+		     "combine");
+		return 1;
+	}
 	LCHK(moe_launch_gateup(L->wtype, L->d_gate, L->d_up, L->gu_stride, ids, -1, d_x,
 			       L->d_h, P, (int)L->topk, (int)L->E, (int)L->EI, s),
 	     "gate/up");
@@ -720,6 +763,23 @@ int hip_moe_expert_ffn_dev(hip_moe_layer *L, size_t expert, const float *d_x,
 	hipStream_t s = pick_stream(L, stream);
 	if (!ensure_scratch(L, 1, s))
 		return 0;
+	if (L->kq) {
+		/* the kernels take the expert from an id list: one entry */
+		const uint32_t id = (uint32_t)expert;
+		/* ordered after the stream's earlier users of d_ids; the source
+		 * lives on this stack frame, so the copy completes here */
+		HIPCHK(hipMemcpyAsync(L->d_ids, &id, sizeof(id), hipMemcpyHostToDevice, s),
+		       "copy expert id");
+		HIPCHK(hipStreamSynchronize(s), "synchronize");
+		LCHK(moe_launch_kq_gateup(L->wtype, L->d_gate, L->d_up, L->gu_stride, L->d_ids,
+					  d_x, L->d_h, 1, 1, (int)L->E, (int)L->EI, s),
+		     "K-quant gate/up");
+		LCHK(moe_launch_kq_down(L->dtype, L->d_down, L->down_stride, L->d_ids, L->d_h,
+					L->d_ypart, 1, (int)L->E, (int)L->EI, s),
+		     "K-quant down");
+		LCHK(moe_launch_combine(L->d_ypart, NULL, d_out, 1, 1, (int)L->E, 1, s), "combine");
+		return 1;
+	}
 	LCHK(moe_launch_gateup(L->wtype, L->d_gate, L->d_up, L->gu_stride, NULL, (int)expert,
 			       d_x, L->d_h, 1, 1, (int)L->E, (int)L->EI, s), "gate/up");
 	int kch = 1;
@@ -728,6 +788,8 @@ int hip_moe_expert_ffn_dev(hip_moe_layer *L, size_t expert, const float *d_x,
 	     "down");
 	LCHK(moe_launch_combine(L->d_ypart, NULL, d_out, 1, 1, (int)L->E, kch, s), "combine");
 	return 1;
+fail:
+	return 0;
 }
 
 static int ensure_io(hip_moe_layer *L, size_t T)

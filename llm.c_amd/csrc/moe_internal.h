@@ -76,6 +76,16 @@ int moe_kq_supported(int wtype, int K);
 int moe_kq_grid(int wtype, int K, int T);
 int moe_launch_kq_gemv(int wtype, const uint8_t *W, int N, int K, const float *x, int T,
                        const float *add, int add_rows, float *out, int nwg, void *stream);
+/* The expert products of a MoE layer with K-quant experts (kq_moe.hip):
+ * gate/up type gt, down type dt (3 = Q4_K, 5 = Q6_K), bit for bit the
+ * reference's fused_ffn_silu; y [P][E] goes to moe_launch_combine with one
+ * chunk. */
+int moe_kq_layer_supported(int gt, int dt, size_t E, size_t EI);
+int moe_launch_kq_gateup(int gt, const uint8_t *gate, const uint8_t *up, size_t gu_stride,
+                         const uint32_t *ids, const float *x, float *h, int P, int K, int E,
+                         int EI, void *stream);
+int moe_launch_kq_down(int dt, const uint8_t *down, size_t dn_stride, const uint32_t *ids,
+                       const float *h, float *y, int P, int E, int EI, void *stream);
 /* quantize_row_q8 of T rows of K values: d[T][K/256], qs[T][K], bsums[T][K/256][16] */
 int moe_launch_q8k_quantize(const float *x, int T, int K, float *d, int8_t *qs,
                             int16_t *bsums, void *stream);

@@ -50,6 +50,8 @@ def lib():
     vp, sz, i32, f32p, u32p = C.c_void_p, C.c_size_t, C.c_int, C.c_void_p, C.c_void_p
     L.hip_moe_upload.restype = vp
     L.hip_moe_upload.argtypes = [vp, vp, vp, vp, i32, sz, sz, sz, sz, i32]
+    L.hip_moe_upload_typed.restype = vp
+    L.hip_moe_upload_typed.argtypes = [vp, vp, vp, vp, i32, i32, sz, sz, sz, sz, i32]
     L.hip_moe_ffn.restype = i32
     L.hip_moe_ffn.argtypes = [vp, f32p, f32p, sz, f32p, u32p, f32p]
     L.hip_moe_ffn_dev.restype = i32
@@ -153,29 +155,39 @@ def synth_quant_matrix(seed, stream, std, wtype, rows, cols) -> np.ndarray:
     return out
 
 
+def wtypes(wtype: int):
+    """(gate/up type, down type) of a layer's wtype: the gate/up type,
+    or'ed with the down type << 8 where that differs (a Q4_K_M file's
+    Q4_K gate/up with Q6_K down: Q4_K | Q6_K << 8)."""
+    gt = wtype & 0xff
+    return gt, (wtype >> 8) or gt
+
+
 def synth_layer(seed: int, layer: int, wtype: int, E: int, EI: int, NE: int,
                 std: float = 0.02, bias_std: float | None = None) -> dict:
     """One MoE layer of the given shape: router fp32 N(0, std) [NE][E],
     optional router bias N(0, bias_std) [NE], stacked expert tensors
     gate/up [NE][EI][E/32 blocks] and down [NE][E][EI/32 blocks] as uint8
-    arrays of shape [NE, bytes_per_expert] (GGUF *_exps layout)."""
+    arrays of shape [NE, bytes_per_expert] (GGUF *_exps layout).  wtype may
+    carry a down type (wtypes)."""
     L = lib()
     router = synth_normal(seed, L.moe_stream_router(layer), NE * E, 0.0, std).reshape(NE, E)
     bias = None
     if bias_std is not None:
         bias = synth_normal(seed, L.moe_stream_bias(layer), NE, 0.0, bias_std)
-    gu = EI * row_bytes(wtype, E)
-    dn = E * row_bytes(wtype, EI)
+    gt, dt = wtypes(wtype)
+    gu = EI * row_bytes(gt, E)
+    dn = E * row_bytes(dt, EI)
     gate = np.empty((NE, gu), np.uint8)
     up = np.empty((NE, gu), np.uint8)
     down = np.empty((NE, dn), np.uint8)
     nt = _threads()
     for e in range(NE):
-        L.moe_synth_quant_matrix(seed, L.moe_stream_gate(layer, e), std, wtype, EI, E,
+        L.moe_synth_quant_matrix(seed, L.moe_stream_gate(layer, e), std, gt, EI, E,
                                  _ptr(gate[e]), nt)
-        L.moe_synth_quant_matrix(seed, L.moe_stream_up(layer, e), std, wtype, EI, E,
+        L.moe_synth_quant_matrix(seed, L.moe_stream_up(layer, e), std, gt, EI, E,
                                  _ptr(up[e]), nt)
-        L.moe_synth_quant_matrix(seed, L.moe_stream_down(layer, e), std, wtype, E, EI,
+        L.moe_synth_quant_matrix(seed, L.moe_stream_down(layer, e), std, dt, E, EI,
                                  _ptr(down[e]), nt)
     return dict(router=router, bias=bias, gate=gate, up=up, down=down, wtype=wtype,
                 E=E, EI=EI, NE=NE)
@@ -337,8 +349,13 @@ class MoeLayer:
         self.E, self.EI, self.NE, self.topk = E, EI, NE, topk
         self.wtype, self.renorm = wtype, renorm
         gp, upp, dp = expert_ptrs(gate), expert_ptrs(up), expert_ptrs(down)
-        self.h = L.hip_moe_upload(_ptr(self.router), gp, upp, dp, wtype, E, EI, NE, topk,
-                                  int(renorm))
+        gt, dt = wtypes(wtype)
+        if gt == dt:
+            self.h = L.hip_moe_upload(_ptr(self.router), gp, upp, dp, wtype, E, EI, NE, topk,
+                                      int(renorm))
+        else:
+            self.h = L.hip_moe_upload_typed(_ptr(self.router), gp, upp, dp, gt, dt, E, EI, NE,
+                                            topk, int(renorm))
         if not self.h:
             raise HipMoeError("hip_moe_upload: " + last_error())
 

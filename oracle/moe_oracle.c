@@ -349,43 +349,78 @@ void orc_dequant_row(const void *qrow, int wtype, float *dst, size_t n)
 struct ffn_job {
 	const float *x;
 	const uint8_t *g8, *u8, *d8;
-	int wtype;
+	int gt, dt; /* gate/up and down block types */
 	size_t E, EI;
 	float *h, *out;
+	const float *q8d; /* K-quant gate/up: x in Q8_K */
+	const int8_t *q8s;
+	const int16_t *q8b;
 };
 
-/* nn.c:455-478: thread tidx's chunk of gate/up rows, then SwiGLU in place */
+static int is_kq(int t)
+{
+	return t == ORC_Q4_K || t == ORC_Q6_K;
+}
+
+/* nn.c:455-478: thread tidx's chunk of gate/up rows, then SwiGLU in place;
+ * dot_q8_quant takes the integer dots for K-quant rows, the fp32 ones
+ * otherwise (quant.c:656-668) */
 static void ffn_gateup_task(void *arg, int tidx, int nt)
 {
 	const struct ffn_job *w = arg;
-	const size_t rb_in = row_bytes(w->wtype, w->E), chunk = (w->EI + nt - 1) / nt;
+	const size_t rb_in = row_bytes(w->gt, w->E), chunk = (w->EI + nt - 1) / nt;
 	const size_t j0 = tidx * chunk, j1 = j0 + chunk < w->EI ? j0 + chunk : w->EI;
 	for (size_t j = j0; j < j1; j++) {
-		float g = orc_dot_quant(w->x, w->g8 + j * rb_in, w->wtype, w->E);
-		float u = orc_dot_quant(w->x, w->u8 + j * rb_in, w->wtype, w->E);
+		float g, u;
+		if (w->q8d) {
+			g = orc_dot_q8k(w->q8d, w->q8s, w->q8b, w->g8 + j * rb_in, w->gt, w->E);
+			u = orc_dot_q8k(w->q8d, w->q8s, w->q8b, w->u8 + j * rb_in, w->gt, w->E);
+		} else {
+			g = orc_dot_quant(w->x, w->g8 + j * rb_in, w->gt, w->E);
+			u = orc_dot_quant(w->x, w->u8 + j * rb_in, w->gt, w->E);
+		}
 		w->h[j] = (g / (1.0f + expf(-g))) * u;
 	}
 }
 
-/* nn.c:483-492: after the barrier, thread tidx's chunk of down rows */
+/* nn.c:483-492: after the barrier, thread tidx's chunk of down rows (fp32
+ * dots: h is not quantized) */
 static void ffn_down_task(void *arg, int tidx, int nt)
 {
 	const struct ffn_job *w = arg;
-	const size_t rb_mid = row_bytes(w->wtype, w->EI), chunk = (w->E + nt - 1) / nt;
+	const size_t rb_mid = row_bytes(w->dt, w->EI), chunk = (w->E + nt - 1) / nt;
 	const size_t i0 = tidx * chunk, i1 = i0 + chunk < w->E ? i0 + chunk : w->E;
 	for (size_t i = i0; i < i1; i++)
-		w->out[i] = orc_dot_quant(w->h, w->d8 + i * rb_mid, w->wtype, w->EI);
+		w->out[i] = orc_dot_quant(w->h, w->d8 + i * rb_mid, w->dt, w->EI);
 }
 
 void orc_fused_ffn(const float *x, const void *gate, const void *up,
 		   const void *down, int wtype, size_t E, size_t EI,
 		   float *h, float *out)
 {
-	struct ffn_job w = {x, gate, up, down, wtype, E, EI, h, out};
+	const int gt = wtype & 0xff, dt = (wtype >> 8) ? (wtype >> 8) : gt;
+	struct ffn_job w = {x, gate, up, down, gt, dt, E, EI, h, out, NULL, NULL, NULL};
+	/* the -DQ8_DOT build quantizes the token to Q8_K when E % 256 == 0
+	 * (nn.c:527-531) */
+	float *q8d = NULL;
+	int8_t *q8s = NULL;
+	int16_t *q8b = NULL;
+	if (is_kq(gt) && E % QKK == 0) {
+		q8d = malloc(E / QKK * sizeof(float));
+		q8s = malloc(E);
+		q8b = malloc(E / QKK * 16 * sizeof(int16_t));
+		orc_quantize_q8k(x, E, q8d, q8s, q8b);
+		w.q8d = q8d;
+		w.q8s = q8s;
+		w.q8b = q8b;
+	}
 	/* fused_ffn_silu's thread_pool_run(.., 1, k, inter) (nn.c:534) */
 	const int nt = orc_pool_threads(1, E, EI);
 	orc_pool_run(ffn_gateup_task, &w, nt);
 	orc_pool_run(ffn_down_task, &w, nt);
+	free(q8d);
+	free(q8s);
+	free(q8b);
 }
 
 struct moe_job {

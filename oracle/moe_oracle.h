@@ -68,7 +68,10 @@ float orc_dot_q8k(const float *yd, const int8_t *q8, const int16_t *bsums, const
                   int wtype, size_t n);
 
 /* One expert, one token: out[E] = down . (silu(gate . x) * (up . x))
- * (nn.c:449-493 fused_ffn_fn).  h is a caller scratch of EI floats. */
+ * (nn.c:449-493 fused_ffn_fn).  h is a caller scratch of EI floats.
+ * wtype: the gate/up block type, or'ed with the down type << 8 where that
+ * differs (a Q4_K_M file's Q4_K gate/up with Q6_K down: 3 | 5 << 8); the
+ * same encoding runs through orc_moe_ffn and the model oracles. */
 void orc_fused_ffn(const float *x, const void *gate, const void *up,
                    const void *down, int wtype, size_t E, size_t EI,
                    float *h, float *out);

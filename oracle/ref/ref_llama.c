@@ -25,12 +25,14 @@ void ref_llama_moe_ffn(const float *x, float *out, size_t T, const float *wr,
 	hl.gate_exp = calloc(NE, sizeof(tensor_t *));
 	hl.up_exp = calloc(NE, sizeof(tensor_t *));
 	hl.down_exp = calloc(NE, sizeof(tensor_t *));
+	/* wtype: gate/up type, or'ed with the down type << 8 where it differs */
+	const int gt = wtype & 0xff, dt = (wtype >> 8) ? (wtype >> 8) : gt;
 	for (size_t e = 0; e < NE; e++) {
-		tensor_t *g = tensor_new_mapped((void *)gate_e[e], EI * E, wtype);
+		tensor_t *g = tensor_new_mapped((void *)gate_e[e], EI * E, gt);
 		tensor_reshape_2d(g, EI, E);
-		tensor_t *u = tensor_new_mapped((void *)up_e[e], EI * E, wtype);
+		tensor_t *u = tensor_new_mapped((void *)up_e[e], EI * E, gt);
 		tensor_reshape_2d(u, EI, E);
-		tensor_t *d = tensor_new_mapped((void *)down_e[e], E * EI, wtype);
+		tensor_t *d = tensor_new_mapped((void *)down_e[e], E * EI, dt);
 		tensor_reshape_2d(d, E, EI);
 		hl.gate_exp[e] = g;
 		hl.up_exp[e] = u;

@@ -21,11 +21,13 @@ void ref_olmoe_moe_ffn(const float *x, float *out, size_t T, const float *wr,
 
 	tensor_t *gi = tensor_new_mapped((void *)wr, NE * E, TENSOR_F32);
 	tensor_reshape_2d(gi, NE, E);
-	tensor_t *g = tensor_new_mapped((void *)gate_exps, NE * EI * E, wtype);
+	/* wtype: gate/up type, or'ed with the down type << 8 where it differs */
+	const int gt = wtype & 0xff, dt = (wtype >> 8) ? (wtype >> 8) : gt;
+	tensor_t *g = tensor_new_mapped((void *)gate_exps, NE * EI * E, gt);
 	tensor_reshape_3d(g, NE, EI, E);
-	tensor_t *u = tensor_new_mapped((void *)up_exps, NE * EI * E, wtype);
+	tensor_t *u = tensor_new_mapped((void *)up_exps, NE * EI * E, gt);
 	tensor_reshape_3d(u, NE, EI, E);
-	tensor_t *d = tensor_new_mapped((void *)down_exps, NE * E * EI, wtype);
+	tensor_t *d = tensor_new_mapped((void *)down_exps, NE * E * EI, dt);
 	tensor_reshape_3d(d, NE, E, EI);
 	hl.gate_inp = gi;
 	hl.gate_exps = g;

@@ -21,6 +21,11 @@
 #include <stdlib.h>
 #include <string.h>
 
+/* expert block types: wtype holds the gate/up type, or'ed with the down
+ * type << 8 where that differs */
+#define WT_GU(w) ((w) & 0xff)
+#define WT_DN(w) (((w) >> 8) ? ((w) >> 8) : ((w) & 0xff))
+
 static tensor_t *map2(const void *p, size_t d0, size_t d1, int type)
 {
 	tensor_t *t = tensor_new_mapped((void *)p, d0 * d1, type);
@@ -95,9 +100,9 @@ void ref_moe_ffn_composed(const float *x, float *out, size_t T, const float *wr,
 		tensor_reshape_2d(&tok_in, 1, E);
 		for (size_t e = 0; e < topk; e++) {
 			uint32_t id = ids[t * topk + e];
-			tensor_t *gw = map2(gate_e[id], EI, E, wtype);
-			tensor_t *uw = map2(up_e[id], EI, E, wtype);
-			tensor_t *dw = map2(down_e[id], E, EI, wtype);
+			tensor_t *gw = map2(gate_e[id], EI, E, WT_GU(wtype));
+			tensor_t *uw = map2(up_e[id], EI, E, WT_GU(wtype));
+			tensor_t *dw = map2(down_e[id], E, EI, WT_DN(wtype));
 			int ok = fused_ffn_silu(&tok_in, eo, eg, gw, eu, uw, dw);
 			if (!ok)
 				abort();
@@ -128,9 +133,9 @@ void ref_fused_ffn(const float *x, const void *gate, const void *up, const void 
 	tensor_t *eg = tensor_new_zero(2, (size_t)1, (size_t)EI);
 	tensor_t *eu = tensor_new_zero(2, (size_t)1, (size_t)EI);
 	tensor_t *eo = tensor_new_zero(2, (size_t)1, (size_t)E);
-	tensor_t *gw = map2(gate, EI, E, wtype);
-	tensor_t *uw = map2(up, EI, E, wtype);
-	tensor_t *dw = map2(down, E, EI, wtype);
+	tensor_t *gw = map2(gate, EI, E, WT_GU(wtype));
+	tensor_t *uw = map2(up, EI, E, WT_GU(wtype));
+	tensor_t *dw = map2(down, E, EI, WT_DN(wtype));
 	if (!fused_ffn_silu(in, eo, eg, gw, eu, uw, dw))
 		abort();
 	memcpy(out, eo->data, E * sizeof(float));

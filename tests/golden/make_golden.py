@@ -30,6 +30,10 @@ same bytes.  Outputs are the reference's own results:
                      Q4_K/Q6_K rows (the fill patterns of test/quant_dot.c:
                      12-34 and seeded rows); tensor_mma_transposed_2x2 with
                      a Q4_K/Q6_K right operand (matmul.c:285-312)
+  kquant_moe.npz     the reference's moe_ffn (olmoe.c:343-407, llama.c:393-457)
+                     on Q4_K/Q6_K experts (gate/up Q4_K with down Q6_K, as a
+                     Q4_K_M file mixes them, and all Q6_K), and one expert's
+                     fused_ffn_silu (nn.c:496-539) for both mixes
   model_<case>.npz   the whole OLMoE model (olmoe.c:409-580): greedy tokens
                      and per-step logits of the reference's olmoe_decode run
                      over the prompt then n_gen steps, and of its generate
@@ -252,6 +256,51 @@ def kquant_goldens(R):
     np.savez(os.path.join(HERE, "kquant.npz"), seed=SEED, **fx)
 
 
+# K-quant MoE layers (the gate/up type | the down type << 8, as a Q4_K_M
+# file mixes them): name: (wtype, E, EI, NE, topk, renorm, T)
+KQ_LAYERS = {
+    "olmoe_q4k_q6k": (hipmoe.Q4_K | hipmoe.Q6_K << 8, 2048, 1024, 64, 8, 0, 4),
+    "olmoe_q6k": (hipmoe.Q6_K, 2048, 1024, 64, 8, 0, 2),
+    "mixtral_q4k_q6k": (hipmoe.Q4_K | hipmoe.Q6_K << 8, 4096, 14336, 8, 2, 1, 2),
+}
+
+
+def kq_layer_goldens(R):
+    """The reference's own static moe_ffn (olmoe.c:343-407 / llama.c:393-457)
+    on K-quant expert tensors, and one expert's fused_ffn_silu for both
+    mixes."""
+    fx = {}
+    for name, (wt, E, EI, NE, K, renorm, T) in KQ_LAYERS.items():
+        lw = hipmoe.synth_layer(SEED, 0, wt, E, EI, NE, 0.02, None)
+        x = hipmoe.synth_input(SEED, 0, T, E)
+        gp, up_, dp = (hipmoe.expert_ptrs(lw[k]) for k in ("gate", "up", "down"))
+        out = np.empty((T, E), np.float32)
+        if renorm:
+            R.ref_llama_moe_ffn(p(x), p(out), T, p(lw["router"]), gp, up_, dp, wt, E, EI, NE, K)
+        else:
+            R.ref_olmoe_moe_ffn(p(x), p(out), T, p(lw["router"]), p(lw["gate"]), p(lw["up"]),
+                                p(lw["down"]), wt, E, EI, NE, K)
+        fx[f"{name}_sha_gate"] = sha(lw["gate"])
+        fx[f"{name}_sha_down"] = sha(lw["down"])
+        fx[f"{name}_sha_x"] = sha(x)
+        fx[f"{name}_out"] = out
+        print(f"kq layer {name}: T={T} |out|={np.linalg.norm(out):.4f}")
+        del lw
+    for name, wt in (("q4k_q6k", hipmoe.Q4_K | hipmoe.Q6_K << 8),
+                     ("q6k_q4k", hipmoe.Q6_K | hipmoe.Q4_K << 8)):
+        E, EI = 2048, 1024
+        gt, dt = hipmoe.wtypes(wt)
+        g = hipmoe.synth_quant_matrix(SEED, 0x9011, 0.02, gt, EI, E)
+        u = hipmoe.synth_quant_matrix(SEED, 0x9012, 0.02, gt, EI, E)
+        d = hipmoe.synth_quant_matrix(SEED, 0x9013, 0.02, dt, E, EI)
+        x = hipmoe.synth_normal(SEED, 0x9014, E)
+        out = np.empty(E, np.float32)
+        R.ref_fused_ffn(p(x), p(g), p(u), p(d), wt, E, EI, p(out))
+        fx[f"ffn_{name}_sha"] = sha(np.concatenate([g, u, d, x.view(np.uint8)]))
+        fx[f"ffn_{name}_out"] = out
+    np.savez(os.path.join(HERE, "kquant_moe.npz"), seed=SEED, **fx)
+
+
 def qmat_goldens(R):
     fx = {}
     for i, (name, (wt, T, N, K, add)) in enumerate(QMAT_CASES.items()):
@@ -366,11 +415,13 @@ def main():
         return
     if sys.argv[1:] == ["kquant"]:
         kquant_goldens(R)
+        kq_layer_goldens(R)
         return
     qmat_goldens(R)
     if sys.argv[1:] == ["qmat"]:
         return
     kquant_goldens(R)
+    kq_layer_goldens(R)
 
     # ---- quantizers -----------------------------------------------------
     blocks = quant_blocks()

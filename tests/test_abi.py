@@ -44,8 +44,9 @@ def _upload(router, gate, up, down, wtype, E, EI, NE, topk, renorm=0):
 
 
 @pytest.mark.parametrize("wtype,E,EI,NE,topk,msg", [
-    (3, 256, 256, 4, 2, "unsupported weight type"),
+    (4, 256, 256, 4, 2, "unsupported weight type"),
     (0, 256, 256, 4, 2, "unsupported weight type"),
+    (3, 16384, 256, 4, 2, "not supported for K-quant experts"),
     (1, 250, 256, 4, 2, "multiples of 256"),
     (1, 256, 300, 4, 2, "multiples of 256"),
     (1, 768, 256, 4, 2, "not supported"),
@@ -55,6 +56,24 @@ def _upload(router, gate, up, down, wtype, E, EI, NE, topk, renorm=0):
 def test_upload_rejects_unsupported(wtype, E, EI, NE, topk, msg):
     router, gate, up, down = _tiny_layer(1 if wtype not in (1, 2) else wtype, 256, 256, 4)
     h = _upload(router, gate, up, down, wtype, E, EI, NE, topk)
+    assert not h
+    assert msg in hipmoe.last_error()
+
+
+@pytest.mark.parametrize("gt,dt,msg", [
+    (1, 3, "unsupported weight types"),   # Q8_0 gate/up with a K-quant down
+    (3, 1, "unsupported weight types"),
+    (1, 2, "unsupported weight types"),   # Q8_0 / Q4_0 take one type
+    (3, 5, "no HIP device"),              # a Q4_K_M mix passes the checks
+])
+def test_upload_typed_checks_the_mix(gt, dt, msg):
+    if msg == "no HIP device" and hipmoe.hip().device_count() > 0:
+        pytest.skip("a GPU is visible: the GPU tests upload this mix")
+    L = hipmoe.lib()
+    router, gate, up, down = _tiny_layer(hipmoe.Q8_0, 256, 256, 4)
+    h = L.hip_moe_upload_typed(router.ctypes.data, hipmoe.expert_ptrs(gate),
+                               hipmoe.expert_ptrs(up), hipmoe.expert_ptrs(down), gt, dt, 256,
+                               256, 4, 2, 0)
     assert not h
     assert msg in hipmoe.last_error()
 

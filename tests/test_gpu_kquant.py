@@ -122,3 +122,67 @@ def test_gpu_kquant_qmat_graph_replays():
             H.free(p)
         W6.free()
         W4.free()
+
+
+# ---- MoE layers on K-quant experts -----------------------------------------
+
+def _kq_layer(name):
+    sys.path.insert(0, __import__("os").path.dirname(__import__("os").path.abspath(__file__)))
+    from test_oracle_kquant import kq_layer
+    return kq_layer(name)
+
+
+@pytest.mark.parametrize("name", ["olmoe_q4k_q6k", "olmoe_q6k", "mixtral_q4k_q6k"])
+def test_gpu_kq_layer_vs_reference_golden(name):
+    """hip_moe_upload_typed / hip_moe_ffn on K-quant experts: outputs equal the
+    compiled reference's moe_ffn bit for bit, ids and weights the oracle's."""
+    (wt, E, EI, NE, K, renorm, T), lw, x, want = _kq_layer(name)
+    say(f"kq layer {name}: wtype={wt:#x} T={T} E={E} EI={EI} NE={NE} K={K}")
+    M = hipmoe.MoeLayer.from_synth(lw, K, bool(renorm))
+    try:
+        assert M.path_for(T) == hipmoe.PATH_GEMV
+        out, ids, w = M.ffn(x)
+    finally:
+        M.free()
+    _, oids, ow, _, _ = oracle.moe_ffn(x, lw, K, bool(renorm), None)
+    assert np.array_equal(ids, oids) and np.array_equal(bits(w), bits(ow))
+    same = np.array_equal(bits(out), bits(want))
+    say(f"kq layer {name}: bitwise {same}, rel L2 {rel_l2(out, want):.3e}")
+    assert same
+
+
+@pytest.mark.parametrize("T", [1, 13, 64])
+def test_gpu_kq_layer_token_counts_vs_oracle(T):
+    (wt, E, EI, NE, K, renorm, _), lw, _, _ = _kq_layer("olmoe_q4k_q6k")
+    x = hipmoe.synth_input(SEED, 4000 + T, T, E)
+    say(f"kq layer olmoe_q4k_q6k at T={T} against the oracle")
+    M = hipmoe.MoeLayer.from_synth(lw, K, bool(renorm))
+    try:
+        out, ids, w = M.ffn(x)
+    finally:
+        M.free()
+    oout, oids, ow, _, _ = oracle.moe_ffn(x, lw, K, bool(renorm), None)
+    assert np.array_equal(ids, oids) and np.array_equal(bits(w), bits(ow))
+    nbad = int(np.sum(bits(out) != bits(oout)))
+    say(f"kq layer T={T}: {nbad} of {out.size} outputs differ")
+    assert nbad == 0
+
+
+@pytest.mark.parametrize("wt", [hipmoe.Q4_K | hipmoe.Q6_K << 8, hipmoe.Q6_K | hipmoe.Q4_K << 8,
+                                hipmoe.Q4_K])
+def test_gpu_kq_expert_ffn_vs_oracle(wt):
+    E, EI, NE = 2048, 1024, 4
+    lw = hipmoe.synth_layer(SEED, 3, wt, E, EI, NE, 0.02, None)
+    x = hipmoe.synth_normal(SEED, 0x9020, E)
+    say(f"kq expert ffn wtype={wt:#x}")
+    M = hipmoe.MoeLayer.from_synth(lw, 2, False)
+    try:
+        for e in (0, 3):
+            got = M.expert_ffn(e, x)
+            want = oracle.fused_ffn(x, lw["gate"][e], lw["up"][e], lw["down"][e], wt, E, EI)
+            assert np.array_equal(bits(got), bits(want)), (e, rel_l2(got, want))
+        with pytest.raises(hipmoe.HipMoeError, match="does not apply"):
+            M.set_path(hipmoe.PATH_DECODE)
+            M.ffn(x.reshape(1, E))
+    finally:
+        M.free()

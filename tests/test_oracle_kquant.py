@@ -191,3 +191,59 @@ def test_synth_kquantizer_roundtrip(wt):
         tol = 0.6 * amax / 7.0 if wt == hipmoe.Q4_K else 1.1 * amax / 32.0
         assert np.max(np.abs(deq - x[r])) <= tol
         assert rel_l2(deq, x[r]) < (0.1 if wt == hipmoe.Q4_K else 0.03)
+
+
+# ---- MoE layers on K-quant experts (tests/golden/kquant_moe.npz) -----------
+
+def kq_layer(name):
+    """(wtype, E, EI, NE, K, renorm, T), the layer and the tokens of K-quant
+    layer case `name`, after checking they are the fixture's bytes."""
+    import importlib.util
+    import os
+    spec = importlib.util.spec_from_file_location(
+        "make_golden", os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                                    "make_golden.py"))
+    mg = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mg)
+    wt, E, EI, NE, K, renorm, T = mg.KQ_LAYERS[name]
+    lw = hipmoe.synth_layer(SEED, 0, wt, E, EI, NE, 0.02, None)
+    x = hipmoe.synth_input(SEED, 0, T, E)
+    g = golden("kquant_moe.npz")
+    assert sha(lw["gate"]) == str(g[f"{name}_sha_gate"])
+    assert sha(lw["down"]) == str(g[f"{name}_sha_down"]) and sha(x) == str(g[f"{name}_sha_x"])
+    return (wt, E, EI, NE, K, renorm, T), lw, x, g[f"{name}_out"]
+
+
+@pytest.mark.parametrize("name", ["olmoe_q4k_q6k", "olmoe_q6k",
+                                  pytest.param("mixtral_q4k_q6k", marks=pytest.mark.slow)])
+def test_oracle_kq_layer_vs_reference(name):
+    """The oracle's moe_ffn on K-quant experts (the Q8_K gate/up dots, the
+    fp32 down dot) equals the reference's own moe_ffn bit for bit."""
+    (wt, E, EI, NE, K, renorm, T), lw, x, want = kq_layer(name)
+    got = oracle.moe_ffn(x, lw, K, bool(renorm), None)[0]
+    assert np.array_equal(bits(got), bits(want)), rel_l2(got, want)
+
+
+@pytest.mark.parametrize("name,wt", [("q4k_q6k", hipmoe.Q4_K | hipmoe.Q6_K << 8),
+                                     ("q6k_q4k", hipmoe.Q6_K | hipmoe.Q4_K << 8)])
+def test_oracle_kq_fused_ffn_vs_reference(name, wt):
+    E, EI = 2048, 1024
+    gt, dt = hipmoe.wtypes(wt)
+    gq = hipmoe.synth_quant_matrix(SEED, 0x9011, 0.02, gt, EI, E)
+    uq = hipmoe.synth_quant_matrix(SEED, 0x9012, 0.02, gt, EI, E)
+    dq = hipmoe.synth_quant_matrix(SEED, 0x9013, 0.02, dt, E, EI)
+    x = hipmoe.synth_normal(SEED, 0x9014, E)
+    g = golden("kquant_moe.npz")
+    assert sha(np.concatenate([gq, uq, dq, x.view(np.uint8)])) == str(g[f"ffn_{name}_sha"])
+    got = oracle.fused_ffn(x, gq, uq, dq, wt, E, EI)
+    assert np.array_equal(bits(got), bits(g[f"ffn_{name}_out"]))
+    # and against the formats' own values in float64 (a dropped min or a
+    # swapped scale moves it far more than the rounding bound)
+    d8, q8, _ = oracle.quantize_q8k(x)
+    xq = np.repeat(d8.astype(np.float64), 256) * q8
+    rb_in, rb_mid = hipmoe.row_bytes(gt, E), hipmoe.row_bytes(dt, EI)
+    gv = np.array([exact_weights(gq[j * rb_in:(j + 1) * rb_in], gt, E) @ xq for j in range(EI)])
+    uv = np.array([exact_weights(uq[j * rb_in:(j + 1) * rb_in], gt, E) @ xq for j in range(EI)])
+    hv = gv / (1 + np.exp(-gv)) * uv
+    yv = np.array([exact_weights(dq[i * rb_mid:(i + 1) * rb_mid], dt, EI) @ hv for i in range(E)])
+    assert rel_l2(got, yv) < 1e-5
