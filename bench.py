@@ -59,6 +59,11 @@ WORKLOADS = {
                            bias_std=None),
     "mixtral_q4_T64": dict(wtype=hipmoe.Q4_0, E=4096, EI=14336, NE=8, K=2, renorm=1, T=64,
                            bias_std=None),
+    # K-quant experts as a Q4_K_M file mixes them: Q4_K gate/up, Q6_K down
+    "olmoe_q4km_decode": dict(wtype=hipmoe.Q4_K | hipmoe.Q6_K << 8, E=2048, EI=1024, NE=64, K=8,
+                              renorm=0, T=1, bias_std=None),
+    "mixtral_q4km_decode": dict(wtype=hipmoe.Q4_K | hipmoe.Q6_K << 8, E=4096, EI=14336, NE=8,
+                                K=2, renorm=1, T=1, bias_std=None),
     # dense quantized products: N rows of K columns, T tokens
     "olmoe_q8_lm_head": dict(kind="qmat", wtype=hipmoe.Q8_0, N=50304, Kc=2048, T=1),
     "mixtral_q4_lm_head": dict(kind="qmat", wtype=hipmoe.Q4_0, N=32000, Kc=4096, T=1),
@@ -81,8 +86,14 @@ def log(msg):
 
 
 def expert_bytes(w):
-    return 2 * w["EI"] * hipmoe.row_bytes(w["wtype"], w["E"]) + \
-        w["E"] * hipmoe.row_bytes(w["wtype"], w["EI"])
+    gt, dt = hipmoe.wtypes(w["wtype"])
+    return 2 * w["EI"] * hipmoe.row_bytes(gt, w["E"]) + w["E"] * hipmoe.row_bytes(dt, w["EI"])
+
+
+def type_name(wtype):
+    names = {hipmoe.Q8_0: "Q8_0", hipmoe.Q4_0: "Q4_0", hipmoe.Q4_K: "Q4_K", hipmoe.Q6_K: "Q6_K"}
+    gt, dt = hipmoe.wtypes(wtype)
+    return names[gt] if gt == dt else f"{names[gt]} gate/up, {names[dt]} down"
 
 
 def cpu_baseline(w, seconds):
@@ -122,7 +133,11 @@ def bench_qmat(args, w, H):
     `--layers` copies in turn.  Algorithmic bytes per call: the matrix's
     blocks + x + out."""
     wt, N, Kc, T = w["wtype"], w["N"], w["Kc"], w["T"]
-    kname = "k_kq_gemv" if wt in (hipmoe.Q4_K, hipmoe.Q6_K) else "k_qgemv"
+    kquant = wt in (hipmoe.Q4_K, hipmoe.Q6_K)
+    # a Q6_K single token of up to 8192 columns (a multiple of 2048) streams
+    # through the LDS ring kernel; other K-quant products take the register one
+    ring = wt == hipmoe.Q6_K and T == 1 and Kc % 2048 == 0 and Kc <= 8192
+    kname = ("k_kq_stream" if ring else "k_kq_gemv") if kquant else "k_qgemv"
     q = hipmoe.synth_quant_matrix(SEED, 0x7700 + wt, 0.02, wt, N, Kc)
     nl = max(1, args.layers)
     mats = [hipmoe.QMat(q, wt, N, Kc) for _ in range(nl)]
@@ -195,7 +210,7 @@ def bench_qmat(args, w, H):
         "metric": QMAT_METRIC, "value": round(tokens_per_s, 2), "unit": "tokens/s",
         "n_gpus": 1, "steps": steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 6), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "i8" if kname == "k_kq_gemv" else "f32",
+        "vs_baseline": None, "dtype": "i8" if kquant else "f32",
         "data": "synthetic",
         "config": {"workload": args.workload, "rows": N, "cols": Kc, "tokens_per_call": T,
                    "weights": {hipmoe.Q8_0: "Q8_0", hipmoe.Q4_0: "Q4_0", hipmoe.Q4_K: "Q4_K",
@@ -438,7 +453,7 @@ def main():
         "config": {
             "workload": args.workload,
             "d_model": E, "experts": w["NE"], "topk": K, "d_ff": w["EI"],
-            "weights": "Q8_0" if w["wtype"] == hipmoe.Q8_0 else "Q4_0",
+            "weights": type_name(w["wtype"]),
             "tokens_per_call": T, "renorm": bool(w["renorm"]),
             "router_bias_std": w["bias_std"], "layer_copies": nl, "distinct_inputs": ntok,
             "graphs": bool(graphs),

@@ -6,8 +6,8 @@
  * maintainer adds live in a field of struct olmoe_layer and at the top of
  * moe_ffn; here they sit in a side table and a wrapper around the static
  * moe_ffn, unchanged otherwise:
- *   - the upload loop of olmoe_load (tensor_at_q views, HIP_MOE_Q8_0 /
- *     HIP_MOE_Q4_0 from the tensor type, NULL = stay on the CPU);
+ *   - the upload loop of olmoe_load (tensor_at_q views, the HIP_MOE_* types
+ *     of the gate/up and down tensors, NULL = stay on the CPU);
  *   - the early return of moe_ffn (hip_moe_ffn, else the CPU body);
  *   - the hip_moe_free loop of olmoe_close.
  * With no GPU the upload returns NULL and the reference's CPU body runs;
@@ -16,6 +16,13 @@
 #include "models/olmoe/olmoe.c"
 
 #include "hip_moe.h"
+
+/* the library's block type of a reference tensor type, 0 = not taken */
+static int hip_moe_type(int t)
+{
+	return t == TENSOR_Q8_0 ? HIP_MOE_Q8_0 : t == TENSOR_Q4_0 ? HIP_MOE_Q4_0 :
+	       t == TENSOR_Q4_K ? HIP_MOE_Q4_K : t == TENSOR_Q6_K ? HIP_MOE_Q6_K : 0;
+}
 
 /* olmoe_load's loop body for layer i ("At load time") */
 static hip_moe_layer *dropin_upload(struct olmoe *model, struct olmoe_layer *hl)
@@ -29,11 +36,10 @@ static hip_moe_layer *dropin_upload(struct olmoe *model, struct olmoe_layer *hl)
 		tensor_at_q(hl->up_exps, e, &v);   u[e] = v.qdata;
 		tensor_at_q(hl->down_exps, e, &v); d[e] = v.qdata;
 	}
-	int wt = hl->gate_exps->type == TENSOR_Q8_0 ? HIP_MOE_Q8_0 :
-		 hl->gate_exps->type == TENSOR_Q4_0 ? HIP_MOE_Q4_0 : 0;
-	return wt ? hip_moe_upload(hl->gate_inp->data, g, u, d, wt, E, EI, NE,
-				   model->top_k_experts, 0)
-		  : NULL; /* NULL: this layer stays on the CPU */
+	const int gt = hip_moe_type(hl->gate_exps->type), dt = hip_moe_type(hl->down_exps->type);
+	return gt && dt ? hip_moe_upload_typed(hl->gate_inp->data, g, u, d, gt, dt, E, EI, NE,
+					       model->top_k_experts, 0)
+			: NULL; /* NULL: this layer stays on the CPU */
 }
 
 /* moe_ffn with INTEGRATION.md's early return in front of its body */
@@ -50,8 +56,9 @@ static void dropin_moe_ffn(struct olmoe *model, hip_moe_layer *gpu_moe, tensor_t
 }
 
 /*
- * One OLMoE MoE layer (stacked *_exps tensors of type wtype) through the
- * integration lines: out[T][E].  Returns 1 if the GPU took the call, 0 if
+ * One OLMoE MoE layer through the integration lines: out[T][E].  The stacked
+ * *_exps tensors are of reference type wtype & 0xff (gate, up) and
+ * wtype >> 8 (down; 0 = the same).  Returns 1 if the GPU took the call, 0 if
  * the CPU body ran; *uploaded says whether the upload returned a layer.
  */
 int dropin_olmoe_moe_ffn(const float *x, float *out, size_t T, const float *wr,
@@ -68,11 +75,12 @@ int dropin_olmoe_moe_ffn(const float *x, float *out, size_t T, const float *wr,
 	m.top_k_experts = topk;
 	tensor_t *gi = tensor_new_mapped((void *)wr, NE * E, TENSOR_F32);
 	tensor_reshape_2d(gi, NE, E);
-	tensor_t *g = tensor_new_mapped((void *)gate_exps, NE * EI * E, wtype);
+	const int gtype = wtype & 0xff, dtype = (wtype >> 8) ? (wtype >> 8) : gtype;
+	tensor_t *g = tensor_new_mapped((void *)gate_exps, NE * EI * E, gtype);
 	tensor_reshape_3d(g, NE, EI, E);
-	tensor_t *u = tensor_new_mapped((void *)up_exps, NE * EI * E, wtype);
+	tensor_t *u = tensor_new_mapped((void *)up_exps, NE * EI * E, gtype);
 	tensor_reshape_3d(u, NE, EI, E);
-	tensor_t *d = tensor_new_mapped((void *)down_exps, NE * E * EI, wtype);
+	tensor_t *d = tensor_new_mapped((void *)down_exps, NE * E * EI, dtype);
 	tensor_reshape_3d(d, NE, E, EI);
 	hl.gate_inp = gi;
 	hl.gate_exps = g;
