@@ -24,6 +24,10 @@ layers, d_model 2048, 16 heads of 128, 64 experts top-8 d_ff 1024, vocab
 decoding greedily after a 16-token random-id prompt: a step is one
 generated token, the whole step (embedding to greedy pick) replayed from a
 captured HIP graph with the token fed back on the device.
+`mixtral_full_decode` does the same for the Mixtral-8x7B shape after a
+1024-token prompt, and `mixtral_full_decode_b16` for sixteen sequences in
+lockstep (hip_lm_batch_*: each step one token of every sequence, their own
+KV caches, the MoE layer at T = 16): tokens/s counts all sixteen.
 
 The CPU baseline runs in a process of its own (oracle/cpu_baseline.py): the
 oracle with the reference's threading on this host's cores, after the GPU
@@ -77,6 +81,11 @@ WORKLOADS = {
     "mixtral_full_decode": dict(kind="model", arch="mixtral", wtype=hipmoe.Q4_0, layers=32,
                                 E=4096, H=32, KH=8, V=32000, NE=8, K=2, EI=14336, C=4096,
                                 prompt=1024, window=0, theta=1e6),
+    # sixteen sequences in lockstep (hip_lm_batch_*): each step one token of
+    # each, 1024-token prompts
+    "mixtral_full_decode_b16": dict(kind="model", arch="mixtral", wtype=hipmoe.Q4_0, layers=32,
+                                    E=4096, H=32, KH=8, V=32000, NE=8, K=2, EI=14336, C=4096,
+                                    prompt=1024, window=0, theta=1e6, nseq=16),
 }
 MODEL_METRIC = "full-model decode tok/s & % of HBM roofline"
 
@@ -247,42 +256,63 @@ def bench_model(args, w, H):
         md = hiplm.synth_mixtral(SEED, Lh, E, H, KH, V, NE, K, EI, wt, theta=w["theta"],
                                  window=w["window"], share_layers=True)
     prompt = hiplm.synth_prompt(SEED, w["prompt"], V)
+    nseq = w.get("nseq", 1)
     log(f"generated the model in {time.perf_counter() - t0:.1f} s")
     M = hiplm.LmModel(md, Cx)
     log(f"uploaded ({M.weight_bytes() / 1e9:.2f} GB on the device)")
     steps, warm = args.steps, max(1, args.warmup)
     if w["prompt"] + steps + 1 > Cx:
         sys.exit(f"--steps {steps} runs past the context {Cx}")
-    # unique experts per layer and step, from eager steps' routing traces
-    uniq = []
+    # unique experts per layer and step, from eager steps' routing traces: one
+    # token's, or (several sequences) the union over nseq tokens of
+    # single-sequence steps
+    traces = []
     tok = 0
-    for i, t in enumerate(list(prompt[:16]) + [None] * 8):
+    for i, t in enumerate(list(prompt[:16]) + [None] * max(8, nseq)):
         tok, _ = M.decode(int(t) if t is not None else tok)
         if t is None:
-            uniq.append(np.mean([len(np.unique(r)) for r in M.trace()[1]]))
-    mean_uniq = float(np.mean(uniq))
+            traces.append(M.trace()[1])
+    if nseq == 1:
+        mean_uniq = float(np.mean([[len(np.unique(r)) for r in tr] for tr in traces]))
+    else:
+        tr = np.stack(traces[:nseq])  # [nseq][layers][K]
+        mean_uniq = float(np.mean([len(np.unique(tr[:, l])) for l in range(Lh)]))
     M.reset()
-    M.generate(prompt[:16], warm)  # captures the step graphs of short contexts
-    M.reset()
-    toks, ms = M.generate(prompt, steps)
+    if nseq == 1:
+        M.generate(prompt[:16], warm)  # captures the step graphs of short contexts
+        M.reset()
+        toks, ms = M.generate(prompt, steps)
+    else:
+        prompts = np.stack([prompt] + [hiplm.synth_prompt(SEED + 1 + q, w["prompt"], V)
+                                       for q in range(1, nseq)])
+        Bt = hiplm.LmBatch(M, nseq)
+        Bt.generate(prompts[:, :16], warm)
+        Bt.reset()
+        log(f"{nseq} sequences: {w['prompt']} prompt steps, then {steps} timed")
+        toks, ms = Bt.generate(prompts, steps)
+        Bt.free()
     ms_per_step = ms / steps
-    tokens_per_s = steps / (ms / 1e3)
+    tokens_per_s = nseq * steps / (ms / 1e3)
     bpw = 34 / 32 if wt == hipmoe.Q8_0 else 18 / 32
     expert = 3 * E * EI * bpw
     EQ, EKV = H * 128, KH * 128
     attn_w = (2 * EQ + 2 * EKV) * E * bpw  # q, k, v rows of E columns, output E x EQ
     kv_rows = np.mean([w["prompt"] + s + 1 for s in range(1, steps + 1)])
-    per_layer = attn_w + NE * E * 4 + mean_uniq * expert + 2 * kv_rows * EKV * 4
-    bytes_per_tok = Lh * per_layer + V * E * bpw + E * bpw
-    achieved_gbs = bytes_per_tok / (ms_per_step / 1e3) / 1e9
-    log(f"{steps} tokens in {ms:.2f} ms: {ms_per_step * 1e3:.1f} us/token, "
+    # a step reads the weights once for all sequences, and each sequence's
+    # own KV rows and embedding row
+    per_layer = attn_w + NE * E * 4 + mean_uniq * expert + nseq * 2 * kv_rows * EKV * 4
+    bytes_per_step = Lh * per_layer + V * E * bpw + nseq * E * bpw
+    achieved_gbs = bytes_per_step / (ms_per_step / 1e3) / 1e9
+    log(f"{steps} steps x {nseq} sequences in {ms:.2f} ms: {ms_per_step * 1e3:.1f} us/step, "
         f"{tokens_per_s:.1f} tokens/s, {achieved_gbs:.1f} GB/s algorithmic "
-        f"({bytes_per_tok / 1e9:.3f} GB/token)")
+        f"({bytes_per_step / 1e9:.3f} GB/step)")
     M.free()
     cpu = None
     if not args.no_cpu_baseline:
         log(f"cpu baseline ({args.cpu_seconds:.0f} s, own process)")
-        cpu = cpu_baseline(w, args.cpu_seconds)
+        # the reference decodes one sequence at a time: sixteen sequences
+        # are sixteen sequential runs at the single-sequence rate
+        cpu = cpu_baseline({k: v for k, v in w.items() if k != "nseq"}, args.cpu_seconds)
         if cpu:
             log(f"cpu baseline: {cpu['value']:.2f} tokens/s on {cpu['cores']} threads")
     line = {
@@ -295,9 +325,9 @@ def bench_model(args, w, H):
                    "context": Cx,
                    "weights": {hipmoe.Q8_0: "Q8_0", hipmoe.Q4_0: "Q4_0", hipmoe.Q4_K: "Q4_K",
                                hipmoe.Q6_K: "Q6_K"}[wt],
-                   "prompt_tokens": w["prompt"], "graphs": True,
+                   "prompt_tokens": w["prompt"], "sequences": nseq, "graphs": True,
                    "mean_unique_experts": round(mean_uniq, 3),
-                   "algorithmic_bytes_per_token": int(bytes_per_tok)},
+                   "algorithmic_bytes_per_step": int(bytes_per_step)},
         "roofline": {"bound": "hbm", "kernel": "decode_step", "achieved": round(achieved_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),

@@ -113,6 +113,45 @@ size_t hip_lm_weight_bytes(const hip_lm *M);
 /* Release everything (NULL is a no-op). */
 void hip_lm_free(hip_lm *M);
 
+/*
+ * Several sequences decoding in lockstep on one model's weights: every step
+ * takes one token of each of nseq sequences (the same position in each,
+ * their own KV caches), so the weights stream once per step for all of
+ * them and the MoE layer runs at T = nseq.  No counterpart in the
+ * reference, which decodes one sequence per model (llama.c:578-667, one
+ * kvcache); a sequence's results are those of its own single-sequence
+ * decode, within the 1e-3 the steps are held to (the MoE layer at T = nseq
+ * may take the grouped path, f16 operands).
+ *
+ * hip_lm_batch_new allocates nseq KV caches (each as hip_lm_upload's) and
+ * the step's buffers, and reserves the MoE layers' scratch for T = nseq.
+ * It shares M's weights and MoE layers: do not run M and its batches at the
+ * same time.  NULL if not applicable.
+ */
+typedef struct hip_lm_batch hip_lm_batch;
+
+hip_lm_batch *hip_lm_batch_new(hip_lm *M, size_t nseq);
+
+/* One step: toks[nseq] in, logits[nseq][vocab] (host, optional) and the
+ * greedy picks next[nseq] (optional) out.  Synchronous. */
+int hip_lm_batch_decode(hip_lm_batch *B, const int *toks, float *logits, int *next);
+
+/*
+ * hip_lm_generate for every sequence: prompts[nseq][n_prompt] one step
+ * each, then n_gen greedy steps; tokens[nseq][n_gen + 1] receive each
+ * sequence's picks after its prompt and after each generated token.  Steps
+ * replay captured HIP graphs with no host round trip.  decode_ms
+ * (optional): device time of the n_gen generated steps.
+ */
+int hip_lm_batch_generate(hip_lm_batch *B, const int *prompts, size_t n_prompt, size_t n_gen,
+                          int *tokens, float *decode_ms);
+
+/* Empty the caches and reset the position. */
+int hip_lm_batch_reset(hip_lm_batch *B);
+
+/* Release the batch (not the model; NULL is a no-op). */
+void hip_lm_batch_free(hip_lm_batch *B);
+
 #ifdef __cplusplus
 }
 #endif

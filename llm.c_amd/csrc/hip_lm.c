@@ -419,7 +419,7 @@ static int enqueue_step(hip_lm *M, int head, int nact)
 		LCHK(lm_launch_attn(M->d_qkv, y->q_norm, y->k_norm, M->d_freq, M->d_st, M->d_kc + co,
 				    M->d_vc + co, M->d_part, cnt_attn, M->d_attn, (int)M->H,
 				    (int)M->KH, (int)M->C, (int)M->window, M->scale,
-				    M->arch != HIP_LM_OLMOE, (int)l, nact, s), "attention");
+				    M->arch != HIP_LM_OLMOE, (int)l, nact, 1, 0, s), "attention");
 		/* h1 = h0 + attn . Wo^T, moe_in = rms_norm(h1) */
 		LCHK(lm_launch_oproj(wt, y->wo, E, (int)M->EQ, M->d_attn, M->d_h0, M->d_h1,
 				     M->d_rows_t, cnt_o, y->ffn_norm, M->d_moe_in + l * M->E,
@@ -660,6 +660,404 @@ int hip_lm_reset(hip_lm *M)
 	memset(&M->st, 0, sizeof(M->st));
 	/* the host's counters and tok; the epoch keeps counting */
 	HIPCHK(hipMemcpy(M->d_st, &M->st, 5 * sizeof(int), hipMemcpyHostToDevice), "clear state");
+	HIPCHK(hipDeviceSynchronize(), "synchronize");
+	return 1;
+fail:
+	return 0;
+}
+
+/* ---------------------------------------------------------------------- */
+/* several sequences in lockstep                                          */
+/* ---------------------------------------------------------------------- */
+
+/*
+ * A step of S sequences: per layer
+ *   norm rows (residual + rms_norm, or the embedding rows at layer 0) ->
+ *   q/k/v product for S tokens -> attention (grid heads x chunks x S, each
+ *   sequence its own cache) -> output product with the residual rows as
+ *   its add operand -> rms_norm rows -> the MoE layer at T = S,
+ * then the final norm rows, the lm_head product for S tokens and a
+ * first-maximum pick per sequence.  Every sequence is at the same position,
+ * so the step counters (LmState) are shared; the tokens are per sequence.
+ */
+struct hip_lm_batch {
+	hip_lm *M;
+	size_t S;
+	hipStream_t stream;
+	float *d_kc, *d_vc; /* [S][L][KH][C][HL] */
+	float *d_h0, *d_h1, *d_xn, *d_moe_in, *d_moe_out; /* [S][E] */
+	float *d_qkv;       /* [S][EQ + 2 EKV] */
+	float *d_attn;      /* [S][EQ] */
+	float *d_logits;    /* [S][V] */
+	uint64_t *d_part;   /* [S][H][chunks][HL + 2] */
+	uint32_t *d_cnt;    /* [S][H] */
+	int *d_btok;        /* [S] each sequence's last pick */
+	LmState *d_st;
+	int *d_prompt;      /* [S][n_prompt] */
+	int *d_tokens;      /* [S][tokens_cap] */
+	size_t prompt_cap, tokens_cap;
+	LmState st;
+	hipGraphExec_t *g_body, *g_head;
+	hipEvent_t ev0, ev1;
+};
+
+static size_t batch_cache_floats(const hip_lm *M)
+{
+	return M->L * M->KH * M->C * M->HL;
+}
+
+static void batch_drop_graphs(hip_lm_batch *B)
+{
+	for (int i = 0; B->g_body && i <= B->M->nch; i++) {
+		if (B->g_body[i])
+			hipGraphExecDestroy(B->g_body[i]);
+		if (B->g_head[i])
+			hipGraphExecDestroy(B->g_head[i]);
+		B->g_body[i] = B->g_head[i] = NULL;
+	}
+}
+
+void hip_lm_batch_free(hip_lm_batch *B)
+{
+	if (!B)
+		return;
+	batch_drop_graphs(B);
+	free(B->g_body);
+	free(B->g_head);
+	void *bufs[] = {B->d_kc, B->d_vc, B->d_h0, B->d_h1, B->d_xn, B->d_moe_in, B->d_moe_out,
+			B->d_qkv, B->d_attn, B->d_logits, B->d_part, B->d_cnt, B->d_btok, B->d_st,
+			B->d_prompt, B->d_tokens};
+	for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
+		hipFree(bufs[i]);
+	if (B->ev0)
+		hipEventDestroy(B->ev0);
+	if (B->ev1)
+		hipEventDestroy(B->ev1);
+	if (B->stream)
+		hipStreamDestroy(B->stream);
+	free(B);
+}
+
+hip_lm_batch *hip_lm_batch_new(hip_lm *M, size_t nseq)
+{
+	if (!M || nseq < 1 || nseq > 4096) {
+		lm_err("lm_batch_new: NULL model or %zu sequences (1 .. 4096)", nseq);
+		return NULL;
+	}
+	hip_lm_batch *B = calloc(1, sizeof(*B));
+	if (!B) {
+		lm_err("lm_batch_new: out of host memory");
+		return NULL;
+	}
+	B->M = M;
+	B->S = nseq;
+	B->g_body = calloc((size_t)M->nch + 1, sizeof(hipGraphExec_t));
+	B->g_head = calloc((size_t)M->nch + 1, sizeof(hipGraphExec_t));
+	if (!B->g_body || !B->g_head) {
+		lm_err("lm_batch_new: out of host memory");
+		goto fail;
+	}
+	const size_t S = nseq, E = M->E, NQKV = M->EQ + 2 * M->EKV;
+	const size_t cache = S * batch_cache_floats(M) * sizeof(float);
+	const size_t part = S * M->H * (size_t)M->nch * (LM_HLEN + 2) * sizeof(uint64_t);
+	HIPCHK(hipSetDevice(M->device), "hipSetDevice");
+	HIPCHK(hipStreamCreateWithFlags(&B->stream, hipStreamNonBlocking), "hipStreamCreate");
+	HIPCHK(hipEventCreate(&B->ev0), "hipEventCreate");
+	HIPCHK(hipEventCreate(&B->ev1), "hipEventCreate");
+	HIPCHK(hipMalloc((void **)&B->d_kc, cache), "hipMalloc(batch k caches)");
+	HIPCHK(hipMalloc((void **)&B->d_vc, cache), "hipMalloc(batch v caches)");
+	HIPCHK(hipMemset(B->d_kc, 0, cache), "clear k caches");
+	HIPCHK(hipMemset(B->d_vc, 0, cache), "clear v caches");
+	HIPCHK(hipMalloc((void **)&B->d_h0, S * E * 4), "hipMalloc(h0)");
+	HIPCHK(hipMalloc((void **)&B->d_h1, S * E * 4), "hipMalloc(h1)");
+	HIPCHK(hipMalloc((void **)&B->d_xn, S * E * 4), "hipMalloc(xn)");
+	HIPCHK(hipMalloc((void **)&B->d_moe_in, S * E * 4), "hipMalloc(moe_in)");
+	HIPCHK(hipMalloc((void **)&B->d_moe_out, S * E * 4), "hipMalloc(moe_out)");
+	HIPCHK(hipMalloc((void **)&B->d_qkv, S * NQKV * 4), "hipMalloc(qkv)");
+	HIPCHK(hipMalloc((void **)&B->d_attn, S * M->EQ * 4), "hipMalloc(attn)");
+	HIPCHK(hipMalloc((void **)&B->d_logits, S * M->V * 4), "hipMalloc(logits)");
+	HIPCHK(hipMalloc((void **)&B->d_part, part), "hipMalloc(attention partials)");
+	HIPCHK(hipMemset(B->d_part, 0, part), "clear attention partials");
+	HIPCHK(hipMalloc((void **)&B->d_cnt, S * M->H * sizeof(uint32_t)), "hipMalloc(counters)");
+	HIPCHK(hipMemset(B->d_cnt, 0, S * M->H * sizeof(uint32_t)), "clear counters");
+	HIPCHK(hipMalloc((void **)&B->d_btok, S * sizeof(int)), "hipMalloc(tokens)");
+	HIPCHK(hipMemset(B->d_btok, 0, S * sizeof(int)), "clear tokens");
+	HIPCHK(hipMalloc((void **)&B->d_st, sizeof(LmState)), "hipMalloc(state)");
+	/* epoch 1: tags never match the zeroed partials */
+	B->st.epoch = 1;
+	HIPCHK(hipMemcpy(B->d_st, &B->st, sizeof(LmState), hipMemcpyHostToDevice), "set state");
+	/* the MoE layers' scratch for S tokens now: never allocated under capture */
+	for (size_t l = 0; l < M->L; l++)
+		if (!hip_moe_reserve(M->ly[l].moe, S))
+			goto fail;
+	HIPCHK(hipDeviceSynchronize(), "synchronize after batch setup");
+	return B;
+fail:
+	hip_lm_batch_free(B);
+	return NULL;
+}
+
+/* kvcache_rotate of every sequence's cache (they are all at one size) */
+static int batch_rotate_if_full(hip_lm_batch *B)
+{
+	hip_lm *M = B->M;
+	if ((size_t)B->st.size < M->C)
+		return 1;
+	size_t keep = M->window ? M->window : M->C / 2;
+	if (keep > (size_t)B->st.size)
+		keep = (size_t)B->st.size;
+	const size_t drop = (size_t)B->st.size - keep;
+	const size_t slab = M->C * M->HL, slabs = B->S * M->L * M->KH;
+	if (drop > 0) {
+		for (int kv = 0; kv < 2; kv++) {
+			float *base = kv ? B->d_vc : B->d_kc;
+			for (size_t r = 0; r < keep; r += drop) {
+				size_t n = keep - r < drop ? keep - r : drop;
+				LCHK(lm_launch_copy_rows(base + (r + drop) * M->HL, base + r * M->HL,
+							 slab, n * M->HL, slabs, B->stream),
+				     "kv rotate");
+			}
+		}
+	}
+	B->st.size = (int)keep;
+	HIPCHK(hipMemcpyAsync(&B->d_st->size, &B->st.size, sizeof(int), hipMemcpyHostToDevice,
+			      B->stream), "set cache size");
+	HIPCHK(hipStreamSynchronize(B->stream), "synchronize after rotate");
+	return 1;
+fail:
+	return 0;
+}
+
+static int batch_step(hip_lm_batch *B, int head, int nact)
+{
+	hip_lm *M = B->M;
+	const int wt = M->wtype, E = (int)M->E, S = (int)B->S;
+	const int NQKV = (int)(M->EQ + 2 * M->EKV);
+	const size_t cseq = batch_cache_floats(M);
+	hipStream_t s = B->stream;
+	for (size_t l = 0; l < M->L; l++) {
+		struct lm_layer *y = &M->ly[l];
+		const size_t co = l * M->KH * M->C * M->HL;
+		/* layer 0: the tokens' embedding rows; then h0 = h1 + moe_out */
+		LCHK(lm_launch_norm_rows(wt, S, E, l ? B->d_h1 : NULL, l ? B->d_moe_out : NULL,
+					 y->attn_norm, B->d_h0, B->d_xn, M->d_wte, B->d_st,
+					 B->d_prompt, B->d_btok, s), "batch norm");
+		LCHK(moe_launch_qgemv(wt, y->wqkv, NQKV, E, B->d_xn, S, NULL, 0, B->d_qkv, 0, s),
+		     "batch q/k/v");
+		LCHK(lm_launch_attn(B->d_qkv, y->q_norm, y->k_norm, M->d_freq, B->d_st, B->d_kc + co,
+				    B->d_vc + co, B->d_part, B->d_cnt, B->d_attn, (int)M->H,
+				    (int)M->KH, (int)M->C, (int)M->window, M->scale,
+				    M->arch != HIP_LM_OLMOE, (int)l, nact, S, cseq, s),
+		     "batch attention");
+		/* h1 = h0 + attn . Wo^T, moe_in = rms_norm(h1) */
+		LCHK(moe_launch_qgemv(wt, y->wo, E, (int)M->EQ, B->d_attn, S, B->d_h0, 1, B->d_h1, 0,
+				      s), "batch output product");
+		LCHK(lm_launch_norm_rows(wt, S, E, B->d_h1, NULL, y->ffn_norm, NULL, B->d_moe_in,
+					 NULL, B->d_st, NULL, NULL, s), "batch MoE norm");
+		if (!hip_moe_ffn_dev(y->moe, B->d_moe_in, B->d_moe_out, B->S, NULL, NULL, NULL, s))
+			return 0;
+	}
+	if (head) {
+		LCHK(lm_launch_norm_rows(wt, S, E, B->d_h1, B->d_moe_out, M->d_onorm, NULL, B->d_xn,
+					 NULL, B->d_st, NULL, NULL, s), "batch final norm");
+		LCHK(moe_launch_qgemv(wt, M->d_head, (int)M->V, E, B->d_xn, S, NULL, 0, B->d_logits,
+				      0, s), "batch lm_head");
+		LCHK(lm_launch_pick_rows(B->d_logits, S, (int)M->V, B->d_st, B->d_btok, B->d_tokens,
+					 (int)B->tokens_cap, s), "batch pick");
+	}
+	LCHK(lm_launch_step_end(B->d_st, s), "step end");
+	return 1;
+}
+
+/* prompts [S][n_prompt] and tokens [S][n_tokens]; growing drops the graphs */
+static int batch_io(hip_lm_batch *B, size_t n_prompt, size_t n_tokens)
+{
+	if (n_prompt * B->S > B->prompt_cap) {
+		batch_drop_graphs(B);
+		hipFree(B->d_prompt);
+		B->d_prompt = NULL;
+		B->prompt_cap = 0;
+		HIPCHK(hipMalloc((void **)&B->d_prompt, n_prompt * B->S * sizeof(int)),
+		       "hipMalloc(prompts)");
+		B->prompt_cap = n_prompt * B->S;
+	}
+	if (n_tokens > B->tokens_cap) {
+		batch_drop_graphs(B);
+		hipFree(B->d_tokens);
+		B->d_tokens = NULL;
+		B->tokens_cap = 0;
+		HIPCHK(hipMalloc((void **)&B->d_tokens, n_tokens * B->S * sizeof(int)),
+		       "hipMalloc(tokens)");
+		B->tokens_cap = n_tokens;
+	}
+	return 1;
+fail:
+	return 0;
+}
+
+static int batch_start(hip_lm_batch *B, const int *prompts, size_t n_prompt)
+{
+	HIPCHK(hipStreamSynchronize(B->stream), "synchronize");
+	B->st.step = 0;
+	B->st.n_prompt = (int)n_prompt;
+	HIPCHK(hipMemcpy(B->d_prompt, prompts, n_prompt * B->S * sizeof(int),
+			 hipMemcpyHostToDevice), "copy prompts");
+	HIPCHK(hipMemcpy(B->d_st, &B->st, 4 * sizeof(int), hipMemcpyHostToDevice), "set state");
+	return 1;
+fail:
+	return 0;
+}
+
+static int batch_errors(hip_lm_batch *B, const char *what)
+{
+	int err = 0;
+	HIPCHK(hipStreamSynchronize(B->stream), "synchronize");
+	HIPCHK(hipMemcpy(&err, &B->d_st->err, sizeof(int), hipMemcpyDeviceToHost), "read error");
+	if (err) {
+		const int zero = 0;
+		HIPCHK(hipMemcpy(&B->d_st->err, &zero, sizeof(int), hipMemcpyHostToDevice),
+		       "clear error");
+		lm_err("%s: a gather of the step kernels ran out of polls (%d)", what, err);
+		return 0;
+	}
+	for (size_t l = 0; l < B->M->L; l++) {
+		int rc = hip_moe_status(B->M->ly[l].moe, B->stream);
+		if (rc != 0) {
+			lm_err("%s: layer %zu: MoE decode wait failed (%d)", what, l, rc);
+			return 0;
+		}
+	}
+	return 1;
+fail:
+	return 0;
+}
+
+static void batch_advance(hip_lm_batch *B)
+{
+	B->st.step++;
+	B->st.pos++;
+	B->st.size++;
+}
+
+int hip_lm_batch_decode(hip_lm_batch *B, const int *toks, float *logits, int *next)
+{
+	if (!B || !toks) {
+		lm_err("lm_batch_decode: NULL argument");
+		return 0;
+	}
+	for (size_t i = 0; i < B->S; i++)
+		if (!check_token(B->M, toks[i]))
+			return 0;
+	if (!batch_io(B, 1, 1) || !batch_rotate_if_full(B) || !batch_start(B, toks, 1) ||
+	    !batch_step(B, 1, lm_attn_active(B->st.size, (int)B->M->window)))
+		return 0;
+	batch_advance(B);
+	if (!batch_errors(B, "lm_batch_decode"))
+		return 0;
+	if (logits)
+		HIPCHK(hipMemcpy(logits, B->d_logits, B->S * B->M->V * 4, hipMemcpyDeviceToHost),
+		       "copy logits");
+	if (next)
+		HIPCHK(hipMemcpy(next, B->d_btok, B->S * sizeof(int), hipMemcpyDeviceToHost),
+		       "copy picks");
+	return 1;
+fail:
+	return 0;
+}
+
+static int batch_capture(hip_lm_batch *B, int head, int nact, hipGraphExec_t *out)
+{
+	hipGraph_t g = NULL;
+	HIPCHK(hipStreamBeginCapture(B->stream, hipStreamCaptureModeThreadLocal), "begin capture");
+	if (!batch_step(B, head, nact)) {
+		hipStreamEndCapture(B->stream, &g);
+		if (g)
+			hipGraphDestroy(g);
+		return 0;
+	}
+	HIPCHK(hipStreamEndCapture(B->stream, &g), "end capture");
+	HIPCHK(hipGraphInstantiate(out, g, NULL, NULL, 0), "instantiate step graph");
+	hipGraphDestroy(g);
+	return 1;
+fail:
+	if (g)
+		hipGraphDestroy(g);
+	return 0;
+}
+
+int hip_lm_batch_generate(hip_lm_batch *B, const int *prompts, size_t n_prompt, size_t n_gen,
+			  int *tokens, float *decode_ms)
+{
+	if (!B || !prompts || !tokens || n_prompt == 0) {
+		lm_err("lm_batch_generate: NULL argument or empty prompt");
+		return 0;
+	}
+	hip_lm *M = B->M;
+	for (size_t i = 0; i < n_prompt * B->S; i++)
+		if (!check_token(M, prompts[i]))
+			return 0;
+	const size_t steps = n_prompt + n_gen;
+	if (steps > 0x7fffffff || steps * B->S > 0x7fffffff) {
+		lm_err("lm_batch_generate: too many steps");
+		return 0;
+	}
+	if (!batch_io(B, n_prompt, steps) || !batch_start(B, prompts, n_prompt))
+		return 0;
+	/* every step shape of the run, captured before its first launch */
+	{
+		size_t size = (size_t)B->st.size;
+		for (size_t i = 0; i < steps; i++) {
+			if (size >= M->C) {
+				size_t keep = M->window ? M->window : M->C / 2;
+				size = keep < size ? keep : size;
+			}
+			const int head = i + 1 >= n_prompt;
+			const int nact = lm_attn_active((int)size, (int)M->window);
+			hipGraphExec_t *ge = head ? &B->g_head[nact] : &B->g_body[nact];
+			if (!*ge && !batch_capture(B, head, nact, ge))
+				return 0;
+			size++;
+		}
+	}
+	for (size_t i = 0; i < steps; i++) {
+		if (!batch_rotate_if_full(B))
+			return 0;
+		const int head = i + 1 >= n_prompt;
+		const int nact = lm_attn_active(B->st.size, (int)M->window);
+		hipGraphExec_t *ge = head ? &B->g_head[nact] : &B->g_body[nact];
+		if (i == n_prompt)
+			HIPCHK(hipEventRecord(B->ev0, B->stream), "event");
+		HIPCHK(hipGraphLaunch(*ge, B->stream), "step graph");
+		batch_advance(B);
+	}
+	HIPCHK(hipEventRecord(B->ev1, B->stream), "event");
+	if (!batch_errors(B, "lm_batch_generate"))
+		return 0;
+	if (decode_ms) {
+		*decode_ms = 0.0f;
+		if (n_gen)
+			HIPCHK(hipEventElapsedTime(decode_ms, B->ev0, B->ev1), "event time");
+	}
+	for (size_t q = 0; q < B->S; q++)
+		HIPCHK(hipMemcpy(tokens + q * (n_gen + 1), B->d_tokens + q * B->tokens_cap + (n_prompt - 1),
+				 (n_gen + 1) * sizeof(int), hipMemcpyDeviceToHost), "copy tokens");
+	return 1;
+fail:
+	return 0;
+}
+
+int hip_lm_batch_reset(hip_lm_batch *B)
+{
+	if (!B) {
+		lm_err("lm_batch_reset: NULL batch");
+		return 0;
+	}
+	const size_t cache = B->S * batch_cache_floats(B->M) * sizeof(float);
+	HIPCHK(hipStreamSynchronize(B->stream), "synchronize");
+	HIPCHK(hipMemset(B->d_kc, 0, cache), "clear k caches");
+	HIPCHK(hipMemset(B->d_vc, 0, cache), "clear v caches");
+	memset(&B->st, 0, sizeof(B->st));
+	HIPCHK(hipMemcpy(B->d_st, &B->st, 5 * sizeof(int), hipMemcpyHostToDevice), "clear state");
 	HIPCHK(hipDeviceSynchronize(), "synchronize");
 	return 1;
 fail:

@@ -46,12 +46,15 @@ int lm_launch_qkv(int wtype, const uint8_t *W, int N, int K, const float *a, con
                   const int *prompt, float *out, int grid, void *stream);
 /* attention partials hold H * lm_attn_chunks(C, window) * (LM_HLEN + 2)
  * tagged words; cnt holds H zeroed counters.  nact: the chunks of
- * LM_CHUNK rows covering the step's cache rows (lm_attn_active). */
+ * LM_CHUNK rows covering the step's cache rows (lm_attn_active).  nseq
+ * sequences in lockstep: qkv, out, part and cnt hold nseq consecutive
+ * copies, and sequence s's cache is kc/vc + s * cstride floats. */
 int lm_attn_chunks(int C, int window);
 int lm_launch_attn(const float *qkv, const float *q_norm, const float *k_norm,
                    const float *freq, LmState *st, float *kc, float *vc, uint64_t *part,
                    uint32_t *cnt, float *out, int H, int KH, int C, int window,
-                   float scale, int scale_mul, int layer, int nact, void *stream);
+                   float scale, int scale_mul, int layer, int nact, int nseq,
+                   size_t cstride, void *stream);
 
 /* chunks a step over a cache of `size` rows (before the step) reads */
 static inline int lm_attn_active(int size, int window)
@@ -71,6 +74,17 @@ int lm_launch_head(int wtype, const uint8_t *W, int N, int K, const float *a, co
                    const float *w, float *out, uint64_t *best, uint32_t *cnt, LmState *st,
                    int *tokens, int grid, void *stream);
 int lm_launch_step_end(LmState *st, void *stream);
+/* nseq sequences in lockstep: x_out[s] = rms_norm(a[s] + b[s]) * w (b may
+ * be NULL; a NULL: the embedding row of sequence s's step token, from
+ * prompt[s][step] while the prompt lasts, then btok[s]); h_out[s] (may be
+ * NULL) receives a[s] + b[s] */
+int lm_launch_norm_rows(int wtype, int nseq, int E, const float *a, const float *b,
+                        const float *w, float *h_out, float *x_out, const uint8_t *wte,
+                        const LmState *st, const int *prompt, const int *btok, void *stream);
+/* btok[s] = the first maximum of logits[s][V], also into
+ * tokens[s * tstride + step] (tokens may be NULL) */
+int lm_launch_pick_rows(const float *logits, int nseq, int V, const LmState *st, int *btok,
+                        int *tokens, int tstride, void *stream);
 /* dst[s * slab + i] = src[s * slab + i], i < n, s < slabs (ranges must not
  * overlap within a slab) */
 int lm_launch_copy_rows(const float *src, float *dst, size_t slab, size_t n, size_t slabs,

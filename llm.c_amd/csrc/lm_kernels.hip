@@ -244,7 +244,7 @@ void k_lm_qkv(const uint8_t *__restrict__ W, size_t rb, int N, int K, const floa
  * olmoe.c:295) or q . k * scale (Mixtral's flash_attention, scale =
  * 1 / sqrt(HLEN), nn.c:578) as scale_mul says.
  *
- * Grid (H, nact): nact = the chunks of LM_CHUNK rows that cover the cache
+ * Grid (H, nact, sequences): nact = the chunks of LM_CHUNK rows that cover the cache
  * rows [lo, AT), AT = size + 1 (lo > 0 past a sliding window), which the
  * host knows for every step.  Workgroup (h, c) covers rows [j0, j0 + n);
  * the row `size` is this step's k and v, which the chunk holding it takes
@@ -262,7 +262,7 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 						   float *__restrict__ kc, float *__restrict__ vc,
 						   uint64_t *part, u32 *cnt, float *__restrict__ out,
 						   int H, int KH, int C, int window, float scale,
-						   int scale_mul, int layer, int nstride)
+						   int scale_mul, int layer, int nstride, size_t cstride)
 {
 	constexpr int HL = LM_HLEN, CH = LM_CHUNK;
 	__shared__ float cs[HL / 2], sn[HL / 2], sq[HL], sk[HL], sv[HL], sp[CH], so[LM_NT];
@@ -272,6 +272,16 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 	const int h = blockIdx.x, c = blockIdx.y, nact = gridDim.y;
 	const int G = H / KH, kh = h / G;
 	const int EQ = H * HL, EK = KH * HL;
+	{ /* sequence blockIdx.z of several decoding in lockstep: its q/k/v row,
+	   * cache, partials, counters and output row */
+		const size_t sq = blockIdx.z;
+		qkv += sq * (size_t)(EQ + 2 * EK);
+		kc += sq * cstride;
+		vc += sq * cstride;
+		part += sq * (size_t)H * nstride * (HL + 2);
+		cnt += sq * (size_t)H;
+		out += sq * (size_t)EQ;
+	}
 	const float *q = qkv, *k = qkv + EQ, *v = qkv + EQ + EK;
 	const int tid = threadIdx.x;
 
@@ -587,6 +597,77 @@ __global__ void k_lm_copy_rows(const float *__restrict__ src, float *__restrict_
 }
 
 /* ---------------------------------------------------------------------- */
+/* several sequences in lockstep                                          */
+/* ---------------------------------------------------------------------- */
+
+/*
+ * Workgroup s, sequence s: v = a[s] + b[s] (b may be NULL), or the
+ * embedding row of the sequence's step token when a is NULL (the prompt's,
+ * prompt[s][step], while it lasts, then its last pick btok[s]); h_out[s]
+ * receives v (may be NULL), x_out[s] = rms_norm(v) * w.
+ */
+template <int WT>
+__global__ __launch_bounds__(LM_NT) void k_lm_norm_rows(int E, const float *a, const float *b,
+							const float *__restrict__ w, float *h_out,
+							float *__restrict__ x_out,
+							const uint8_t *__restrict__ wte,
+							const LmState *__restrict__ st,
+							const int *__restrict__ prompt,
+							const int *__restrict__ btok)
+{
+	extern __shared__ __attribute__((aligned(16))) float sx[];
+	__shared__ float red[LM_NT / WAVE];
+	constexpr int BB = WT == 1 ? 34 : 18;
+	const int s = blockIdx.x;
+	const size_t o = (size_t)s * E;
+	const uint8_t *emb = nullptr;
+	if (!a) {
+		const int tok = st->step < st->n_prompt
+					? prompt[(size_t)s * st->n_prompt + st->step]
+					: btok[s];
+		emb = wte + (size_t)tok * (size_t)(E / 32) * BB;
+	}
+	stage_norm<WT>(sx, red, E, a ? a + o : nullptr, b ? b + o : nullptr, emb, w,
+		       h_out ? h_out + o : nullptr);
+	for (int c4 = threadIdx.x; c4 < E / 4; c4 += LM_NT)
+		((float4 *)(x_out + o))[c4] =
+			*(const float4 *)(sx + (c4 >> 4) * SEG_STRIDE + (c4 & 15) * 4);
+}
+
+/* workgroup s: the first maximum of logits[s] (main.c:189-193) becomes the
+ * sequence's next token btok[s] and tokens[s * tstride + step] */
+__global__ __launch_bounds__(LM_NT) void k_lm_pick_rows(const float *__restrict__ logits,
+							int V, const LmState *__restrict__ st,
+							int *__restrict__ btok, int *tokens,
+							int tstride)
+{
+	__shared__ float s_v[LM_NT / WAVE];
+	__shared__ int s_i[LM_NT / WAVE];
+	const float *row = logits + (size_t)blockIdx.x * V;
+	float bv = -INFINITY;
+	int bi = 0x7fffffff;
+	for (int i = threadIdx.x; i < V; i += LM_NT)
+		better(bv, bi, row[i], i);
+	for (int o = WAVE / 2; o > 0; o >>= 1)
+		better(bv, bi, __shfl_xor(bv, o, WAVE), __shfl_xor(bi, o, WAVE));
+	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+	if (lane == 0) {
+		s_v[wave] = bv;
+		s_i[wave] = bi;
+	}
+	__syncthreads();
+	if (threadIdx.x == 0) {
+		for (int u = 1; u < LM_NT / WAVE; u++)
+			better(bv, bi, s_v[u], s_i[u]);
+		/* no value above -inf (all NaN): index 0, as main.c's loop leaves it */
+		const int tok = bi == 0x7fffffff ? 0 : bi;
+		btok[blockIdx.x] = tok;
+		if (tokens)
+			tokens[(size_t)blockIdx.x * tstride + st->step] = tok;
+	}
+}
+
+/* ---------------------------------------------------------------------- */
 /* launchers                                                              */
 /* ---------------------------------------------------------------------- */
 
@@ -675,15 +756,45 @@ extern "C" int lm_launch_attn(const float *qkv, const float *q_norm, const float
 			      const float *freq, LmState *st, float *kc, float *vc,
 			      uint64_t *part, uint32_t *cnt, float *out, int H, int KH, int C,
 			      int window, float scale, int scale_mul, int layer, int nact,
-			      void *stream)
+			      int nseq, size_t cstride, void *stream)
 {
 	const int nch = lm_attn_chunks(C, window);
 	if (KH < 1 || H % KH || nch > LM_MAX_CHUNKS || nact < 1 || nact > nch || layer < 0 ||
-	    layer >= LM_HEAD_SLOT)
+	    layer >= LM_HEAD_SLOT || nseq < 1 || nseq > 65535)
 		return (int)hipErrorInvalidValue;
-	hipLaunchKernelGGL(k_lm_attn, dim3(H, nact), dim3(LM_NT), 0, (hipStream_t)stream, qkv,
-			   q_norm, k_norm, freq, st, kc, vc, part, cnt, out, H, KH, C, window, scale,
-			   scale_mul, layer, nch);
+	hipLaunchKernelGGL(k_lm_attn, dim3(H, nact, nseq), dim3(LM_NT), 0, (hipStream_t)stream,
+			   qkv, q_norm, k_norm, freq, st, kc, vc, part, cnt, out, H, KH, C, window,
+			   scale, scale_mul, layer, nch, cstride);
+	return (int)hipGetLastError();
+}
+
+extern "C" int lm_launch_norm_rows(int wtype, int nseq, int E, const float *a, const float *b,
+				   const float *w, float *h_out, float *x_out, const uint8_t *wte,
+				   const LmState *st, const int *prompt, const int *btok,
+				   void *stream)
+{
+	if (nseq < 1 || E % MOE_SEG_COLS || (!a && (!wte || !prompt || !btok)))
+		return (int)hipErrorInvalidValue;
+	const size_t lds = tok_lds(E);
+	hipStream_t s = (hipStream_t)stream;
+	if (wtype == 1)
+		hipLaunchKernelGGL(k_lm_norm_rows<1>, dim3(nseq), dim3(LM_NT), lds, s, E, a, b, w,
+				   h_out, x_out, wte, st, prompt, btok);
+	else if (wtype == 2)
+		hipLaunchKernelGGL(k_lm_norm_rows<2>, dim3(nseq), dim3(LM_NT), lds, s, E, a, b, w,
+				   h_out, x_out, wte, st, prompt, btok);
+	else
+		return (int)hipErrorInvalidValue;
+	return (int)hipGetLastError();
+}
+
+extern "C" int lm_launch_pick_rows(const float *logits, int nseq, int V, const LmState *st,
+				   int *btok, int *tokens, int tstride, void *stream)
+{
+	if (nseq < 1 || V < 1)
+		return (int)hipErrorInvalidValue;
+	hipLaunchKernelGGL(k_lm_pick_rows, dim3(nseq), dim3(LM_NT), 0, (hipStream_t)stream, logits,
+			   V, st, btok, tokens, tstride);
 	return (int)hipGetLastError();
 }
 

@@ -77,6 +77,36 @@ __device__ __forceinline__ static void qgemv_body(float *sx, QG_ARGS, Hook hook 
 		return; /* the whole workgroup: no barrier below is left waiting */
 	u32 dn[DW];
 	load(g, dn);
+	if constexpr (!ONE) {
+		if (!once) {
+			/* more tokens than LDS holds: token groups outside, this
+			 * workgroup's row groups inside, so each token group is
+			 * staged once (a row group's weights load again per token
+			 * group, mostly from L2); the same dots as below */
+			for (int t0 = 0; t0 < T; t0 += tgmax) {
+				const int tg = min(tgmax, T - t0);
+				__syncthreads(); /* the previous token group's readers are done */
+				stage(t0, tg);
+				__syncthreads();
+				if (t0 > 0)
+					load(blockIdx.x, dn);
+				for (int gg = blockIdx.x; gg < ngroups; gg += gridDim.x) {
+					u32 d[DW];
+#pragma unroll
+					for (int i = 0; i < DW; i++)
+						d[i] = dn[i];
+					if (gg + (int)gridDim.x < ngroups)
+						load(gg + gridDim.x, dn);
+					for (int t = 0; t < tg; t++) {
+						float xr[64];
+						lds_x64(sx + t * tstride, seg, xr);
+						store(gg, t0 + t, dot(d, xr, sum32(xr), sum32(xr + 32)));
+					}
+				}
+			}
+			return;
+		}
+	}
 	if (!STAGED && once) {
 		stage(0, T);
 		__syncthreads();
@@ -102,18 +132,10 @@ __device__ __forceinline__ static void qgemv_body(float *sx, QG_ARGS, Hook hook 
 			store(g, 0, dot(d, x1, x1s0, x1s1));
 			continue;
 		}
-		for (int t0 = 0; t0 < T; t0 += tgmax) {
-			const int tg = min(tgmax, T - t0);
-			if (!once) {
-				__syncthreads(); /* the previous group's readers are done */
-				stage(t0, tg);
-				__syncthreads();
-			}
-			for (int t = 0; t < tg; t++) {
-				float xr[64];
-				lds_x64(sx + t * tstride, seg, xr);
-				store(g, t0 + t, dot(d, xr, sum32(xr), sum32(xr + 32)));
-			}
+		for (int t = 0; t < T; t++) { /* every token is staged */
+			float xr[64];
+			lds_x64(sx + t * tstride, seg, xr);
+			store(g, t, dot(d, xr, sum32(xr), sum32(xr + 32)));
 		}
 	}
 }

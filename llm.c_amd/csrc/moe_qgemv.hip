@@ -31,11 +31,15 @@
  * current one's dots run.  Measured with fixed grids of 512 / 768 / 1024 /
  * 2048: OLMoE lm_head (Q8_0, 3 workgroups per CU) 24.5 / 22.0 / 27.1 /
  * 24.8 us, Mixtral lm_head (Q4_0, 5 per CU) 23.5 / 20.5 / 19.8 / 20.8 us:
- * a grid past what is resident leaves a second partial round.  The tokens are staged in LDS tg at a time (up to 4, within
- * QG_LDS_MAX; each segment padded by 4 floats so the C lanes of a row read
- * distinct banks): once per workgroup when they all fit (one token: see
- * k_qgemv1).  Every token reuses the
- * registers' weights, so W is read from HBM once for any T.  (One pass of a
+ * a grid past what is resident leaves a second partial round.  The tokens
+ * are staged in LDS tg at a time (up to 4, within QG_LDS_MAX; each segment
+ * padded by 4 floats so the C lanes of a row read distinct banks): once per
+ * workgroup when they all fit (one token: see k_qgemv1), every token reusing
+ * the registers' weights, so W is read from HBM once.  With more tokens
+ * than that, the token groups go outside and the workgroup's row groups
+ * inside: each group of tokens is staged once and the weights load again
+ * per group, mostly from L2 (sixteen tokens of 4096 columns: 6 groups of 3).
+ * (One pass of a
  * workgroup per row group measured 26.3 us for the OLMoE lm_head and 32.2
  * for Mixtral's: every workgroup staged the token again, 51 and 128 MB of
  * L2 reads.)

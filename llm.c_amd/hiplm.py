@@ -175,6 +175,16 @@ def _bind():
     L.hip_lm_weight_bytes.argtypes = [_vp]
     L.hip_lm_free.restype = None
     L.hip_lm_free.argtypes = [_vp]
+    L.hip_lm_batch_new.restype = _vp
+    L.hip_lm_batch_new.argtypes = [_vp, _sz]
+    L.hip_lm_batch_decode.restype = i32
+    L.hip_lm_batch_decode.argtypes = [_vp, _vp, _vp, _vp]
+    L.hip_lm_batch_generate.restype = i32
+    L.hip_lm_batch_generate.argtypes = [_vp, _vp, _sz, _sz, _vp, f32p]
+    L.hip_lm_batch_reset.restype = i32
+    L.hip_lm_batch_reset.argtypes = [_vp]
+    L.hip_lm_batch_free.restype = None
+    L.hip_lm_batch_free.argtypes = [_vp]
     _lm_bound = True
     return L
 
@@ -267,6 +277,55 @@ class LmModel:
     def free(self):
         if self.h:
             _bind().hip_lm_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class LmBatch:
+    """nseq sequences decoding in lockstep on an LmModel's weights
+    (hip_lm_batch_*)."""
+
+    def __init__(self, model: LmModel, nseq: int):
+        self.model, self.S, self.V = model, nseq, model.V
+        self.h = _bind().hip_lm_batch_new(model.h, nseq)
+        if not self.h:
+            raise HipMoeError("hip_lm_batch_new: " + last_error())
+
+    def decode(self, toks):
+        """One step: (picks [S], logits [S][V])."""
+        t = np.ascontiguousarray(toks, np.int32)
+        assert t.size == self.S
+        lg = np.empty((self.S, self.V), np.float32)
+        nxt = np.empty(self.S, np.int32)
+        if _bind().hip_lm_batch_decode(self.h, t.ctypes.data, lg.ctypes.data,
+                                       nxt.ctypes.data) != 1:
+            raise HipMoeError("hip_lm_batch_decode: " + last_error())
+        return nxt, lg
+
+    def generate(self, prompts, n_gen: int):
+        """prompts [S][n_prompt] -> (tokens [S][n_gen + 1], device ms of the
+        n_gen generated steps)."""
+        pr = np.ascontiguousarray(prompts, np.int32)
+        assert pr.ndim == 2 and pr.shape[0] == self.S
+        toks = np.empty((self.S, n_gen + 1), np.int32)
+        ms = C.c_float(0)
+        if _bind().hip_lm_batch_generate(self.h, pr.ctypes.data, pr.shape[1], n_gen,
+                                         toks.ctypes.data, C.byref(ms)) != 1:
+            raise HipMoeError("hip_lm_batch_generate: " + last_error())
+        return toks, ms.value
+
+    def reset(self):
+        if _bind().hip_lm_batch_reset(self.h) != 1:
+            raise HipMoeError("hip_lm_batch_reset: " + last_error())
+
+    def free(self):
+        if self.h:
+            _bind().hip_lm_batch_free(self.h)
             self.h = None
 
     def __del__(self):

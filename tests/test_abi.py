@@ -157,6 +157,12 @@ def test_lm_calls_on_null_return_zero():
     assert L.hip_lm_reset(None) == 0
     assert L.hip_lm_weight_bytes(None) == 0
     L.hip_lm_free(None)
+    assert not L.hip_lm_batch_new(None, 4)
+    assert "NULL model" in hipmoe.last_error()
+    assert L.hip_lm_batch_decode(None, None, None, None) == 0
+    assert L.hip_lm_batch_generate(None, None, 0, 0, None, None) == 0
+    assert L.hip_lm_batch_reset(None) == 0
+    L.hip_lm_batch_free(None)
 
 
 def test_lm_upload_rejects_bad_descriptors():

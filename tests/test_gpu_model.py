@@ -116,3 +116,81 @@ def test_gpu_model_mixtral_small_vs_reference():
 @pytest.mark.timeout(900)
 def test_gpu_model_mixtral_layer_shape_vs_reference():
     teacher_forced("mixtral_2l", 1e-3, route_steps=(3, 7))
+
+
+# --------------------------------------------------------------------------
+# several sequences in lockstep (hip_lm_batch_*)
+# --------------------------------------------------------------------------
+
+def batch_vs_oracle(name, nseq, tol, n_prompt=None, n_gen=None):
+    """nseq sequences with their own prompts (the first is the fixture's)
+    decoded in lockstep: each sequence's logits against the oracle's
+    decode of that sequence alone (teacher-forced on the oracle's picks),
+    the picks equal wherever the oracle's top two logits are apart; then
+    generate from fresh caches gives each sequence's oracle tokens."""
+    import hiplm
+    from common import SEED
+    mg_md, prompt0, case, g = model_case(name)
+    L, E, H, V, NE, K, EI, Cx, wt, nstd, np_, ng_, stride = case
+    n_prompt = n_prompt or np_
+    n_gen = n_gen or ng_
+    md = mg_md
+    prompts = np.stack([np.asarray(prompt0[:n_prompt], np.int32)] +
+                       [hiplm.synth_prompt(SEED + 101 + s, n_prompt, V) for s in range(1, nseq)])
+    say(f"{name}: {nseq} sequences, {n_prompt} prompt + {n_gen} steps, oracle")
+    table = (hiplm.ptr_table(md) if md["arch"] == "olmoe" else hiplm.ptr_table_llama(md))
+    ref_tok, ref_lg = [], []
+    for s in range(nseq):
+        om = oracle.OlmoeModel(md, Cx, table)
+        t, lg = om.run(prompts[s], n_gen)
+        om.free()
+        ref_tok.append(t)
+        ref_lg.append(lg)
+    ref_tok, ref_lg = np.stack(ref_tok), np.stack(ref_lg)
+    top2 = np.sort(ref_lg, axis=2)[:, :, ::-1][:, :, :2]
+    safe = np.abs(top2[:, :, 0] - top2[:, :, 1]) > 1e-4 * np.abs(top2[:, :, 0])
+    say(f"{name}: upload and {nseq}-sequence batch")
+    M = hiplm.LmModel(md, Cx)
+    Bt = hiplm.LmBatch(M, nseq)
+    try:
+        seqs = np.concatenate([prompts, ref_tok[:, :-1]], axis=1)
+        worst = 0.0
+        for i in range(seqs.shape[1]):
+            nxt, lg = Bt.decode(seqs[:, i])
+            st = i - (n_prompt - 1)
+            if st < 0:
+                continue
+            for s in range(nseq):
+                err = rel_l2(lg[s], ref_lg[s, st])
+                worst = max(worst, err)
+                assert err <= tol, f"sequence {s} step {st}: rel L2 {err:.3e}"
+                if safe[s, st]:
+                    assert nxt[s] == ref_tok[s, st], f"sequence {s} step {st}: pick {nxt[s]}"
+        say(f"{name}: teacher-forced, worst logit rel L2 {worst:.3e}")
+        Bt.reset()
+        toks, ms = Bt.generate(prompts, n_gen)
+        for s in range(nseq):
+            bad = np.nonzero(~safe[s])[0]
+            upto = int(bad[0]) + 1 if bad.size else n_gen + 1
+            assert np.array_equal(toks[s, :upto], ref_tok[s, :upto]), (s, toks[s], ref_tok[s])
+        say(f"{name}: generate {n_gen} steps x {nseq} sequences: tokens equal the oracle's, "
+            f"{ms:.2f} ms")
+    finally:
+        Bt.free()
+        M.free()
+
+
+def test_gpu_batch_olmoe_small_vs_oracle():
+    batch_vs_oracle("olmoe_small", 4, TIGHT)
+
+
+def test_gpu_batch_mixtral_small_vs_oracle():
+    # T = 4 x 2 slots takes the grouped MoE path (f16 operands)
+    batch_vs_oracle("mixtral_small", 4, 1e-3)
+
+
+@pytest.mark.timeout(900)
+def test_gpu_batch16_mixtral_layer_shape_vs_oracle():
+    """Sixteen sequences on two layers of the Mixtral-8x7B shape (32 / 8
+    heads, d_ff 14336, vocab 32000): the MoE layer at T = 16."""
+    batch_vs_oracle("mixtral_2l", 16, 1e-3, n_prompt=4, n_gen=3)

@@ -347,6 +347,14 @@ def test_gpu_grouped_vs_gemv_paths():
     assert rel_l2(m, g) <= REL_L2_TOL
 
 
+def test_gpu_mixtral_T16_vs_oracle():
+    """The MoE layer of sixteen sequences decoding together (one token each):
+    Mixtral Q4_0 at T=16 on the path the layer picks (grouped) against the
+    oracle's moe_ffn, ids and weights bit-exact."""
+    say("mixtral_q4 T=16 vs oracle")
+    _check_layer_vs_oracle("mixtral_q4", 16, 741, expect_path=hipmoe.PATH_GROUPED)
+
+
 # --------------------------------------------------------------------------
 # size-independent properties
 # --------------------------------------------------------------------------
