@@ -348,6 +348,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch without HIP graphs")
+    ap.add_argument("--prompt", type=int, default=0,
+                    help="model workloads: prompt length in place of the workload's (for "
+                         "profiling runs, whose tracers hold every dispatch)")
     ap.add_argument("--copy-calib-mb", type=int, default=0,
                     help="before warmup, run a plain device copy of this many MiB four "
                          "times (its byte counters calibrate the kernels' counters)")
@@ -360,6 +363,10 @@ def main():
         sys.exit(2)
 
     w = WORKLOADS[args.workload]
+    if args.prompt > 0:
+        if w.get("kind") != "model":
+            sys.exit("--prompt applies to the model workloads")
+        w = dict(w, prompt=args.prompt)
     H = hipmoe.hip()
     if H.device_count() < 1:
         sys.exit("no HIP device")

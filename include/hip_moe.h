@@ -281,7 +281,12 @@ hip_moe_qmat *hip_moe_qmat_upload(const void *qdata, int wtype, size_t N, size_t
  * as d * (sum((q + c) x) - c * sum(x)), c = 128 (Q8_0) or 8 (Q4_0):
  * absolute error per output within 2^-24 * (32 (127 + c) + 31 c + 64 * 255)
  * * (sum over blocks of |d| * sum |x|) to first order; ~1e-6 relative L2 on
- * zero-mean activations.  Q4_K/Q6_K matrices take the reference's Q8_K
+ * zero-mean activations.  Several tokens (T >= 2) of a Q8_0/Q4_0 matrix run
+ * on the matrix cores instead: each 32-value token block scaled by a power
+ * of two and split into two f16 parts (~22 bits together), the quants
+ * unscaled (exact in f16), the block scale applied per block in fp32, so the
+ * outputs keep fp32 accuracy (~1e-7 relative, summation order only).
+ * Q4_K/Q6_K matrices take the reference's Q8_K
  * path (matmul.c:291-297: each token quantized by quantize_row_q8, then
  * dot_q4_K_q8_K / dot_q6_K_q8_K, quant_avx2.h:8-209): there every output
  * equals the reference's bit for bit (the integer sums are exact and the
@@ -292,7 +297,11 @@ int hip_moe_qmat_mul(hip_moe_qmat *W, const float *x, size_t T, const float *add
                      size_t add_len, float *out);
 
 /* The same on device pointers (d_x 16-byte aligned), enqueued on `stream`
- * without waiting (NULL = the library's stream for W's device). */
+ * without waiting (NULL = the library's stream for W's device).  It
+ * allocates nothing: the matrix-core form's token buffer, made at upload,
+ * holds 64 tokens (more after a host call of more tokens); calls with more
+ * take the per-token product.  Calls that overlap on one matrix race on
+ * that buffer. */
 int hip_moe_qmat_mul_dev(const hip_moe_qmat *W, const float *d_x, size_t T,
                          const float *d_add, size_t add_len, float *d_out, void *stream);
 

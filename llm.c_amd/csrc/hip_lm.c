@@ -692,6 +692,7 @@ struct hip_lm_batch {
 	uint64_t *d_part;   /* [S][H][chunks][HL + 2] */
 	uint32_t *d_cnt;    /* [S][H] */
 	int *d_btok;        /* [S] each sequence's last pick */
+	void *d_split;      /* the split tokens of a matrix-core product */
 	LmState *d_st;
 	int *d_prompt;      /* [S][n_prompt] */
 	int *d_tokens;      /* [S][tokens_cap] */
@@ -726,7 +727,7 @@ void hip_lm_batch_free(hip_lm_batch *B)
 	free(B->g_head);
 	void *bufs[] = {B->d_kc, B->d_vc, B->d_h0, B->d_h1, B->d_xn, B->d_moe_in, B->d_moe_out,
 			B->d_qkv, B->d_attn, B->d_logits, B->d_part, B->d_cnt, B->d_btok, B->d_st,
-			B->d_prompt, B->d_tokens};
+			B->d_prompt, B->d_tokens, B->d_split};
 	for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
 		hipFree(bufs[i]);
 	if (B->ev0)
@@ -737,6 +738,8 @@ void hip_lm_batch_free(hip_lm_batch *B)
 		hipStreamDestroy(B->stream);
 	free(B);
 }
+
+static int batch_io(hip_lm_batch *B, size_t n_prompt, size_t n_tokens);
 
 hip_lm_batch *hip_lm_batch_new(hip_lm *M, size_t nseq)
 {
@@ -780,6 +783,11 @@ hip_lm_batch *hip_lm_batch_new(hip_lm *M, size_t nseq)
 	HIPCHK(hipMemset(B->d_part, 0, part), "clear attention partials");
 	HIPCHK(hipMalloc((void **)&B->d_cnt, S * M->H * sizeof(uint32_t)), "hipMalloc(counters)");
 	HIPCHK(hipMemset(B->d_cnt, 0, S * M->H * sizeof(uint32_t)), "clear counters");
+	{
+		const size_t KM = E > M->EQ ? E : M->EQ;
+		HIPCHK(hipMalloc(&B->d_split, moe_qmm_split_bytes((int)S, (int)KM)),
+		       "hipMalloc(token split)");
+	}
 	HIPCHK(hipMalloc((void **)&B->d_btok, S * sizeof(int)), "hipMalloc(tokens)");
 	HIPCHK(hipMemset(B->d_btok, 0, S * sizeof(int)), "clear tokens");
 	HIPCHK(hipMalloc((void **)&B->d_st, sizeof(LmState)), "hipMalloc(state)");
@@ -790,6 +798,10 @@ hip_lm_batch *hip_lm_batch_new(hip_lm *M, size_t nseq)
 	for (size_t l = 0; l < M->L; l++)
 		if (!hip_moe_reserve(M->ly[l].moe, S))
 			goto fail;
+	/* prompts and tokens of runs up to the context long: later runs of
+	 * that length reuse the captured step graphs */
+	if (!batch_io(B, M->C, M->C))
+		goto fail;
 	HIPCHK(hipDeviceSynchronize(), "synchronize after batch setup");
 	return B;
 fail:
@@ -828,6 +840,23 @@ fail:
 	return 0;
 }
 
+/* out[S][N] = add + x[S][K] . W^T: on the matrix cores (tokens split
+ * first) where K suits them, else the per-token product */
+static int batch_product(hip_lm_batch *B, const uint8_t *W, int N, int K, const float *x,
+			 const float *add, float *out)
+{
+	const int wt = B->M->wtype, S = (int)B->S;
+	if (moe_qmm_supported(wt, K)) {
+		LCHK(moe_launch_qmm_split(wt, x, S, K, B->d_split, B->stream), "token split");
+		LCHK(moe_launch_qmm(wt, W, N, K, B->d_split, S, add, add != NULL, out, B->stream),
+		     "product");
+	} else {
+		LCHK(moe_launch_qgemv(wt, W, N, K, x, S, add, add != NULL, out, 0, B->stream),
+		     "product");
+	}
+	return 1;
+}
+
 static int batch_step(hip_lm_batch *B, int head, int nact)
 {
 	hip_lm *M = B->M;
@@ -842,16 +871,16 @@ static int batch_step(hip_lm_batch *B, int head, int nact)
 		LCHK(lm_launch_norm_rows(wt, S, E, l ? B->d_h1 : NULL, l ? B->d_moe_out : NULL,
 					 y->attn_norm, B->d_h0, B->d_xn, M->d_wte, B->d_st,
 					 B->d_prompt, B->d_btok, s), "batch norm");
-		LCHK(moe_launch_qgemv(wt, y->wqkv, NQKV, E, B->d_xn, S, NULL, 0, B->d_qkv, 0, s),
-		     "batch q/k/v");
+		if (!batch_product(B, y->wqkv, NQKV, E, B->d_xn, NULL, B->d_qkv))
+			return 0;
 		LCHK(lm_launch_attn(B->d_qkv, y->q_norm, y->k_norm, M->d_freq, B->d_st, B->d_kc + co,
 				    B->d_vc + co, B->d_part, B->d_cnt, B->d_attn, (int)M->H,
 				    (int)M->KH, (int)M->C, (int)M->window, M->scale,
 				    M->arch != HIP_LM_OLMOE, (int)l, nact, S, cseq, s),
 		     "batch attention");
 		/* h1 = h0 + attn . Wo^T, moe_in = rms_norm(h1) */
-		LCHK(moe_launch_qgemv(wt, y->wo, E, (int)M->EQ, B->d_attn, S, B->d_h0, 1, B->d_h1, 0,
-				      s), "batch output product");
+		if (!batch_product(B, y->wo, E, (int)M->EQ, B->d_attn, B->d_h0, B->d_h1))
+			return 0;
 		LCHK(lm_launch_norm_rows(wt, S, E, B->d_h1, NULL, y->ffn_norm, NULL, B->d_moe_in,
 					 NULL, B->d_st, NULL, NULL, s), "batch MoE norm");
 		if (!hip_moe_ffn_dev(y->moe, B->d_moe_in, B->d_moe_out, B->S, NULL, NULL, NULL, s))
@@ -860,8 +889,8 @@ static int batch_step(hip_lm_batch *B, int head, int nact)
 	if (head) {
 		LCHK(lm_launch_norm_rows(wt, S, E, B->d_h1, B->d_moe_out, M->d_onorm, NULL, B->d_xn,
 					 NULL, B->d_st, NULL, NULL, s), "batch final norm");
-		LCHK(moe_launch_qgemv(wt, M->d_head, (int)M->V, E, B->d_xn, S, NULL, 0, B->d_logits,
-				      0, s), "batch lm_head");
+		if (!batch_product(B, M->d_head, (int)M->V, E, B->d_xn, NULL, B->d_logits))
+			return 0;
 		LCHK(lm_launch_pick_rows(B->d_logits, S, (int)M->V, B->d_st, B->d_btok, B->d_tokens,
 					 (int)B->tokens_cap, s), "batch pick");
 	}

@@ -876,10 +876,19 @@ struct hip_moe_qmat {
 	uint8_t *d_w;       /* the GGUF blocks, row-major, unchanged */
 	hipStream_t stream; /* the device's shared library stream */
 	int grid1, grid;    /* workgroups for T == 1 and T > 1 (moe_qgemv_grid) */
+	/* the split tokens of the matrix-core product (T > 1), for up to split_T
+	 * tokens; calls that overlap on one matrix race on it */
+	void *d_split;
+	size_t split_T;
 	/* staging for the host-pointer entry point */
 	size_t cap_T;
 	float *d_x, *d_add, *d_out;
 };
+
+/* tokens the matrix-core product's split buffer holds from upload on (the
+ * device entry point allocates nothing: more tokens take the per-token
+ * product) */
+#define QMAT_SPLIT_T 64
 
 hip_moe_qmat *hip_moe_qmat_upload(const void *qdata, int wtype, size_t N, size_t K)
 {
@@ -935,6 +944,11 @@ hip_moe_qmat *hip_moe_qmat_upload(const void *qdata, int wtype, size_t N, size_t
 		W->grid1 = moe_qgemv_grid(wtype, (int)K, 1);
 		W->grid = moe_qgemv_grid(wtype, (int)K, 0);
 	}
+	if (!is_kquant(wtype) && moe_qmm_supported(wtype, (int)K)) {
+		HIPCHK(hipMalloc(&W->d_split, moe_qmm_split_bytes(QMAT_SPLIT_T, (int)K)),
+		       "hipMalloc(qmat split)");
+		W->split_T = QMAT_SPLIT_T;
+	}
 	/* the K-quant loads read up to MOE_KQ_SLACK bytes past the last block */
 	HIPCHK(hipMalloc((void **)&W->d_w, W->bytes + MOE_KQ_SLACK), "hipMalloc(qmat)");
 	HIPCHK(hipMemset(W->d_w + W->bytes, 0, MOE_KQ_SLACK), "clear qmat slack");
@@ -973,15 +987,20 @@ int hip_moe_qmat_mul_dev(const hip_moe_qmat *W, const float *d_x, size_t T,
 	}
 	if (!check_add(W, T, d_add, add_len))
 		return 0;
-	if (is_kquant(W->wtype))
+	void *s = stream ? stream : (void *)W->stream;
+	if (is_kquant(W->wtype)) {
 		LCHK(moe_launch_kq_gemv(W->wtype, W->d_w, (int)W->N, (int)W->K, d_x, (int)T, d_add,
-					add_len == T * W->N, d_out, T == 1 ? W->grid1 : W->grid,
-					stream ? stream : (void *)W->stream),
+					add_len == T * W->N, d_out, T == 1 ? W->grid1 : W->grid, s),
 		     "kq_gemv");
-	else
+	} else if (T > 1 && W->d_split && T <= W->split_T) {
+		/* several tokens: on the matrix cores, at fp32 accuracy */
+		LCHK(moe_launch_qmm_split(W->wtype, d_x, (int)T, (int)W->K, W->d_split, s),
+		     "qmm token split");
+		LCHK(moe_launch_qmm(W->wtype, W->d_w, (int)W->N, (int)W->K, W->d_split, (int)T,
+				    d_add, add_len == T * W->N, d_out, s), "qmm");
+	} else
 		LCHK(moe_launch_qgemv(W->wtype, W->d_w, (int)W->N, (int)W->K, d_x, (int)T, d_add,
-				      add_len == T * W->N, d_out, T == 1 ? W->grid1 : W->grid,
-				      stream ? stream : (void *)W->stream),
+				      add_len == T * W->N, d_out, T == 1 ? W->grid1 : W->grid, s),
 		     "qgemv");
 	return 1;
 }
@@ -1011,6 +1030,15 @@ int hip_moe_qmat_mul(hip_moe_qmat *W, const float *x, size_t T, const float *add
 		HIPCHK(hipMalloc((void **)&W->d_out, T * W->N * sizeof(float)), "hipMalloc(out)");
 		W->cap_T = T;
 	}
+	if (W->d_split && T > W->split_T) { /* the host entry point may allocate */
+		HIPCHK(hipStreamSynchronize(s), "synchronize");
+		hipFree(W->d_split);
+		W->d_split = NULL;
+		W->split_T = 0;
+		HIPCHK(hipMalloc(&W->d_split, moe_qmm_split_bytes((int)T, (int)W->K)),
+		       "hipMalloc(qmat split)");
+		W->split_T = T;
+	}
 	HIPCHK(hipMemcpyAsync(W->d_x, x, T * W->K * sizeof(float), hipMemcpyHostToDevice, s),
 	       "copy x");
 	if (add)
@@ -1036,6 +1064,7 @@ void hip_moe_qmat_free(hip_moe_qmat *W)
 	if (!W)
 		return;
 	hipFree(W->d_w);
+	hipFree(W->d_split);
 	hipFree(W->d_x);
 	hipFree(W->d_add);
 	hipFree(W->d_out);

@@ -67,6 +67,16 @@ int moe_launch_qgemv(int wtype, const uint8_t *W, int N, int K, const float *x, 
 /* workgroups the device holds at once for the (wtype, K, T == 1) instance */
 int moe_qgemv_grid(int wtype, int K, int one);
 
+/* the same product for several tokens on the matrix cores at fp32
+ * accuracy (moe_qmm.hip): the tokens are first split (moe_launch_qmm_split
+ * into moe_qmm_split_bytes(T, K) bytes, 16-byte aligned), then multiplied;
+ * K = 256 * 2^i up to 4096 (moe_qmm_supported) */
+int moe_qmm_supported(int wtype, int K);
+size_t moe_qmm_split_bytes(int T, int K);
+int moe_launch_qmm_split(int wtype, const float *x, int T, int K, void *split, void *stream);
+int moe_launch_qmm(int wtype, const uint8_t *W, int N, int K, const void *split, int T,
+                   const float *add, int add_rows, float *out, void *stream);
+
 /* The same product on a Q4_K (wtype 3) or Q6_K (5) matrix through Q8_K
  * activations, bit for bit the reference's (kquant.hip); the matrix buffer
  * needs MOE_KQ_SLACK bytes past its end.  moe_kq_supported: K a multiple of

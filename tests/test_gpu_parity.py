@@ -609,10 +609,49 @@ def test_gpu_qmat_lm_head_full_size(wt, N, K):
         assert int(np.argmax(got)) == int(np.argmax(want))
 
 
+@pytest.mark.parametrize("wt", [hipmoe.Q8_0, hipmoe.Q4_0])
+def test_gpu_qmat_matrix_cores_vs_oracle(wt):
+    """Several tokens take the matrix-core product (tokens split into two
+    f16 parts under a per-block power of two, unscaled quants, the block
+    scale applied in fp32): every K it takes (256 .. 4096), token counts
+    that fill one tile, pad one (T = 3) and span three (T = 33), ragged N,
+    held to the fp32 bar TIGHT against the oracle; T = 65 goes past the
+    split buffer of the device entry point (the per-token product) and
+    through the host entry point (which grows it)."""
+    H = hipmoe.hip()
+    for K in (256, 512, 1024, 2048, 4096):
+        N = 16 * (K // 256) + 7
+        q = hipmoe.synth_quant_matrix(SEED, 0x7c00 + K + wt, 0.02, wt, N, K)
+        W = hipmoe.QMat(q, wt, N, K)
+        try:
+            for T in (3, 16, 33):
+                x = hipmoe.synth_normal(SEED, 0x7d00 + K + T + wt, T * K).reshape(T, K)
+                a = hipmoe.synth_normal(SEED, 0x7e00 + K + T, N) if T == 16 else None
+                got = W.mul(x, a)
+                err = rel_l2(got, oracle.qmat_mul(x, q, wt, N, K, a))
+                say(f"qmm wt={wt} K={K} N={N} T={T}: rel L2 {err:.3e}")
+                assert err <= TIGHT
+            if K == 2048:
+                T = 65
+                x = hipmoe.synth_normal(SEED, 0x7f00 + wt, T * K).reshape(T, K)
+                want = oracle.qmat_mul(x, q, wt, N, K)
+                d_x, d_o = H.upload(x), H.malloc(T * N * 4)
+                try:
+                    W.mul_dev(d_x, T, d_o, None, 0, None)
+                    H.sync()
+                    assert rel_l2(H.download(d_o, (T, N), np.float32), want) <= TIGHT
+                finally:
+                    H.free(d_x)
+                    H.free(d_o)
+                assert rel_l2(W.mul(x), want) <= TIGHT
+        finally:
+            W.free()
+
+
 def test_gpu_qmat_dev_token_groups_on_stream():
     """Device-pointer entry point on a caller's stream, T = 8 at K = 4096
-    (tokens staged in LDS three at a time: three groups), N = 257 (a partial
-    last workgroup), add [T][N], then add [N] on the same buffers."""
+    (the matrix-core product), N = 257 (a partial last workgroup), add
+    [T][N], then add [N] on the same buffers."""
     H = hipmoe.hip()
     wt, N, K, T = hipmoe.Q4_0, 257, 4096, 8
     q = hipmoe.synth_quant_matrix(SEED, 0x7800, 0.02, wt, N, K)
