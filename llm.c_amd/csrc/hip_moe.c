@@ -439,7 +439,7 @@ static int ensure_scratch(hip_moe_layer *L, size_t T, hipStream_t s)
 		size_t rows = moe_prefill_max_rows(P, L->NE);
 		HIPCHK(hipMalloc((void **)&L->d_rows, rows * sizeof(int)), "hipMalloc(rows)");
 		HIPCHK(hipMalloc((void **)&L->d_tile_e,
-				 ((size_t)moe_prefill_max_tiles(P, L->NE) + 1) * sizeof(int)),
+				 moe_prefill_tile_ints(P, L->NE) * sizeof(int)),
 		       "hipMalloc(tiles)");
 		HIPCHK(hipMalloc(&L->d_h16, rows * L->EI * 2), "hipMalloc(h16)");
 		HIPCHK(hipMalloc(&L->d_xh, T * L->E * 2), "hipMalloc(xh)");

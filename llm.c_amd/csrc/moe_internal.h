@@ -117,6 +117,7 @@ int moe_prefill_supported(int wtype, size_t E, size_t EI, size_t NE);
 /* tile-table entries and sorted rows any call of at most P pairs uses */
 int moe_prefill_max_tiles(size_t P, size_t NE);
 size_t moe_prefill_max_rows(size_t P, size_t NE);
+size_t moe_prefill_tile_ints(size_t P, size_t NE);
 int moe_prefill_tile_cap(void);
 /* ypart[p][split][E] for every pair p, *split (<= max_split) K-splits of
  * the down projection; combine with kchunks = *split */

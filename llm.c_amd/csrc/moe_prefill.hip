@@ -294,7 +294,7 @@ template <int ODD> struct bsrc<2, ODD> { /* Q4_0 */
 #define PF_WAVES 8
 #define PF_BROWS 512 /* weight rows per workgroup */
 
-template <int WT> struct pf_geo {
+template <int WT, int AL = 1> struct pf_geo { /* AL: A loads per thread (64 rows each) */
 	static constexpr int BB = WT == 1 ? 34 : 18;    /* block bytes */
 	static constexpr int RBS = 2 * BB;               /* bytes of a row per stage */
 	/* 16-byte chunks loaded per row and stage (LDS-DMA writes one 16-byte
@@ -306,9 +306,9 @@ template <int WT> struct pf_geo {
 	static constexpr int RBL = CH * NCH;             /* LDS bytes per row */
 	static constexpr int JB = PF_BROWS * NCH / (PF_WAVES * WAVE); /* B loads per wave */
 	static constexpr int BSZ = PF_BROWS * RBL;       /* B bytes per stage */
-	static constexpr int ASZ = PF_MT_MAX * PF_KB * 2; /* A bytes per stage */
+	static constexpr int ASZ = 64 * AL * PF_KB * 2; /* A bytes per stage */
 	static constexpr int SSZ = BSZ + ASZ;
-	static constexpr int LOADS = JB + 1;             /* loads per wave per stage */
+	static constexpr int LOADS = JB + AL;            /* loads per wave per stage */
 };
 
 
@@ -317,13 +317,14 @@ template <int WT> struct pf_geo {
  * once per operand. */
 template <int WT, int MB>
 __device__ static inline void pf_stage_mfma(const uint8_t *sb, const _Float16 *sa,
-					    const int (&brow)[2], floatx16 (&acc)[2][2], int lane)
+					    const int (&brow)[2], floatx16 (&acc)[MB < 2 ? 2 : MB][2],
+					    int lane)
 {
 	typedef pf_geo<WT> GG;
 	const int h = lane >> 5, r = lane & 31;
 	bsrc<WT, 0> ev[2];
 	bsrc<WT, 1> od[2];
-	half8_t a[2][2][2]; /* [block][k-half][mb] */
+	half8_t a[2][2][MB]; /* [block][k-half][mb] */
 #pragma unroll
 	for (int g = 0; g < 2; g++) {
 		const uint8_t *row = sb + brow[g] * GG::RBS;
@@ -366,7 +367,7 @@ __device__ static inline void pf_stage_mfma(const uint8_t *sb, const _Float16 *s
  * off), so each group reads blocks of one alignment. */
 template <int WT, int MB>
 __device__ static inline void pf_stage_mfma_panel(const uint8_t *sb, const _Float16 *sa, int n,
-						  floatx16 (&acc)[2][2], int lane)
+						  floatx16 (&acc)[MB < 2 ? 2 : MB][2], int lane)
 {
 	typedef pf_geo<WT> GG;
 	constexpr int RUN = PF_BROWS * GG::BB;
@@ -378,7 +379,7 @@ __device__ static inline void pf_stage_mfma_panel(const uint8_t *sb, const _Floa
 		ev[pp].load(sb + pp * RUN + n * GG::BB, h);
 		od[pp].load(sb + pp * RUN + (n + 1) * GG::BB, h);
 	}
-	half8_t a[2][2][2]; /* [block][k-half][mb] */
+	half8_t a[2][2][MB]; /* [block][k-half][mb] */
 #pragma unroll
 	for (int bb = 0; bb < 2; bb++)
 #pragma unroll
@@ -410,13 +411,13 @@ __device__ static inline void pf_stage_mfma_panel(const uint8_t *sb, const _Floa
  * (weights) and s * 128 (A) to the bases.  PANEL: the stage holds two down
  * panels (brow[0] = the lane's even row) instead of [row][chunk] rows.
  */
-template <int WT, int PANEL, int NS, int MB>
+template <int WT, int PANEL, int NS, int MB, int AL = 1>
 __device__ static inline void pf_kloop(uint8_t *lds, const uint8_t *wbase, size_t wstep,
 				       const u32 (&woff)[pf_geo<WT>::JB], const uint8_t *abase,
-				       u32 aoff, const int (&brow)[2], int nsteps,
-				       floatx16 (&acc)[2][2])
+				       const u32 (&aoff)[AL], const int (&brow)[2], int nsteps,
+				       floatx16 (&acc)[MB < 2 ? 2 : MB][2])
 {
-	typedef pf_geo<WT> GG;
+	typedef pf_geo<WT, AL> GG;
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 	const u32 l0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
 	auto issue = [&](int s) {
@@ -427,7 +428,10 @@ __device__ static inline void pf_kloop(uint8_t *lds, const uint8_t *wbase, size_
 			dma_dwordx4(wb, woff[j], st + (u32)((wave * GG::JB + j) * WAVE * GG::CH));
 		/* every wave issues the same loads per stage (the waits count
 		 * them); lanes of padding rows all read the same 16 bytes */
-		dma_dwordx4(abase + (size_t)s * 128, aoff, st + GG::BSZ + (u32)(wave * 1024));
+#pragma unroll
+		for (int a = 0; a < AL; a++)
+			dma_dwordx4(abase + (size_t)s * 128, aoff[a],
+				    st + GG::BSZ + (u32)(a * 8192 + wave * 1024));
 	};
 #pragma unroll
 	for (int s = 0; s < NS - 1; s++)
@@ -530,7 +534,7 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_gateup(
 	const int p = L.arow < MT ? rows[tile * MT + L.arow] : -1;
 	/* padding rows (and the stage's rows past MT): one shared 16-byte chunk
 	 * instead of a row each */
-	const u32 aoff = p >= 0 ? (u32)((size_t)(p / K) * E * 2 + 16 * L.achunk) : 0u;
+	const u32 aoff[1] = {p >= 0 ? (u32)((size_t)(p / K) * E * 2 + 16 * L.achunk) : 0u};
 	const int brow[2] = {wave * 32 + (lane & 31), 256 + wave * 32 + (lane & 31)};
 
 	floatx16 acc[2][2];
@@ -588,9 +592,9 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down(
 				(f < 2 * RUN ? (f / RUN) * PANEL + (size_t)n0 * GG::BB + f % RUN
 					     : (size_t)n0 * GG::BB));
 	}
-	const u32 aoff = L.arow < MT && rows[tile * MT + L.arow] >= 0
-				 ? (u32)((size_t)(tile * MT + L.arow) * EI * 2 + 16 * L.achunk)
-				 : 0u;
+	const u32 aoff[1] = {L.arow < MT && rows[tile * MT + L.arow] >= 0
+				     ? (u32)((size_t)(tile * MT + L.arow) * EI * 2 + 16 * L.achunk)
+				     : 0u};
 	/* MFMA column r of group g = output row wave*64 + 2r + g */
 	const int brow[2] = {wave * 64 + 2 * (lane & 31), wave * 64 + 2 * (lane & 31) + 1};
 
@@ -622,6 +626,338 @@ __global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down(
 }
 
 /* ---------------------------------------------------------------------- */
+/* tiles of 32, 64 or 128 rows per expert                                  */
+/* ---------------------------------------------------------------------- */
+
+/*
+ * With many pairs per expert (prefill), an expert of c pairs takes
+ * floor(c / 128) tiles of 128 rows, and its remainder r one more tile: of
+ * 128 rows if r > 64, of 64 if r > 32, of 32 if r > 0.  A 128-row tile
+ * feeds each dequantised weight block to twice the MFMAs of a 64-row one
+ * (the dequantisation is most of a K-step's VALU work), and the tails keep
+ * the padding of light experts under 32 rows.  The tile list puts every
+ * 128-row tile first, then the 64- and the 32-row tails, so the largest
+ * items are dealt out first.
+ *
+ * tinfo[0] = tiles in use; tile i: tinfo[1 + 2i] = expert | rows/32 << 16,
+ * tinfo[2 + 2i] = its first row.  rows[] holds each expert's pairs at its
+ * first row on, padding -1 to the end of its last tile.  One workgroup;
+ * every entry it names is rewritten on every call (graph-safe).
+ */
+__global__ __launch_bounds__(SORT_THREADS) void k_moe_sort_v(const u32 *__restrict__ ids, int P,
+							     int NE, int Tmax,
+							     int *__restrict__ rows,
+							     int *__restrict__ tinfo)
+{
+	__shared__ int cnt[MOE_MAX_NE], fill[MOE_MAX_NE];
+	__shared__ int rb[MOE_MAX_NE], p4[MOE_MAX_NE], p2[MOE_MAX_NE], p1[MOE_MAX_NE];
+	__shared__ int s_tot[4]; /* rows, 128-, 64-, 32-row tiles */
+	const int tid = threadIdx.x;
+	for (int i = tid; i < NE; i += SORT_THREADS) {
+		cnt[i] = 0;
+		fill[i] = 0;
+	}
+	__syncthreads();
+	u32 v0[16];
+	for (int p0 = 16 * tid; p0 < P; p0 += 16 * SORT_THREADS) {
+		u32 v[16];
+#pragma unroll
+		for (int k = 0; k < 16; k++)
+			v[k] = p0 + k < P ? ids[p0 + k] : 0xffffffffu;
+#pragma unroll
+		for (int k = 0; k < 16; k++) {
+			if (p0 == 16 * tid)
+				v0[k] = v[k];
+			if (v[k] < (u32)NE)
+				atomicAdd(&cnt[v[k]], 1);
+		}
+	}
+	__syncthreads();
+	if (tid < WAVE) { /* exclusive scans over experts, 4 per lane */
+		const int lane = tid;
+		int r4[4], n4[4], t2[4], t1[4], sr = 0, s4 = 0, s2 = 0, s1 = 0;
+#pragma unroll
+		for (int i = 0; i < 4; i++) {
+			const int ex = 4 * lane + i;
+			const int c = ex < NE ? cnt[ex] : 0;
+			int n = c / 128;
+			const int rem = c - 128 * n;
+			int tail = 0;
+			if (rem > 64)
+				n++;
+			else if (rem > 32)
+				tail = 2;
+			else if (rem > 0)
+				tail = 1;
+			n4[i] = n;
+			t2[i] = tail == 2;
+			t1[i] = tail == 1;
+			r4[i] = 128 * n + 32 * tail;
+			sr += r4[i];
+			s4 += n4[i];
+			s2 += t2[i];
+			s1 += t1[i];
+		}
+		int ir = sr, i4 = s4, i2 = s2, i1 = s1;
+#pragma unroll
+		for (int d = 1; d < WAVE; d <<= 1) {
+			const int a = __shfl_up(ir, d, WAVE), b = __shfl_up(i4, d, WAVE);
+			const int c = __shfl_up(i2, d, WAVE), e = __shfl_up(i1, d, WAVE);
+			if (lane >= d) {
+				ir += a;
+				i4 += b;
+				i2 += c;
+				i1 += e;
+			}
+		}
+		int br = ir - sr, b4 = i4 - s4, b2 = i2 - s2, b1 = i1 - s1;
+#pragma unroll
+		for (int i = 0; i < 4; i++) {
+			const int ex = 4 * lane + i;
+			if (ex < NE) {
+				rb[ex] = br;
+				p4[ex] = b4;
+				p2[ex] = b2;
+				p1[ex] = b1;
+			}
+			br += r4[i];
+			b4 += n4[i];
+			b2 += t2[i];
+			b1 += t1[i];
+		}
+		if (lane == WAVE - 1) {
+			s_tot[0] = ir;
+			s_tot[1] = i4;
+			s_tot[2] = i2;
+			s_tot[3] = i1;
+		}
+	}
+	__syncthreads();
+	const int T4 = s_tot[1], T2 = s_tot[2], T1 = s_tot[3], ntiles = T4 + T2 + T1;
+	if (tid == 0)
+		tinfo[0] = ntiles;
+	/* the tile list */
+	for (int ex = tid; ex < NE; ex += SORT_THREADS) {
+		const int c = cnt[ex];
+		int n = c / 128;
+		const int rem = c - 128 * n;
+		int tail = 0;
+		if (rem > 64)
+			n++;
+		else if (rem > 32)
+			tail = 2;
+		else if (rem > 0)
+			tail = 1;
+		for (int i = 0; i < n; i++) {
+			tinfo[1 + 2 * (p4[ex] + i)] = ex | (4 << 16);
+			tinfo[2 + 2 * (p4[ex] + i)] = rb[ex] + 128 * i;
+		}
+		if (tail) {
+			const int tl = tail == 2 ? T4 + p2[ex] : T4 + T2 + p1[ex];
+			tinfo[1 + 2 * tl] = ex | (tail << 16);
+			tinfo[2 + 2 * tl] = rb[ex] + 128 * n;
+		}
+	}
+	for (int tl = ntiles + tid; tl < Tmax; tl += SORT_THREADS) {
+		tinfo[1 + 2 * tl] = -1;
+		tinfo[2 + 2 * tl] = 0;
+	}
+	/* padding rows, then every pair's row */
+	const int R = s_tot[0];
+	for (int i = tid; i < R; i += SORT_THREADS)
+		rows[i] = -1;
+	__syncthreads();
+	for (int p0 = 16 * tid; p0 < P; p0 += 16 * SORT_THREADS) {
+		u32 v[16];
+#pragma unroll
+		for (int k = 0; k < 16; k++)
+			v[k] = p0 == 16 * tid ? v0[k] : p0 + k < P ? ids[p0 + k] : 0xffffffffu;
+#pragma unroll
+		for (int k = 0; k < 16; k++)
+			if (v[k] < (u32)NE)
+				rows[rb[v[k]] + atomicAdd(&fill[v[k]], 1)] = p0 + k;
+	}
+}
+
+/* item of a variable-tile grid: in dispatch order, which is the tile list's
+ * (the largest tiles first) with each tile's column blocks side by side;
+ * consecutive workgroups land on different XCDs, so the 128-row tiles
+ * spread over all of them */
+__device__ static inline bool pf_item_v(int ntiles, int &tile, int &nb)
+{
+	const int NB = (int)gridDim.x, L = (int)blockIdx.x + NB * (int)blockIdx.y;
+	if (L >= NB * ntiles)
+		return false;
+	tile = L / NB;
+	nb = L % NB;
+	return true;
+}
+
+/* this lane's two A chunks (rows arow and arow + 64 of a 128-row stage) */
+struct pf_lanes2 {
+	int arow, achunk;
+	__device__ inline pf_lanes2()
+	{
+		const int slot = threadIdx.x; /* 0 .. 511: rows 0 .. 63 */
+		arow = slot >> 3;
+		achunk = (slot & 7) ^ (arow & 7);
+	}
+};
+
+/* one gate/up tile of 32 * MB rows starting at row r0 (expert e) */
+template <int WT, int NS, int MB>
+__device__ static void pf_gateup_tile(uint8_t *lds, const _Float16 *xh, const uint8_t *gate,
+				      size_t up_off, size_t gu_stride, const int *rows, int K,
+				      int E, int EI, _Float16 *h, int e, int r0, int nb)
+{
+	typedef pf_geo<WT, 2> GG;
+	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+	const int n0 = nb * (PF_BROWS / 2);
+	const size_t rb = (size_t)(E / MOE_QK) * GG::BB;
+	constexpr int CPG = MOE_GU_GROUP * GG::RBS / GG::CH;
+	u32 woff[GG::JB];
+#pragma unroll
+	for (int j = 0; j < GG::JB; j++) {
+		const int f = (wave * GG::JB + j) * WAVE + lane, lg = f / CPG;
+		const size_t o = f < 16 * CPG
+					 ? (lg < 8 ? 0 : up_off) + (size_t)e * gu_stride +
+						   (size_t)(n0 + MOE_GU_GROUP * (lg & 7)) * rb +
+						   (size_t)GG::CH * (f % CPG)
+					 : (size_t)e * gu_stride + (size_t)n0 * rb;
+		woff[j] = (u32)o;
+	}
+	constexpr int MT = 32 * MB;
+	pf_lanes2 L;
+	u32 aoff[2];
+#pragma unroll
+	for (int a = 0; a < 2; a++) {
+		const int ar = L.arow + 64 * a;
+		const int p = ar < MT ? rows[r0 + ar] : -1;
+		aoff[a] = p >= 0 ? (u32)((size_t)(p / K) * E * 2 + 16 * L.achunk) : 0u;
+	}
+	const int brow[2] = {wave * 32 + (lane & 31), 256 + wave * 32 + (lane & 31)};
+	floatx16 acc[MB < 2 ? 2 : MB][2];
+#pragma unroll
+	for (int mb = 0; mb < (MB < 2 ? 2 : MB); mb++)
+#pragma unroll
+		for (int g = 0; g < 2; g++)
+#pragma unroll
+			for (int j = 0; j < 16; j++)
+				acc[mb][g][j] = 0.0f;
+	pf_kloop<WT, 0, NS, MB, 2>(lds, gate, MOE_GU_GROUP * GG::RBS, woff, (const uint8_t *)xh,
+				   aoff, brow, E / PF_KB, acc);
+	const int col = n0 + wave * 32 + (lane & 31), hh = lane >> 5;
+#pragma unroll
+	for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+		for (int j = 0; j < 16; j++) {
+			const int row = r0 + mb * 32 + 8 * (j / 4) + 4 * hh + (j % 4);
+			const float g = acc[mb][0][j], u = acc[mb][1][j];
+			h[(size_t)row * EI + col] = (_Float16)((g / (1.0f + moe_expf(-g))) * u);
+		}
+}
+
+/* k_pf_gateup over the tiles of k_moe_sort_v: one workgroup per CU (the
+ * 128-row instance holds 4 x 2 accumulator tiles per wave) */
+template <int WT, int NS>
+__global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_gateup_v(
+	const _Float16 *__restrict__ xh, const uint8_t *__restrict__ gate, size_t up_off,
+	size_t gu_stride, const int *__restrict__ rows, const int *__restrict__ tinfo, int K,
+	int E, int EI, _Float16 *__restrict__ h)
+{
+	__shared__ __attribute__((aligned(16))) uint8_t lds[NS * pf_geo<WT, 2>::SSZ];
+	int tile, nb;
+	if (!pf_item_v(tinfo[0], tile, nb))
+		return;
+	const int te = tinfo[1 + 2 * tile], e = te & 0xffff, mb = te >> 16, r0 = tinfo[2 + 2 * tile];
+	if (mb == 4)
+		pf_gateup_tile<WT, NS, 4>(lds, xh, gate, up_off, gu_stride, rows, K, E, EI, h, e, r0, nb);
+	else if (mb == 2)
+		pf_gateup_tile<WT, NS, 2>(lds, xh, gate, up_off, gu_stride, rows, K, E, EI, h, e, r0, nb);
+	else
+		pf_gateup_tile<WT, NS, 1>(lds, xh, gate, up_off, gu_stride, rows, K, E, EI, h, e, r0, nb);
+}
+
+/* one down tile of 32 * MB rows starting at row r0 (expert e) */
+template <int WT, int NS, int MB>
+__device__ static void pf_down_tile(uint8_t *lds, int *srow, const _Float16 *h,
+				    const uint8_t *down, size_t dn_stride, const int *rows, int E,
+				    int EI, float *ypart, int e, int r0, int nb)
+{
+	typedef pf_geo<WT, 2> GG;
+	constexpr int MT = 32 * MB;
+	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+	const int S = gridDim.z, nst = EI / PF_KB;
+	const int s0 = blockIdx.z * nst / S, s1 = (blockIdx.z + 1) * nst / S;
+	if (threadIdx.x < MT)
+		srow[threadIdx.x] = rows[r0 + threadIdx.x];
+	const int n0 = nb * PF_BROWS;
+	const size_t RUN = (size_t)PF_BROWS * GG::BB, PANEL = (size_t)E * GG::BB;
+	u32 woff[GG::JB];
+#pragma unroll
+	for (int j = 0; j < GG::JB; j++) {
+		const size_t f = (size_t)((wave * GG::JB + j) * WAVE + lane) * GG::CH;
+		woff[j] = (u32)((size_t)e * dn_stride +
+				(f < 2 * RUN ? (f / RUN) * PANEL + (size_t)n0 * GG::BB + f % RUN
+					     : (size_t)n0 * GG::BB));
+	}
+	pf_lanes2 L;
+	u32 aoff[2];
+#pragma unroll
+	for (int a = 0; a < 2; a++) {
+		const int ar = L.arow + 64 * a;
+		aoff[a] = ar < MT && rows[r0 + ar] >= 0
+				  ? (u32)((size_t)(r0 + ar) * EI * 2 + 16 * L.achunk)
+				  : 0u;
+	}
+	const int brow[2] = {wave * 64 + 2 * (lane & 31), wave * 64 + 2 * (lane & 31) + 1};
+	floatx16 acc[MB < 2 ? 2 : MB][2];
+#pragma unroll
+	for (int mb = 0; mb < (MB < 2 ? 2 : MB); mb++)
+#pragma unroll
+		for (int g = 0; g < 2; g++)
+#pragma unroll
+			for (int j = 0; j < 16; j++)
+				acc[mb][g][j] = 0.0f;
+	pf_kloop<WT, 1, NS, MB, 2>(lds, down + (size_t)s0 * 2 * PANEL, 2 * PANEL, woff,
+				   (const uint8_t *)(h + (size_t)s0 * PF_KB), aoff, brow, s1 - s0,
+				   acc); /* syncs srow */
+	const int hh = lane >> 5;
+#pragma unroll
+	for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+		for (int j = 0; j < 16; j++) {
+			const int pr = srow[mb * 32 + 8 * (j / 4) + 4 * hh + (j % 4)];
+			if (pr < 0)
+				continue;
+#pragma unroll
+			for (int g = 0; g < 2; g++)
+				ypart[((size_t)pr * S + blockIdx.z) * E + n0 + wave * 64 +
+				      2 * (lane & 31) + g] = acc[mb][g][j];
+		}
+}
+
+template <int WT, int NS>
+__global__ __launch_bounds__(PF_WAVES * WAVE) void k_pf_down_v(
+	const _Float16 *__restrict__ h, const uint8_t *__restrict__ down, size_t dn_stride,
+	const int *__restrict__ rows, const int *__restrict__ tinfo, int E, int EI,
+	float *__restrict__ ypart)
+{
+	__shared__ __attribute__((aligned(16))) uint8_t lds[NS * pf_geo<WT, 2>::SSZ];
+	__shared__ int srow[128];
+	int tile, nb;
+	if (!pf_item_v(tinfo[0], tile, nb))
+		return;
+	const int te = tinfo[1 + 2 * tile], e = te & 0xffff, mb = te >> 16, r0 = tinfo[2 + 2 * tile];
+	if (mb == 4)
+		pf_down_tile<WT, NS, 4>(lds, srow, h, down, dn_stride, rows, E, EI, ypart, e, r0, nb);
+	else if (mb == 2)
+		pf_down_tile<WT, NS, 2>(lds, srow, h, down, dn_stride, rows, E, EI, ypart, e, r0, nb);
+	else
+		pf_down_tile<WT, NS, 1>(lds, srow, h, down, dn_stride, rows, E, EI, ypart, e, r0, nb);
+}
+
+/* ---------------------------------------------------------------------- */
 /* host                                                                    */
 /* ---------------------------------------------------------------------- */
 
@@ -646,20 +982,40 @@ static size_t pf_tiles(size_t P, size_t NE, size_t mt)
 	return (P + mt - 1) / mt + (NE < P ? NE : P);
 }
 
-/* capacities for every call of at most P pairs (both tile sizes; each term
- * grows with P, so a smaller call always fits) */
+/* tiles and rows of k_moe_sort_v for P pairs: an expert of c pairs takes at
+ * most c / 128 + 1 tiles and c + 63 rows */
+static size_t pf_vtiles(size_t P, size_t NE)
+{
+	return P / 128 + (NE < P ? NE : P) + 1;
+}
+
+static size_t pf_vrows(size_t P, size_t NE)
+{
+	return P + 64 * (NE < P ? NE : P);
+}
+
+/* capacities for every call of at most P pairs (32-row tiles below 32 pairs
+ * per expert, variable tiles from there; each term grows with P, so a
+ * smaller call always fits) */
 extern "C" int moe_prefill_max_tiles(size_t P, size_t NE)
 {
 	const size_t p32 = P < 32 * NE ? P : 32 * NE;
-	const size_t a = pf_tiles(P, NE, 64), b = pf_tiles(p32, NE, 32);
+	const size_t a = pf_vtiles(P, NE), b = pf_tiles(p32, NE, 32);
 	return (int)(a > b ? a : b);
 }
 
 extern "C" size_t moe_prefill_max_rows(size_t P, size_t NE)
 {
 	const size_t p32 = P < 32 * NE ? P : 32 * NE;
-	const size_t a = pf_tiles(P, NE, 64) * 64, b = pf_tiles(p32, NE, 32) * 32;
+	const size_t a = pf_vrows(P, NE), b = pf_tiles(p32, NE, 32) * 32;
 	return a > b ? a : b;
+}
+
+/* ints of the tile table: 32-row tiles keep one per tile plus the count,
+ * variable tiles two per tile plus the count */
+extern "C" size_t moe_prefill_tile_ints(size_t P, size_t NE)
+{
+	return 2 * (size_t)moe_prefill_max_tiles(P, NE) + 1;
 }
 
 /* the largest tile table the sort kernel handles */
@@ -686,6 +1042,39 @@ extern "C" int moe_launch_prefill(int wtype, const void *xh_, const uint8_t *gat
 	const _Float16 *xh = (const _Float16 *)xh_;
 	const int P = T * K;
 	const int mt = pf_mt((size_t)P, (size_t)NE);
+	if (mt == 64) { /* many pairs per expert: tiles of 32, 64 or 128 rows */
+		const int Tv = (int)pf_vtiles((size_t)P, (size_t)NE);
+		if (Tv > 65535 || pf_vrows((size_t)P, (size_t)NE) * EI * 2 > 0xffffffffull)
+			return (int)hipErrorInvalidValue;
+		hipLaunchKernelGGL(k_moe_sort_v, dim3(1), dim3(SORT_THREADS), 0, s, ids, P, NE, Tv,
+				   rows, tile_e);
+		_Float16 *hh = (_Float16 *)h16;
+		const int nx = E / PF_BROWS, nst = EI / PF_KB;
+		int S = 512 / (nx * Tv);
+		if (S > max_split)
+			S = max_split;
+		if (S > nst / 8)
+			S = nst / 8;
+		if (S < 1)
+			S = 1;
+		*split = S;
+		const dim3 ggu(EI / (PF_BROWS / 2), Tv), gdn(nx, Tv, S), blk(PF_WAVES * WAVE);
+		/* one workgroup per CU: gate/up Q4_0 4 stages of 40 KB (3 in flight:
+		 * 79.4 -> 76.6 us against 3 stages at OLMoE T=512), down 3 (its
+		 * row table takes LDS too); Q8_0 2 of 56 KB */
+		if (wtype == 1) {
+			hipLaunchKernelGGL((k_pf_gateup_v<1, 2>), ggu, blk, 0, s, xh, gate, up_off,
+					   gu_stride, rows, tile_e, K, E, EI, hh);
+			hipLaunchKernelGGL((k_pf_down_v<1, 2>), gdn, blk, 0, s, hh, down, dn_stride, rows,
+					   tile_e, E, EI, ypart);
+		} else {
+			hipLaunchKernelGGL((k_pf_gateup_v<2, 4>), ggu, blk, 0, s, xh, gate, up_off,
+					   gu_stride, rows, tile_e, K, E, EI, hh);
+			hipLaunchKernelGGL((k_pf_down_v<2, 3>), gdn, blk, 0, s, hh, down, dn_stride, rows,
+					   tile_e, E, EI, ypart);
+		}
+		return (int)hipGetLastError();
+	}
 	const int Tmax = (int)pf_tiles((size_t)P, (size_t)NE, (size_t)mt);
 	if (Tmax > SORT_MAX_TILES || (size_t)Tmax * mt * EI * 2 > 0xffffffffull)
 		return (int)hipErrorInvalidValue;
