@@ -495,6 +495,79 @@ __device__ static void router_row(const DecodeArgs &a, int j, u32 prev_epoch, fl
 	__shared__ float s_logit;
 	uint64_t *rep = (uint64_t *)(a.sync + a.off_rep);
 
+	if (a.T == 1) {
+		/* one token: the row and the token arrive in one round trip and
+		 * land transposed in LDS (element k at [k % 8][k / 8]); then the
+		 * chains run from registers.  Lane 8c + s of wave 0 reads elements
+		 * 8m + c for m in segment s (M = E / 64 of them, contiguous in the
+		 * transposed copy) and runs that stretch of AVX2 lane c's chain;
+		 * segment s + 1 takes the running sum from lane 8c + s (a DPP shift
+		 * inside the lanes' 16-lane row), so each chain keeps its FMAs and
+		 * their order.  The other waves stage the token's digit blocks
+		 * from the LDS copy meanwhile. */
+		constexpr int M = E / 64;
+		const float4 *w4 = (const float4 *)(a.router + (size_t)j * E);
+		const float4 *x4 = (const float4 *)a.x;
+		for (int i = threadIdx.x; i < E / 4; i += NT) {
+			const float4 wv = w4[i], xv = x4[i];
+			const int k = 4 * i;
+			sw[((k + 0) & 7) * RS + ((k + 0) >> 3)] = wv.x;
+			sw[((k + 1) & 7) * RS + ((k + 1) >> 3)] = wv.y;
+			sw[((k + 2) & 7) * RS + ((k + 2) >> 3)] = wv.z;
+			sw[((k + 3) & 7) * RS + ((k + 3) >> 3)] = wv.w;
+			sx[((k + 0) & 7) * RS + ((k + 0) >> 3)] = xv.x;
+			sx[((k + 1) & 7) * RS + ((k + 1) >> 3)] = xv.y;
+			sx[((k + 2) & 7) * RS + ((k + 2) >> 3)] = xv.z;
+			sx[((k + 3) & 7) * RS + ((k + 3) >> 3)] = xv.w;
+		}
+		__syncthreads();
+		if (wave == 0) {
+			const int c = lane >> 3, sg = lane & 7;
+			const float4 *wr = (const float4 *)(sw + c * RS + M * sg);
+			const float4 *xr = (const float4 *)(sx + c * RS + M * sg);
+			float4 wv[M / 4], xv[M / 4];
+#pragma unroll
+			for (int i = 0; i < M / 4; i++) {
+				wv[i] = wr[i];
+				xv[i] = xr[i];
+			}
+			float acc = 0.0f;
+#pragma unroll
+			for (int q = 0; q < 8; q++) {
+				if (sg == q)
+#pragma unroll
+					for (int i = 0; i < M / 4; i++) {
+						acc = __builtin_fmaf(xv[i].x, wv[i].x, acc);
+						acc = __builtin_fmaf(xv[i].y, wv[i].y, acc);
+						acc = __builtin_fmaf(xv[i].z, wv[i].z, acc);
+						acc = __builtin_fmaf(xv[i].w, wv[i].w, acc);
+					}
+				if (q < 7) /* lane 8c + q + 1 <- lane 8c + q */
+					acc = __builtin_bit_cast(
+						float, __builtin_amdgcn_update_dpp(
+							       0, __builtin_bit_cast(int, acc), 0x111, 0xf,
+							       0xf, false));
+			}
+			/* chain c's sum sits in lane 8c + 7: lanes 0-7 take them, then
+			 * the AVX2 tree ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) */
+			acc = __shfl(acc, 8 * (lane & 7) + 7, WAVE);
+			acc = acc + __shfl_xor(acc, 4, 8);
+			acc = acc + __shfl_xor(acc, 2, 8);
+			acc = acc + __shfl_xor(acc, 1, 8);
+			if (lane == 0)
+				s_logit = (a.bias ? a.bias[j] : 0.0f) + acc;
+		} else if (dig) {
+			stage_digits_lds<NT - WAVE>(dig, sx, E, RS, (int)threadIdx.x - WAVE);
+		}
+		__syncthreads();
+		if (wave == 0) { /* NREP == WAVE: lane r writes replica r */
+			const u32 ep = __shfl(prev_epoch, 0, WAVE) + 1;
+			const uint64_t v = ((uint64_t)ep << 32) | __builtin_bit_cast(u32, s_logit);
+			st_dev_u64(&rep[(size_t)lane * a.rep_stride + (size_t)j], v);
+		}
+		__syncthreads();
+		return;
+	}
 	for (int t = 0; t < a.T; t++) {
 		if (t == 0) { /* router row and token 0: one round trip */
 			const float4 *w4 = (const float4 *)(a.router + (size_t)j * E);
