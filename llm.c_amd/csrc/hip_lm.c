@@ -692,7 +692,7 @@ struct hip_lm_batch {
 	uint64_t *d_part;   /* [S][H][chunks][HL + 2] */
 	uint32_t *d_cnt;    /* [S][H] */
 	int *d_btok;        /* [S] each sequence's last pick */
-	void *d_split;      /* the split tokens of a matrix-core product */
+	void *d_split;      /* the partial sums of a matrix-core product */
 	LmState *d_st;
 	int *d_prompt;      /* [S][n_prompt] */
 	int *d_tokens;      /* [S][tokens_cap] */
@@ -783,10 +783,14 @@ hip_lm_batch *hip_lm_batch_new(hip_lm *M, size_t nseq)
 	HIPCHK(hipMemset(B->d_part, 0, part), "clear attention partials");
 	HIPCHK(hipMalloc((void **)&B->d_cnt, S * M->H * sizeof(uint32_t)), "hipMalloc(counters)");
 	HIPCHK(hipMemset(B->d_cnt, 0, S * M->H * sizeof(uint32_t)), "clear counters");
-	{
-		const size_t KM = E > M->EQ ? E : M->EQ;
-		HIPCHK(hipMalloc(&B->d_split, moe_qmm_split_bytes((int)S, (int)KM)),
-		       "hipMalloc(token split)");
+	{ /* the largest partial sums: the lm_head's or the q/k/v product's */
+		size_t wb = moe_qmm_work_bytes((int)S, (int)M->V, (int)E);
+		const size_t w2 = moe_qmm_work_bytes((int)S, (int)(M->EQ + 2 * M->EKV), (int)E);
+		const size_t w3 = moe_qmm_work_bytes((int)S, (int)E, (int)M->EQ);
+		wb = wb > w2 ? wb : w2;
+		wb = wb > w3 ? wb : w3;
+		if (wb)
+			HIPCHK(hipMalloc(&B->d_split, wb), "hipMalloc(partial sums)");
 	}
 	HIPCHK(hipMalloc((void **)&B->d_btok, S * sizeof(int)), "hipMalloc(tokens)");
 	HIPCHK(hipMemset(B->d_btok, 0, S * sizeof(int)), "clear tokens");
@@ -840,15 +844,14 @@ fail:
 	return 0;
 }
 
-/* out[S][N] = add + x[S][K] . W^T: on the matrix cores (tokens split
- * first) where K suits them, else the per-token product */
+/* out[S][N] = add + x[S][K] . W^T: on the matrix cores where K suits
+ * them, else the per-token product */
 static int batch_product(hip_lm_batch *B, const uint8_t *W, int N, int K, const float *x,
 			 const float *add, float *out)
 {
 	const int wt = B->M->wtype, S = (int)B->S;
 	if (moe_qmm_supported(wt, K)) {
-		LCHK(moe_launch_qmm_split(wt, x, S, K, B->d_split, B->stream), "token split");
-		LCHK(moe_launch_qmm(wt, W, N, K, B->d_split, S, add, add != NULL, out, B->stream),
+		LCHK(moe_launch_qmm(wt, W, N, K, x, S, add, add != NULL, out, B->d_split, B->stream),
 		     "product");
 	} else {
 		LCHK(moe_launch_qgemv(wt, W, N, K, x, S, add, add != NULL, out, 0, B->stream),

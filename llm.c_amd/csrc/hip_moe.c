@@ -876,10 +876,11 @@ struct hip_moe_qmat {
 	uint8_t *d_w;       /* the GGUF blocks, row-major, unchanged */
 	hipStream_t stream; /* the device's shared library stream */
 	int grid1, grid;    /* workgroups for T == 1 and T > 1 (moe_qgemv_grid) */
-	/* the split tokens of the matrix-core product (T > 1), for up to split_T
-	 * tokens; calls that overlap on one matrix race on it */
+	/* the partial sums of the matrix-core product (T > 1), for up to
+	 * split_T tokens; calls that overlap on one matrix race on them */
 	void *d_split;
 	size_t split_T;
+	int qmm;            /* K suits the matrix-core product */
 	/* staging for the host-pointer entry point */
 	size_t cap_T;
 	float *d_x, *d_add, *d_out;
@@ -889,6 +890,22 @@ struct hip_moe_qmat {
  * device entry point allocates nothing: more tokens take the per-token
  * product) */
 #define QMAT_SPLIT_T 64
+
+/* the matrix-core product's partial sums for up to T tokens (the old ones
+ * freed first) */
+static int qmat_split_alloc(hip_moe_qmat *W, size_t T)
+{
+	hipFree(W->d_split);
+	W->d_split = NULL;
+	W->split_T = 0;
+	const size_t wb = moe_qmm_work_bytes((int)T, (int)W->N, (int)W->K);
+	if (wb)
+		HIPCHK(hipMalloc(&W->d_split, wb), "hipMalloc(qmat partial sums)");
+	W->split_T = T;
+	return 1;
+fail:
+	return 0;
+}
 
 hip_moe_qmat *hip_moe_qmat_upload(const void *qdata, int wtype, size_t N, size_t K)
 {
@@ -944,11 +961,9 @@ hip_moe_qmat *hip_moe_qmat_upload(const void *qdata, int wtype, size_t N, size_t
 		W->grid1 = moe_qgemv_grid(wtype, (int)K, 1);
 		W->grid = moe_qgemv_grid(wtype, (int)K, 0);
 	}
-	if (!is_kquant(wtype) && moe_qmm_supported(wtype, (int)K)) {
-		HIPCHK(hipMalloc(&W->d_split, moe_qmm_split_bytes(QMAT_SPLIT_T, (int)K)),
-		       "hipMalloc(qmat split)");
-		W->split_T = QMAT_SPLIT_T;
-	}
+	W->qmm = !is_kquant(wtype) && moe_qmm_supported(wtype, (int)K);
+	if (W->qmm && !qmat_split_alloc(W, QMAT_SPLIT_T))
+		goto fail;
 	/* the K-quant loads read up to MOE_KQ_SLACK bytes past the last block */
 	HIPCHK(hipMalloc((void **)&W->d_w, W->bytes + MOE_KQ_SLACK), "hipMalloc(qmat)");
 	HIPCHK(hipMemset(W->d_w + W->bytes, 0, MOE_KQ_SLACK), "clear qmat slack");
@@ -992,12 +1007,10 @@ int hip_moe_qmat_mul_dev(const hip_moe_qmat *W, const float *d_x, size_t T,
 		LCHK(moe_launch_kq_gemv(W->wtype, W->d_w, (int)W->N, (int)W->K, d_x, (int)T, d_add,
 					add_len == T * W->N, d_out, T == 1 ? W->grid1 : W->grid, s),
 		     "kq_gemv");
-	} else if (T > 1 && W->d_split && T <= W->split_T) {
+	} else if (T > 1 && W->qmm && T <= W->split_T) {
 		/* several tokens: on the matrix cores, at fp32 accuracy */
-		LCHK(moe_launch_qmm_split(W->wtype, d_x, (int)T, (int)W->K, W->d_split, s),
-		     "qmm token split");
-		LCHK(moe_launch_qmm(W->wtype, W->d_w, (int)W->N, (int)W->K, W->d_split, (int)T,
-				    d_add, add_len == T * W->N, d_out, s), "qmm");
+		LCHK(moe_launch_qmm(W->wtype, W->d_w, (int)W->N, (int)W->K, d_x, (int)T, d_add,
+				    add_len == T * W->N, d_out, W->d_split, s), "qmm");
 	} else
 		LCHK(moe_launch_qgemv(W->wtype, W->d_w, (int)W->N, (int)W->K, d_x, (int)T, d_add,
 				      add_len == T * W->N, d_out, T == 1 ? W->grid1 : W->grid, s),
@@ -1030,14 +1043,10 @@ int hip_moe_qmat_mul(hip_moe_qmat *W, const float *x, size_t T, const float *add
 		HIPCHK(hipMalloc((void **)&W->d_out, T * W->N * sizeof(float)), "hipMalloc(out)");
 		W->cap_T = T;
 	}
-	if (W->d_split && T > W->split_T) { /* the host entry point may allocate */
+	if (W->qmm && T > W->split_T) { /* the host entry point may allocate */
 		HIPCHK(hipStreamSynchronize(s), "synchronize");
-		hipFree(W->d_split);
-		W->d_split = NULL;
-		W->split_T = 0;
-		HIPCHK(hipMalloc(&W->d_split, moe_qmm_split_bytes((int)T, (int)W->K)),
-		       "hipMalloc(qmat split)");
-		W->split_T = T;
+		if (!qmat_split_alloc(W, T))
+			return 0;
 	}
 	HIPCHK(hipMemcpyAsync(W->d_x, x, T * W->K * sizeof(float), hipMemcpyHostToDevice, s),
 	       "copy x");

@@ -68,14 +68,13 @@ int moe_launch_qgemv(int wtype, const uint8_t *W, int N, int K, const float *x, 
 int moe_qgemv_grid(int wtype, int K, int one);
 
 /* the same product for several tokens on the matrix cores at fp32
- * accuracy (moe_qmm.hip): the tokens are first split (moe_launch_qmm_split
- * into moe_qmm_split_bytes(T, K) bytes, 16-byte aligned), then multiplied;
- * K = 256 * 2^i up to 4096 (moe_qmm_supported) */
+ * accuracy (moe_qmm.hip): x [T][K] fp32, 16-byte aligned; K = 256, 512
+ * or a multiple of 512 (moe_qmm_supported); work holds
+ * moe_qmm_work_bytes(T, N, K) bytes (none for K <= 512) */
 int moe_qmm_supported(int wtype, int K);
-size_t moe_qmm_split_bytes(int T, int K);
-int moe_launch_qmm_split(int wtype, const float *x, int T, int K, void *split, void *stream);
-int moe_launch_qmm(int wtype, const uint8_t *W, int N, int K, const void *split, int T,
-                   const float *add, int add_rows, float *out, void *stream);
+size_t moe_qmm_work_bytes(int T, int N, int K);
+int moe_launch_qmm(int wtype, const uint8_t *W, int N, int K, const float *x, int T,
+                   const float *add, int add_rows, float *out, void *work, void *stream);
 
 /* The same product on a Q4_K (wtype 3) or Q6_K (5) matrix through Q8_K
  * activations, bit for bit the reference's (kquant.hip); the matrix buffer

@@ -24,17 +24,23 @@
  * of group l / 16, and the result D[token 4g + j][row l % 16] (j < 4).  The
  * values of group g are the block's elements 8g .. 8g+7 for Q8_0 (quant
  * bytes 8g.. of the block) and 4g .. 4g+3, 16+4g .. 16+4g+3 for Q4_0 (the
- * low and high nibbles of quant bytes 4g ..).  The tokens are split once
- * per call (k_qmm_split) into that order: xs[token][block] = hi groups 0-3
- * then lo groups 0-3 (8 f16 each, 128 bytes), tsc[block][token] = 2^-e,
- * tokens padded to a multiple of 16 with zeros.
+ * low and high nibbles of quant bytes 4g ..).
  *
- * Work: a workgroup of four waves takes 16 rows and one tile of 16 tokens;
- * wave w the w-th quarter of K.  A wave loads all of its weights first
- * (Q4_0 five, Q8_0 seven dwords per lane and pair of blocks, the windows
- * aligned to 4 bytes), then walks its blocks with the next pair's token
- * operands in flight; the four quarters meet in LDS and are added in wave
- * order.
+ * Work: a workgroup of four waves takes 64 rows (16 a wave), one tile of 16
+ * tokens and one stretch of QMM_PZ pairs of blocks (512 columns) of K.  It
+ * first puts every load of its weights in flight (each wave its 16 rows:
+ * Q4_0 five, Q8_0 seven dwords per lane and pair of blocks, windows aligned
+ * to 4 bytes), then stages the 16 tokens' columns of its stretch in LDS,
+ * split as above (hi and lo in [block][group][token] order, so a wave's
+ * operand reads are 1 KB contiguous), so each token value is read once
+ * per 64 rows.  With K longer than one stretch the stretches are
+ * workgroups of their own (grid z), whose partial sums a second launch
+ * adds in stretch order (k_qmm_reduce): deterministic, and enough
+ * workgroups for the few-thousand-row projections.  (Adding them in the
+ * product launch instead, by the last stretch of a tile to arrive, polling
+ * epoch-tagged partials, measured 26.7 us against 22.8 us for the two
+ * launches at 16 tokens x 6144 x 4096 Q4_0: the last arrivals' polls sit
+ * in series behind the slowest stretch.)
  *
  * Bound: HBM for a few tokens (the weights are read once per token tile;
  * the tokens, T * K * 4 bytes, come from L2).  Algorithmic bytes per call:
@@ -49,69 +55,9 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 #define QMM_ROWS 16
 #define QMM_TOK 16
 #define QMM_WAVES 4
-#define QMM_MAX_PPW 16 /* pairs of blocks per wave: K up to 4096 */
-
-/* ---------------------------------------------------------------------- */
-/* token split                                                            */
-/* ---------------------------------------------------------------------- */
-
-/* thread (token t, block b, group g): the group's 8 values of x[t][32b..],
- * scaled by the block's 2^e, as hi and lo f16 */
-template <int WT>
-__global__ __launch_bounds__(256) void k_qmm_split(const float *__restrict__ x, int T, int TP,
-						    int K, uint4 *__restrict__ xs,
-						    float *__restrict__ tsc)
-{
-	const int nb = K / 32;
-	const int i = blockIdx.x * 256 + threadIdx.x; /* TP * nb * 4 threads, a multiple of 64 */
-	const int g = i & 3, b = (i >> 2) % nb, t = (i >> 2) / nb;
-	float v[8];
-	if (t < T) {
-		const float *xb = x + (size_t)t * K + 32 * b;
-		if (WT == 1) {
-			const float4 p = ((const float4 *)(xb + 8 * g))[0];
-			const float4 q = ((const float4 *)(xb + 8 * g))[1];
-			v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w;
-			v[4] = q.x; v[5] = q.y; v[6] = q.z; v[7] = q.w;
-		} else {
-			const float4 p = *(const float4 *)(xb + 4 * g);
-			const float4 q = *(const float4 *)(xb + 16 + 4 * g);
-			v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w;
-			v[4] = q.x; v[5] = q.y; v[6] = q.z; v[7] = q.w;
-		}
-	} else {
-#pragma unroll
-		for (int k = 0; k < 8; k++)
-			v[k] = 0.0f;
-	}
-	float m = 0.0f;
-#pragma unroll
-	for (int k = 0; k < 8; k++)
-		m = fmaxf(m, fabsf(v[k]));
-	m = fmaxf(m, __shfl_xor(m, 1, 4));
-	m = fmaxf(m, __shfl_xor(m, 2, 4));
-	/* 2^sh * m in [2^13, 2^14); a zero block keeps sh = 0 */
-	int sh = 0;
-	if (m > 0.0f) {
-		const int ex = (int)((__builtin_bit_cast(u32, m) >> 23) & 0xffu) - 127;
-		sh = 13 - ex;
-		sh = sh > 100 ? 100 : sh < -100 ? -100 : sh;
-	}
-	const float s = __builtin_bit_cast(float, (u32)(sh + 127) << 23);
-	half8_t hi, lo;
-#pragma unroll
-	for (int k = 0; k < 8; k++) {
-		const float y = v[k] * s;
-		const _Float16 h = (_Float16)y;
-		hi[k] = h;
-		lo[k] = (_Float16)(y - (float)h);
-	}
-	uint4 *o = xs + ((size_t)t * nb + b) * 8;
-	o[g] = __builtin_bit_cast(uint4, hi);
-	o[4 + g] = __builtin_bit_cast(uint4, lo);
-	if (g == 0)
-		tsc[(size_t)b * TP + t] = __builtin_bit_cast(float, (u32)(127 - sh) << 23);
-}
+#define QMM_PZ 8 /* pairs of blocks per workgroup: 512 columns of K; at 16
+		  * the weights in flight take 256 VGPRs and one wave per SIMD
+		  * fits (1.4x slower at 16 tokens x 6144 x 4096 Q4_0) */
 
 /* ---------------------------------------------------------------------- */
 /* the product                                                            */
@@ -194,156 +140,203 @@ template <> struct qmm_pair<1> { /* Q8_0: 68 bytes, 4-byte aligned */
 	}
 };
 
+/* the split of one token block: the 8 values of a lane group scaled by the
+ * block's 2^e (the 4 groups of a block are lanes l, l ^ 16, l ^ 32, l ^ 48) */
+__device__ static inline void qmm_split8(const float (&v)[8], half8_t &hi, half8_t &lo,
+					 float &unscale)
+{
+	float m = 0.0f;
+#pragma unroll
+	for (int k = 0; k < 8; k++)
+		m = fmaxf(m, fabsf(v[k]));
+	m = fmaxf(m, __shfl_xor(m, 16, WAVE));
+	m = fmaxf(m, __shfl_xor(m, 32, WAVE));
+	/* 2^sh * m in [2^13, 2^14); a zero block keeps sh = 0 */
+	int sh = 0;
+	if (m > 0.0f) {
+		const int ex = (int)((__builtin_bit_cast(u32, m) >> 23) & 0xffu) - 127;
+		sh = 13 - ex;
+		sh = sh > 100 ? 100 : sh < -100 ? -100 : sh;
+	}
+	const float s = __builtin_bit_cast(float, (u32)(sh + 127) << 23);
+#pragma unroll
+	for (int k = 0; k < 8; k++) {
+		const float y = v[k] * s;
+		const _Float16 h = (_Float16)y;
+		hi[k] = h;
+		lo[k] = (_Float16)(y - (float)h);
+	}
+	unscale = __builtin_bit_cast(float, (u32)(127 - sh) << 23);
+}
+
 /*
- * Grid (ceil(N / 16), TP / 16), four waves.  PPW: pairs of blocks per wave
- * (K = 256 * PPW).
+ * Grid (ceil(N / 64), ceil(T / 16), K / (64 PZ)), four waves.  PZ: pairs of
+ * blocks per workgroup.  part (grid z > 1): [z][T][N] partial sums.
  */
-template <int WT, int PPW>
+template <int WT, int PZ>
 __global__ __launch_bounds__(QMM_WAVES * WAVE) void k_qmm(
-	const uint8_t *__restrict__ W, size_t rb, int N, int K, const uint4 *__restrict__ xs,
-	const float *__restrict__ tsc, int T, int TP, const float *__restrict__ add, int add_rows,
-	float *__restrict__ out)
+	const uint8_t *__restrict__ W, size_t rb, int N, int K, const float *__restrict__ x, int T,
+	const float *__restrict__ add, int add_rows, float *__restrict__ out,
+	float *__restrict__ part)
 {
 	typedef qmm_pair<WT> P;
-	constexpr int BB = WT == 1 ? 34 : 18;
-	__shared__ floatx4 red[QMM_WAVES - 1][WAVE];
+	constexpr int BB = WT == 1 ? 34 : 18, NB = 2 * PZ;
+	__shared__ uint4 s_hi[NB][4][QMM_TOK], s_lo[NB][4][QMM_TOK];
+	/* read as float4: 16-byte aligned whatever else the LDS holds */
+	__shared__ __attribute__((aligned(16))) float s_ts[NB][QMM_TOK];
 	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
 	const int r = lane & 15, g = lane >> 4;
-	const int n = blockIdx.x * QMM_ROWS + r, t0 = blockIdx.y * QMM_TOK;
-	const int nb = K / 32, p0 = wave * PPW;
+	const int n = blockIdx.x * (QMM_WAVES * QMM_ROWS) + wave * QMM_ROWS + r;
+	const int t0 = blockIdx.y * QMM_TOK, z = blockIdx.z;
 	/* rows past N repeat the last row (their results are not stored) */
-	const uint8_t *row = W + (size_t)min(n, N - 1) * rb + (size_t)p0 * 2 * BB;
-
-	u32 w[PPW][P::DW];
+	const uint8_t *row = W + (size_t)min(n, N - 1) * rb + (size_t)z * PZ * 2 * BB;
+	u32 w[PZ][P::DW];
 #pragma unroll
-	for (int p = 0; p < PPW; p++)
+	for (int p = 0; p < PZ; p++)
 		P::load(row + (size_t)p * 2 * BB, g, w[p]);
 
-	/* token operands of pair p: hi and lo of both blocks, the scales of
-	 * tokens 4g .. 4g+3 */
-	const uint4 *xt = xs + ((size_t)(t0 + r) * nb) * 8 + g;
-	auto ld_tok = [&](int p, uint4 (&a)[4], float4 (&ts)[2]) {
-		const int b = 2 * (p0 + p);
-		a[0] = xt[(size_t)b * 8];
-		a[1] = xt[(size_t)b * 8 + 4];
-		a[2] = xt[(size_t)(b + 1) * 8];
-		a[3] = xt[(size_t)(b + 1) * 8 + 4];
-		ts[0] = *(const float4 *)(tsc + (size_t)b * TP + t0 + 4 * g);
-		ts[1] = *(const float4 *)(tsc + (size_t)(b + 1) * TP + t0 + 4 * g);
-	};
-	floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-	uint4 a[4], an[4];
-	float4 ts[2], tn[2];
-	ld_tok(0, a, ts);
+	/* the tokens' blocks of this stretch, split into LDS: thread item i =
+	 * (block, group, token), the token fastest, so a wave's stores are 1 KB
+	 * contiguous (with the group fastest every lane of a wave hit the same
+	 * banks); all of a thread's loads go out before any is used (a loop
+	 * that waited for each made the staging eight round trips: 33 -> ? us
+	 * for the Mixtral q/k/v product of 16 tokens) */
+	constexpr int IT = QMM_TOK * NB * 4 / (QMM_WAVES * WAVE); /* items per thread */
+	float v[IT][8];
 #pragma unroll
-	for (int p = 0; p < PPW; p++) {
-		if (p + 1 < PPW)
-			ld_tok(p + 1, an, tn);
+	for (int u = 0; u < IT; u++) { /* every load first: one round trip */
+		const int i = (int)threadIdx.x + u * QMM_WAVES * WAVE;
+		const int t = i & 15, gg = (i >> 4) & 3, b = i >> 6;
+		float4 p = {0.0f, 0.0f, 0.0f, 0.0f}, q = p;
+		if (t0 + t < T) {
+			const float *xb = x + (size_t)(t0 + t) * K + (size_t)(z * NB + b) * 32;
+			p = WT == 1 ? ((const float4 *)(xb + 8 * gg))[0] : *(const float4 *)(xb + 4 * gg);
+			q = WT == 1 ? ((const float4 *)(xb + 8 * gg))[1]
+				    : *(const float4 *)(xb + 16 + 4 * gg);
+		}
+		v[u][0] = p.x; v[u][1] = p.y; v[u][2] = p.z; v[u][3] = p.w;
+		v[u][4] = q.x; v[u][5] = q.y; v[u][6] = q.z; v[u][7] = q.w;
+	}
+#pragma unroll
+	for (int u = 0; u < IT; u++) {
+		const int i = (int)threadIdx.x + u * QMM_WAVES * WAVE;
+		const int t = i & 15, gg = (i >> 4) & 3, b = i >> 6;
+		half8_t hi, lo;
+		float us;
+		qmm_split8(v[u], hi, lo, us);
+		s_hi[b][gg][t] = __builtin_bit_cast(uint4, hi);
+		s_lo[b][gg][t] = __builtin_bit_cast(uint4, lo);
+		if (gg == 0)
+			s_ts[b][t] = us;
+	}
+	__syncthreads();
+
+	floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+	for (int p = 0; p < PZ; p++) {
 #pragma unroll
 		for (int h = 0; h < 2; h++) {
+			const int b = 2 * p + h;
 			float d;
 			const half8_t bq = P::operand(w[p], h, d);
-			const floatx4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+			const floatx4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
 			floatx4 blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-				__builtin_bit_cast(half8_t, a[2 * h]), bq, z, 0, 0, 0);
+				__builtin_bit_cast(half8_t, s_hi[b][g][r]), bq, zero, 0, 0, 0);
 			blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-				__builtin_bit_cast(half8_t, a[2 * h + 1]), bq, blk, 0, 0, 0);
-			const float4 s = ts[h];
+				__builtin_bit_cast(half8_t, s_lo[b][g][r]), bq, blk, 0, 0, 0);
+			const float4 s = *(const float4 *)&s_ts[b][4 * g];
 			acc[0] = __builtin_fmaf(d * s.x, blk[0], acc[0]);
 			acc[1] = __builtin_fmaf(d * s.y, blk[1], acc[1]);
 			acc[2] = __builtin_fmaf(d * s.z, blk[2], acc[2]);
 			acc[3] = __builtin_fmaf(d * s.w, blk[3], acc[3]);
 		}
-		if (p + 1 < PPW) {
-#pragma unroll
-			for (int k = 0; k < 4; k++)
-				a[k] = an[k];
-			ts[0] = tn[0];
-			ts[1] = tn[1];
-		}
-	}
-	/* the quarters of K in wave order */
-	if (wave > 0)
-		red[wave - 1][lane] = acc;
-	__syncthreads();
-	if (wave > 0)
-		return;
-#pragma unroll
-	for (int v = 0; v < QMM_WAVES - 1; v++) {
-		const floatx4 o = red[v][lane];
-		acc[0] += o[0];
-		acc[1] += o[1];
-		acc[2] += o[2];
-		acc[3] += o[3];
+		/* one pair at a time: left to itself the scheduler issued every
+		 * MFMA first and held all 64 results (256 AGPRs: one wave per
+		 * SIMD) */
+		__builtin_amdgcn_sched_barrier(0);
 	}
 	if (n >= N)
 		return;
 #pragma unroll
 	for (int j = 0; j < 4; j++) {
 		const int t = t0 + 4 * g + j;
-		if (t < T) {
-			const size_t o = (size_t)t * N + n;
+		if (t >= T)
+			continue;
+		const size_t o = (size_t)t * N + n;
+		if (gridDim.z == 1)
 			out[o] = (add ? add[add_rows ? o : (size_t)n] : 0.0f) + acc[j];
-		}
+		else
+			part[(size_t)z * T * N + o] = acc[j];
 	}
+}
+
+/* out = add + the stretches' partial sums, added in stretch order */
+__global__ __launch_bounds__(256) void k_qmm_reduce(const float *__restrict__ part, int KS,
+						     size_t TN, int N, const float *__restrict__ add,
+						     int add_rows, float *__restrict__ out)
+{
+	const size_t o = (size_t)blockIdx.x * 256 + threadIdx.x;
+	if (o >= TN)
+		return;
+	float s = part[o];
+	for (int k = 1; k < KS; k++)
+		s += part[(size_t)k * TN + o];
+	out[o] = (add ? add[add_rows ? o : o % (size_t)N] : 0.0f) + s;
 }
 
 /* ---------------------------------------------------------------------- */
 /* host                                                                    */
 /* ---------------------------------------------------------------------- */
 
+static int qmm_pz(int K)
+{
+	return K / 64 < QMM_PZ ? K / 64 : QMM_PZ;
+}
+
 extern "C" int moe_qmm_supported(int wtype, int K)
 {
 	return (wtype == 1 || wtype == 2) && K >= 256 && K % 256 == 0 &&
-	       K / 256 <= QMM_MAX_PPW && ((K / 256) & (K / 256 - 1)) == 0;
+	       (K <= 64 * QMM_PZ ? ((K / 256) & (K / 256 - 1)) == 0 : K % (64 * QMM_PZ) == 0);
 }
 
-extern "C" size_t moe_qmm_split_bytes(int T, int K)
+/* the partial sums of a call with K longer than one stretch */
+extern "C" size_t moe_qmm_work_bytes(int T, int N, int K)
 {
-	const size_t TP = (size_t)(T + QMM_TOK - 1) / QMM_TOK * QMM_TOK;
-	return TP * (size_t)(K / 32) * 128 + (size_t)(K / 32) * TP * sizeof(float);
+	const int KS = K / (64 * qmm_pz(K));
+	return KS > 1 ? (size_t)KS * T * N * sizeof(float) : 0;
 }
 
-extern "C" int moe_launch_qmm_split(int wtype, const float *x, int T, int K, void *split,
-				    void *stream)
+extern "C" int moe_launch_qmm(int wtype, const uint8_t *W, int N, int K, const float *x, int T,
+			      const float *add, int add_rows, float *out, void *work,
+			      void *stream)
 {
-	if (!moe_qmm_supported(wtype, K) || T < 1)
+	if (!moe_qmm_supported(wtype, K) || N < 1 || T < 1 || (size_t)T * N > 0xffffffffull)
 		return (int)hipErrorInvalidValue;
-	const int TP = (T + QMM_TOK - 1) / QMM_TOK * QMM_TOK, nb = K / 32;
-	uint4 *xs = (uint4 *)split;
-	float *tsc = (float *)((uint8_t *)split + (size_t)TP * nb * 128);
-	const int nthr = TP * nb * 4; /* a multiple of 256: TP % 16 == 0, nb % 8 == 0 */
+	const int PZ = qmm_pz(K), KS = K / (64 * PZ);
+	if ((T + QMM_TOK - 1) / QMM_TOK > 65535 || (KS > 1 && !work))
+		return (int)hipErrorInvalidValue;
+	const size_t rb = (size_t)(K / 32) * (wtype == 1 ? 34 : 18);
+	const dim3 grid((N + QMM_WAVES * QMM_ROWS - 1) / (QMM_WAVES * QMM_ROWS),
+			(T + QMM_TOK - 1) / QMM_TOK, KS),
+		blk(QMM_WAVES * WAVE);
 	hipStream_t s = (hipStream_t)stream;
-	if (wtype == 1)
-		hipLaunchKernelGGL(k_qmm_split<1>, dim3(nthr / 256), dim3(256), 0, s, x, T, TP, K, xs,
-				   tsc);
-	else
-		hipLaunchKernelGGL(k_qmm_split<2>, dim3(nthr / 256), dim3(256), 0, s, x, T, TP, K, xs,
-				   tsc);
-	return (int)hipGetLastError();
-}
-
-extern "C" int moe_launch_qmm(int wtype, const uint8_t *W, int N, int K, const void *split,
-			      int T, const float *add, int add_rows, float *out, void *stream)
-{
-	if (!moe_qmm_supported(wtype, K) || N < 1 || T < 1 || N > 16 * 65535)
-		return (int)hipErrorInvalidValue;
-	const int TP = (T + QMM_TOK - 1) / QMM_TOK * QMM_TOK, nb = K / 32;
-	if (TP / QMM_TOK > 65535)
-		return (int)hipErrorInvalidValue;
-	const uint4 *xs = (const uint4 *)split;
-	const float *tsc = (const float *)((const uint8_t *)split + (size_t)TP * nb * 128);
-	const size_t rb = (size_t)nb * (wtype == 1 ? 34 : 18);
-	const dim3 grid((N + QMM_ROWS - 1) / QMM_ROWS, TP / QMM_TOK), blk(QMM_WAVES * WAVE);
-	hipStream_t s = (hipStream_t)stream;
+	float *part = (float *)work;
+	bool done = false;
 #define QMM(WTT, PP)                                                                        \
-	if (wtype == WTT && K / 256 == PP) {                                                \
-		hipLaunchKernelGGL((k_qmm<WTT, PP>), grid, blk, 0, s, W, rb, N, K, xs, tsc, T, TP, \
-				   add, add_rows, out);                                     \
-		return (int)hipGetLastError();                                              \
+	if (!done && wtype == WTT && PZ == PP) {                                            \
+		hipLaunchKernelGGL((k_qmm<WTT, PP>), grid, blk, 0, s, W, rb, N, K, x, T, add,   \
+				   add_rows, out, part);                                    \
+		done = true;                                                                \
 	}
-	QMM(1, 1) QMM(1, 2) QMM(1, 4) QMM(1, 8) QMM(1, 16)
-	QMM(2, 1) QMM(2, 2) QMM(2, 4) QMM(2, 8) QMM(2, 16)
+	QMM(1, 4) QMM(1, 8)
+	QMM(2, 4) QMM(2, 8)
 #undef QMM
-	return (int)hipErrorInvalidValue;
+	if (!done)
+		return (int)hipErrorInvalidValue;
+	if (KS > 1) {
+		const size_t TN = (size_t)T * N;
+		hipLaunchKernelGGL(k_qmm_reduce, dim3((unsigned)((TN + 255) / 256)), dim3(256), 0, s,
+				   part, KS, TN, N, add, add_rows, out);
+	}
+	return (int)hipGetLastError();
 }
