@@ -286,10 +286,24 @@ def bench_model(args, w, H):
         prompts = np.stack([prompt] + [hiplm.synth_prompt(SEED + 1 + q, w["prompt"], V)
                                        for q in range(1, nseq)])
         Bt = hiplm.LmBatch(M, nseq)
-        Bt.generate(prompts[:, :16], warm)
-        Bt.reset()
-        log(f"{nseq} sequences: {w['prompt']} prompt steps, then {steps} timed")
-        toks, ms = Bt.generate(prompts, steps)
+        if args.eager:
+            # for kernel traces (the profiler's trace of replayed step graphs
+            # fails): the same steps launched one kernel at a time, each step
+            # synchronised by the host-pointer entry point
+            log(f"{nseq} sequences, eager: {w['prompt']} prompt steps, then {steps} timed")
+            for i in range(w["prompt"]):
+                nxt, _ = Bt.decode(prompts[:, i])
+            for i in range(warm):
+                nxt, _ = Bt.decode(nxt)
+            t1 = time.perf_counter()
+            for i in range(steps):
+                nxt, _ = Bt.decode(nxt)
+            ms = (time.perf_counter() - t1) * 1e3
+        else:
+            Bt.generate(prompts[:, :16], warm)
+            Bt.reset()
+            log(f"{nseq} sequences: {w['prompt']} prompt steps, then {steps} timed")
+            toks, ms = Bt.generate(prompts, steps)
         Bt.free()
     ms_per_step = ms / steps
     tokens_per_s = nseq * steps / (ms / 1e3)
@@ -325,7 +339,7 @@ def bench_model(args, w, H):
                    "context": Cx,
                    "weights": {hipmoe.Q8_0: "Q8_0", hipmoe.Q4_0: "Q4_0", hipmoe.Q4_K: "Q4_K",
                                hipmoe.Q6_K: "Q6_K"}[wt],
-                   "prompt_tokens": w["prompt"], "sequences": nseq, "graphs": True,
+                   "prompt_tokens": w["prompt"], "sequences": nseq, "graphs": not args.eager,
                    "mean_unique_experts": round(mean_uniq, 3),
                    "algorithmic_bytes_per_step": int(bytes_per_step)},
         "roofline": {"bound": "hbm", "kernel": "decode_step", "achieved": round(achieved_gbs, 1),

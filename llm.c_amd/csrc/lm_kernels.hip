@@ -7,7 +7,7 @@
  *                 rms_norm (nn.c:8-51) into LDS by every workgroup, then the
  *                 one-token product with the stacked [q; k; v] matrix
  *                 (olmoe.c:448-450)
- *   k_lm_attn     one (head, chunk of cache positions): the full-vector
+ *   k_lm_attn     one (kv head, chunk of cache positions): the full-vector
  *                 RMSNorm of q and k (olmoe.c:454-458), RoPE on consecutive
  *                 pairs (rope_apply, nn.c:192-219), the new k/v row into the
  *                 cache (olmoe.c:240-262), then scores / sqrt(HLEN), the
@@ -244,17 +244,23 @@ void k_lm_qkv(const uint8_t *__restrict__ W, size_t rb, int N, int K, const floa
  * olmoe.c:295) or q . k * scale (Mixtral's flash_attention, scale =
  * 1 / sqrt(HLEN), nn.c:578) as scale_mul says.
  *
- * Grid (H, nact, sequences): nact = the chunks of LM_CHUNK rows that cover the cache
- * rows [lo, AT), AT = size + 1 (lo > 0 past a sliding window), which the
- * host knows for every step.  Workgroup (h, c) covers rows [j0, j0 + n);
- * the row `size` is this step's k and v, which the chunk holding it takes
- * from LDS (the workgroup of the kv head's first query head also writes it
- * to the cache).  Scores: 4 threads per position, 32 dims each; v sums: one
- * dim per thread over half the positions.  One chunk writes
- * out[h] = o / l itself; with more, partials part[h][c] = {m, l, o[HL]}
- * (stride nstride chunks) go out tagged, and the last of the head's chunks
- * merges them: out[h][d] = sum_c exp(m_c - M) o_c[d] / sum_c exp(m_c - M) l_c.
+ * Grid (KH, nact, sequences): nact = the chunks of LM_CHUNK rows that cover
+ * the cache rows [lo, AT), AT = size + 1 (lo > 0 past a sliding window),
+ * which the host knows for every step.  Workgroup (kh, c) takes the G = H /
+ * KH query heads of kv head kh (grouped-query attention, llama.c:286-288:
+ * head h reads kv head h / G) over rows [j0, j0 + n), so each k and v row
+ * is read once for its G heads; the row `size` is this step's k and v,
+ * which the chunk holding it takes from LDS (and writes to the cache).
+ * Scores: 4 threads per position, 32 dims each, all G heads from one read
+ * of the row; softmax: wave g % NW takes head g (lane = position); v sums:
+ * one dim per thread over half the positions, G heads from one read.  One
+ * chunk writes out[h] = o / l itself; with more, partials part[h][c] =
+ * {m, l, o[HL]} (stride nstride chunks) go out tagged, and the last of kv
+ * head kh's chunks merges its G heads: out[h][d] = sum_c exp(m_c - M)
+ * o_c[d] / sum_c exp(m_c - M) l_c.  Every head's arithmetic is the same
+ * whatever G.
  */
+template <int G>
 __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv,
 						   const float *__restrict__ q_norm,
 						   const float *__restrict__ k_norm,
@@ -264,13 +270,15 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 						   int H, int KH, int C, int window, float scale,
 						   int scale_mul, int layer, int nstride, size_t cstride)
 {
-	constexpr int HL = LM_HLEN, CH = LM_CHUNK;
-	__shared__ float cs[HL / 2], sn[HL / 2], sq[HL], sk[HL], sv[HL], sp[CH], so[LM_NT];
-	__shared__ float red[LM_NT / WAVE];
+	constexpr int HL = LM_HLEN, CH = LM_CHUNK, NW = LM_NT / WAVE;
+	__shared__ float cs[HL / 2], sn[HL / 2], sq[G][HL], sk[HL], sv[HL], sp[G][CH];
+	__shared__ float so[G][LM_NT];
+	__shared__ float red[NW];
 	__shared__ float s_f[LM_MAX_CHUNKS], s_l[LM_MAX_CHUNKS];
+	__shared__ float s_m[G], s_sum[G];
 	__shared__ int s_flag;
-	const int h = blockIdx.x, c = blockIdx.y, nact = gridDim.y;
-	const int G = H / KH, kh = h / G;
+	const int kh = blockIdx.x, c = blockIdx.y, nact = gridDim.y;
+	const int h0 = kh * G; /* the group's first query head */
 	const int EQ = H * HL, EK = KH * HL;
 	{ /* sequence blockIdx.z of several decoding in lockstep: its q/k/v row,
 	   * cache, partials, counters and output row */
@@ -283,16 +291,25 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 		out += sq * (size_t)EQ;
 	}
 	const float *q = qkv, *k = qkv + EQ, *v = qkv + EQ + EK;
-	const int tid = threadIdx.x;
+	const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
 
 	/* every load that does not depend on the counters goes out first */
-	float qx = 0.0f, kx = 0.0f, vx = 0.0f, qw = 1.0f, kw = 1.0f, fr = 0.0f;
+	float qx[G], qw[G], kx = 0.0f, vx = 0.0f, kw = 1.0f, fr = 0.0f;
+#pragma unroll
+	for (int g = 0; g < G; g++) {
+		qx[g] = 0.0f;
+		qw[g] = 1.0f;
+	}
 	if (tid < HL) {
-		qx = q[h * HL + tid];
+#pragma unroll
+		for (int g = 0; g < G; g++)
+			qx[g] = q[(h0 + g) * HL + tid];
 		kx = k[kh * HL + tid];
 		vx = v[kh * HL + tid];
 		if (q_norm) {
-			qw = q_norm[h * HL + tid];
+#pragma unroll
+			for (int g = 0; g < G; g++)
+				qw[g] = q_norm[(h0 + g) * HL + tid];
 			kw = k_norm[kh * HL + tid];
 		}
 	}
@@ -327,131 +344,184 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 	if (q_norm) {
 		const float rq = sqrtf(block_sum(s1, red) / (float)EQ + 1e-5f);
 		const float rk = sqrtf(block_sum(s2, red) / (float)EK + 1e-5f);
-		const float r = qx / rq, t = kx / rk;
-		qx = r * qw;
+#pragma unroll
+		for (int g = 0; g < G; g++) {
+			const float r = qx[g] / rq;
+			qx[g] = r * qw[g];
+		}
+		const float t = kx / rk;
 		kx = t * kw;
 	}
 	if (tid < HL) {
-		sq[tid] = qx;
+#pragma unroll
+		for (int g = 0; g < G; g++)
+			sq[g][tid] = qx[g];
 		sk[tid] = kx;
 		sv[tid] = vx;
 	}
 	__syncthreads();
-	if (tid < HL / 2) { /* x0' = x0 cos - x1 sin, x1' = x0 sin + x1 cos (one FMA each) */
-		const float co = cs[tid], si = sn[tid];
-		float x0 = sq[2 * tid], x1 = sq[2 * tid + 1];
-		sq[2 * tid] = __builtin_fmaf(x0, co, -(x1 * si));
-		sq[2 * tid + 1] = __builtin_fmaf(x0, si, x1 * co);
-		x0 = sk[2 * tid];
-		x1 = sk[2 * tid + 1];
-		sk[2 * tid] = __builtin_fmaf(x0, co, -(x1 * si));
-		sk[2 * tid + 1] = __builtin_fmaf(x0, si, x1 * co);
+	/* x0' = x0 cos - x1 sin, x1' = x0 sin + x1 cos (one FMA each): pair i
+	 * of head g is item g * HL / 2 + i, k's the last HL / 2 items */
+	for (int it = tid; it < (G + 1) * (HL / 2); it += LM_NT) {
+		const int g = it / (HL / 2), i = it % (HL / 2);
+		float *x = g < G ? sq[g] : sk;
+		const float co = cs[i], si = sn[i];
+		const float x0 = x[2 * i], x1 = x[2 * i + 1];
+		x[2 * i] = __builtin_fmaf(x0, co, -(x1 * si));
+		x[2 * i + 1] = __builtin_fmaf(x0, si, x1 * co);
 	}
 	__syncthreads();
 	const int jn = size - j0; /* the new row's place in this chunk, if 0 <= jn < n */
-	if (jn >= 0 && jn < n && h % G == 0 && tid < HL) {
+	if (jn >= 0 && jn < n && tid < HL) {
 		kc[((size_t)kh * C + size) * HL + tid] = sk[tid];
 		vc[((size_t)kh * C + size) * HL + tid] = sv[tid];
 	}
 	const float *K = kc + ((size_t)kh * C + j0) * HL, *V = vc + ((size_t)kh * C + j0) * HL;
 	{
 		const int j = tid / 4, d0 = (tid % 4) * 32;
-		float acc = 0.0f;
+		float acc[G];
+#pragma unroll
+		for (int g = 0; g < G; g++)
+			acc[g] = 0.0f;
 		if (j < n) {
+			float kr[32];
 			if (j == jn) {
 #pragma unroll
 				for (int u = 0; u < 32; u++)
-					acc = __builtin_fmaf(sq[d0 + u], sk[d0 + u], acc);
+					kr[u] = sk[d0 + u];
 			} else {
 				const float4 *k4 = (const float4 *)(K + (size_t)j * HL + d0);
 #pragma unroll
 				for (int u = 0; u < 8; u++) {
 					const float4 kv = k4[u];
-					acc = __builtin_fmaf(sq[d0 + 4 * u + 0], kv.x, acc);
-					acc = __builtin_fmaf(sq[d0 + 4 * u + 1], kv.y, acc);
-					acc = __builtin_fmaf(sq[d0 + 4 * u + 2], kv.z, acc);
-					acc = __builtin_fmaf(sq[d0 + 4 * u + 3], kv.w, acc);
+					kr[4 * u + 0] = kv.x;
+					kr[4 * u + 1] = kv.y;
+					kr[4 * u + 2] = kv.z;
+					kr[4 * u + 3] = kv.w;
 				}
 			}
+#pragma unroll
+			for (int g = 0; g < G; g++)
+#pragma unroll
+				for (int u = 0; u < 32; u++)
+					acc[g] = __builtin_fmaf(sq[g][d0 + u], kr[u], acc[g]);
 		}
-		acc += __shfl_xor(acc, 1, WAVE);
-		acc += __shfl_xor(acc, 2, WAVE);
-		if (tid % 4 == 0)
-			sp[j] = j < n ? (scale_mul ? acc * scale : acc / scale) : -INFINITY;
+#pragma unroll
+		for (int g = 0; g < G; g++) {
+			float a = acc[g];
+			a += __shfl_xor(a, 1, WAVE);
+			a += __shfl_xor(a, 2, WAVE);
+			if (tid % 4 == 0)
+				sp[g][j] = j < n ? (scale_mul ? a * scale : a / scale) : -INFINITY;
+		}
 	}
 	__syncthreads();
-	const float m = block_max(tid < CH ? sp[tid] : -INFINITY, red);
-	float e = 0.0f;
-	if (tid < CH) {
-		e = tid < n ? moe_expf(sp[tid] - m) : 0.0f;
-		sp[tid] = e;
+	/* softmax of head g on wave g % NW, lane = position (the wave's xor
+	 * trees: the same sums as a workgroup-wide reduction whose other waves
+	 * add zeros) */
+	for (int g = wave; g < G; g += NW) {
+		float mv = sp[g][lane];
+		for (int o2 = WAVE / 2; o2 > 0; o2 >>= 1)
+			mv = fmaxf(mv, __shfl_xor(mv, o2, WAVE));
+		const float e = lane < n ? moe_expf(sp[g][lane] - mv) : 0.0f;
+		sp[g][lane] = e;
+		float sv2 = e;
+		for (int o2 = WAVE / 2; o2 > 0; o2 >>= 1)
+			sv2 += __shfl_xor(sv2, o2, WAVE);
+		if (lane == 0) {
+			s_m[g] = mv;
+			s_sum[g] = sv2;
+		}
 	}
-	const float l = block_sum(e, red); /* its barriers also publish sp */
+	__syncthreads();
 	{
 		const int d = tid % HL, half = tid / HL;
-		float o = 0.0f;
-		for (int j = half; j < n; j += LM_NT / HL)
-			o = __builtin_fmaf(sp[j], j == jn ? sv[d] : V[(size_t)j * HL + d], o);
-		so[tid] = o;
+		float o[G];
+#pragma unroll
+		for (int g = 0; g < G; g++)
+			o[g] = 0.0f;
+#pragma unroll 4
+		for (int j = half; j < n; j += LM_NT / HL) {
+			const float vj = j == jn ? sv[d] : V[(size_t)j * HL + d];
+#pragma unroll
+			for (int g = 0; g < G; g++)
+				o[g] = __builtin_fmaf(sp[g][j], vj, o[g]);
+		}
+#pragma unroll
+		for (int g = 0; g < G; g++)
+			so[g][tid] = o[g];
 	}
 	__syncthreads();
-	float o = 0.0f;
+	float o[G];
 	if (tid < HL) {
-		o = so[tid];
-		for (int u = 1; u < LM_NT / HL; u++)
-			o += so[tid + u * HL];
+#pragma unroll
+		for (int g = 0; g < G; g++) {
+			o[g] = so[g][tid];
+			for (int u = 1; u < LM_NT / HL; u++)
+				o[g] += so[g][tid + u * HL];
+		}
 	}
 	if (nact == 1) { /* the whole context in one chunk: no merge */
 		if (tid < HL)
-			out[h * HL + tid] = o / l;
+#pragma unroll
+			for (int g = 0; g < G; g++)
+				out[(h0 + g) * HL + tid] = o[g] / s_sum[g];
 		return;
 	}
-	uint64_t *pp = part + ((size_t)h * nstride + c) * (HL + 2);
-	if (tid < HL)
-		st_dev_u64(&pp[2 + tid], tagged(tag, o));
-	if (tid == 0) {
-		st_dev_u64(&pp[0], tagged(tag, n > 0 ? m : -INFINITY));
-		st_dev_u64(&pp[1], tagged(tag, l));
-	}
-	if (!last_to_arrive(&cnt[h], (u32)nact, &s_flag))
-		return;
-	/* merge the head's nact chunks */
-	const uint64_t *ph = part + (size_t)h * nstride * (HL + 2);
-	gather_tagged(ph, HL + 2, nact, tag, st,
-		      [&](int cc, u32 b) { s_f[cc] = __builtin_bit_cast(float, b); });
-	gather_tagged(ph + 1, HL + 2, nact, tag, st,
-		      [&](int cc, u32 b) { s_l[cc] = __builtin_bit_cast(float, b); });
-	__syncthreads();
-	float M = -INFINITY;
-	for (int cc = 0; cc < nact; cc++)
-		M = fmaxf(M, s_f[cc]);
-	__syncthreads();
-	for (int cc = tid; cc < nact; cc += LM_NT)
-		s_f[cc] = s_l[cc] > 0.0f ? moe_expf(s_f[cc] - M) : 0.0f;
-	__syncthreads();
-	if (tid < HL) {
-		float L = 0.0f, acc = 0.0f;
-		for (int c0 = 0; c0 < nact; c0 += 8) {
-			/* eight loads in flight, then a poll only for a late one */
-			uint64_t vv[8];
 #pragma unroll
-			for (int u = 0; u < 8; u++)
-				vv[u] = c0 + u < nact ? ld_dev_u64(&ph[(size_t)(c0 + u) * (HL + 2) + 2 + tid])
-						      : 0;
-#pragma unroll
-			for (int u = 0; u < 8; u++) {
-				const int cc = c0 + u;
-				if (cc >= nact)
-					break;
-				const u32 ob = (u32)(vv[u] >> 32) == tag
-						       ? (u32)vv[u]
-						       : poll_tag(&ph[(size_t)cc * (HL + 2) + 2 + tid], tag, st);
-				const float f = s_f[cc];
-				L = __builtin_fmaf(f, s_l[cc], L);
-				acc = __builtin_fmaf(f, __builtin_bit_cast(float, ob), acc);
-			}
+	for (int g = 0; g < G; g++) {
+		uint64_t *pp = part + ((size_t)(h0 + g) * nstride + c) * (HL + 2);
+		if (tid < HL)
+			st_dev_u64(&pp[2 + tid], tagged(tag, o[g]));
+		if (tid == 0) {
+			st_dev_u64(&pp[0], tagged(tag, n > 0 ? s_m[g] : -INFINITY));
+			st_dev_u64(&pp[1], tagged(tag, s_sum[g]));
 		}
-		out[h * HL + tid] = acc / L;
+	}
+	if (!last_to_arrive(&cnt[kh], (u32)nact, &s_flag))
+		return;
+	/* merge the nact chunks of each of the G heads */
+	for (int g = 0; g < G; g++) {
+		const uint64_t *ph = part + (size_t)(h0 + g) * nstride * (HL + 2);
+		gather_tagged(ph, HL + 2, nact, tag, st,
+			      [&](int cc, u32 b) { s_f[cc] = __builtin_bit_cast(float, b); });
+		gather_tagged(ph + 1, HL + 2, nact, tag, st,
+			      [&](int cc, u32 b) { s_l[cc] = __builtin_bit_cast(float, b); });
+		__syncthreads();
+		float M = -INFINITY;
+		for (int cc = 0; cc < nact; cc++)
+			M = fmaxf(M, s_f[cc]);
+		__syncthreads();
+		for (int cc = tid; cc < nact; cc += LM_NT)
+			s_f[cc] = s_l[cc] > 0.0f ? moe_expf(s_f[cc] - M) : 0.0f;
+		__syncthreads();
+		if (tid < HL) {
+			float L = 0.0f, acc = 0.0f;
+			for (int c0 = 0; c0 < nact; c0 += 8) {
+				/* eight loads in flight, then a poll only for a late one */
+				uint64_t vv[8];
+#pragma unroll
+				for (int u = 0; u < 8; u++)
+					vv[u] = c0 + u < nact
+							? ld_dev_u64(&ph[(size_t)(c0 + u) * (HL + 2) + 2 + tid])
+							: 0;
+#pragma unroll
+				for (int u = 0; u < 8; u++) {
+					const int cc = c0 + u;
+					if (cc >= nact)
+						break;
+					const u32 ob =
+						(u32)(vv[u] >> 32) == tag
+							? (u32)vv[u]
+							: poll_tag(&ph[(size_t)cc * (HL + 2) + 2 + tid], tag, st);
+					const float f = s_f[cc];
+					L = __builtin_fmaf(f, s_l[cc], L);
+					acc = __builtin_fmaf(f, __builtin_bit_cast(float, ob), acc);
+				}
+			}
+			out[(h0 + g) * HL + tid] = acc / L;
+		}
+		__syncthreads(); /* s_f and s_l are rewritten for the next head */
 	}
 }
 
@@ -762,9 +832,20 @@ extern "C" int lm_launch_attn(const float *qkv, const float *q_norm, const float
 	if (KH < 1 || H % KH || nch > LM_MAX_CHUNKS || nact < 1 || nact > nch || layer < 0 ||
 	    layer >= LM_HEAD_SLOT || nseq < 1 || nseq > 65535)
 		return (int)hipErrorInvalidValue;
-	hipLaunchKernelGGL(k_lm_attn, dim3(H, nact, nseq), dim3(LM_NT), 0, (hipStream_t)stream,
-			   qkv, q_norm, k_norm, freq, st, kc, vc, part, cnt, out, H, KH, C, window,
-			   scale, scale_mul, layer, nch, cstride);
+	const dim3 grid(KH, nact, nseq);
+	hipStream_t s = (hipStream_t)stream;
+#define ATTN(GG)                                                                            \
+	hipLaunchKernelGGL(k_lm_attn<GG>, grid, dim3(LM_NT), 0, s, qkv, q_norm, k_norm, freq,   \
+			   st, kc, vc, part, cnt, out, H, KH, C, window, scale, scale_mul, layer,  \
+			   nch, cstride)
+	switch (H / KH) {
+	case 1: ATTN(1); break;
+	case 2: ATTN(2); break;
+	case 4: ATTN(4); break;
+	case 8: ATTN(8); break;
+	default: return (int)hipErrorInvalidValue;
+	}
+#undef ATTN
 	return (int)hipGetLastError();
 }
 
