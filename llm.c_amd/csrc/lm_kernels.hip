@@ -251,6 +251,8 @@ void k_lm_qkv(const uint8_t *__restrict__ W, size_t rb, int N, int K, const floa
  * head h reads kv head h / G) over rows [j0, j0 + n), so each k and v row
  * is read once for its G heads; the row `size` is this step's k and v,
  * which the chunk holding it takes from LDS (and writes to the cache).
+ * The cached k and v rows of the chunk are loaded as soon as the cache size
+ * is known, so they arrive while q and k are normalised and rotated.
  * Scores: 4 threads per position, 32 dims each, all G heads from one read
  * of the row; softmax: wave g % NW takes head g (lane = position); v sums:
  * one dim per thread over half the positions, G heads from one read.  One
@@ -260,7 +262,7 @@ void k_lm_qkv(const uint8_t *__restrict__ W, size_t rb, int N, int K, const floa
  * o_c[d] / sum_c exp(m_c - M) l_c.  Every head's arithmetic is the same
  * whatever G.
  */
-template <int G>
+template <int G, bool PF>
 __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv,
 						   const float *__restrict__ q_norm,
 						   const float *__restrict__ k_norm,
@@ -335,6 +337,40 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 	/* olmoe_decode: a position past the context is the cache size
 	 * (olmoe.c:514-515) */
 	const int pos = spos < C ? spos : size;
+	const int jn = size - j0; /* the new row's place in this chunk, if 0 <= jn < n */
+	const float *K = kc + ((size_t)kh * C + j0) * HL, *V = vc + ((size_t)kh * C + j0) * HL;
+	/* the chunk's cached k and v rows (all but the new one): thread (j =
+	 * tid / 4, d0) takes 32 dims of row j's k; thread (d, half) dim d of
+	 * rows half, half + 2, ... of v.  PF: they go out now, to arrive while
+	 * q and k are normalised and rotated (3 waves per SIMD instead of 7,
+	 * for grids that fit the device at once) */
+	const int jq = tid / 4, d0 = (tid % 4) * 32;
+	const int dv = tid % HL, half = tid / HL;
+	float kr[32], vr[CH / (LM_NT / HL)];
+	auto load_k = [&]() {
+		if (jq < n && jq != jn) {
+			const float4 *k4 = (const float4 *)(K + (size_t)jq * HL + d0);
+#pragma unroll
+			for (int u = 0; u < 8; u++) {
+				const float4 kv = k4[u];
+				kr[4 * u + 0] = kv.x;
+				kr[4 * u + 1] = kv.y;
+				kr[4 * u + 2] = kv.z;
+				kr[4 * u + 3] = kv.w;
+			}
+		}
+	};
+	auto load_v = [&]() {
+#pragma unroll
+		for (int i = 0; i < CH / (LM_NT / HL); i++) {
+			const int j = half + i * (LM_NT / HL);
+			vr[i] = j < n && j != jn ? V[(size_t)j * HL + dv] : 0.0f;
+		}
+	};
+	if constexpr (PF) {
+		load_k();
+		load_v();
+	}
 
 	if (tid < HL / 2) {
 		const float ang = (float)pos * fr;
@@ -371,34 +407,23 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 		x[2 * i + 1] = __builtin_fmaf(x0, si, x1 * co);
 	}
 	__syncthreads();
-	const int jn = size - j0; /* the new row's place in this chunk, if 0 <= jn < n */
 	if (jn >= 0 && jn < n && tid < HL) {
 		kc[((size_t)kh * C + size) * HL + tid] = sk[tid];
 		vc[((size_t)kh * C + size) * HL + tid] = sv[tid];
 	}
-	const float *K = kc + ((size_t)kh * C + j0) * HL, *V = vc + ((size_t)kh * C + j0) * HL;
+	if constexpr (!PF)
+		load_k();
 	{
-		const int j = tid / 4, d0 = (tid % 4) * 32;
+		const int j = jq;
 		float acc[G];
 #pragma unroll
 		for (int g = 0; g < G; g++)
 			acc[g] = 0.0f;
 		if (j < n) {
-			float kr[32];
 			if (j == jn) {
 #pragma unroll
 				for (int u = 0; u < 32; u++)
 					kr[u] = sk[d0 + u];
-			} else {
-				const float4 *k4 = (const float4 *)(K + (size_t)j * HL + d0);
-#pragma unroll
-				for (int u = 0; u < 8; u++) {
-					const float4 kv = k4[u];
-					kr[4 * u + 0] = kv.x;
-					kr[4 * u + 1] = kv.y;
-					kr[4 * u + 2] = kv.z;
-					kr[4 * u + 3] = kv.w;
-				}
 			}
 #pragma unroll
 			for (int g = 0; g < G; g++)
@@ -433,16 +458,20 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 			s_sum[g] = sv2;
 		}
 	}
+	if constexpr (!PF)
+		load_v();
 	__syncthreads();
 	{
-		const int d = tid % HL, half = tid / HL;
 		float o[G];
 #pragma unroll
 		for (int g = 0; g < G; g++)
 			o[g] = 0.0f;
-#pragma unroll 4
-		for (int j = half; j < n; j += LM_NT / HL) {
-			const float vj = j == jn ? sv[d] : V[(size_t)j * HL + d];
+#pragma unroll
+		for (int i = 0; i < CH / (LM_NT / HL); i++) {
+			const int j = half + i * (LM_NT / HL);
+			if (j >= n)
+				break;
+			const float vj = j == jn ? sv[dv] : vr[i];
 #pragma unroll
 			for (int g = 0; g < G; g++)
 				o[g] = __builtin_fmaf(sp[g][j], vj, o[g]);
@@ -761,6 +790,24 @@ static const void *lm_kernel(int kind, int wtype, int K)
 	return nullptr;
 }
 
+/* compute units of the current device (256 if the query fails), cached
+ * per device: the attention launch asks at every step, also under capture */
+static int lm_cus()
+{
+	static int cus[64];
+	int dev = 0, ncu = 0;
+	if (hipGetDevice(&dev) != hipSuccess)
+		return 256;
+	if (dev >= 0 && dev < 64 && cus[dev] > 0)
+		return cus[dev];
+	if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+	    ncu < 1)
+		return 256;
+	if (dev >= 0 && dev < 64)
+		__atomic_store_n(&cus[dev], ncu, __ATOMIC_RELAXED);
+	return ncu;
+}
+
 extern "C" int lm_gemv_grid(int kind, int wtype, int K, int N)
 {
 	const void *fn = lm_kernel(kind, wtype, K);
@@ -834,10 +881,19 @@ extern "C" int lm_launch_attn(const float *qkv, const float *q_norm, const float
 		return (int)hipErrorInvalidValue;
 	const dim3 grid(KH, nact, nseq);
 	hipStream_t s = (hipStream_t)stream;
-#define ATTN(GG)                                                                            \
-	hipLaunchKernelGGL(k_lm_attn<GG>, grid, dim3(LM_NT), 0, s, qkv, q_norm, k_norm, freq,   \
-			   st, kc, vc, part, cnt, out, H, KH, C, window, scale, scale_mul, layer,  \
-			   nch, cstride)
+	/* the early loads while the grid fits 3 workgroups per CU at once */
+	const bool pf = (size_t)KH * nact * nseq <= 3 * (size_t)lm_cus();
+#define ATTN(GG)                                                                               \
+	do {                                                                                   \
+		if (pf)                                                                        \
+			hipLaunchKernelGGL((k_lm_attn<GG, true>), grid, dim3(LM_NT), 0, s, qkv,   \
+					   q_norm, k_norm, freq, st, kc, vc, part, cnt, out, H, KH,   \
+					   C, window, scale, scale_mul, layer, nch, cstride);         \
+		else                                                                           \
+			hipLaunchKernelGGL((k_lm_attn<GG, false>), grid, dim3(LM_NT), 0, s, qkv,  \
+					   q_norm, k_norm, freq, st, kc, vc, part, cnt, out, H, KH,   \
+					   C, window, scale, scale_mul, layer, nch, cstride);         \
+	} while (0)
 	switch (H / KH) {
 	case 1: ATTN(1); break;
 	case 2: ATTN(2); break;
