@@ -278,7 +278,20 @@ def bench_model(args, w, H):
         tr = np.stack(traces[:nseq])  # [nseq][layers][K]
         mean_uniq = float(np.mean([len(np.unique(tr[:, l])) for l in range(Lh)]))
     M.reset()
-    if nseq == 1:
+    if nseq == 1 and args.eager:
+        # for kernel traces: the same steps launched one kernel at a time,
+        # each synchronised by the host-pointer entry point
+        log(f"eager: {w['prompt']} prompt steps, then {steps} timed")
+        tok = 0
+        for t in prompt:
+            tok, _ = M.decode(int(t))
+        for i in range(warm):
+            tok, _ = M.decode(tok)
+        t1 = time.perf_counter()
+        for i in range(steps):
+            tok, _ = M.decode(tok)
+        ms = (time.perf_counter() - t1) * 1e3
+    elif nseq == 1:
         M.generate(prompt[:16], warm)  # captures the step graphs of short contexts
         M.reset()
         toks, ms = M.generate(prompt, steps)

@@ -51,7 +51,8 @@ struct hip_lm {
 	uint64_t *d_part;   /* tagged attention partials [H][chunks][HL + 2] */
 	uint64_t *d_rows_t; /* tagged output-product rows [E] */
 	uint64_t *d_best;   /* tagged per-workgroup maxima of the lm_head [2 * grid] */
-	uint32_t *d_cnt;    /* arrival counters: [H] attention, output product, lm_head */
+	uint32_t *d_cnt;    /* arrival counters: [H] attention, then LM_ARRIVE_WORDS each for
+			     * the output product and the lm_head */
 	uint32_t *d_ids;   /* [L][K] */
 	float *d_w;        /* [L][K] */
 	LmState *d_st;
@@ -260,7 +261,7 @@ hip_lm *hip_lm_upload(const hip_lm_desc *d)
 	/* (the output product's last workgroup gathers E rows in the LDS that
 	 * staged its heads * 128 inputs) */
 	if (M->grid_qkv <= 0 || M->grid_o <= 0 || M->grid_head <= 0 ||
-	    M->grid_head > LM_MAX_HEAD_WG || E * 64 > M->EQ * 68) {
+	    M->grid_head > LM_MAX_HEAD_WG || M->grid_o > LM_MAX_HEAD_WG || E * 64 > M->EQ * 68) {
 		lm_err("lm_upload: E=%zu / heads*128=%zu not supported by the dense product", E,
 		       M->EQ);
 		goto fail;
@@ -342,8 +343,10 @@ hip_lm *hip_lm_upload(const hip_lm_desc *d)
 	HIPCHK(hipMalloc((void **)&M->d_best, 2 * LM_MAX_HEAD_WG * sizeof(uint64_t)),
 	       "hipMalloc(best)");
 	HIPCHK(hipMemset(M->d_best, 0, 2 * LM_MAX_HEAD_WG * sizeof(uint64_t)), "clear best");
-	HIPCHK(hipMalloc((void **)&M->d_cnt, (M->H + 2) * sizeof(uint32_t)), "hipMalloc(counters)");
-	HIPCHK(hipMemset(M->d_cnt, 0, (M->H + 2) * sizeof(uint32_t)), "clear counters");
+	HIPCHK(hipMalloc((void **)&M->d_cnt, (M->H + 2 * LM_ARRIVE_WORDS) * sizeof(uint32_t)),
+	       "hipMalloc(counters)");
+	HIPCHK(hipMemset(M->d_cnt, 0, (M->H + 2 * LM_ARRIVE_WORDS) * sizeof(uint32_t)),
+	       "clear counters");
 	HIPCHK(hipMalloc((void **)&M->d_logits, M->V * 4), "hipMalloc(logits)");
 	HIPCHK(hipMalloc((void **)&M->d_ids, M->L * M->K * 4), "hipMalloc(ids)");
 	HIPCHK(hipMalloc((void **)&M->d_w, M->L * M->K * 4), "hipMalloc(w)");
@@ -407,7 +410,8 @@ static int enqueue_step(hip_lm *M, int head, int nact)
 {
 	const int wt = M->wtype, E = (int)M->E, NQKV = (int)(M->EQ + 2 * M->EKV);
 	hipStream_t s = M->stream;
-	uint32_t *cnt_attn = M->d_cnt, *cnt_o = M->d_cnt + M->H, *cnt_head = cnt_o + 1;
+	uint32_t *cnt_attn = M->d_cnt, *cnt_o = M->d_cnt + M->H,
+		 *cnt_head = cnt_o + LM_ARRIVE_WORDS;
 	for (size_t l = 0; l < M->L; l++) {
 		struct lm_layer *y = &M->ly[l];
 		const size_t co = l * M->KH * M->C * M->HL;

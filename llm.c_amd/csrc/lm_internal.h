@@ -19,6 +19,10 @@ extern "C" {
 #define LM_TAG_SLOTS 64    /* gather tags: epoch * 64 + slot */
 #define LM_HEAD_SLOT 63    /* the lm_head's slot; layers use 0 .. 62 */
 #define LM_MAX_HEAD_WG 4096
+/* arrival counters of a one-token product of up to LM_MAX_HEAD_WG
+ * workgroups: groups of LM_ARRIVE_GROUP, then one for the groups */
+#define LM_ARRIVE_GROUP 32
+#define LM_ARRIVE_WORDS (1 + LM_MAX_HEAD_WG / LM_ARRIVE_GROUP)
 #define LM_ERR_GATHER 1    /* a gather's poll ran out */
 
 /* The step's counters in device memory, read by every step kernel so that

@@ -139,6 +139,36 @@ __device__ static inline bool last_to_arrive(u32 *cnt, u32 n, int *s_flag)
 	return *s_flag != 0;
 }
 
+/* the same for the n = gridDim.x workgroups of a wide grid: workgroup b
+ * counts in at cnt[1 + b / LM_ARRIVE_GROUP], the last of each group at
+ * cnt[0] (same-address device atomics serialise: one counter for 1024
+ * workgroups held the Mixtral output product at ~27 us); every counter is
+ * reset by its last arrival */
+__device__ static inline bool last_to_arrive_wide(u32 *cnt, int *s_flag)
+{
+	__syncthreads(); /* every thread's tagged stores are issued */
+	if (threadIdx.x == 0) {
+		const u32 n = gridDim.x, gi = blockIdx.x / LM_ARRIVE_GROUP;
+		const u32 gn = min((u32)LM_ARRIVE_GROUP, n - gi * LM_ARRIVE_GROUP);
+		int last = 0;
+		u32 old = __hip_atomic_fetch_add(&cnt[1 + gi], 1u, __ATOMIC_RELAXED,
+						 __HIP_MEMORY_SCOPE_AGENT);
+		if (old == gn - 1) {
+			__hip_atomic_store(&cnt[1 + gi], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+			const u32 ng = (n + LM_ARRIVE_GROUP - 1) / LM_ARRIVE_GROUP;
+			old = __hip_atomic_fetch_add(&cnt[0], 1u, __ATOMIC_RELAXED,
+						     __HIP_MEMORY_SCOPE_AGENT);
+			last = old == ng - 1;
+			if (last)
+				__hip_atomic_store(&cnt[0], 0u, __ATOMIC_RELAXED,
+						   __HIP_MEMORY_SCOPE_AGENT);
+		}
+		*s_flag = last;
+	}
+	__syncthreads();
+	return *s_flag != 0;
+}
+
 /* the step's token: the prompt's while it lasts, then the last pick */
 __device__ static inline int step_token(const LmState *st, const int *prompt)
 {
@@ -175,40 +205,76 @@ template <int WT>
 __device__ static void stage_norm(float *sx, float *red, int E, const float *a, const float *b,
 				  const uint8_t *emb, const float *w, float *h_out)
 {
+	/* NB float4s of a thread in flight at once (a loop that loaded one per
+	 * iteration waited a round trip each: h_out may alias a and b); w stays
+	 * in registers when one batch covers E */
+	constexpr int NB = 4;
+	const int n4 = E / 4;
+	const bool one = n4 <= NB * LM_NT;
+	float4 wv[NB];
 	float ss = 0.0f;
-	for (int c4 = threadIdx.x; c4 < E / 4; c4 += LM_NT) {
-		float4 v;
-		if (emb) {
-			v = dequant4<WT>(emb, c4);
-		} else {
-			v = ((const float4 *)a)[c4];
-			if (b) {
-				const float4 u = ((const float4 *)b)[c4];
-				v.x = v.x + u.x;
-				v.y = v.y + u.y;
-				v.z = v.z + u.z;
-				v.w = v.w + u.w;
+	for (int c0 = threadIdx.x; c0 < n4; c0 += NB * LM_NT) {
+		float4 v[NB], u[NB];
+#pragma unroll
+		for (int k = 0; k < NB; k++) {
+			const int c4 = c0 + k * LM_NT;
+			if (c4 >= n4)
+				break;
+			if (emb) {
+				v[k] = dequant4<WT>(emb, c4);
+			} else {
+				v[k] = ((const float4 *)a)[c4];
+				if (b)
+					u[k] = ((const float4 *)b)[c4];
 			}
+			if (one)
+				wv[k] = ((const float4 *)w)[c4];
 		}
-		if (h_out)
-			((float4 *)h_out)[c4] = v;
-		*(float4 *)(sx + (c4 >> 4) * SEG_STRIDE + (c4 & 15) * 4) = v;
-		const float q0 = v.x * v.x, q1 = v.y * v.y, q2 = v.z * v.z, q3 = v.w * v.w;
-		ss = ss + q0;
-		ss = ss + q1;
-		ss = ss + q2;
-		ss = ss + q3;
+#pragma unroll
+		for (int k = 0; k < NB; k++) {
+			const int c4 = c0 + k * LM_NT;
+			if (c4 >= n4)
+				break;
+			if (!emb && b) {
+				v[k].x = v[k].x + u[k].x;
+				v[k].y = v[k].y + u[k].y;
+				v[k].z = v[k].z + u[k].z;
+				v[k].w = v[k].w + u[k].w;
+			}
+			if (h_out)
+				((float4 *)h_out)[c4] = v[k];
+			*(float4 *)(sx + (c4 >> 4) * SEG_STRIDE + (c4 & 15) * 4) = v[k];
+			const float q0 = v[k].x * v[k].x, q1 = v[k].y * v[k].y;
+			const float q2 = v[k].z * v[k].z, q3 = v[k].w * v[k].w;
+			ss = ss + q0;
+			ss = ss + q1;
+			ss = ss + q2;
+			ss = ss + q3;
+		}
 	}
 	const float rms = sqrtf(block_sum(ss, red) / (float)E + 1e-5f);
-	for (int c4 = threadIdx.x; c4 < E / 4; c4 += LM_NT) {
-		float4 *p = (float4 *)(sx + (c4 >> 4) * SEG_STRIDE + (c4 & 15) * 4);
-		float4 v = *p;
-		const float4 wv = ((const float4 *)w)[c4];
-		v.x = (v.x / rms) * wv.x;
-		v.y = (v.y / rms) * wv.y;
-		v.z = (v.z / rms) * wv.z;
-		v.w = (v.w / rms) * wv.w;
-		*p = v;
+	for (int c0 = threadIdx.x; c0 < n4; c0 += NB * LM_NT) {
+		if (!one) {
+#pragma unroll
+			for (int k = 0; k < NB; k++) {
+				const int c4 = c0 + k * LM_NT;
+				if (c4 < n4)
+					wv[k] = ((const float4 *)w)[c4];
+			}
+		}
+#pragma unroll
+		for (int k = 0; k < NB; k++) {
+			const int c4 = c0 + k * LM_NT;
+			if (c4 >= n4)
+				break;
+			float4 *p = (float4 *)(sx + (c4 >> 4) * SEG_STRIDE + (c4 & 15) * 4);
+			float4 v = *p;
+			v.x = (v.x / rms) * wv[k].x;
+			v.y = (v.y / rms) * wv[k].y;
+			v.z = (v.z / rms) * wv[k].z;
+			v.w = (v.w / rms) * wv[k].w;
+			*p = v;
+		}
 	}
 	__syncthreads();
 }
@@ -576,8 +642,21 @@ void k_lm_oproj(const uint8_t *__restrict__ W, size_t rb, int N, int K,
 	const u32 tag = lm_tag(st, layer);
 	auto hook = [=](int row, float r) { st_dev_u64(&rows_t[row], tagged(tag, r)); };
 	qgemv_body<WT, C, true>(sx, W, rb, N, K, x, 1, 1, add, 0, out, hook);
-	if (!last_to_arrive(cnt, gridDim.x, &s_flag))
+	if (!last_to_arrive_wide(cnt, &s_flag))
 		return;
+	/* the norm weights of this thread's outputs, WB at a time, the first
+	 * batch loading while the rows are gathered (a loop of one load per
+	 * output waited a round trip each) */
+	constexpr int WB = 16;
+	float wv[WB];
+	auto load_w = [&](int i0) {
+#pragma unroll
+		for (int k = 0; k < WB; k++) {
+			const int i = i0 + k * LM_NT;
+			wv[k] = i < N ? w[i] : 0.0f;
+		}
+	};
+	load_w(threadIdx.x);
 	float ss = 0.0f;
 	gather_tagged(rows_t, 1, N, tag, st, [&](int i, u32 b) {
 		const float v = __builtin_bit_cast(float, b);
@@ -586,9 +665,17 @@ void k_lm_oproj(const uint8_t *__restrict__ W, size_t rb, int N, int K,
 		ss = ss + t;
 	});
 	const float rms = sqrtf(block_sum(ss, red) / (float)N + 1e-5f);
-	for (int i = threadIdx.x; i < N; i += LM_NT) {
-		const float r = sx[i] / rms;
-		x_out[i] = r * w[i];
+	for (int i0 = threadIdx.x; i0 < N; i0 += WB * LM_NT) {
+		if (i0 != (int)threadIdx.x)
+			load_w(i0);
+#pragma unroll
+		for (int k = 0; k < WB; k++) {
+			const int i = i0 + k * LM_NT;
+			if (i < N) {
+				const float r = sx[i] / rms;
+				x_out[i] = r * wv[k];
+			}
+		}
 	}
 }
 
@@ -642,7 +729,7 @@ void k_lm_head(const uint8_t *__restrict__ W, size_t rb, int N, int K, const flo
 		st_dev_u64(&best[2 * blockIdx.x], tagged(tag, bv));
 		st_dev_u64(&best[2 * blockIdx.x + 1], ((uint64_t)tag << 32) | (u32)bi);
 	}
-	if (!last_to_arrive(cnt, gridDim.x, &s_flag))
+	if (!last_to_arrive_wide(cnt, &s_flag))
 		return;
 	bv = -INFINITY;
 	bi = 0x7fffffff;
@@ -842,7 +929,7 @@ extern "C" int lm_launch_oproj(int wtype, const uint8_t *W, int N, int K, const 
 			       void *stream)
 {
 	const void *fn = lm_kernel(1, wtype, K);
-	if (!fn || grid < 1 || N > (int)(tok_lds(K) / sizeof(float)))
+	if (!fn || grid < 1 || grid > LM_MAX_HEAD_WG || N > (int)(tok_lds(K) / sizeof(float)))
 		return (int)hipErrorInvalidValue;
 	size_t rb = (size_t)(K / MOE_QK) * (wtype == 1 ? 34 : 18);
 	void *args[] = {&W, &rb, &N, &K, &x, &add, &out, &rows_t, &cnt, &w, &x_out, &st, &layer};
