@@ -51,8 +51,7 @@ struct hip_lm {
 	uint64_t *d_part;   /* tagged attention partials [H][chunks][HL + 2] */
 	uint64_t *d_rows_t; /* tagged output-product rows [E] */
 	uint64_t *d_best;   /* tagged per-workgroup maxima of the lm_head [2 * grid] */
-	uint32_t *d_cnt;    /* arrival counters: [H] attention, then LM_ARRIVE_WORDS each for
-			     * the output product and the lm_head */
+	uint32_t *d_cnt;    /* attention arrival counters [H] */
 	uint32_t *d_ids;   /* [L][K] */
 	float *d_w;        /* [L][K] */
 	LmState *d_st;
@@ -343,10 +342,8 @@ hip_lm *hip_lm_upload(const hip_lm_desc *d)
 	HIPCHK(hipMalloc((void **)&M->d_best, 2 * LM_MAX_HEAD_WG * sizeof(uint64_t)),
 	       "hipMalloc(best)");
 	HIPCHK(hipMemset(M->d_best, 0, 2 * LM_MAX_HEAD_WG * sizeof(uint64_t)), "clear best");
-	HIPCHK(hipMalloc((void **)&M->d_cnt, (M->H + 2 * LM_ARRIVE_WORDS) * sizeof(uint32_t)),
-	       "hipMalloc(counters)");
-	HIPCHK(hipMemset(M->d_cnt, 0, (M->H + 2 * LM_ARRIVE_WORDS) * sizeof(uint32_t)),
-	       "clear counters");
+	HIPCHK(hipMalloc((void **)&M->d_cnt, M->H * sizeof(uint32_t)), "hipMalloc(counters)");
+	HIPCHK(hipMemset(M->d_cnt, 0, M->H * sizeof(uint32_t)), "clear counters");
 	HIPCHK(hipMalloc((void **)&M->d_logits, M->V * 4), "hipMalloc(logits)");
 	HIPCHK(hipMalloc((void **)&M->d_ids, M->L * M->K * 4), "hipMalloc(ids)");
 	HIPCHK(hipMalloc((void **)&M->d_w, M->L * M->K * 4), "hipMalloc(w)");
@@ -410,8 +407,7 @@ static int enqueue_step(hip_lm *M, int head, int nact)
 {
 	const int wt = M->wtype, E = (int)M->E, NQKV = (int)(M->EQ + 2 * M->EKV);
 	hipStream_t s = M->stream;
-	uint32_t *cnt_attn = M->d_cnt, *cnt_o = M->d_cnt + M->H,
-		 *cnt_head = cnt_o + LM_ARRIVE_WORDS;
+	uint32_t *cnt_attn = M->d_cnt;
 	for (size_t l = 0; l < M->L; l++) {
 		struct lm_layer *y = &M->ly[l];
 		const size_t co = l * M->KH * M->C * M->HL;
@@ -426,7 +422,7 @@ static int enqueue_step(hip_lm *M, int head, int nact)
 				    M->arch != HIP_LM_OLMOE, (int)l, nact, 1, 0, s), "attention");
 		/* h1 = h0 + attn . Wo^T, moe_in = rms_norm(h1) */
 		LCHK(lm_launch_oproj(wt, y->wo, E, (int)M->EQ, M->d_attn, M->d_h0, M->d_h1,
-				     M->d_rows_t, cnt_o, y->ffn_norm, M->d_moe_in + l * M->E,
+				     M->d_rows_t, y->ffn_norm, M->d_moe_in + l * M->E,
 				     M->d_st, (int)l, M->grid_o, s), "output product + norm");
 		if (!hip_moe_ffn_dev(y->moe, M->d_moe_in + l * M->E, M->d_moe_out, 1, NULL,
 				     M->d_ids + l * M->K, M->d_w + l * M->K, s))
@@ -434,7 +430,7 @@ static int enqueue_step(hip_lm *M, int head, int nact)
 	}
 	if (head) /* logits = rms_norm(h1 + moe_out) . lm_head^T, pick, advance */
 		LCHK(lm_launch_head(wt, M->d_head, (int)M->V, E, M->d_h1, M->d_moe_out, M->d_onorm,
-				    M->d_logits, M->d_best, cnt_head, M->d_st, M->d_tokens,
+				    M->d_logits, M->d_best, M->d_st, M->d_tokens,
 				    M->grid_head, s), "lm_head + pick");
 	else
 		LCHK(lm_launch_step_end(M->d_st, s), "step end");

@@ -19,10 +19,7 @@ extern "C" {
 #define LM_TAG_SLOTS 64    /* gather tags: epoch * 64 + slot */
 #define LM_HEAD_SLOT 63    /* the lm_head's slot; layers use 0 .. 62 */
 #define LM_MAX_HEAD_WG 4096
-/* arrival counters of a one-token product of up to LM_MAX_HEAD_WG
- * workgroups: groups of LM_ARRIVE_GROUP, then one for the groups */
-#define LM_ARRIVE_GROUP 32
-#define LM_ARRIVE_WORDS (1 + LM_MAX_HEAD_WG / LM_ARRIVE_GROUP)
+
 #define LM_ERR_GATHER 1    /* a gather's poll ran out */
 
 /* The step's counters in device memory, read by every step kernel so that
@@ -69,14 +66,13 @@ static inline int lm_attn_active(int size, int window)
 /* out[N] = add + x . W^T, then x_out = rms_norm(out) * w (rows_t: N tagged
  * words, cnt one zeroed counter) */
 int lm_launch_oproj(int wtype, const uint8_t *W, int N, int K, const float *x,
-                    const float *add, float *out, uint64_t *rows_t, uint32_t *cnt,
-                    const float *w, float *x_out, LmState *st, int layer, int grid,
-                    void *stream);
+                    const float *add, float *out, uint64_t *rows_t, const float *w,
+                    float *x_out, LmState *st, int layer, int grid, void *stream);
 /* logits out[N] = rms_norm(a + b) * w . W^T, the greedy pick and the
  * counters' advance (best: 2 * grid tagged words, cnt one zeroed counter) */
 int lm_launch_head(int wtype, const uint8_t *W, int N, int K, const float *a, const float *b,
-                   const float *w, float *out, uint64_t *best, uint32_t *cnt, LmState *st,
-                   int *tokens, int grid, void *stream);
+                   const float *w, float *out, uint64_t *best, LmState *st, int *tokens,
+                   int grid, void *stream);
 int lm_launch_step_end(LmState *st, void *stream);
 /* nseq sequences in lockstep: x_out[s] = rms_norm(a[s] + b[s]) * w (b may
  * be NULL; a NULL: the embedding row of sequence s's step token, from

@@ -15,23 +15,26 @@
  *                 a head to finish merges the chunks into softmax . V
  *                 (olmoe.c:296-320, flash-decoding form)
  *   k_lm_oproj    the output product with the residual as its add operand
- *                 (olmoe.c:476-478); the last workgroup to finish computes
- *                 the pre-MoE rms_norm (olmoe.c:482) for the MoE layer
+ *                 (olmoe.c:476-478); workgroup 0 computes the pre-MoE
+ *                 rms_norm (olmoe.c:482) for the MoE layer
  *   k_lm_head     the residual add and the final rms_norm into LDS, the
  *                 lm_head product (olmoe.c:558-564), and the greedy pick
- *                 (main.c:189-193, the first maximum) by the last workgroup,
- *                 which also advances the step's counters
+ *                 (main.c:189-193, the first maximum) by workgroup 0, which
+ *                 also advances the step's counters
  *
  * Every kernel reads the step's token, position and cache row from the
  * device state block (LmState), so one captured HIP graph serves every step.
  *
- * Results that a last workgroup gathers from the others (attention
- * partials, the output product's rows, the workgroups' best logits) travel
- * as 64-bit words tagged with the step's epoch and the layer, written with
+ * Results that one workgroup gathers from the others (attention partials,
+ * the output product's rows, the workgroups' best logits) travel as 64-bit
+ * words tagged with the step's epoch and the layer, written with
  * device-coherent stores and polled with device-coherent loads: no fence,
- * no reliance on store order.  A counter per gather picks the last
- * workgroup (relaxed device atomics) and is reset by it.  Every poll is
- * bounded; one that runs out sets LmState.err, which the host reports.
+ * no reliance on store order.  The attention chunks of a head pick the
+ * last of them with a counter (relaxed device atomics), reset by it; the
+ * one-token products, whose grids the host sizes to be resident at once,
+ * leave the gather to workgroup 0, which polls the words as they land.
+ * Every poll is bounded; one that runs out sets LmState.err, which the
+ * host reports.
  *
  * Compiled with -ffp-contract=off: fused multiply-adds only where written.
  */
@@ -134,36 +137,6 @@ __device__ static inline bool last_to_arrive(u32 *cnt, u32 n, int *s_flag)
 		*s_flag = old == n - 1;
 		if (old == n - 1)
 			__hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-	}
-	__syncthreads();
-	return *s_flag != 0;
-}
-
-/* the same for the n = gridDim.x workgroups of a wide grid: workgroup b
- * counts in at cnt[1 + b / LM_ARRIVE_GROUP], the last of each group at
- * cnt[0] (same-address device atomics serialise: one counter for 1024
- * workgroups held the Mixtral output product at ~27 us); every counter is
- * reset by its last arrival */
-__device__ static inline bool last_to_arrive_wide(u32 *cnt, int *s_flag)
-{
-	__syncthreads(); /* every thread's tagged stores are issued */
-	if (threadIdx.x == 0) {
-		const u32 n = gridDim.x, gi = blockIdx.x / LM_ARRIVE_GROUP;
-		const u32 gn = min((u32)LM_ARRIVE_GROUP, n - gi * LM_ARRIVE_GROUP);
-		int last = 0;
-		u32 old = __hip_atomic_fetch_add(&cnt[1 + gi], 1u, __ATOMIC_RELAXED,
-						 __HIP_MEMORY_SCOPE_AGENT);
-		if (old == gn - 1) {
-			__hip_atomic_store(&cnt[1 + gi], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-			const u32 ng = (n + LM_ARRIVE_GROUP - 1) / LM_ARRIVE_GROUP;
-			old = __hip_atomic_fetch_add(&cnt[0], 1u, __ATOMIC_RELAXED,
-						     __HIP_MEMORY_SCOPE_AGENT);
-			last = old == ng - 1;
-			if (last)
-				__hip_atomic_store(&cnt[0], 0u, __ATOMIC_RELAXED,
-						   __HIP_MEMORY_SCOPE_AGENT);
-		}
-		*s_flag = last;
 	}
 	__syncthreads();
 	return *s_flag != 0;
@@ -626,23 +599,26 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 
 /*
  * out[E] = add + x . Wo^T (the residual stream after attention), each row
- * also stored tagged in rows_t; the last workgroup to finish reads them
- * all back and writes x_out = rms_norm(out) * w (the MoE layer's input).
+ * also stored tagged in rows_t; workgroup 0 reads them all back and writes
+ * x_out = rms_norm(out) * w (the MoE layer's input).
  */
 template <int WT, int C>
 __global__ __launch_bounds__(LM_NT) __attribute__((amdgpu_waves_per_eu(4)))
 void k_lm_oproj(const uint8_t *__restrict__ W, size_t rb, int N, int K,
 		const float *__restrict__ x, const float *__restrict__ add, float *__restrict__ out,
-		uint64_t *rows_t, u32 *cnt, const float *__restrict__ w, float *__restrict__ x_out,
+		uint64_t *rows_t, const float *__restrict__ w, float *__restrict__ x_out,
 		LmState *st, int layer)
 {
 	extern __shared__ __attribute__((aligned(16))) float sx[];
 	__shared__ float red[LM_NT / WAVE];
-	__shared__ int s_flag;
 	const u32 tag = lm_tag(st, layer);
 	auto hook = [=](int row, float r) { st_dev_u64(&rows_t[row], tagged(tag, r)); };
 	qgemv_body<WT, C, true>(sx, W, rb, N, K, x, 1, 1, add, 0, out, hook);
-	if (!last_to_arrive_wide(cnt, &s_flag))
+	/* workgroup 0 normalises, polling the rows as they land: the host sizes
+	 * the grid to be resident at once, so every row comes (counting the
+	 * workgroups in at device counters put 2-3 us of atomics behind the
+	 * slowest one) */
+	if (blockIdx.x != 0)
 		return;
 	/* the norm weights of this thread's outputs, WB at a time, the first
 	 * batch loading while the rows are gathered (a loop of one load per
@@ -702,13 +678,12 @@ template <int WT, int C>
 __global__ __launch_bounds__(LM_NT) __attribute__((amdgpu_waves_per_eu(4)))
 void k_lm_head(const uint8_t *__restrict__ W, size_t rb, int N, int K, const float *a,
 	       const float *b, const float *__restrict__ w, float *__restrict__ out,
-	       uint64_t *best, u32 *cnt, LmState *st, int *tokens)
+	       uint64_t *best, LmState *st, int *tokens)
 {
 	extern __shared__ __attribute__((aligned(16))) float sx[];
 	__shared__ float red[LM_NT / WAVE];
 	__shared__ float s_v[LM_NT / WAVE];
 	__shared__ int s_i[LM_NT / WAVE];
-	__shared__ int s_flag;
 	const u32 tag = lm_tag(st, LM_HEAD_SLOT);
 	stage_norm<WT>(sx, red, K, a, b, nullptr, w, nullptr);
 	float bv = -INFINITY;
@@ -729,7 +704,10 @@ void k_lm_head(const uint8_t *__restrict__ W, size_t rb, int N, int K, const flo
 		st_dev_u64(&best[2 * blockIdx.x], tagged(tag, bv));
 		st_dev_u64(&best[2 * blockIdx.x + 1], ((uint64_t)tag << 32) | (u32)bi);
 	}
-	if (!last_to_arrive_wide(cnt, &s_flag))
+	/* workgroup 0 picks, polling the workgroups' bests as they land (the
+	 * grid is resident at once; every workgroup read the epoch before its
+	 * tagged best, so advancing it after all of them is safe) */
+	if (blockIdx.x != 0)
 		return;
 	bv = -INFINITY;
 	bi = 0x7fffffff;
@@ -924,28 +902,27 @@ extern "C" int lm_launch_qkv(int wtype, const uint8_t *W, int N, int K, const fl
 }
 
 extern "C" int lm_launch_oproj(int wtype, const uint8_t *W, int N, int K, const float *x,
-			       const float *add, float *out, uint64_t *rows_t, uint32_t *cnt,
-			       const float *w, float *x_out, LmState *st, int layer, int grid,
-			       void *stream)
+			       const float *add, float *out, uint64_t *rows_t, const float *w,
+			       float *x_out, LmState *st, int layer, int grid, void *stream)
 {
 	const void *fn = lm_kernel(1, wtype, K);
 	if (!fn || grid < 1 || grid > LM_MAX_HEAD_WG || N > (int)(tok_lds(K) / sizeof(float)))
 		return (int)hipErrorInvalidValue;
 	size_t rb = (size_t)(K / MOE_QK) * (wtype == 1 ? 34 : 18);
-	void *args[] = {&W, &rb, &N, &K, &x, &add, &out, &rows_t, &cnt, &w, &x_out, &st, &layer};
+	void *args[] = {&W, &rb, &N, &K, &x, &add, &out, &rows_t, &w, &x_out, &st, &layer};
 	return (int)hipLaunchKernel(fn, dim3(grid), dim3(LM_NT), args, tok_lds(K),
 				    (hipStream_t)stream);
 }
 
 extern "C" int lm_launch_head(int wtype, const uint8_t *W, int N, int K, const float *a,
 			      const float *b, const float *w, float *out, uint64_t *best,
-			      uint32_t *cnt, LmState *st, int *tokens, int grid, void *stream)
+			      LmState *st, int *tokens, int grid, void *stream)
 {
 	const void *fn = lm_kernel(2, wtype, K);
 	if (!fn || grid < 1 || grid > LM_MAX_HEAD_WG)
 		return (int)hipErrorInvalidValue;
 	size_t rb = (size_t)(K / MOE_QK) * (wtype == 1 ? 34 : 18);
-	void *args[] = {&W, &rb, &N, &K, &a, &b, &w, &out, &best, &cnt, &st, &tokens};
+	void *args[] = {&W, &rb, &N, &K, &a, &b, &w, &out, &best, &st, &tokens};
 	return (int)hipLaunchKernel(fn, dim3(grid), dim3(LM_NT), args, tok_lds(K),
 				    (hipStream_t)stream);
 }
