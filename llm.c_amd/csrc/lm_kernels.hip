@@ -296,8 +296,9 @@ void k_lm_qkv(const uint8_t *__restrict__ W, size_t rb, int N, int K, const floa
  * of the row; softmax: wave g % NW takes head g (lane = position); v sums:
  * one dim per thread over half the positions, G heads from one read.  One
  * chunk writes out[h] = o / l itself; with more, partials part[h][c] =
- * {m, l, o[HL]} (stride nstride chunks) go out tagged, and the last of kv
- * head kh's chunks merges its G heads: out[h][d] = sum_c exp(m_c - M)
+ * {m, l, o[HL]} (stride nstride chunks) go out tagged, and one of kv head
+ * kh's chunks (chunk 0 where the grid is resident at once, else the last
+ * to count in) merges its G heads: out[h][d] = sum_c exp(m_c - M)
  * o_c[d] / sum_c exp(m_c - M) l_c.  Every head's arithmetic is the same
  * whatever G.
  */
@@ -546,8 +547,14 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 			st_dev_u64(&pp[1], tagged(tag, s_sum[g]));
 		}
 	}
-	if (!last_to_arrive(&cnt[kh], (u32)nact, &s_flag))
+	/* PF (the grid is resident at once): chunk 0 merges, polling the
+	 * others' partials as they land; else the last chunk to count in */
+	if constexpr (PF) {
+		if (c != 0)
+			return;
+	} else if (!last_to_arrive(&cnt[kh], (u32)nact, &s_flag)) {
 		return;
+	}
 	/* merge the nact chunks of each of the G heads */
 	for (int g = 0; g < G; g++) {
 		const uint64_t *ph = part + (size_t)(h0 + g) * nstride * (HL + 2);
