@@ -358,14 +358,30 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 	if (tid < HL / 2)
 		fr = freq[tid];
 	float s1 = 0.0f, s2 = 0.0f;
-	if (q_norm) {
-		for (int i = tid; i < EQ; i += LM_NT) {
-			const float t = q[i] * q[i];
-			s1 = s1 + t;
+	if (q_norm) { /* eight loads in flight, added in index order */
+		for (int i0 = tid; i0 < EQ; i0 += 8 * LM_NT) {
+			float qv[8];
+#pragma unroll
+			for (int u = 0; u < 8; u++)
+				qv[u] = i0 + u * LM_NT < EQ ? q[i0 + u * LM_NT] : 0.0f;
+#pragma unroll
+			for (int u = 0; u < 8; u++)
+				if (i0 + u * LM_NT < EQ) {
+					const float t = qv[u] * qv[u];
+					s1 = s1 + t;
+				}
 		}
-		for (int i = tid; i < EK; i += LM_NT) {
-			const float t = k[i] * k[i];
-			s2 = s2 + t;
+		for (int i0 = tid; i0 < EK; i0 += 8 * LM_NT) {
+			float kv[8];
+#pragma unroll
+			for (int u = 0; u < 8; u++)
+				kv[u] = i0 + u * LM_NT < EK ? k[i0 + u * LM_NT] : 0.0f;
+#pragma unroll
+			for (int u = 0; u < 8; u++)
+				if (i0 + u * LM_NT < EK) {
+					const float t = kv[u] * kv[u];
+					s2 = s2 + t;
+				}
 		}
 	}
 	const int size = st->size, spos = st->pos;
