@@ -833,8 +833,18 @@ __global__ __launch_bounds__(LM_NT) void k_lm_pick_rows(const float *__restrict_
 	const float *row = logits + (size_t)blockIdx.x * V;
 	float bv = -INFINITY;
 	int bi = 0x7fffffff;
-	for (int i = threadIdx.x; i < V; i += LM_NT)
-		better(bv, bi, row[i], i);
+	/* sixteen loads in flight (one per iteration waited a round trip
+	 * each); better() does not depend on the order */
+	for (int i0 = threadIdx.x; i0 < V; i0 += 16 * LM_NT) {
+		float v[16];
+#pragma unroll
+		for (int u = 0; u < 16; u++)
+			v[u] = i0 + u * LM_NT < V ? row[i0 + u * LM_NT] : -INFINITY;
+#pragma unroll
+		for (int u = 0; u < 16; u++)
+			if (i0 + u * LM_NT < V)
+				better(bv, bi, v[u], i0 + u * LM_NT);
+	}
 	for (int o = WAVE / 2; o > 0; o >>= 1)
 		better(bv, bi, __shfl_xor(bv, o, WAVE), __shfl_xor(bi, o, WAVE));
 	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;

@@ -397,26 +397,41 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypart
 	if (i >= E)
 		return;
 	float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-	for (int s0 = 0; s0 < K; s0 += 8) {
-		const int ns = K - s0 < 8 ? K - s0 : 8;
-		float4 y[8];
+	/* slots s0 .. s0 + ns - 1 (ns <= NS), their K chunks added in chunk
+	 * order, KB chunks' loads in flight at a time (one chunk per round trip
+	 * held Mixtral's eight-chunk combine at ~8 us) */
+	auto slots = [&](auto nsmax, auto kbc, int s0, int ns) {
+		constexpr int NS = decltype(nsmax)::value, KB = decltype(kbc)::value;
+		float4 y[NS];
 #pragma unroll
-		for (int s = 0; s < 8; s++)
-			if (s < ns)
-				y[s] = *(const float4 *)&ypart[((size_t)t * K + s0 + s) * kchunks * E + i];
-		for (int kc = 1; kc < kchunks; kc++)
+		for (int s = 0; s < NS; s++)
+			y[s] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+		for (int kc0 = 0; kc0 < kchunks; kc0 += KB) {
+			float4 v[KB][NS];
 #pragma unroll
-			for (int s = 0; s < 8; s++)
-				if (s < ns) {
-					const float4 v = *(const float4 *)&ypart
-						[(((size_t)t * K + s0 + s) * kchunks + kc) * E + i];
-					y[s].x += v.x;
-					y[s].y += v.y;
-					y[s].z += v.z;
-					y[s].w += v.w;
-				}
+			for (int j = 0; j < KB; j++)
 #pragma unroll
-		for (int s = 0; s < 8; s++)
+				for (int s = 0; s < NS; s++)
+					if (s < ns && kc0 + j < kchunks)
+						v[j][s] = *(const float4 *)&ypart
+							[(((size_t)t * K + s0 + s) * kchunks + kc0 + j) * E + i];
+#pragma unroll
+			for (int j = 0; j < KB; j++)
+#pragma unroll
+				for (int s = 0; s < NS; s++)
+					if (s < ns && kc0 + j < kchunks) {
+						if (kc0 + j == 0) {
+							y[s] = v[j][s];
+						} else {
+							y[s].x += v[j][s].x;
+							y[s].y += v[j][s].y;
+							y[s].z += v[j][s].z;
+							y[s].w += v[j][s].w;
+						}
+					}
+		}
+#pragma unroll
+		for (int s = 0; s < NS; s++)
 			if (s < ns) {
 				const float inv = 1.0f / (w ? w[(size_t)t * K + s0 + s] : 1.0f);
 				acc.x = acc.x + y[s].x / inv;
@@ -424,6 +439,13 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypart
 				acc.z = acc.z + y[s].z / inv;
 				acc.w = acc.w + y[s].w / inv;
 			}
+	};
+	if (K <= 2) {
+		slots(std::integral_constant<int, 2>(), std::integral_constant<int, 4>(), 0, K);
+	} else {
+		for (int s0 = 0; s0 < K; s0 += 8)
+			slots(std::integral_constant<int, 8>(), std::integral_constant<int, 1>(), s0,
+			      K - s0 < 8 ? K - s0 : 8);
 	}
 	float *o = &out[(size_t)t * E + i];
 	if (((uintptr_t)out & 15) == 0) {
