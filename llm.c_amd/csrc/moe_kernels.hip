@@ -180,12 +180,23 @@ __global__ __launch_bounds__(NW * WAVE) void k_router(const float *__restrict__ 
 template <int NT>
 __device__ static inline void rows_to_f16(const float *x, _Float16 *xh, int r0, int r1, int E)
 {
+	typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 	const size_t n4 = (size_t)(r1 - r0) * E / 4, o4 = (size_t)r0 * E / 4;
-	for (size_t i = threadIdx.x; i < n4; i += NT) {
-		const float4 v = ((const float4 *)x)[o4 + i];
-		typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-		half4_t h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
-		((half4_t *)xh)[o4 + i] = h;
+	/* eight loads of a thread in flight at once (one per iteration waited
+	 * a round trip each) */
+	for (size_t i0 = threadIdx.x; i0 < n4; i0 += 8 * NT) {
+		float4 v[8];
+#pragma unroll
+		for (int u = 0; u < 8; u++)
+			if (i0 + u * NT < n4)
+				v[u] = ((const float4 *)x)[o4 + i0 + u * NT];
+#pragma unroll
+		for (int u = 0; u < 8; u++)
+			if (i0 + u * NT < n4) {
+				half4_t h = {(_Float16)v[u].x, (_Float16)v[u].y, (_Float16)v[u].z,
+					     (_Float16)v[u].w};
+				((half4_t *)xh)[o4 + i0 + u * NT] = h;
+			}
 	}
 }
 
