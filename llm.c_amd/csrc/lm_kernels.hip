@@ -302,7 +302,7 @@ void k_lm_qkv(const uint8_t *__restrict__ W, size_t rb, int N, int K, const floa
  * o_c[d] / sum_c exp(m_c - M) l_c.  Every head's arithmetic is the same
  * whatever G.
  */
-template <int G, bool PF>
+template <int G, int PF>
 __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv,
 						   const float *__restrict__ q_norm,
 						   const float *__restrict__ k_norm,
@@ -423,10 +423,10 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 			vr[i] = j < n && j != jn ? V[(size_t)j * HL + dv] : 0.0f;
 		}
 	};
-	if constexpr (PF) {
+	if constexpr (PF >= 1)
 		load_k();
+	if constexpr (PF >= 2)
 		load_v();
-	}
 
 	if (tid < HL / 2) {
 		const float ang = (float)pos * fr;
@@ -467,7 +467,7 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 		kc[((size_t)kh * C + size) * HL + tid] = sk[tid];
 		vc[((size_t)kh * C + size) * HL + tid] = sv[tid];
 	}
-	if constexpr (!PF)
+	if constexpr (PF < 1)
 		load_k();
 	{
 		const int j = jq;
@@ -514,7 +514,7 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 			s_sum[g] = sv2;
 		}
 	}
-	if constexpr (!PF)
+	if constexpr (PF < 2)
 		load_v();
 	__syncthreads();
 	{
@@ -563,9 +563,9 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 			st_dev_u64(&pp[1], tagged(tag, s_sum[g]));
 		}
 	}
-	/* PF (the grid is resident at once): chunk 0 merges, polling the
+	/* PF 2 (the grid is resident at once): chunk 0 merges, polling the
 	 * others' partials as they land; else the last chunk to count in */
-	if constexpr (PF) {
+	if constexpr (PF == 2) {
 		if (c != 0)
 			return;
 	} else if (!last_to_arrive(&cnt[kh], (u32)nact, &s_flag)) {
@@ -978,16 +978,18 @@ extern "C" int lm_launch_attn(const float *qkv, const float *q_norm, const float
 		return (int)hipErrorInvalidValue;
 	const dim3 grid(KH, nact, nseq);
 	hipStream_t s = (hipStream_t)stream;
-	/* the early loads while the grid fits 3 workgroups per CU at once */
+	/* all of a chunk's rows loaded early while the grid fits 3 workgroups
+	 * per CU at once; larger grids load k early and v before its use (at
+	 * a register count that keeps more workgroups resident) */
 	const bool pf = (size_t)KH * nact * nseq <= 3 * (size_t)lm_cus();
 #define ATTN(GG)                                                                               \
 	do {                                                                                   \
 		if (pf)                                                                        \
-			hipLaunchKernelGGL((k_lm_attn<GG, true>), grid, dim3(LM_NT), 0, s, qkv,   \
+			hipLaunchKernelGGL((k_lm_attn<GG, 2>), grid, dim3(LM_NT), 0, s, qkv,      \
 					   q_norm, k_norm, freq, st, kc, vc, part, cnt, out, H, KH,   \
 					   C, window, scale, scale_mul, layer, nch, cstride);         \
 		else                                                                           \
-			hipLaunchKernelGGL((k_lm_attn<GG, false>), grid, dim3(LM_NT), 0, s, qkv,  \
+			hipLaunchKernelGGL((k_lm_attn<GG, 1>), grid, dim3(LM_NT), 0, s, qkv,      \
 					   q_norm, k_norm, freq, st, kc, vc, part, cnt, out, H, KH,   \
 					   C, window, scale, scale_mul, layer, nch, cstride);         \
 	} while (0)

@@ -189,6 +189,16 @@ def test_gpu_batch_mixtral_small_vs_oracle():
     batch_vs_oracle("mixtral_small", 4, 1e-3)
 
 
+@pytest.mark.timeout(600)
+def test_gpu_batch120_olmoe_small_large_attention_grid_vs_oracle():
+    """120 sequences: the attention grid (8 kv heads x 1 chunk x 120) is
+    larger than three workgroups per CU of any MI3xx device holds at once,
+    so attention takes its large-grid form (k rows loaded early, v rows
+    before their sums, the last chunk to count in merges); the MoE layer
+    at T = 120 takes the grouped path (f16 operands)."""
+    batch_vs_oracle("olmoe_small", 120, 1e-3, n_gen=8)
+
+
 @pytest.mark.timeout(900)
 def test_gpu_batch16_mixtral_layer_shape_vs_oracle():
     """Sixteen sequences on two layers of the Mixtral-8x7B shape (32 / 8
