@@ -316,7 +316,7 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 	__shared__ float cs[HL / 2], sn[HL / 2], sq[G][HL], sk[HL], sv[HL], sp[G][CH];
 	__shared__ float so[G][LM_NT];
 	__shared__ float red[NW];
-	__shared__ float s_f[LM_MAX_CHUNKS], s_l[LM_MAX_CHUNKS];
+	__shared__ float s_f[G][LM_MAX_CHUNKS], s_l[G][LM_MAX_CHUNKS];
 	__shared__ float s_m[G], s_sum[G];
 	__shared__ int s_flag;
 	const int kh = blockIdx.x, c = blockIdx.y, nact = gridDim.y;
@@ -571,48 +571,77 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 	} else if (!last_to_arrive(&cnt[kh], (u32)nact, &s_flag)) {
 		return;
 	}
-	/* merge the nact chunks of each of the G heads */
-	for (int g = 0; g < G; g++) {
-		const uint64_t *ph = part + (size_t)(h0 + g) * nstride * (HL + 2);
-		gather_tagged(ph, HL + 2, nact, tag, st,
-			      [&](int cc, u32 b) { s_f[cc] = __builtin_bit_cast(float, b); });
-		gather_tagged(ph + 1, HL + 2, nact, tag, st,
-			      [&](int cc, u32 b) { s_l[cc] = __builtin_bit_cast(float, b); });
-		__syncthreads();
-		float M = -INFINITY;
-		for (int cc = 0; cc < nact; cc++)
-			M = fmaxf(M, s_f[cc]);
-		__syncthreads();
-		for (int cc = tid; cc < nact; cc += LM_NT)
-			s_f[cc] = s_l[cc] > 0.0f ? moe_expf(s_f[cc] - M) : 0.0f;
-		__syncthreads();
-		if (tid < HL) {
-			float L = 0.0f, acc = 0.0f;
-			for (int c0 = 0; c0 < nact; c0 += 8) {
-				/* eight loads in flight, then a poll only for a late one */
-				uint64_t vv[8];
+	/* merge the nact chunks of the G heads: every head's m and l in one
+	 * batch of loads (a late one polled alone), then the o sums two heads
+	 * at a time, sixteen chunks' loads in flight (merging the heads one
+	 * after another took ~20 dependent round trips for 4 heads x 17
+	 * chunks); each head's arithmetic in chunk order as before */
+	const int NML = G * nact;
+	for (int e0 = tid; e0 < NML; e0 += 8 * LM_NT) {
+		uint64_t vm[8], vl[8];
 #pragma unroll
-				for (int u = 0; u < 8; u++)
+		for (int u = 0; u < 8; u++) {
+			const int e = e0 + u * LM_NT;
+			const uint64_t *pe =
+				part + ((size_t)(h0 + e / nact) * nstride + e % nact) * (HL + 2);
+			vm[u] = e < NML ? ld_dev_u64(&pe[0]) : 0;
+			vl[u] = e < NML ? ld_dev_u64(&pe[1]) : 0;
+		}
+#pragma unroll
+		for (int u = 0; u < 8; u++) {
+			const int e = e0 + u * LM_NT;
+			if (e >= NML)
+				break;
+			const int g = e / nact, cc = e % nact;
+			const uint64_t *pe = part + ((size_t)(h0 + g) * nstride + cc) * (HL + 2);
+			const u32 mb = (u32)(vm[u] >> 32) == tag ? (u32)vm[u] : poll_tag(&pe[0], tag, st);
+			const u32 lb = (u32)(vl[u] >> 32) == tag ? (u32)vl[u] : poll_tag(&pe[1], tag, st);
+			s_f[g][cc] = __builtin_bit_cast(float, mb);
+			s_l[g][cc] = __builtin_bit_cast(float, lb);
+		}
+	}
+	__syncthreads();
+	/* head g's maximum M on wave g % NW (max: any order), then its weights
+	 * exp(m_c - M) (0 for an empty chunk) */
+	for (int g = wave; g < G; g += NW) {
+		float M = -INFINITY;
+		for (int cc = lane; cc < nact; cc += WAVE)
+			M = fmaxf(M, s_f[g][cc]);
+		for (int o2 = WAVE / 2; o2 > 0; o2 >>= 1)
+			M = fmaxf(M, __shfl_xor(M, o2, WAVE));
+		for (int cc = lane; cc < nact; cc += WAVE)
+			s_f[g][cc] = s_l[g][cc] > 0.0f ? moe_expf(s_f[g][cc] - M) : 0.0f;
+	}
+	__syncthreads();
+	{
+		constexpr int HPR = LM_NT / HL; /* heads merged at once */
+		const int d = tid % HL;
+		for (int g = tid / HL; g < G; g += HPR) {
+			const uint64_t *ph = part + (size_t)(h0 + g) * nstride * (HL + 2);
+			float L = 0.0f, acc = 0.0f;
+			for (int c0 = 0; c0 < nact; c0 += 16) {
+				uint64_t vv[16];
+#pragma unroll
+				for (int u = 0; u < 16; u++)
 					vv[u] = c0 + u < nact
-							? ld_dev_u64(&ph[(size_t)(c0 + u) * (HL + 2) + 2 + tid])
+							? ld_dev_u64(&ph[(size_t)(c0 + u) * (HL + 2) + 2 + d])
 							: 0;
 #pragma unroll
-				for (int u = 0; u < 8; u++) {
+				for (int u = 0; u < 16; u++) {
 					const int cc = c0 + u;
 					if (cc >= nact)
 						break;
 					const u32 ob =
 						(u32)(vv[u] >> 32) == tag
 							? (u32)vv[u]
-							: poll_tag(&ph[(size_t)cc * (HL + 2) + 2 + tid], tag, st);
-					const float f = s_f[cc];
-					L = __builtin_fmaf(f, s_l[cc], L);
+							: poll_tag(&ph[(size_t)cc * (HL + 2) + 2 + d], tag, st);
+					const float f = s_f[g][cc];
+					L = __builtin_fmaf(f, s_l[g][cc], L);
 					acc = __builtin_fmaf(f, __builtin_bit_cast(float, ob), acc);
 				}
 			}
-			out[(h0 + g) * HL + tid] = acc / L;
+			out[(h0 + g) * HL + d] = acc / L;
 		}
-		__syncthreads(); /* s_f and s_l are rewritten for the next head */
 	}
 }
 
