@@ -208,8 +208,20 @@ __global__ __launch_bounds__(KG_THREADS) void k_kq_gateup(
 		load_dwords<36>(blk, w);
 	else
 		kg_load<53>(blk, w);
-	for (int i = wave; i < nb; i += KG_THREADS / WAVE) {
-		const float4 v = ((const float4 *)(x + (size_t)t * E + (size_t)i * 256))[lane];
+	/* the wave's token blocks (nb <= 32: at most 8 a wave), loaded together */
+	float4 xv[8];
+#pragma unroll
+	for (int u = 0; u < 8; u++) {
+		const int i = wave + u * (KG_THREADS / WAVE);
+		if (i < nb)
+			xv[u] = ((const float4 *)(x + (size_t)t * E + (size_t)i * 256))[lane];
+	}
+#pragma unroll
+	for (int u = 0; u < 8; u++) {
+		const int i = wave + u * (KG_THREADS / WAVE);
+		if (i >= nb)
+			break;
+		const float4 v = xv[u];
 		float d;
 		int bs;
 		const u32 q = kg_q8k(v, lane, &d, &bs);
@@ -356,22 +368,51 @@ __global__ __launch_bounds__(KD_THREADS) void k_kq_down(const uint8_t *__restric
 	for (int c0 = 0; c0 < nb; c0 += KD_CB) {
 		const int cb = min(KD_CB, nb - c0);
 		const int run = cb * BY;
-		__syncthreads(); /* the previous chunk's readers are done */
-		for (int i = tid; i < cb * 64; i += KD_THREADS)
-			((float4 *)s_h)[i] = ((const float4 *)(h + (size_t)p * EI + (size_t)c0 * 256))[i];
 		/* the 32 runs, 8 bytes a thread per step (runs are 2-byte aligned for
-		 * Q6_K: dword pairs from the aligned address, realigned) */
-		for (int e = tid; e < KD_ROWS * (RUN / 8); e += KD_THREADS) {
+		 * Q6_K: dword pairs from the aligned address, realigned), and the
+		 * chunk's h: every load of the thread goes out before any is stored
+		 * (a loop that stored each before the next load waited ~13 round
+		 * trips a chunk) */
+		constexpr int NIT = (KD_ROWS * (RUN / 8) + KD_THREADS - 1) / KD_THREADS;
+		u32 v[NIT][3], shv[NIT];
+#pragma unroll
+		for (int it = 0; it < NIT; it++) {
+			const int e = tid + it * KD_THREADS;
 			const int r = e / (RUN / 8), o = 8 * (e % (RUN / 8));
-			if (o >= run)
-				continue;
-			const int row = min(r0 + r, E - 1);
-			const uint8_t *src = base + (size_t)row * rb + (size_t)c0 * BY + o;
-			const u32 sh = (u32)((uintptr_t)src & 3);
-			const u32 *a = (const u32 *)(src - sh);
-			const u32 v0 = a[0], v1 = a[1], v2 = a[2];
-			*(uint2 *)(s_w + r * RUN + o) = make_uint2(__builtin_amdgcn_alignbyte(v1, v0, sh),
-								   __builtin_amdgcn_alignbyte(v2, v1, sh));
+			shv[it] = 0;
+			if (e < KD_ROWS * (RUN / 8) && o < run) {
+				const int row = min(r0 + r, E - 1);
+				const uint8_t *src = base + (size_t)row * rb + (size_t)c0 * BY + o;
+				const u32 sh = (u32)((uintptr_t)src & 3);
+				const u32 *a = (const u32 *)(src - sh);
+				v[it][0] = a[0];
+				v[it][1] = a[1];
+				v[it][2] = a[2];
+				shv[it] = sh;
+			}
+		}
+		float4 hv[(KD_CB * 64 + KD_THREADS - 1) / KD_THREADS];
+#pragma unroll
+		for (int u = 0; u < (KD_CB * 64 + KD_THREADS - 1) / KD_THREADS; u++) {
+			const int i = tid + u * KD_THREADS;
+			if (i < cb * 64)
+				hv[u] = ((const float4 *)(h + (size_t)p * EI + (size_t)c0 * 256))[i];
+		}
+		__syncthreads(); /* the previous chunk's readers are done */
+#pragma unroll
+		for (int u = 0; u < (KD_CB * 64 + KD_THREADS - 1) / KD_THREADS; u++) {
+			const int i = tid + u * KD_THREADS;
+			if (i < cb * 64)
+				((float4 *)s_h)[i] = hv[u];
+		}
+#pragma unroll
+		for (int it = 0; it < NIT; it++) {
+			const int e = tid + it * KD_THREADS;
+			const int r = e / (RUN / 8), o = 8 * (e % (RUN / 8));
+			if (e < KD_ROWS * (RUN / 8) && o < run)
+				*(uint2 *)(s_w + r * RUN + o) =
+					make_uint2(__builtin_amdgcn_alignbyte(v[it][1], v[it][0], shv[it]),
+						   __builtin_amdgcn_alignbyte(v[it][2], v[it][1], shv[it]));
 		}
 		__syncthreads();
 		for (int k = 0; k < cb; k++) {
