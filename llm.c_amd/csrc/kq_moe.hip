@@ -364,17 +364,17 @@ __global__ __launch_bounds__(KD_THREADS) void k_kq_down(const uint8_t *__restric
 	const size_t rb = (size_t)nb * BY;
 	const uint8_t *base = down + (size_t)ids[p] * dn_stride;
 
-	float acc = 0.0f;
-	for (int c0 = 0; c0 < nb; c0 += KD_CB) {
-		const int cb = min(KD_CB, nb - c0);
-		const int run = cb * BY;
-		/* the 32 runs, 8 bytes a thread per step (runs are 2-byte aligned for
-		 * Q6_K: dword pairs from the aligned address, realigned), and the
-		 * chunk's h: every load of the thread goes out before any is stored
-		 * (a loop that stored each before the next load waited ~13 round
-		 * trips a chunk) */
-		constexpr int NIT = (KD_ROWS * (RUN / 8) + KD_THREADS - 1) / KD_THREADS;
-		u32 v[NIT][3], shv[NIT];
+	/* a chunk's 32 runs, 8 bytes a thread per step (runs are 2-byte aligned
+	 * for Q6_K: dword pairs from the aligned address, realigned), and its h,
+	 * into registers: every load goes out before any is stored (a loop that
+	 * stored each before the next load waited ~13 round trips a chunk), and
+	 * the next chunk's go out while this one's dots run */
+	constexpr int NIT = (KD_ROWS * (RUN / 8) + KD_THREADS - 1) / KD_THREADS;
+	constexpr int NH = (KD_CB * 64 + KD_THREADS - 1) / KD_THREADS;
+	u32 v[NIT][3], shv[NIT];
+	float4 hv[NH];
+	auto load_chunk = [&](int c0) {
+		const int run = min(KD_CB, nb - c0) * BY, cb = min(KD_CB, nb - c0);
 #pragma unroll
 		for (int it = 0; it < NIT; it++) {
 			const int e = tid + it * KD_THREADS;
@@ -391,16 +391,21 @@ __global__ __launch_bounds__(KD_THREADS) void k_kq_down(const uint8_t *__restric
 				shv[it] = sh;
 			}
 		}
-		float4 hv[(KD_CB * 64 + KD_THREADS - 1) / KD_THREADS];
 #pragma unroll
-		for (int u = 0; u < (KD_CB * 64 + KD_THREADS - 1) / KD_THREADS; u++) {
+		for (int u = 0; u < NH; u++) {
 			const int i = tid + u * KD_THREADS;
 			if (i < cb * 64)
 				hv[u] = ((const float4 *)(h + (size_t)p * EI + (size_t)c0 * 256))[i];
 		}
+	};
+	float acc = 0.0f;
+	load_chunk(0);
+	for (int c0 = 0; c0 < nb; c0 += KD_CB) {
+		const int cb = min(KD_CB, nb - c0);
+		const int run = cb * BY;
 		__syncthreads(); /* the previous chunk's readers are done */
 #pragma unroll
-		for (int u = 0; u < (KD_CB * 64 + KD_THREADS - 1) / KD_THREADS; u++) {
+		for (int u = 0; u < NH; u++) {
 			const int i = tid + u * KD_THREADS;
 			if (i < cb * 64)
 				((float4 *)s_h)[i] = hv[u];
@@ -415,6 +420,8 @@ __global__ __launch_bounds__(KD_THREADS) void k_kq_down(const uint8_t *__restric
 						   __builtin_amdgcn_alignbyte(v[it][2], v[it][1], shv[it]));
 		}
 		__syncthreads();
+		if (c0 + KD_CB < nb)
+			load_chunk(c0 + KD_CB);
 		for (int k = 0; k < cb; k++) {
 			const uint8_t *blk = s_w + rk * RUN + k * BY;
 			if constexpr (WT == 3)
