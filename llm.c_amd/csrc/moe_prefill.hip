@@ -793,7 +793,7 @@ __device__ static inline bool pf_item_v(int ntiles, int &tile, int &nb)
 	return true;
 }
 
-/* this lane's two A chunks (rows arow and arow + 64 of a 128-row stage) */
+/* this lane's A chunks: row arow of a stage, and row arow + 64 for tiles over 64 rows */
 struct pf_lanes2 {
 	int arow, achunk;
 	__device__ inline pf_lanes2()
@@ -810,7 +810,8 @@ __device__ static void pf_gateup_tile(uint8_t *lds, const _Float16 *xh, const ui
 				      size_t up_off, size_t gu_stride, const int *rows, int K,
 				      int E, int EI, _Float16 *h, int e, int r0, int nb)
 {
-	typedef pf_geo<WT, 2> GG;
+	constexpr int AL = MB > 2 ? 2 : 1; /* 64-row A loads: tiles up to 64 rows need one */
+	typedef pf_geo<WT, AL> GG;
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 	const int n0 = nb * (PF_BROWS / 2);
 	const size_t rb = (size_t)(E / MOE_QK) * GG::BB;
@@ -828,9 +829,9 @@ __device__ static void pf_gateup_tile(uint8_t *lds, const _Float16 *xh, const ui
 	}
 	constexpr int MT = 32 * MB;
 	pf_lanes2 L;
-	u32 aoff[2];
+	u32 aoff[AL];
 #pragma unroll
-	for (int a = 0; a < 2; a++) {
+	for (int a = 0; a < AL; a++) {
 		const int ar = L.arow + 64 * a;
 		const int p = ar < MT ? rows[r0 + ar] : -1;
 		aoff[a] = p >= 0 ? (u32)((size_t)(p / K) * E * 2 + 16 * L.achunk) : 0u;
@@ -844,7 +845,7 @@ __device__ static void pf_gateup_tile(uint8_t *lds, const _Float16 *xh, const ui
 #pragma unroll
 			for (int j = 0; j < 16; j++)
 				acc[mb][g][j] = 0.0f;
-	pf_kloop<WT, 0, NS, MB, 2>(lds, gate, MOE_GU_GROUP * GG::RBS, woff, (const uint8_t *)xh,
+	pf_kloop<WT, 0, NS, MB, AL>(lds, gate, MOE_GU_GROUP * GG::RBS, woff, (const uint8_t *)xh,
 				   aoff, brow, E / PF_KB, acc);
 	const int col = n0 + wave * 32 + (lane & 31), hh = lane >> 5;
 #pragma unroll
@@ -884,7 +885,8 @@ __device__ static void pf_down_tile(uint8_t *lds, int *srow, const _Float16 *h,
 				    const uint8_t *down, size_t dn_stride, const int *rows, int E,
 				    int EI, float *ypart, int e, int r0, int nb)
 {
-	typedef pf_geo<WT, 2> GG;
+	constexpr int AL = MB > 2 ? 2 : 1;
+	typedef pf_geo<WT, AL> GG;
 	constexpr int MT = 32 * MB;
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 	const int S = gridDim.z, nst = EI / PF_KB;
@@ -902,9 +904,9 @@ __device__ static void pf_down_tile(uint8_t *lds, int *srow, const _Float16 *h,
 					     : (size_t)n0 * GG::BB));
 	}
 	pf_lanes2 L;
-	u32 aoff[2];
+	u32 aoff[AL];
 #pragma unroll
-	for (int a = 0; a < 2; a++) {
+	for (int a = 0; a < AL; a++) {
 		const int ar = L.arow + 64 * a;
 		aoff[a] = ar < MT && rows[r0 + ar] >= 0
 				  ? (u32)((size_t)(r0 + ar) * EI * 2 + 16 * L.achunk)
@@ -919,7 +921,7 @@ __device__ static void pf_down_tile(uint8_t *lds, int *srow, const _Float16 *h,
 #pragma unroll
 			for (int j = 0; j < 16; j++)
 				acc[mb][g][j] = 0.0f;
-	pf_kloop<WT, 1, NS, MB, 2>(lds, down + (size_t)s0 * 2 * PANEL, 2 * PANEL, woff,
+	pf_kloop<WT, 1, NS, MB, AL>(lds, down + (size_t)s0 * 2 * PANEL, 2 * PANEL, woff,
 				   (const uint8_t *)(h + (size_t)s0 * PF_KB), aoff, brow, s1 - s0,
 				   acc); /* syncs srow */
 	const int hh = lane >> 5;
