@@ -418,6 +418,7 @@ __device__ static inline void pf_kloop(uint8_t *lds, const uint8_t *wbase, size_
 				       floatx16 (&acc)[MB < 2 ? 2 : MB][2])
 {
 	typedef pf_geo<WT, AL> GG;
+	constexpr bool HALF_A = MB == 1 && AL == 1 && NS == 2;
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 	const u32 l0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
 	auto issue = [&](int s) {
@@ -426,12 +427,17 @@ __device__ static inline void pf_kloop(uint8_t *lds, const uint8_t *wbase, size_
 #pragma unroll
 		for (int j = 0; j < GG::JB; j++)
 			dma_dwordx4(wb, woff[j], st + (u32)((wave * GG::JB + j) * WAVE * GG::CH));
-		/* every wave issues the same loads per stage (the waits count
-		 * them); lanes of padding rows all read the same 16 bytes */
+		/* lanes of padding rows all read the same 16 bytes; a 32-row
+		 * tile's waves 4-7 would load only rows 32-63, which no MFMA
+		 * reads, so a 2-stage ring (which waits for all of a wave's
+		 * loads) skips them: Mixtral T=64 217.1 -> 213.0 us, T=16 209.3
+		 * -> 204.9 us.  In the 4-stage ring the waves' uneven waits cost
+		 * more than the loads (OLMoE T=512 155.2 -> 157.3 us). */
 #pragma unroll
 		for (int a = 0; a < AL; a++)
-			dma_dwordx4(abase + (size_t)s * 128, aoff[a],
-				    st + GG::BSZ + (u32)(a * 8192 + wave * 1024));
+			if (!HALF_A || wave < 4)
+				dma_dwordx4(abase + (size_t)s * 128, aoff[a],
+					    st + GG::BSZ + (u32)(a * 8192 + wave * 1024));
 	};
 #pragma unroll
 	for (int s = 0; s < NS - 1; s++)
