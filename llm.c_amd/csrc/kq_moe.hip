@@ -316,28 +316,50 @@ __device__ static inline void kd_q4k(const uint8_t *blk, const float *hb, int l,
 
 __device__ static inline void kd_q6k(const uint8_t *blk, const float *hb, int l, float &acc)
 {
-	const float d = f16_bits_to_f32(blk[208] | (blk[209] << 8));
-	const int8_t *sc = (const int8_t *)(blk + 192);
+	/* every LDS read of the super-block goes out before the first product
+	 * (the grid holds one wave per SIMD, so nothing else hides a read's
+	 * round trip); the products and their order are unchanged: element
+	 * 128c + 32g + 16hf + 8m + l is step j = 16c + 4g + 2hf + m of the
+	 * lane's chain */
+	u32 ql[2][2][2][2], qh[2][2][2]; /* [c][hf][m][+32] and [c][hf][m] */
+	int sc[16];
+	float hv[32];
 #pragma unroll
-	for (int c = 0; c < 2; c++) {
-		const uint8_t *ql = blk + 64 * c, *qh = blk + 128 + 32 * c;
+	for (int c = 0; c < 2; c++)
+#pragma unroll
+		for (int hf = 0; hf < 2; hf++)
+#pragma unroll
+			for (int m = 0; m < 2; m++) {
+				const int e = 16 * hf + l + 8 * m;
+				ql[c][hf][m][0] = blk[64 * c + e];
+				ql[c][hf][m][1] = blk[64 * c + e + 32];
+				qh[c][hf][m] = blk[128 + 32 * c + e];
+			}
+#pragma unroll
+	for (int i = 0; i < 16; i++)
+		sc[i] = ((const int8_t *)(blk + 192))[i];
+	const u32 dlo = blk[208], dhi = blk[209];
+#pragma unroll
+	for (int jj = 0; jj < 32; jj++)
+		hv[jj] = hb[l + 8 * jj];
+	const float d = f16_bits_to_f32(dlo | (dhi << 8));
+#pragma unroll
+	for (int c = 0; c < 2; c++)
 #pragma unroll
 		for (int g = 0; g < 4; g++)
 #pragma unroll
 			for (int hf = 0; hf < 2; hf++) {
-				/* elements c*128 + g*32 + hf*16 + {l, l + 8} */
 				const float vs = d * (float)sc[8 * c + 2 * g + hf];
 #pragma unroll
 				for (int m = 0; m < 2; m++) {
-					const int e = 16 * hf + l + 8 * m;
-					const int lo = (g & 1) ? ql[e + 32] : ql[e];
-					const int q = ((g < 2 ? lo & 0xF : lo >> 4) | (((qh[e] >> (2 * g)) & 3) << 4)) -
+					const int lo = (int)ql[c][hf][m][g & 1];
+					const int q = ((g < 2 ? lo & 0xF : lo >> 4) |
+						       (((int)(qh[c][hf][m] >> (2 * g)) & 3) << 4)) -
 						      32;
 					const float vt = (float)q * vs;
-					acc = fmaf(vt, hb[128 * c + 32 * g + e], acc);
+					acc = fmaf(vt, hv[16 * c + 4 * g + 2 * hf + m], acc);
 				}
 			}
-	}
 }
 
 /*
