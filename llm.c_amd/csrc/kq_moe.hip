@@ -275,9 +275,24 @@ __global__ __launch_bounds__(KG_THREADS) void k_kq_gateup(
  * elements l, l + 8, ... with h from LDS */
 __device__ static inline void kd_q4k(const uint8_t *blk, const float *hb, int l, float &acc)
 {
-	const float d = f16_bits_to_f32(blk[0] | (blk[1] << 8));
-	const float dmin = f16_bits_to_f32(blk[2] | (blk[3] << 8));
-	const uint8_t *sc = blk + 4, *qs = blk + 16;
+	/* as kd_q6k: every LDS read first, then the products in their order
+	 * (element 64j + 32hi + 8m + l is step 8j + 4hi + m of the chain) */
+	u32 sc[12], q[4][4];
+	float hv[32];
+	const u32 b0 = blk[0], b1 = blk[1], b2 = blk[2], b3 = blk[3];
+#pragma unroll
+	for (int i = 0; i < 12; i++)
+		sc[i] = blk[4 + i];
+#pragma unroll
+	for (int j = 0; j < 4; j++)
+#pragma unroll
+		for (int m = 0; m < 4; m++)
+			q[j][m] = blk[16 + 32 * j + l + 8 * m];
+#pragma unroll
+	for (int jj = 0; jj < 32; jj++)
+		hv[jj] = hb[l + 8 * jj];
+	const float d = f16_bits_to_f32(b0 | (b1 << 8));
+	const float dmin = f16_bits_to_f32(b2 | (b3 << 8));
 #pragma unroll
 	for (int j = 0; j < 4; j++) {
 		int s1, m1, s2, m2;
@@ -295,21 +310,17 @@ __device__ static inline void kd_q4k(const uint8_t *blk, const float *hb, int l,
 		}
 		const float d1 = d * (float)s1, n1 = dmin * (float)m1;
 		const float d2 = d * (float)s2, n2 = dmin * (float)m2;
-		u32 q[4];
-#pragma unroll
-		for (int m = 0; m < 4; m++)
-			q[m] = qs[32 * j + l + 8 * m];
 #pragma unroll
 		for (int m = 0; m < 4; m++) {
-			float v = d1 * (float)(q[m] & 0xF);
+			float v = d1 * (float)(q[j][m] & 0xF);
 			v = v - n1;
-			acc = fmaf(v, hb[64 * j + l + 8 * m], acc);
+			acc = fmaf(v, hv[8 * j + m], acc);
 		}
 #pragma unroll
 		for (int m = 0; m < 4; m++) {
-			float v = d2 * (float)(q[m] >> 4);
+			float v = d2 * (float)(q[j][m] >> 4);
 			v = v - n2;
-			acc = fmaf(v, hb[64 * j + 32 + l + 8 * m], acc);
+			acc = fmaf(v, hv[8 * j + 4 + m], acc);
 		}
 	}
 }
