@@ -187,9 +187,13 @@ __global__ __launch_bounds__(KG_THREADS) void k_kq_gateup(
 	const u32 *__restrict__ ids, const float *__restrict__ x, float *__restrict__ h, int K,
 	int E, int EI, int R)
 {
-	__shared__ __attribute__((aligned(16))) int s_q8[32 * 64]; /* E <= 8192 */
+	/* the token's Q8_K blocks, rows padded by one int: a wave's lanes read
+	 * up to 16 blocks at the same offset, which then fall in distinct banks
+	 * (a 64-int stride put them all in one) */
+	constexpr int QS = 65, BS = 17;
+	__shared__ int s_q8[32 * QS]; /* E <= 8192 */
 	__shared__ float s_d[32];
-	__shared__ int s_bs[32 * 16];
+	__shared__ int s_bs[32 * BS];
 	__shared__ int s_rec[4][512]; /* 2 R (nb + 1) <= 512 for R * nb <= 128 */
 	constexpr int BY = kqb<WT>::BYTES, DW = WT == 3 ? 36 : 53;
 	const int p = blockIdx.y, t = p / K, nb = E / 256;
@@ -225,9 +229,9 @@ __global__ __launch_bounds__(KG_THREADS) void k_kq_gateup(
 		float d;
 		int bs;
 		const u32 q = kg_q8k(v, lane, &d, &bs);
-		s_q8[i * 64 + lane] = (int)q;
+		s_q8[i * QS + lane] = (int)q;
 		if (lane % 4 == 0)
-			s_bs[i * 16 + lane / 4] = bs;
+			s_bs[i * BS + lane / 4] = bs;
 		if (lane == 0)
 			s_d[i] = d;
 	}
@@ -236,9 +240,9 @@ __global__ __launch_bounds__(KG_THREADS) void k_kq_gateup(
 		float dsc, dmn = 0.0f;
 		int sumi, msum = 0;
 		if constexpr (WT == 3)
-			kg_q4k(w, s_q8 + sb * 64, s_bs + sb * 16, s_d[sb], dsc, sumi, dmn, msum);
+			kg_q4k(w, s_q8 + sb * QS, s_bs + sb * BS, s_d[sb], dsc, sumi, dmn, msum);
 		else
-			kg_q6k(w, s_q8 + sb * 64, s_bs + sb * 16, s_d[sb], dsc, sumi);
+			kg_q6k(w, s_q8 + sb * QS, s_bs + sb * BS, s_d[sb], dsc, sumi);
 		const int slot = (mat * R + rl) * rs + sb;
 		((float *)s_rec[0])[slot] = dsc;
 		s_rec[1][slot] = sumi;
