@@ -301,7 +301,10 @@ int hip_moe_qmat_mul(hip_moe_qmat *W, const float *x, size_t T, const float *add
  * allocates nothing: the matrix-core form's token buffer, made at upload,
  * holds 64 tokens (more after a host call of more tokens); calls with more
  * take the per-token product.  Calls that overlap on one matrix race on
- * that buffer. */
+ * that buffer.  A host call (hip_moe_qmat_mul) with more tokens than the
+ * buffer holds replaces it (after waiting for the device): HIP graphs
+ * captured earlier with this function on W name the freed buffer and must
+ * be captured again. */
 int hip_moe_qmat_mul_dev(const hip_moe_qmat *W, const float *d_x, size_t T,
                          const float *d_add, size_t add_len, float *d_out, void *stream);
 

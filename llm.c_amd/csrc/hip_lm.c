@@ -64,6 +64,7 @@ struct hip_lm {
 	 * attention chunks (the attention grid), captured when first needed */
 	int nch;
 	hipGraphExec_t *g_body, *g_head;
+	unsigned graph_gen; /* the MoE layers' scratch generation the graphs name */
 	hipEvent_t ev0, ev1;
 };
 
@@ -118,6 +119,17 @@ static void drop_graphs(hip_lm *M)
 			hipGraphExecDestroy(M->g_head[i]);
 		M->g_body[i] = M->g_head[i] = NULL;
 	}
+}
+
+/* the sum of the MoE layers' scratch generations: it changes whenever a
+ * layer reallocates its scratch (a lockstep batch reserving more tokens),
+ * after which step graphs captured before name freed buffers */
+static unsigned moe_gen(const hip_lm *M)
+{
+	unsigned g = 0;
+	for (size_t l = 0; M->ly && l < M->L; l++)
+		g += moe_scratch_gen(M->ly[l].moe);
+	return g;
 }
 
 void hip_lm_free(hip_lm *M)
@@ -364,15 +376,32 @@ size_t hip_lm_weight_bytes(const hip_lm *M)
 	return M ? M->weight_bytes : 0;
 }
 
+/* the rows kvcache_rotate keeps of a full cache of `size` rows
+ * (kvcache.c:36-39: the sliding window, else half the context), or 0 with
+ * an error when it would keep them all: a sliding window of at least the
+ * context, where the reference's next step writes its k/v row past the end
+ * of its cache */
+static size_t rotate_keep(const hip_lm *M, size_t size)
+{
+	size_t keep = M->window ? M->window : M->C / 2;
+	if (keep >= size) {
+		lm_err("lm: the cache is full (%zu rows) and kvcache_rotate would keep every row "
+		       "(sliding window %zu, context %zu): no room for the next step", size,
+		       M->window, M->C);
+		return 0;
+	}
+	return keep;
+}
+
 /* kvcache_rotate (kvcache.c:31-56) when the cache is full, before a step;
  * the host mirror of the counters is exact (one row per step) */
 static int rotate_if_full(hip_lm *M)
 {
 	if ((size_t)M->st.size < M->C)
 		return 1;
-	size_t keep = M->window ? M->window : M->C / 2;
-	if (keep > (size_t)M->st.size)
-		keep = (size_t)M->st.size;
+	const size_t keep = rotate_keep(M, (size_t)M->st.size);
+	if (!keep)
+		return 0;
 	const size_t drop = (size_t)M->st.size - keep;
 	const size_t slab = M->C * M->HL, slabs = M->L * M->KH;
 	if (drop > 0) {
@@ -583,16 +612,18 @@ int hip_lm_generate(hip_lm *M, const int *prompt, size_t n_prompt, size_t n_gen,
 	}
 	if (!ensure_io(M, n_prompt, steps) || !start_run(M, prompt, n_prompt))
 		return 0;
+	if (M->graph_gen != moe_gen(M)) {
+		drop_graphs(M);
+		M->graph_gen = moe_gen(M);
+	}
 	/* capture every step shape the run needs before its first launch: the
 	 * cache size of each step is known here (one row per step, and
 	 * kvcache_rotate's keep when full) */
 	{
 		size_t size = (size_t)M->st.size;
 		for (size_t i = 0; i < steps; i++) {
-			if (size >= M->C) {
-				size_t keep = M->window ? M->window : M->C / 2;
-				size = keep < size ? keep : size;
-			}
+			if (size >= M->C && !(size = rotate_keep(M, size)))
+				return 0;
 			const int head = i + 1 >= n_prompt;
 			const int nact = lm_attn_active((int)size, (int)M->window);
 			hipGraphExec_t *ge = head ? &M->g_head[nact] : &M->g_body[nact];
@@ -699,6 +730,7 @@ struct hip_lm_batch {
 	size_t prompt_cap, tokens_cap;
 	LmState st;
 	hipGraphExec_t *g_body, *g_head;
+	unsigned graph_gen; /* the MoE layers' scratch generation the graphs name */
 	hipEvent_t ev0, ev1;
 };
 
@@ -819,9 +851,9 @@ static int batch_rotate_if_full(hip_lm_batch *B)
 	hip_lm *M = B->M;
 	if ((size_t)B->st.size < M->C)
 		return 1;
-	size_t keep = M->window ? M->window : M->C / 2;
-	if (keep > (size_t)B->st.size)
-		keep = (size_t)B->st.size;
+	const size_t keep = rotate_keep(M, (size_t)B->st.size);
+	if (!keep)
+		return 0;
 	const size_t drop = (size_t)B->st.size - keep;
 	const size_t slab = M->C * M->HL, slabs = B->S * M->L * M->KH;
 	if (drop > 0) {
@@ -1035,14 +1067,16 @@ int hip_lm_batch_generate(hip_lm_batch *B, const int *prompts, size_t n_prompt, 
 	}
 	if (!batch_io(B, n_prompt, steps) || !batch_start(B, prompts, n_prompt))
 		return 0;
+	if (B->graph_gen != moe_gen(M)) { /* another batch grew the layers' scratch */
+		batch_drop_graphs(B);
+		B->graph_gen = moe_gen(M);
+	}
 	/* every step shape of the run, captured before its first launch */
 	{
 		size_t size = (size_t)B->st.size;
 		for (size_t i = 0; i < steps; i++) {
-			if (size >= M->C) {
-				size_t keep = M->window ? M->window : M->C / 2;
-				size = keep < size ? keep : size;
-			}
+			if (size >= M->C && !(size = rotate_keep(M, size)))
+				return 0;
 			const int head = i + 1 >= n_prompt;
 			const int nact = lm_attn_active((int)size, (int)M->window);
 			hipGraphExec_t *ge = head ? &B->g_head[nact] : &B->g_body[nact];

@@ -43,8 +43,11 @@ struct hip_moe_layer {
 	int path;           /* HIP_MOE_PATH_*, AUTO unless set */
 	int spin;           /* poll rounds of a decode-kernel wait, 0 = MOE_SPIN_DEFAULT */
 
-	/* scratch for up to cap_T tokens */
+	/* scratch for up to cap_T tokens; scratch_gen counts its reallocations
+	 * (a graph captured before one names freed buffers) */
 	size_t cap_T;
+	unsigned scratch_gen;
+	int used_static;    /* a hip_moe_ffn_dev_noalloc call ran on this layer */
 	float *d_logits;
 	uint32_t *d_ids;
 	float *d_w;
@@ -445,9 +448,15 @@ static int ensure_scratch(hip_moe_layer *L, size_t T, hipStream_t s)
 		HIPCHK(hipMalloc(&L->d_xh, T * L->E * 2), "hipMalloc(xh)");
 	}
 	L->cap_T = T;
+	L->scratch_gen++;
 	return 1;
 fail:
 	return 0;
+}
+
+unsigned moe_scratch_gen(const hip_moe_layer *L)
+{
+	return L ? L->scratch_gen : 0;
 }
 
 static int check_T(size_t T);
@@ -539,7 +548,9 @@ int hip_moe_status(hip_moe_layer *L, void *stream)
 		return -1;
 	}
 	int rc = check_and_reset(L, pick_stream(L, stream));
-	int rs = rc < 0 ? 0 : check_and_reset_static(L->device);
+	/* the device's static scratch only for a layer that ran there: another
+	 * caller of the no-allocation entry point may still be using it */
+	int rs = rc < 0 || !L->used_static ? 0 : check_and_reset_static(L->device);
 	return rc != 0 ? rc : rs;
 }
 
@@ -589,6 +600,7 @@ int hip_moe_ffn_dev_noalloc(hip_moe_layer *L, const float *d_x, float *d_out, si
 	}
 	uint32_t *ids = d_ids_out ? d_ids_out : (uint32_t *)(base + ids_off);
 	float *w = d_w_out ? d_w_out : (float *)(base + ids_off + P * sizeof(uint32_t));
+	L->used_static = 1;
 	LCHK(moe_launch_fused(L->wtype, d_x, L->d_router, d_router_bias, L->d_gate, L->d_up,
 			      L->d_down, L->gu_stride, L->down_stride, ids, w,
 			      (uint64_t *)(base + part_off), d_out, (uint32_t *)base, (int)T,
@@ -1044,7 +1056,8 @@ int hip_moe_qmat_mul(hip_moe_qmat *W, const float *x, size_t T, const float *add
 		W->cap_T = T;
 	}
 	if (W->qmm && T > W->split_T) { /* the host entry point may allocate */
-		HIPCHK(hipStreamSynchronize(s), "synchronize");
+		/* device-pointer calls on any stream may still read the old buffer */
+		HIPCHK(hipDeviceSynchronize(), "synchronize");
 		if (!qmat_split_alloc(W, T))
 			return 0;
 	}

@@ -51,6 +51,9 @@ int lm_launch_qkv(int wtype, const uint8_t *W, int N, int K, const float *a, con
  * sequences in lockstep: qkv, out, part and cnt hold nseq consecutive
  * copies, and sequence s's cache is kc/vc + s * cstride floats. */
 int lm_attn_chunks(int C, int window);
+/* which chunk merges a launch's partials: 2 = chunk 0 (the grid KH x nact x
+ * nseq is resident at once on the current device), 1 = the last to count in */
+int lm_attn_merge_form(int KH, int nact, int nseq);
 int lm_launch_attn(const float *qkv, const float *q_norm, const float *k_norm,
                    const float *freq, LmState *st, float *kc, float *vc, uint64_t *part,
                    uint32_t *cnt, float *out, int H, int KH, int C, int window,

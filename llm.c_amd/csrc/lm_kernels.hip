@@ -995,6 +995,14 @@ extern "C" int lm_attn_chunks(int C, int window)
 	return (span + LM_CHUNK - 1) / LM_CHUNK;
 }
 
+/* 2: the attention grid of kh kv heads, nact chunks and nseq sequences is
+ * resident at once and chunk 0 merges; 1: the last chunk to count in
+ * merges (the current device) */
+extern "C" int lm_attn_merge_form(int KH, int nact, int nseq)
+{
+	return (size_t)KH * nact * nseq <= 3 * (size_t)lm_cus() ? 2 : 1;
+}
+
 extern "C" int lm_launch_attn(const float *qkv, const float *q_norm, const float *k_norm,
 			      const float *freq, LmState *st, float *kc, float *vc,
 			      uint64_t *part, uint32_t *cnt, float *out, int H, int KH, int C,
@@ -1010,7 +1018,7 @@ extern "C" int lm_launch_attn(const float *qkv, const float *q_norm, const float
 	/* all of a chunk's rows loaded early while the grid fits 3 workgroups
 	 * per CU at once; larger grids load k early and v before its use (at
 	 * a register count that keeps more workgroups resident) */
-	const bool pf = (size_t)KH * nact * nseq <= 3 * (size_t)lm_cus();
+	const bool pf = lm_attn_merge_form(KH, nact, nseq) == 2;
 #define ATTN(GG)                                                                               \
 	do {                                                                                   \
 		if (pf)                                                                        \

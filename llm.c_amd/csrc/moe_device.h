@@ -39,8 +39,12 @@ __device__ static inline float f16_bits_to_f32(u32 h)
 
 /* One LDS-DMA load per lane (global_load_lds_dwordx4): 16 bytes from
  * sbase + voff into LDS at lds + 16 * lane (lds wave-uniform).  Issued from
- * inline assembly, so the compiler's own waits do not count it: callers
- * wait with wait_vm. */
+ * inline assembly, so the compiler's own waits do not count it (its
+ * conservative wait for every LDS-DMA write before any LDS read would undo
+ * the kernels' multi-stage buffering): callers wait with wait_vm.  The LDS
+ * address goes in as an m0 operand, so the compiler writes m0 itself and
+ * knows it does; the s_nop is the one wait state an m0 write needs before
+ * an LDS-DMA instruction. */
 __device__ static inline void dma_dwordx4(const void *sbase, u32 voff, u32 lds)
 {
 	/* the base is wave-uniform by contract: pinned to SGPRs (the builtin
@@ -48,11 +52,11 @@ __device__ static inline void dma_dwordx4(const void *sbase, u32 voff, u32 lds)
 	const uint64_t b = (uint64_t)(uintptr_t)sbase;
 	const uint64_t bs = (uint64_t)(u32)__builtin_amdgcn_readfirstlane((int)(u32)b) |
 			    ((uint64_t)(u32)__builtin_amdgcn_readfirstlane((int)(u32)(b >> 32)) << 32);
-	asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+	asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
 		     :
 		     : "v"(voff), "s"((const void *)(uintptr_t)bs),
-		       "s"(__builtin_amdgcn_readfirstlane(lds))
-		     : "memory", "m0");
+		       "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+		     : "memory");
 }
 
 /* wait until at most N of this wave's vector memory operations are pending

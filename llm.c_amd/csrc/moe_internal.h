@@ -139,6 +139,11 @@ int moe_launch_fused(int wtype, const float *x, const float *router, const float
                      uint64_t *part, float *out, uint32_t *sync, int T, int E, int EI, int NE,
                      int K, int renorm, int grid, int spin, void *stream);
 
+/* How many times the layer's scratch was (re)allocated: a HIP graph that
+ * was captured at another count names freed buffers and must be dropped. */
+struct hip_moe_layer;
+unsigned moe_scratch_gen(const struct hip_moe_layer *L);
+
 /* Record an error message for hip_moe_last_error (and print it). */
 void moe_set_error(const char *msg);
 

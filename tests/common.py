@@ -145,6 +145,19 @@ def _make_golden_module():
 
 
 @functools.lru_cache(maxsize=1)
+def batch_case(name: str):
+    """(model dict, prompts [nseq][n_prompt], batch case, fixture) of the
+    lockstep-batch fixture batch_<name>.npz; bc["case"] is the model case
+    tuple."""
+    mg = _make_golden_module()
+    md, _, case = mg.model_case(name)
+    g = golden(f"batch_{name}.npz")
+    assert mg.model_digest(md) == str(g["sha_model"]), "regenerated model differs from fixture"
+    bc = dict(mg.BATCH_CASES[name])
+    bc["case"] = case
+    return md, mg.batch_prompts(name, case[3]), bc, g
+
+
 def model_case(name: str):
     """(model dict, prompt, case tuple, fixture) of model fixture `name`,
     after checking the regenerated weights are the fixture's bytes."""

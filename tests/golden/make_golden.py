@@ -34,10 +34,14 @@ same bytes.  Outputs are the reference's own results:
                      on Q4_K/Q6_K experts (gate/up Q4_K with down Q6_K, as a
                      Q4_K_M file mixes them, and all Q6_K), and one expert's
                      fused_ffn_silu (nn.c:496-539) for both mixes
-  model_<case>.npz   the whole OLMoE model (olmoe.c:409-580): greedy tokens
-                     and per-step logits of the reference's olmoe_decode run
-                     over the prompt then n_gen steps, and of its generate
-                     order (one olmoe_prefill of the prompt, then decode)
+  model_<case>.npz   the whole OLMoE model (olmoe.c:409-580) or Mixtral model
+                     (llama.c:458-576): greedy tokens and per-step logits of
+                     the reference's olmoe_decode / llama_decode run over the
+                     prompt then n_gen steps, and (but for MODEL_DEC_ONLY) of
+                     its generate order (one prefill of the prompt, then
+                     decode)
+  batch_<case>.npz   several seeded prompts, each decoded by the reference
+                     alone (BATCH_CASES), for the lockstep batch
 
 `python tests/golden/make_golden.py qmat` writes qmat.npz alone, `... kquant`
 kquant.npz alone, `... model` the model fixtures alone.
@@ -262,6 +266,11 @@ KQ_LAYERS = {
     "olmoe_q4k_q6k": (hipmoe.Q4_K | hipmoe.Q6_K << 8, 2048, 1024, 64, 8, 0, 4),
     "olmoe_q6k": (hipmoe.Q6_K, 2048, 1024, 64, 8, 0, 2),
     "mixtral_q4k_q6k": (hipmoe.Q4_K | hipmoe.Q6_K << 8, 4096, 14336, 8, 2, 1, 2),
+    # d_model of 5 super-blocks (128 % 5 != 0: the gate/up kernel's rows per
+    # workgroup do not divide its 128 lanes) and d_ff of 6 (the down
+    # kernel's last chunk of super-blocks is partial), both type mixes
+    "ragged_q4k_q6k": (hipmoe.Q4_K | hipmoe.Q6_K << 8, 1280, 1536, 16, 4, 0, 3),
+    "ragged_q6k_q4k": (hipmoe.Q6_K | hipmoe.Q4_K << 8, 1280, 1536, 16, 4, 1, 2),
 }
 
 
@@ -328,13 +337,53 @@ MODEL_CASES = {
     "olmoe_full": (16, 2048, 16, 50304, 64, 8, 1024, 2048, hipmoe.Q8_0, 0.0, 4, 4, 16),
     "mixtral_small": (2, 2048, 16, 512, 8, 2, 1024, 32, hipmoe.Q4_0, 0.1, 8, 40, 1),
     "mixtral_2l": (2, 4096, 32, 32000, 8, 2, 14336, 64, hipmoe.Q4_0, 0.0, 4, 4, 16),
+    # caches longer than one 64-row attention block (nn.c:542,570-641 in
+    # Mixtral's flash_attention; OLMoE's masked softmax over AT rows,
+    # olmoe.c:286-320): 308 positions in a 256-row context, so up to four
+    # blocks, one kvcache_rotate at 256 (OLMoE keeps 128, the Mixtral one its
+    # sliding window of 200, which straddles block boundaries as it moves)
+    "olmoe_long": (2, 1024, 8, 512, 64, 8, 512, 256, hipmoe.Q8_0, 0.1, 8, 300, 4),
+    "mixtral_long": (2, 2048, 16, 512, 8, 2, 1024, 256, hipmoe.Q4_0, 0.1, 8, 300, 4),
+    # the full OLMoE-1B-7B shape over 300 positions (five blocks), and two
+    # layers of the Mixtral-8x7B shape after a 1024-token prompt (seventeen
+    # blocks): the benchmarked lengths
+    "olmoe_full_long": (16, 2048, 16, 50304, 64, 8, 1024, 2048, hipmoe.Q8_0, 0.0, 4, 296, 64),
+    "mixtral_2l_long": (2, 4096, 32, 32000, 8, 2, 14336, 4096, hipmoe.Q4_0, 0.0, 1024, 32, 64),
 }
-# Mixtral cases: (kv heads, sliding window, rope theta)
+# Mixtral cases: (kv heads, sliding window, rope theta).  The window stays
+# at least C - 64: with a longer cache, once the first 64-row block lies
+# wholly outside the window the reference's flash_attention computes
+# expf(-inf - -inf) for it (nn.c:603-608) and every later logit is NaN
+# (C = 256, window 100: from position 163 on).
 MIXTRAL_EXTRA = {
     "mixtral_small": (4, 20, 1e6),
     "mixtral_2l": (8, 0, 1e6),
+    "mixtral_long": (4, 200, 1e6),
+    "mixtral_2l_long": (8, 0, 1e6),
 }
+# cases written in decode order only (one olmoe_decode / llama_decode per
+# prompt id); the others also in generate order (one prefill of the prompt)
+MODEL_DEC_ONLY = ("olmoe_full_long", "mixtral_2l_long")
 MODEL_TOPN = 32
+
+# Several sequences at once, for the lockstep batch (hip_lm_batch_*): nseq
+# prompts of n_prompt ids (sequence s: synth_prompt(SEED + 101 + s)), each
+# decoded by the reference alone, then n_gen greedy steps; the reference's
+# logits are written for the sequences in `check` (every sequence is
+# independent of the others).  Sizes put the attention grid (kv heads x
+# blocks x sequences) past three workgroups per CU of a 256-CU device with
+# four blocks per kv head.
+BATCH_CASES = {
+    "olmoe_long": dict(nseq=26, n_prompt=200, n_gen=6, check=(0, 13, 25)),
+    "mixtral_long": dict(nseq=52, n_prompt=200, n_gen=4, check=(0, 26, 51)),
+}
+
+
+def batch_prompts(name: str, V: int) -> np.ndarray:
+    import hiplm
+    bc = BATCH_CASES[name]
+    return np.stack([hiplm.synth_prompt(SEED + 101 + s, bc["n_prompt"], V)
+                     for s in range(bc["nseq"])])
 
 
 def model_case(name: str):
@@ -384,7 +433,8 @@ def model_goldens(R, names):
         L, E, H, V, NE, K, EI, Cx, wt, nstd, n_prompt, n_gen, stride = case
         tab = model_table(md)
         fx = dict(seed=SEED, prompt=prompt, sha_model=model_digest(md), stride=stride)
-        for mode, prefill in (("dec", 0), ("pre", 1)):
+        modes = (("dec", 0),) if name in MODEL_DEC_ONLY else (("dec", 0), ("pre", 1))
+        for mode, prefill in modes:
             if md["arch"] == "olmoe":
                 h = R.ref_olmoe_model_new(L, E, H, V, NE, K, EI, Cx, md["theta"], wt, tab)
                 run, free = R.ref_olmoe_model_run, R.ref_olmoe_model_free
@@ -401,9 +451,45 @@ def model_goldens(R, names):
             fx[f"{mode}_logits"] = np.ascontiguousarray(lg[:, ::stride])
             fx[f"{mode}_top_ids"] = top
             fx[f"{mode}_top_logits"] = np.take_along_axis(lg, top, axis=1)
-            print(f"model {name} [{mode}]: tokens {toks.tolist()}")
+            assert np.isfinite(lg).all(), f"{name} [{mode}]: non-finite reference logits"
+            print(f"model {name} [{mode}]: tokens {toks.tolist()}", flush=True)
         np.savez_compressed(os.path.join(HERE, f"model_{name}.npz"), **fx)
+        if name in BATCH_CASES:
+            batch_goldens(R, name, md, case, tab)
         del md
+
+
+def batch_goldens(R, name, md, case, tab):
+    """batch_<name>.npz: the reference's decode of each checked sequence of
+    BATCH_CASES[name] alone (logits at every stride-th id, each step's top
+    MODEL_TOPN, greedy tokens)."""
+    L, E, H, V, NE, K, EI, Cx, wt, nstd, _, _, stride = case
+    bc = BATCH_CASES[name]
+    prompts = batch_prompts(name, V)
+    fx = dict(seed=SEED, sha_model=model_digest(md), sha_prompts=sha(prompts), stride=stride,
+              check=np.asarray(bc["check"], np.int32), nseq=bc["nseq"],
+              n_prompt=bc["n_prompt"], n_gen=bc["n_gen"])
+    for s in bc["check"]:
+        if md["arch"] == "olmoe":
+            h = R.ref_olmoe_model_new(L, E, H, V, NE, K, EI, Cx, md["theta"], wt, tab)
+            run, free = R.ref_olmoe_model_run, R.ref_olmoe_model_free
+        else:
+            h = R.ref_llama_model_new(L, E, H, md["KH"], V, NE, K, EI, Cx, md["theta"],
+                                      md["window"], wt, tab)
+            run, free = R.ref_llama_model_run, R.ref_llama_model_free
+        n_gen = bc["n_gen"]
+        lg = np.empty((n_gen + 1, V), np.float32)
+        toks = np.empty(n_gen + 1, np.int32)
+        run(h, p(prompts[s]), bc["n_prompt"], 0, n_gen, p(lg), p(toks))
+        free(h)
+        assert np.isfinite(lg).all()
+        top = np.argsort(-lg, axis=1, kind="stable")[:, :MODEL_TOPN].astype(np.int32)
+        fx[f"s{s}_tokens"] = toks
+        fx[f"s{s}_logits"] = np.ascontiguousarray(lg[:, ::stride])
+        fx[f"s{s}_top_ids"] = top
+        fx[f"s{s}_top_logits"] = np.take_along_axis(lg, top, axis=1)
+        print(f"batch {name} sequence {s}: tokens {toks.tolist()}", flush=True)
+    np.savez_compressed(os.path.join(HERE, f"batch_{name}.npz"), **fx)
 
 
 def main():

@@ -132,7 +132,8 @@ def _kq_layer(name):
     return kq_layer(name)
 
 
-@pytest.mark.parametrize("name", ["olmoe_q4k_q6k", "olmoe_q6k", "mixtral_q4k_q6k"])
+@pytest.mark.parametrize("name", ["olmoe_q4k_q6k", "olmoe_q6k", "mixtral_q4k_q6k",
+                                  "ragged_q4k_q6k", "ragged_q6k_q4k"])
 def test_gpu_kq_layer_vs_reference_golden(name):
     """hip_moe_upload_typed / hip_moe_ffn on K-quant experts: outputs equal the
     compiled reference's moe_ffn bit for bit, ids and weights the oracle's."""

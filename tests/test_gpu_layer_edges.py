@@ -219,3 +219,49 @@ def test_gpu_scratch_growth_refused_under_capture():
         H.free(d_x)
         H.free(d_o)
         lay.free()
+
+
+# --------------------------------------------------------------------------
+# the grouped path with the tokens crowded onto one or two experts
+# --------------------------------------------------------------------------
+
+_skew_layer = {}
+
+
+def skew_layer():
+    """A reduced Mixtral-shaped layer (d_model 2048, d_ff 1024, 8 experts,
+    top-2 with renorm, Q4_0): 32-row tiles at these token counts."""
+    if "lw" not in _skew_layer:
+        _skew_layer["lw"] = hipmoe.synth_layer(SEED, 5, hipmoe.Q4_0, 2048, 1024, 8, 0.02, None)
+    return _skew_layer["lw"]
+
+
+@pytest.mark.parametrize("T", [52, 100])
+@pytest.mark.parametrize("case", ["two_experts", "near_identical_tokens"])
+def test_gpu_grouped_path_crowded_experts_vs_oracle(case, T):
+    """Every token on the same two experts (a router bias), or tokens that
+    differ only slightly (as a model's hidden states can): experts of
+    T pairs span several 32-row tiles, others have none."""
+    lw = skew_layer()
+    E, NE, K = 2048, 8, 2
+    x = hipmoe.synth_input(SEED, 830 + T, T, E)
+    bias = None
+    if case == "two_experts":
+        bias = np.zeros(NE, np.float32)
+        bias[3], bias[5] = 50.0, 40.0
+    else:
+        x = (x[:1] + 0.02 * x).astype(np.float32)
+    say(f"grouped path, crowded experts: {case} T={T}")
+    lay = hipmoe.MoeLayer.from_synth(lw, K, True)
+    try:
+        lay.set_path(hipmoe.PATH_GROUPED)
+        assert lay.path_for(T) == hipmoe.PATH_GROUPED
+        out, ids, w = lay.ffn(x, bias)
+    finally:
+        lay.free()
+    oout, oids, ow, _, _ = oracle.moe_ffn(x, lw, K, True, bias)
+    counts = np.bincount(oids.reshape(-1).astype(np.int64), minlength=NE)
+    err = rel_l2(out, oout)
+    say(f"  pairs per expert {counts.tolist()}: rel L2 {err:.3e}")
+    assert np.array_equal(ids, oids) and np.array_equal(bits(w), bits(ow))
+    assert err <= REL_L2_TOL

@@ -214,7 +214,8 @@ def kq_layer(name):
     return (wt, E, EI, NE, K, renorm, T), lw, x, g[f"{name}_out"]
 
 
-@pytest.mark.parametrize("name", ["olmoe_q4k_q6k", "olmoe_q6k",
+@pytest.mark.parametrize("name", ["olmoe_q4k_q6k", "olmoe_q6k", "ragged_q4k_q6k",
+                                  "ragged_q6k_q4k",
                                   pytest.param("mixtral_q4k_q6k", marks=pytest.mark.slow)])
 def test_oracle_kq_layer_vs_reference(name):
     """The oracle's moe_ffn on K-quant experts (the Q8_K gate/up dots, the

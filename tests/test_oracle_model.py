@@ -85,3 +85,60 @@ def test_model_oracle_matches_reference_decode_bits_mixtral_layer_shape():
     assert np.array_equal(bits(lg[:, ::stride]), bits(g["dec_logits"]))
     top = np.take_along_axis(lg, g["dec_top_ids"].astype(np.int64), axis=1)
     assert np.array_equal(bits(top), bits(g["dec_top_logits"]))
+
+
+# --------------------------------------------------------------------------
+# caches longer than one 64-row attention block
+# --------------------------------------------------------------------------
+
+def _check_long(name):
+    toks, lg, g, stride = _run(name)
+    assert np.array_equal(toks, g["dec_tokens"])
+    assert np.array_equal(bits(lg[:, ::stride]), bits(g["dec_logits"]))
+    top = np.take_along_axis(lg, g["dec_top_ids"].astype(np.int64), axis=1)
+    assert np.array_equal(bits(top), bits(g["dec_top_logits"]))
+    assert np.array_equal(toks, g["pre_tokens"])
+    for s in range(lg.shape[0]):
+        assert rel_l2(lg[s, ::stride], g["pre_logits"][s]) <= 1e-5
+
+
+def test_model_oracle_matches_reference_decode_bits_olmoe_long_cache():
+    """308 positions in a 256-row context: OLMoE's masked softmax over up to
+    256 cache rows, one kvcache_rotate (keeps 128), RoPE positions restarting
+    at the cache size after it (olmoe.c:509-520)."""
+    _check_long("olmoe_long")
+
+
+def test_model_oracle_matches_reference_decode_bits_mixtral_long_cache():
+    """The multi-block flash_attention (nn.c:570-641: up to four 64-row
+    blocks, rescaled by each block's maximum) with a sliding window of 200
+    that straddles block boundaries, grouped-query heads (16 / 4), and one
+    kvcache_rotate that keeps the window."""
+    _check_long("mixtral_long")
+
+
+@pytest.mark.parametrize("name", ["olmoe_long", "mixtral_long"])
+def test_batch_fixture_prompts_regenerate(name):
+    """The lockstep-batch fixtures' prompts and model are the seeded ones."""
+    import hashlib
+    from common import batch_case
+    md, prompts, bc, g = batch_case(name)
+    assert hashlib.sha256(np.ascontiguousarray(prompts).tobytes()).hexdigest() == \
+        str(g["sha_prompts"])
+
+
+def test_model_oracle_matches_reference_batch_sequence_long_prompt():
+    """One checked sequence of the lockstep-batch fixture (a 200-id prompt,
+    then greedy steps) decoded by the model oracle alone equals the
+    reference's decode bit for bit."""
+    from common import batch_case
+    md, prompts, bc, g = batch_case("olmoe_long")
+    s = int(g["check"][-1])
+    L, E, H, V, NE, K, EI, Cx, wt, nstd, _, _, stride = bc["case"]
+    m = oracle.OlmoeModel(md, Cx, hiplm.ptr_table(md))
+    try:
+        toks, lg = m.run(prompts[s], int(g["n_gen"]))
+    finally:
+        m.free()
+    assert np.array_equal(toks, g[f"s{s}_tokens"])
+    assert np.array_equal(bits(lg[:, ::stride]), bits(g[f"s{s}_logits"]))
