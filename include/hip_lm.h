@@ -85,13 +85,28 @@ hip_lm *hip_lm_upload(const hip_lm_desc *d);
 int hip_lm_decode(hip_lm *M, int tok, float *logits, int *next);
 
 /*
+ * olmoe_prefill / llama_prefill (olmoe.c:504-508, llama.c:560-564): the n
+ * prompt ids as one forward at the model's position (causal attention over
+ * the cache and the new rows; every layer on n rows), then the lm_head
+ * product of the last row: logits[vocab] (host, optional) and the greedy
+ * pick *next (optional), which the next hip_lm_decode does not need (pass
+ * it as that step's token).  The cache grows by n rows; the ids must fit
+ * (cache rows in use + n <= context; the reference's prefill does not
+ * rotate and writes past its cache otherwise): 0 with an error if not.
+ * Synchronous.
+ */
+int hip_lm_prefill(hip_lm *M, const int *prompt, size_t n, float *logits, int *next);
+
+/*
  * olmoe_generate without tokenizer and EOS stop (olmoe.c:522-600): the
- * prompt ids one step each, then n_gen greedy steps; tokens[0..n_gen] are
- * the n_gen + 1 picks (after the prompt, and after each generated token).
- * Every step runs from device memory (token, position and cache row are
- * device counters; steps replay captured HIP graphs), with no host round
- * trip until the end.  decode_ms (optional): device time of the n_gen
- * generated steps.  Continues from the model's position.
+ * prompt as one prefill (as hip_lm_prefill; a prompt of one id, or one that
+ * does not fit the cache, runs one step per id instead), then n_gen greedy
+ * steps; tokens[0..n_gen] are the n_gen + 1 picks (after the prompt, and
+ * after each generated token).  Every step runs from device memory (token,
+ * position and cache row are device counters; steps replay captured HIP
+ * graphs), with no host round trip until the end.  decode_ms (optional):
+ * device time of the n_gen generated steps.  Continues from the model's
+ * position.
  */
 int hip_lm_generate(hip_lm *M, const int *prompt, size_t n_prompt, size_t n_gen, int *tokens,
                     float *decode_ms);
@@ -103,6 +118,16 @@ int hip_lm_generate(hip_lm *M, const int *prompt, size_t n_prompt, size_t n_gen,
  * (its tensor_trace hooks, tensor_trace.c, serve the same purpose).
  */
 int hip_lm_trace(hip_lm *M, float *moe_in, uint32_t *ids, float *w);
+
+/*
+ * Force every layer's MoE path (HIP_MOE_PATH_*, as hip_moe_set_path; AUTO
+ * restores the choice by token count).  A forced path applies to every
+ * call, the decode steps' too; HIP_MOE_PATH_GEMV keeps a prefill's MoE
+ * layers in fp32 where the grouped path's f16 operands would move them by
+ * ~5e-4.  The model's lockstep batches take it as well.  No counterpart
+ * in the reference.  1 = ok.
+ */
+int hip_lm_set_moe_path(hip_lm *M, int path);
 
 /* Empty the KV cache and reset the position (a fresh olmoe_load's state). */
 int hip_lm_reset(hip_lm *M);
@@ -137,11 +162,16 @@ hip_lm_batch *hip_lm_batch_new(hip_lm *M, size_t nseq);
 int hip_lm_batch_decode(hip_lm_batch *B, const int *toks, float *logits, int *next);
 
 /*
- * hip_lm_generate for every sequence: prompts[nseq][n_prompt] one step
- * each, then n_gen greedy steps; tokens[nseq][n_gen + 1] receive each
- * sequence's picks after its prompt and after each generated token.  Steps
- * replay captured HIP graphs with no host round trip.  decode_ms
- * (optional): device time of the n_gen generated steps.
+ * hip_lm_generate for every sequence: prompts[nseq][n_prompt] as prefills
+ * (each sequence's prompt one forward into its own cache, as
+ * hip_lm_prefill; sequences in groups of about 2048 prompt rows per
+ * launch; a prompt of one id, or one that does not fit the caches, runs one
+ * step per id instead), then n_gen greedy steps; tokens[nseq][n_gen + 1]
+ * receive each sequence's picks after its prompt and after each generated
+ * token.  Steps replay captured HIP graphs with no host round trip.
+ * decode_ms (optional): device time of the n_gen generated steps.  The
+ * prefill uses the model's prefill rows: the model and its batches never
+ * run at the same time.
  */
 int hip_lm_batch_generate(hip_lm_batch *B, const int *prompts, size_t n_prompt, size_t n_gen,
                           int *tokens, float *decode_ms);

@@ -25,6 +25,9 @@
 #include <stdlib.h>
 #include <string.h>
 
+/* rows of one prefill launch group of a lockstep batch's prompts */
+#define PF_GROUP_ROWS 2048
+
 struct lm_layer {
 	float *attn_norm, *q_norm, *k_norm, *ffn_norm;
 	uint8_t *wqkv; /* [q rows | k rows | v rows][E] blocks */
@@ -65,7 +68,15 @@ struct hip_lm {
 	int nch;
 	hipGraphExec_t *g_body, *g_head;
 	unsigned graph_gen; /* the MoE layers' scratch generation the graphs name */
+	unsigned path_gen;  /* forced MoE path changes (hip_lm_set_moe_path) */
 	hipEvent_t ev0, ev1;
+
+	/* prefill: a prompt of up to pf_cap rows in one forward, rows [T][.] */
+	size_t pf_cap, pf_heads; /* rows, and sequences whose last rows take the lm_head */
+	float *d_pf_h0, *d_pf_h1, *d_pf_x, *d_pf_qkv, *d_pf_q, *d_pf_attn, *d_pf_min,
+		*d_pf_mout;
+	void *d_pf_split; /* the matrix-core products' partial sums */
+	LmState *d_pst;   /* step 0 of one-id prompts: row s takes prompt[s] */
 };
 
 static void lm_err(const char *fmt, ...)
@@ -126,10 +137,23 @@ static void drop_graphs(hip_lm *M)
  * after which step graphs captured before name freed buffers */
 static unsigned moe_gen(const hip_lm *M)
 {
-	unsigned g = 0;
+	unsigned g = M->path_gen * 1000003u; /* a forced path changes the launches */
 	for (size_t l = 0; M->ly && l < M->L; l++)
 		g += moe_scratch_gen(M->ly[l].moe);
 	return g;
+}
+
+static void free_prefill(hip_lm *M)
+{
+	void *bufs[] = {M->d_pf_h0,   M->d_pf_h1,  M->d_pf_x,    M->d_pf_qkv, M->d_pf_q,
+			M->d_pf_attn, M->d_pf_min, M->d_pf_mout, M->d_pf_split};
+	for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
+		hipFree(bufs[i]);
+	M->d_pf_h0 = M->d_pf_h1 = M->d_pf_x = M->d_pf_qkv = M->d_pf_q = M->d_pf_attn = NULL;
+	M->d_pf_min = M->d_pf_mout = NULL;
+	M->d_pf_split = NULL;
+	M->pf_cap = 0;
+	M->pf_heads = 0;
 }
 
 void hip_lm_free(hip_lm *M)
@@ -137,6 +161,8 @@ void hip_lm_free(hip_lm *M)
 	if (!M)
 		return;
 	drop_graphs(M);
+	free_prefill(M);
+	hipFree(M->d_pst);
 	free(M->g_body);
 	free(M->g_head);
 	if (M->ly) {
@@ -363,12 +389,36 @@ hip_lm *hip_lm_upload(const hip_lm_desc *d)
 	/* epoch 1: tags never match the zeroed gather buffers */
 	M->st.epoch = 1;
 	HIPCHK(hipMemcpy(M->d_st, &M->st, sizeof(LmState), hipMemcpyHostToDevice), "set state");
+	{ /* the prefill rows' embedding lookups: row s takes prompt[s] */
+		LmState ps;
+		memset(&ps, 0, sizeof(ps));
+		ps.n_prompt = 1;
+		HIPCHK(hipMalloc((void **)&M->d_pst, sizeof(LmState)), "hipMalloc(prefill state)");
+		HIPCHK(hipMemcpy(M->d_pst, &ps, sizeof(ps), hipMemcpyHostToDevice),
+		       "set prefill state");
+	}
 	HIPCHK(hipDeviceSynchronize(), "synchronize after upload");
 	return M;
 fail:
 	free(stage);
 	hip_lm_free(M);
 	return NULL;
+}
+
+int hip_lm_set_moe_path(hip_lm *M, int path)
+{
+	if (!M) {
+		lm_err("lm_set_moe_path: NULL model");
+		return 0;
+	}
+	HIPCHK(hipStreamSynchronize(M->stream), "synchronize");
+	for (size_t l = 0; l < M->L; l++)
+		if (!hip_moe_set_path(M->ly[l].moe, path))
+			return 0;
+	M->path_gen++; /* step graphs (the model's and its batches') hold the old launches */
+	return 1;
+fail:
+	return 0;
 }
 
 size_t hip_lm_weight_bytes(const hip_lm *M)
@@ -550,6 +600,200 @@ static int check_token(const hip_lm *M, int tok)
 	return 1;
 }
 
+/* ---------------------------------------------------------------------- */
+/* prefill                                                                */
+/* ---------------------------------------------------------------------- */
+
+/* rows for a prefill of T rows in all (nseq sequences' last rows through
+ * the lm_head) and the MoE layers' scratch for T tokens (synchronous, never
+ * under capture; the layers count the regrowth, which the step graphs
+ * check before their next replay) */
+static int ensure_prefill(hip_lm *M, size_t T, size_t nseq)
+{
+	if (T <= M->pf_cap && nseq <= M->pf_heads)
+		return 1;
+	if (T < M->pf_cap)
+		T = M->pf_cap;
+	if (nseq < M->pf_heads)
+		nseq = M->pf_heads;
+	HIPCHK(hipStreamSynchronize(M->stream), "synchronize before growing prefill rows");
+	free_prefill(M);
+	const size_t E = M->E, NQKV = M->EQ + 2 * M->EKV;
+	HIPCHK(hipMalloc((void **)&M->d_pf_h0, T * E * 4), "hipMalloc(prefill h0)");
+	HIPCHK(hipMalloc((void **)&M->d_pf_h1, T * E * 4), "hipMalloc(prefill h1)");
+	HIPCHK(hipMalloc((void **)&M->d_pf_x, T * E * 4), "hipMalloc(prefill x)");
+	HIPCHK(hipMalloc((void **)&M->d_pf_min, T * E * 4), "hipMalloc(prefill moe_in)");
+	HIPCHK(hipMalloc((void **)&M->d_pf_mout, T * E * 4), "hipMalloc(prefill moe_out)");
+	HIPCHK(hipMalloc((void **)&M->d_pf_qkv, T * NQKV * 4), "hipMalloc(prefill qkv)");
+	HIPCHK(hipMalloc((void **)&M->d_pf_q, T * M->EQ * 4), "hipMalloc(prefill q)");
+	HIPCHK(hipMalloc((void **)&M->d_pf_attn, T * M->EQ * 4), "hipMalloc(prefill attn)");
+	{ /* the partial sums of the largest of the three products: q/k/v and
+	   * output over T rows, the lm_head over the nseq last rows */
+		size_t wb = moe_qmm_work_bytes((int)T, (int)NQKV, (int)E);
+		const size_t w2 = moe_qmm_work_bytes((int)T, (int)E, (int)M->EQ);
+		const size_t w3 = moe_qmm_work_bytes((int)nseq, (int)M->V, (int)E);
+		wb = wb > w2 ? wb : w2;
+		wb = wb > w3 ? wb : w3;
+		if (wb)
+			HIPCHK(hipMalloc(&M->d_pf_split, wb), "hipMalloc(prefill partial sums)");
+	}
+	for (size_t l = 0; l < M->L; l++)
+		if (!hip_moe_reserve(M->ly[l].moe, T))
+			return 0;
+	M->pf_cap = T;
+	M->pf_heads = nseq;
+	return 1;
+fail:
+	free_prefill(M);
+	return 0;
+}
+
+/* out[T][N] = add + x[T][K] . W^T (add NULL or [T][N]): the matrix cores
+ * where K suits them, else the per-token product */
+static int rows_product(hip_lm *M, const uint8_t *W, int N, int K, const float *x, int T,
+			const float *add, float *out, hipStream_t s)
+{
+	const int wt = M->wtype;
+	if (moe_qmm_supported(wt, K))
+		LCHK(moe_launch_qmm(wt, W, N, K, x, T, add, add != NULL, out, M->d_pf_split, s),
+		     "prefill product");
+	else
+		LCHK(moe_launch_qgemv(wt, W, N, K, x, T, add, add != NULL, out, 0, s),
+		     "prefill product");
+	return 1;
+}
+
+/*
+ * olmoe_prefill / llama_prefill (olmoe.c:409-508, llama.c:458-564) of nseq
+ * sequences at once: T ids each (sequence z's at d_ids + z * T, its cache
+ * at kc / vc + z * cstride), all at cache size `size` and position `pos`,
+ * as one forward of nseq * T rows: every layer on the rows (rms_norm rows,
+ * the stacked q/k/v product, q/k norms and RoPE with the new k/v rows into
+ * the caches, causal attention over each sequence's cache, the output
+ * product with the residual, rms_norm, the MoE layer at nseq * T tokens),
+ * then each sequence's last row: the final rms_norm, the lm_head product
+ * into logits [nseq][V] and the greedy pick into btok[z] and, when tokens
+ * is not NULL, tokens[z * tstride].  Enqueued on `s`; the caller advances
+ * the position and cache size by T.
+ */
+static int enqueue_prefill(hip_lm *M, int size, int pos, size_t T, size_t nseq,
+			   const int *d_ids, float *kc, float *vc, size_t cstride, float *logits,
+			   int *btok, int *tokens, int tstride, hipStream_t s)
+{
+	const int wt = M->wtype, E = (int)M->E, NQKV = (int)(M->EQ + 2 * M->EKV);
+	const int n = (int)(T * nseq);
+	int ok = 0;
+	for (size_t l = 0; l < M->L; l++) {
+		struct lm_layer *y = &M->ly[l];
+		const size_t co = l * M->KH * M->C * M->HL;
+		/* layer 0: the ids' embedding rows; then h0 = h1 + moe_out */
+		if (lm_launch_norm_rows(wt, n, E, l ? M->d_pf_h1 : NULL, l ? M->d_pf_mout : NULL,
+					y->attn_norm, M->d_pf_h0, M->d_pf_x, M->d_wte, M->d_pst, d_ids,
+					d_ids, s) != 0) {
+			lm_err("prefill norm: launch failed");
+			goto out;
+		}
+		if (!rows_product(M, y->wqkv, NQKV, E, M->d_pf_x, n, NULL, M->d_pf_qkv, s))
+			goto out;
+		if (lm_launch_pf_qk(M->d_pf_qkv, y->q_norm, y->k_norm, M->d_freq, kc + co, vc + co,
+				    M->d_pf_q, (int)M->H, (int)M->KH, (int)M->C, size, pos, (int)T,
+				    (int)nseq, cstride, s) != 0 ||
+		    lm_launch_pf_attn(M->d_pf_q, kc + co, vc + co, M->d_pf_attn, (int)M->H,
+				      (int)M->KH, (int)M->C, size, (int)T, (int)M->window, M->scale,
+				      M->arch != HIP_LM_OLMOE, (int)nseq, cstride, s) != 0) {
+			lm_err("prefill attention: launch failed");
+			goto out;
+		}
+		/* h1 = h0 + attn . Wo^T, moe_in = rms_norm(h1) */
+		if (!rows_product(M, y->wo, E, (int)M->EQ, M->d_pf_attn, n, M->d_pf_h0, M->d_pf_h1,
+				  s))
+			goto out;
+		if (lm_launch_norm_rows(wt, n, E, M->d_pf_h1, NULL, y->ffn_norm, NULL, M->d_pf_min,
+					NULL, M->d_pst, NULL, NULL, s) != 0) {
+			lm_err("prefill MoE norm: launch failed");
+			goto out;
+		}
+		if (!hip_moe_ffn_dev(y->moe, M->d_pf_min, M->d_pf_mout, (size_t)n, NULL, NULL, NULL, s))
+			goto out;
+	}
+	{ /* each sequence's last row (gathered where there are several):
+	   * rms_norm(h1 + moe_out) . lm_head^T and the pick */
+		const size_t last = (T - 1) * M->E;
+		const float *h1 = M->d_pf_h1 + last, *mo = M->d_pf_mout + last;
+		if (nseq > 1) { /* into the first nseq of two spent [rows][E] buffers */
+			const size_t pitch = T * M->E * 4;
+			HIPCHK(hipMemcpy2DAsync(M->d_pf_h0, M->E * 4, h1, pitch, M->E * 4, nseq,
+						hipMemcpyDeviceToDevice, s), "gather last rows");
+			HIPCHK(hipMemcpy2DAsync(M->d_pf_min, M->E * 4, mo, pitch, M->E * 4, nseq,
+						hipMemcpyDeviceToDevice, s), "gather last rows");
+			h1 = M->d_pf_h0;
+			mo = M->d_pf_min;
+		}
+		if (lm_launch_norm_rows(wt, (int)nseq, E, h1, mo, M->d_onorm, NULL, M->d_pf_x, NULL,
+					M->d_pst, NULL, NULL, s) != 0) {
+			lm_err("prefill final norm: launch failed");
+			goto out;
+		}
+		if (!rows_product(M, M->d_head, (int)M->V, E, M->d_pf_x, (int)nseq, NULL, logits, s))
+			goto out;
+		if (lm_launch_pick_rows(logits, (int)nseq, (int)M->V, M->d_pst, btok, tokens,
+					tstride, s) != 0) {
+			lm_err("prefill pick: launch failed");
+			goto out;
+		}
+	}
+	ok = 1;
+fail:
+out:
+	return ok;
+}
+
+/* a prefill of n ids fits the cache from the model's current size (the
+ * reference's prefill does not rotate: past the context it writes beyond
+ * its cache) */
+static int prefill_fits(const hip_lm *M, size_t n)
+{
+	return (size_t)M->st.size + n <= M->C;
+}
+
+int hip_lm_prefill(hip_lm *M, const int *prompt, size_t n, float *logits, int *next)
+{
+	if (!M || !prompt || n == 0) {
+		lm_err("lm_prefill: NULL argument or empty prompt");
+		return 0;
+	}
+	for (size_t i = 0; i < n; i++)
+		if (!check_token(M, prompt[i]))
+			return 0;
+	if (!prefill_fits(M, n)) {
+		lm_err("lm_prefill: %zu ids from cache row %d do not fit the context of %zu", n,
+		       M->st.size, M->C);
+		return 0;
+	}
+	if (!ensure_io(M, n, 1) || !ensure_prefill(M, n, 1))
+		return 0;
+	HIPCHK(hipStreamSynchronize(M->stream), "synchronize");
+	HIPCHK(hipMemcpy(M->d_prompt, prompt, n * sizeof(int), hipMemcpyHostToDevice),
+	       "copy prompt");
+	if (!enqueue_prefill(M, M->st.size, M->st.pos, n, 1, M->d_prompt, M->d_kc, M->d_vc, 0,
+			     M->d_logits, &M->d_st->tok, NULL, 0, M->stream))
+		return 0;
+	M->st.pos += (int)n;
+	M->st.size += (int)n;
+	if (!check_errors(M, "lm_prefill"))
+		return 0;
+	/* step and prompt counters belong to a run; the device's token stays */
+	HIPCHK(hipMemcpy(M->d_st, &M->st, 4 * sizeof(int), hipMemcpyHostToDevice), "set state");
+	if (logits)
+		HIPCHK(hipMemcpy(logits, M->d_logits, M->V * 4, hipMemcpyDeviceToHost), "copy logits");
+	if (next)
+		HIPCHK(hipMemcpy(next, &M->d_st->tok, sizeof(int), hipMemcpyDeviceToHost),
+		       "read pick");
+	return 1;
+fail:
+	return 0;
+}
+
 int hip_lm_decode(hip_lm *M, int tok, float *logits, int *next)
 {
 	if (!M) {
@@ -610,8 +854,27 @@ int hip_lm_generate(hip_lm *M, const int *prompt, size_t n_prompt, size_t n_gen,
 		lm_err("lm_generate: too many steps");
 		return 0;
 	}
-	if (!ensure_io(M, n_prompt, steps) || !start_run(M, prompt, n_prompt))
+	/* the prompt as one forward (olmoe_generate's olmoe_prefill,
+	 * olmoe.c:556-558) where it fits the cache; else a step per id */
+	const int pf = n_prompt >= 2 && prefill_fits(M, n_prompt);
+	if (!ensure_io(M, n_prompt, steps) || (pf && !ensure_prefill(M, n_prompt, 1)) ||
+	    !start_run(M, prompt, n_prompt))
 		return 0;
+	size_t first = 0; /* the first step that runs a step graph */
+	if (pf) {
+		if (!enqueue_prefill(M, M->st.size, M->st.pos, n_prompt, 1, M->d_prompt, M->d_kc,
+				     M->d_vc, 0, M->d_logits, &M->d_st->tok,
+				     M->d_tokens + (n_prompt - 1), 0, M->stream))
+			return 0;
+		M->st.step = (int)n_prompt;
+		M->st.pos += (int)n_prompt;
+		M->st.size += (int)n_prompt;
+		/* the prefill kernels do not read these four (the pick writes the
+		 * token after them); the step graphs below do */
+		HIPCHK(hipMemcpy(M->d_st, &M->st, 4 * sizeof(int), hipMemcpyHostToDevice),
+		       "set state after prefill");
+		first = n_prompt;
+	}
 	if (M->graph_gen != moe_gen(M)) {
 		drop_graphs(M);
 		M->graph_gen = moe_gen(M);
@@ -621,7 +884,7 @@ int hip_lm_generate(hip_lm *M, const int *prompt, size_t n_prompt, size_t n_gen,
 	 * kvcache_rotate's keep when full) */
 	{
 		size_t size = (size_t)M->st.size;
-		for (size_t i = 0; i < steps; i++) {
+		for (size_t i = first; i < steps; i++) {
 			if (size >= M->C && !(size = rotate_keep(M, size)))
 				return 0;
 			const int head = i + 1 >= n_prompt;
@@ -632,7 +895,7 @@ int hip_lm_generate(hip_lm *M, const int *prompt, size_t n_prompt, size_t n_gen,
 			size++;
 		}
 	}
-	for (size_t i = 0; i < steps; i++) {
+	for (size_t i = first; i < steps; i++) {
 		if (!rotate_if_full(M))
 			return 0;
 		/* prompt steps before the last need no lm_head */
@@ -1065,8 +1328,36 @@ int hip_lm_batch_generate(hip_lm_batch *B, const int *prompts, size_t n_prompt, 
 		lm_err("lm_batch_generate: too many steps");
 		return 0;
 	}
-	if (!batch_io(B, n_prompt, steps) || !batch_start(B, prompts, n_prompt))
+	/* the prompts as prefills of groups of sequences (~PF_GROUP_ROWS rows:
+	 * every MoE layer's scratch grows with the rows of one launch) where
+	 * they fit the caches; else a step per id */
+	const int pf = n_prompt >= 2 && (size_t)B->st.size + n_prompt <= M->C;
+	size_t gseq = n_prompt >= PF_GROUP_ROWS ? 1 : PF_GROUP_ROWS / n_prompt;
+	gseq = gseq < B->S ? gseq : B->S;
+	if (!batch_io(B, n_prompt, steps) || (pf && !ensure_prefill(M, gseq * n_prompt, gseq)) ||
+	    !batch_start(B, prompts, n_prompt))
 		return 0;
+	size_t first = 0; /* the first step that runs a step graph */
+	if (pf) {
+		const size_t cseq = batch_cache_floats(M);
+		for (size_t z0 = 0; z0 < B->S; z0 += gseq) {
+			const size_t gz = B->S - z0 < gseq ? B->S - z0 : gseq;
+			if (!enqueue_prefill(M, B->st.size, B->st.pos, n_prompt, gz,
+					     B->d_prompt + z0 * n_prompt, B->d_kc + z0 * cseq,
+					     B->d_vc + z0 * cseq, cseq, B->d_logits + z0 * M->V,
+					     B->d_btok + z0,
+					     B->d_tokens + z0 * B->tokens_cap + (n_prompt - 1),
+					     (int)B->tokens_cap, B->stream))
+				return 0;
+		}
+		B->st.step = (int)n_prompt;
+		B->st.pos += (int)n_prompt;
+		B->st.size += (int)n_prompt;
+		/* the prefills do not read the batch's state; the step graphs do */
+		HIPCHK(hipMemcpy(B->d_st, &B->st, 4 * sizeof(int), hipMemcpyHostToDevice),
+		       "set state after prefill");
+		first = n_prompt;
+	}
 	if (B->graph_gen != moe_gen(M)) { /* another batch grew the layers' scratch */
 		batch_drop_graphs(B);
 		B->graph_gen = moe_gen(M);
@@ -1074,7 +1365,7 @@ int hip_lm_batch_generate(hip_lm_batch *B, const int *prompts, size_t n_prompt, 
 	/* every step shape of the run, captured before its first launch */
 	{
 		size_t size = (size_t)B->st.size;
-		for (size_t i = 0; i < steps; i++) {
+		for (size_t i = first; i < steps; i++) {
 			if (size >= M->C && !(size = rotate_keep(M, size)))
 				return 0;
 			const int head = i + 1 >= n_prompt;
@@ -1085,7 +1376,7 @@ int hip_lm_batch_generate(hip_lm_batch *B, const int *prompts, size_t n_prompt, 
 			size++;
 		}
 	}
-	for (size_t i = 0; i < steps; i++) {
+	for (size_t i = first; i < steps; i++) {
 		if (!batch_rotate_if_full(B))
 			return 0;
 		const int head = i + 1 >= n_prompt;

@@ -60,6 +60,19 @@ int lm_launch_attn(const float *qkv, const float *q_norm, const float *k_norm,
                    float scale, int scale_mul, int layer, int nact, int nseq,
                    size_t cstride, void *stream);
 
+/* prefill of T prompt rows of nseq sequences (rows z * T + t) at cache row
+ * `size` and position pos0 (size + T <= C): q/k norms (q_norm and k_norm
+ * both NULL for Mixtral) and RoPE of the stacked q/k/v rows, q into qo
+ * [nseq * T][H * 128], k and v into the cache rows size .. size + T - 1 */
+int lm_launch_pf_qk(const float *qkv, const float *q_norm, const float *k_norm,
+                    const float *freq, float *kc, float *vc, float *qo, int H, int KH, int C,
+                    int size, int pos0, int T, int nseq, size_t cstride, void *stream);
+/* causal (and sliding-window) attention of those rows over the cache rows
+ * 0 .. size + T - 1 into out [nseq * T][H * 128] */
+int lm_launch_pf_attn(const float *qo, const float *kc, const float *vc, float *out, int H,
+                      int KH, int C, int size, int T, int window, float scale, int scale_mul,
+                      int nseq, size_t cstride, void *stream);
+
 /* chunks a step over a cache of `size` rows (before the step) reads */
 static inline int lm_attn_active(int size, int window)
 {

@@ -894,6 +894,210 @@ __global__ __launch_bounds__(LM_NT) void k_lm_pick_rows(const float *__restrict_
 }
 
 /* ---------------------------------------------------------------------- */
+/* prefill: a prompt of T rows in one forward                              */
+/* ---------------------------------------------------------------------- */
+
+/*
+ * k_lm_pf_qk: row t of sequence z (grid T x S) of a prompt's stacked q/k/v
+ * product: the full-vector RMSNorms of q and k (OLMoE, olmoe.c:454-458),
+ * RoPE at position pos0 + t on consecutive pairs of every head (rope_apply,
+ * nn.c:192-219; the position is not clamped, as olmoe_prefill passes it,
+ * olmoe.c:504-508), q into qo[z * T + t], k and v into the cache rows
+ * size + t of every kv head (olmoe.c:276-289, llama.c:268-281).  The same
+ * arithmetic as k_lm_attn's one row.
+ */
+__global__ __launch_bounds__(LM_NT) void k_lm_pf_qk(const float *__restrict__ qkv,
+						    const float *__restrict__ q_norm,
+						    const float *__restrict__ k_norm,
+						    const float *__restrict__ freq,
+						    float *__restrict__ kc, float *__restrict__ vc,
+						    float *__restrict__ qo, int H, int KH, int C,
+						    int size, int pos0, int T, size_t cstride)
+{
+	constexpr int HL = LM_HLEN;
+	__shared__ float cs[HL / 2], sn[HL / 2];
+	__shared__ float red[LM_NT / WAVE];
+	const int t = blockIdx.x, z = blockIdx.y, EQ = H * HL, EK = KH * HL;
+	const size_t r = (size_t)z * T + t;
+	const float *q = qkv + r * (size_t)(EQ + 2 * EK), *k = q + EQ, *v = k + EK;
+	kc += (size_t)z * cstride;
+	vc += (size_t)z * cstride;
+	float *qd = qo + r * (size_t)EQ;
+	if (threadIdx.x < HL / 2) {
+		const float ang = (float)(pos0 + t) * freq[threadIdx.x];
+		cs[threadIdx.x] = cosf(ang);
+		sn[threadIdx.x] = sinf(ang);
+	}
+	float rq = 1.0f, rk = 1.0f;
+	if (q_norm) {
+		float s1 = 0.0f, s2 = 0.0f;
+		for (int i = threadIdx.x; i < EQ; i += LM_NT) {
+			const float x = q[i] * q[i];
+			s1 = s1 + x;
+		}
+		for (int i = threadIdx.x; i < EK; i += LM_NT) {
+			const float x = k[i] * k[i];
+			s2 = s2 + x;
+		}
+		rq = sqrtf(block_sum(s1, red) / (float)EQ + 1e-5f);
+		rk = sqrtf(block_sum(s2, red) / (float)EK + 1e-5f);
+	}
+	__syncthreads();
+	/* pair i of head h: item (h, i) of q's EQ / 2, then k's EK / 2 */
+	for (int it = threadIdx.x; it < (EQ + EK) / 2; it += LM_NT) {
+		const bool isq = it < EQ / 2;
+		const int e = 2 * (isq ? it : it - EQ / 2), i = (e % HL) / 2;
+		const float *src = isq ? q : k;
+		const float *w = isq ? q_norm : k_norm;
+		const float rr = isq ? rq : rk;
+		float x0 = src[e], x1 = src[e + 1];
+		if (q_norm) {
+			x0 = (x0 / rr) * w[e];
+			x1 = (x1 / rr) * w[e + 1];
+		}
+		const float co = cs[i], si = sn[i];
+		const float y0 = __builtin_fmaf(x0, co, -(x1 * si));
+		const float y1 = __builtin_fmaf(x0, si, x1 * co);
+		if (isq) {
+			qd[e] = y0;
+			qd[e + 1] = y1;
+		} else {
+			const int kh = e / HL, d = e % HL;
+			float *kr = kc + ((size_t)kh * C + size + t) * HL + d;
+			kr[0] = y0;
+			kr[1] = y1;
+		}
+	}
+	for (int i = threadIdx.x; i < EK; i += LM_NT) {
+		const int kh = i / HL, d = i % HL;
+		vc[((size_t)kh * C + size + t) * HL + d] = v[i];
+	}
+}
+
+#define PF_QB 64 /* query rows of a prefill attention workgroup */
+#define PF_KB 64 /* cache rows per step of its key loop */
+
+/*
+ * k_lm_pf_attn: query head h of rows q0 .. q0 + PF_QB - 1 of sequence z
+ * (grid H x ceil(T / PF_QB) x S) over the cache rows the causal mask (and
+ * Mixtral's sliding window) leave it: query row t (absolute size + t) sees
+ * rows j <= size + t, and with a window only size + t - j < window
+ * (olmoe.c:309-320 with -1e4 for masked scores, whose exp is 0 as -inf's;
+ * flash_attention's masks, nn.c:597-603).  Scores q . k / scale (OLMoE) or
+ * * scale (Mixtral); the softmax runs online over blocks of PF_KB rows
+ * (each block's maximum, the running sum rescaled), as flash_attention
+ * does (nn.c:570-641), with a fully masked prefix taken as weight 0 rather
+ * than exp(-inf - -inf).  Thread (row qi = tid / 4, quarter u = tid % 4)
+ * holds dims 32u .. 32u + 31 of the row's q and of its output; the four
+ * quarters' partial dots meet in two lane shuffles.
+ */
+__global__ __launch_bounds__(LM_NT) void k_lm_pf_attn(const float *__restrict__ qo,
+						      const float *__restrict__ kc,
+						      const float *__restrict__ vc,
+						      float *__restrict__ out, int H, int KH, int C,
+						      int size, int T, int window, float scale,
+						      int scale_mul, size_t cstride)
+{
+	constexpr int HL = LM_HLEN, RS = HL + 4;
+	static_assert(LM_NT == 4 * PF_QB, "four threads per query row");
+	__shared__ __attribute__((aligned(16))) float sk[PF_KB * RS], sv[PF_KB * RS];
+	const int h = blockIdx.x, q0 = blockIdx.y * PF_QB, z = blockIdx.z;
+	const int EQ = H * HL, kh = h / (H / KH);
+	const int tid = threadIdx.x, qi = tid / 4, u = tid % 4;
+	const int t = q0 + qi;
+	const bool live = t < T;
+	kc += (size_t)z * cstride + (size_t)kh * C * HL;
+	vc += (size_t)z * cstride + (size_t)kh * C * HL;
+	float qv[32], o[32];
+	{
+		const float4 *q4 = (const float4 *)(qo + ((size_t)z * T + (live ? t : 0)) * EQ +
+						    (size_t)h * HL + 32 * u);
+#pragma unroll
+		for (int i = 0; i < 8; i++) {
+			const float4 v = q4[i];
+			qv[4 * i] = v.x;
+			qv[4 * i + 1] = v.y;
+			qv[4 * i + 2] = v.z;
+			qv[4 * i + 3] = v.w;
+		}
+	}
+#pragma unroll
+	for (int i = 0; i < 32; i++)
+		o[i] = 0.0f;
+	const int qa = size + t; /* this row's absolute position in the cache */
+	const int tlast = min(q0 + PF_QB, T) - 1;
+	const int jhi = size + tlast + 1; /* rows the block's last query sees */
+	const int jlo = window > 0 ? max(0, size + q0 - window + 1) : 0;
+	float m = -INFINITY, l = 0.0f;
+	for (int j0 = jlo; j0 < jhi; j0 += PF_KB) {
+		__syncthreads(); /* the previous block's readers are done */
+		for (int e = tid; e < PF_KB * HL / 4; e += LM_NT) {
+			const int jj = e / (HL / 4), c4 = e % (HL / 4);
+			float4 kv = {0.0f, 0.0f, 0.0f, 0.0f}, vv = kv;
+			if (j0 + jj < jhi) {
+				kv = ((const float4 *)(kc + (size_t)(j0 + jj) * HL))[c4];
+				vv = ((const float4 *)(vc + (size_t)(j0 + jj) * HL))[c4];
+			}
+			*(float4 *)(sk + jj * RS + 4 * c4) = kv;
+			*(float4 *)(sv + jj * RS + 4 * c4) = vv;
+		}
+		__syncthreads();
+		float sc[PF_KB];
+#pragma unroll
+		for (int jj = 0; jj < PF_KB; jj++) {
+			const float4 *k4 = (const float4 *)(sk + jj * RS + 32 * u);
+			float a = 0.0f;
+#pragma unroll
+			for (int i = 0; i < 8; i++) {
+				const float4 kv = k4[i];
+				a = __builtin_fmaf(qv[4 * i], kv.x, a);
+				a = __builtin_fmaf(qv[4 * i + 1], kv.y, a);
+				a = __builtin_fmaf(qv[4 * i + 2], kv.z, a);
+				a = __builtin_fmaf(qv[4 * i + 3], kv.w, a);
+			}
+			a += __shfl_xor(a, 1, WAVE);
+			a += __shfl_xor(a, 2, WAVE);
+			const int j = j0 + jj;
+			const bool keep = j <= qa && (window <= 0 || qa - j < window);
+			sc[jj] = keep ? (scale_mul ? a * scale : a / scale) : -INFINITY;
+		}
+		float mb = -INFINITY;
+#pragma unroll
+		for (int jj = 0; jj < PF_KB; jj++)
+			mb = fmaxf(mb, sc[jj]);
+		const float mn = fmaxf(m, mb);
+		if (mn == -INFINITY)
+			continue; /* nothing of this row so far */
+		const float corr = m == -INFINITY ? 0.0f : moe_expf(m - mn);
+		l = l * corr;
+#pragma unroll
+		for (int i = 0; i < 32; i++)
+			o[i] = o[i] * corr;
+#pragma unroll
+		for (int jj = 0; jj < PF_KB; jj++) {
+			const float pj = sc[jj] == -INFINITY ? 0.0f : moe_expf(sc[jj] - mn);
+			l = l + pj;
+			const float4 *v4 = (const float4 *)(sv + jj * RS + 32 * u);
+#pragma unroll
+			for (int i = 0; i < 8; i++) {
+				const float4 vv = v4[i];
+				o[4 * i] = __builtin_fmaf(pj, vv.x, o[4 * i]);
+				o[4 * i + 1] = __builtin_fmaf(pj, vv.y, o[4 * i + 1]);
+				o[4 * i + 2] = __builtin_fmaf(pj, vv.z, o[4 * i + 2]);
+				o[4 * i + 3] = __builtin_fmaf(pj, vv.w, o[4 * i + 3]);
+			}
+		}
+		m = mn;
+	}
+	if (live) {
+		float4 *o4 = (float4 *)(out + ((size_t)z * T + t) * EQ + (size_t)h * HL + 32 * u);
+#pragma unroll
+		for (int i = 0; i < 8; i++)
+			o4[i] = float4{o[4 * i] / l, o[4 * i + 1] / l, o[4 * i + 2] / l, o[4 * i + 3] / l};
+	}
+}
+
+/* ---------------------------------------------------------------------- */
 /* launchers                                                              */
 /* ---------------------------------------------------------------------- */
 
@@ -1084,5 +1288,31 @@ extern "C" int lm_launch_copy_rows(const float *src, float *dst, size_t slab, si
 		return 0;
 	hipLaunchKernelGGL(k_lm_copy_rows, dim3(64, (unsigned)slabs), dim3(256), 0,
 			   (hipStream_t)stream, src, dst, slab, n);
+	return (int)hipGetLastError();
+}
+
+extern "C" int lm_launch_pf_qk(const float *qkv, const float *q_norm, const float *k_norm,
+			       const float *freq, float *kc, float *vc, float *qo, int H, int KH,
+			       int C, int size, int pos0, int T, int nseq, size_t cstride,
+			       void *stream)
+{
+	if (T < 1 || nseq < 1 || nseq > 65535 || KH < 1 || H % KH || size < 0 || size + T > C ||
+	    (!q_norm) != (!k_norm))
+		return (int)hipErrorInvalidValue;
+	hipLaunchKernelGGL(k_lm_pf_qk, dim3(T, nseq), dim3(LM_NT), 0, (hipStream_t)stream, qkv,
+			   q_norm, k_norm, freq, kc, vc, qo, H, KH, C, size, pos0, T, cstride);
+	return (int)hipGetLastError();
+}
+
+extern "C" int lm_launch_pf_attn(const float *qo, const float *kc, const float *vc, float *out,
+				 int H, int KH, int C, int size, int T, int window, float scale,
+				 int scale_mul, int nseq, size_t cstride, void *stream)
+{
+	if (T < 1 || nseq < 1 || nseq > 65535 || KH < 1 || H % KH || size < 0 || size + T > C ||
+	    (T + PF_QB - 1) / PF_QB > 65535)
+		return (int)hipErrorInvalidValue;
+	hipLaunchKernelGGL(k_lm_pf_attn, dim3(H, (T + PF_QB - 1) / PF_QB, nseq), dim3(LM_NT), 0,
+			   (hipStream_t)stream, qo, kc, vc, out, H, KH, C, size, T, window, scale,
+			   scale_mul, cstride);
 	return (int)hipGetLastError();
 }

@@ -71,6 +71,26 @@
 #define DEC_CHUNK 32 /* d_ff rows per item: one down block per row */
 #define CMB_MAX 16   /* combine entries per thread, two slices: grid * PSLICE <= CMB_MAX / 2 * NT */
 
+/* Stage stamps (a build with -DMOE_STAGE_STAMPS only, libhip_moe_stamps.so):
+ * thread 0 of each workgroup writes the 100 MHz wall clock at its start,
+ * after routing, after its last item's gate/up, after its partials, and
+ * after the combine, into a device array that moe_stage_stamps copies out.
+ * The product library compiles the stamps to nothing. */
+#define MOE_STAMP_WGS 1024
+#define MOE_STAMPS 5
+#ifdef MOE_STAGE_STAMPS
+__device__ unsigned long long g_stage_stamps[MOE_STAMP_WGS * MOE_STAMPS];
+#define STAMP(k)                                                                           \
+	do {                                                                               \
+		if (threadIdx.x == 0 && blockIdx.x < MOE_STAMP_WGS)                         \
+			g_stage_stamps[blockIdx.x * MOE_STAMPS + (k)] = wall_clock64();      \
+	} while (0)
+#else
+#define STAMP(k) \
+	do {     \
+	} while (0)
+#endif
+
 struct DecodeArgs {
 	const float *x;
 	const float *router;
@@ -772,6 +792,7 @@ void k_moe_decode(DecodeArgs a)
 	const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
 	const int G = (int)gridDim.x, b = (int)blockIdx.x;
 	const int NC = a.EI / DEC_CHUNK, IPT = a.K * NC, N = a.n_items;
+	STAMP(0);
 	/* work is dealt in half items (16 rows of d_ff), so that every
 	 * workgroup gets the same share when the items do not divide evenly
 	 * (Mixtral: 3.5 items each); x0 .. x1 are this workgroup's halves */
@@ -825,6 +846,7 @@ void k_moe_decode(DecodeArgs a)
 	if (threadIdx.x == 0 && b != 0)
 		st_dev_u32(&startf[b], epoch);
 	route_local<NT>(a, epoch, rl, s_ids, s_w, s_tab);
+	STAMP(1);
 	if (b == 0)
 		for (int i = threadIdx.x; i < a.T * a.K; i += NT) {
 			a.ids_out[i] = s_ids[i];
@@ -953,8 +975,10 @@ void k_moe_decode(DecodeArgs a)
 		}
 		gateup(q, (m >> hw) & 1);
 		__syncthreads();
+		STAMP(2);
 		down(q);
 		flush(q / IPT);
+		STAMP(3);
 	}
 
 	/* ---- combine: slices b, b + G, ... of the T*E outputs, NP at a time
@@ -1046,6 +1070,7 @@ void k_moe_decode(DecodeArgs a)
 		}
 	}
 
+	STAMP(4);
 	/* workgroup 0 advances the epoch for the next launch once every
 	 * workgroup has read it (they did so long ago: no wait in practice);
 	 * the next launch starts only after this one drains */
@@ -1265,3 +1290,12 @@ extern "C" void *moe_static_scratch(int dev)
 	pthread_mutex_unlock(&g_scratch_mu);
 	return p;
 }
+
+#ifdef MOE_STAGE_STAMPS
+/* the stage stamps of the last launch: [MOE_STAMP_WGS][MOE_STAMPS] */
+extern "C" int moe_stage_stamps(unsigned long long *out)
+{
+	return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_stage_stamps), sizeof(g_stage_stamps), 0,
+					 hipMemcpyDeviceToHost);
+}
+#endif

@@ -167,6 +167,10 @@ def _bind():
     L.hip_lm_decode.argtypes = [_vp, i32, _vp, C.POINTER(C.c_int)]
     L.hip_lm_generate.restype = i32
     L.hip_lm_generate.argtypes = [_vp, _vp, _sz, _sz, _vp, f32p]
+    L.hip_lm_set_moe_path.restype = i32
+    L.hip_lm_set_moe_path.argtypes = [_vp, i32]
+    L.hip_lm_prefill.restype = i32
+    L.hip_lm_prefill.argtypes = [_vp, _vp, _sz, _vp, C.POINTER(C.c_int)]
     L.hip_lm_trace.restype = i32
     L.hip_lm_trace.argtypes = [_vp, _vp, _vp, _vp]
     L.hip_lm_reset.restype = i32
@@ -248,6 +252,17 @@ class LmModel:
             raise HipMoeError("hip_lm_decode: " + last_error())
         return nxt.value, lg
 
+    def prefill(self, prompt):
+        """The prompt as one forward (hip_lm_prefill): (greedy pick, logits
+        [V] of its last row)."""
+        pr = np.ascontiguousarray(prompt, np.int32)
+        lg = np.empty(self.V, np.float32)
+        nxt = C.c_int(-1)
+        if _bind().hip_lm_prefill(self.h, pr.ctypes.data, pr.size, lg.ctypes.data,
+                                  C.byref(nxt)) != 1:
+            raise HipMoeError("hip_lm_prefill: " + last_error())
+        return nxt.value, lg
+
     def generate(self, prompt, n_gen: int):
         """(tokens [n_gen + 1], device ms of the n_gen generated steps)."""
         pr = np.ascontiguousarray(prompt, np.int32)
@@ -270,6 +285,11 @@ class LmModel:
     def reset(self):
         if _bind().hip_lm_reset(self.h) != 1:
             raise HipMoeError("hip_lm_reset: " + last_error())
+
+    def set_moe_path(self, path: int):
+        """Force every layer's MoE path (hipmoe.PATH_*)."""
+        if _bind().hip_lm_set_moe_path(self.h, path) != 1:
+            raise HipMoeError("hip_lm_set_moe_path: " + last_error())
 
     def weight_bytes(self) -> int:
         return _bind().hip_lm_weight_bytes(self.h)

@@ -167,3 +167,72 @@ def model_case(name: str):
     assert np.array_equal(prompt, g["prompt"])
     assert mg.model_digest(md) == str(g["sha_model"]), "regenerated model differs from fixture"
     return md, prompt, case, g
+
+
+# --------------------------------------------------------------------------
+# routing near-ties and generate's picks
+# --------------------------------------------------------------------------
+
+# a routing probability moves by ~3e-4 (relative) downstream of a layer on
+# the grouped path (f16 operands); gaps under ~7 times that are near-ties
+ROUTE_GAP = 2e-3
+
+
+def routing_margins(md, Cx, seq, n_prompt):
+    """The model oracle's (bit for bit the reference's) decode of one
+    sequence: for every step from the prompt's last id on, the smallest
+    relative gap over the layers between the last selected and the first
+    unselected routing probability, (p_K - p_K+1) / p_K."""
+    import hiplm
+    import oracle
+    L, K = md["layers"], md["K"]
+    tab = hiplm.ptr_table(md) if md["arch"] == "olmoe" else hiplm.ptr_table_llama(md)
+    om = oracle.OlmoeModel(md, Cx, tab)
+    gaps = []
+    try:
+        for i, tok in enumerate(seq):
+            _, _, (mi, _, _) = om.decode(int(tok), trace=True)
+            if i < n_prompt - 1:
+                continue
+            gap = 1.0
+            for l in range(L):
+                b = md["blk"][l]
+                lay = dict(router=b["router"], gate=b["gate"], up=b["up"], down=b["down"],
+                           wtype=md["wtype"], E=md["E"], EI=md["EI"], NE=md["NE"])
+                pr = np.sort(oracle.moe_ffn(mi[l:l + 1], lay, K, md["arch"] != "olmoe",
+                                            None)[4][0])[::-1]
+                gap = min(gap, float((pr[K - 1] - pr[K]) / pr[K - 1]))
+            gaps.append(gap)
+    finally:
+        om.free()
+    return np.asarray(gaps)
+
+
+def prefill_moe_fp32(md, rows):
+    """A prefill launch of `rows` rows keeps its MoE layers in fp32: the
+    decode kernel takes them (4 * rows * K <= 3 * NE); past that the grouped
+    path's f16 operands move each layer's output by ~5e-4."""
+    return 4 * rows * md["K"] <= 3 * md["NE"]
+
+
+def generate_upto(md, Cx, prompt, ref_tokens, top_logits, rows):
+    """How many of generate's picks (one prefill of the prompt, `rows` rows
+    per launch, then decode steps) must equal the reference's ref_tokens
+    [n_gen + 1]: those before the first whose reference top-two logits are
+    within 1e-4 relative (an fp32 prefill) or 2e-3 (a prefill on the grouped
+    path).  After a grouped-path prefill, whose f16 layers move the prompt's
+    rows (and the cache rows later steps attend to) by ~5e-4, also none past
+    a routing near-tie (ROUTE_GAP) of a prompt row, or of the step that makes
+    the pick: there the other expert may be picked."""
+    t = np.asarray(top_logits, np.float64)
+    fp32 = prefill_moe_fp32(md, rows)
+    gap = np.abs(t[:, 0] - t[:, 1]) / np.abs(t[:, 0])
+    bad = list(np.nonzero(gap <= (1e-4 if fp32 else 2e-3))[0])
+    if not fp32:
+        n = len(prompt)
+        seq = np.concatenate([np.asarray(prompt), np.asarray(ref_tokens)[:-1]])
+        rg = routing_margins(md, Cx, seq, 1)
+        if n > 1 and rg[:n - 1].min() <= ROUTE_GAP:
+            return 0
+        bad += list(np.nonzero(rg[n - 1:] <= ROUTE_GAP)[0])
+    return int(min(bad)) if bad else t.shape[0]

@@ -349,6 +349,12 @@ MODEL_CASES = {
     # blocks): the benchmarked lengths
     "olmoe_full_long": (16, 2048, 16, 50304, 64, 8, 1024, 2048, hipmoe.Q8_0, 0.0, 4, 296, 64),
     "mixtral_2l_long": (2, 4096, 32, 32000, 8, 2, 14336, 4096, hipmoe.Q4_0, 0.0, 1024, 32, 64),
+    # long prompts in the reference's generate order (one prefill of the
+    # prompt, olmoe.c:504-508, llama.c:560-564): OLMoE's masked softmax over
+    # a 200-row prompt, and Mixtral's flash_attention over 240 rows with its
+    # window of 200 masking inside the prefill
+    "olmoe_prompt": (2, 1024, 8, 512, 64, 8, 512, 256, hipmoe.Q8_0, 0.1, 200, 8, 4),
+    "mixtral_window_prompt": (2, 2048, 16, 512, 8, 2, 1024, 256, hipmoe.Q4_0, 0.1, 240, 8, 4),
 }
 # Mixtral cases: (kv heads, sliding window, rope theta).  The window stays
 # at least C - 64: with a longer cache, once the first 64-row block lies
@@ -360,6 +366,7 @@ MIXTRAL_EXTRA = {
     "mixtral_2l": (8, 0, 1e6),
     "mixtral_long": (4, 200, 1e6),
     "mixtral_2l_long": (8, 0, 1e6),
+    "mixtral_window_prompt": (4, 200, 1e6),
 }
 # cases written in decode order only (one olmoe_decode / llama_decode per
 # prompt id); the others also in generate order (one prefill of the prompt)

@@ -34,8 +34,8 @@ import numpy as np
 import pytest
 
 import hiplm
-import oracle
-from common import SEED, batch_case, model_case, rel_l2
+from common import (ROUTE_GAP, SEED, batch_case, generate_upto, model_case, rel_l2,
+                    routing_margins)
 from test_gpu_model import TIGHT, safe_steps, say, teacher_forced
 
 pytestmark = pytest.mark.gpu
@@ -76,40 +76,7 @@ def test_gpu_model_full_shape_long_vs_reference():
 def test_gpu_model_mixtral_layer_shape_long_prompt_vs_reference():
     md, _, case, _ = model_case("mixtral_2l_long")
     assert merge_form(md["KH"], 17, 1) == 2
-    teacher_forced("mixtral_2l_long", 1e-3, route_steps=(1023, 1050))
-
-
-# a routing probability moves by ~3e-4 (relative) downstream of a grouped
-# layer; gaps under ~7 times that are near-ties
-ROUTE_GAP = 2e-3
-
-
-def routing_margins(md, Cx, seq, n_prompt):
-    """The model oracle's (bit for bit the reference's) decode of one
-    sequence: for every step from the prompt's last id on, the smallest
-    relative gap over the layers between the last selected and the first
-    unselected routing probability, (p_K - p_K+1) / p_K."""
-    L, K = md["layers"], md["K"]
-    tab = hiplm.ptr_table(md) if md["arch"] == "olmoe" else hiplm.ptr_table_llama(md)
-    om = oracle.OlmoeModel(md, Cx, tab)
-    gaps = []
-    try:
-        for i, tok in enumerate(seq):
-            _, _, (mi, _, _) = om.decode(int(tok), trace=True)
-            if i < n_prompt - 1:
-                continue
-            gap = 1.0
-            for l in range(L):
-                b = md["blk"][l]
-                lay = dict(router=b["router"], gate=b["gate"], up=b["up"], down=b["down"],
-                           wtype=md["wtype"], E=md["E"], EI=md["EI"], NE=md["NE"])
-                pr = np.sort(oracle.moe_ffn(mi[l:l + 1], lay, K, md["arch"] != "olmoe",
-                                            None)[4][0])[::-1]
-                gap = min(gap, float((pr[K - 1] - pr[K]) / pr[K - 1]))
-            gaps.append(gap)
-    finally:
-        om.free()
-    return np.asarray(gaps)
+    teacher_forced("mixtral_2l_long", 1e-3, route_steps=(1023, 1050), fp32_generate=True)
 
 
 def batch_vs_reference(name, tol):
@@ -139,6 +106,7 @@ def batch_vs_reference(name, tol):
     seqs = np.concatenate([prompts, feed], axis=1)
     say(f"{name}: routing margins of the checked sequences (model oracle)")
     route_ok = {s: routing_margins(md, Cx, seqs[s], n_prompt) > ROUTE_GAP for s in check}
+    rows = min(max(1, 2048 // n_prompt), S) * n_prompt
     nskip = sum(int((~v).sum()) for v in route_ok.values())
     assert nskip <= len(check) * (n_gen + 1) // 4, "too few steps without a routing near-tie"
     say(f"{name}: {S} sequences in lockstep, {n_prompt} prompt ids + {n_gen} steps, "
@@ -170,10 +138,9 @@ def batch_vs_reference(name, tol):
         Bt.reset()
         toks, ms = Bt.generate(prompts, n_gen)
         for s in check:
-            # the picks before the first step whose pick a near-tie decides
-            safe = safe_steps(g[f"s{s}_top_logits"]) & route_ok[s]
-            bad = np.nonzero(~safe)[0]
-            upto = int(bad[0]) if bad.size else n_gen + 1
+            # the prompts as prefills (grouped-path MoE layers at these rows)
+            upto = generate_upto(md, Cx, prompts[s], g[f"s{s}_tokens"],
+                                 g[f"s{s}_top_logits"], rows)
             assert np.array_equal(toks[s, :upto], g[f"s{s}_tokens"][:upto]), \
                 (s, toks[s], g[f"s{s}_tokens"])
         say(f"{name}: generate {n_gen} steps x {S} sequences: checked tokens equal the "
@@ -222,16 +189,13 @@ def test_gpu_model_generate_after_a_batch_grew_the_moe_scratch():
     """A lockstep batch reserves the shared MoE layers' scratch for its
     sequences, which reallocates it; the model's step graphs captured by an
     earlier generate name the freed buffers and are captured again, so a
-    later generate still gives the reference's tokens."""
+    later generate gives the same tokens as the first (the runs are
+    deterministic: the grouped path's rows do not depend on their order)."""
     md, prompt, case, g = model_case("olmoe_small")
     L, E, H, V, NE, K, EI, Cx, wt, nstd, n_prompt, n_gen, stride = case
-    safe = safe_steps(g["dec_top_logits"])
-    bad = np.nonzero(~safe)[0]
-    upto = int(bad[0]) + 1 if bad.size else n_gen + 1
     M = hiplm.LmModel(md, Cx)
     try:
-        toks, _ = M.generate(prompt, n_gen)
-        assert np.array_equal(toks[:upto], g["dec_tokens"][:upto])
+        first, _ = M.generate(prompt, n_gen)
         Bt = hiplm.LmBatch(M, 24)
         try:
             nxt, _ = Bt.decode(np.full(24, int(prompt[0]), np.int32))
@@ -239,8 +203,7 @@ def test_gpu_model_generate_after_a_batch_grew_the_moe_scratch():
             Bt.free()
         M.reset()
         toks, _ = M.generate(prompt, n_gen)
-        assert np.array_equal(toks[:upto], g["dec_tokens"][:upto])
-        say(f"olmoe_small: generate, a 24-sequence batch, generate again: "
-            f"{upto} tokens equal the reference's")
+        assert np.array_equal(toks, first)
+        say("olmoe_small: generate, a 24-sequence batch, generate again: the same tokens")
     finally:
         M.free()

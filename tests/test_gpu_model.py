@@ -25,8 +25,9 @@ import numpy as np
 import pytest
 
 import hiplm
+import hipmoe
 import oracle
-from common import bits, model_case, rel_l2
+from common import bits, generate_upto, model_case, rel_l2
 
 pytestmark = pytest.mark.gpu
 TIGHT = 2e-5
@@ -63,7 +64,7 @@ def check_routing(md, case, M):
         assert np.array_equal(bits(w[l]), bits(ow[0])), f"layer {l}: weights"
 
 
-def teacher_forced(name, tol, route_steps=()):
+def teacher_forced(name, tol, route_steps=(), fp32_generate=False):
     md, prompt, case, g = model_case(name)
     L, E, H, V, NE, K, EI, Cx, wt, nstd, n_prompt, n_gen, stride = case
     say(f"{name}: upload ({L} layers, E={E}, heads {H}/{md.get('KH', H)}, vocab {V}, "
@@ -88,11 +89,16 @@ def teacher_forced(name, tol, route_steps=()):
             if safe[s]:
                 assert nxt == int(g["dec_tokens"][s]), f"step {s}: pick {nxt}"
         say(f"{name}: {len(seq)} teacher-forced steps, worst logit rel L2 {worst:.3e}")
-        # the device-side greedy loop from a fresh cache
+        # the device-side greedy loop from a fresh cache (the prompt as one
+        # prefill, as the reference's generate; a 1024-id prompt's with the
+        # MoE layers in fp32, whose routing margins the oracle would take
+        # minutes to find)
         M.reset()
+        if fp32_generate:
+            M.set_moe_path(hipmoe.PATH_GEMV)
         toks, ms = M.generate(prompt, n_gen)
-        bad = np.nonzero(~safe)[0]
-        upto = int(bad[0]) + 1 if bad.size else n_gen + 1
+        rows = 1 if fp32_generate else n_prompt
+        upto = generate_upto(md, Cx, prompt, g["dec_tokens"], g["dec_top_logits"], rows)
         assert np.array_equal(toks[:upto], g["dec_tokens"][:upto]), (toks, g["dec_tokens"])
         say(f"{name}: generate {n_gen} steps: tokens equal the reference's "
             f"({upto} checked), {ms:.2f} ms")
@@ -169,9 +175,12 @@ def batch_vs_oracle(name, nseq, tol, n_prompt=None, n_gen=None):
         say(f"{name}: teacher-forced, worst logit rel L2 {worst:.3e}")
         Bt.reset()
         toks, ms = Bt.generate(prompts, n_gen)
-        for s in range(nseq):
-            bad = np.nonzero(~safe[s])[0]
-            upto = int(bad[0]) + 1 if bad.size else n_gen + 1
+        # the prompts as prefills of ~2048 rows a launch; the picks of the
+        # first four sequences against the oracle's
+        rows = min(max(1, 2048 // n_prompt), nseq) * n_prompt
+        for s in range(min(nseq, 4)):
+            top2 = np.sort(ref_lg[s], axis=1)[:, ::-1][:, :2]
+            upto = generate_upto(md, Cx, prompts[s], ref_tok[s], top2, rows)
             assert np.array_equal(toks[s, :upto], ref_tok[s, :upto]), (s, toks[s], ref_tok[s])
         say(f"{name}: generate {n_gen} steps x {nseq} sequences: tokens equal the oracle's, "
             f"{ms:.2f} ms")

@@ -142,3 +142,12 @@ def test_model_oracle_matches_reference_batch_sequence_long_prompt():
         m.free()
     assert np.array_equal(toks, g[f"s{s}_tokens"])
     assert np.array_equal(bits(lg[:, ::stride]), bits(g[f"s{s}_logits"]))
+
+
+@pytest.mark.parametrize("name", ["olmoe_prompt", "mixtral_window_prompt"])
+def test_model_oracle_matches_reference_long_prompt(name):
+    """A 200-id prompt (OLMoE) and a 240-id prompt under a 200-row sliding
+    window (Mixtral): the decode order bit for bit, and the reference's
+    generate order (one prefill of the whole prompt, whose flash_attention
+    masks rows outside the window, nn.c:597-603) within fp32 rounding."""
+    _check_long(name)
