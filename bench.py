@@ -23,7 +23,10 @@ layers, d_model 2048, 16 heads of 128, 64 experts top-8 d_ff 1024, vocab
 50304, Q8_0 weights N(0, 0.02), unit norms, fp32 KV cache of context 2048)
 decoding greedily after a 16-token random-id prompt: a step is one
 generated token, the whole step (embedding to greedy pick) replayed from a
-captured HIP graph with the token fed back on the device.
+captured HIP graph with the token fed back on the device;
+`olmoe_q4km_full_decode` the same model with its tensors' block types mixed as
+a Q4_K_M file mixes them (Q4_K; Q6_K output, and attn_v and the experts' down
+in 8 of the 16 layers).
 `mixtral_full_decode` does the same for the Mixtral-8x7B shape after a
 1024-token prompt, and `mixtral_full_decode_b16` for sixteen sequences in
 lockstep (hip_lm_batch_*: each step one token of every sequence, their own
@@ -78,6 +81,11 @@ WORKLOADS = {
     # the whole model, one generated token per step
     "olmoe_full_decode": dict(kind="model", arch="olmoe", wtype=hipmoe.Q8_0, layers=16, E=2048,
                               H=16, KH=16, V=50304, NE=64, K=8, EI=1024, C=2048, prompt=16),
+    # the same model with its tensors' types mixed as a Q4_K_M file mixes
+    # them (hiplm.q4_k_m_types): every product through Q8_K activations
+    "olmoe_q4km_full_decode": dict(kind="model", arch="olmoe", wtype=hipmoe.Q4_K, q4km=True,
+                                   layers=16, E=2048, H=16, KH=16, V=50304, NE=64, K=8,
+                                   EI=1024, C=2048, prompt=16),
     "mixtral_full_decode": dict(kind="model", arch="mixtral", wtype=hipmoe.Q4_0, layers=32,
                                 E=4096, H=32, KH=8, V=32000, NE=8, K=2, EI=14336, C=4096,
                                 prompt=1024, window=0, theta=1e6),
@@ -247,8 +255,9 @@ def bench_model(args, w, H):
                                    w["EI"], w["C"])
     H, KH = w["H"], w["KH"]
     t0 = time.perf_counter()
+    types = hiplm.q4_k_m_types(Lh) if w.get("q4km") else None
     if w["arch"] == "olmoe":
-        md = hiplm.synth_olmoe(SEED, Lh, E, H, V, NE, K, EI, wt)
+        md = hiplm.synth_olmoe(SEED, Lh, E, H, V, NE, K, EI, wt, types=types)
     else:
         # 32 layers of 8 Mixtral experts are ~26 GB of Q4_0: the layers share
         # one generated set of values on the host, each uploaded to its own
@@ -320,15 +329,23 @@ def bench_model(args, w, H):
         Bt.free()
     ms_per_step = ms / steps
     tokens_per_s = nseq * steps / (ms / 1e3)
-    bpw = 34 / 32 if wt == hipmoe.Q8_0 else 18 / 32
-    expert = 3 * E * EI * bpw
     EQ, EKV = H * 128, KH * 128
-    attn_w = (2 * EQ + 2 * EKV) * E * bpw  # q, k, v rows of E columns, output E x EQ
     kv_rows = np.mean([w["prompt"] + s + 1 for s in range(1, steps + 1)])
+
+    def tb(t, rows, cols):  # bytes of a rows x cols matrix of block type t
+        return rows * hipmoe.row_bytes(t, cols)
+    lt = types["layers"] if types else [(wt,) * 6] * Lh
+    et, ot = (types["embd"], types["output"]) if types else (wt, wt)
     # a step reads the weights once for all sequences, and each sequence's
-    # own KV rows and embedding row
-    per_layer = attn_w + NE * E * 4 + mean_uniq * expert + nseq * 2 * kv_rows * EKV * 4
-    bytes_per_step = Lh * per_layer + V * E * bpw + nseq * E * bpw
+    # own KV rows and embedding row: per layer q, k, v (rows of E columns),
+    # the output (E rows of EQ), the router, the unique experts' gate, up
+    # and down, the KV rows attention reads
+    bytes_per_step = tb(ot, V, E) + nseq * tb(et, 1, E)
+    for t in lt:
+        bytes_per_step += (tb(t[0], EQ, E) + tb(t[1], EKV, E) + tb(t[2], EKV, E) +
+                           tb(t[3], E, EQ) + NE * E * 4 +
+                           mean_uniq * (2 * tb(t[4], EI, E) + tb(t[5], E, EI)) +
+                           nseq * 2 * kv_rows * EKV * 4)
     achieved_gbs = bytes_per_step / (ms_per_step / 1e3) / 1e9
     log(f"{steps} steps x {nseq} sequences in {ms:.2f} ms: {ms_per_step * 1e3:.1f} us/step, "
         f"{tokens_per_s:.1f} tokens/s, {achieved_gbs:.1f} GB/s algorithmic "
@@ -350,8 +367,9 @@ def bench_model(args, w, H):
         "config": {"workload": args.workload, "layers": Lh, "d_model": E, "heads": H,
                    "kv_heads": KH, "vocab": V, "experts": NE, "topk": K, "d_ff": EI,
                    "context": Cx,
-                   "weights": {hipmoe.Q8_0: "Q8_0", hipmoe.Q4_0: "Q4_0", hipmoe.Q4_K: "Q4_K",
-                               hipmoe.Q6_K: "Q6_K"}[wt],
+                   "weights": "Q4_K_M" if types else {
+                       hipmoe.Q8_0: "Q8_0", hipmoe.Q4_0: "Q4_0", hipmoe.Q4_K: "Q4_K",
+                       hipmoe.Q6_K: "Q6_K"}[wt],
                    "prompt_tokens": w["prompt"], "sequences": nseq, "graphs": not args.eager,
                    "mean_unique_experts": round(mean_uniq, 3),
                    "algorithmic_bytes_per_step": int(bytes_per_step)},

@@ -38,8 +38,12 @@ extern "C" {
 /*
  * The model's tensors as the reference's loader maps them (gguf.c views of
  * the GGUF file; the caller keeps ownership, they are only read):
- * quantized matrices are rows of GGUF blocks of type wtype (HIP_MOE_Q8_0 or
- * HIP_MOE_Q4_0), norms and the router fp32.  Per-layer arrays hold `layers`
+ * quantized matrices are rows of GGUF blocks of type wtype (HIP_MOE_Q8_0,
+ * HIP_MOE_Q4_0, HIP_MOE_Q4_K or HIP_MOE_Q6_K) unless the per-tensor types
+ * below say otherwise, norms and the router fp32.  A model whose matrices
+ * are all Q8_0 or all Q4_0 runs the fused step kernels; any other mix runs
+ * a step of separate norm, product and attention launches (the K-quant
+ * products through Q8_K activations, bit for bit the reference's dots).  Per-layer arrays hold `layers`
  * pointers; the expert arrays hold layers * NE pointers (layer-major), each
  * the base of one expert's matrix: for OLMoE's stacked *_exps tensors base +
  * e * expert_bytes (tensor_at_q, olmoe.c:20-60), for Mixtral the per-expert
@@ -63,6 +67,14 @@ typedef struct hip_lm_desc {
 	const float *const *gate_inp;                 /* router [NE][E] */
 	const void *const *gate_e, *const *up_e;      /* [layers * NE]: [EI][E] each */
 	const void *const *down_e;                    /* [layers * NE]: [E][EI] each */
+	/* Block types per tensor, as the reference's tensors carry them
+	 * (tensor->type; a Q4_K_M GGUF mixes Q4_K and Q6_K): 0 = wtype.
+	 * layer_types (NULL = wtype everywhere) holds [layers][6]: attn_q,
+	 * attn_k, attn_v, attn_output, the experts' gate/up, the experts' down.
+	 * Each of HIP_MOE_Q8_0, Q4_0, Q4_K, Q6_K (K-quant tensors: E, heads *
+	 * 128 and EI multiples of 256); wtype itself may be Q4_K or Q6_K. */
+	int embd_type, output_type;
+	const int *layer_types;
 } hip_lm_desc;
 
 typedef struct hip_lm hip_lm;

@@ -17,6 +17,7 @@
 #include "hip_lm.h"
 #include "lm_internal.h"
 #include "moe_internal.h"
+#include "moe_synth.h"
 
 #include <hip/hip_runtime_api.h>
 #include <math.h>
@@ -30,13 +31,23 @@
 
 struct lm_layer {
 	float *attn_norm, *q_norm, *k_norm, *ffn_norm;
-	uint8_t *wqkv; /* [q rows | k rows | v rows][E] blocks */
+	uint8_t *wqkv; /* [q rows | k rows | v rows][E] blocks (one block type) */
 	uint8_t *wo;   /* [E][heads * 128] blocks */
 	hip_moe_layer *moe;
+	/* mixed block types (the generic step): q, k, v apart, each tensor's
+	 * type and its product's workgroups */
+	uint8_t *wq, *wk, *wv;
+	int tq, tk, tv, to;
+	int gq, gk, gv, go;
 };
 
 struct hip_lm {
 	int arch, wtype, device;
+	/* generic: the matrices are not all Q8_0 or all Q4_0 (per-tensor types,
+	 * K-quants): the step runs separate norm, product and attention
+	 * launches instead of the fused step kernels */
+	int generic, embd_type, output_type, ghead;
+	float *d_x; /* generic step: the normalised row a product takes */
 	size_t L, E, H, KH, HL, V, C, NE, K, EI, window;
 	float theta, scale; /* attention: scores / scale (OLMoE) or * scale (Mixtral) */
 	size_t EQ, EKV; /* rows of q, and of k (= of v) */
@@ -112,10 +123,45 @@ static size_t qbytes(int wtype, size_t rows, size_t cols)
 	return rows * (cols / 32) * (wtype == HIP_MOE_Q8_0 ? 34 : 18);
 }
 
+static int is_kq(int t)
+{
+	return t == HIP_MOE_Q4_K || t == HIP_MOE_Q6_K;
+}
+
+/* tensor i (0 attn_q, 1 attn_k, 2 attn_v, 3 attn_output, 4 experts' gate/up,
+ * 5 experts' down) of layer l */
+static int layer_type(const hip_lm_desc *d, size_t l, int i)
+{
+	const int t = d->layer_types ? d->layer_types[6 * l + i] : 0;
+	return t ? t : d->wtype;
+}
+
+/* bytes of a rows x cols matrix in type t, with the K-quant products'
+ * read slack past the end */
+static size_t tbytes(int t, size_t rows, size_t cols)
+{
+	return rows * moe_row_bytes(t, cols) + (is_kq(t) ? MOE_KQ_SLACK : 0);
+}
+
 static int upload(void **dst, const void *src, size_t bytes, const char *what)
 {
 	HIPCHK(hipMalloc(dst, bytes), what);
 	HIPCHK(hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice), what);
+	return 1;
+fail:
+	return 0;
+}
+
+/* a rows x cols matrix of type t (tbytes: the K-quant read slack after it,
+ * zeroed) */
+static int upload_t(uint8_t **dst, const void *src, int t, size_t rows, size_t cols,
+		    const char *what)
+{
+	const size_t n = rows * moe_row_bytes(t, cols), all = tbytes(t, rows, cols);
+	HIPCHK(hipMalloc((void **)dst, all), what);
+	if (all > n)
+		HIPCHK(hipMemset(*dst + n, 0, all - n), what);
+	HIPCHK(hipMemcpy(*dst, src, n, hipMemcpyHostToDevice), what);
 	return 1;
 fail:
 	return 0;
@@ -174,10 +220,14 @@ void hip_lm_free(hip_lm *M)
 			hipFree(y->ffn_norm);
 			hipFree(y->wqkv);
 			hipFree(y->wo);
+			hipFree(y->wq);
+			hipFree(y->wk);
+			hipFree(y->wv);
 			hip_moe_free(y->moe);
 		}
 		free(M->ly);
 	}
+	hipFree(M->d_x);
 	void *bufs[] = {M->d_wte, M->d_head, M->d_onorm, M->d_kc, M->d_vc, M->d_freq, M->d_h0,
 			M->d_h1, M->d_qkv, M->d_attn, M->d_moe_in, M->d_moe_out, M->d_part,
 			M->d_rows_t, M->d_best, M->d_cnt, M->d_logits, M->d_ids, M->d_w,
@@ -193,6 +243,35 @@ void hip_lm_free(hip_lm *M)
 	free(M);
 }
 
+static int type_ok(int t)
+{
+	return t == HIP_MOE_Q8_0 || t == HIP_MOE_Q4_0 || t == HIP_MOE_Q4_K || t == HIP_MOE_Q6_K;
+}
+
+/* a product over K columns in type t runs for one token */
+static int product_ok(int t, size_t K)
+{
+	if (is_kq(t))
+		return moe_kq_supported(t, (int)K);
+	return K % 64 == 0 && K / 64 >= 4 && K / 64 <= 64 && ((K / 64) & (K / 64 - 1)) == 0;
+}
+
+static int product_grid(int t, size_t K)
+{
+	return is_kq(t) ? moe_kq_grid(t, (int)K, 1) : moe_qgemv_grid(t, (int)K, 1);
+}
+
+/* out[N] = add + x . W^T for one token (add NULL or [N]) in type t */
+static int vec_product(int t, const uint8_t *W, int N, int K, const float *x, const float *add,
+		       float *out, int grid, hipStream_t s)
+{
+	if (is_kq(t))
+		LCHK(moe_launch_kq_gemv(t, W, N, K, x, 1, add, 0, out, grid, s), "product");
+	else
+		LCHK(moe_launch_qgemv(t, W, N, K, x, 1, add, 0, out, grid, s), "product");
+	return 1;
+}
+
 static int check_desc(const hip_lm_desc *d)
 {
 	if (!d) {
@@ -203,10 +282,21 @@ static int check_desc(const hip_lm_desc *d)
 		lm_err("lm_upload: unknown arch %d", d->arch);
 		return 0;
 	}
-	if (d->wtype != HIP_MOE_Q8_0 && d->wtype != HIP_MOE_Q4_0) {
+	if (!type_ok(d->wtype)) {
 		lm_err("lm_upload: unsupported weight type %d", d->wtype);
 		return 0;
 	}
+	if ((d->embd_type && !type_ok(d->embd_type)) ||
+	    (d->output_type && !type_ok(d->output_type))) {
+		lm_err("lm_upload: unsupported embedding / output type %d / %d", d->embd_type,
+		       d->output_type);
+		return 0;
+	}
+	for (size_t i = 0; d->layer_types && i < 6 * d->layers; i++)
+		if (d->layer_types[i] && !type_ok(d->layer_types[i])) {
+			lm_err("lm_upload: unsupported type %d of layer %zu", d->layer_types[i], i / 6);
+			return 0;
+		}
 	if (!d->layers || !d->E || !d->heads || !d->kv_heads || d->heads % d->kv_heads ||
 	    !d->vocab || d->vocab > 0x7fffffff || d->context < 2 || d->context > (1u << 24)) {
 		lm_err("lm_upload: bad sizes (layers %zu, E %zu, heads %zu/%zu, vocab %zu, "
@@ -266,6 +356,13 @@ hip_lm *hip_lm_upload(const hip_lm_desc *d)
 	M->EI = d->EI;
 	M->window = d->sliding_window;
 	M->theta = d->rope_theta;
+	M->embd_type = d->embd_type ? d->embd_type : d->wtype;
+	M->output_type = d->output_type ? d->output_type : d->wtype;
+	M->generic = (d->wtype != HIP_MOE_Q8_0 && d->wtype != HIP_MOE_Q4_0) ||
+		     M->embd_type != d->wtype || M->output_type != d->wtype;
+	for (size_t l = 0; l < M->L; l++)
+		for (int i = 0; i < 6; i++)
+			M->generic |= layer_type(d, l, i) != d->wtype;
 	/* hlen_sq = sqrt((scalar_t)HLEN) (olmoe.c:150, llama.c:118): OLMoE
 	 * divides the scores by it, Mixtral's flash_attention multiplies them
 	 * by 1.0f / hlen_sq (llama.c:324) */
@@ -290,25 +387,37 @@ hip_lm *hip_lm_upload(const hip_lm_desc *d)
 	HIPCHK(hipEventCreate(&M->ev0), "hipEventCreate");
 	HIPCHK(hipEventCreate(&M->ev1), "hipEventCreate");
 
-	/* products: one token, K = E (qkv) and heads * 128 (output); the
-	 * workgroups resident at once, queried here, not under capture */
-	M->grid_qkv = lm_gemv_grid(0, wt, (int)E, (int)(M->EQ + 2 * M->EKV));
-	M->grid_o = lm_gemv_grid(1, wt, (int)M->EQ, (int)E);
-	M->grid_head = lm_gemv_grid(2, wt, (int)E, (int)M->V);
-	/* (the output product's last workgroup gathers E rows in the LDS that
-	 * staged its heads * 128 inputs) */
-	if (M->grid_qkv <= 0 || M->grid_o <= 0 || M->grid_head <= 0 ||
-	    M->grid_head > LM_MAX_HEAD_WG || M->grid_o > LM_MAX_HEAD_WG || E * 64 > M->EQ * 68) {
-		lm_err("lm_upload: E=%zu / heads*128=%zu not supported by the dense product", E,
-		       M->EQ);
-		goto fail;
+	if (!M->generic) {
+		/* products: one token, K = E (qkv) and heads * 128 (output); the
+		 * workgroups resident at once, queried here, not under capture */
+		M->grid_qkv = lm_gemv_grid(0, wt, (int)E, (int)(M->EQ + 2 * M->EKV));
+		M->grid_o = lm_gemv_grid(1, wt, (int)M->EQ, (int)E);
+		M->grid_head = lm_gemv_grid(2, wt, (int)E, (int)M->V);
+		/* (the output product's last workgroup gathers E rows in the LDS
+		 * that staged its heads * 128 inputs) */
+		if (M->grid_qkv <= 0 || M->grid_o <= 0 || M->grid_head <= 0 ||
+		    M->grid_head > LM_MAX_HEAD_WG || M->grid_o > LM_MAX_HEAD_WG ||
+		    E * 64 > M->EQ * 68) {
+			lm_err("lm_upload: E=%zu / heads*128=%zu not supported by the dense product",
+			       E, M->EQ);
+			goto fail;
+		}
+	} else {
+		M->ghead = product_grid(M->output_type, E);
+		if (!product_ok(M->output_type, E) || M->ghead <= 0 ||
+		    !(is_kq(M->embd_type) ? E % 256 == 0 : E % 32 == 0)) {
+			lm_err("lm_upload: E=%zu not supported by the embedding / output types %d / %d",
+			       E, M->embd_type, M->output_type);
+			goto fail;
+		}
 	}
 
-	if (!upload((void **)&M->d_wte, d->token_embd, qbytes(wt, M->V, E), "upload token_embd") ||
-	    !upload((void **)&M->d_head, d->output, qbytes(wt, M->V, E), "upload output") ||
+	if (!upload_t(&M->d_wte, d->token_embd, M->embd_type, M->V, E, "upload token_embd") ||
+	    !upload_t(&M->d_head, d->output, M->output_type, M->V, E, "upload output") ||
 	    !upload((void **)&M->d_onorm, d->output_norm, E * sizeof(float), "upload output_norm"))
 		goto fail;
-	M->weight_bytes = 2 * qbytes(wt, M->V, E) + E * sizeof(float);
+	M->weight_bytes = M->V * (moe_row_bytes(M->embd_type, E) + moe_row_bytes(M->output_type, E)) +
+			  E * sizeof(float);
 
 	M->ly = calloc(M->L, sizeof(*M->ly));
 	const size_t qb = qbytes(wt, M->EQ, E), kb = qbytes(wt, M->EKV, E);
@@ -324,28 +433,58 @@ hip_lm *hip_lm_upload(const hip_lm_desc *d)
 			lm_err("lm_upload: NULL tensor of layer %zu", l);
 			goto fail;
 		}
-		memcpy(stage, d->attn_q[l], qb);
-		memcpy(stage + qb, d->attn_k[l], kb);
-		memcpy(stage + qb + kb, d->attn_v[l], kb);
-		if (!upload((void **)&y->wqkv, stage, qb + 2 * kb, "upload attn_q/k/v") ||
-		    !upload((void **)&y->wo, d->attn_o[l], qbytes(wt, E, M->EQ), "upload attn_output") ||
-		    !upload((void **)&y->attn_norm, d->attn_norm[l], E * 4, "upload attn_norm") ||
+		if (!M->generic) {
+			memcpy(stage, d->attn_q[l], qb);
+			memcpy(stage + qb, d->attn_k[l], kb);
+			memcpy(stage + qb + kb, d->attn_v[l], kb);
+			if (!upload((void **)&y->wqkv, stage, qb + 2 * kb, "upload attn_q/k/v") ||
+			    !upload((void **)&y->wo, d->attn_o[l], qbytes(wt, E, M->EQ),
+				    "upload attn_output"))
+				goto fail;
+		} else {
+			y->tq = layer_type(d, l, 0);
+			y->tk = layer_type(d, l, 1);
+			y->tv = layer_type(d, l, 2);
+			y->to = layer_type(d, l, 3);
+			y->gq = product_grid(y->tq, E);
+			y->gk = product_grid(y->tk, E);
+			y->gv = product_grid(y->tv, E);
+			y->go = product_grid(y->to, M->EQ);
+			if (!product_ok(y->tq, E) || !product_ok(y->tk, E) || !product_ok(y->tv, E) ||
+			    !product_ok(y->to, M->EQ) || y->gq <= 0 || y->gk <= 0 || y->gv <= 0 ||
+			    y->go <= 0) {
+				lm_err("lm_upload: layer %zu: E=%zu / heads*128=%zu not supported by "
+				       "the types %d %d %d %d", l, E, M->EQ, y->tq, y->tk, y->tv, y->to);
+				goto fail;
+			}
+			if (!upload_t(&y->wq, d->attn_q[l], y->tq, M->EQ, E, "upload attn_q") ||
+			    !upload_t(&y->wk, d->attn_k[l], y->tk, M->EKV, E, "upload attn_k") ||
+			    !upload_t(&y->wv, d->attn_v[l], y->tv, M->EKV, E, "upload attn_v") ||
+			    !upload_t(&y->wo, d->attn_o[l], y->to, E, M->EQ, "upload attn_output"))
+				goto fail;
+		}
+		if (!upload((void **)&y->attn_norm, d->attn_norm[l], E * 4, "upload attn_norm") ||
 		    !upload((void **)&y->ffn_norm, d->ffn_norm[l], E * 4, "upload ffn_norm"))
 			goto fail;
 		if (d->arch == HIP_LM_OLMOE &&
 		    (!upload((void **)&y->q_norm, d->q_norm[l], M->EQ * 4, "upload attn_q_norm") ||
 		     !upload((void **)&y->k_norm, d->k_norm[l], M->EKV * 4, "upload attn_k_norm")))
 			goto fail;
-		y->moe = hip_moe_upload(d->gate_inp[l], d->gate_e + l * M->NE, d->up_e + l * M->NE,
-					d->down_e + l * M->NE, wt, E, M->EI, M->NE, M->K,
-					d->arch == HIP_LM_MIXTRAL);
+		y->moe = hip_moe_upload_typed(d->gate_inp[l], d->gate_e + l * M->NE,
+					      d->up_e + l * M->NE, d->down_e + l * M->NE,
+					      layer_type(d, l, 4), layer_type(d, l, 5), E, M->EI,
+					      M->NE, M->K, d->arch == HIP_LM_MIXTRAL);
 		if (!y->moe)
 			goto fail; /* hip_moe_upload recorded why */
 		/* scratch for one token now: never allocated under capture */
 		if (!hip_moe_reserve(y->moe, 1))
 			goto fail;
-		M->weight_bytes += qb + 2 * kb + qbytes(wt, E, M->EQ) + 2 * E * 4 +
-				   (y->q_norm ? (M->EQ + M->EKV) * 4 : 0) +
+		M->weight_bytes += (M->generic ? M->EQ * moe_row_bytes(y->tq, E) +
+							 M->EKV * (moe_row_bytes(y->tk, E) +
+								   moe_row_bytes(y->tv, E)) +
+							 E * moe_row_bytes(y->to, M->EQ)
+					       : qb + 2 * kb + qbytes(wt, E, M->EQ)) +
+				   2 * E * 4 + (y->q_norm ? (M->EQ + M->EKV) * 4 : 0) +
 				   hip_moe_weight_bytes(y->moe);
 	}
 	free(stage);
@@ -365,6 +504,7 @@ hip_lm *hip_lm_upload(const hip_lm_desc *d)
 	HIPCHK(hipMemset(M->d_kc, 0, cache), "clear k cache");
 	HIPCHK(hipMemset(M->d_vc, 0, cache), "clear v cache");
 	const size_t EA = E > M->EQ ? E : M->EQ;
+	HIPCHK(hipMalloc((void **)&M->d_x, EA * 4), "hipMalloc(x)");
 	HIPCHK(hipMalloc((void **)&M->d_h0, E * 4), "hipMalloc(h0)");
 	HIPCHK(hipMalloc((void **)&M->d_h1, E * 4), "hipMalloc(h1)");
 	HIPCHK(hipMalloc((void **)&M->d_qkv, (M->EQ + 2 * M->EKV) * 4), "hipMalloc(qkv)");
@@ -480,10 +620,66 @@ fail:
 	return 0;
 }
 
+/* the step of a model with mixed block types (K-quants): the same stages
+ * as enqueue_step's fused kernels, one launch each: the token's embedding
+ * row (any type), rms_norm, the q, k and v products in their own types
+ * (K-quants through Q8_K activations, bit for bit dot_q8_quant), the same
+ * attention, the output product with the residual, rms_norm, the MoE layer
+ * on its experts' types; then the final rms_norm, the lm_head product,
+ * the greedy pick and the counters' advance */
+static int enqueue_step_generic(hip_lm *M, int head, int nact)
+{
+	const int E = (int)M->E, EQ = (int)M->EQ, EK = (int)M->EKV;
+	hipStream_t s = M->stream;
+	for (size_t l = 0; l < M->L; l++) {
+		struct lm_layer *y = &M->ly[l];
+		const size_t co = l * M->KH * M->C * M->HL;
+		if (l == 0) {
+			LCHK(lm_launch_embed(M->embd_type, M->d_wte, E, M->d_st, M->d_prompt, M->d_h0, s),
+			     "embedding");
+			LCHK(lm_launch_norm_rows(1, 1, E, M->d_h0, NULL, y->attn_norm, NULL, M->d_x, NULL,
+						 M->d_st, NULL, NULL, s), "norm");
+		} else { /* h0 = h1 + moe_out */
+			LCHK(lm_launch_norm_rows(1, 1, E, M->d_h1, M->d_moe_out, y->attn_norm, M->d_h0,
+						 M->d_x, NULL, M->d_st, NULL, NULL, s), "norm");
+		}
+		if (!vec_product(y->tq, y->wq, EQ, E, M->d_x, NULL, M->d_qkv, y->gq, s) ||
+		    !vec_product(y->tk, y->wk, EK, E, M->d_x, NULL, M->d_qkv + EQ, y->gk, s) ||
+		    !vec_product(y->tv, y->wv, EK, E, M->d_x, NULL, M->d_qkv + EQ + EK, y->gv, s))
+			return 0;
+		LCHK(lm_launch_attn(M->d_qkv, y->q_norm, y->k_norm, M->d_freq, M->d_st, M->d_kc + co,
+				    M->d_vc + co, M->d_part, M->d_cnt, M->d_attn, (int)M->H,
+				    (int)M->KH, (int)M->C, (int)M->window, M->scale,
+				    M->arch != HIP_LM_OLMOE, (int)l, nact, 1, 0, s), "attention");
+		/* h1 = h0 + attn . Wo^T, moe_in = rms_norm(h1) */
+		if (!vec_product(y->to, y->wo, E, EQ, M->d_attn, M->d_h0, M->d_h1, y->go, s))
+			return 0;
+		LCHK(lm_launch_norm_rows(1, 1, E, M->d_h1, NULL, y->ffn_norm, NULL,
+					 M->d_moe_in + l * M->E, NULL, M->d_st, NULL, NULL, s),
+		     "MoE norm");
+		if (!hip_moe_ffn_dev(y->moe, M->d_moe_in + l * M->E, M->d_moe_out, 1, NULL,
+				     M->d_ids + l * M->K, M->d_w + l * M->K, s))
+			return 0;
+	}
+	if (head) { /* logits = rms_norm(h1 + moe_out) . lm_head^T, the pick */
+		LCHK(lm_launch_norm_rows(1, 1, E, M->d_h1, M->d_moe_out, M->d_onorm, NULL, M->d_x, NULL,
+					 M->d_st, NULL, NULL, s), "final norm");
+		if (!vec_product(M->output_type, M->d_head, (int)M->V, E, M->d_x, NULL, M->d_logits,
+				 M->ghead, s))
+			return 0;
+		LCHK(lm_launch_pick_rows(M->d_logits, 1, (int)M->V, M->d_st, &M->d_st->tok,
+					 M->d_tokens, 0, s), "pick");
+	}
+	LCHK(lm_launch_step_end(M->d_st, s), "step end");
+	return 1;
+}
+
 /* one step on M->stream; head: also the lm_head product and the pick;
  * nact: the attention chunks of this step (lm_attn_active) */
 static int enqueue_step(hip_lm *M, int head, int nact)
 {
+	if (M->generic)
+		return enqueue_step_generic(M, head, nact);
 	const int wt = M->wtype, E = (int)M->E, NQKV = (int)(M->EQ + 2 * M->EKV);
 	hipStream_t s = M->stream;
 	uint32_t *cnt_attn = M->d_cnt;
@@ -770,6 +966,11 @@ int hip_lm_prefill(hip_lm *M, const int *prompt, size_t n, float *logits, int *n
 		       M->st.size, M->C);
 		return 0;
 	}
+	if (M->generic) {
+		lm_err("lm_prefill: a model of mixed block types (K-quants) decodes its prompt "
+		       "a step per id (hip_lm_decode / hip_lm_generate)");
+		return 0;
+	}
 	if (!ensure_io(M, n, 1) || !ensure_prefill(M, n, 1))
 		return 0;
 	HIPCHK(hipStreamSynchronize(M->stream), "synchronize");
@@ -856,7 +1057,7 @@ int hip_lm_generate(hip_lm *M, const int *prompt, size_t n_prompt, size_t n_gen,
 	}
 	/* the prompt as one forward (olmoe_generate's olmoe_prefill,
 	 * olmoe.c:556-558) where it fits the cache; else a step per id */
-	const int pf = n_prompt >= 2 && prefill_fits(M, n_prompt);
+	const int pf = n_prompt >= 2 && prefill_fits(M, n_prompt) && !M->generic;
 	if (!ensure_io(M, n_prompt, steps) || (pf && !ensure_prefill(M, n_prompt, 1)) ||
 	    !start_run(M, prompt, n_prompt))
 		return 0;
@@ -1040,6 +1241,10 @@ hip_lm_batch *hip_lm_batch_new(hip_lm *M, size_t nseq)
 {
 	if (!M || nseq < 1 || nseq > 4096) {
 		lm_err("lm_batch_new: NULL model or %zu sequences (1 .. 4096)", nseq);
+		return NULL;
+	}
+	if (M->generic) {
+		lm_err("lm_batch_new: lockstep batches take models of one block type, Q8_0 or Q4_0");
 		return NULL;
 	}
 	hip_lm_batch *B = calloc(1, sizeof(*B));

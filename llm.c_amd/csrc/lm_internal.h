@@ -60,6 +60,11 @@ int lm_launch_attn(const float *qkv, const float *q_norm, const float *k_norm,
                    float scale, int scale_mul, int layer, int nact, int nseq,
                    size_t cstride, void *stream);
 
+/* out[K] = the dequantized token_embd row of the step's token (wtype 1
+ * Q8_0, 2 Q4_0, 3 Q4_K, 5 Q6_K) */
+int lm_launch_embed(int wtype, const uint8_t *wte, int K, const LmState *st, const int *prompt,
+                    float *out, void *stream);
+
 /* prefill of T prompt rows of nseq sequences (rows z * T + t) at cache row
  * `size` and position pos0 (size + T <= C): q/k norms (q_norm and k_norm
  * both NULL for Mixtral) and RoPE of the stacked q/k/v rows, q into qo

@@ -894,6 +894,71 @@ __global__ __launch_bounds__(LM_NT) void k_lm_pick_rows(const float *__restrict_
 }
 
 /* ---------------------------------------------------------------------- */
+/* k_lm_embed: the step token's row of token_embd in any block type         */
+/* ---------------------------------------------------------------------- */
+
+/*
+ * out[K] = the dequantized row of the step's token (tensor_pick_rows,
+ * tensor.c:263-294, through dequant_row, quant.c:420-575), element by
+ * element with the reference's roundings: Q8_0 d * q, Q4_0 d * (n - 8),
+ * Q4_K fl(fl(d * sc) * q) - fl(dmin * m) with the 6-bit scale and min of
+ * the element's 32-value group (get_scale_min_k4, quant.h:60-69), Q6_K
+ * fl(fl(d * sc) * q) with the signed scale of its 16 values.
+ */
+template <int WT>
+__global__ __launch_bounds__(LM_NT) void k_lm_embed(const uint8_t *__restrict__ wte, int K,
+						    const LmState *__restrict__ st,
+						    const int *__restrict__ prompt,
+						    float *__restrict__ out)
+{
+	const size_t rb = WT == 1   ? (size_t)(K / 32) * 34
+			  : WT == 2 ? (size_t)(K / 32) * 18
+			  : WT == 3 ? (size_t)(K / 256) * 144
+				    : (size_t)(K / 256) * 210;
+	const uint8_t *row = wte + (size_t)step_token(st, prompt) * rb;
+	for (int e = threadIdx.x; e < K; e += LM_NT) {
+		float v;
+		if constexpr (WT == 1 || WT == 2) {
+			const float4 q4 = dequant4<WT>(row, e / 4);
+			v = (e & 3) == 0 ? q4.x : (e & 3) == 1 ? q4.y : (e & 3) == 2 ? q4.z : q4.w;
+		} else if constexpr (WT == 3) {
+			const uint8_t *b = row + (size_t)(e / 256) * 144;
+			const int r = e % 256, j = r / 64, hi = (r % 64) / 32, g = r % 32;
+			const int sb = 2 * j + hi; /* the 32-value group */
+			const uint8_t *sc = b + 4;
+			int sv, mv;
+			if (sb < 4) {
+				sv = sc[sb] & 63;
+				mv = sc[sb + 4] & 63;
+			} else {
+				sv = (sc[sb + 4] & 0xF) | ((sc[sb - 4] >> 6) << 4);
+				mv = (sc[sb + 4] >> 4) | ((sc[sb] >> 6) << 4);
+			}
+			const float d = f16_bits_to_f32((u32)b[0] | ((u32)b[1] << 8));
+			const float dmin = f16_bits_to_f32((u32)b[2] | ((u32)b[3] << 8));
+			const int qb = b[16 + 32 * j + g];
+			const int q = hi ? qb >> 4 : qb & 0xF;
+			const float ds = d * (float)sv, dm = dmin * (float)mv;
+			const float t = ds * (float)q;
+			v = t - dm;
+		} else {
+			const uint8_t *b = row + (size_t)(e / 256) * 210;
+			const int r = e % 256, chunk = r / 128, rr = r % 128, quad = rr / 32,
+				  l = rr % 32;
+			const uint8_t *ql = b + 64 * chunk, *qh = b + 128 + 32 * chunk;
+			const int lo = quad & 1 ? ql[l + 32] : ql[l];
+			const int q = ((quad < 2 ? lo & 0xF : lo >> 4) | (((qh[l] >> (2 * quad)) & 3) << 4)) -
+				      32;
+			const int is = chunk * 8 + l / 16 + 2 * quad;
+			const float d = f16_bits_to_f32((u32)b[208] | ((u32)b[209] << 8));
+			const float ds = d * (float)(int8_t)b[192 + is];
+			v = ds * (float)q;
+		}
+		out[e] = v;
+	}
+}
+
+/* ---------------------------------------------------------------------- */
 /* prefill: a prompt of T rows in one forward                              */
 /* ---------------------------------------------------------------------- */
 
@@ -1314,5 +1379,25 @@ extern "C" int lm_launch_pf_attn(const float *qo, const float *kc, const float *
 	hipLaunchKernelGGL(k_lm_pf_attn, dim3(H, (T + PF_QB - 1) / PF_QB, nseq), dim3(LM_NT), 0,
 			   (hipStream_t)stream, qo, kc, vc, out, H, KH, C, size, T, window, scale,
 			   scale_mul, cstride);
+	return (int)hipGetLastError();
+}
+
+extern "C" int lm_launch_embed(int wtype, const uint8_t *wte, int K, const LmState *st,
+			       const int *prompt, float *out, void *stream)
+{
+	hipStream_t s = (hipStream_t)stream;
+	if ((wtype == 1 || wtype == 2) && K % 32 == 0) {
+		if (wtype == 1)
+			hipLaunchKernelGGL(k_lm_embed<1>, dim3(1), dim3(LM_NT), 0, s, wte, K, st, prompt, out);
+		else
+			hipLaunchKernelGGL(k_lm_embed<2>, dim3(1), dim3(LM_NT), 0, s, wte, K, st, prompt, out);
+	} else if ((wtype == 3 || wtype == 5) && K % 256 == 0) {
+		if (wtype == 3)
+			hipLaunchKernelGGL(k_lm_embed<3>, dim3(1), dim3(LM_NT), 0, s, wte, K, st, prompt, out);
+		else
+			hipLaunchKernelGGL(k_lm_embed<5>, dim3(1), dim3(LM_NT), 0, s, wte, K, st, prompt, out);
+	} else {
+		return (int)hipErrorInvalidValue;
+	}
 	return (int)hipGetLastError();
 }

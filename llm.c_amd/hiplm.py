@@ -35,27 +35,49 @@ def _norm(seed, layer, kind, n, norm_std):
     return hipmoe.synth_normal(seed, _stream(layer, kind), n, 1.0, norm_std)
 
 
+def q4_k_m_types(layers: int) -> dict:
+    """Per-tensor block types as a Q4_K_M GGUF mixes them: Q4_K throughout,
+    Q6_K for the output, and for attn_v and the experts' down in the first
+    and last eighth of the layers and every third layer between
+    (hip_lm_desc's embd_type / output_type / layer_types)."""
+    Q4K, Q6K = hipmoe.Q4_K, hipmoe.Q6_K
+
+    def more(l):
+        return l < layers // 8 or l >= 7 * layers // 8 or (l - layers // 8) % 3 == 2
+    return dict(embd=Q4K, output=Q6K,
+                layers=[(Q4K, Q4K, Q6K if more(l) else Q4K, Q4K, Q4K, Q6K if more(l) else Q4K)
+                        for l in range(layers)])
+
+
 def synth_olmoe(seed: int, layers: int, E: int, H: int, V: int, NE: int, K: int, EI: int,
                 wtype: int = Q8_0, std: float = 0.02, norm_std: float = 0.0,
-                theta: float = 10000.0) -> dict:
+                theta: float = 10000.0, types: dict | None = None) -> dict:
     """An OLMoE-shaped model (models/olmoe/olmoe.c:123-183 tensors): every
-    matrix N(0, std) quantized to wtype, the router fp32 N(0, std), norm
-    weights fp32 (1, or N(1, norm_std))."""
+    matrix N(0, std) quantized to wtype (or to its type in `types`, as
+    q4_k_m_types gives them), the router fp32 N(0, std), norm weights fp32
+    (1, or N(1, norm_std))."""
     G = T_GLOBAL
     md = dict(arch="olmoe", layers=layers, E=E, H=H, V=V, NE=NE, K=K, EI=EI, wtype=wtype,
               theta=theta)
-    md["token_embd"] = hipmoe.synth_quant_matrix(seed, _stream(G, T_TOKEN_EMBD), std, wtype, V, E)
-    md["output"] = hipmoe.synth_quant_matrix(seed, _stream(G, T_OUTPUT), std, wtype, V, E)
+    et = types["embd"] if types else wtype
+    ot = types["output"] if types else wtype
+    if types:
+        md["types"] = types
+    md["token_embd"] = hipmoe.synth_quant_matrix(seed, _stream(G, T_TOKEN_EMBD), std, et, V, E)
+    md["output"] = hipmoe.synth_quant_matrix(seed, _stream(G, T_OUTPUT), std, ot, V, E)
     md["output_norm"] = _norm(seed, G, T_OUTPUT_NORM, E, norm_std)
     md["blk"] = []
     for l in range(layers):
         b = {}
-        for key, kind in (("q", T_ATTN_Q), ("k", T_ATTN_K), ("v", T_ATTN_V), ("o", T_ATTN_O)):
-            b[key] = hipmoe.synth_quant_matrix(seed, _stream(l, kind), std, wtype, E, E)
+        lt = types["layers"][l] if types else (wtype,) * 6
+        for i, (key, kind) in enumerate((("q", T_ATTN_Q), ("k", T_ATTN_K), ("v", T_ATTN_V),
+                                         ("o", T_ATTN_O))):
+            b[key] = hipmoe.synth_quant_matrix(seed, _stream(l, kind), std, lt[i], E, E)
         for key, kind in (("attn_norm", T_ATTN_NORM), ("q_norm", T_Q_NORM),
                           ("k_norm", T_K_NORM), ("ffn_norm", T_FFN_NORM)):
             b[key] = _norm(seed, l, kind, E, norm_std)
-        moe = hipmoe.synth_layer(seed, l, wtype, E, EI, NE, std, None)
+        mt = lt[4] | (lt[5] << 8 if lt[5] != lt[4] else 0)
+        moe = hipmoe.synth_layer(seed, l, mt, E, EI, NE, std, None)
         b["router"], b["gate"], b["up"], b["down"] = (moe["router"], moe["gate"], moe["up"],
                                                       moe["down"])
         md["blk"].append(b)
@@ -64,7 +86,8 @@ def synth_olmoe(seed: int, layers: int, E: int, H: int, V: int, NE: int, K: int,
 
 def synth_mixtral(seed: int, layers: int, E: int, H: int, KH: int, V: int, NE: int, K: int,
                   EI: int, wtype: int = Q4_0, std: float = 0.02, norm_std: float = 0.0,
-                  theta: float = 1e6, window: int = 0, share_layers: bool = False) -> dict:
+                  theta: float = 1e6, window: int = 0, share_layers: bool = False,
+                  types: dict | None = None) -> dict:
     """A Mixtral-shaped model (models/llama/llama.c:80-175 tensors): H query
     heads and KH kv heads of 128, NE experts in separate tensors (kept
     stacked here, one row per expert), every matrix N(0, std) quantized to
@@ -75,8 +98,12 @@ def synth_mixtral(seed: int, layers: int, E: int, H: int, KH: int, V: int, NE: i
     HL = 128
     md = dict(arch="mixtral", layers=layers, E=E, H=H, KH=KH, V=V, NE=NE, K=K, EI=EI,
               wtype=wtype, theta=theta, window=window)
-    md["token_embd"] = hipmoe.synth_quant_matrix(seed, _stream(G, T_TOKEN_EMBD), std, wtype, V, E)
-    md["output"] = hipmoe.synth_quant_matrix(seed, _stream(G, T_OUTPUT), std, wtype, V, E)
+    et = types["embd"] if types else wtype
+    ot = types["output"] if types else wtype
+    if types:
+        md["types"] = types
+    md["token_embd"] = hipmoe.synth_quant_matrix(seed, _stream(G, T_TOKEN_EMBD), std, et, V, E)
+    md["output"] = hipmoe.synth_quant_matrix(seed, _stream(G, T_OUTPUT), std, ot, V, E)
     md["output_norm"] = _norm(seed, G, T_OUTPUT_NORM, E, norm_std)
     md["blk"] = []
     for l in range(layers):
@@ -84,12 +111,15 @@ def synth_mixtral(seed: int, layers: int, E: int, H: int, KH: int, V: int, NE: i
             md["blk"].append(md["blk"][0])
             continue
         b = {}
-        for key, kind, rows, cols in (("q", T_ATTN_Q, H * HL, E), ("k", T_ATTN_K, KH * HL, E),
-                                      ("v", T_ATTN_V, KH * HL, E), ("o", T_ATTN_O, E, H * HL)):
-            b[key] = hipmoe.synth_quant_matrix(seed, _stream(l, kind), std, wtype, rows, cols)
+        lt = types["layers"][l] if types else (wtype,) * 6
+        for i, (key, kind, rows, cols) in enumerate(
+                (("q", T_ATTN_Q, H * HL, E), ("k", T_ATTN_K, KH * HL, E),
+                 ("v", T_ATTN_V, KH * HL, E), ("o", T_ATTN_O, E, H * HL))):
+            b[key] = hipmoe.synth_quant_matrix(seed, _stream(l, kind), std, lt[i], rows, cols)
         for key, kind in (("attn_norm", T_ATTN_NORM), ("ffn_norm", T_FFN_NORM)):
             b[key] = _norm(seed, l, kind, E, norm_std)
-        moe = hipmoe.synth_layer(seed, l, wtype, E, EI, NE, std, None)
+        mt = lt[4] | (lt[5] << 8 if lt[5] != lt[4] else 0)
+        moe = hipmoe.synth_layer(seed, l, mt, E, EI, NE, std, None)
         b["router"], b["gate"], b["up"], b["down"] = (moe["router"], moe["gate"], moe["up"],
                                                       moe["down"])
         md["blk"].append(b)
@@ -149,7 +179,8 @@ class Desc(C.Structure):
                 ("output_norm", _vp), ("attn_norm", _vp), ("attn_q", _vp), ("attn_k", _vp),
                 ("attn_v", _vp), ("attn_o", _vp), ("q_norm", _vp), ("k_norm", _vp),
                 ("ffn_norm", _vp), ("gate_inp", _vp), ("gate_e", _vp), ("up_e", _vp),
-                ("down_e", _vp)]
+                ("down_e", _vp), ("embd_type", C.c_int), ("output_type", C.c_int),
+                ("layer_types", _vp)]
 
 
 _lm_bound = False
@@ -240,6 +271,12 @@ class LmModel:
             d.q_norm, d.k_norm = per_layer("q_norm"), per_layer("k_norm")
         d.gate_inp = per_layer("router")
         d.gate_e, d.up_e, d.down_e = experts("gate"), experts("up"), experts("down")
+        if "types" in md:
+            ty = md["types"]
+            d.embd_type, d.output_type = ty["embd"], ty["output"]
+            lt = np.ascontiguousarray(np.asarray(ty["layers"], np.int32).reshape(-1))
+            self._keep.append(lt)
+            d.layer_types = lt.ctypes.data
         self.h = L.hip_lm_upload(C.byref(d))
         if not self.h:
             raise HipMoeError("hip_lm_upload: " + last_error())

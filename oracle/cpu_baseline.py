@@ -17,7 +17,7 @@ It never touches the GPU.  Prints one JSON line:
 Usage: cpu_baseline.py --spec JSON --seconds S
   spec kind "moe"   : {wtype, E, EI, NE, K, renorm, T, bias_std}
        kind "qmat"  : {wtype, N, Kc, T}
-       kind "model" : {layers, E, H, V, NE, K, EI, C, wtype, prompt, gen}
+       kind "model" : {layers, E, H, V, NE, K, EI, C, wtype, prompt, gen[, q4km]}
 """
 import argparse
 import json
@@ -148,8 +148,10 @@ def bench_model(spec, seconds, pool):
     import hiplm
     import oracle
     if spec.get("arch", "olmoe") == "olmoe":
+        # q4km: the tensors' types mixed as a Q4_K_M file mixes them
+        types = hiplm.q4_k_m_types(spec["layers"]) if spec.get("q4km") else None
         md = hiplm.synth_olmoe(SEED, spec["layers"], spec["E"], spec["H"], spec["V"],
-                               spec["NE"], spec["K"], spec["EI"], spec["wtype"])
+                               spec["NE"], spec["K"], spec["EI"], spec["wtype"], types=types)
         tab = hiplm.ptr_table(md)
     else:
         md = hiplm.synth_mixtral(SEED, spec["layers"], spec["E"], spec["H"], spec["KH"],

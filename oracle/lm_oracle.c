@@ -19,7 +19,9 @@
  * (tests/golden/model_*.npz): reduced models with non-unit norms that run
  * past their context (kvcache_rotate; for Mixtral with a sliding window),
  * the full OLMoE shape, and a two-layer model of the full Mixtral layer
- * shape.
+ * shape; with per-tensor block types as a Q4_K_M file mixes them
+ * (orc_*_new_typed: Q4_K, Q6_K for the output and some layers' attn_v and
+ * experts' down), reduced OLMoE and Mixtral models over 48 positions.
  */
 #define _GNU_SOURCE
 #include "moe_oracle.h"
@@ -36,7 +38,8 @@ struct orc_lm {
 	int arch;
 	size_t L, E, QH, KVH, HLEN, V, NE, K, EI, C, window;
 	float theta, hlen_sq;
-	int wtype;
+	int *types; /* token_embd, output, then per layer attn_q, attn_k, attn_v,
+		     * attn_output, ffn_gate/up_exps, ffn_down_exps */
 	const void *const *p; /* the caller's pointer table */
 	size_t size;          /* kvcache size (kvcache.h:14) */
 	int pos;              /* the model's position counter */
@@ -52,9 +55,12 @@ struct orc_llama {
 	struct orc_lm m;
 };
 
-static size_t qrow_bytes(int wtype, size_t n)
+/* bytes of one row of n values in block type t (quant.h:20-78) */
+static size_t qrow_bytes(int t, size_t n)
 {
-	return n / 32 * (wtype == ORC_Q8_0 ? 34 : 18);
+	if (t == ORC_Q4_K || t == ORC_Q6_K)
+		return n / 256 * (t == ORC_Q4_K ? 144 : 210);
+	return n / 32 * (t == ORC_Q8_0 ? 34 : 18);
 }
 
 /* vector_avx2.h:126-132 */
@@ -120,9 +126,11 @@ static void kv_rotate(struct orc_lm *m)
 	m->size = keep;
 }
 
+/* types: 2 + 6 * layers block types (struct orc_lm), or NULL for wtype in
+ * every quantized tensor */
 static struct orc_lm *lm_new(int arch, size_t layers, size_t E, size_t QH, size_t KVH, size_t V,
 			     size_t NE, size_t topk, size_t EI, size_t C, float theta,
-			     size_t window, int wtype, const void *const *ptrs)
+			     size_t window, int wtype, const int *types, const void *const *ptrs)
 {
 	struct orc_lm *m = calloc(1, sizeof(struct orc_olmoe) > sizeof(struct orc_llama)
 					     ? sizeof(struct orc_olmoe)
@@ -143,7 +151,13 @@ static struct orc_lm *lm_new(int arch, size_t layers, size_t E, size_t QH, size_
 	m->window = window;
 	m->theta = theta;
 	m->hlen_sq = (float)sqrt((double)(float)m->HLEN); /* olmoe.c:150, llama.c:118 */
-	m->wtype = wtype;
+	m->types = malloc((2 + 6 * layers) * sizeof(int));
+	if (!m->types) {
+		free(m);
+		return NULL;
+	}
+	for (size_t i = 0; i < 2 + 6 * layers; i++)
+		m->types[i] = types ? types[i] : wtype;
 	m->p = ptrs;
 	m->kc = calloc(layers * KVH * C * m->HLEN, sizeof(float));
 	m->vc = calloc(layers * KVH * C * m->HLEN, sizeof(float));
@@ -177,6 +191,7 @@ static void lm_free(struct orc_lm *m)
 	free(m->ge);
 	free(m->ue);
 	free(m->de);
+	free(m->types);
 	free(m);
 }
 
@@ -278,23 +293,26 @@ static int lm_decode(struct orc_lm *m, int tok, int pos, float *logits, float *t
 {
 	const size_t E = m->E, NE = m->NE, EI = m->EI, K = m->K, HL = m->HLEN;
 	const size_t EQ = m->QH * HL, EK = m->KVH * HL;
-	const int wt = m->wtype, olmoe = m->arch == ARCH_OLMOE;
+	const int olmoe = m->arch == ARCH_OLMOE, te = m->types[0];
 	if (m->size >= m->C)
 		kv_rotate(m);
 	if (pos >= (int)m->C)
 		pos = (int)m->size;
 
-	orc_dequant_row((const uint8_t *)m->p[0] + (size_t)tok * qrow_bytes(wt, E), wt, m->hidden, E);
-	const size_t gu = EI * qrow_bytes(wt, E), dn = E * qrow_bytes(wt, EI);
+	orc_dequant_row((const uint8_t *)m->p[0] + (size_t)tok * qrow_bytes(te, E), te, m->hidden, E);
 	for (size_t l = 0; l < m->L; l++) {
+		const int *t = m->types + 2 + 6 * l;
+		/* the experts' encoding of orc_moe_ffn: gate/up type | down << 8 */
+		const int wx = t[4] | (t[5] != t[4] ? t[5] << 8 : 0);
+		const size_t gu = EI * qrow_bytes(t[4], E), dn = E * qrow_bytes(t[5], EI);
 		const void *const *p = olmoe ? m->p + 3 + 12 * l : m->p + 3 + l * (7 + 3 * NE);
 		const void *wq = p[1], *wk = p[2], *wv = p[3], *wo = olmoe ? p[6] : p[4];
 		const float *attn_norm = p[0], *ffn_norm = olmoe ? p[7] : p[5];
 		const float *router = olmoe ? p[8] : p[6];
 		rms_norm_row(m->x, m->hidden, attn_norm, E);
-		orc_qmat_mul(m->x, 1, wq, wt, EQ, E, NULL, 0, m->q);
-		orc_qmat_mul(m->x, 1, wk, wt, EK, E, NULL, 0, m->k);
-		orc_qmat_mul(m->x, 1, wv, wt, EK, E, NULL, 0, m->v);
+		orc_qmat_mul(m->x, 1, wq, t[0], EQ, E, NULL, 0, m->q);
+		orc_qmat_mul(m->x, 1, wk, t[1], EK, E, NULL, 0, m->k);
+		orc_qmat_mul(m->x, 1, wv, t[2], EK, E, NULL, 0, m->v);
 		if (olmoe) { /* q/k norms over the full vectors (olmoe.c:454-458) */
 			rms_norm_row(m->q, m->q, (const float *)p[4], EQ);
 			rms_norm_row(m->k, m->k, (const float *)p[5], EK);
@@ -309,7 +327,7 @@ static int lm_decode(struct orc_lm *m, int tok, int pos, float *logits, float *t
 			attention_olmoe(m, l);
 		else
 			attention_llama(m, l);
-		orc_qmat_mul(m->attn, 1, wo, wt, E, EQ, NULL, 0, m->out);
+		orc_qmat_mul(m->attn, 1, wo, t[3], E, EQ, NULL, 0, m->out);
 		for (size_t i = 0; i < E; i++) { /* tensor_add (tensor.c:334-353) */
 			m->hidden[i] = m->hidden[i] + m->out[i];
 			m->resid[i] = m->hidden[i];
@@ -328,7 +346,7 @@ static int lm_decode(struct orc_lm *m, int tok, int pos, float *logits, float *t
 				m->de[e] = p[7 + 2 * NE + e];
 			}
 		}
-		orc_moe_ffn(m->moe_in, m->out, 1, router, NULL, m->ge, m->ue, m->de, wt, E, EI, NE, K,
+		orc_moe_ffn(m->moe_in, m->out, 1, router, NULL, m->ge, m->ue, m->de, wx, E, EI, NE, K,
 			    !olmoe, trace_ids ? trace_ids + l * K : NULL,
 			    trace_w ? trace_w + l * K : NULL, NULL, NULL, nthreads);
 		for (size_t i = 0; i < E; i++)
@@ -337,7 +355,7 @@ static int lm_decode(struct orc_lm *m, int tok, int pos, float *logits, float *t
 	m->size++;
 	rms_norm_row(m->x, m->hidden, (const float *)m->p[2], E);
 	float *lg = logits ? logits : malloc(m->V * sizeof(float));
-	orc_qmat_mul(m->x, 1, m->p[1], wt, m->V, E, NULL, 0, lg);
+	orc_qmat_mul(m->x, 1, m->p[1], m->types[1], m->V, E, NULL, 0, lg);
 	size_t best = 0;
 	for (size_t i = 1; i < m->V; i++)
 		if (lg[i] > lg[best])
@@ -366,7 +384,15 @@ orc_olmoe *orc_olmoe_new(size_t layers, size_t E, size_t H, size_t V, size_t NE,
 			 size_t EI, size_t C, float theta, int wtype, const void *const *ptrs)
 {
 	return (orc_olmoe *)lm_new(ARCH_OLMOE, layers, E, H, H, V, NE, topk, EI, C, theta, 0, wtype,
-				   ptrs);
+				   NULL, ptrs);
+}
+
+orc_olmoe *orc_olmoe_new_typed(size_t layers, size_t E, size_t H, size_t V, size_t NE,
+			       size_t topk, size_t EI, size_t C, float theta, const int *types,
+			       const void *const *ptrs)
+{
+	return (orc_olmoe *)lm_new(ARCH_OLMOE, layers, E, H, H, V, NE, topk, EI, C, theta, 0,
+				   types[0], types, ptrs);
 }
 
 int orc_olmoe_decode(orc_olmoe *m, int tok, int pos, float *logits, float *trace_moe_in,
@@ -391,7 +417,15 @@ orc_llama *orc_llama_new(size_t layers, size_t E, size_t QH, size_t KVH, size_t 
 			 const void *const *ptrs)
 {
 	return (orc_llama *)lm_new(ARCH_LLAMA, layers, E, QH, KVH, V, NE, topk, EI, C, theta, window,
-				   wtype, ptrs);
+				   wtype, NULL, ptrs);
+}
+
+orc_llama *orc_llama_new_typed(size_t layers, size_t E, size_t QH, size_t KVH, size_t V,
+			       size_t NE, size_t topk, size_t EI, size_t C, float theta,
+			       size_t window, const int *types, const void *const *ptrs)
+{
+	return (orc_llama *)lm_new(ARCH_LLAMA, layers, E, QH, KVH, V, NE, topk, EI, C, theta, window,
+				   types[0], types, ptrs);
 }
 
 int orc_llama_decode(orc_llama *m, int tok, int pos, float *logits, float *trace_moe_in,

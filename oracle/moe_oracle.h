@@ -122,6 +122,12 @@ typedef struct orc_olmoe orc_olmoe;
 
 orc_olmoe *orc_olmoe_new(size_t layers, size_t E, size_t H, size_t V, size_t NE, size_t topk,
                          size_t EI, size_t C, float theta, int wtype, const void *const *ptrs);
+/* the same with a block type per quantized tensor, as a GGUF's tensors carry
+ * them: types[0] token_embd, types[1] output, then per layer attn_q, attn_k,
+ * attn_v, attn_output, ffn_gate/up_exps, ffn_down_exps (2 + 6 * layers) */
+orc_olmoe *orc_olmoe_new_typed(size_t layers, size_t E, size_t H, size_t V, size_t NE,
+                               size_t topk, size_t EI, size_t C, float theta, const int *types,
+                               const void *const *ptrs);
 
 /* olmoe_decode (olmoe.c:509-520) of token tok at position pos, then the
  * lm_head product into logits[V] (optional).  Optional traces per layer:
@@ -152,6 +158,9 @@ typedef struct orc_llama orc_llama;
 orc_llama *orc_llama_new(size_t layers, size_t E, size_t QH, size_t KVH, size_t V, size_t NE,
                          size_t topk, size_t EI, size_t C, float theta, size_t window,
                          int wtype, const void *const *ptrs);
+orc_llama *orc_llama_new_typed(size_t layers, size_t E, size_t QH, size_t KVH, size_t V,
+                               size_t NE, size_t topk, size_t EI, size_t C, float theta,
+                               size_t window, const int *types, const void *const *ptrs);
 int orc_llama_decode(orc_llama *m, int tok, int pos, float *logits, float *trace_moe_in,
                      uint32_t *trace_ids, float *trace_w, int nthreads);
 void orc_llama_run(orc_llama *m, const int *prompt, size_t n_prompt, size_t n_gen,

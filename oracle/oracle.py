@@ -61,6 +61,11 @@ def lib():
         L.orc_olmoe_free.restype = None
         L.orc_llama_new.argtypes = [sz, sz, sz, sz, sz, sz, sz, sz, sz, C.c_float, sz, i32, vp]
         L.orc_llama_new.restype = vp
+        L.orc_olmoe_new_typed.argtypes = [sz, sz, sz, sz, sz, sz, sz, sz, C.c_float, vp, vp]
+        L.orc_olmoe_new_typed.restype = vp
+        L.orc_llama_new_typed.argtypes = [sz, sz, sz, sz, sz, sz, sz, sz, sz, C.c_float, sz, vp,
+                                          vp]
+        L.orc_llama_new_typed.restype = vp
         L.orc_llama_decode.argtypes = [vp, i32, i32, vp, vp, vp, vp, i32]
         L.orc_llama_decode.restype = i32
         L.orc_llama_run.argtypes = [vp, vp, sz, sz, vp, vp, i32]
@@ -207,15 +212,24 @@ class OlmoeModel:
         self.V, self.E, self.L, self.K = md["V"], md["E"], md["layers"], md["K"]
         self.table = table  # keeps the pointer table alive
         L = lib()
+        # per-tensor block types (hiplm.q4_k_m_types), as orc_*_new_typed take them
+        self.types = None
+        if "types" in md:
+            t = md["types"]
+            self.types = np.asarray([t["embd"], t["output"]] +
+                                    [x for lt in t["layers"] for x in lt], np.int32)
         if md["arch"] == "olmoe":
             self._dec, self._run, self._free = L.orc_olmoe_decode, L.orc_olmoe_run, L.orc_olmoe_free
-            self.h = L.orc_olmoe_new(md["layers"], md["E"], md["H"], md["V"], md["NE"], md["K"],
-                                     md["EI"], C_ctx, md["theta"], md["wtype"], table)
+            args = (md["layers"], md["E"], md["H"], md["V"], md["NE"], md["K"], md["EI"], C_ctx,
+                    md["theta"])
+            self.h = (L.orc_olmoe_new(*args, md["wtype"], table) if self.types is None else
+                      L.orc_olmoe_new_typed(*args, _p(self.types), table))
         else:
             self._dec, self._run, self._free = L.orc_llama_decode, L.orc_llama_run, L.orc_llama_free
-            self.h = L.orc_llama_new(md["layers"], md["E"], md["H"], md["KH"], md["V"], md["NE"],
-                                     md["K"], md["EI"], C_ctx, md["theta"], md["window"],
-                                     md["wtype"], table)
+            args = (md["layers"], md["E"], md["H"], md["KH"], md["V"], md["NE"], md["K"], md["EI"],
+                    C_ctx, md["theta"], md["window"])
+            self.h = (L.orc_llama_new(*args, md["wtype"], table) if self.types is None else
+                      L.orc_llama_new_typed(*args, _p(self.types), table))
         self.pos = 0
 
     def decode(self, tok: int, trace: bool = False):

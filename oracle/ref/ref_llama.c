@@ -96,9 +96,29 @@ static const tensor_t *ref_lmap(struct ref_lmodel *r, const void *p, int type, s
 	return t;
 }
 
+void *ref_llama_model_new_typed(size_t layers, size_t E, size_t QH, size_t KVH, size_t V,
+				size_t NE, size_t topk, size_t EI, size_t C, float theta,
+				size_t window, const int *types, const void *const *ptrs);
+
 void *ref_llama_model_new(size_t layers, size_t E, size_t QH, size_t KVH, size_t V, size_t NE,
 			  size_t topk, size_t EI, size_t C, float theta, size_t window, int wtype,
 			  const void *const *ptrs)
+{
+	int *types = malloc((2 + 6 * layers) * sizeof(int));
+	for (size_t i = 0; i < 2 + 6 * layers; i++)
+		types[i] = wtype;
+	void *r = ref_llama_model_new_typed(layers, E, QH, KVH, V, NE, topk, EI, C, theta, window,
+					    types, ptrs);
+	free(types);
+	return r;
+}
+
+/* the same with a block type per tensor (types: token_embd, output, then
+ * per layer attn_q, attn_k, attn_v, attn_output, the experts' gate/up, the
+ * experts' down) */
+void *ref_llama_model_new_typed(size_t layers, size_t E, size_t QH, size_t KVH, size_t V,
+				size_t NE, size_t topk, size_t EI, size_t C, float theta,
+				size_t window, const int *types, const void *const *ptrs)
 {
 	struct ref_lmodel *r = calloc(1, sizeof(*r));
 	struct llama *m = &r->m;
@@ -121,27 +141,28 @@ void *ref_llama_model_new(size_t layers, size_t E, size_t QH, size_t KVH, size_t
 	m->hlen_sq = sqrt((scalar_t)m->head_len);
 	const size_t HLEN = m->head_len;
 
-	m->wte = ref_lmap(r, ptrs[0], wtype, V, E);
-	m->lm_head = ref_lmap(r, ptrs[1], wtype, V, E);
+	m->wte = ref_lmap(r, ptrs[0], types[0], V, E);
+	m->lm_head = ref_lmap(r, ptrs[1], types[1], V, E);
 	m->output_norm = ref_lmap(r, ptrs[2], TENSOR_F32, E, 0);
 	m->hl = calloc(layers, sizeof(*m->hl));
 	for (size_t l = 0; l < layers; l++) {
 		const void *const *p = ptrs + 3 + l * (7 + 3 * NE);
+		const int *t = types + 2 + 6 * l;
 		struct llama_layer *hl = &m->hl[l];
 		hl->attn_norm = ref_lmap(r, p[0], TENSOR_F32, E, 0);
-		hl->q_weight = ref_lmap(r, p[1], wtype, QH * HLEN, E);
-		hl->k_weight = ref_lmap(r, p[2], wtype, KVH * HLEN, E);
-		hl->v_weight = ref_lmap(r, p[3], wtype, KVH * HLEN, E);
-		hl->o_weight = ref_lmap(r, p[4], wtype, E, QH * HLEN);
+		hl->q_weight = ref_lmap(r, p[1], t[0], QH * HLEN, E);
+		hl->k_weight = ref_lmap(r, p[2], t[1], KVH * HLEN, E);
+		hl->v_weight = ref_lmap(r, p[3], t[2], KVH * HLEN, E);
+		hl->o_weight = ref_lmap(r, p[4], t[3], E, QH * HLEN);
 		hl->ffn_norm = ref_lmap(r, p[5], TENSOR_F32, E, 0);
 		hl->gate_inp = ref_lmap(r, p[6], TENSOR_F32, NE, E);
 		hl->gate_exp = calloc(NE, sizeof(tensor_t *));
 		hl->up_exp = calloc(NE, sizeof(tensor_t *));
 		hl->down_exp = calloc(NE, sizeof(tensor_t *));
 		for (size_t e = 0; e < NE; e++) {
-			hl->gate_exp[e] = ref_lmap(r, p[7 + e], wtype, EI, E);
-			hl->up_exp[e] = ref_lmap(r, p[7 + NE + e], wtype, EI, E);
-			hl->down_exp[e] = ref_lmap(r, p[7 + 2 * NE + e], wtype, E, EI);
+			hl->gate_exp[e] = ref_lmap(r, p[7 + e], t[4], EI, E);
+			hl->up_exp[e] = ref_lmap(r, p[7 + NE + e], t[4], EI, E);
+			hl->down_exp[e] = ref_lmap(r, p[7 + 2 * NE + e], t[5], E, EI);
 		}
 	}
 	/* llama_load's state tensors (llama.c:177-200) and cache */

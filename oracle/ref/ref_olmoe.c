@@ -90,8 +90,27 @@ static const tensor_t *ref_map(struct ref_model *r, const void *p, int type, siz
 	return t;
 }
 
+void *ref_olmoe_model_new_typed(size_t layers, size_t E, size_t H, size_t V, size_t NE,
+				size_t topk, size_t EI, size_t C, float theta, const int *types,
+				const void *const *ptrs);
+
 void *ref_olmoe_model_new(size_t layers, size_t E, size_t H, size_t V, size_t NE, size_t topk,
 			  size_t EI, size_t C, float theta, int wtype, const void *const *ptrs)
+{
+	int *types = malloc((2 + 6 * layers) * sizeof(int));
+	for (size_t i = 0; i < 2 + 6 * layers; i++)
+		types[i] = wtype;
+	void *r = ref_olmoe_model_new_typed(layers, E, H, V, NE, topk, EI, C, theta, types, ptrs);
+	free(types);
+	return r;
+}
+
+/* the same with a block type per tensor, as a GGUF's tensors carry them:
+ * types[0] token_embd, types[1] output, then per layer attn_q, attn_k,
+ * attn_v, attn_output, ffn_gate/up_exps, ffn_down_exps */
+void *ref_olmoe_model_new_typed(size_t layers, size_t E, size_t H, size_t V, size_t NE,
+				size_t topk, size_t EI, size_t C, float theta, const int *types,
+				const void *const *ptrs)
 {
 	struct ref_model *r = calloc(1, sizeof(*r));
 	struct olmoe *m = &r->m;
@@ -111,24 +130,25 @@ void *ref_olmoe_model_new(size_t layers, size_t E, size_t H, size_t V, size_t NE
 	m->hlen_sq = sqrt((scalar_t)m->head_len);
 	size_t HLEN = m->head_len;
 
-	m->wte = ref_map(r, ptrs[0], wtype, V, E, 0);
-	m->lm_head = ref_map(r, ptrs[1], wtype, V, E, 0);
+	m->wte = ref_map(r, ptrs[0], types[0], V, E, 0);
+	m->lm_head = ref_map(r, ptrs[1], types[1], V, E, 0);
 	m->output_norm = ref_map(r, ptrs[2], TENSOR_F32, E, 0, 0);
 	m->hl = calloc(layers, sizeof(*m->hl));
 	for (size_t l = 0; l < layers; l++) {
 		const void *const *p = ptrs + 3 + 12 * l;
+		const int *t = types + 2 + 6 * l;
 		m->hl[l].attn_norm = ref_map(r, p[0], TENSOR_F32, E, 0, 0);
-		m->hl[l].q_weight = ref_map(r, p[1], wtype, E, E, 0);
-		m->hl[l].k_weight = ref_map(r, p[2], wtype, E, E, 0);
-		m->hl[l].v_weight = ref_map(r, p[3], wtype, E, E, 0);
+		m->hl[l].q_weight = ref_map(r, p[1], t[0], E, E, 0);
+		m->hl[l].k_weight = ref_map(r, p[2], t[1], E, E, 0);
+		m->hl[l].v_weight = ref_map(r, p[3], t[2], E, E, 0);
 		m->hl[l].q_norm = ref_map(r, p[4], TENSOR_F32, E, 0, 0);
 		m->hl[l].k_norm = ref_map(r, p[5], TENSOR_F32, E, 0, 0);
-		m->hl[l].o_weight = ref_map(r, p[6], wtype, E, E, 0);
+		m->hl[l].o_weight = ref_map(r, p[6], t[3], E, E, 0);
 		m->hl[l].ffn_norm = ref_map(r, p[7], TENSOR_F32, E, 0, 0);
 		m->hl[l].gate_inp = ref_map(r, p[8], TENSOR_F32, NE, E, 0);
-		m->hl[l].gate_exps = ref_map(r, p[9], wtype, NE, EI, E);
-		m->hl[l].up_exps = ref_map(r, p[10], wtype, NE, EI, E);
-		m->hl[l].down_exps = ref_map(r, p[11], wtype, NE, E, EI);
+		m->hl[l].gate_exps = ref_map(r, p[9], t[4], NE, EI, E);
+		m->hl[l].up_exps = ref_map(r, p[10], t[4], NE, EI, E);
+		m->hl[l].down_exps = ref_map(r, p[11], t[5], NE, E, EI);
 	}
 	/* olmoe_load's state tensors (olmoe.c:185-199) and cache */
 	m->state.output = tensor_new_zero(2, C, E);

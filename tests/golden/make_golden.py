@@ -355,7 +355,17 @@ MODEL_CASES = {
     # window of 200 masking inside the prefill
     "olmoe_prompt": (2, 1024, 8, 512, 64, 8, 512, 256, hipmoe.Q8_0, 0.1, 200, 8, 4),
     "mixtral_window_prompt": (2, 2048, 16, 512, 8, 2, 1024, 256, hipmoe.Q4_0, 0.1, 240, 8, 4),
+    # K-quant models, the tensors' types mixed as a Q4_K_M GGUF mixes them
+    # (hiplm.q4_k_m_types: Q4_K, Q6_K output, Q6_K attn_v and experts' down
+    # in layer 1 of 2, in 8 of 16): past the context (one kvcache_rotate),
+    # and the full OLMoE-1B-7B shape.  One-id prompts, so that the logits of
+    # every position are written (a Q8_K rounding flip can come at any)
+    "olmoe_q4km": (2, 1024, 8, 512, 64, 8, 512, 32, hipmoe.Q4_K, 0.1, 1, 47, 1),
+    "mixtral_q4km": (2, 2048, 16, 512, 8, 2, 1024, 32, hipmoe.Q4_K, 0.1, 1, 47, 1),
+    "olmoe_full_q4km": (16, 2048, 16, 50304, 64, 8, 1024, 2048, hipmoe.Q4_K, 0.0, 1, 11, 16),
 }
+# cases whose tensors carry per-tensor block types (hiplm.q4_k_m_types)
+MODEL_TYPED = ("olmoe_q4km", "mixtral_q4km", "olmoe_full_q4km")
 # Mixtral cases: (kv heads, sliding window, rope theta).  The window stays
 # at least C - 64: with a longer cache, once the first 64-row block lies
 # wholly outside the window the reference's flash_attention computes
@@ -367,10 +377,11 @@ MIXTRAL_EXTRA = {
     "mixtral_long": (4, 200, 1e6),
     "mixtral_2l_long": (8, 0, 1e6),
     "mixtral_window_prompt": (4, 200, 1e6),
+    "mixtral_q4km": (4, 20, 1e6),
 }
 # cases written in decode order only (one olmoe_decode / llama_decode per
 # prompt id); the others also in generate order (one prefill of the prompt)
-MODEL_DEC_ONLY = ("olmoe_full_long", "mixtral_2l_long")
+MODEL_DEC_ONLY = ("olmoe_full_long", "mixtral_2l_long") + MODEL_TYPED
 MODEL_TOPN = 32
 
 # Several sequences at once, for the lockstep batch (hip_lm_batch_*): nseq
@@ -398,11 +409,13 @@ def model_case(name: str):
     from the seed."""
     import hiplm
     L, E, H, V, NE, K, EI, Cx, wt, nstd, n_prompt, n_gen, stride = MODEL_CASES[name]
+    types = hiplm.q4_k_m_types(L) if name in MODEL_TYPED else None
     if name in MIXTRAL_EXTRA:
         KH, window, theta = MIXTRAL_EXTRA[name]
-        md = hiplm.synth_mixtral(SEED, L, E, H, KH, V, NE, K, EI, wt, 0.02, nstd, theta, window)
+        md = hiplm.synth_mixtral(SEED, L, E, H, KH, V, NE, K, EI, wt, 0.02, nstd, theta, window,
+                                 types=types)
     else:
-        md = hiplm.synth_olmoe(SEED, L, E, H, V, NE, K, EI, wt, 0.02, nstd)
+        md = hiplm.synth_olmoe(SEED, L, E, H, V, NE, K, EI, wt, 0.02, nstd, types=types)
     prompt = hiplm.synth_prompt(SEED, n_prompt, V)
     return md, prompt, MODEL_CASES[name]
 
@@ -435,19 +448,30 @@ def model_goldens(R, names):
     R.ref_llama_model_new.restype = vp
     R.ref_llama_model_run.argtypes = [vp, vp, sz, i32, sz, vp, vp]
     R.ref_llama_model_free.argtypes = [vp]
+    R.ref_olmoe_model_new_typed.argtypes = [sz, sz, sz, sz, sz, sz, sz, sz, C.c_float, vp, vp]
+    R.ref_olmoe_model_new_typed.restype = vp
+    R.ref_llama_model_new_typed.argtypes = [sz, sz, sz, sz, sz, sz, sz, sz, sz, C.c_float, sz,
+                                            vp, vp]
+    R.ref_llama_model_new_typed.restype = vp
     for name in names:
         md, prompt, case = model_case(name)
         L, E, H, V, NE, K, EI, Cx, wt, nstd, n_prompt, n_gen, stride = case
         tab = model_table(md)
         fx = dict(seed=SEED, prompt=prompt, sha_model=model_digest(md), stride=stride)
         modes = (("dec", 0),) if name in MODEL_DEC_ONLY else (("dec", 0), ("pre", 1))
+        ty = np.asarray([wt] * (2 + 6 * L), np.int32)
+        if "types" in md:
+            t = md["types"]
+            ty = np.asarray([t["embd"], t["output"]] + [x for lt in t["layers"] for x in lt],
+                            np.int32)
         for mode, prefill in modes:
             if md["arch"] == "olmoe":
-                h = R.ref_olmoe_model_new(L, E, H, V, NE, K, EI, Cx, md["theta"], wt, tab)
+                h = R.ref_olmoe_model_new_typed(L, E, H, V, NE, K, EI, Cx, md["theta"], p(ty),
+                                                tab)
                 run, free = R.ref_olmoe_model_run, R.ref_olmoe_model_free
             else:
-                h = R.ref_llama_model_new(L, E, H, md["KH"], V, NE, K, EI, Cx, md["theta"],
-                                          md["window"], wt, tab)
+                h = R.ref_llama_model_new_typed(L, E, H, md["KH"], V, NE, K, EI, Cx,
+                                                md["theta"], md["window"], p(ty), tab)
                 run, free = R.ref_llama_model_run, R.ref_llama_model_free
             lg = np.empty((n_gen + 1, V), np.float32)
             toks = np.empty(n_gen + 1, np.int32)

@@ -6,8 +6,9 @@ oracle/ref/ref_olmoe.c and ref_llama.c over seeded weights,
 tests/golden/model_*.npz) bit for bit, on reduced models with non-unit norms
 that run past their context (kvcache_rotate; Mixtral's keeps its sliding
 window, and its flash_attention masks), at the full OLMoE shape and on two
-layers of the Mixtral-8x7B shape; and the reference's generate order (one
-prefill of the prompt) within fp32 rounding."""
+layers of the Mixtral-8x7B shape; with per-tensor block types (Q4_K_M's
+mix of Q4_K and Q6_K); and the reference's generate order (one prefill of
+the prompt) within fp32 rounding."""
 import numpy as np
 import pytest
 
@@ -151,3 +152,17 @@ def test_model_oracle_matches_reference_long_prompt(name):
     generate order (one prefill of the whole prompt, whose flash_attention
     masks rows outside the window, nn.c:597-603) within fp32 rounding."""
     _check_long(name)
+
+
+@pytest.mark.parametrize("name", ["olmoe_q4km", "mixtral_q4km"])
+def test_model_oracle_matches_reference_q4_k_m(name):
+    """Per-tensor block types as a Q4_K_M GGUF mixes them (hiplm.q4_k_m_types:
+    Q4_K, the output and layer 1's attn_v and experts' down Q6_K): the
+    embedding row through dequant_row, every product through Q8_K
+    activations (dot_q8_quant, quant.c:627-666), the K-quant experts; every
+    position of a one-id prompt and 47 steps, past the context, bit for
+    bit."""
+    toks, lg, g, stride = _run(name)
+    assert np.array_equal(toks, g["dec_tokens"])
+    assert np.array_equal(bits(lg[:, ::stride]), bits(g["dec_logits"]))
+
