@@ -306,7 +306,9 @@ hip_moe_layer *hip_moe_upload_typed(const float *gate_inp, const void *const *ga
 	const size_t wbytes = NE * (2 * L->gu_stride + L->down_stride) +
 			      (grouped ? 2 * NE * L->gu_stride : 0);
 	L->weight_bytes = NE * E * sizeof(float) + wbytes;
-	L->fused_grid = kq ? 0 : moe_fused_grid(wtype, E, EI, NE);
+	/* the persistent first launch of the decode path (K-quants: routing
+	 * and gate/up) */
+	L->fused_grid = kq ? moe_kq_decode_grid(wtype, E, NE) : moe_fused_grid(wtype, E, EI, NE);
 
 	HIPCHK(hipGetDevice(&L->device), "hipGetDevice");
 	L->stream = device_stream(L->device);
@@ -423,7 +425,8 @@ static int ensure_scratch(hip_moe_layer *L, size_t T, hipStream_t s)
 	/* decode kernel: epoch-tagged partials, for every T it can take up to
 	 * this capacity */
 	L->part_words = 1;
-	for (size_t t = 1; L->fused_grid > 0 && t <= T && t * L->topk <= MOE_FUSED_MAX_P; t++) {
+	for (size_t t = 1; !L->kq && L->fused_grid > 0 && t <= T && t * L->topk <= MOE_FUSED_MAX_P;
+	     t++) {
 		size_t w = moe_fused_part_words(t, L->topk, L->E, L->EI, L->fused_grid);
 		L->part_words = w > L->part_words ? w : L->part_words;
 	}
@@ -573,6 +576,11 @@ int hip_moe_ffn_dev_noalloc(hip_moe_layer *L, const float *d_x, float *d_out, si
 	}
 	if (!check_T(T))
 		return 0;
+	if (L->kq) {
+		set_err("ffn_noalloc: K-quant experts take the layer's own scratch "
+			"(hip_moe_ffn_dev)");
+		return 0;
+	}
 	if (L->fused_grid <= 0 ||
 	    !moe_fused_supported(L->wtype, L->E, L->EI, L->NE, T, L->topk) ||
 	    (L->path != HIP_MOE_PATH_AUTO && L->path != HIP_MOE_PATH_DECODE)) {
@@ -648,11 +656,24 @@ int hip_moe_route_dev(hip_moe_layer *L, const float *d_x, size_t T,
 /* the path a call of T tokens takes (HIP_MOE_PATH_*), 0 if none applies */
 static int choose_path(const hip_moe_layer *L, size_t T)
 {
-	/* K-quant experts: the per-pair products of kq_moe.hip for every T */
-	if (L->kq)
-		return L->path == HIP_MOE_PATH_AUTO || L->path == HIP_MOE_PATH_GEMV
-			       ? HIP_MOE_PATH_GEMV
-			       : 0;
+	/* K-quant experts: two launches (routing and gate/up, then down and
+	 * combine) for a decode-sized call, else the per-pair products of
+	 * kq_moe.hip */
+	if (L->kq) {
+		const int kdec = L->fused_grid > 0 &&
+				 moe_kq_decode_supported(L->wtype, L->E, L->EI, L->NE, T, L->topk) &&
+				 moe_kq_down_combine_ok(T, L->topk, L->E);
+		switch (L->path) {
+		case HIP_MOE_PATH_DECODE:
+			return kdec ? HIP_MOE_PATH_DECODE : 0;
+		case HIP_MOE_PATH_GEMV:
+			return HIP_MOE_PATH_GEMV;
+		case HIP_MOE_PATH_GROUPED:
+			return 0;
+		default:
+			return kdec ? HIP_MOE_PATH_DECODE : HIP_MOE_PATH_GEMV;
+		}
+	}
 	int dec = L->fused_grid > 0 &&
 		  moe_fused_supported(L->wtype, L->E, L->EI, L->NE, T, L->topk);
 	int grp = moe_prefill_supported(L->wtype, L->E, L->EI, L->NE) &&
@@ -714,6 +735,18 @@ int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 	if (!path) {
 		set_err("ffn: the requested path does not apply to this layer and T=%zu", T);
 		return 0;
+	}
+	if (path == HIP_MOE_PATH_DECODE && L->kq) {
+		LCHK(moe_launch_kq_route_gateup(L->wtype, d_x, L->d_router, d_router_bias, L->d_gate,
+						L->d_up, L->gu_stride, ids, w, L->d_h, L->d_sync,
+						(int)T, (int)L->E, (int)L->EI, (int)L->NE,
+						(int)L->topk, L->renorm, L->fused_grid, L->spin, s),
+		     "K-quant routing + gate/up");
+		LCHK(moe_launch_kq_down_combine(L->dtype, L->d_down, L->down_stride, ids, w, L->d_h,
+						d_out, (int)T, (int)L->topk, (int)L->E,
+						(int)L->EI, s),
+		     "K-quant down + combine");
+		return 1;
 	}
 	if (path == HIP_MOE_PATH_DECODE) {
 		LCHK(moe_launch_fused(L->wtype, d_x, L->d_router, d_router_bias, L->d_gate,

@@ -31,146 +31,16 @@
  * Bound: HBM.  Algorithmic bytes per call: per pair, 2 * EI rows of E
  * columns and E rows of EI columns in their block types, plus x and h.
  */
-#include "moe_device.h"
+#include "kq_device.h"
 
 #define KG_THREADS 256
 #define KD_THREADS 256
 #define KD_ROWS 32 /* down rows a workgroup takes: 8 lanes each */
 #define KD_CB 4    /* super-blocks of every row a chunk stages */
-
-template <int WT> struct kqb;
-template <> struct kqb<3> {
-	static constexpr int BYTES = 144;
-};
-template <> struct kqb<5> {
-	static constexpr int BYTES = 210;
-};
-
-/* ------------------------------------------------------------------ */
-/* Q8_K of one token and the integer sums of one super-block            */
-/* ------------------------------------------------------------------ */
-
-/* quantize_row_q8 (quant.c:627-654) of 256 values, lane l holding 4l..4l+3
- * (the same steps as kquant.hip's) */
-__device__ static inline u32 kg_q8k(float4 v, int lane, float *d, int *bsum)
-{
-	const float xv[4] = {v.x, v.y, v.z, v.w};
-	float best = 0.0f, bv = 0.0f;
-	int bi = 0x7fffffff;
-#pragma unroll
-	for (int j = 0; j < 4; j++) {
-		const float a = fabsf(xv[j]);
-		if (a > best) {
-			best = a;
-			bv = xv[j];
-			bi = 4 * lane + j;
-		}
-	}
-#pragma unroll
-	for (int off = 32; off >= 1; off >>= 1) {
-		const float ob = __shfl_xor(best, off, WAVE), ov = __shfl_xor(bv, off, WAVE);
-		const int oi = __shfl_xor(bi, off, WAVE);
-		if (ob > best || (ob == best && oi < bi)) {
-			best = ob;
-			bv = ov;
-			bi = oi;
-		}
-	}
-	u32 packed = 0;
-	int s = 0;
-	if (best == 0.0f) {
-		*d = 0.0f;
-	} else {
-		const float iscale = -127.0f / bv;
-		*d = 1.0f / iscale;
-#pragma unroll
-		for (int j = 0; j < 4; j++) {
-			int q = (int)roundf(iscale * xv[j]);
-			q = q < 127 ? q : 127;
-			s += q;
-			packed |= (u32)(q & 0xff) << (8 * j);
-		}
-	}
-	s += __shfl_xor(s, 1, WAVE);
-	s += __shfl_xor(s, 2, WAVE);
-	*bsum = s;
-	return packed;
-}
-
-/* dwords of a block at a 2-byte aligned global address: n, realigned (the
- * buffer is readable MOE_WEIGHT_SLACK bytes past its last block) */
-template <int N>
-__device__ static inline void kg_load(const uint8_t *p, u32 (&w)[N])
-{
-	const u32 sh = (u32)((uintptr_t)p & 3);
-	u32 raw[N + 1];
-	load_dwords<N + 1>(p - sh, raw);
-#pragma unroll
-	for (int k = 0; k < N; k++)
-		w[k] = __builtin_amdgcn_alignbyte(raw[k + 1], raw[k], sh);
-}
-
-/* Q4_K block (36 dwords) against the staged Q8_K block q8 (64 dwords, its
- * 16 sums bs): sumi and msum, and the scale products with yd */
-__device__ static inline void kg_q4k(const u32 (&w)[36], const int *q8, const int *bs, float yd,
-				     float &dsc, int &sumi, float &dmn, int &msum)
-{
-	dsc = yd * f16_bits_to_f32(w[0]);
-	dmn = -yd * f16_bits_to_f32(w[0] >> 16);
-	const u32 s0 = w[1], s1 = w[2], s2 = w[3];
-	const u32 sc_lo = s0 & 0x3f3f3f3fu, m_lo = s1 & 0x3f3f3f3fu;
-	const u32 sc_hi = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
-	const u32 m_hi = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
-	int si = 0, mi = 0;
-#pragma unroll
-	for (int j = 0; j < 4; j++) {
-		const u32 scw = j < 2 ? sc_lo : sc_hi, mw = j < 2 ? m_lo : m_hi;
-		const int sh = 16 * (j & 1);
-		const int sa = (scw >> sh) & 0xff, sb = (scw >> (sh + 8)) & 0xff;
-		const int ma = (mw >> sh) & 0xff, mb = (mw >> (sh + 8)) & 0xff;
-		int lo = 0, hi = 0;
-#pragma unroll
-		for (int k = 0; k < 8; k++) {
-			lo = __builtin_amdgcn_sdot4((int)(w[4 + 8 * j + k] & 0x0f0f0f0fu), q8[16 * j + k],
-						    lo, false);
-			hi = __builtin_amdgcn_sdot4((int)((w[4 + 8 * j + k] >> 4) & 0x0f0f0f0fu),
-						    q8[16 * j + 8 + k], hi, false);
-		}
-		si += sa * lo + sb * hi;
-		mi += ma * (bs[4 * j] + bs[4 * j + 1]) + mb * (bs[4 * j + 2] + bs[4 * j + 3]);
-	}
-	sumi = si;
-	msum = mi;
-}
-
-/* Q6_K block (53 dwords): sumi with the q6 + 32 bytes, 32 * bsum taken off
- * per 16 values */
-__device__ static inline void kg_q6k(const u32 (&w)[53], const int *q8, const int *bs, float yd,
-				     float &dsc, int &sumi)
-{
-	dsc = yd * f16_bits_to_f32(w[52]);
-	int si = 0;
-#pragma unroll
-	for (int c = 0; c < 2; c++)
-#pragma unroll
-		for (int g = 0; g < 4; g++)
-#pragma unroll
-			for (int hf = 0; hf < 2; hf++) {
-				int s = 0;
-#pragma unroll
-				for (int m = 0; m < 4; m++) {
-					const u32 lq = w[16 * c + (g & 1) * 8 + 4 * hf + m];
-					const u32 lo = g < 2 ? lq & 0x0f0f0f0fu : (lq >> 4) & 0x0f0f0f0fu;
-					const u32 hi = ((w[32 + 8 * c + 4 * hf + m] >> (2 * g)) & 0x03030303u) << 4;
-					s = __builtin_amdgcn_sdot4((int)(lo | hi), q8[32 * c + 8 * g + 4 * hf + m],
-								   s, false);
-				}
-				const int j = 8 * c + 2 * g + hf;
-				const int sc = (int)(int8_t)((w[48 + j / 4] >> (8 * (j % 4))) & 0xff);
-				si += sc * (s - 32 * bs[j]);
-			}
-	sumi = si;
-}
+#define KC_DOTS 32 /* (row, pair) dots of a k_kq_down_combine workgroup: 8 lanes each */
+#define KC_CB 4    /* super-blocks of every dot a chunk stages (whole 8-byte steps: 4 * 210) */
+#define KC_MAXP 8  /* pairs of a k_kq_down_combine call (P divides KC_DOTS) */
+#define KC_HPAD 8  /* floats between two pairs' staged h (banks apart) */
 
 /* ------------------------------------------------------------------ */
 /* gate/up                                                              */
@@ -275,108 +145,6 @@ __global__ __launch_bounds__(KG_THREADS) void k_kq_gateup(
 /* down                                                                 */
 /* ------------------------------------------------------------------ */
 
-/* accumulator l's part of one staged super-block (LDS) of a down row: the
- * elements l, l + 8, ... with h from LDS */
-__device__ static inline void kd_q4k(const uint8_t *blk, const float *hb, int l, float &acc)
-{
-	/* as kd_q6k: every LDS read first, then the products in their order
-	 * (element 64j + 32hi + 8m + l is step 8j + 4hi + m of the chain) */
-	u32 sc[12], q[4][4];
-	float hv[32];
-	const u32 b0 = blk[0], b1 = blk[1], b2 = blk[2], b3 = blk[3];
-#pragma unroll
-	for (int i = 0; i < 12; i++)
-		sc[i] = blk[4 + i];
-#pragma unroll
-	for (int j = 0; j < 4; j++)
-#pragma unroll
-		for (int m = 0; m < 4; m++)
-			q[j][m] = blk[16 + 32 * j + l + 8 * m];
-#pragma unroll
-	for (int jj = 0; jj < 32; jj++)
-		hv[jj] = hb[l + 8 * jj];
-	const float d = f16_bits_to_f32(b0 | (b1 << 8));
-	const float dmin = f16_bits_to_f32(b2 | (b3 << 8));
-#pragma unroll
-	for (int j = 0; j < 4; j++) {
-		int s1, m1, s2, m2;
-		/* get_scale_min_k4 (quant.h:63-73) for sub-blocks 2j, 2j + 1 */
-		if (j < 2) {
-			s1 = sc[2 * j] & 63;
-			m1 = sc[2 * j + 4] & 63;
-			s2 = sc[2 * j + 1] & 63;
-			m2 = sc[2 * j + 5] & 63;
-		} else {
-			s1 = (sc[2 * j + 4] & 0xF) | ((sc[2 * j - 4] >> 6) << 4);
-			m1 = (sc[2 * j + 4] >> 4) | ((sc[2 * j] >> 6) << 4);
-			s2 = (sc[2 * j + 5] & 0xF) | ((sc[2 * j - 3] >> 6) << 4);
-			m2 = (sc[2 * j + 5] >> 4) | ((sc[2 * j + 1] >> 6) << 4);
-		}
-		const float d1 = d * (float)s1, n1 = dmin * (float)m1;
-		const float d2 = d * (float)s2, n2 = dmin * (float)m2;
-#pragma unroll
-		for (int m = 0; m < 4; m++) {
-			float v = d1 * (float)(q[j][m] & 0xF);
-			v = v - n1;
-			acc = fmaf(v, hv[8 * j + m], acc);
-		}
-#pragma unroll
-		for (int m = 0; m < 4; m++) {
-			float v = d2 * (float)(q[j][m] >> 4);
-			v = v - n2;
-			acc = fmaf(v, hv[8 * j + 4 + m], acc);
-		}
-	}
-}
-
-__device__ static inline void kd_q6k(const uint8_t *blk, const float *hb, int l, float &acc)
-{
-	/* every LDS read of the super-block goes out before the first product
-	 * (the grid holds one wave per SIMD, so nothing else hides a read's
-	 * round trip); the products and their order are unchanged: element
-	 * 128c + 32g + 16hf + 8m + l is step j = 16c + 4g + 2hf + m of the
-	 * lane's chain */
-	u32 ql[2][2][2][2], qh[2][2][2]; /* [c][hf][m][+32] and [c][hf][m] */
-	int sc[16];
-	float hv[32];
-#pragma unroll
-	for (int c = 0; c < 2; c++)
-#pragma unroll
-		for (int hf = 0; hf < 2; hf++)
-#pragma unroll
-			for (int m = 0; m < 2; m++) {
-				const int e = 16 * hf + l + 8 * m;
-				ql[c][hf][m][0] = blk[64 * c + e];
-				ql[c][hf][m][1] = blk[64 * c + e + 32];
-				qh[c][hf][m] = blk[128 + 32 * c + e];
-			}
-#pragma unroll
-	for (int i = 0; i < 16; i++)
-		sc[i] = ((const int8_t *)(blk + 192))[i];
-	const u32 dlo = blk[208], dhi = blk[209];
-#pragma unroll
-	for (int jj = 0; jj < 32; jj++)
-		hv[jj] = hb[l + 8 * jj];
-	const float d = f16_bits_to_f32(dlo | (dhi << 8));
-#pragma unroll
-	for (int c = 0; c < 2; c++)
-#pragma unroll
-		for (int g = 0; g < 4; g++)
-#pragma unroll
-			for (int hf = 0; hf < 2; hf++) {
-				const float vs = d * (float)sc[8 * c + 2 * g + hf];
-#pragma unroll
-				for (int m = 0; m < 2; m++) {
-					const int lo = (int)ql[c][hf][m][g & 1];
-					const int q = ((g < 2 ? lo & 0xF : lo >> 4) |
-						       (((int)(qh[c][hf][m] >> (2 * g)) & 3) << 4)) -
-						      32;
-					const float vt = (float)q * vs;
-					acc = fmaf(vt, hv[16 * c + 4 * g + 2 * hf + m], acc);
-				}
-			}
-}
-
 /*
  * Workgroup (row block r0 = blockIdx.x * KD_ROWS, pair p): wave w holds rows
  * r0 + 8w .. r0 + 8w + 7, lane 8k + l accumulator l of row r0 + 8w + k.
@@ -478,6 +246,158 @@ __global__ __launch_bounds__(KD_THREADS) void k_kq_down(const uint8_t *__restric
 }
 
 /* ------------------------------------------------------------------ */
+/* down and combine of a decode-sized call                              */
+/* ------------------------------------------------------------------ */
+
+/*
+ * The second launch of the decode-sized K-quant layer (the first,
+ * k_kq_route_gateup in moe_decode.hip, routes and writes h[P][EI], ids and
+ * weights): workgroup b takes output rows r0 = b * RB .. r0 + RB - 1 (RB =
+ * KC_DOTS / P) for every pair p = t * K + k, one (row, pair) dot per 8
+ * lanes, the same dot and order as k_kq_down (dot_f32_quant of h[p] with
+ * down row r of expert ids[p]); then out[t][r] = sum over the slots k in
+ * order of y / (1/w), as k_combine adds them (olmoe.c:401-403,
+ * tensor.c:334-353, 435-456).  The chunk's h of every pair is staged in
+ * LDS with the 32 dots' runs of super-blocks.  Dots go pair-major (dot d:
+ * pair d / RB, row d % RB), so a wave's eight dots read at most two pairs'
+ * h, whose LDS rows are padded apart by KC_HPAD floats (other banks).
+ *
+ * Dynamic LDS: P rows of KC_CB * 256 + KC_HPAD floats of h, then KC_DOTS
+ * runs of KC_CB super-blocks.
+ */
+template <int WT, bool PIPE, int PM>
+__global__ __launch_bounds__(KD_THREADS) void k_kq_down_combine(
+	const uint8_t *__restrict__ down, size_t dn_stride, const u32 *__restrict__ ids,
+	const float *__restrict__ wts, const float *__restrict__ h, float *__restrict__ out, int T,
+	int K, int E, int EI)
+{
+	constexpr int BY = kqb<WT>::BYTES;
+	constexpr int RUN = KC_CB * BY; /* bytes of one dot's run */
+	static_assert(RUN % 8 == 0, "a run is staged in 8-byte steps");
+	constexpr int HS = KC_CB * 256 + KC_HPAD; /* floats of one pair's staged h */
+	extern __shared__ __attribute__((aligned(16))) float kc_lds[];
+	__shared__ float s_y[KC_DOTS];
+	/* each pair's expert as a byte offset: a pointer read from LDS would be
+	 * a generic one, and its flat loads wait on the LDS counter */
+	__shared__ size_t s_eo[KC_MAXP];
+	const int P = T * K, RB = KC_DOTS / P, nb = EI / 256;
+	float *s_h = kc_lds;                              /* [P][HS] */
+	uint8_t *s_w = (uint8_t *)(kc_lds + (size_t)P * HS); /* [KC_DOTS][RUN] */
+	const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+	const int l = lane & 7, dk = wave * 8 + lane / 8; /* this lane's dot */
+	const int r0 = blockIdx.x * RB;
+	const size_t rb = (size_t)nb * BY;
+	if (tid < P) /* each pair's expert, once */
+		s_eo[tid] = (size_t)ids[tid] * dn_stride;
+	__syncthreads();
+
+	constexpr int NIT = (KC_DOTS * (RUN / 8) + KD_THREADS - 1) / KD_THREADS;
+	/* PM >= P: the pairs' h a thread holds in flight (registers) */
+	constexpr int NH = (PM * KC_CB * 64 + KD_THREADS - 1) / KD_THREADS;
+	const float *hp = s_h + (size_t)(dk / RB) * HS;
+	float acc = 0.0f;
+	/* round c: chunk c's loads go out, chunk c - 1's dots run from LDS while
+	 * they are in flight (PIPE: rows of several chunks; one chunk has its
+	 * dots after its stores, and no second chunk's registers), then chunk c
+	 * goes to LDS; every load of a chunk is issued before any is stored (as
+	 * k_kq_down) */
+	for (int c0 = 0; c0 < nb + KC_CB; c0 += KC_CB) {
+		const int cb = min(KC_CB, nb - c0), run = cb * BY;
+		/* a native vector type: an array of the float4 struct stays in
+		 * scratch memory */
+		typedef float f4v __attribute__((ext_vector_type(4)));
+		u32 v[NIT][3], shv[NIT];
+		f4v hv[NH];
+		if (c0 < nb) {
+#pragma unroll
+			for (int it = 0; it < NIT; it++) {
+				const int e = tid + it * KD_THREADS;
+				const int d = e / (RUN / 8), o = 8 * (e % (RUN / 8));
+				shv[it] = 0;
+				if (e < KC_DOTS * (RUN / 8) && o < run) {
+					const int row = r0 + d % RB, p = d / RB;
+					const uint8_t *src = down + s_eo[p] + (size_t)row * rb +
+							     (size_t)c0 * BY + o;
+					const u32 sh = (u32)((uintptr_t)src & 3);
+					const u32 *a = (const u32 *)(src - sh);
+					v[it][0] = a[0];
+					v[it][1] = a[1];
+					v[it][2] = a[2];
+					shv[it] = sh;
+				}
+			}
+#pragma unroll
+			for (int u = 0; u < NH; u++) {
+				/* float4 i of the chunk's P x KC_CB * 64, clamped into
+				 * the chunk (the stores below skip the clamped ones) */
+				const int i = tid + u * KD_THREADS;
+				const int p = min(i / (KC_CB * 64), P - 1);
+				const int q = min(i % (KC_CB * 64), cb * 64 - 1);
+				hv[u] = ((const f4v *)(h + (size_t)p * EI + (size_t)c0 * 256))[q];
+			}
+		}
+		if (PIPE && c0 > 0) { /* the previous chunk, staged last round */
+			const int pcb = min(KC_CB, nb - (c0 - KC_CB));
+			for (int k = 0; k < pcb; k++) {
+				const uint8_t *blk = s_w + dk * RUN + k * BY;
+				if constexpr (WT == 3)
+					kd_q4k(blk, hp + k * 256, l, acc);
+				else
+					kd_q6k(blk, hp + k * 256, l, acc);
+			}
+		}
+		if (c0 >= nb)
+			break;
+		if (PIPE)
+			__syncthreads(); /* the previous chunk's readers are done */
+#pragma unroll
+		for (int u = 0; u < NH; u++) {
+			const int i = tid + u * KD_THREADS;
+			const int p = i / (KC_CB * 64), q = i % (KC_CB * 64);
+			if (p < P && q < cb * 64)
+				((f4v *)(s_h + (size_t)p * HS))[q] = hv[u];
+		}
+#pragma unroll
+		for (int it = 0; it < NIT; it++) {
+			const int e = tid + it * KD_THREADS;
+			const int d = e / (RUN / 8), o = 8 * (e % (RUN / 8));
+			if (e < KC_DOTS * (RUN / 8) && o < run)
+				*(uint2 *)(s_w + d * RUN + o) =
+					make_uint2(__builtin_amdgcn_alignbyte(v[it][1], v[it][0], shv[it]),
+						   __builtin_amdgcn_alignbyte(v[it][2], v[it][1], shv[it]));
+		}
+		__syncthreads();
+		if (!PIPE) { /* the one chunk */
+			for (int k = 0; k < cb; k++) {
+				const uint8_t *blk = s_w + dk * RUN + k * BY;
+				if constexpr (WT == 3)
+					kd_q4k(blk, hp + k * 256, l, acc);
+				else
+					kd_q6k(blk, hp + k * 256, l, acc);
+			}
+			break;
+		}
+	}
+	/* vector_reduce_sum's tree, as k_kq_down */
+	acc = acc + __shfl_xor(acc, 4, 8);
+	acc = acc + __shfl_xor(acc, 2, 8);
+	acc = acc + __shfl_xor(acc, 1, 8);
+	if (l == 0) /* (row, pair) in the combine's order */
+		s_y[(dk % RB) * P + dk / RB] = acc;
+	__syncthreads();
+	if (tid < RB * T) {
+		const int r = tid / T, t = tid % T;
+		float o = 0.0f;
+		for (int k = 0; k < K; k++) {
+			const int p = t * K + k;
+			const float inv = 1.0f / wts[p];
+			o = o + s_y[r * P + p] / inv;
+		}
+		out[(size_t)t * E + r0 + r] = o;
+	}
+}
+
+/* ------------------------------------------------------------------ */
 /* host side                                                            */
 /* ------------------------------------------------------------------ */
 
@@ -515,5 +435,45 @@ extern "C" int moe_launch_kq_down(int dt, const uint8_t *down, size_t dn_stride,
 	else
 		hipLaunchKernelGGL(k_kq_down<5>, grid, dim3(KD_THREADS), 0, s, down, dn_stride, ids, h,
 				   y, E, EI);
+	return (int)hipGetLastError();
+}
+
+/* the down + combine launch of a decode-sized call of P = T * K pairs: P a
+ * divisor of KC_DOTS up to KC_MAXP, every output row of E in one workgroup's
+ * block of KC_DOTS / P */
+extern "C" int moe_kq_down_combine_ok(size_t T, size_t K, size_t E)
+{
+	const size_t P = T * K;
+	return P >= 1 && P <= KC_MAXP && KC_DOTS % P == 0 && E % (KC_DOTS / P) == 0;
+}
+
+extern "C" int moe_launch_kq_down_combine(int dt, const uint8_t *down, size_t dn_stride,
+					  const u32 *ids, const float *w, const float *h,
+					  float *out, int T, int K, int E, int EI, void *stream)
+{
+	if (!moe_kq_down_combine_ok((size_t)T, (size_t)K, (size_t)E) || EI % 256 ||
+	    (dt != 3 && dt != 5))
+		return (int)hipErrorInvalidValue;
+	const int P = T * K, RB = KC_DOTS / P;
+	const size_t lds = (size_t)P * (KC_CB * 256 + KC_HPAD) * sizeof(float) +
+			   (size_t)KC_DOTS * KC_CB * (dt == 3 ? 144 : 210);
+	const dim3 grid(E / RB);
+	hipStream_t s = (hipStream_t)stream;
+	const bool pipe = EI > 256 * KC_CB;
+	const int pm = P <= 1 ? 1 : P <= 2 ? 2 : P <= 4 ? 4 : 8;
+	const void *fn = NULL;
+#define KCPICK(D_, PI_, PM_)                                                  \
+	if (dt == D_ && pipe == PI_ && pm == PM_)                             \
+		fn = (const void *)k_kq_down_combine<D_, PI_, PM_>;
+	KCPICK(3, false, 1) KCPICK(3, false, 2) KCPICK(3, false, 4) KCPICK(3, false, 8)
+	KCPICK(3, true, 1) KCPICK(3, true, 2) KCPICK(3, true, 4) KCPICK(3, true, 8)
+	KCPICK(5, false, 1) KCPICK(5, false, 2) KCPICK(5, false, 4) KCPICK(5, false, 8)
+	KCPICK(5, true, 1) KCPICK(5, true, 2) KCPICK(5, true, 4) KCPICK(5, true, 8)
+#undef KCPICK
+	static_assert(KC_MAXP == 8, "instances cover pair bounds 1, 2, 4, 8");
+	void *args[] = {&down, &dn_stride, &ids, &w, &h, &out, &T, &K, &E, &EI};
+	hipError_t rc = hipLaunchKernel(fn, grid, dim3(KD_THREADS), args, lds, s);
+	if (rc != hipSuccess)
+		return (int)rc;
 	return (int)hipGetLastError();
 }

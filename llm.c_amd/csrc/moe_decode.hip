@@ -62,6 +62,7 @@
  * the panel, one block each, and the item's 32 h values.
  */
 #include "moe_device.h"
+#include "kq_device.h"
 
 #include <pthread.h>
 
@@ -1233,6 +1234,283 @@ extern "C" int moe_launch_fused(int wtype, const float *x, const float *router,
 	void *args[] = {&a};
 	hipError_t rc = hipLaunchKernel(g.fn, dim3(grid), dim3(g.NT), args,
 					decode_lds_bytes(g, (size_t)E), (hipStream_t)stream);
+	if (rc != hipSuccess)
+		return (int)rc;
+	return (int)hipGetLastError();
+}
+
+/* ---------------------------------------------------------------------- */
+/* K-quant experts: routing and gate/up of a decode-sized call            */
+/* ---------------------------------------------------------------------- */
+
+/*
+ * k_kq_route_gateup: the first of the two launches of a decode-sized layer
+ * on K-quant experts (the second, k_kq_down_combine in kq_moe.hip, takes
+ * the down products and the combine).  The reference's down product runs
+ * one fp32 dot over all EI values of h per output (dot_f32_quant in
+ * fused_ffn_silu, nn.c:483-492), so an output needs every h value of its
+ * pair first: the launch boundary is that wait.
+ *
+ * Routing as k_moe_decode's (router rows by workgroups j < NE into tagged
+ * replicas, softmax and top-k in every workgroup), with the same epoch,
+ * start flags and poison rules.  Then units of R rows of the gate and R of
+ * the up matrix of one (token, slot) pair p, R = NT / (2 * NB) so that a
+ * unit is one super-block per thread: thread i takes super-block i % NB of
+ * row i / NB (gate rows first, then up), its integer sums against the
+ * token's Q8_K blocks (quantized by the workgroup while the routing is in
+ * flight) go to LDS, and thread r < R runs row r's sequential steps
+ * (dot_q4_K_q8_K / dot_q6_K_q8_K) for gate and up and writes h[p][row] =
+ * (g / (1 + expf(-g))) * u (nn.c:455-478), bit for bit k_kq_gateup.  Each
+ * workgroup takes a balanced contiguous range of the P * EI / R units; the
+ * next unit's super-block is loaded while the current one's sums run.
+ * Workgroup 0 writes the call's ids and weights.
+ */
+#define KQ_NT 512
+
+template <int GT, int E>
+__global__ __launch_bounds__(KQ_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void k_kq_route_gateup(DecodeArgs a)
+{
+	constexpr int NT = KQ_NT, NB = E / 256, R = NT / (2 * NB), RS = NB + 1;
+	constexpr int QS = 65, BS = 17; /* token rows padded: distinct banks */
+	constexpr int BY = kqb<GT>::BYTES, DW = GT == 3 ? 36 : 53;
+	static_assert(2 * R * NB == NT, "a unit is one super-block per thread");
+	extern __shared__ float lds[];
+	__shared__ u32 s_ids[MOE_FUSED_MAX_P];
+	__shared__ float s_w[MOE_FUSED_MAX_P];
+	__shared__ u32 s_epoch;
+	__shared__ u32 s_poison;
+	__shared__ uint64_t s_tab[32];
+	__shared__ int s_q8[NB * QS];
+	__shared__ float s_d[NB];
+	__shared__ int s_bs[NB * BS];
+	__shared__ int s_rec[4][2 * R * RS];
+
+	const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+	const int G = (int)gridDim.x, b = (int)blockIdx.x;
+	const int CH = a.EI / R, N = a.n_items; /* units per pair, all units */
+	const int u0 = item_lo(b, N, G), u1 = item_lo(b + 1, N, G);
+	const size_t rb = (size_t)NB * BY;
+
+	/* quantize_row_q8 of token t into s_q8 / s_bs / s_d (wave w takes
+	 * blocks w, w + NT / 64, ...) */
+	auto quantize = [&](int t) {
+		for (int i = wave; i < NB; i += NT / WAVE) {
+			const float4 v = ((const float4 *)(a.x + (size_t)t * E + (size_t)i * 256))[lane];
+			float d;
+			int bs;
+			const u32 q = kg_q8k(v, lane, &d, &bs);
+			s_q8[i * QS + lane] = (int)q;
+			if (lane % 4 == 0)
+				s_bs[i * BS + lane / 4] = bs;
+			if (lane == 0)
+				s_d[i] = d;
+		}
+	};
+	/* this thread's super-block of unit u: matrix (gate, up), row, block */
+	const int mat = tid / (R * NB), rl = (tid % (R * NB)) / NB, sb = tid % NB;
+	auto load_unit = [&](int u, u32 (&w)[DW]) {
+		const int p = u / CH, row = (u % CH) * R + rl;
+		const uint8_t *blk = (mat ? a.up : a.gate) + (size_t)s_ids[p] * a.gu_stride +
+				     (size_t)row * rb + (size_t)sb * BY;
+		if constexpr (GT == 3)
+			load_dwords<36>(blk, w);
+		else
+			kg_load<53>(blk, w);
+	};
+
+	if (tid < 32)
+		s_tab[tid] = moe_exp2_tab[tid];
+	u32 prev_epoch = 0, err0 = 0;
+	if (tid == 0) { /* consumed late: the loads overlap routing */
+		prev_epoch = ld_dev_u32(a.sync);
+		err0 = ld_dev_u32(a.sync + MOE_SYNC_ERR_WORD);
+	}
+	if (b < a.NE)
+		router_row<NT, E>(a, b, prev_epoch, lds, nullptr);
+	/* the first unit's token does not depend on routing */
+	int cur_t = -1;
+	if (u0 < u1) {
+		cur_t = u0 / CH / a.K;
+		quantize(cur_t);
+	}
+	if (tid == 0) {
+		s_epoch = prev_epoch + 1;
+		s_poison = err0;
+	}
+	__syncthreads();
+	const u32 epoch = s_epoch;
+	/* a wait of an earlier launch ran out (k_moe_decode's rule): NaN h,
+	 * ids 0 and NaN weights, so the second launch writes NaN outputs; no
+	 * start flag, no epoch advance */
+	if (s_poison) {
+		const float nan = __builtin_nanf("");
+		for (int i = b * NT + tid; i < a.T * a.K * a.EI; i += G * NT)
+			a.out[i] = nan;
+		if (b == 0)
+			for (int i = tid; i < a.T * a.K; i += NT) {
+				a.ids_out[i] = 0;
+				a.w_out[i] = nan;
+			}
+		return;
+	}
+	u32 *startf = a.sync + a.off_start;
+	if (tid == 0 && b != 0)
+		st_dev_u32(&startf[b], epoch);
+	route_local<NT>(a, epoch, lds, s_ids, s_w, s_tab);
+	if (b == 0)
+		for (int i = tid; i < a.T * a.K; i += NT) {
+			a.ids_out[i] = s_ids[i];
+			a.w_out[i] = s_w[i];
+		}
+
+	u32 w[DW];
+	if (u0 < u1)
+		load_unit(u0, w);
+	for (int u = u0; u < u1; u++) {
+		const int p = u / CH, t = p / a.K;
+		if (t != cur_t) { /* a later token: the previous unit's readers are done */
+			quantize(t);
+			cur_t = t;
+		}
+		__syncthreads(); /* the token's blocks; the previous unit's records read */
+		float dsc, dmn = 0.0f;
+		int sumi, msum = 0;
+		if constexpr (GT == 3)
+			kg_q4k(w, s_q8 + sb * QS, s_bs + sb * BS, s_d[sb], dsc, sumi, dmn, msum);
+		else
+			kg_q6k(w, s_q8 + sb * QS, s_bs + sb * BS, s_d[sb], dsc, sumi);
+		if (u + 1 < u1) /* the next unit's block, in flight during the sums */
+			load_unit(u + 1, w);
+		const int slot = (mat * R + rl) * RS + sb;
+		((float *)s_rec[0])[slot] = dsc;
+		s_rec[1][slot] = sumi;
+		((float *)s_rec[2])[slot] = dmn;
+		s_rec[3][slot] = msum;
+		__syncthreads();
+		/* thread r < R: row r's steps for gate and up (dot_q4_K_q8_K
+		 * returns acc + acc_m, dot_q6_K_q8_K acc) */
+		if (tid < R) {
+			float v[2];
+#pragma unroll
+			for (int m = 0; m < 2; m++) {
+				const int o = (m * R + tid) * RS;
+				float acc = 0.0f, acc_m = 0.0f;
+#pragma unroll
+				for (int i = 0; i < NB; i++) {
+					acc = fmaf(((const float *)s_rec[0])[o + i], (float)s_rec[1][o + i],
+						   acc);
+					if constexpr (GT == 3)
+						acc_m = fmaf(((const float *)s_rec[2])[o + i],
+							     (float)s_rec[3][o + i], acc_m);
+				}
+				v[m] = GT == 3 ? acc + acc_m : acc;
+			}
+			const float g = v[0];
+			a.out[(size_t)p * a.EI + (size_t)(u % CH) * R + tid] =
+				(g / (1.0f + moe_expf(-g))) * v[1];
+		}
+	}
+
+	/* workgroup 0 advances the epoch once every workgroup has read it (as
+	 * k_moe_decode) */
+	if (b != 0)
+		return;
+	if (wait_flags<NT>(startf + 1, G - 1, epoch, a.sync + MOE_SYNC_ERR_WORD, MOE_ERR_FLAGS,
+			   a.spin) &&
+	    tid == 0)
+		st_dev_u32(a.sync, epoch);
+}
+
+static const void *kq_decode_fn(int gt, size_t E)
+{
+#define KQPICK(G_, E_)                                                        \
+	if (gt == G_ && E == E_)                                             \
+		return (const void *)k_kq_route_gateup<G_, E_>;
+	KQPICK(3, 1024)
+	KQPICK(3, 2048)
+	KQPICK(3, 4096)
+	KQPICK(5, 1024)
+	KQPICK(5, 2048)
+	KQPICK(5, 4096)
+#undef KQPICK
+	return NULL;
+}
+
+/* dynamic LDS: the routing scratch (router row and token transposed, or
+ * the per-wave top-k scratch) */
+static size_t kq_decode_lds_bytes(size_t E)
+{
+	size_t rt = (size_t)2 * 8 * (E / 8 + 4) + CHAIN_OVERRUN;
+	size_t tk = (size_t)(KQ_NT / WAVE) * (MOE_MAX_NE + 2 * MOE_MAX_TOPK);
+	return (rt > tk ? rt : tk) * sizeof(float);
+}
+
+/* a decode-sized call of T tokens on gate/up type gt: the instance exists,
+ * NE fits one wave's lanes, the pairs fit the routing slots, the units
+ * divide d_ff (R = 256 / (E / 256) rows) */
+extern "C" int moe_kq_decode_supported(int gt, size_t E, size_t EI, size_t NE, size_t T,
+				       size_t K)
+{
+	if (!kq_decode_fn(gt, E) || NE > WAVE || NE == 0 || T == 0 ||
+	    T * K > MOE_FUSED_MAX_P)
+		return 0;
+	const size_t R = KQ_NT / (2 * (E / 256));
+	return EI % R == 0 && EI >= R;
+}
+
+/* one workgroup per CU, all resident (the routing waits on the router
+ * workgroups), or 0 */
+extern "C" int moe_kq_decode_grid(int gt, size_t E, size_t NE)
+{
+	const void *fn = kq_decode_fn(gt, E);
+	int dev = 0, ncu = 0, per = 0;
+	if (!fn || hipGetDevice(&dev) != hipSuccess ||
+	    hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+		return 0;
+	if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, fn, KQ_NT,
+							 kq_decode_lds_bytes(E)) != hipSuccess ||
+	    per < 1)
+		return 0;
+	return ncu >= (int)NE && ncu >= MOE_FUSED_MAX_P ? ncu : 0;
+}
+
+extern "C" int moe_launch_kq_route_gateup(int gt, const float *x, const float *router,
+					  const float *bias, const uint8_t *gate, const uint8_t *up,
+					  size_t gu_stride, uint32_t *ids, float *w, float *h,
+					  uint32_t *sync, int T, int E, int EI, int NE, int K,
+					  int renorm, int grid, int spin, void *stream)
+{
+	const void *fn = kq_decode_fn(gt, (size_t)E);
+	if (!fn || grid < NE || grid < T ||
+	    !moe_kq_decode_supported(gt, (size_t)E, (size_t)EI, (size_t)NE, (size_t)T, (size_t)K))
+		return (int)hipErrorInvalidValue;
+	SyncLayout sl = sync_layout((size_t)T, (size_t)NE, grid);
+	DecodeArgs a = {};
+	a.x = x;
+	a.router = router;
+	a.bias = bias;
+	a.gate = gate;
+	a.up = up;
+	a.gu_stride = gu_stride;
+	a.ids_out = ids;
+	a.w_out = w;
+	a.out = h;
+	a.sync = sync;
+	a.T = T;
+	a.E = E;
+	a.EI = EI;
+	a.NE = NE;
+	a.K = K;
+	a.renorm = renorm;
+	a.n_items = T * K * (EI / (KQ_NT / (2 * (E / 256))));
+	a.off_start = (int)sl.off_start;
+	a.off_rep = (int)sl.off_rep;
+	a.rep_stride = (int)sl.rep_stride;
+	a.spin = spin > 0 ? spin : MOE_SPIN_DEFAULT;
+	void *args[] = {&a};
+	hipError_t rc = hipLaunchKernel(fn, dim3(grid), dim3(KQ_NT), args, kq_decode_lds_bytes(E),
+					(hipStream_t)stream);
 	if (rc != hipSuccess)
 		return (int)rc;
 	return (int)hipGetLastError();

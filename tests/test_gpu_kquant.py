@@ -141,7 +141,7 @@ def test_gpu_kq_layer_vs_reference_golden(name):
     say(f"kq layer {name}: wtype={wt:#x} T={T} E={E} EI={EI} NE={NE} K={K}")
     M = hipmoe.MoeLayer.from_synth(lw, K, bool(renorm))
     try:
-        assert M.path_for(T) == hipmoe.PATH_GEMV
+        M.set_path(hipmoe.PATH_GEMV)
         out, ids, w = M.ffn(x)
     finally:
         M.free()
@@ -169,6 +169,41 @@ def test_gpu_kq_layer_token_counts_vs_oracle(T):
     assert nbad == 0
 
 
+@pytest.mark.parametrize("name,Ts", [("olmoe_q4k_q6k", (1,)), ("olmoe_q6k", (1,)),
+                                     ("mixtral_q4k_q6k", (1, 2, 4))])
+def test_gpu_kq_decode_path_vs_oracle(name, Ts):
+    """The decode-sized K-quant layer (two launches: routing and gate/up,
+    then down and combine without partials) for T * K <= 8 pairs: outputs
+    equal the oracle's moe_ffn (bit for bit the reference's, by the golden
+    tests above) and the five-launch path's, ids and weights the oracle's,
+    over successive calls (the routing epoch advances); the OLMoE shape's
+    d_ff is one staged chunk of the down rows, Mixtral's 14 (the pipelined
+    form); past 8 pairs the layer takes the per-pair products."""
+    (wt, E, EI, NE, K, renorm, _), lw, _, _ = _kq_layer(name)
+    M = hipmoe.MoeLayer.from_synth(lw, K, bool(renorm))
+    try:
+        for T in Ts:
+            M.set_path(hipmoe.PATH_AUTO)
+            assert M.path_for(T) == hipmoe.PATH_DECODE, (name, T)
+            for rep in range(3):
+                x = hipmoe.synth_input(SEED, 0x9300 + 16 * T + rep, T, E)
+                M.set_path(hipmoe.PATH_AUTO)
+                out, ids, w = M.ffn(x)
+                M.set_path(hipmoe.PATH_GEMV)
+                out_g, ids_g, w_g = M.ffn(x)
+                oout, oids, ow, _, _ = oracle.moe_ffn(x, lw, K, bool(renorm), None)
+                assert np.array_equal(ids, oids) and np.array_equal(bits(w), bits(ow))
+                nbad = int(np.sum(bits(out) != bits(oout)))
+                say(f"kq decode {name} T={T} call {rep}: {nbad} of {out.size} outputs differ")
+                assert nbad == 0
+                assert np.array_equal(bits(out), bits(out_g))
+        M.set_path(hipmoe.PATH_AUTO)
+        big = 8 // K + 1
+        assert M.path_for(big) == hipmoe.PATH_GEMV, (name, big)
+    finally:
+        M.free()
+
+
 @pytest.mark.parametrize("wt", [hipmoe.Q4_K | hipmoe.Q6_K << 8, hipmoe.Q6_K | hipmoe.Q4_K << 8,
                                 hipmoe.Q4_K])
 def test_gpu_kq_expert_ffn_vs_oracle(wt):
@@ -183,7 +218,7 @@ def test_gpu_kq_expert_ffn_vs_oracle(wt):
             want = oracle.fused_ffn(x, lw["gate"][e], lw["up"][e], lw["down"][e], wt, E, EI)
             assert np.array_equal(bits(got), bits(want)), (e, rel_l2(got, want))
         with pytest.raises(hipmoe.HipMoeError, match="does not apply"):
-            M.set_path(hipmoe.PATH_DECODE)
+            M.set_path(hipmoe.PATH_GROUPED)
             M.ffn(x.reshape(1, E))
     finally:
         M.free()
