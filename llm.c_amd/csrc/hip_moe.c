@@ -661,8 +661,7 @@ static int choose_path(const hip_moe_layer *L, size_t T)
 	 * kq_moe.hip */
 	if (L->kq) {
 		const int kdec = L->fused_grid > 0 &&
-				 moe_kq_decode_supported(L->wtype, L->E, L->EI, L->NE, T, L->topk) &&
-				 moe_kq_down_combine_ok(T, L->topk, L->E);
+				 moe_kq_decode_supported(L->wtype, L->E, L->EI, L->NE, T, L->topk);
 		switch (L->path) {
 		case HIP_MOE_PATH_DECODE:
 			return kdec ? HIP_MOE_PATH_DECODE : 0;
@@ -742,10 +741,18 @@ int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 						(int)T, (int)L->E, (int)L->EI, (int)L->NE,
 						(int)L->topk, L->renorm, L->fused_grid, L->spin, s),
 		     "K-quant routing + gate/up");
-		LCHK(moe_launch_kq_down_combine(L->dtype, L->d_down, L->down_stride, ids, w, L->d_h,
-						d_out, (int)T, (int)L->topk, (int)L->E,
-						(int)L->EI, s),
-		     "K-quant down + combine");
+		if (moe_kq_down_combine_ok(T, L->topk, L->E, L->EI)) {
+			LCHK(moe_launch_kq_down_combine(L->dtype, L->d_down, L->down_stride, ids, w,
+							L->d_h, d_out, (int)T, (int)L->topk,
+							(int)L->E, (int)L->EI, s),
+			     "K-quant down + combine");
+			return 1;
+		}
+		LCHK(moe_launch_kq_down(L->dtype, L->d_down, L->down_stride, ids, L->d_h,
+					L->d_ypart, P, (int)L->E, (int)L->EI, s),
+		     "K-quant down");
+		LCHK(moe_launch_combine(L->d_ypart, w, d_out, (int)T, (int)L->topk, (int)L->E, 1, s),
+		     "combine");
 		return 1;
 	}
 	if (path == HIP_MOE_PATH_DECODE) {

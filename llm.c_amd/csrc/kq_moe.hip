@@ -37,9 +37,9 @@
 #define KD_THREADS 256
 #define KD_ROWS 32 /* down rows a workgroup takes: 8 lanes each */
 #define KD_CB 4    /* super-blocks of every row a chunk stages */
-#define KC_DOTS 32 /* (row, pair) dots of a k_kq_down_combine workgroup: 8 lanes each */
-#define KC_CB 4    /* super-blocks of every dot a chunk stages (whole 8-byte steps: 4 * 210) */
-#define KC_MAXP 8  /* pairs of a k_kq_down_combine call (P divides KC_DOTS) */
+#define KC_DOTS 64 /* (row, pair) dots of a k_kq_down_combine workgroup: 8 lanes each */
+#define KC_CB 4    /* d_ff super-blocks k_kq_down_combine stages (whole 8-byte steps: 4 * 210) */
+#define KC_MAXP 8  /* pairs of a k_kq_down_combine call (a power of two: it divides KC_DOTS) */
 #define KC_HPAD 8  /* floats between two pairs' staged h (banks apart) */
 
 /* ------------------------------------------------------------------ */
@@ -250,27 +250,31 @@ __global__ __launch_bounds__(KD_THREADS) void k_kq_down(const uint8_t *__restric
 /* ------------------------------------------------------------------ */
 
 /*
- * The second launch of the decode-sized K-quant layer (the first,
- * k_kq_route_gateup in moe_decode.hip, routes and writes h[P][EI], ids and
- * weights): workgroup b takes output rows r0 = b * RB .. r0 + RB - 1 (RB =
- * KC_DOTS / P) for every pair p = t * K + k, one (row, pair) dot per 8
- * lanes, the same dot and order as k_kq_down (dot_f32_quant of h[p] with
- * down row r of expert ids[p]); then out[t][r] = sum over the slots k in
- * order of y / (1/w), as k_combine adds them (olmoe.c:401-403,
- * tensor.c:334-353, 435-456).  The chunk's h of every pair is staged in
- * LDS with the 32 dots' runs of super-blocks.  Dots go pair-major (dot d:
+ * The second launch of the decode-sized K-quant layer where d_ff is at most
+ * KC_CB super-blocks (the first, k_kq_route_gateup in moe_decode.hip,
+ * routes and writes h[P][EI], ids and weights): workgroup b takes output
+ * rows r0 = b * RB .. r0 + RB - 1 (RB = KC_DOTS / P) for every pair p = t *
+ * K + k, one (row, pair) dot per 8 lanes, the same dot and order as
+ * k_kq_down (dot_f32_quant of h[p] with down row r of expert ids[p]); then
+ * out[t][r] = sum over the slots k in order of y / (1/w), as k_combine adds
+ * them (olmoe.c:401-403, tensor.c:334-353, 435-456).  The rows' super-blocks
+ * and every pair's h are staged in LDS once.  Dots go pair-major (dot d:
  * pair d / RB, row d % RB), so a wave's eight dots read at most two pairs'
- * h, whose LDS rows are padded apart by KC_HPAD floats (other banks).
+ * h, whose LDS rows are padded apart by KC_HPAD floats (other banks).  The h
+ * loads (independent of the routing) go out before the wait for the ids.
+ * Longer d_ff takes k_kq_down and k_combine after the first launch: there
+ * every workgroup would re-read all pairs' h chunk by chunk.
  *
  * Dynamic LDS: P rows of KC_CB * 256 + KC_HPAD floats of h, then KC_DOTS
  * runs of KC_CB super-blocks.
  */
-template <int WT, bool PIPE, int PM>
-__global__ __launch_bounds__(KD_THREADS) void k_kq_down_combine(
+template <int WT, int PM>
+__global__ __launch_bounds__(KC_DOTS * 8) void k_kq_down_combine(
 	const uint8_t *__restrict__ down, size_t dn_stride, const u32 *__restrict__ ids,
 	const float *__restrict__ wts, const float *__restrict__ h, float *__restrict__ out, int T,
 	int K, int E, int EI)
 {
+	constexpr int NTH = KC_DOTS * 8; /* 8 lanes per dot */
 	constexpr int BY = kqb<WT>::BYTES;
 	constexpr int RUN = KC_CB * BY; /* bytes of one dot's run */
 	static_assert(RUN % 8 == 0, "a run is staged in 8-byte steps");
@@ -280,103 +284,78 @@ __global__ __launch_bounds__(KD_THREADS) void k_kq_down_combine(
 	/* each pair's expert as a byte offset: a pointer read from LDS would be
 	 * a generic one, and its flat loads wait on the LDS counter */
 	__shared__ size_t s_eo[KC_MAXP];
+	__shared__ float s_wt[KC_MAXP];
 	const int P = T * K, RB = KC_DOTS / P, nb = EI / 256;
 	float *s_h = kc_lds;                              /* [P][HS] */
 	uint8_t *s_w = (uint8_t *)(kc_lds + (size_t)P * HS); /* [KC_DOTS][RUN] */
 	const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
 	const int l = lane & 7, dk = wave * 8 + lane / 8; /* this lane's dot */
 	const int r0 = blockIdx.x * RB;
-	const size_t rb = (size_t)nb * BY;
-	if (tid < P) /* each pair's expert, once */
-		s_eo[tid] = (size_t)ids[tid] * dn_stride;
-	__syncthreads();
+	const size_t rb = (size_t)nb * BY, run = (size_t)nb * BY;
 
-	constexpr int NIT = (KC_DOTS * (RUN / 8) + KD_THREADS - 1) / KD_THREADS;
-	/* PM >= P: the pairs' h a thread holds in flight (registers) */
-	constexpr int NH = (PM * KC_CB * 64 + KD_THREADS - 1) / KD_THREADS;
+	constexpr int NIT = (KC_DOTS * (RUN / 8) + NTH - 1) / NTH;
+	/* PM >= P: the pairs' h a thread loads */
+	constexpr int NH = (PM * KC_CB * 64 + NTH - 1) / NTH;
+	/* a native vector type: an array of the float4 struct stays in scratch
+	 * memory */
+	typedef float f4v __attribute__((ext_vector_type(4)));
+	f4v hv[NH];
+#pragma unroll
+	for (int u = 0; u < NH; u++) {
+		/* float4 i of the pairs' P x KC_CB * 64, clamped into the d_ff
+		 * (the stores below skip the clamped ones) */
+		const int i = tid + u * NTH;
+		const int p = min(i / (KC_CB * 64), P - 1), q = min(i % (KC_CB * 64), nb * 64 - 1);
+		hv[u] = ((const f4v *)(h + (size_t)p * EI))[q];
+	}
+	if (tid < P) { /* each pair's expert and slot weight, once */
+		s_eo[tid] = (size_t)ids[tid] * dn_stride;
+		s_wt[tid] = wts[tid];
+	}
+	__syncthreads();
+	/* every weight load goes out before any is stored (as k_kq_down) */
+	u32 v[NIT][3], shv[NIT];
+#pragma unroll
+	for (int it = 0; it < NIT; it++) {
+		const int e = tid + it * NTH;
+		const int d = e / (RUN / 8), o = 8 * (e % (RUN / 8));
+		shv[it] = 0;
+		if (e < KC_DOTS * (RUN / 8) && o < (int)run) {
+			const int row = r0 + d % RB, p = d / RB;
+			const uint8_t *src = down + s_eo[p] + (size_t)row * rb + o;
+			const u32 sh = (u32)((uintptr_t)src & 3);
+			const u32 *a = (const u32 *)(src - sh);
+			v[it][0] = a[0];
+			v[it][1] = a[1];
+			v[it][2] = a[2];
+			shv[it] = sh;
+		}
+	}
+#pragma unroll
+	for (int u = 0; u < NH; u++) {
+		const int i = tid + u * NTH;
+		const int p = i / (KC_CB * 64), q = i % (KC_CB * 64);
+		if (p < P && q < nb * 64)
+			((f4v *)(s_h + (size_t)p * HS))[q] = hv[u];
+	}
+#pragma unroll
+	for (int it = 0; it < NIT; it++) {
+		const int e = tid + it * NTH;
+		const int d = e / (RUN / 8), o = 8 * (e % (RUN / 8));
+		if (e < KC_DOTS * (RUN / 8) && o < (int)run)
+			*(uint2 *)(s_w + d * RUN + o) =
+				make_uint2(__builtin_amdgcn_alignbyte(v[it][1], v[it][0], shv[it]),
+					   __builtin_amdgcn_alignbyte(v[it][2], v[it][1], shv[it]));
+	}
+	__syncthreads();
 	const float *hp = s_h + (size_t)(dk / RB) * HS;
 	float acc = 0.0f;
-	/* round c: chunk c's loads go out, chunk c - 1's dots run from LDS while
-	 * they are in flight (PIPE: rows of several chunks; one chunk has its
-	 * dots after its stores, and no second chunk's registers), then chunk c
-	 * goes to LDS; every load of a chunk is issued before any is stored (as
-	 * k_kq_down) */
-	for (int c0 = 0; c0 < nb + KC_CB; c0 += KC_CB) {
-		const int cb = min(KC_CB, nb - c0), run = cb * BY;
-		/* a native vector type: an array of the float4 struct stays in
-		 * scratch memory */
-		typedef float f4v __attribute__((ext_vector_type(4)));
-		u32 v[NIT][3], shv[NIT];
-		f4v hv[NH];
-		if (c0 < nb) {
-#pragma unroll
-			for (int it = 0; it < NIT; it++) {
-				const int e = tid + it * KD_THREADS;
-				const int d = e / (RUN / 8), o = 8 * (e % (RUN / 8));
-				shv[it] = 0;
-				if (e < KC_DOTS * (RUN / 8) && o < run) {
-					const int row = r0 + d % RB, p = d / RB;
-					const uint8_t *src = down + s_eo[p] + (size_t)row * rb +
-							     (size_t)c0 * BY + o;
-					const u32 sh = (u32)((uintptr_t)src & 3);
-					const u32 *a = (const u32 *)(src - sh);
-					v[it][0] = a[0];
-					v[it][1] = a[1];
-					v[it][2] = a[2];
-					shv[it] = sh;
-				}
-			}
-#pragma unroll
-			for (int u = 0; u < NH; u++) {
-				/* float4 i of the chunk's P x KC_CB * 64, clamped into
-				 * the chunk (the stores below skip the clamped ones) */
-				const int i = tid + u * KD_THREADS;
-				const int p = min(i / (KC_CB * 64), P - 1);
-				const int q = min(i % (KC_CB * 64), cb * 64 - 1);
-				hv[u] = ((const f4v *)(h + (size_t)p * EI + (size_t)c0 * 256))[q];
-			}
-		}
-		if (PIPE && c0 > 0) { /* the previous chunk, staged last round */
-			const int pcb = min(KC_CB, nb - (c0 - KC_CB));
-			for (int k = 0; k < pcb; k++) {
-				const uint8_t *blk = s_w + dk * RUN + k * BY;
-				if constexpr (WT == 3)
-					kd_q4k(blk, hp + k * 256, l, acc);
-				else
-					kd_q6k(blk, hp + k * 256, l, acc);
-			}
-		}
-		if (c0 >= nb)
-			break;
-		if (PIPE)
-			__syncthreads(); /* the previous chunk's readers are done */
-#pragma unroll
-		for (int u = 0; u < NH; u++) {
-			const int i = tid + u * KD_THREADS;
-			const int p = i / (KC_CB * 64), q = i % (KC_CB * 64);
-			if (p < P && q < cb * 64)
-				((f4v *)(s_h + (size_t)p * HS))[q] = hv[u];
-		}
-#pragma unroll
-		for (int it = 0; it < NIT; it++) {
-			const int e = tid + it * KD_THREADS;
-			const int d = e / (RUN / 8), o = 8 * (e % (RUN / 8));
-			if (e < KC_DOTS * (RUN / 8) && o < run)
-				*(uint2 *)(s_w + d * RUN + o) =
-					make_uint2(__builtin_amdgcn_alignbyte(v[it][1], v[it][0], shv[it]),
-						   __builtin_amdgcn_alignbyte(v[it][2], v[it][1], shv[it]));
-		}
-		__syncthreads();
-		if (!PIPE) { /* the one chunk */
-			for (int k = 0; k < cb; k++) {
-				const uint8_t *blk = s_w + dk * RUN + k * BY;
-				if constexpr (WT == 3)
-					kd_q4k(blk, hp + k * 256, l, acc);
-				else
-					kd_q6k(blk, hp + k * 256, l, acc);
-			}
-			break;
-		}
+	for (int k = 0; k < nb; k++) {
+		const uint8_t *blk = s_w + dk * RUN + k * BY;
+		if constexpr (WT == 3)
+			kd_q4k(blk, hp + k * 256, l, acc);
+		else
+			kd_q6k(blk, hp + k * 256, l, acc);
 	}
 	/* vector_reduce_sum's tree, as k_kq_down */
 	acc = acc + __shfl_xor(acc, 4, 8);
@@ -390,7 +369,7 @@ __global__ __launch_bounds__(KD_THREADS) void k_kq_down_combine(
 		float o = 0.0f;
 		for (int k = 0; k < K; k++) {
 			const int p = t * K + k;
-			const float inv = 1.0f / wts[p];
+			const float inv = 1.0f / s_wt[p];
 			o = o + s_y[r * P + p] / inv;
 		}
 		out[(size_t)t * E + r0 + r] = o;
@@ -439,19 +418,20 @@ extern "C" int moe_launch_kq_down(int dt, const uint8_t *down, size_t dn_stride,
 }
 
 /* the down + combine launch of a decode-sized call of P = T * K pairs: P a
- * divisor of KC_DOTS up to KC_MAXP, every output row of E in one workgroup's
- * block of KC_DOTS / P */
-extern "C" int moe_kq_down_combine_ok(size_t T, size_t K, size_t E)
+ * power of two up to KC_MAXP (it divides KC_DOTS), every output row of E in
+ * one workgroup's block of KC_DOTS / P rows, d_ff at most KC_CB super-blocks */
+extern "C" int moe_kq_down_combine_ok(size_t T, size_t K, size_t E, size_t EI)
 {
 	const size_t P = T * K;
-	return P >= 1 && P <= KC_MAXP && KC_DOTS % P == 0 && E % (KC_DOTS / P) == 0;
+	return P >= 1 && P <= KC_MAXP && (P & (P - 1)) == 0 && E % (KC_DOTS / P) == 0 &&
+	       EI % 256 == 0 && EI >= 256 && EI <= 256 * KC_CB;
 }
 
 extern "C" int moe_launch_kq_down_combine(int dt, const uint8_t *down, size_t dn_stride,
 					  const u32 *ids, const float *w, const float *h,
 					  float *out, int T, int K, int E, int EI, void *stream)
 {
-	if (!moe_kq_down_combine_ok((size_t)T, (size_t)K, (size_t)E) || EI % 256 ||
+	if (!moe_kq_down_combine_ok((size_t)T, (size_t)K, (size_t)E, (size_t)EI) ||
 	    (dt != 3 && dt != 5))
 		return (int)hipErrorInvalidValue;
 	const int P = T * K, RB = KC_DOTS / P;
@@ -459,20 +439,17 @@ extern "C" int moe_launch_kq_down_combine(int dt, const uint8_t *down, size_t dn
 			   (size_t)KC_DOTS * KC_CB * (dt == 3 ? 144 : 210);
 	const dim3 grid(E / RB);
 	hipStream_t s = (hipStream_t)stream;
-	const bool pipe = EI > 256 * KC_CB;
 	const int pm = P <= 1 ? 1 : P <= 2 ? 2 : P <= 4 ? 4 : 8;
 	const void *fn = NULL;
-#define KCPICK(D_, PI_, PM_)                                                  \
-	if (dt == D_ && pipe == PI_ && pm == PM_)                             \
-		fn = (const void *)k_kq_down_combine<D_, PI_, PM_>;
-	KCPICK(3, false, 1) KCPICK(3, false, 2) KCPICK(3, false, 4) KCPICK(3, false, 8)
-	KCPICK(3, true, 1) KCPICK(3, true, 2) KCPICK(3, true, 4) KCPICK(3, true, 8)
-	KCPICK(5, false, 1) KCPICK(5, false, 2) KCPICK(5, false, 4) KCPICK(5, false, 8)
-	KCPICK(5, true, 1) KCPICK(5, true, 2) KCPICK(5, true, 4) KCPICK(5, true, 8)
+#define KCPICK(D_, PM_)                                                       \
+	if (dt == D_ && pm == PM_)                                            \
+		fn = (const void *)k_kq_down_combine<D_, PM_>;
+	KCPICK(3, 1) KCPICK(3, 2) KCPICK(3, 4) KCPICK(3, 8)
+	KCPICK(5, 1) KCPICK(5, 2) KCPICK(5, 4) KCPICK(5, 8)
 #undef KCPICK
 	static_assert(KC_MAXP == 8, "instances cover pair bounds 1, 2, 4, 8");
 	void *args[] = {&down, &dn_stride, &ids, &w, &h, &out, &T, &K, &E, &EI};
-	hipError_t rc = hipLaunchKernel(fn, grid, dim3(KD_THREADS), args, lds, s);
+	hipError_t rc = hipLaunchKernel(fn, grid, dim3(KC_DOTS * 8), args, lds, s);
 	if (rc != hipSuccess)
 		return (int)rc;
 	return (int)hipGetLastError();

@@ -95,10 +95,12 @@ int moe_launch_kq_gateup(int gt, const uint8_t *gate, const uint8_t *up, size_t 
                          int EI, void *stream);
 int moe_launch_kq_down(int dt, const uint8_t *down, size_t dn_stride, const uint32_t *ids,
                        const float *h, float *y, int P, int E, int EI, void *stream);
-/* The decode-sized K-quant layer in two launches: routing and gate/up
+/* The decode-sized K-quant layer: routing and gate/up in one launch
  * (moe_decode.hip: one workgroup per CU, the decode kernel's sync words)
  * writing h [P][EI], ids and weights; then the down dots and the combine
- * into out (kq_moe.hip).  The same arithmetic as the kernels above. */
+ * into out in one launch where d_ff is at most 1024 (kq_moe.hip), else
+ * moe_launch_kq_down and moe_launch_combine.  The same arithmetic as the
+ * kernels above. */
 int moe_kq_decode_supported(int gt, size_t E, size_t EI, size_t NE, size_t T, size_t K);
 int moe_kq_decode_grid(int gt, size_t E, size_t NE);
 int moe_launch_kq_route_gateup(int gt, const float *x, const float *router, const float *bias,
@@ -106,7 +108,7 @@ int moe_launch_kq_route_gateup(int gt, const float *x, const float *router, cons
                                uint32_t *ids, float *w, float *h, uint32_t *sync, int T, int E,
                                int EI, int NE, int K, int renorm, int grid, int spin,
                                void *stream);
-int moe_kq_down_combine_ok(size_t T, size_t K, size_t E);
+int moe_kq_down_combine_ok(size_t T, size_t K, size_t E, size_t EI);
 int moe_launch_kq_down_combine(int dt, const uint8_t *down, size_t dn_stride,
                                const uint32_t *ids, const float *w, const float *h, float *out,
                                int T, int K, int E, int EI, void *stream);

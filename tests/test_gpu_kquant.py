@@ -172,13 +172,13 @@ def test_gpu_kq_layer_token_counts_vs_oracle(T):
 @pytest.mark.parametrize("name,Ts", [("olmoe_q4k_q6k", (1,)), ("olmoe_q6k", (1,)),
                                      ("mixtral_q4k_q6k", (1, 2, 4))])
 def test_gpu_kq_decode_path_vs_oracle(name, Ts):
-    """The decode-sized K-quant layer (two launches: routing and gate/up,
-    then down and combine without partials) for T * K <= 8 pairs: outputs
-    equal the oracle's moe_ffn (bit for bit the reference's, by the golden
-    tests above) and the five-launch path's, ids and weights the oracle's,
-    over successive calls (the routing epoch advances); the OLMoE shape's
-    d_ff is one staged chunk of the down rows, Mixtral's 14 (the pipelined
-    form); past 8 pairs the layer takes the per-pair products."""
+    """The decode-sized K-quant layer (routing and gate/up in one launch;
+    then, with d_ff up to 1024, down and combine in one launch without
+    partials, else the per-pair down and the combine): outputs equal the
+    oracle's moe_ffn (bit for bit the reference's, by the golden tests
+    above) and the five-launch path's, ids and weights the oracle's, over
+    successive calls (the routing epoch advances); past the routing slots
+    (T * K > 64) the layer takes the per-pair products."""
     (wt, E, EI, NE, K, renorm, _), lw, _, _ = _kq_layer(name)
     M = hipmoe.MoeLayer.from_synth(lw, K, bool(renorm))
     try:
@@ -198,8 +198,40 @@ def test_gpu_kq_decode_path_vs_oracle(name, Ts):
                 assert nbad == 0
                 assert np.array_equal(bits(out), bits(out_g))
         M.set_path(hipmoe.PATH_AUTO)
-        big = 8 // K + 1
+        big = 64 // K + 1
         assert M.path_for(big) == hipmoe.PATH_GEMV, (name, big)
+    finally:
+        M.free()
+
+
+KQ_DEC_SHAPES = {
+    # name: (types, E, EI, NE, K, renorm, token counts)
+    "mixtral_like_2048": (hipmoe.Q4_K | hipmoe.Q6_K << 8, 2048, 1024, 8, 2, 1, (1, 2, 4)),
+    "top1_1024_half_chunk": (hipmoe.Q6_K | hipmoe.Q4_K << 8, 1024, 512, 16, 1, 0, (1, 8)),
+    "e4096_ragged_chunk": (hipmoe.Q4_K, 4096, 768, 8, 2, 1, (1, 4)),
+}
+
+
+@pytest.mark.parametrize("name", sorted(KQ_DEC_SHAPES))
+def test_gpu_kq_decode_down_combine_shapes_vs_oracle(name):
+    """The one-launch down and combine at every pair bound it has an
+    instance for (P = 1, 2, 4, 8), with d_ff of 4, 3 and 2 super-blocks
+    (a staged chunk partly filled), renormalised (Mixtral) and plain
+    (OLMoE) slot weights, both type mixes; the first launch's units at
+    d_model 1024, 2048 and 4096 (64, 32, 16 rows a unit)."""
+    wt, E, EI, NE, K, renorm, Ts = KQ_DEC_SHAPES[name]
+    lw = hipmoe.synth_layer(SEED, 7, wt, E, EI, NE, 0.02, None)
+    M = hipmoe.MoeLayer.from_synth(lw, K, bool(renorm))
+    try:
+        for T in Ts:
+            assert M.path_for(T) == hipmoe.PATH_DECODE, (name, T)
+            x = hipmoe.synth_input(SEED, 0x9400 + T, T, E)
+            out, ids, w = M.ffn(x)
+            oout, oids, ow, _, _ = oracle.moe_ffn(x, lw, K, bool(renorm), None)
+            assert np.array_equal(ids, oids) and np.array_equal(bits(w), bits(ow))
+            nbad = int(np.sum(bits(out) != bits(oout)))
+            say(f"kq decode {name} T={T}: {nbad} of {out.size} outputs differ")
+            assert nbad == 0
     finally:
         M.free()
 
