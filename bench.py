@@ -503,12 +503,13 @@ def main():
     log(f"{steps} steps in {ms:.2f} ms: {ms_per_step * 1e3:.2f} us/step, "
         f"{tokens_per_s:.1f} tokens/s, {achieved_gbs:.1f} GB/s algorithmic")
 
-    # the path the library takes for this T: one launch of k_moe_decode, or
-    # router, top-k, sort and the grouped GEMMs, or router, top-k, GEMVs
+    # the path the library takes for this T: one launch of k_moe_decode (K-quant
+    # experts: routing + gate/up, then down + combine), or router, top-k, sort
+    # and the grouped GEMMs, or router, top-k, GEMVs
     path = layers[0].path_for(T)
-    # (layer_grouped / layer_gemv: the whole call, whose kernels the counter
-    # summaries add up)
-    kernel = {hipmoe.PATH_DECODE: "k_moe_decode",
+    kq = hipmoe.wtypes(w["wtype"])[0] in (hipmoe.Q4_K, hipmoe.Q6_K)
+    # (layer_*: the whole call, whose kernels the counter summaries add up)
+    kernel = {hipmoe.PATH_DECODE: "layer_decode" if kq else "k_moe_decode",
               hipmoe.PATH_GROUPED: "layer_grouped",
               hipmoe.PATH_GEMV: "layer_gemv"}[path]
 
