@@ -416,11 +416,17 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 			}
 		}
 	};
+	/* every load unconditional, its row clamped into [0, n - 1] (rows of the
+	 * cache: every launched chunk has j0 < AT, so n >= 1): rows past n and
+	 * the new row jn are loaded but never used (the sums below stop at n
+	 * and take row jn from LDS); one branch per load had cost a wave ~2 us
+	 * of issue */
 	auto load_v = [&]() {
+		const int nc = max(n, 1);
 #pragma unroll
 		for (int i = 0; i < CH / (LM_NT / HL); i++) {
-			const int j = half + i * (LM_NT / HL);
-			vr[i] = j < n && j != jn ? V[(size_t)j * HL + dv] : 0.0f;
+			const int j = min(half + i * (LM_NT / HL), nc - 1);
+			vr[i] = V[(size_t)j * HL + dv];
 		}
 	};
 	if constexpr (PF >= 1)
