@@ -31,12 +31,9 @@
  * with FMA (the tiled T>1 path of matmul.c:213-238 keeps the same
  * per-element order); then the tree ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7))
  * of vector_avx2.h:126-132 and logit = fl(bias + dot) (matmul.c:24-32).
- *   CH = 4: lane (token, expert, half h) runs accumulators 4h .. 4h+3,
- *           reading each step's operands as one 16-byte LDS read of w and
- *           of x; the halves meet through one lane shuffle.  Many tokens.
- *   CH = 1: lane (token, expert, l) runs accumulator l alone (8 lanes per
- *           logit, the shortest chain); the tree is three lane shuffles.
- *           Few tokens: more workgroups.
+ * Lane (token, expert, l) runs accumulator l alone (8 lanes per logit, the
+ * shortest chain); the tree is three lane shuffles.  For few tokens (one a
+ * workgroup: more workgroups); k_router_b below takes many.
  *
  * Router rows and tokens stream through an LDS ring of NST stages of
  * RT_KC = 256 columns (one 1 KB row piece per wave-wide LDS-DMA load,
@@ -51,8 +48,8 @@
 #define RT_RS (RT_KC * 4 + 32)
 
 
-template <int JT, int CH, int NW> struct rt_geo {
-	static constexpr int LPL = 8 / CH;                /* lanes per logit */
+template <int JT, int NW> struct rt_geo {
+	static constexpr int LPL = 8;                     /* lanes per logit */
 	static constexpr int TPW = WAVE / (LPL * JT);     /* tokens per wave */
 	static constexpr int TT = NW * TPW;               /* tokens per workgroup */
 	static constexpr int ROWS = JT + TT;              /* LDS rows per stage */
@@ -63,13 +60,13 @@ template <int JT, int CH, int NW> struct rt_geo {
 	static_assert(ROWS % NW == 0 && TPW >= 1 && NST >= 3, "router tile geometry");
 };
 
-template <int JT, int CH, int NW>
+template <int JT, int NW>
 __global__ __launch_bounds__(NW * WAVE) void k_router(const float *__restrict__ x,
 						      const float *__restrict__ wr,
 						      const float *__restrict__ bias,
 						      float *__restrict__ logits, int T, int E, int NE)
 {
-	typedef rt_geo<JT, CH, NW> RG;
+	typedef rt_geo<JT, NW> RG;
 	constexpr int NST = RG::NST;
 	__shared__ __attribute__((aligned(16))) uint8_t ring[NST * RG::SSZ + 1024];
 	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -112,10 +109,7 @@ __global__ __launch_bounds__(NW * WAVE) void k_router(const float *__restrict__ 
 				 st + (u32)((wave + NW * q) * RT_RS));
 	};
 
-	float acc[CH];
-#pragma unroll
-	for (int c = 0; c < CH; c++)
-		acc[c] = 0.0f;
+	float acc = 0.0f;
 #pragma unroll
 	for (int s = 0; s < NST - 1; s++)
 		if (s < ns)
@@ -129,47 +123,158 @@ __global__ __launch_bounds__(NW * WAVE) void k_router(const float *__restrict__ 
 		if (s + NST - 1 < ns)
 			issue(s + NST - 1);
 		const uint8_t *st = ring + (s % NST) * RG::SSZ;
-		const float *wrow = (const float *)(st + jl * RT_RS) + CH * sub;
-		const float *xrow = (const float *)(st + (JT + tl) * RT_RS) + CH * sub;
-		if (CH == 4) {
-#pragma unroll 8
-			for (int i = 0; i < RT_KC / 8; i++) {
-				const float4 wv = *(const float4 *)(wrow + 8 * i);
-				const float4 xv = *(const float4 *)(xrow + 8 * i);
-				acc[0] = __builtin_fmaf(xv.x, wv.x, acc[0]);
-				acc[1 % CH] = __builtin_fmaf(xv.y, wv.y, acc[1 % CH]);
-				acc[2 % CH] = __builtin_fmaf(xv.z, wv.z, acc[2 % CH]);
-				acc[3 % CH] = __builtin_fmaf(xv.w, wv.w, acc[3 % CH]);
-			}
-		} else {
-			/* one wave: all 64 operand reads of the stage go out before
-			 * the chain, one LDS latency per stage */
-			float xs[RT_KC / 8], ws[RT_KC / 8];
+		const float *wrow = (const float *)(st + jl * RT_RS) + sub;
+		const float *xrow = (const float *)(st + (JT + tl) * RT_RS) + sub;
+		/* all 64 operand reads of the stage go out before the chain, one
+		 * LDS latency per stage */
+		float xs[RT_KC / 8], ws[RT_KC / 8];
 #pragma unroll
-			for (int i = 0; i < RT_KC / 8; i++) {
-				xs[i] = xrow[8 * i];
-				ws[i] = wrow[8 * i];
-			}
-#pragma unroll
-			for (int i = 0; i < RT_KC / 8; i++)
-				acc[0] = __builtin_fmaf(xs[i], ws[i], acc[0]);
+		for (int i = 0; i < RT_KC / 8; i++) {
+			xs[i] = xrow[8 * i];
+			ws[i] = wrow[8 * i];
 		}
-	}
-	float d;
-	if (CH == 4) { /* accumulators 4..7 from the partner lane (sub = 1) */
-		float b[4];
 #pragma unroll
-		for (int c = 0; c < 4; c++)
-			b[c] = __shfl_xor(acc[c % CH], 1, WAVE);
-		d = ((acc[0] + b[0]) + (acc[2 % CH] + b[2])) + ((acc[1 % CH] + b[1]) + (acc[3 % CH] + b[3]));
-	} else { /* lane l holds a_l: (a_l + a_l+4), then pairs, then the two halves */
-		float v = acc[0];
-		v = v + __shfl_xor(v, 4, 8);
-		v = v + __shfl_xor(v, 2, 8);
-		d = v + __shfl_xor(v, 1, 8);
+		for (int i = 0; i < RT_KC / 8; i++)
+			acc = __builtin_fmaf(xs[i], ws[i], acc);
 	}
+	/* lane l holds a_l: (a_l + a_l+4), then pairs, then the two halves */
+	float v = acc;
+	v = v + __shfl_xor(v, 4, 8);
+	v = v + __shfl_xor(v, 2, 8);
+	const float d = v + __shfl_xor(v, 1, 8);
 	if (sub == 0 && t < T && j < NE)
 		logits[(size_t)t * NE + j] = (bias ? bias[j] : 0.0f) + d;
+}
+
+/*
+ * Many tokens: tiles of 16 experts x 8 tokens (RB_JT x RB_TT), 256 threads.
+ * Lane (chain l = lane % 8, expert pair ep = lane / 8) of wave w runs
+ * accumulator l of tokens 2w, 2w + 1 against experts 2ep, 2ep + 1: four
+ * logits' chain l, so each LDS dword a lane reads feeds two FMAs (a lane
+ * that ran four chains of one logit read two per FMA).  Chain l's values of
+ * a row piece are every eighth dword (l, l + 8, ...): read in pairs
+ * (ds_read2_b32).  Rows are padded to RB_RS bytes (260 dwords: row r starts
+ * in bank 4r mod 32), so the 64 w addresses of a wave's read hit 32
+ * distinct banks per half-wave and the x reads are broadcasts.  The chains
+ * and the tree are the ones k_router forms: the same logits, bit for bit.
+ * A 4-stage ring (3 in flight) starts computing sooner than a deeper one.
+ * Stage stamps put a stage at ~0.8 us with or without its loads: the LDS
+ * reads, at one wave per SIMD, bound it.
+ */
+#define RB_JT 16
+#define RB_TT 8
+#define RB_RS (RT_KC * 4 + 16)
+#define RB_NST 4
+
+__global__ __launch_bounds__(256) void k_router_b(const float *__restrict__ x,
+						  const float *__restrict__ wr,
+						  const float *__restrict__ bias,
+						  float *__restrict__ logits, int T, int E, int NE)
+{
+	constexpr int ROWS = RB_JT + RB_TT, NW = 4, PER = ROWS / NW, SSZ = ROWS * RB_RS;
+	static_assert(ROWS % NW == 0 && RB_RS % 16 == 0 && (RB_RS / 4) % 32 == 4, "router tile");
+	__shared__ __attribute__((aligned(16))) uint8_t ring[RB_NST * SSZ + 1024];
+	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+	const int l = lane & 7, ep = lane >> 3;
+	const int t0 = blockIdx.x * RB_TT, j0 = blockIdx.y * RB_JT;
+	const int ns = E / RT_KC;
+	const u32 l0 = (u32)(uintptr_t)(const __attribute__((address_space(3))) char *)ring;
+
+	/* this workgroup's slice of the expert block, into L2 (as k_router) */
+	{
+		const int nrow = min(RB_JT, NE - j0);
+		const int nlines = nrow * E / 32;
+		const int nsl = max(1, min(16, (int)gridDim.x / 8)), sl = (blockIdx.x / 8) % nsl;
+		const float *blk = wr + (size_t)j0 * E;
+		for (int q = wave; q * WAVE < nlines / nsl; q += NW) {
+			const int line = sl + nsl * min(q * WAVE + lane, nlines / nsl - 1);
+			dma_dwordx4(blk, (u32)line * 128u, l0 + (u32)(RB_NST * SSZ));
+		}
+	}
+
+	/* row loads of this wave: rows wave, wave + NW, ... of [w rows | x rows];
+	 * rows past NE or T repeat the last one (their results are not kept) */
+	u32 roff[PER];
+	bool isw[PER];
+#pragma unroll
+	for (int q = 0; q < PER; q++) {
+		const int r = wave + NW * q;
+		isw[q] = r < RB_JT;
+		const int src = isw[q] ? min(j0 + r, NE - 1) : min(t0 + r - RB_JT, T - 1);
+		roff[q] = (u32)((size_t)src * E * 4 + 16 * lane);
+	}
+	auto issue = [&](int s) {
+		const u32 st = l0 + (u32)((s % RB_NST) * SSZ);
+#pragma unroll
+		for (int q = 0; q < PER; q++)
+			dma_dwordx4((isw[q] ? wr : x) + (size_t)s * RT_KC, roff[q],
+				    st + (u32)((wave + NW * q) * RB_RS));
+	};
+
+	float acc[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}}; /* [token][expert] */
+#pragma unroll
+	for (int s = 0; s < RB_NST - 1; s++)
+		if (s < ns)
+			issue(s);
+	for (int s = 0; s < ns; s++) {
+		if (s + RB_NST - 2 < ns)
+			wait_vm<(RB_NST - 2) * PER>();
+		else
+			wait_vm<0>();
+		__syncthreads(); /* stage s landed for every wave; stage s-1 is free */
+		if (s + RB_NST - 1 < ns)
+			issue(s + RB_NST - 1);
+		const uint8_t *st = ring + (s % RB_NST) * SSZ;
+		const float *xr = (const float *)(st + (RB_JT + 2 * wave) * RB_RS) + l;
+		const float *wv = (const float *)(st + 2 * ep * RB_RS) + l;
+		/* the stage's 32 steps of the chain in batches of 4, double
+		 * buffered: batch b + 1's reads go out before batch b's FMAs (a
+		 * batch read then used at once left the LDS idle during the FMAs
+		 * and the VALU idle during the reads) */
+		float xa[2][4], wa[2][4], xb[2][4], wb[2][4];
+		auto rd = [&](int b, float (&xs)[2][4], float (&ws)[2][4])
+				  __attribute__((always_inline)) {
+#pragma unroll
+			for (int i = 0; i < 4; i++)
+#pragma unroll
+				for (int r = 0; r < 2; r++) {
+					xs[r][i] = xr[r * (RB_RS / 4) + 8 * (4 * b + i)];
+					ws[r][i] = wv[r * (RB_RS / 4) + 8 * (4 * b + i)];
+				}
+		};
+		auto fm = [&](const float (&xs)[2][4], const float (&ws)[2][4])
+				  __attribute__((always_inline)) {
+#pragma unroll
+			for (int i = 0; i < 4; i++)
+#pragma unroll
+				for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+					for (int ee = 0; ee < 2; ee++)
+						acc[tt][ee] = __builtin_fmaf(xs[tt][i], ws[ee][i], acc[tt][ee]);
+		};
+		rd(0, xa, wa);
+#pragma unroll
+		for (int b = 0; b < RT_KC / 32; b += 2) {
+			rd(b + 1, xb, wb);
+			fm(xa, wa);
+			if (b + 2 < RT_KC / 32)
+				rd(b + 2, xa, wa);
+			fm(xb, wb);
+		}
+	}
+	/* lane l holds a_l of each logit: (a_l + a_l+4), then pairs, then the halves */
+#pragma unroll
+	for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+		for (int ee = 0; ee < 2; ee++) {
+			float v = acc[tt][ee];
+			v = v + __shfl_xor(v, 4, 8);
+			v = v + __shfl_xor(v, 2, 8);
+			const float d = v + __shfl_xor(v, 1, 8);
+			const int t = t0 + 2 * wave + tt, j = j0 + 2 * ep + ee;
+			if (l == 0 && t < T && j < NE)
+				logits[(size_t)t * NE + j] = (bias ? bias[j] : 0.0f) + d;
+		}
 }
 
 /* ------------------------------------------------------------------ */
@@ -510,20 +615,21 @@ extern "C" int moe_launch_router(const float *x, const float *wr, const float *b
 	if (T < 1 || NE < 1 || E % RT_KC || (size_t)NE * E * 4 > 0xffffffffull ||
 	    (size_t)T * E * 4 > 0xffffffffull)
 		return (int)hipErrorInvalidValue;
-	/* 4 chains a lane, tiles of 16 experts x 8 tokens (a 6-stage ring); for
-	 * few tokens a chain a lane, tiles of 8 experts x 1 token (more
-	 * workgroups, but every token's workgroups load the router rows again).
-	 * Routing stage at NE = 64: one-token tiles 7.8 us up to T = 32, 11.5
-	 * at 64, 15.2 at 96, 39.6 at 320; 16x8 tiles 12.4-13.4 us from T = 128
-	 * to 512 (32x4 tiles with a 4-stage ring: 12.7-13.5). */
+	/* tiles of 16 experts x 8 tokens, a lane one chain of 2 x 2 logits
+	 * (k_router_b); for few tokens a chain a lane, tiles of 8 experts x 1
+	 * token (more workgroups, but every token's workgroups load the router
+	 * rows again).  Routing stage at NE = 64: one-token tiles 7.8 us up to
+	 * T = 32, 11.5 at 64, 15.2 at 96, 39.6 at 320; 16x8 tiles with 4 chains
+	 * of one logit a lane 12.4-13.4 us from T = 128 to 512; k_router_b at
+	 * T = 512 10.6 us against 11.6 for those. */
 	const int wide = ((T + 7) / 8) * ((NE + 15) / 16);
 	if (NE > 8 && wide >= 36) {
-		dim3 grid((T + 7) / 8, (NE + 15) / 16);
-		hipLaunchKernelGGL((k_router<16, 4, 4>), grid, dim3(256), 0, (hipStream_t)stream, x,
-				   wr, bias, logits, T, E, NE);
+		dim3 grid((T + RB_TT - 1) / RB_TT, (NE + RB_JT - 1) / RB_JT);
+		hipLaunchKernelGGL(k_router_b, grid, dim3(256), 0, (hipStream_t)stream, x, wr, bias,
+				   logits, T, E, NE);
 	} else {
 		dim3 grid(T, (NE + 7) / 8);
-		hipLaunchKernelGGL((k_router<8, 1, 1>), grid, dim3(64), 0, (hipStream_t)stream, x,
+		hipLaunchKernelGGL((k_router<8, 1>), grid, dim3(64), 0, (hipStream_t)stream, x,
 				   wr, bias, logits, T, E, NE);
 	}
 	return (int)hipGetLastError();
