@@ -147,6 +147,36 @@ def test_gpu_routing_edge_cases(case):
         assert (ids == 0).all()
 
 
+@pytest.mark.parametrize("NE,T", [(64, 77), (64, 133), (24, 150)])
+def test_gpu_router_many_token_tiles_ragged(NE, T):
+    """The many-token router tiles (16 experts x 8 tokens, from 36 tiles on)
+    at a token count that leaves the last token tile partial and an expert
+    count that leaves the last expert tile half empty: every logit equal,
+    bit for bit, to the oracle's router (matmul.c:91-105, vector_avx2.h:126-132,
+    pinned to the reference by the route goldens)."""
+    say(f"router tiles NE={NE} T={T}")
+    E = 2048
+    if NE == 64:
+        lay = gpu_layer("olmoe_q8")
+        K = CONFIGS["olmoe_q8"][4]
+    else:
+        K = 4
+        lay = hipmoe.MoeLayer.from_synth(
+            hipmoe.synth_layer(SEED, 3, hipmoe.Q8_0, E, 256, NE, 0.02, None), K, False)
+    assert ((T + 7) // 8) * ((NE + 15) // 16) >= 36  # the many-token tiles
+    x = hipmoe.synth_input(SEED, 40 + T, T, E)
+    bias = np.random.default_rng(T).standard_normal(NE).astype(np.float32)
+    try:
+        lg, pr, ids, w = lay.route(x, bias)
+        assert np.array_equal(bits(lg), bits(oracle.router(x, lay.router, bias)))
+        oids, ow = _oracle_route(x, lay.router, bias, K, False)
+        assert np.array_equal(ids, oids)
+        assert np.array_equal(bits(w), bits(ow))
+    finally:
+        if NE != 64:
+            lay.free()
+
+
 # --------------------------------------------------------------------------
 # one expert, one token (fused_ffn_silu)
 # --------------------------------------------------------------------------
