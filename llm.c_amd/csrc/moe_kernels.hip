@@ -158,8 +158,9 @@ __global__ __launch_bounds__(NW * WAVE) void k_router(const float *__restrict__ 
  * distinct banks per half-wave and the x reads are broadcasts.  The chains
  * and the tree are the ones k_router forms: the same logits, bit for bit.
  * A 4-stage ring (3 in flight) starts computing sooner than a deeper one.
- * Stage stamps put a stage at ~0.8 us with or without its loads: the LDS
- * reads, at one wave per SIMD, bound it.
+ * A stage takes ~0.8 us with or without its loads (timed by stamping a
+ * copy whose stages all compute from one loaded stage): the LDS reads, at
+ * one wave per SIMD, bound it.
  */
 #define RB_JT 16
 #define RB_TT 8
