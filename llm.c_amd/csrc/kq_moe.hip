@@ -245,6 +245,104 @@ __global__ __launch_bounds__(KD_THREADS) void k_kq_down(const uint8_t *__restric
 		y[(size_t)p * E + r0 + rk] = acc;
 }
 
+/*
+ * k_kq_down with its chunks streamed through an LDS ring (KD_NS stages,
+ * KD_NS - 1 chunks in flight) by LDS-DMA loads that the kernel counts
+ * itself, where every row's run starts 4-byte aligned (nb * BY % 4 == 0:
+ * Q4_K always, Q6_K for an even number of super-blocks a row).  k_kq_down
+ * holds one chunk in flight in registers (the compiler waits for all of a
+ * thread's loads before it stores any, so more chunks in registers do not
+ * overlap); at Mixtral's shape a workgroup (one per CU) then waited out
+ * most of a round trip per chunk.  A stage: the 32 rows' runs as 16-byte
+ * pieces (KD_NPR a row, row stride KD_NPR * 16 in LDS; the last piece
+ * reads up to 8 bytes past the run, inside the row's successor or the
+ * weights' slack) and the chunk's h.  The same dots in the same order.
+ */
+#define KD_NS 4
+
+template <int WT>
+__global__ __launch_bounds__(KD_THREADS) void k_kq_down_r(const uint8_t *__restrict__ down,
+							size_t dn_stride, const u32 *__restrict__ ids,
+							const float *__restrict__ h, float *__restrict__ y,
+							int E, int EI)
+{
+	constexpr int BY = kqb<WT>::BYTES;
+	constexpr int RUN = KD_CB * BY;                         /* bytes of a row's run */
+	constexpr int NPR = (RUN + 15) / 16;                    /* 16-byte pieces a row */
+	constexpr int RSL = NPR * 16;                           /* LDS row stride */
+	constexpr int NPC = KD_ROWS * NPR;                      /* pieces a chunk */
+	constexpr int JB = (NPC + KD_THREADS - 1) / KD_THREADS; /* weight loads a thread */
+	constexpr int SW = JB * KD_THREADS * 16;                /* weight bytes a stage */
+	constexpr int SSZ = SW + KD_CB * 256 * 4;               /* + the chunk's h */
+	constexpr int LOADS = JB + 1;                           /* loads a wave a stage */
+	static_assert(KD_CB * 64 == KD_THREADS, "one h piece a thread");
+	static_assert((KD_NS - 2) * LOADS < 64, "vmcnt");
+	__shared__ __attribute__((aligned(16))) uint8_t ring[KD_NS * SSZ];
+	const int p = blockIdx.y, nb = EI / 256, nch = (nb + KD_CB - 1) / KD_CB;
+	const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+	const int l = lane & 7, rk = wave * 8 + lane / 8; /* row of the block */
+	const int r0 = blockIdx.x * KD_ROWS;
+	const u32 rb = (u32)(nb * BY);
+	const uint8_t *base = down + (size_t)ids[p] * dn_stride;
+	const float *hp = h + (size_t)p * EI;
+	const u32 l0 = __builtin_amdgcn_readfirstlane(lds_addr(ring));
+	/* piece f = (wave * JB + j) * 64 + lane of a chunk: row f / NPR, piece
+	 * f % NPR; pieces past NPC read row r0's first piece (never used) */
+	u32 woff[JB], wpc[JB];
+#pragma unroll
+	for (int j = 0; j < JB; j++) {
+		const int f = (wave * JB + j) * WAVE + lane;
+		const int row = min(r0 + (f < NPC ? f / NPR : 0), E - 1);
+		woff[j] = (u32)row * rb;
+		wpc[j] = f < NPC ? 16u * (u32)(f % NPR) : 0u;
+	}
+	auto issue = [&](int s) {
+		const u32 st = l0 + (u32)((s % KD_NS) * SSZ);
+		/* a partial last chunk's pieces past its blocks re-read the run's
+		 * first piece (read past the run, they would leave the last row) */
+		const u32 lim = (u32)(min(KD_CB, nb - s * KD_CB) * BY);
+#pragma unroll
+		for (int j = 0; j < JB; j++)
+			dma_dwordx4(base, woff[j] + (u32)s * RUN + (wpc[j] < lim ? wpc[j] : 0u),
+				    st + (u32)((wave * JB + j) * WAVE * 16));
+		/* h piece tid of the chunk, clamped into the row's EI values
+		 * (a partial last chunk's pieces past the row are never used) */
+		const int cb = min(KD_CB, nb - s * KD_CB);
+		const int g = min(tid, cb * 64 - 1);
+		dma_dwordx4(hp, (u32)(s * KD_CB * 256 + 4 * g) * 4u, st + SW + (u32)(wave * WAVE * 16));
+	};
+#pragma unroll
+	for (int s = 0; s < KD_NS - 1; s++)
+		if (s < nch)
+			issue(s);
+	float acc = 0.0f;
+	for (int s = 0; s < nch; s++) {
+		if (s + KD_NS - 2 < nch)
+			wait_vm<(KD_NS - 2) * LOADS>();
+		else
+			wait_vm<0>();
+		__syncthreads(); /* chunk s landed for every wave; slot s - 1 is free */
+		if (s + KD_NS - 1 < nch)
+			issue(s + KD_NS - 1);
+		const uint8_t *st = ring + (s % KD_NS) * SSZ;
+		const float *sh = (const float *)(st + SW);
+		const int cb = min(KD_CB, nb - s * KD_CB);
+		for (int k = 0; k < cb; k++) {
+			const uint8_t *blk = st + rk * RSL + k * BY;
+			if constexpr (WT == 3)
+				kd_q4k(blk, sh + k * 256, l, acc);
+			else
+				kd_q6k(blk, sh + k * 256, l, acc);
+		}
+	}
+	/* vector_reduce_sum's tree, as k_kq_down */
+	acc = acc + __shfl_xor(acc, 4, 8);
+	acc = acc + __shfl_xor(acc, 2, 8);
+	acc = acc + __shfl_xor(acc, 1, 8);
+	if (l == 0 && r0 + rk < E)
+		y[(size_t)p * E + r0 + rk] = acc;
+}
+
 /* ------------------------------------------------------------------ */
 /* down and combine of a decode-sized call                              */
 /* ------------------------------------------------------------------ */
@@ -408,7 +506,19 @@ extern "C" int moe_launch_kq_down(int dt, const uint8_t *down, size_t dn_stride,
 {
 	const dim3 grid((E + KD_ROWS - 1) / KD_ROWS, P);
 	hipStream_t s = (hipStream_t)stream;
-	if (dt == 3)
+	const int nb = EI / 256;
+	/* the LDS ring where every row's run is 4-byte aligned and the
+	 * offsets of one expert's rows fit 32 bits */
+	const int bytes = dt == 3 ? 144 : 210;
+	const bool ring = (nb * bytes) % 4 == 0 && dn_stride % 4 == 0 && ((uintptr_t)down & 3) == 0 &&
+			  dn_stride + 4096 < 0xffffffffull;
+	if (dt == 3 && ring)
+		hipLaunchKernelGGL(k_kq_down_r<3>, grid, dim3(KD_THREADS), 0, s, down, dn_stride, ids,
+				   h, y, E, EI);
+	else if (ring)
+		hipLaunchKernelGGL(k_kq_down_r<5>, grid, dim3(KD_THREADS), 0, s, down, dn_stride, ids,
+				   h, y, E, EI);
+	else if (dt == 3)
 		hipLaunchKernelGGL(k_kq_down<3>, grid, dim3(KD_THREADS), 0, s, down, dn_stride, ids, h,
 				   y, E, EI);
 	else
