@@ -70,6 +70,27 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
  */
 #define SORT_MAX_TILES 8704 /* Tmax for T*K up to 2^19 pairs and NE <= 256 */
 
+/* ids a sort thread takes per round: one 16-byte load (with 16 a thread,
+ * the 256 threads that had ids did all the counting and placing: 6.9 us a
+ * sort at OLMoE T = 512, 2.8 of them counting) */
+#define SORT_IPT 4
+
+/* ids p0 .. p0 + SORT_IPT - 1 (~0 past P) */
+__device__ static inline void sort_ids(const u32 *ids, int p0, int P, u32 (&v)[SORT_IPT])
+{
+	if (p0 + SORT_IPT <= P && ((uintptr_t)(ids + p0) & 15) == 0) {
+		const uint4 q = *(const uint4 *)(ids + p0);
+		v[0] = q.x;
+		v[1] = q.y;
+		v[2] = q.z;
+		v[3] = q.w;
+	} else {
+#pragma unroll
+		for (int k = 0; k < SORT_IPT; k++)
+			v[k] = p0 + k < P ? ids[p0 + k] : 0xffffffffu;
+	}
+}
+
 template <int MT>
 __global__ __launch_bounds__(SORT_THREADS) void k_moe_sort(const u32 *__restrict__ ids, int P,
 							   int NE, int Tmax,
@@ -85,17 +106,15 @@ __global__ __launch_bounds__(SORT_THREADS) void k_moe_sort(const u32 *__restrict
 		fill[i] = 0;
 	}
 	__syncthreads();
-	/* counts: 16 ids per thread and round, loaded together; the first
-	 * round's ids stay in registers for the placement below */
-	u32 v0[16];
-	for (int p0 = 16 * tid; p0 < P; p0 += 16 * SORT_THREADS) {
-		u32 v[16];
+	/* counts: SORT_IPT ids per thread and round, loaded together; the
+	 * first round's ids stay in registers for the placement below */
+	u32 v0[SORT_IPT];
+	for (int p0 = SORT_IPT * tid; p0 < P; p0 += SORT_IPT * SORT_THREADS) {
+		u32 v[SORT_IPT];
+		sort_ids(ids, p0, P, v);
 #pragma unroll
-		for (int k = 0; k < 16; k++)
-			v[k] = p0 + k < P ? ids[p0 + k] : 0xffffffffu;
-#pragma unroll
-		for (int k = 0; k < 16; k++) {
-			if (p0 == 16 * tid)
+		for (int k = 0; k < SORT_IPT; k++) {
+			if (p0 == SORT_IPT * tid)
 				v0[k] = v[k];
 			if (v[k] < (u32)NE) /* always, for ids from the top-k kernel */
 				atomicAdd(&cnt[v[k]], 1);
@@ -158,13 +177,17 @@ __global__ __launch_bounds__(SORT_THREADS) void k_moe_sort(const u32 *__restrict
 			rows[i] = -1;
 	}
 	/* every pair's row */
-	for (int p0 = 16 * tid; p0 < P; p0 += 16 * SORT_THREADS) {
-		u32 v[16];
+	for (int p0 = SORT_IPT * tid; p0 < P; p0 += SORT_IPT * SORT_THREADS) {
+		u32 v[SORT_IPT];
+		if (p0 == SORT_IPT * tid) {
 #pragma unroll
-		for (int k = 0; k < 16; k++)
-			v[k] = p0 == 16 * tid ? v0[k] : p0 + k < P ? ids[p0 + k] : 0xffffffffu;
+			for (int k = 0; k < SORT_IPT; k++)
+				v[k] = v0[k];
+		} else {
+			sort_ids(ids, p0, P, v);
+		}
 #pragma unroll
-		for (int k = 0; k < 16; k++)
+		for (int k = 0; k < SORT_IPT; k++)
 			if (v[k] < (u32)NE)
 				rows[toff[v[k]] * MT + atomicAdd(&fill[v[k]], 1)] = p0 + k;
 	}
@@ -664,15 +687,13 @@ __global__ __launch_bounds__(SORT_THREADS) void k_moe_sort_v(const u32 *__restri
 		fill[i] = 0;
 	}
 	__syncthreads();
-	u32 v0[16];
-	for (int p0 = 16 * tid; p0 < P; p0 += 16 * SORT_THREADS) {
-		u32 v[16];
+	u32 v0[SORT_IPT];
+	for (int p0 = SORT_IPT * tid; p0 < P; p0 += SORT_IPT * SORT_THREADS) {
+		u32 v[SORT_IPT];
+		sort_ids(ids, p0, P, v);
 #pragma unroll
-		for (int k = 0; k < 16; k++)
-			v[k] = p0 + k < P ? ids[p0 + k] : 0xffffffffu;
-#pragma unroll
-		for (int k = 0; k < 16; k++) {
-			if (p0 == 16 * tid)
+		for (int k = 0; k < SORT_IPT; k++) {
+			if (p0 == SORT_IPT * tid)
 				v0[k] = v[k];
 			if (v[k] < (u32)NE)
 				atomicAdd(&cnt[v[k]], 1);
@@ -773,13 +794,17 @@ __global__ __launch_bounds__(SORT_THREADS) void k_moe_sort_v(const u32 *__restri
 	for (int i = tid; i < R; i += SORT_THREADS)
 		rows[i] = -1;
 	__syncthreads();
-	for (int p0 = 16 * tid; p0 < P; p0 += 16 * SORT_THREADS) {
-		u32 v[16];
+	for (int p0 = SORT_IPT * tid; p0 < P; p0 += SORT_IPT * SORT_THREADS) {
+		u32 v[SORT_IPT];
+		if (p0 == SORT_IPT * tid) {
 #pragma unroll
-		for (int k = 0; k < 16; k++)
-			v[k] = p0 == 16 * tid ? v0[k] : p0 + k < P ? ids[p0 + k] : 0xffffffffu;
+			for (int k = 0; k < SORT_IPT; k++)
+				v[k] = v0[k];
+		} else {
+			sort_ids(ids, p0, P, v);
+		}
 #pragma unroll
-		for (int k = 0; k < 16; k++)
+		for (int k = 0; k < SORT_IPT; k++)
 			if (v[k] < (u32)NE)
 				rows[rb[v[k]] + atomicAdd(&fill[v[k]], 1)] = p0 + k;
 	}
