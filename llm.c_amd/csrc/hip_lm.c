@@ -695,12 +695,25 @@ static int enqueue_step(hip_lm *M, int head, int nact)
 				    M->d_vc + co, M->d_part, cnt_attn, M->d_attn, (int)M->H,
 				    (int)M->KH, (int)M->C, (int)M->window, M->scale,
 				    M->arch != HIP_LM_OLMOE, (int)l, nact, 1, 0, s), "attention");
-		/* h1 = h0 + attn . Wo^T, moe_in = rms_norm(h1) */
+		/* h1 = h0 + attn . Wo^T, moe_in = rms_norm(h1): where one token
+		 * takes the MoE decode kernel, its workgroups each normalise h1
+		 * (no gather of h1's rows behind the output product) */
+		float *moe_in = M->d_moe_in + l * M->E;
+		uint32_t *ids = M->d_ids + l * M->K;
+		float *wts = M->d_w + l * M->K;
+		if (moe_norm_decode_ok(y->moe)) {
+			LCHK(lm_launch_oproj(wt, y->wo, E, (int)M->EQ, M->d_attn, M->d_h0, M->d_h1,
+					     NULL, NULL, NULL, M->d_st, (int)l, M->grid_o, s),
+			     "output product");
+			if (!moe_ffn_dev_norm(y->moe, M->d_h1, y->ffn_norm, moe_in, M->d_moe_out,
+					      ids, wts, s))
+				return 0;
+			continue;
+		}
 		LCHK(lm_launch_oproj(wt, y->wo, E, (int)M->EQ, M->d_attn, M->d_h0, M->d_h1,
-				     M->d_rows_t, y->ffn_norm, M->d_moe_in + l * M->E,
-				     M->d_st, (int)l, M->grid_o, s), "output product + norm");
-		if (!hip_moe_ffn_dev(y->moe, M->d_moe_in + l * M->E, M->d_moe_out, 1, NULL,
-				     M->d_ids + l * M->K, M->d_w + l * M->K, s))
+				     M->d_rows_t, y->ffn_norm, moe_in, M->d_st, (int)l, M->grid_o, s),
+		     "output product + norm");
+		if (!hip_moe_ffn_dev(y->moe, moe_in, M->d_moe_out, 1, NULL, ids, wts, s))
 			return 0;
 	}
 	if (head) /* logits = rms_norm(h1 + moe_out) . lm_head^T, pick, advance */

@@ -613,7 +613,7 @@ int hip_moe_ffn_dev_noalloc(hip_moe_layer *L, const float *d_x, float *d_out, si
 			      L->d_down, L->gu_stride, L->down_stride, ids, w,
 			      (uint64_t *)(base + part_off), d_out, (uint32_t *)base, (int)T,
 			      (int)L->E, (int)L->EI, (int)L->NE, (int)L->topk, L->renorm,
-			      L->fused_grid, L->spin, pick_stream(L, stream)),
+			      L->fused_grid, L->spin, NULL, NULL, pick_stream(L, stream)),
 	     "fused layer (static scratch)");
 	return 1;
 }
@@ -715,6 +715,34 @@ int hip_moe_path_for(const hip_moe_layer *L, size_t T)
 	return choose_path(L, T);
 }
 
+int moe_norm_decode_ok(const hip_moe_layer *L)
+{
+	return L && !L->kq && choose_path(L, 1) == HIP_MOE_PATH_DECODE;
+}
+
+int moe_ffn_dev_norm(hip_moe_layer *L, const float *d_h, const float *d_norm_w, float *d_x_out,
+		     float *d_out, uint32_t *d_ids_out, float *d_w_out, void *stream)
+{
+	if (!L || !d_h || !d_norm_w || !d_x_out || !d_out) {
+		set_err("ffn_norm: NULL argument");
+		return 0;
+	}
+	if (!moe_norm_decode_ok(L)) {
+		set_err("ffn_norm: one token does not take the decode kernel on this layer");
+		return 0;
+	}
+	hipStream_t s = pick_stream(L, stream);
+	if (!ensure_scratch(L, 1, s))
+		return 0;
+	LCHK(moe_launch_fused(L->wtype, d_h, L->d_router, NULL, L->d_gate, L->d_up, L->d_down,
+			      L->gu_stride, L->down_stride, d_ids_out ? d_ids_out : L->d_ids,
+			      d_w_out ? d_w_out : L->d_w, L->d_part, d_out, L->d_sync, 1,
+			      (int)L->E, (int)L->EI, (int)L->NE, (int)L->topk, L->renorm,
+			      L->fused_grid, L->spin, d_norm_w, d_x_out, s),
+	     "fused layer (normalising its input)");
+	return 1;
+}
+
 int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 		    const float *d_router_bias, uint32_t *d_ids_out, float *d_w_out,
 		    void *stream)
@@ -760,7 +788,8 @@ int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 				      L->d_up, L->d_down, L->gu_stride, L->down_stride,
 				      ids, w, L->d_part, d_out, L->d_sync,
 				      (int)T, (int)L->E, (int)L->EI, (int)L->NE, (int)L->topk,
-				      L->renorm, L->fused_grid, L->spin, s), "fused layer");
+				      L->renorm, L->fused_grid, L->spin, NULL, NULL, s),
+		     "fused layer");
 		return 1;
 	}
 	if (!route(L, d_x, T, d_router_bias, L->d_logits, NULL, ids, w,

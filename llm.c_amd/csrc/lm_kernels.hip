@@ -658,7 +658,8 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 /*
  * out[E] = add + x . Wo^T (the residual stream after attention), each row
  * also stored tagged in rows_t; workgroup 0 reads them all back and writes
- * x_out = rms_norm(out) * w (the MoE layer's input).
+ * x_out = rms_norm(out) * w (the MoE layer's input).  x_out NULL: the
+ * product alone (the MoE launch normalises out itself).
  */
 template <int WT, int C>
 __global__ __launch_bounds__(LM_NT) __attribute__((amdgpu_waves_per_eu(4)))
@@ -669,6 +670,10 @@ void k_lm_oproj(const uint8_t *__restrict__ W, size_t rb, int N, int K,
 {
 	extern __shared__ __attribute__((aligned(16))) float sx[];
 	__shared__ float red[LM_NT / WAVE];
+	if (!x_out) {
+		qgemv_body<WT, C, true>(sx, W, rb, N, K, x, 1, 1, add, 0, out, QgNoHook{});
+		return;
+	}
 	const u32 tag = lm_tag(st, layer);
 	auto hook = [=](int row, float r) { st_dev_u64(&rows_t[row], tagged(tag, r)); };
 	qgemv_body<WT, C, true>(sx, W, rb, N, K, x, 1, 1, add, 0, out, hook);

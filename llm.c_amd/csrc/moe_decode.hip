@@ -108,6 +108,11 @@ struct DecodeArgs {
 	int off_start, off_rep;
 	int rep_stride; /* u64 entries between replicas (a multiple of 512: 4 KB) */
 	int spin;       /* poll rounds after which a wait gives up (MOE_SPIN_DEFAULT) */
+	/* k_moe_decode<..., NORM = true> (one token): x is the residual h, the
+	 * layer's input rms_norm(h) * norm_w, which router workgroup 0 also
+	 * writes to x_out */
+	const float *norm_w;
+	float *x_out;
 };
 
 /* balanced split of n items over G workgroups: b gets [item_lo(b), item_lo(b+1));
@@ -499,12 +504,74 @@ __device__ static inline float router_chain(const float *xrow, const float *wrow
 	return acc;
 }
 
+/*
+ * One token's rms_norm(h) * w in every workgroup of a NORM launch.  The rms
+ * is taken as the one-token model kernels take it (256 threads: thread v
+ * adds h[v]^2, h[v + 256]^2, ... in order; xor trees in waves of 64; the
+ * four waves' sums in order; sqrtf(sum / E + 1e-5f)), so every workgroup
+ * and the model's own norms get the same bits; then x = (h / rms) * w
+ * (olmoe.c:486-488, rmsnorm nn.c:8-31).  hv: this thread's float4s i = tid
+ * + NT v (< E / 4) of the token, normalised.  The whole workgroup calls it.
+ */
+template <int NT, int NV>
+__device__ static void norm_token(const float *h, const float *w, int E, float4 (&hv)[NV])
+{
+	constexpr int MS = NV * NT / 64; /* terms of a summing thread, E / 256 at most */
+	__shared__ float s_red[4];
+	const float4 *h4 = (const float4 *)h, *w4 = (const float4 *)w;
+	const int tid = threadIdx.x, lane = tid % WAVE;
+	float4 wv[NV];
+	float sv[MS];
+#pragma unroll
+	for (int v = 0; v < NV; v++) {
+		const int i = tid + NT * v;
+		if (i < E / 4) {
+			hv[v] = h4[i];
+			wv[v] = w4[i];
+		}
+	}
+	float ss = 0.0f;
+	if (tid < 256) {
+#pragma unroll
+		for (int m = 0; m < MS; m++)
+			sv[m] = 256 * m + tid < E ? h[256 * m + tid] : 0.0f;
+#pragma unroll
+		for (int m = 0; m < MS; m++)
+			if (256 * m + tid < E) {
+				const float t = sv[m] * sv[m];
+				ss = ss + t;
+			}
+		for (int o = WAVE / 2; o > 0; o >>= 1)
+			ss += __shfl_xor(ss, o, WAVE);
+		if (lane == 0)
+			s_red[tid / WAVE] = ss;
+	}
+	__syncthreads();
+	float sum = 0.0f;
+#pragma unroll
+	for (int k = 0; k < 4; k++)
+		sum += s_red[k];
+	const float rms = sqrtf(sum / (float)E + 1e-5f);
+#pragma unroll
+	for (int v = 0; v < NV; v++)
+		if (tid + NT * v < E / 4) {
+			float r = hv[v].x / rms;
+			hv[v].x = r * wv[v].x;
+			r = hv[v].y / rms;
+			hv[v].y = r * wv[v].y;
+			r = hv[v].z / rms;
+			hv[v].z = r * wv[v].z;
+			r = hv[v].w / rms;
+			hv[v].w = r * wv[v].w;
+		}
+}
+
 /* router row j for every token, published into every replica by wave 0;
  * prev_epoch (the launch's epoch minus one, valid in thread 0) is consumed
  * only after the chain, so its load is in flight meanwhile.  dig (one
  * token): the other waves stage the token's digit blocks there while wave
  * 0 runs the chain. */
-template <int NT, int E>
+template <int NT, int E, bool NORM = false>
 __device__ static void router_row(const DecodeArgs &a, int j, u32 prev_epoch, float *lds,
 				  u32 *dig)
 {
@@ -529,8 +596,7 @@ __device__ static void router_row(const DecodeArgs &a, int j, u32 prev_epoch, fl
 		constexpr int M = E / 64;
 		const float4 *w4 = (const float4 *)(a.router + (size_t)j * E);
 		const float4 *x4 = (const float4 *)a.x;
-		for (int i = threadIdx.x; i < E / 4; i += NT) {
-			const float4 wv = w4[i], xv = x4[i];
+		auto put = [&](int i, float4 wv, float4 xv) {
 			const int k = 4 * i;
 			sw[((k + 0) & 7) * RS + ((k + 0) >> 3)] = wv.x;
 			sw[((k + 1) & 7) * RS + ((k + 1) >> 3)] = wv.y;
@@ -540,6 +606,29 @@ __device__ static void router_row(const DecodeArgs &a, int j, u32 prev_epoch, fl
 			sx[((k + 1) & 7) * RS + ((k + 1) >> 3)] = xv.y;
 			sx[((k + 2) & 7) * RS + ((k + 2) >> 3)] = xv.z;
 			sx[((k + 3) & 7) * RS + ((k + 3) >> 3)] = xv.w;
+		};
+		if constexpr (NORM) {
+			/* the row's loads go out with the residual's and the norm
+			 * weights'; x = rms_norm(h) * w lands in LDS (and x_out) */
+			constexpr int NV = (E / 4 + NT - 1) / NT;
+			float4 rv[NV], hv[NV];
+#pragma unroll
+			for (int v = 0; v < NV; v++)
+				if ((int)threadIdx.x + NT * v < E / 4)
+					rv[v] = w4[threadIdx.x + NT * v];
+			norm_token<NT, NV>(a.x, a.norm_w, E, hv);
+#pragma unroll
+			for (int v = 0; v < NV; v++) {
+				const int i = threadIdx.x + NT * v;
+				if (i < E / 4) {
+					put(i, rv[v], hv[v]);
+					if (j == 0)
+						((float4 *)a.x_out)[i] = hv[v];
+				}
+			}
+		} else {
+			for (int i = threadIdx.x; i < E / 4; i += NT)
+				put(i, w4[i], x4[i]);
 		}
 		__syncthreads();
 		if (wave == 0) {
@@ -773,7 +862,7 @@ __device__ static inline void load_down(const DecodeArgs &a, int q, const u32 *s
  * WT: 1 = Q8_0, 2 = Q4_0.  CG: lanes per gate/up row (E / segment columns).
  * NT: threads (one workgroup per CU).  RPT = E / NT: down rows per thread.
  */
-template <int WT, int CG, int NT, int RPT>
+template <int WT, int CG, int NT, int RPT, bool NORM>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT / 256, NT / 256)))
 void k_moe_decode(DecodeArgs a)
 {
@@ -815,11 +904,24 @@ void k_moe_decode(DecodeArgs a)
 	 * copy (no second round trip) */
 	const bool st0 = b < a.NE && x0 < x1 && a.T == 1;
 	if (b < a.NE)
-		router_row<NT, CG * S::COLS>(a, b, prev_epoch, rl, st0 ? sx : nullptr);
+		router_row<NT, CG * S::COLS, NORM>(a, b, prev_epoch, rl, st0 ? sx : nullptr);
 	/* the tokens of this workgroup's items (they do not depend on routing) */
-	if (x0 < x1 && !st0)
-		for (int t = t0; t <= (x1 - 1) / 2 / IPT; t++)
-			stage_digits<NT>(sx + (t - t0) * XS, a.x + (size_t)t * a.E, a.E);
+	if (x0 < x1 && !st0) {
+		if constexpr (NORM) { /* one token, normalised here */
+			constexpr int NV = (RPT + 3) / 4;
+			float4 hv[NV];
+			norm_token<NT, NV>(a.x, a.norm_w, a.E, hv);
+#pragma unroll
+			for (int v = 0; v < NV; v++) {
+				const int i = threadIdx.x + NT * v;
+				if (i < a.E / 4)
+					stage_digits4(sx + (i / 8) * DBLK, hv[v], i & 7);
+			}
+		} else {
+			for (int t = t0; t <= (x1 - 1) / 2 / IPT; t++)
+				stage_digits<NT>(sx + (t - t0) * XS, a.x + (size_t)t * a.E, a.E);
+		}
+	}
 	if (threadIdx.x == 0) {
 		s_epoch = prev_epoch + 1;
 		s_poison = err0;
@@ -1090,7 +1192,7 @@ void k_moe_decode(DecodeArgs a)
 
 struct Geo {
 	int NT, CG, RPT, cols;
-	const void *fn;
+	const void *fn, *fn_norm; /* x ready / x = rms_norm(h) * w in the launch */
 };
 
 /* 512 threads (two waves per SIMD: 256 VGPRs for an item's weights and
@@ -1099,7 +1201,7 @@ struct Geo {
 static Geo geometry(int wtype, size_t E, size_t EI)
 {
 	Geo g;
-	g.fn = NULL;
+	g.fn = g.fn_norm = NULL;
 	g.cols = wtype == 1 ? 32 : 64;
 	g.NT = 512;
 	g.CG = (int)(E / (size_t)g.cols);
@@ -1107,8 +1209,10 @@ static Geo geometry(int wtype, size_t E, size_t EI)
 	if (E % (size_t)g.cols || E % (size_t)g.NT || EI % DEC_CHUNK || EI == 0)
 		return g;
 #define PICK(W_, CG_, NT_, RPT_)                                                    \
-	if (wtype == W_ && g.CG == CG_ && g.NT == NT_ && g.RPT == RPT_)              \
-		g.fn = (const void *)k_moe_decode<W_, CG_, NT_, RPT_>;
+	if (wtype == W_ && g.CG == CG_ && g.NT == NT_ && g.RPT == RPT_) {            \
+		g.fn = (const void *)k_moe_decode<W_, CG_, NT_, RPT_, false>;         \
+		g.fn_norm = (const void *)k_moe_decode<W_, CG_, NT_, RPT_, true>;     \
+	}
 	PICK(1, 32, 512, 2)
 	PICK(1, 64, 512, 4)
 	PICK(2, 32, 512, 4)
@@ -1182,9 +1286,13 @@ extern "C" int moe_fused_grid(int wtype, size_t E, size_t EI, size_t NE)
 	if (hipGetDevice(&dev) != hipSuccess ||
 	    hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
 		return 0;
+	int per_n = 0;
 	if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, g.fn, g.NT,
 							 decode_lds_bytes(g, E)) != hipSuccess ||
-	    per < 1)
+	    per < 1 ||
+	    hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_n, g.fn_norm, g.NT,
+							 decode_lds_bytes(g, E)) != hipSuccess ||
+	    per_n < 1)
 		return 0;
 	/* one workgroup per CU; the router rows need one workgroup each, a
 	 * workgroup's items must span at most DEC_TOKS tokens (T <= grid), and
@@ -1199,10 +1307,10 @@ extern "C" int moe_launch_fused(int wtype, const float *x, const float *router,
 				const uint8_t *down, size_t gu_stride, size_t dn_stride,
 				uint32_t *ids, float *w, uint64_t *part, float *out, uint32_t *sync,
 				int T, int E, int EI, int NE, int K, int renorm, int grid,
-				int spin, void *stream)
+				int spin, const float *norm_w, float *x_out, void *stream)
 {
 	Geo g = geometry(wtype, (size_t)E, (size_t)EI);
-	if (!g.fn || grid < NE || grid < T)
+	if (!g.fn || grid < NE || grid < T || (norm_w && (T != 1 || !x_out)))
 		return (int)hipErrorInvalidValue;
 	SyncLayout sl = sync_layout((size_t)T, (size_t)NE, grid);
 	DecodeArgs a;
@@ -1231,8 +1339,10 @@ extern "C" int moe_launch_fused(int wtype, const float *x, const float *router,
 	a.off_rep = (int)sl.off_rep;
 	a.rep_stride = (int)sl.rep_stride;
 	a.spin = spin > 0 ? spin : MOE_SPIN_DEFAULT;
+	a.norm_w = norm_w;
+	a.x_out = x_out;
 	void *args[] = {&a};
-	hipError_t rc = hipLaunchKernel(g.fn, dim3(grid), dim3(g.NT), args,
+	hipError_t rc = hipLaunchKernel(norm_w ? g.fn_norm : g.fn, dim3(grid), dim3(g.NT), args,
 					decode_lds_bytes(g, (size_t)E), (hipStream_t)stream);
 	if (rc != hipSuccess)
 		return (int)rc;

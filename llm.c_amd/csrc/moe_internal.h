@@ -154,7 +154,19 @@ int moe_launch_fused(int wtype, const float *x, const float *router, const float
                      const uint8_t *gate, const uint8_t *up, const uint8_t *down,
                      size_t gu_stride, size_t dn_stride, uint32_t *ids, float *w,
                      uint64_t *part, float *out, uint32_t *sync, int T, int E, int EI, int NE,
-                     int K, int renorm, int grid, int spin, void *stream);
+                     int K, int renorm, int grid, int spin, const float *norm_w, float *x_out,
+                     void *stream);
+
+/* One token through the decode kernel with the layer's input normalised in
+ * the launch: x = rms_norm(d_h) * d_norm_w (the one-token model kernels'
+ * arithmetic; also written to d_x_out), then the layer on x, as
+ * hip_moe_ffn_dev(L, x, d_out, 1, NULL, ids, w).  moe_norm_decode_ok: whether
+ * one token takes that kernel on L (Q8_0/Q4_0 experts, decode path). */
+struct hip_moe_layer;
+int moe_norm_decode_ok(const struct hip_moe_layer *L);
+int moe_ffn_dev_norm(struct hip_moe_layer *L, const float *d_h, const float *d_norm_w,
+                     float *d_x_out, float *d_out, uint32_t *d_ids_out, float *d_w_out,
+                     void *stream);
 
 /* How many times the layer's scratch was (re)allocated: a HIP graph that
  * was captured at another count names freed buffers and must be dropped. */
