@@ -651,14 +651,23 @@ static int enqueue_step_generic(hip_lm *M, int head, int nact)
 				    M->d_vc + co, M->d_part, M->d_cnt, M->d_attn, (int)M->H,
 				    (int)M->KH, (int)M->C, (int)M->window, M->scale,
 				    M->arch != HIP_LM_OLMOE, (int)l, nact, 1, 0, s), "attention");
-		/* h1 = h0 + attn . Wo^T, moe_in = rms_norm(h1) */
+		/* h1 = h0 + attn . Wo^T, moe_in = rms_norm(h1): the MoE layer's
+		 * decode launch normalises h1 itself where one token takes it */
 		if (!vec_product(y->to, y->wo, E, EQ, M->d_attn, M->d_h0, M->d_h1, y->go, s))
 			return 0;
-		LCHK(lm_launch_norm_rows(1, 1, E, M->d_h1, NULL, y->ffn_norm, NULL,
-					 M->d_moe_in + l * M->E, NULL, M->d_st, NULL, NULL, s),
+		float *moe_in = M->d_moe_in + l * M->E;
+		uint32_t *ids = M->d_ids + l * M->K;
+		float *wts = M->d_w + l * M->K;
+		if (moe_norm_decode_ok(y->moe)) {
+			if (!moe_ffn_dev_norm(y->moe, M->d_h1, y->ffn_norm, moe_in, M->d_moe_out, ids,
+					      wts, s))
+				return 0;
+			continue;
+		}
+		LCHK(lm_launch_norm_rows(1, 1, E, M->d_h1, NULL, y->ffn_norm, NULL, moe_in, NULL,
+					 M->d_st, NULL, NULL, s),
 		     "MoE norm");
-		if (!hip_moe_ffn_dev(y->moe, M->d_moe_in + l * M->E, M->d_moe_out, 1, NULL,
-				     M->d_ids + l * M->K, M->d_w + l * M->K, s))
+		if (!hip_moe_ffn_dev(y->moe, moe_in, M->d_moe_out, 1, NULL, ids, wts, s))
 			return 0;
 	}
 	if (head) { /* logits = rms_norm(h1 + moe_out) . lm_head^T, the pick */

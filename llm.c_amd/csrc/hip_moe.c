@@ -715,9 +715,30 @@ int hip_moe_path_for(const hip_moe_layer *L, size_t T)
 	return choose_path(L, T);
 }
 
+/* the second launch of a decode-sized call on K-quant experts: down and
+ * combine as one, or (longer d_ff) the per-pair down products and the
+ * combine */
+static int kq_decode_tail(hip_moe_layer *L, const uint32_t *ids, const float *w, float *d_out,
+			  size_t T, hipStream_t s)
+{
+	if (moe_kq_down_combine_ok(T, L->topk, L->E, L->EI)) {
+		LCHK(moe_launch_kq_down_combine(L->dtype, L->d_down, L->down_stride, ids, w, L->d_h,
+						d_out, (int)T, (int)L->topk, (int)L->E, (int)L->EI,
+						s),
+		     "K-quant down + combine");
+		return 1;
+	}
+	LCHK(moe_launch_kq_down(L->dtype, L->d_down, L->down_stride, ids, L->d_h, L->d_ypart,
+				(int)(T * L->topk), (int)L->E, (int)L->EI, s),
+	     "K-quant down");
+	LCHK(moe_launch_combine(L->d_ypart, w, d_out, (int)T, (int)L->topk, (int)L->E, 1, s),
+	     "combine");
+	return 1;
+}
+
 int moe_norm_decode_ok(const hip_moe_layer *L)
 {
-	return L && !L->kq && choose_path(L, 1) == HIP_MOE_PATH_DECODE;
+	return L && choose_path(L, 1) == HIP_MOE_PATH_DECODE;
 }
 
 int moe_ffn_dev_norm(hip_moe_layer *L, const float *d_h, const float *d_norm_w, float *d_x_out,
@@ -734,9 +755,19 @@ int moe_ffn_dev_norm(hip_moe_layer *L, const float *d_h, const float *d_norm_w, 
 	hipStream_t s = pick_stream(L, stream);
 	if (!ensure_scratch(L, 1, s))
 		return 0;
+	uint32_t *ids = d_ids_out ? d_ids_out : L->d_ids;
+	float *w = d_w_out ? d_w_out : L->d_w;
+	if (L->kq) {
+		LCHK(moe_launch_kq_route_gateup(L->wtype, d_h, L->d_router, NULL, L->d_gate,
+						L->d_up, L->gu_stride, ids, w, L->d_h, L->d_sync, 1,
+						(int)L->E, (int)L->EI, (int)L->NE, (int)L->topk,
+						L->renorm, L->fused_grid, L->spin, d_norm_w, d_x_out,
+						s),
+		     "K-quant routing + gate/up (normalising its input)");
+		return kq_decode_tail(L, ids, w, d_out, 1, s);
+	}
 	LCHK(moe_launch_fused(L->wtype, d_h, L->d_router, NULL, L->d_gate, L->d_up, L->d_down,
-			      L->gu_stride, L->down_stride, d_ids_out ? d_ids_out : L->d_ids,
-			      d_w_out ? d_w_out : L->d_w, L->d_part, d_out, L->d_sync, 1,
+			      L->gu_stride, L->down_stride, ids, w, L->d_part, d_out, L->d_sync, 1,
 			      (int)L->E, (int)L->EI, (int)L->NE, (int)L->topk, L->renorm,
 			      L->fused_grid, L->spin, d_norm_w, d_x_out, s),
 	     "fused layer (normalising its input)");
@@ -767,21 +798,10 @@ int hip_moe_ffn_dev(hip_moe_layer *L, const float *d_x, float *d_out, size_t T,
 		LCHK(moe_launch_kq_route_gateup(L->wtype, d_x, L->d_router, d_router_bias, L->d_gate,
 						L->d_up, L->gu_stride, ids, w, L->d_h, L->d_sync,
 						(int)T, (int)L->E, (int)L->EI, (int)L->NE,
-						(int)L->topk, L->renorm, L->fused_grid, L->spin, s),
+						(int)L->topk, L->renorm, L->fused_grid, L->spin, NULL,
+						NULL, s),
 		     "K-quant routing + gate/up");
-		if (moe_kq_down_combine_ok(T, L->topk, L->E, L->EI)) {
-			LCHK(moe_launch_kq_down_combine(L->dtype, L->d_down, L->down_stride, ids, w,
-							L->d_h, d_out, (int)T, (int)L->topk,
-							(int)L->E, (int)L->EI, s),
-			     "K-quant down + combine");
-			return 1;
-		}
-		LCHK(moe_launch_kq_down(L->dtype, L->d_down, L->down_stride, ids, L->d_h,
-					L->d_ypart, P, (int)L->E, (int)L->EI, s),
-		     "K-quant down");
-		LCHK(moe_launch_combine(L->d_ypart, w, d_out, (int)T, (int)L->topk, (int)L->E, 1, s),
-		     "combine");
-		return 1;
+		return kq_decode_tail(L, ids, w, d_out, T, s);
 	}
 	if (path == HIP_MOE_PATH_DECODE) {
 		LCHK(moe_launch_fused(L->wtype, d_x, L->d_router, d_router_bias, L->d_gate,

@@ -506,22 +506,26 @@ __device__ static inline float router_chain(const float *xrow, const float *wrow
 
 /*
  * One token's rms_norm(h) * w in every workgroup of a NORM launch.  The rms
- * is taken as the one-token model kernels take it (256 threads: thread v
- * adds h[v]^2, h[v + 256]^2, ... in order; xor trees in waves of 64; the
- * four waves' sums in order; sqrtf(sum / E + 1e-5f)), so every workgroup
- * and the model's own norms get the same bits; then x = (h / rms) * w
- * (olmoe.c:486-488, rmsnorm nn.c:8-31).  hv: this thread's float4s i = tid
- * + NT v (< E / 4) of the token, normalised.  The whole workgroup calls it.
+ * is taken as the one-token model kernels take it, with 256 threads whose
+ * sums go through xor trees in waves of 64 and then the four waves' sums
+ * in order, sqrtf(sum / E + 1e-5f): ORD 1 as the output product's gathered
+ * norm (thread v adds h[v]^2, h[v + 256]^2, ... in order), ORD 2 as the
+ * row norm kernel's (thread v adds the four squares of float4 v, then of
+ * float4 v + 256, ...).  So every workgroup, and the norm launch it
+ * replaces, get the same bits; then x = (h / rms) * w (olmoe.c:486-488,
+ * rmsnorm nn.c:8-31).  hv: this thread's float4s i = tid + NT v (< E / 4)
+ * of the token, normalised.  The whole workgroup calls it.
  */
-template <int NT, int NV>
+template <int NT, int NV, int ORD>
 __device__ static void norm_token(const float *h, const float *w, int E, float4 (&hv)[NV])
 {
-	constexpr int MS = NV * NT / 64; /* terms of a summing thread, E / 256 at most */
+	static_assert(ORD == 1 || ORD == 2, "a summation order");
+	constexpr int MS = NV * NT / 64; /* ORD 1: terms of a summing thread (E / 256) */
+	constexpr int M4 = NV * NT / 256; /* ORD 2: its float4s (E / 1024) */
 	__shared__ float s_red[4];
 	const float4 *h4 = (const float4 *)h, *w4 = (const float4 *)w;
 	const int tid = threadIdx.x, lane = tid % WAVE;
 	float4 wv[NV];
-	float sv[MS];
 #pragma unroll
 	for (int v = 0; v < NV; v++) {
 		const int i = tid + NT * v;
@@ -532,15 +536,34 @@ __device__ static void norm_token(const float *h, const float *w, int E, float4 
 	}
 	float ss = 0.0f;
 	if (tid < 256) {
+		if constexpr (ORD == 1) {
+			float sv[MS];
 #pragma unroll
-		for (int m = 0; m < MS; m++)
-			sv[m] = 256 * m + tid < E ? h[256 * m + tid] : 0.0f;
+			for (int m = 0; m < MS; m++)
+				sv[m] = 256 * m + tid < E ? h[256 * m + tid] : 0.0f;
 #pragma unroll
-		for (int m = 0; m < MS; m++)
-			if (256 * m + tid < E) {
-				const float t = sv[m] * sv[m];
-				ss = ss + t;
-			}
+			for (int m = 0; m < MS; m++)
+				if (256 * m + tid < E) {
+					const float t = sv[m] * sv[m];
+					ss = ss + t;
+				}
+		} else {
+			float4 sv[M4 > 0 ? M4 : 1];
+#pragma unroll
+			for (int m = 0; m < (M4 > 0 ? M4 : 1); m++)
+				if (256 * m + tid < E / 4)
+					sv[m] = h4[256 * m + tid];
+#pragma unroll
+			for (int m = 0; m < (M4 > 0 ? M4 : 1); m++)
+				if (256 * m + tid < E / 4) {
+					const float q0 = sv[m].x * sv[m].x, q1 = sv[m].y * sv[m].y;
+					const float q2 = sv[m].z * sv[m].z, q3 = sv[m].w * sv[m].w;
+					ss = ss + q0;
+					ss = ss + q1;
+					ss = ss + q2;
+					ss = ss + q3;
+				}
+		}
 		for (int o = WAVE / 2; o > 0; o >>= 1)
 			ss += __shfl_xor(ss, o, WAVE);
 		if (lane == 0)
@@ -571,7 +594,7 @@ __device__ static void norm_token(const float *h, const float *w, int E, float4 
  * only after the chain, so its load is in flight meanwhile.  dig (one
  * token): the other waves stage the token's digit blocks there while wave
  * 0 runs the chain. */
-template <int NT, int E, bool NORM = false>
+template <int NT, int E, int NORM = 0>
 __device__ static void router_row(const DecodeArgs &a, int j, u32 prev_epoch, float *lds,
 				  u32 *dig)
 {
@@ -607,7 +630,7 @@ __device__ static void router_row(const DecodeArgs &a, int j, u32 prev_epoch, fl
 			sx[((k + 2) & 7) * RS + ((k + 2) >> 3)] = xv.z;
 			sx[((k + 3) & 7) * RS + ((k + 3) >> 3)] = xv.w;
 		};
-		if constexpr (NORM) {
+		if constexpr (NORM != 0) {
 			/* the row's loads go out with the residual's and the norm
 			 * weights'; x = rms_norm(h) * w lands in LDS (and x_out) */
 			constexpr int NV = (E / 4 + NT - 1) / NT;
@@ -616,7 +639,7 @@ __device__ static void router_row(const DecodeArgs &a, int j, u32 prev_epoch, fl
 			for (int v = 0; v < NV; v++)
 				if ((int)threadIdx.x + NT * v < E / 4)
 					rv[v] = w4[threadIdx.x + NT * v];
-			norm_token<NT, NV>(a.x, a.norm_w, E, hv);
+			norm_token<NT, NV, NORM>(a.x, a.norm_w, E, hv);
 #pragma unroll
 			for (int v = 0; v < NV; v++) {
 				const int i = threadIdx.x + NT * v;
@@ -904,13 +927,13 @@ void k_moe_decode(DecodeArgs a)
 	 * copy (no second round trip) */
 	const bool st0 = b < a.NE && x0 < x1 && a.T == 1;
 	if (b < a.NE)
-		router_row<NT, CG * S::COLS, NORM>(a, b, prev_epoch, rl, st0 ? sx : nullptr);
+		router_row<NT, CG * S::COLS, NORM ? 1 : 0>(a, b, prev_epoch, rl, st0 ? sx : nullptr);
 	/* the tokens of this workgroup's items (they do not depend on routing) */
 	if (x0 < x1 && !st0) {
 		if constexpr (NORM) { /* one token, normalised here */
 			constexpr int NV = (RPT + 3) / 4;
 			float4 hv[NV];
-			norm_token<NT, NV>(a.x, a.norm_w, a.E, hv);
+			norm_token<NT, NV, 1>(a.x, a.norm_w, a.E, hv);
 #pragma unroll
 			for (int v = 0; v < NV; v++) {
 				const int i = threadIdx.x + NT * v;
@@ -1377,7 +1400,7 @@ extern "C" int moe_launch_fused(int wtype, const float *x, const float *router,
  */
 #define KQ_NT 512
 
-template <int GT, int E>
+template <int GT, int E, bool NORM>
 __global__ __launch_bounds__(KQ_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_kq_route_gateup(DecodeArgs a)
 {
@@ -1437,12 +1460,33 @@ void k_kq_route_gateup(DecodeArgs a)
 		err0 = ld_dev_u32(a.sync + MOE_SYNC_ERR_WORD);
 	}
 	if (b < a.NE)
-		router_row<NT, E>(a, b, prev_epoch, lds, nullptr);
+		router_row<NT, E, NORM ? 2 : 0>(a, b, prev_epoch, lds, nullptr);
 	/* the first unit's token does not depend on routing */
 	int cur_t = -1;
 	if (u0 < u1) {
 		cur_t = u0 / CH / a.K;
-		quantize(cur_t);
+		if constexpr (NORM) { /* one token, normalised here: wave w's
+				       * block w + k NT / 64 is float4 tid + k NT */
+			constexpr int NV = (E / 4 + NT - 1) / NT;
+			float4 hv[NV];
+			norm_token<NT, NV, 2>(a.x, a.norm_w, E, hv);
+#pragma unroll
+			for (int k = 0; k < NV; k++) {
+				const int i = wave + k * (NT / WAVE);
+				if (i < NB) {
+					float d;
+					int bs;
+					const u32 q = kg_q8k(hv[k], lane, &d, &bs);
+					s_q8[i * QS + lane] = (int)q;
+					if (lane % 4 == 0)
+						s_bs[i * BS + lane / 4] = bs;
+					if (lane == 0)
+						s_d[i] = d;
+				}
+			}
+		} else {
+			quantize(cur_t);
+		}
 	}
 	if (tid == 0) {
 		s_epoch = prev_epoch + 1;
@@ -1532,11 +1576,12 @@ void k_kq_route_gateup(DecodeArgs a)
 		st_dev_u32(a.sync, epoch);
 }
 
-static const void *kq_decode_fn(int gt, size_t E)
+static const void *kq_decode_fn(int gt, size_t E, bool norm = false)
 {
 #define KQPICK(G_, E_)                                                        \
 	if (gt == G_ && E == E_)                                             \
-		return (const void *)k_kq_route_gateup<G_, E_>;
+		return norm ? (const void *)k_kq_route_gateup<G_, E_, true>          \
+			    : (const void *)k_kq_route_gateup<G_, E_, false>;
 	KQPICK(3, 1024)
 	KQPICK(3, 2048)
 	KQPICK(3, 4096)
@@ -1573,14 +1618,17 @@ extern "C" int moe_kq_decode_supported(int gt, size_t E, size_t EI, size_t NE, s
  * workgroups), or 0 */
 extern "C" int moe_kq_decode_grid(int gt, size_t E, size_t NE)
 {
-	const void *fn = kq_decode_fn(gt, E);
-	int dev = 0, ncu = 0, per = 0;
+	const void *fn = kq_decode_fn(gt, E), *fn_n = kq_decode_fn(gt, E, true);
+	int dev = 0, ncu = 0, per = 0, per_n = 0;
 	if (!fn || hipGetDevice(&dev) != hipSuccess ||
 	    hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
 		return 0;
 	if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, fn, KQ_NT,
 							 kq_decode_lds_bytes(E)) != hipSuccess ||
-	    per < 1)
+	    per < 1 ||
+	    hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_n, fn_n, KQ_NT,
+							 kq_decode_lds_bytes(E)) != hipSuccess ||
+	    per_n < 1)
 		return 0;
 	return ncu >= (int)NE && ncu >= MOE_FUSED_MAX_P ? ncu : 0;
 }
@@ -1589,10 +1637,11 @@ extern "C" int moe_launch_kq_route_gateup(int gt, const float *x, const float *r
 					  const float *bias, const uint8_t *gate, const uint8_t *up,
 					  size_t gu_stride, uint32_t *ids, float *w, float *h,
 					  uint32_t *sync, int T, int E, int EI, int NE, int K,
-					  int renorm, int grid, int spin, void *stream)
+					  int renorm, int grid, int spin, const float *norm_w,
+					  float *x_out, void *stream)
 {
-	const void *fn = kq_decode_fn(gt, (size_t)E);
-	if (!fn || grid < NE || grid < T ||
+	const void *fn = kq_decode_fn(gt, (size_t)E, norm_w != NULL);
+	if (!fn || grid < NE || grid < T || (norm_w && (T != 1 || !x_out)) ||
 	    !moe_kq_decode_supported(gt, (size_t)E, (size_t)EI, (size_t)NE, (size_t)T, (size_t)K))
 		return (int)hipErrorInvalidValue;
 	SyncLayout sl = sync_layout((size_t)T, (size_t)NE, grid);
@@ -1614,6 +1663,8 @@ extern "C" int moe_launch_kq_route_gateup(int gt, const float *x, const float *r
 	a.K = K;
 	a.renorm = renorm;
 	a.n_items = T * K * (EI / (KQ_NT / (2 * (E / 256))));
+	a.norm_w = norm_w;
+	a.x_out = x_out;
 	a.off_start = (int)sl.off_start;
 	a.off_rep = (int)sl.off_rep;
 	a.rep_stride = (int)sl.rep_stride;

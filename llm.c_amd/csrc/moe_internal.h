@@ -107,7 +107,7 @@ int moe_launch_kq_route_gateup(int gt, const float *x, const float *router, cons
                                const uint8_t *gate, const uint8_t *up, size_t gu_stride,
                                uint32_t *ids, float *w, float *h, uint32_t *sync, int T, int E,
                                int EI, int NE, int K, int renorm, int grid, int spin,
-                               void *stream);
+                               const float *norm_w, float *x_out, void *stream);
 int moe_kq_down_combine_ok(size_t T, size_t K, size_t E, size_t EI);
 int moe_launch_kq_down_combine(int dt, const uint8_t *down, size_t dn_stride,
                                const uint32_t *ids, const float *w, const float *h, float *out,
@@ -161,7 +161,9 @@ int moe_launch_fused(int wtype, const float *x, const float *router, const float
  * the launch: x = rms_norm(d_h) * d_norm_w (the one-token model kernels'
  * arithmetic; also written to d_x_out), then the layer on x, as
  * hip_moe_ffn_dev(L, x, d_out, 1, NULL, ids, w).  moe_norm_decode_ok: whether
- * one token takes that kernel on L (Q8_0/Q4_0 experts, decode path). */
+ * one token takes the decode path on L (Q8_0/Q4_0 experts: k_moe_decode,
+ * whose norm sums as the output product's gather; K-quant experts:
+ * k_kq_route_gateup, whose norm sums as the row norm kernel). */
 struct hip_moe_layer;
 int moe_norm_decode_ok(const struct hip_moe_layer *L);
 int moe_ffn_dev_norm(struct hip_moe_layer *L, const float *d_h, const float *d_norm_w,
