@@ -34,11 +34,15 @@ struct lm_layer {
 	uint8_t *wqkv; /* [q rows | k rows | v rows][E] blocks (one block type) */
 	uint8_t *wo;   /* [E][heads * 128] blocks */
 	hip_moe_layer *moe;
-	/* mixed block types (the generic step): q, k, v apart, each tensor's
-	 * type and its product's workgroups */
+	/* mixed block types (the generic step): each tensor's type and its
+	 * product's workgroups.  The first nqkv of q, k, v (those sharing q's
+	 * type, in that order) are stacked in wq and run as one product
+	 * (their rows are consecutive in the step's q/k/v row); wk and wv are
+	 * set only for tensors not stacked */
 	uint8_t *wq, *wk, *wv;
 	int tq, tk, tv, to;
 	int gq, gk, gv, go;
+	int nqkv;
 };
 
 struct hip_lm {
@@ -162,6 +166,28 @@ static int upload_t(uint8_t **dst, const void *src, int t, size_t rows, size_t c
 	if (all > n)
 		HIPCHK(hipMemset(*dst + n, 0, all - n), what);
 	HIPCHK(hipMemcpy(*dst, src, n, hipMemcpyHostToDevice), what);
+	return 1;
+fail:
+	return 0;
+}
+
+/* n matrices of one type t and `cols` columns, rows[i] rows each, stacked
+ * into one buffer (the rows of matrix i after those of matrix i - 1) */
+static int upload_stacked(uint8_t **dst, const void *const *src, const size_t *rows, int n,
+			  int t, size_t cols, const char *what)
+{
+	const size_t rb = moe_row_bytes(t, cols);
+	size_t all = 0, off = 0;
+	for (int i = 0; i < n; i++)
+		all += rows[i];
+	const size_t n_bytes = all * rb, bytes = tbytes(t, all, cols);
+	HIPCHK(hipMalloc((void **)dst, bytes), what);
+	if (bytes > n_bytes)
+		HIPCHK(hipMemset(*dst + n_bytes, 0, bytes - n_bytes), what);
+	for (int i = 0; i < n; i++) {
+		HIPCHK(hipMemcpy(*dst + off, src[i], rows[i] * rb, hipMemcpyHostToDevice), what);
+		off += rows[i] * rb;
+	}
 	return 1;
 fail:
 	return 0;
@@ -457,9 +483,16 @@ hip_lm *hip_lm_upload(const hip_lm_desc *d)
 				       "the types %d %d %d %d", l, E, M->EQ, y->tq, y->tk, y->tv, y->to);
 				goto fail;
 			}
-			if (!upload_t(&y->wq, d->attn_q[l], y->tq, M->EQ, E, "upload attn_q") ||
-			    !upload_t(&y->wk, d->attn_k[l], y->tk, M->EKV, E, "upload attn_k") ||
-			    !upload_t(&y->wv, d->attn_v[l], y->tv, M->EKV, E, "upload attn_v") ||
+			/* q with k (and v) of its type as one matrix: every row's dot
+			 * is the same whatever rows share its launch */
+			y->nqkv = y->tk != y->tq ? 1 : y->tv != y->tq ? 2 : 3;
+			const void *src[3] = {d->attn_q[l], d->attn_k[l], d->attn_v[l]};
+			const size_t rows[3] = {M->EQ, M->EKV, M->EKV};
+			if (!upload_stacked(&y->wq, src, rows, y->nqkv, y->tq, E, "upload attn_q/k/v") ||
+			    (y->nqkv < 2 &&
+			     !upload_t(&y->wk, d->attn_k[l], y->tk, M->EKV, E, "upload attn_k")) ||
+			    (y->nqkv < 3 &&
+			     !upload_t(&y->wv, d->attn_v[l], y->tv, M->EKV, E, "upload attn_v")) ||
 			    !upload_t(&y->wo, d->attn_o[l], y->to, E, M->EQ, "upload attn_output"))
 				goto fail;
 		}
@@ -643,9 +676,13 @@ static int enqueue_step_generic(hip_lm *M, int head, int nact)
 			LCHK(lm_launch_norm_rows(1, 1, E, M->d_h1, M->d_moe_out, y->attn_norm, M->d_h0,
 						 M->d_x, NULL, M->d_st, NULL, NULL, s), "norm");
 		}
-		if (!vec_product(y->tq, y->wq, EQ, E, M->d_x, NULL, M->d_qkv, y->gq, s) ||
-		    !vec_product(y->tk, y->wk, EK, E, M->d_x, NULL, M->d_qkv + EQ, y->gk, s) ||
-		    !vec_product(y->tv, y->wv, EK, E, M->d_x, NULL, M->d_qkv + EQ + EK, y->gv, s))
+		/* q (with the k and v rows stacked after it) into [q | k | v] */
+		if (!vec_product(y->tq, y->wq, EQ + (y->nqkv - 1) * EK, E, M->d_x, NULL, M->d_qkv,
+				 y->gq, s) ||
+		    (y->nqkv < 2 &&
+		     !vec_product(y->tk, y->wk, EK, E, M->d_x, NULL, M->d_qkv + EQ, y->gk, s)) ||
+		    (y->nqkv < 3 &&
+		     !vec_product(y->tv, y->wv, EK, E, M->d_x, NULL, M->d_qkv + EQ + EK, y->gv, s)))
 			return 0;
 		LCHK(lm_launch_attn(M->d_qkv, y->q_norm, y->k_norm, M->d_freq, M->d_st, M->d_kc + co,
 				    M->d_vc + co, M->d_part, M->d_cnt, M->d_attn, (int)M->H,
