@@ -667,19 +667,27 @@ static int enqueue_step_generic(hip_lm *M, int head, int nact)
 	for (size_t l = 0; l < M->L; l++) {
 		struct lm_layer *y = &M->ly[l];
 		const size_t co = l * M->KH * M->C * M->HL;
-		if (l == 0) {
+		/* layer 0: the token's embedding row; then h0 = h1 + moe_out */
+		if (l == 0)
 			LCHK(lm_launch_embed(M->embd_type, M->d_wte, E, M->d_st, M->d_prompt, M->d_h0, s),
 			     "embedding");
-			LCHK(lm_launch_norm_rows(1, 1, E, M->d_h0, NULL, y->attn_norm, NULL, M->d_x, NULL,
-						 M->d_st, NULL, NULL, s), "norm");
-		} else { /* h0 = h1 + moe_out */
-			LCHK(lm_launch_norm_rows(1, 1, E, M->d_h1, M->d_moe_out, y->attn_norm, M->d_h0,
-						 M->d_x, NULL, M->d_st, NULL, NULL, s), "norm");
+		const float *na = l ? M->d_h1 : M->d_h0, *nb = l ? M->d_moe_out : NULL;
+		float *nh = l ? M->d_h0 : NULL;
+		const int nq = EQ + (y->nqkv - 1) * EK;
+		/* q (with the k and v rows stacked after it) into [q | k | v], on
+		 * x = rms_norm(h0): a K-quant q product normalises h0 in each of its
+		 * workgroups (and writes h0 and x for the other products) */
+		if (is_kq(y->tq) && moe_kq_norm_ok(y->tq, E)) {
+			LCHK(moe_launch_kq_gemv_norm(y->tq, y->wq, nq, E, na, nb, y->attn_norm, nh,
+						     y->nqkv < 3 ? M->d_x : NULL, M->d_qkv, y->gq, s),
+			     "norm + product");
+		} else {
+			LCHK(lm_launch_norm_rows(1, 1, E, na, nb, y->attn_norm, nh, M->d_x, NULL, M->d_st,
+						 NULL, NULL, s), "norm");
+			if (!vec_product(y->tq, y->wq, nq, E, M->d_x, NULL, M->d_qkv, y->gq, s))
+				return 0;
 		}
-		/* q (with the k and v rows stacked after it) into [q | k | v] */
-		if (!vec_product(y->tq, y->wq, EQ + (y->nqkv - 1) * EK, E, M->d_x, NULL, M->d_qkv,
-				 y->gq, s) ||
-		    (y->nqkv < 2 &&
+		if ((y->nqkv < 2 &&
 		     !vec_product(y->tk, y->wk, EK, E, M->d_x, NULL, M->d_qkv + EQ, y->gk, s)) ||
 		    (y->nqkv < 3 &&
 		     !vec_product(y->tv, y->wv, EK, E, M->d_x, NULL, M->d_qkv + EQ + EK, y->gv, s)))

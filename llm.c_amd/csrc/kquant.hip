@@ -260,8 +260,85 @@ template <> struct kq<5> {
 __host__ __device__ static inline int kq_tok_words(int nb) { return nb * KQ_QSTRIDE + nb + nb * 16; }
 __host__ __device__ static inline int kq_rec_words(int R, int nb) { return R * (nb + 1); }
 
-template <int WT>
-__global__ __launch_bounds__(KQ_THREADS) void k_kq_gemv(KQ_ARGS)
+/*
+ * x = rms_norm(a + b) * w of one token (b may be NULL) into LDS (xl, K <=
+ * 4096 floats) with the model's row norm arithmetic (thread v adds the four
+ * squares of float4 v of a + b, then of float4 v + 256, ...; the xor trees
+ * of the four waves; their sums in order; sqrtf(sum / K + 1e-5f); then
+ * (v / rms) * w), so the bits are the row norm kernel's (rmsnorm,
+ * nn.c:8-31).  a + b also goes to h_out and x to x_out (either NULL).
+ */
+__device__ static void kq_norm_token(float *xl, const float *a, const float *b, const float *w,
+				     int K, float *h_out, float *x_out)
+{
+	constexpr int NV = 4096 / 4 / KQ_THREADS;
+	__shared__ float s_red[KQ_THREADS / WAVE];
+	const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE, n4 = K / 4;
+	float4 v[NV], u[NV], wv[NV];
+#pragma unroll
+	for (int k = 0; k < NV; k++) {
+		const int c4 = tid + k * KQ_THREADS;
+		if (c4 < n4) {
+			v[k] = ((const float4 *)a)[c4];
+			if (b)
+				u[k] = ((const float4 *)b)[c4];
+			wv[k] = ((const float4 *)w)[c4];
+		}
+	}
+	float ss = 0.0f;
+#pragma unroll
+	for (int k = 0; k < NV; k++) {
+		const int c4 = tid + k * KQ_THREADS;
+		if (c4 < n4) {
+			if (b) {
+				v[k].x = v[k].x + u[k].x;
+				v[k].y = v[k].y + u[k].y;
+				v[k].z = v[k].z + u[k].z;
+				v[k].w = v[k].w + u[k].w;
+			}
+			if (h_out)
+				((float4 *)h_out)[c4] = v[k];
+			const float q0 = v[k].x * v[k].x, q1 = v[k].y * v[k].y;
+			const float q2 = v[k].z * v[k].z, q3 = v[k].w * v[k].w;
+			ss = ss + q0;
+			ss = ss + q1;
+			ss = ss + q2;
+			ss = ss + q3;
+		}
+	}
+	for (int o = WAVE / 2; o > 0; o >>= 1)
+		ss += __shfl_xor(ss, o, WAVE);
+	if (lane == 0)
+		s_red[wave] = ss;
+	__syncthreads();
+	float sum = 0.0f;
+#pragma unroll
+	for (int k = 0; k < KQ_THREADS / WAVE; k++)
+		sum += s_red[k];
+	const float rms = sqrtf(sum / (float)K + 1e-5f);
+#pragma unroll
+	for (int k = 0; k < NV; k++) {
+		const int c4 = tid + k * KQ_THREADS;
+		if (c4 < n4) {
+			float4 x = v[k];
+			x.x = (x.x / rms) * wv[k].x;
+			x.y = (x.y / rms) * wv[k].y;
+			x.z = (x.z / rms) * wv[k].z;
+			x.w = (x.w / rms) * wv[k].w;
+			((float4 *)xl)[c4] = x;
+			if (x_out)
+				((float4 *)x_out)[c4] = x;
+		}
+	}
+}
+
+/* NORM (one token): x is a, the token is rms_norm(a + xb) * nw, staged from
+ * LDS after the records; workgroup 0 writes a + xb to h_out and the token
+ * to x_out (either NULL) */
+template <int WT, bool NORM>
+__global__ __launch_bounds__(KQ_THREADS) void k_kq_gemv(KQ_ARGS, const float *__restrict__ xb,
+							const float *__restrict__ nw, float *h_out,
+							float *x_out)
 {
 	extern __shared__ __attribute__((aligned(16))) int kq_lds[];
 	using B = kq<WT>;
@@ -289,7 +366,17 @@ __global__ __launch_bounds__(KQ_THREADS) void k_kq_gemv(KQ_ARGS)
 	for (int t0 = 0; t0 < T; t0 += TT) {
 		const int tt = min(TT, T - t0);
 		__syncthreads(); /* the previous pass's readers of the staged tokens are done */
-		kq_stage(st, x, K, t0, tt);
+		if constexpr (NORM) {
+			/* after the records, 16-byte aligned (float4 stores and reads) */
+			float *xl = (float *)(kq_lds +
+					      ((TT * (kq_tok_words(nb) + NREC * rw) + 3) & ~3));
+			kq_norm_token(xl, x, xb, nw, K, blockIdx.x == 0 ? h_out : nullptr,
+				      blockIdx.x == 0 ? x_out : nullptr);
+			__syncthreads();
+			kq_stage_lds(st, xl, K);
+		} else {
+			kq_stage(st, x, K, t0, tt);
+		}
 		__syncthreads();
 		u32 wn[B::DW];
 		{
@@ -656,9 +743,9 @@ extern "C" int moe_kq_grid(int wtype, int K, int T)
 	    hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
 		return 0;
 	const hipError_t e = wtype == 3 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
-						  &per, k_kq_gemv<3>, KQ_THREADS, lds)
+						  &per, k_kq_gemv<3, false>, KQ_THREADS, lds)
 					: hipOccupancyMaxActiveBlocksPerMultiprocessor(
-						  &per, k_kq_gemv<5>, KQ_THREADS, lds);
+						  &per, k_kq_gemv<5, false>, KQ_THREADS, lds);
 	if (e != hipSuccess || per < 1)
 		return 0;
 	return per * ncu;
@@ -704,12 +791,42 @@ extern "C" int moe_launch_kq_gemv(int wtype, const uint8_t *W, int N, int K, con
 	const dim3 grid(min(ngroups, nwg > 0 ? nwg : KQ_GRID));
 	const size_t lds = kq_lds_bytes(wtype, K, TT);
 	hipStream_t s = (hipStream_t)stream;
+	const float *nul = nullptr;
+	float *nulw = nullptr;
 	if (wtype == 3)
-		hipLaunchKernelGGL(k_kq_gemv<3>, grid, dim3(KQ_THREADS), lds, s, W, N, K, R, x, T, TT,
-				   add, add_rows, out);
+		hipLaunchKernelGGL((k_kq_gemv<3, false>), grid, dim3(KQ_THREADS), lds, s, W, N, K, R,
+				   x, T, TT, add, add_rows, out, nul, nul, nulw, nulw);
 	else
-		hipLaunchKernelGGL(k_kq_gemv<5>, grid, dim3(KQ_THREADS), lds, s, W, N, K, R, x, T, TT,
-				   add, add_rows, out);
+		hipLaunchKernelGGL((k_kq_gemv<5, false>), grid, dim3(KQ_THREADS), lds, s, W, N, K, R,
+				   x, T, TT, add, add_rows, out, nul, nul, nulw, nulw);
+	return (int)hipGetLastError();
+}
+
+extern "C" int moe_kq_norm_ok(int wtype, int K)
+{
+	return moe_kq_supported(wtype, K) && !kq_stream_ok(wtype, K, 1, NULL) && K <= 4096 &&
+	       kq_lds_bytes(wtype, K, 1) + 16 + (size_t)K * 4 <= KQ_LDS_MAX;
+}
+
+extern "C" int moe_launch_kq_gemv_norm(int wtype, const uint8_t *W, int N, int K, const float *a,
+				       const float *b, const float *w, float *h_out, float *x_out,
+				       float *out, int nwg, void *stream)
+{
+	if (!moe_kq_norm_ok(wtype, K) || N < 1 || !a || !w)
+		return (int)hipErrorInvalidValue;
+	const int nb = K / 256, R = kq_rows(nb), TT = 1;
+	const int ngroups = (N + R - 1) / R;
+	const dim3 grid(min(ngroups, nwg > 0 ? nwg : KQ_GRID));
+	const size_t lds = kq_lds_bytes(wtype, K, TT) + 16 + (size_t)K * 4;
+	hipStream_t s = (hipStream_t)stream;
+	const float *nul = nullptr;
+	const int T = 1, add_rows = 0;
+	if (wtype == 3)
+		hipLaunchKernelGGL((k_kq_gemv<3, true>), grid, dim3(KQ_THREADS), lds, s, W, N, K, R,
+				   a, T, TT, nul, add_rows, out, b, w, h_out, x_out);
+	else
+		hipLaunchKernelGGL((k_kq_gemv<5, true>), grid, dim3(KQ_THREADS), lds, s, W, N, K, R,
+				   a, T, TT, nul, add_rows, out, b, w, h_out, x_out);
 	return (int)hipGetLastError();
 }
 

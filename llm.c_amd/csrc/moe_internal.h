@@ -85,6 +85,15 @@ int moe_kq_supported(int wtype, int K);
 int moe_kq_grid(int wtype, int K, int T);
 int moe_launch_kq_gemv(int wtype, const uint8_t *W, int N, int K, const float *x, int T,
                        const float *add, int add_rows, float *out, int nwg, void *stream);
+/* The same product for one token whose input is rms_norm(a + b) * w (b may
+ * be NULL), normalised in every workgroup with the row norm kernel's
+ * arithmetic (the same bits); workgroup 0 writes a + b to h_out and the
+ * normalised token to x_out (either may be NULL).  moe_kq_norm_ok: whether
+ * this form takes wtype at K (the register path, K <= 4096). */
+int moe_kq_norm_ok(int wtype, int K);
+int moe_launch_kq_gemv_norm(int wtype, const uint8_t *W, int N, int K, const float *a,
+                            const float *b, const float *w, float *h_out, float *x_out,
+                            float *out, int nwg, void *stream);
 /* The expert products of a MoE layer with K-quant experts (kq_moe.hip):
  * gate/up type gt, down type dt (3 = Q4_K, 5 = Q6_K), bit for bit the
  * reference's fused_ffn_silu; y [P][E] goes to moe_launch_combine with one
