@@ -1448,11 +1448,23 @@ static int batch_step(hip_lm_batch *B, int head, int nact)
 				    (int)M->KH, (int)M->C, (int)M->window, M->scale,
 				    M->arch != HIP_LM_OLMOE, (int)l, nact, S, cseq, s),
 		     "batch attention");
-		/* h1 = h0 + attn . Wo^T, moe_in = rms_norm(h1) */
-		if (!batch_product(B, y->wo, E, (int)M->EQ, B->d_attn, B->d_h0, B->d_h1))
-			return 0;
-		LCHK(lm_launch_norm_rows(wt, S, E, B->d_h1, NULL, y->ffn_norm, NULL, B->d_moe_in,
-					 NULL, B->d_st, NULL, NULL, s), "batch MoE norm");
+		/* h1 = h0 + attn . Wo^T, moe_in = rms_norm(h1): where the matrix-core
+		 * product leaves partial sums, one launch adds them (the reduce's
+		 * order), adds h0 and normalises */
+		const int EQ = (int)M->EQ;
+		if (moe_qmm_supported(wt, EQ) && moe_qmm_stretches(EQ) > 1) {
+			LCHK(moe_launch_qmm_parts(wt, y->wo, E, EQ, B->d_attn, S, B->d_split, s),
+			     "output product");
+			LCHK(lm_launch_norm_parts(S, E, B->d_split, moe_qmm_stretches(EQ), (size_t)S * E,
+						  B->d_h0, y->ffn_norm, B->d_h1, B->d_moe_in, s),
+			     "batch reduce + MoE norm");
+		} else {
+			if (!batch_product(B, y->wo, E, EQ, B->d_attn, B->d_h0, B->d_h1))
+				return 0;
+			LCHK(lm_launch_norm_rows(wt, S, E, B->d_h1, NULL, y->ffn_norm, NULL,
+						 B->d_moe_in, NULL, B->d_st, NULL, NULL, s),
+			     "batch MoE norm");
+		}
 		if (!hip_moe_ffn_dev(y->moe, B->d_moe_in, B->d_moe_out, B->S, NULL, NULL, NULL, s))
 			return 0;
 	}

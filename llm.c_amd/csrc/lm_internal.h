@@ -78,6 +78,14 @@ int lm_launch_pf_attn(const float *qo, const float *kc, const float *vc, float *
                       int KH, int C, int size, int T, int window, float scale, int scale_mul,
                       int nseq, size_t cstride, void *stream);
 
+/* h_out[s] = add[s] + the KS partial-sum slices (TN floats apart) of a
+ * matrix-core product added in stretch order (k_qmm_reduce's sum) and x_out[s]
+ * = rms_norm(h_out[s]) * w, for the nseq rows of E floats: the product's
+ * reduce and the row norm as one launch, with the same bits */
+int lm_launch_norm_parts(int nseq, int E, const float *part, int KS, size_t TN,
+                         const float *add, const float *w, float *h_out, float *x_out,
+                         void *stream);
+
 /* chunks a step over a cache of `size` rows (before the step) reads */
 static inline int lm_attn_active(int size, int window)
 {

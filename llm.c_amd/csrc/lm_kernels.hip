@@ -861,6 +861,91 @@ __global__ __launch_bounds__(LM_NT) void k_lm_norm_rows(int E, const float *a, c
 			*(const float4 *)(sx + (c4 >> 4) * SEG_STRIDE + (c4 & 15) * 4);
 }
 
+/*
+ * Row s of h = add + the KS partial sums of a matrix-core product (slices
+ * of TN floats, added in stretch order after the first, then added to add:
+ * k_qmm_reduce's arithmetic) into h_out, then x_out = rms_norm(h) * w with
+ * stage_norm's arithmetic (the thread's float4s in order, the four squares
+ * of each, block_sum, (h / rms) * w): one launch where the product's
+ * reduce and the row norm were two, with the same bits.
+ */
+__global__ __launch_bounds__(LM_NT) void k_lm_norm_parts(int E, const float *__restrict__ part,
+							 int KS, size_t TN,
+							 const float *__restrict__ add,
+							 const float *__restrict__ w,
+							 float *__restrict__ h_out,
+							 float *__restrict__ x_out)
+{
+	extern __shared__ __attribute__((aligned(16))) float sx[];
+	__shared__ float red[LM_NT / WAVE];
+	constexpr int NB = 4;
+	const size_t o = (size_t)blockIdx.x * E;
+	const int n4 = E / 4;
+	const float4 *p4 = (const float4 *)(part + o), *a4 = (const float4 *)(add + o);
+	const size_t ts = TN / 4; /* float4s between slices */
+	float ss = 0.0f;
+	for (int c0 = threadIdx.x; c0 < n4; c0 += NB * LM_NT) {
+		/* the slices' loads in batches of 8, all of a batch before its adds */
+		float4 v[NB], a[NB];
+#pragma unroll
+		for (int k = 0; k < NB; k++) {
+			const int c4 = min(c0 + k * LM_NT, n4 - 1);
+			v[k] = p4[c4];
+			a[k] = a4[c4];
+		}
+		for (int z0 = 1; z0 < KS; z0 += 8) {
+			float4 q[NB][8];
+#pragma unroll
+			for (int k = 0; k < NB; k++)
+#pragma unroll
+				for (int u = 0; u < 8; u++)
+					q[k][u] = p4[(size_t)min(z0 + u, KS - 1) * ts +
+						     min(c0 + k * LM_NT, n4 - 1)];
+#pragma unroll
+			for (int k = 0; k < NB; k++)
+#pragma unroll
+				for (int u = 0; u < 8; u++)
+					if (z0 + u < KS) {
+						v[k].x += q[k][u].x;
+						v[k].y += q[k][u].y;
+						v[k].z += q[k][u].z;
+						v[k].w += q[k][u].w;
+					}
+		}
+#pragma unroll
+		for (int k = 0; k < NB; k++) {
+			v[k].x = a[k].x + v[k].x;
+			v[k].y = a[k].y + v[k].y;
+			v[k].z = a[k].z + v[k].z;
+			v[k].w = a[k].w + v[k].w;
+		}
+#pragma unroll
+		for (int k = 0; k < NB; k++) {
+			const int c4 = c0 + k * LM_NT;
+			if (c4 >= n4)
+				break;
+			((float4 *)(h_out + o))[c4] = v[k];
+			((float4 *)sx)[c4] = v[k];
+			const float q0 = v[k].x * v[k].x, q1 = v[k].y * v[k].y;
+			const float q2 = v[k].z * v[k].z, q3 = v[k].w * v[k].w;
+			ss = ss + q0;
+			ss = ss + q1;
+			ss = ss + q2;
+			ss = ss + q3;
+		}
+	}
+	const float rms = sqrtf(block_sum(ss, red) / (float)E + 1e-5f);
+	for (int c4 = threadIdx.x; c4 < n4; c4 += LM_NT) {
+		float4 v = ((const float4 *)sx)[c4];
+		const float4 wv = ((const float4 *)w)[c4];
+		v.x = (v.x / rms) * wv.x;
+		v.y = (v.y / rms) * wv.y;
+		v.z = (v.z / rms) * wv.z;
+		v.w = (v.w / rms) * wv.w;
+		((float4 *)(x_out + o))[c4] = v;
+	}
+}
+
 /* workgroup s: the first maximum of logits[s] (main.c:189-193) becomes the
  * sequence's next token btok[s] and tokens[s * tstride + step] */
 #define PK_NT 1024 /* threads of the pick: a 50304-entry row in one round of loads */
@@ -1363,6 +1448,18 @@ extern "C" int lm_launch_norm_rows(int wtype, int nseq, int E, const float *a, c
 				   h_out, x_out, wte, st, prompt, btok);
 	else
 		return (int)hipErrorInvalidValue;
+	return (int)hipGetLastError();
+}
+
+extern "C" int lm_launch_norm_parts(int nseq, int E, const float *part, int KS, size_t TN,
+				    const float *add, const float *w, float *h_out, float *x_out,
+				    void *stream)
+{
+	if (nseq < 1 || E % 4 || KS < 1 || TN < (size_t)nseq * E || !part || !add || !w ||
+	    !h_out || !x_out)
+		return (int)hipErrorInvalidValue;
+	hipLaunchKernelGGL(k_lm_norm_parts, dim3(nseq), dim3(LM_NT), (size_t)E * sizeof(float),
+			   (hipStream_t)stream, E, part, KS, TN, add, w, h_out, x_out);
 	return (int)hipGetLastError();
 }
 

@@ -75,6 +75,12 @@ int moe_qmm_supported(int wtype, int K);
 size_t moe_qmm_work_bytes(int T, int N, int K);
 int moe_launch_qmm(int wtype, const uint8_t *W, int N, int K, const float *x, int T,
                    const float *add, int add_rows, float *out, void *work, void *stream);
+/* moe_qmm_stretches: the KS column stretches a product of K columns splits
+ * into; moe_launch_qmm_parts (KS > 1): only the KS partial sums, slices of
+ * T * N floats in work, for the caller to add in stretch order */
+int moe_qmm_stretches(int K);
+int moe_launch_qmm_parts(int wtype, const uint8_t *W, int N, int K, const float *x, int T,
+                         void *work, void *stream);
 
 /* The same product on a Q4_K (wtype 3) or Q6_K (5) matrix through Q8_K
  * activations, bit for bit the reference's (kquant.hip); the matrix buffer

@@ -306,14 +306,23 @@ extern "C" size_t moe_qmm_work_bytes(int T, int N, int K)
 	return KS > 1 ? (size_t)KS * T * N * sizeof(float) : 0;
 }
 
-extern "C" int moe_launch_qmm(int wtype, const uint8_t *W, int N, int K, const float *x, int T,
-			      const float *add, int add_rows, float *out, void *work,
-			      void *stream)
+/* stretches of 64 * PZ columns the product of K columns splits into (its
+ * partial sums are KS slices of T * N floats when KS > 1) */
+extern "C" int moe_qmm_stretches(int K)
+{
+	return K / (64 * qmm_pz(K));
+}
+
+/* parts_only: KS > 1 and only the partial sums, left for the caller to add
+ * in stretch order (k_qmm_reduce's sum) */
+static int launch_qmm(int wtype, const uint8_t *W, int N, int K, const float *x, int T,
+		      const float *add, int add_rows, float *out, void *work, bool parts_only,
+		      void *stream)
 {
 	if (!moe_qmm_supported(wtype, K) || N < 1 || T < 1 || (size_t)T * N > 0xffffffffull)
 		return (int)hipErrorInvalidValue;
 	const int PZ = qmm_pz(K), KS = K / (64 * PZ);
-	if ((T + QMM_TOK - 1) / QMM_TOK > 65535 || (KS > 1 && !work))
+	if ((T + QMM_TOK - 1) / QMM_TOK > 65535 || (KS > 1 && !work) || (parts_only && KS < 2))
 		return (int)hipErrorInvalidValue;
 	const size_t rb = (size_t)(K / 32) * (wtype == 1 ? 34 : 18);
 	const dim3 grid((N + QMM_WAVES * QMM_ROWS - 1) / (QMM_WAVES * QMM_ROWS),
@@ -333,10 +342,23 @@ extern "C" int moe_launch_qmm(int wtype, const uint8_t *W, int N, int K, const f
 #undef QMM
 	if (!done)
 		return (int)hipErrorInvalidValue;
-	if (KS > 1) {
+	if (KS > 1 && !parts_only) {
 		const size_t TN = (size_t)T * N;
 		hipLaunchKernelGGL(k_qmm_reduce, dim3((unsigned)((TN + 255) / 256)), dim3(256), 0, s,
 				   part, KS, TN, N, add, add_rows, out);
 	}
 	return (int)hipGetLastError();
+}
+
+extern "C" int moe_launch_qmm(int wtype, const uint8_t *W, int N, int K, const float *x, int T,
+			      const float *add, int add_rows, float *out, void *work,
+			      void *stream)
+{
+	return launch_qmm(wtype, W, N, K, x, T, add, add_rows, out, work, false, stream);
+}
+
+extern "C" int moe_launch_qmm_parts(int wtype, const uint8_t *W, int N, int K, const float *x,
+				    int T, void *work, void *stream)
+{
+	return launch_qmm(wtype, W, N, K, x, T, NULL, 0, NULL, work, true, stream);
 }
