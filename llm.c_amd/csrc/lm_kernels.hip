@@ -15,12 +15,18 @@
  *                 a head to finish merges the chunks into softmax . V
  *                 (olmoe.c:296-320, flash-decoding form)
  *   k_lm_oproj    the output product with the residual as its add operand
- *                 (olmoe.c:476-478); workgroup 0 computes the pre-MoE
- *                 rms_norm (olmoe.c:482) for the MoE layer
+ *                 (olmoe.c:476-478); where the MoE launch does not take the
+ *                 pre-MoE rms_norm (olmoe.c:482) itself, workgroup 0
+ *                 gathers the rows and computes it
  *   k_lm_head     the residual add and the final rms_norm into LDS, the
  *                 lm_head product (olmoe.c:558-564), and the greedy pick
  *                 (main.c:189-193, the first maximum) by workgroup 0, which
  *                 also advances the step's counters
+ *
+ * The several-sequence and K-quant steps also use k_lm_norm_rows (residual
+ * add and rms_norm of whole rows), k_lm_norm_parts (a matrix-core product's
+ * partial sums, the residual and rms_norm in one launch), k_lm_pick_rows
+ * and k_lm_embed.
  *
  * Every kernel reads the step's token, position and cache row from the
  * device state block (LmState), so one captured HIP graph serves every step.
