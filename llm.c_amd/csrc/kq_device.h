@@ -237,14 +237,17 @@ __device__ static inline void kd_q6k(const uint8_t *blk, const float *hb, int l,
 		for (int g = 0; g < 4; g++)
 #pragma unroll
 			for (int hf = 0; hf < 2; hf++) {
+				/* (q - 32) * vs as fma(q, vs, -32 vs): the exact product
+				 * rounded once, as the reference's (float)(q - 32) * vs
+				 * (-32 vs is exact), one instruction fewer */
 				const float vs = d * (float)sc[8 * c + 2 * g + hf];
+				const float nvs = -32.0f * vs;
 #pragma unroll
 				for (int m = 0; m < 2; m++) {
 					const int lo = (int)ql[c][hf][m][g & 1];
-					const int q = ((g < 2 ? lo & 0xF : lo >> 4) |
-						       (((int)(qh[c][hf][m] >> (2 * g)) & 3) << 4)) -
-						      32;
-					const float vt = (float)q * vs;
+					const int q = (g < 2 ? lo & 0xF : lo >> 4) |
+						      (((int)(qh[c][hf][m] >> (2 * g)) & 3) << 4);
+					const float vt = fmaf((float)q, vs, nvs);
 					acc = fmaf(vt, hv[16 * c + 4 * g + 2 * hf + m], acc);
 				}
 			}
