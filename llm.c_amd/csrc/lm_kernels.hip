@@ -364,24 +364,23 @@ __global__ __launch_bounds__(LM_NT) void k_lm_attn(const float *__restrict__ qkv
 	if (tid < HL / 2)
 		fr = freq[tid];
 	float s1 = 0.0f, s2 = 0.0f;
-	if (q_norm) { /* eight loads in flight, added in index order */
-		for (int i0 = tid; i0 < EQ; i0 += 8 * LM_NT) {
-			float qv[8];
+	if (q_norm) {
+		/* eight q and eight k loads in flight (rows clamped: no branch per
+		 * load), each sum added in index order; one loop, so the k loads
+		 * do not wait behind the q sums (two loops took two round trips) */
+		for (int i0 = tid; i0 < max(EQ, EK); i0 += 8 * LM_NT) {
+			float qv[8], kv[8];
 #pragma unroll
-			for (int u = 0; u < 8; u++)
-				qv[u] = i0 + u * LM_NT < EQ ? q[i0 + u * LM_NT] : 0.0f;
+			for (int u = 0; u < 8; u++) {
+				qv[u] = q[min(i0 + u * LM_NT, EQ - 1)];
+				kv[u] = k[min(i0 + u * LM_NT, EK - 1)];
+			}
 #pragma unroll
 			for (int u = 0; u < 8; u++)
 				if (i0 + u * LM_NT < EQ) {
 					const float t = qv[u] * qv[u];
 					s1 = s1 + t;
 				}
-		}
-		for (int i0 = tid; i0 < EK; i0 += 8 * LM_NT) {
-			float kv[8];
-#pragma unroll
-			for (int u = 0; u < 8; u++)
-				kv[u] = i0 + u * LM_NT < EK ? k[i0 + u * LM_NT] : 0.0f;
 #pragma unroll
 			for (int u = 0; u < 8; u++)
 				if (i0 + u * LM_NT < EK) {
