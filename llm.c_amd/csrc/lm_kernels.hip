@@ -1189,9 +1189,12 @@ __global__ __launch_bounds__(LM_NT) void k_lm_pf_attn(const float *__restrict__ 
 						      int size, int T, int window, float scale,
 						      int scale_mul, size_t cstride)
 {
-	constexpr int HL = LM_HLEN, RS = HL + 4;
+	constexpr int HL = LM_HLEN, RS = HL + 4, SS = PF_KB + 1;
 	static_assert(LM_NT == 4 * PF_QB, "four threads per query row");
 	__shared__ __attribute__((aligned(16))) float sk[PF_KB * RS], sv[PF_KB * RS];
+	/* a block's scores of each query row (kept in registers, unrolled, the
+	 * 64 scores and their operands spilled ~6.5 KB a lane to scratch) */
+	__shared__ float ssc[PF_QB * SS];
 	const int h = blockIdx.x, q0 = blockIdx.y * PF_QB, z = blockIdx.z;
 	const int EQ = H * HL, kh = h / (H / KH);
 	const int tid = threadIdx.x, qi = tid / 4, u = tid % 4;
@@ -1233,8 +1236,8 @@ __global__ __launch_bounds__(LM_NT) void k_lm_pf_attn(const float *__restrict__ 
 			*(float4 *)(sv + jj * RS + 4 * c4) = vv;
 		}
 		__syncthreads();
-		float sc[PF_KB];
-#pragma unroll
+		float *sc = ssc + qi * SS;
+#pragma unroll 2
 		for (int jj = 0; jj < PF_KB; jj++) {
 			const float4 *k4 = (const float4 *)(sk + jj * RS + 32 * u);
 			float a = 0.0f;
@@ -1250,10 +1253,12 @@ __global__ __launch_bounds__(LM_NT) void k_lm_pf_attn(const float *__restrict__ 
 			a += __shfl_xor(a, 2, WAVE);
 			const int j = j0 + jj;
 			const bool keep = j <= qa && (window <= 0 || qa - j < window);
-			sc[jj] = keep ? (scale_mul ? a * scale : a / scale) : -INFINITY;
+			if (u == 0)
+				sc[jj] = keep ? (scale_mul ? a * scale : a / scale) : -INFINITY;
 		}
+		__syncthreads(); /* the row's scores, from its quarter 0 */
 		float mb = -INFINITY;
-#pragma unroll
+#pragma unroll 8
 		for (int jj = 0; jj < PF_KB; jj++)
 			mb = fmaxf(mb, sc[jj]);
 		const float mn = fmaxf(m, mb);
@@ -1264,9 +1269,10 @@ __global__ __launch_bounds__(LM_NT) void k_lm_pf_attn(const float *__restrict__ 
 #pragma unroll
 		for (int i = 0; i < 32; i++)
 			o[i] = o[i] * corr;
-#pragma unroll
+#pragma unroll 2
 		for (int jj = 0; jj < PF_KB; jj++) {
-			const float pj = sc[jj] == -INFINITY ? 0.0f : moe_expf(sc[jj] - mn);
+			const float sj = sc[jj];
+			const float pj = sj == -INFINITY ? 0.0f : moe_expf(sj - mn);
 			l = l + pj;
 			const float4 *v4 = (const float4 *)(sv + jj * RS + 32 * u);
 #pragma unroll
